@@ -1,0 +1,225 @@
+/*
+ * xdna_hip.h -- C ABI of the MI355X (gfx950) training hot path.
+ *
+ * This is the boundary between the PrivateUse1 "xdna" PyTorch backend (host C++)
+ * and the hand-written HIP kernels.  Plain pointers, sizes and a hipStream_t passed
+ * as void*; no torch types.  Every pointer argument of a compute entry point is
+ * DEVICE memory.  Conventions follow the reference's XRT shim
+ * (xdna_train/_vendor/xrt_shim/xrt_shim.h:2-3, 160): an int status (0 = ok,
+ * -1 = error) and a thread-local message from xdna_hip_last_error(); pointer
+ * returning calls return NULL on error.
+ *
+ * bf16 tensors are passed as uint16_t bit patterns (round-to-nearest-even when
+ * produced from fp32).
+ */
+#ifndef XDNA_HIP_H
+#define XDNA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Errors, poisoning and failure injection                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Last error message of the calling thread ("" if none).
+ * Replaces shim_last_error (xrt_shim.h:160; xrt_shim.cpp:235-249). */
+const char* xdna_hip_last_error(void);
+
+/* 1 once the process is poisoned: a launch or wait failed in a way that may
+ * leave device work in flight.  Poisoned processes refuse new launches and
+ * leak frees.  Replaces shim_dispatch_poisoned (xrt_shim.cpp:139-151). */
+int xdna_hip_poisoned(void);
+
+/* Test hook: the n-th launch from now (n >= 1) fails with an injected error
+ * before touching the device; n = 0 disables.  `poison` != 0 also poisons the
+ * process at that point (the timeout-without-abort case of
+ * xrt_shim.cpp:174-233).  Host-only: nothing is launched. */
+int xdna_hip_inject_failure(int64_t nth_launch, int poison);
+
+/* Clears the poisoned flag and the injection counter (tests only). */
+int xdna_hip_reset_failure_state(void);
+
+/* Launches issued so far through this library (profiling/tests). */
+int64_t xdna_hip_launch_count(void);
+
+/* ------------------------------------------------------------------------ */
+/* Device, memory, streams, events  (the shim_* analogue, xrt_shim.h:29-160) */
+/* ------------------------------------------------------------------------ */
+
+int xdna_hip_device_count(void);
+int xdna_hip_set_device(int device);
+int xdna_hip_get_device(int* device);
+/* Name, CU count and HBM bytes of the current device. */
+int xdna_hip_device_properties(char* name, size_t name_len, int* cu_count,
+                               size_t* total_mem, int* gcn_arch);
+
+/* Raw device allocation (no caching).  NULL on failure. */
+void* xdna_hip_malloc(size_t bytes);
+int xdna_hip_free(void* ptr);
+
+/* Size-binned caching allocator over xdna_hip_malloc (the XdnaBoCache analogue,
+ * torch_xdna_device.cpp:205-296).  All work of the library is ordered on the
+ * caller's stream, so a released block is reused by later launches in stream
+ * order.  Blocks are rounded up to 512 B (small) or 2 MiB (large). */
+void* xdna_hip_cache_alloc(size_t bytes);
+int xdna_hip_cache_free(void* ptr);
+/* Returns every cached (unused) block to the device. */
+int xdna_hip_cache_empty(void);
+/* stats[0..5] = cached_bytes, allocated_bytes, max_allocated_bytes,
+ * fresh_allocations, reuses, frees. */
+int xdna_hip_cache_stats(int64_t* stats, int n);
+
+int xdna_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
+                          void* stream); /* kind: 1 H2D, 2 D2H, 3 D2D, 4 default */
+int xdna_hip_memset_async(void* dst, int value, size_t bytes, void* stream);
+int xdna_hip_stream_synchronize(void* stream);
+int xdna_hip_device_synchronize(void);
+
+void* xdna_hip_event_create(int timing);
+int xdna_hip_event_destroy(void* event);
+int xdna_hip_event_record(void* event, void* stream);
+int xdna_hip_event_synchronize(void* event);
+/* 1 done, 0 pending, -1 error. */
+int xdna_hip_event_query(void* event);
+int xdna_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int xdna_hip_stream_wait_event(void* stream, void* event);
+
+/* ------------------------------------------------------------------------ */
+/* conv3x3w layouts: NCHW <-> tiled padded-grid rows (bit-exact with the     */
+/* reference's host packing).  Device pointers; same arguments and meaning   */
+/* as the reference functions named, plus the stream.                        */
+/*                                                                          */
+/* Packed input: [groups][chunks][2126][64] bf16.  Row p of the padded grid   */
+/* of virtual image vb = b*S + s is (vb*(H+2) + y + 1)*wp + j + 1 for data    */
+/* column j; group g holds rows [2048 g, 2048 g + 2126).  Only real pixels    */
+/* and channels are written: the caller zero-fills dst once per shape.        */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces xdna_conv3x3w_pack_input_bf16 (conv_pack.cpp:352-393). */
+int xdna_conv3x3w_pack_input_bf16(const uint16_t* src, uint16_t* dst, int B, int C,
+                                  int H, int W, int chunks, void* stream);
+
+/* Replaces xdna_conv3x3w_pack_input_range_bf16 (conv_pack.cpp:529-583):
+ * groups [g0, g0+ng) written to dst laid out [ng][chunks][2126][64]. */
+int xdna_conv3x3w_pack_input_range_bf16(const uint16_t* src, uint16_t* dst, int B, int C,
+                                        int H, int W, int chunks, int g0, int ng,
+                                        void* stream);
+
+/* Replaces xdna_conv3x3w_pack_input_strips_range_bf16 (conv_pack.cpp:632-700):
+ * width tiling into S strips of So output columns (S = 1: plain layout);
+ * halo_zero writes zeros in the two strip-halo data columns (dY for dW). */
+int xdna_conv3x3w_pack_input_strips_range_bf16(const uint16_t* src, uint16_t* dst, int B,
+                                               int C, int H, int W, int S, int So,
+                                               int halo_zero, int chunks, int g0, int ng,
+                                               void* stream);
+
+/* Replaces xdna_conv3x3w_unpack_output_bf16 (conv_pack.cpp:447-466):
+ * [groups*2048][128] bf16 rows -> channel slice [c_start, c_start+cout_valid)
+ * of NCHW [B][C_total][H][W] (valid pixels only). */
+int xdna_conv3x3w_unpack_output_bf16(const uint16_t* c, uint16_t* dst, int B, int H, int W,
+                                     int cout_valid, int C_total, int c_start, void* stream);
+
+/* Replaces xdna_conv3x3w_unpack_output_range_bf16 (conv_pack.cpp:587-616):
+ * rows [p0, p1); c points at row p0. */
+int xdna_conv3x3w_unpack_output_range_bf16(const uint16_t* c, uint16_t* dst, int B, int H,
+                                           int W, int cout_valid, int C_total, int c_start,
+                                           int p0, int p1, void* stream);
+
+/* Replaces xdna_conv3x3w_unpack_output_strips_range_bf16 (conv_pack.cpp:706-743). */
+int xdna_conv3x3w_unpack_output_strips_range_bf16(const uint16_t* c, uint16_t* dst, int B,
+                                                  int H, int W, int S, int So,
+                                                  int cout_valid, int C_total, int c_start,
+                                                  int p0, int p1, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* 3x3 stride-1 pad-1 convolution (bf16 in/out, fp32 accumulation, one       */
+/* rounding).  Replaces the NPU conv3x3w runtime: XdnaConv3x3wRuntime::run    */
+/* (torch_xdna_device.cpp:2317-2483), input_grad (:2515-2522) and             */
+/* XdnaConv3x3wDwRuntime::compute (:2683-2751).                               */
+/* ------------------------------------------------------------------------ */
+
+/* Geometry of the reference plan (torch_xdna_device.cpp:1927-1937, 2112-2157):
+ * out[0..6] = strips S, strip_out So, grid_w Wg, wp, groups, chunks(Cin), m_total. */
+int xdna_conv3x3w_geometry(int B, int Cin, int H, int W, int64_t* out7);
+
+/* Workspace bytes for the forward (or dgrad, where Cin is dY's channel count)
+ * call: packed input + prepared weights. */
+size_t xdna_conv3x3_fwd_workspace_bytes(int B, int Cin, int Cout, int H, int W);
+
+/* y[B][Cout][H][W] = conv3x3(x[B][Cin][H][W], w[Cout][Cin][3][3]) (+ bias[Cout]).
+ * bias may be NULL.  `workspace` holds the packed input (zero-filled here) and
+ * the prepared weights.  A packed copy of x is left at the start of the
+ * workspace ([groups][chunks][2126][64]). */
+int xdna_conv3x3_fwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                          uint16_t* y, int B, int Cin, int Cout, int H, int W,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* dx[B][Cin][H][W] = conv3x3(dy[B][Cout][H][W], flip-swap(w)):
+ * w'[ci][co][dy][dx] = w[co][ci][2-dy][2-dx] (conv_pack.cpp:470-473),
+ * applied in the weight preparation (no flipped copy of w is made). */
+size_t xdna_conv3x3_dgrad_workspace_bytes(int B, int Cin, int Cout, int H, int W);
+int xdna_conv3x3_dgrad_bf16(const uint16_t* dy, const uint16_t* w, uint16_t* dx, int B,
+                            int Cin, int Cout, int H, int W, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* gw[Cout][Cin][3][3] = sum over pixels of dy x shifted(x); gb[Cout] = sum dy
+ * (gb may be NULL).  fp32 sums, deterministic two-stage reduction (the same
+ * bits on every call), one bf16 rounding. */
+size_t xdna_conv3x3_wgrad_workspace_bytes(int B, int Cin, int Cout, int H, int W);
+int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
+                            uint16_t* gb, int B, int Cin, int Cout, int H, int W,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bias gradient alone: gb[c] = sum_{b,y,x} dy[b][c][y][x] (fp32 sum, one rounding). */
+int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H,
+                                int W, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* GEMM: replaces mm_xdna / XdnaGemmRuntime::run (torch_xdna_device.cpp:      */
+/* 4387-4417, 1358-1457), addmm_out_xdna (:3740-3768) and bmm_out_xdna        */
+/* (:3770-3790).                                                              */
+/*                                                                          */
+/* C[b][m][n] = alpha * sum_k A[b][m][k] B[b][k][n] + beta * bias           */
+/* with arbitrary element strides (lda_m, lda_k), (ldb_k, ldb_n), (ldc_m,     */
+/* ldc_n) and batch strides; fp32 accumulation, one bf16 rounding.  bias is   */
+/* NULL, a [n] row vector (bias_mode 1), an [m][n] matrix with strides        */
+/* (bias_sm, bias_sn) (bias_mode 2) or a [m] column vector (bias_mode 3).     */
+/* beta == 0 ignores bias (NaNs in it are not propagated), like torch.        */
+/* ------------------------------------------------------------------------ */
+int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uint16_t* bias,
+                   int batch, int M, int N, int K,
+                   int64_t lda_m, int64_t lda_k, int64_t stride_a,
+                   int64_t ldb_k, int64_t ldb_n, int64_t stride_b,
+                   int64_t ldc_m, int64_t ldc_n, int64_t stride_c,
+                   int bias_mode, int64_t bias_sm, int64_t bias_sn,
+                   float alpha, float beta, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused Adam / AdamW: replaces torch._fused_adam_ reached through the        */
+/* boxed CPU fallback (xdna_cpu_fallback, torch_xdna_device.cpp:5273-5295;    */
+/* selected by _prefer_fused_optimizer, device.py:408-436).                   */
+/*                                                                          */
+/* One pass per element in fp32 opmath; p, m, v (and max_v) stored once in  */
+/* their dtype.  dtype: 0 = fp32, 1 = bf16 (p, g, m, v share it).  step is a  */
+/* device fp32 scalar per tensor (torch's state_steps, already incremented); */
+/* grad_scale / found_inf are optional device fp32 scalars (NULL = absent).  */
+/* mode 0 = Adam (L2 weight decay), 1 = AdamW (decoupled).                   */
+/* ------------------------------------------------------------------------ */
+int xdna_fused_adam(int n_tensors, void* const* params, void* const* grads,
+                    void* const* exp_avgs, void* const* exp_avg_sqs,
+                    void* const* max_exp_avg_sqs, const float* const* steps,
+                    const int64_t* numels, int dtype, double lr, double beta1,
+                    double beta2, double weight_decay, double eps, int amsgrad,
+                    int maximize, int mode, const float* grad_scale,
+                    const float* found_inf, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XDNA_HIP_H */

@@ -1,0 +1,283 @@
+/*
+ * CPU oracle for the MI355X hot path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
+ * library, and only as the checker (or the timed CPU baseline), never as the product
+ * path.  Plain C restatements of the reference's algorithms, written for clarity:
+ * straight loop nests, double accumulation for the convolutions.
+ *
+ * Each function names the reference code it restates.  How each is pinned (golden
+ * vectors, the reference's own build in oracle/_ref, closed forms) is listed in the
+ * test files under tests/ that exercise it.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define GROUP_OUT_ROWS 2048
+#define GROUP_ROWS 2126
+#define KSTEP 64
+#define RAW_N 128
+
+static float bf16f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static uint16_t f2bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* Strip geometry: conv3x3w_host.py:96-103 (strip_geometry), torch_xdna_device.cpp:1927-1937. */
+void oracle_strip_geometry(int W, int* S, int* So) {
+  if (W <= 36) {
+    *S = 1;
+    *So = W;
+  } else {
+    *S = (W + 33) / 34;
+    *So = (W + *S - 1) / *S;
+  }
+}
+
+/*
+ * Packed input, groups [g0, g0+ng), written into dst = [ng][chunks][2126][64].
+ * Layout: conv3x3w_host.py:32-46 (pack_input: padded-grid rows, zero border, per-group
+ * windows of 2126 rows starting every 2048) and :106-131 (strip_batch: virtual image
+ * b*S+s holds source columns [s*So-1, s*So+So+1), halo columns zeroed for halo_zero).
+ * Write contract: conv_pack.cpp:625-631 (only real pixels and channels are written;
+ * the caller zero-fills dst).
+ */
+void oracle_pack_strips_range(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
+                              int S, int So, int halo_zero, int chunks, int g0, int ng) {
+  const int Wg = S == 1 ? W : So + 2;
+  const int wp = Wg + 2;
+  for (int vb = 0; vb < B * S; ++vb) {
+    const int b = vb / S, s = vb % S;
+    for (int y = 0; y < H; ++y) {
+      for (int j = 0; j < Wg; ++j) {
+        const int x = (S == 1 ? 0 : s * So - 1) + j;
+        if (x < 0 || x >= W) continue;
+        const int64_t p = ((int64_t)vb * (H + 2) + y + 1) * wp + j + 1;
+        const int64_t g = p / GROUP_OUT_ROWS;
+        const int64_t r = p % GROUP_OUT_ROWS;
+        const int zero = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
+        for (int ch = 0; ch < C && ch < chunks * KSTEP; ++ch) {
+          const int chunk = ch / KSTEP, c = ch % KSTEP;
+          const uint16_t v = zero ? 0 : src[(((int64_t)b * C + ch) * H + y) * W + x];
+          if (g >= g0 && g < (int64_t)g0 + ng)
+            dst[((((g - g0) * chunks + chunk) * GROUP_ROWS) + r) * KSTEP + c] = v;
+          if (g - 1 >= g0 && g - 1 < (int64_t)g0 + ng && r + GROUP_OUT_ROWS < GROUP_ROWS)
+            dst[((((g - 1 - g0) * chunks + chunk) * GROUP_ROWS) + GROUP_OUT_ROWS + r) * KSTEP + c] = v;
+        }
+      }
+    }
+  }
+}
+
+/*
+ * Raw output rows [p0, p1) (c points at row p0, 128 channels per row) -> channel slice
+ * [c_start, c_start+cout_valid) of NCHW [B][C_total][H][W].
+ * Layout: conv3x3w_host.py:85-90 (unpack_output: pixel (y, x) of image b at row
+ * (b*(H+2)+y)*wp + x) and :134-140 (unpack_output_strips: strip s output column t is
+ * virtual-image data column 1+t, image column s*So+t).
+ */
+void oracle_unpack_strips_range(const uint16_t* c, uint16_t* dst, int B, int H, int W, int S,
+                                int So, int cout_valid, int C_total, int c_start, int64_t p0,
+                                int64_t p1) {
+  const int Wg = S == 1 ? W : So + 2;
+  const int wp = Wg + 2;
+  for (int vb = 0; vb < B * S; ++vb) {
+    const int b = vb / S, s = vb % S;
+    const int first = S == 1 ? 0 : 1;
+    int cols = S == 1 ? W : W - s * So;
+    if (S > 1 && cols > So) cols = So;
+    for (int y = 0; y < H; ++y) {
+      for (int t = 0; t < cols; ++t) {
+        const int64_t p = ((int64_t)vb * (H + 2) + y) * wp + first + t;
+        if (p < p0 || p >= p1) continue;
+        const int x = (S == 1 ? 0 : s * So) + t;
+        for (int n = 0; n < cout_valid; ++n)
+          dst[(((int64_t)b * C_total + c_start + n) * H + y) * W + x] = c[(p - p0) * RAW_N + n];
+      }
+    }
+  }
+}
+
+/*
+ * 3x3 / stride 1 / pad 1 convolution, double accumulation of bf16 operands.
+ * Forward: y[b][co][i][j] = sum x[b][ci][i+dy-1][j+dx-1] w[co][ci][dy][dx] (+ bias[co]).
+ * This is the direct convolution the reference's own kernel tests compare against
+ * (tests/run_conv3x3w_hw.py:21-30, run_conv3x3w_dw_hw.py:21-30); the CPU BF16 path
+ * (torch_xdna_device.cpp:4594-4604) computes the same sum in fp32.
+ */
+void oracle_conv3x3_fwd(const uint16_t* x, const uint16_t* w, const uint16_t* bias, double* y,
+                        int B, int Cin, int Cout, int H, int W) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int co = 0; co < Cout; ++co) {
+      for (int i = 0; i < H; ++i)
+        for (int j = 0; j < W; ++j) {
+          double s = bias ? (double)bf16f(bias[co]) : 0.0;
+          for (int ci = 0; ci < Cin; ++ci) {
+            const uint16_t* xp = x + (((int64_t)b * Cin + ci) * H) * W;
+            const uint16_t* wq = w + ((int64_t)co * Cin + ci) * 9;
+            for (int dy = 0; dy < 3; ++dy) {
+              const int yy = i + dy - 1;
+              if (yy < 0 || yy >= H) continue;
+              for (int dx = 0; dx < 3; ++dx) {
+                const int xx = j + dx - 1;
+                if (xx < 0 || xx >= W) continue;
+                s += (double)bf16f(xp[(int64_t)yy * W + xx]) * (double)bf16f(wq[dy * 3 + dx]);
+              }
+            }
+          }
+          y[(((int64_t)b * Cout + co) * H + i) * W + j] = s;
+        }
+    }
+}
+
+/* Input gradient: dx[b][ci][i][j] = sum dy[b][co][i-dy+1][j-dx+1] w[co][ci][dy][dx]
+ * (the adjoint of the forward sum, written without the flip+swap rewrite that the
+ * reference's NPU path uses, conv_pack.cpp:470-473, so it checks that rewrite). */
+void oracle_conv3x3_dgrad(const uint16_t* dy, const uint16_t* w, double* dx, int B, int Cin,
+                          int Cout, int H, int W) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int ci = 0; ci < Cin; ++ci) {
+      for (int i = 0; i < H; ++i)
+        for (int j = 0; j < W; ++j) {
+          double s = 0.0;
+          for (int co = 0; co < Cout; ++co) {
+            const uint16_t* gp = dy + (((int64_t)b * Cout + co) * H) * W;
+            const uint16_t* wq = w + ((int64_t)co * Cin + ci) * 9;
+            for (int ky = 0; ky < 3; ++ky) {
+              const int oy = i - ky + 1;
+              if (oy < 0 || oy >= H) continue;
+              for (int kx = 0; kx < 3; ++kx) {
+                const int ox = j - kx + 1;
+                if (ox < 0 || ox >= W) continue;
+                s += (double)bf16f(gp[(int64_t)oy * W + ox]) * (double)bf16f(wq[ky * 3 + kx]);
+              }
+            }
+          }
+          dx[(((int64_t)b * Cin + ci) * H + i) * W + j] = s;
+        }
+    }
+}
+
+/* Weight gradient gw[co][ci][dy][dx] = sum_{b,i,j} dy[b][co][i][j] x[b][ci][i+dy-1][j+dx-1]
+ * (XdnaConv3x3wDwRuntime::compute, torch_xdna_device.cpp:2683-2751, in closed form),
+ * and gb[co] = sum dy[b][co][i][j] (the CPU bias gradient, :4850-4877). gb may be NULL. */
+void oracle_conv3x3_wgrad(const uint16_t* x, const uint16_t* dy, double* gw, double* gb, int B,
+                          int Cin, int Cout, int H, int W) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int co = 0; co < Cout; ++co)
+    for (int ci = 0; ci < Cin; ++ci) {
+      for (int ky = 0; ky < 3; ++ky)
+        for (int kx = 0; kx < 3; ++kx) {
+          double s = 0.0;
+          for (int b = 0; b < B; ++b) {
+            const uint16_t* gp = dy + (((int64_t)b * Cout + co) * H) * W;
+            const uint16_t* xp = x + (((int64_t)b * Cin + ci) * H) * W;
+            for (int i = 0; i < H; ++i) {
+              const int yy = i + ky - 1;
+              if (yy < 0 || yy >= H) continue;
+              for (int j = 0; j < W; ++j) {
+                const int xx = j + kx - 1;
+                if (xx < 0 || xx >= W) continue;
+                s += (double)bf16f(gp[(int64_t)i * W + j]) * (double)bf16f(xp[(int64_t)yy * W + xx]);
+              }
+            }
+          }
+          gw[(((int64_t)co * Cin + ci) * 3 + ky) * 3 + kx] = s;
+        }
+    }
+  if (gb) {
+    for (int co = 0; co < Cout; ++co) {
+      double s = 0.0;
+      for (int b = 0; b < B; ++b)
+        for (int64_t i = 0; i < (int64_t)H * W; ++i)
+          s += (double)bf16f(dy[((int64_t)b * Cout + co) * H * W + i]);
+      gb[co] = s;
+    }
+  }
+}
+
+/*
+ * Fused Adam / AdamW step on one tensor, fp32 opmath, in place.  Restates PyTorch's
+ * CPU _fused_adam_ / _fused_adamw_ (the kernel the reference's fallback runs for
+ * fused=True groups: xdna_train/device.py:408-436, torch_xdna_device.cpp:5124-5260),
+ * per element:
+ *   g = grad / grad_scale (written back), negated if maximize
+ *   Adam: g = fma(p, wd, g);   AdamW: p = p * float(1 - lr*wd)
+ *   m = fma(w, g - m, m), w = float(1 - beta1)   [fma(-(g - m), 1 - w, g) if |w| >= 0.5]
+ *   v = fma(float(1 - beta2) * g, g, v * float(beta2))
+ *   den = sqrt(amsgrad ? max(max_v, v) : v) / float(sqrt(1 - beta2^t)) + float(eps)
+ *   p = p - (float(lr / (1 - beta1^t)) * m) / den
+ * dtype 0 = fp32 arrays, 1 = bf16 bit arrays; every stored value is rounded once.
+ */
+void oracle_adam(void* p_, void* g_, void* m_, void* v_, void* mx_, int64_t n, int dtype,
+                 double step, double lr, double beta1, double beta2, double wd, double eps,
+                 int amsgrad, int maximize, int adamw, double grad_scale, int has_scale) {
+  const double bc1 = 1.0 - pow(beta1, step);
+  const double bc2 = 1.0 - pow(beta2, step);
+  const float step_size = (float)(lr / bc1);
+  const float bc2_sqrt = (float)sqrt(bc2);
+  const float w = (float)(1.0 - beta1);
+  const float one_minus_w = 1.0f - w;
+  const float b2 = (float)beta2, omb2 = (float)(1.0 - beta2), e = (float)eps;
+  const float wdf = (float)wd, decay = (float)(1.0 - lr * wd);
+  for (int64_t i = 0; i < n; ++i) {
+    float p, g, m, v, mx = 0.0f;
+    if (dtype == 1) {
+      p = bf16f(((uint16_t*)p_)[i]);
+      g = bf16f(((uint16_t*)g_)[i]);
+      m = bf16f(((uint16_t*)m_)[i]);
+      v = bf16f(((uint16_t*)v_)[i]);
+      if (amsgrad) mx = bf16f(((uint16_t*)mx_)[i]);
+    } else {
+      p = ((float*)p_)[i];
+      g = ((float*)g_)[i];
+      m = ((float*)m_)[i];
+      v = ((float*)v_)[i];
+      if (amsgrad) mx = ((float*)mx_)[i];
+    }
+    if (has_scale) {
+      g = g / (float)grad_scale;
+      if (dtype == 1) ((uint16_t*)g_)[i] = f2bf16(g);
+      else ((float*)g_)[i] = g;
+    }
+    if (maximize) g = -g;
+    if (wd != 0.0) {
+      if (adamw) p = p * decay;
+      else g = fmaf(p, wdf, g);
+    }
+    const float d = g - m;
+    m = fabsf(w) < 0.5f ? fmaf(w, d, m) : fmaf(-d, one_minus_w, g);
+    v = fmaf(omb2 * g, g, v * b2);
+    float src = v;
+    if (amsgrad) {
+      mx = mx > v ? mx : v;
+      src = mx;
+    }
+    const float den = sqrtf(src) / bc2_sqrt + e;
+    p = p - (step_size * m) / den;
+    if (dtype == 1) {
+      ((uint16_t*)p_)[i] = f2bf16(p);
+      ((uint16_t*)m_)[i] = f2bf16(m);
+      ((uint16_t*)v_)[i] = f2bf16(v);
+      if (amsgrad) ((uint16_t*)mx_)[i] = f2bf16(mx);
+    } else {
+      ((float*)p_)[i] = p;
+      ((float*)m_)[i] = m;
+      ((float*)v_)[i] = v;
+      if (amsgrad) ((float*)mx_)[i] = mx;
+    }
+  }
+}

@@ -1,0 +1,609 @@
+// 3x3 stride-1 pad-1 bf16 convolution on gfx950: forward, dgrad and wgrad as MFMA
+// implicit GEMMs with fp32 accumulation and one bf16 rounding.
+//
+// Forward / dgrad (reference: NPU design xdna_train/_designs/conv3x3w.py:8-29, 155-182
+// and runtime torch_xdna_device.cpp:2317-2483, 2515-2522).  The input is the
+// reference's packed padded-grid layout [groups][chunks][2126][64] (pack.hip).  For
+// output grid row p the 3x3 window is the nine rows p + dy*wp + dx, so
+//     out[co][p] = sum_{chunk, tap, c} Wt[co][(chunk*9 + tap)*64 + c] * X[p + off(tap)][c]
+// is a GEMM with M = output channels, N = grid rows, K = chunks*9*64.  A workgroup
+// owns 128 channels x TP rows of one group; per chunk it stages the TP + 2*wp + 2
+// input rows of its window (the halo tile) in LDS once and reads the nine taps as
+// shifted row windows of it.  Weights are prepared once per call into the A layout
+// [co][chunk][tap][64] (for dgrad with the flip+swap map of conv_pack.cpp:470-473).
+// The epilogue adds the bias in fp32, rounds once and writes NCHW directly (the
+// reference's unpack, conv_pack.cpp:706-743, fused), 32 consecutive pixels per store.
+//
+// Wgrad (reference: XdnaConv3x3wDwRuntime::compute, torch_xdna_device.cpp:2683-2751;
+// NPU design conv3x3w_dw.py).  Its reduction runs over pixels, so both operands are
+// re-laid out channel-major on a padded grid of pitch wp8 = roundup(W+2, 8):
+//     XT[ci][q]  = x[b][ci][yy-1][xx-1] at q = (b*(H+2) + yy)*wp8 + xx (zero border)
+//     DT[co][p]  = dy[b][co][y][x]      at p = (b*(H+2) + y)*wp8 + x   (zero elsewhere)
+//     gw[co][ci][dy][dx] = sum_p DT[co][p] * XT[ci][p + dy*wp8 + dx]
+// With wp8 a multiple of 8 the dy shift keeps 16-byte alignment; the dx = 1, 2 shifts
+// are built in registers from one 16-byte and one 4-byte LDS read (alignbit), so the
+// staged window serves all nine taps.  Pixels are split across workgroups (split-K);
+// partial sums go to a workspace and a second kernel adds them in a fixed order, so
+// every call returns the same bits.  The bias gradient rides along in the
+// first channel tile.
+#include "common.h"
+#include "mfma.h"
+#include "../../include/xdna_hip.h"
+
+#include <algorithm>
+
+namespace xdna {
+namespace {
+
+constexpr int kTCo = 128;            // output channels per workgroup
+constexpr int kPitch = 72;           // LDS row pitch (elements) of 64-wide tiles
+constexpr int kMaxHalo = 2 * (kMaxWidth + 4) + 2;  // 2*wp + 2 for wp <= 38 -> 78
+
+inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// ---------------------------------------------------------------------------------
+// Weight preparation: OIHW bf16 -> Wt[co_pad][chunks*9*64] (k order chunk, tap, c).
+// dgrad: the conv of dY (cin' = Cout channels) with w'[ci][co][t] = w[co][ci][8-t].
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prep_weights_kernel(const uint16_t* __restrict__ w,
+                                                           uint16_t* __restrict__ wt, int Cout,
+                                                           int Cin, int co_pad, int chunks,
+                                                           int dgrad) {
+  const int64_t K = int64_t(chunks) * 9 * kKStep;
+  const int64_t n = int64_t(co_pad) * K;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int row = int(i / K);          // output channel of this conv
+    const int k = int(i - int64_t(row) * K);
+    const int c = k % kKStep;
+    const int tap = (k / kKStep) % 9;
+    const int chunk = k / (kKStep * 9);
+    const int col = chunk * kKStep + c;  // input channel of this conv
+    uint16_t v = 0;
+    if (!dgrad) {
+      if (row < Cout && col < Cin) v = w[(int64_t(row) * Cin + col) * 9 + tap];
+    } else {
+      // this conv: out channel = forward ci (row), in channel = forward co (col)
+      if (row < Cin && col < Cout) v = w[(int64_t(col) * Cin + row) * 9 + (8 - tap)];
+    }
+    wt[i] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Implicit GEMM on packed rows.
+// ---------------------------------------------------------------------------------
+struct RowsArgs {
+  const uint16_t* xp;    // [groups][chunks][2126][64]
+  const uint16_t* wt;    // [co_pad][K]
+  const uint16_t* bias;  // [cout] or null
+  uint16_t* out;         // NCHW [B][cout][H][W]
+  int chunks, cout, wp, H, W, S, So;
+  int64_t img, m_total;
+};
+
+template <int TP>
+__global__ __launch_bounds__(256) void conv_rows_kernel(RowsArgs a) {
+  constexpr int kXRows = TP + kMaxHalo;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kXRows * kPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[kTCo * kPitch];
+
+  constexpr int tiles_per_group = kGroupOutRows / TP;
+  const int g = blockIdx.x / tiles_per_group;
+  const int r0 = (blockIdx.x % tiles_per_group) * TP;
+  if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;  // tail tile: no valid row
+  const int co0 = blockIdx.y * kTCo;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;  // wave tile: 64 channels x TP/2 rows
+  constexpr int NT = TP / 64;               // 32-row MFMA tiles per wave along N
+  const int K = a.chunks * 9 * kKStep;
+  const int nrows = TP + 2 * a.wp + 2;
+
+  f32x16_t acc[2][NT];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = zero_acc();
+
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  for (int ch = 0; ch < a.chunks; ++ch) {
+    __syncthreads();
+    const uint16_t* xsrc = a.xp + ((int64_t(g) * a.chunks + ch) * kGroupRows + r0) * kKStep;
+    for (int i = tid; i < nrows * 8; i += 256) {
+      const int row = i >> 3, q = i & 7;
+      *reinterpret_cast<uint4*>(xs + row * kPitch + q * 8) =
+          *reinterpret_cast<const uint4*>(xsrc + row * kKStep + q * 8);
+    }
+    for (int tap = 0; tap < 9; ++tap) {
+      if (tap) __syncthreads();
+      const uint16_t* wsrc = a.wt + int64_t(co0) * K + (ch * 9 + tap) * kKStep;
+      for (int i = tid; i < kTCo * 8; i += 256) {
+        const int row = i >> 3, q = i & 7;
+        *reinterpret_cast<uint4*>(ws + row * kPitch + q * 8) =
+            *reinterpret_cast<const uint4*>(wsrc + int64_t(row) * K + q * 8);
+      }
+      __syncthreads();
+      const int off = (tap / 3) * a.wp + (tap % 3);
+#pragma unroll
+      for (int ks = 0; ks < kKStep / 16; ++ks) {
+        bf16x8_t af[2], bfr[NT];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          af[mt] = as_bf16x8(*reinterpret_cast<const uint4*>(
+              ws + (wm * 64 + mt * 32 + lr) * kPitch + ks * 16 + lk));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          bfr[nt] = as_bf16x8(*reinterpret_cast<const uint4*>(
+              xs + (wn * (TP / 2) + nt * 32 + lr + off) * kPitch + ks * 16 + lk));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma_32x32x16(af[mt], bfr[nt], acc[mt][nt]);
+      }
+    }
+  }
+
+  // Epilogue: grid row -> NCHW pixel, bias in fp32, one rounding.
+  const int first = a.S == 1 ? 0 : 1;
+  const int64_t plane = int64_t(a.H) * a.W;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + nt * 32 + lr;
+    if (p >= a.m_total) continue;
+    const int64_t vb = p / a.img;
+    const int64_t rem = p - vb * a.img;
+    const int y = int(rem / a.wp);
+    const int col = int(rem - int64_t(y) * a.wp) - first;
+    if (y >= a.H || col < 0) continue;
+    const int b = int(vb / a.S), s = int(vb % a.S);
+    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+    if (col >= cols) continue;
+    const int x = (a.S == 1 ? 0 : s * a.So) + col;
+    uint16_t* obase = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * 64 + mt * 32 + mfma_row(i, lane);
+        if (co < a.cout) {
+          float v = acc[mt][nt][i];
+          if (a.bias) v += bf16_to_f32(a.bias[co]);
+          obase[int64_t(co) * plane] = f32_to_bf16(v);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Channel-major padded grid for wgrad.
+// ---------------------------------------------------------------------------------
+struct CmGeom {
+  int wp8 = 0;
+  int64_t img = 0, npix = 0, ktiles = 0, q = 0;  // q: row length (elements)
+};
+
+constexpr int kTK = 64;  // pixels per wgrad k-tile
+
+CmGeom cm_geom(int B, int H, int W) {
+  CmGeom g;
+  g.wp8 = int(ceil_div(W + 2, 8) * 8);
+  g.img = int64_t(H + 2) * g.wp8;
+  g.npix = int64_t(B) * g.img;
+  g.ktiles = ceil_div(g.npix, kTK);
+  g.q = g.ktiles * kTK + 2 * g.wp8 + 16;
+  return g;
+}
+
+// dst[c][q] for c < c_pad, q < qlen; shift = 1 places pixel (y, x) at grid (y+1, x+1)
+// (the conv input), shift = 0 at (y, x) (the output gradient).  Every element is
+// written (zeros outside the image and for c >= C).
+__global__ __launch_bounds__(256) void pack_cm_kernel(const uint16_t* __restrict__ src,
+                                                      uint16_t* __restrict__ dst, int B, int C,
+                                                      int H, int W, int c_pad, int wp8,
+                                                      int64_t img, int64_t qlen, int shift) {
+  const int64_t nvec_row = qlen / 8;
+  const int64_t n = int64_t(c_pad) * nvec_row;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int c = int(i / nvec_row);
+    const int64_t q0 = (i - int64_t(c) * nvec_row) * 8;
+    uint32_t u[4] = {0, 0, 0, 0};
+    const int64_t b = q0 / img;
+    if (c < C && b < B) {
+      const int64_t rem = q0 - b * img;
+      const int yy = int(rem / wp8) - shift;
+      const int xx0 = int(rem - int64_t(yy + shift) * wp8) - shift;
+      if (yy >= 0 && yy < H) {
+        const uint16_t* row = src + ((b * C + c) * H + yy) * W;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int xx = xx0 + e;
+          if (xx >= 0 && xx < W) {
+            const uint32_t h = row[xx];
+            u[e >> 1] |= (e & 1) ? (h << 16) : h;
+          }
+        }
+      }
+    }
+    *reinterpret_cast<uint4*>(dst + int64_t(c) * qlen + q0) = make_uint4(u[0], u[1], u[2], u[3]);
+  }
+}
+
+struct WgradArgs {
+  const uint16_t* xt;  // [ci_pad][q]
+  const uint16_t* dt;  // [co_pad][q]
+  float* part;         // [splits][co_pad][9][ci_pad]
+  float* bpart;        // [splits][co_pad]
+  int64_t q;           // row length of xt and dt
+  int wp8, ci_pad, co_pad;
+  int kt_per_split, ktiles;
+  int xpitch;          // LDS pitch of the staged x window (elements)
+  int wlen;            // staged window length (elements): kTK + 2*wp8 + 8
+};
+
+// LDS: dY tile [128][kPitch] then the x window [64][xpitch].
+__global__ __launch_bounds__(256) void wgrad_kernel(WgradArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* ds = smem;
+  uint16_t* xs = smem + kTCo * kPitch;
+  const int co0 = blockIdx.x * kTCo;
+  const int ci0 = blockIdx.y * 64;
+  const int split = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  const int kt0 = split * a.kt_per_split;
+  const int kt1 = min(a.ktiles, kt0 + a.kt_per_split);
+
+  f32x16_t acc[9][2];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) {
+    acc[t][0] = zero_acc();
+    acc[t][1] = zero_acc();
+  }
+  float bsum = 0.0f;
+  const bool do_bias = a.bpart && blockIdx.y == 0;
+  const int nvec_w = a.wlen / 8;
+
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int64_t k0 = int64_t(kt) * kTK;
+    __syncthreads();
+    for (int i = tid; i < kTCo * 8; i += 256) {
+      const int row = i >> 3, qv = i & 7;
+      *reinterpret_cast<uint4*>(ds + row * kPitch + qv * 8) =
+          *reinterpret_cast<const uint4*>(a.dt + int64_t(co0 + row) * a.q + k0 + qv * 8);
+    }
+    for (int i = tid; i < 64 * nvec_w; i += 256) {
+      const int row = i / nvec_w, qv = i - row * nvec_w;
+      *reinterpret_cast<uint4*>(xs + row * a.xpitch + qv * 8) =
+          *reinterpret_cast<const uint4*>(a.xt + int64_t(ci0 + row) * a.q + k0 + qv * 8);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ++ks) {
+      const uint4 av = *reinterpret_cast<const uint4*>(ds + (wave * 32 + lr) * kPitch + ks * 16 + lk);
+      if (do_bias) {
+        const uint32_t u[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bsum += __uint_as_float(u[e] << 16) + __uint_as_float(u[e] & 0xFFFF0000u);
+      }
+      const bf16x8_t af = as_bf16x8(av);
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint16_t* src = xs + (h * 32 + lr) * a.xpitch + ks * 16 + lk + dy * a.wp8;
+          const uint4 lo = *reinterpret_cast<const uint4*>(src);
+          const uint32_t hi = *reinterpret_cast<const uint32_t*>(src + 8);
+          const uint4 s1 = make_uint4(__builtin_amdgcn_alignbit(lo.y, lo.x, 16),
+                                      __builtin_amdgcn_alignbit(lo.z, lo.y, 16),
+                                      __builtin_amdgcn_alignbit(lo.w, lo.z, 16),
+                                      __builtin_amdgcn_alignbit(hi, lo.w, 16));
+          const uint4 s2 = make_uint4(lo.y, lo.z, lo.w, hi);
+          acc[dy * 3 + 0][h] = mfma_32x32x16(af, as_bf16x8(lo), acc[dy * 3 + 0][h]);
+          acc[dy * 3 + 1][h] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1][h]);
+          acc[dy * 3 + 2][h] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2][h]);
+        }
+    }
+  }
+
+  // Partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci.
+  float* pbase = a.part + int64_t(split) * a.co_pad * 9 * a.ci_pad;
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wave * 32 + mfma_row(i, lane);
+        const int ci = ci0 + h * 32 + lr;
+        pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][h][i];
+      }
+  if (do_bias) {
+    // lane l and l+32 hold the two k-halves of channel row l%32.
+    const float other = __shfl_down(bsum, 32, 64);
+    if (lane < 32) a.bpart[int64_t(split) * a.co_pad + co0 + wave * 32 + lane] = bsum + other;
+  }
+}
+
+// gw[co][ci][tap] = bf16(sum_s part[s][co][tap][ci]), gb[co] = bf16(sum_s bpart[s][co]),
+// summed in split order.
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part,
+                                                           const float* __restrict__ bpart,
+                                                           uint16_t* __restrict__ gw,
+                                                           uint16_t* __restrict__ gb, int Cout,
+                                                           int Cin, int co_pad, int ci_pad,
+                                                           int splits) {
+  const int64_t n = int64_t(Cout) * 9 * Cin;
+  const int64_t stride = int64_t(co_pad) * 9 * ci_pad;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n + Cout;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    if (i < n) {
+      const int ci = int(i % Cin);
+      const int t = int((i / Cin) % 9);
+      const int co = int(i / (int64_t(Cin) * 9));
+      const float* src = part + (int64_t(co) * 9 + t) * ci_pad + ci;
+      float s = 0.0f;
+      for (int k = 0; k < splits; ++k) s += src[k * stride];
+      gw[(int64_t(co) * Cin + ci) * 9 + t] = f32_to_bf16(s);
+    } else if (gb) {
+      const int co = int(i - n);
+      float s = 0.0f;
+      for (int k = 0; k < splits; ++k) s += bpart[int64_t(k) * co_pad + co];
+      gb[co] = f32_to_bf16(s);
+    }
+  }
+}
+
+// Bias gradient on its own: one workgroup per channel, fixed-order tree.
+__global__ __launch_bounds__(256) void bias_grad_kernel(const uint16_t* __restrict__ dy,
+                                                        uint16_t* __restrict__ gb, int B, int C,
+                                                        int64_t plane) {
+  const int c = blockIdx.x;
+  float s = 0.0f;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* src = dy + (int64_t(b) * C + c) * plane;
+    for (int64_t i = threadIdx.x; i < plane; i += blockDim.x) s += bf16_to_f32(src[i]);
+  }
+  __shared__ float red[256];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (int(threadIdx.x) < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) gb[c] = f32_to_bf16(red[0]);
+}
+
+// ---------------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------------
+
+struct FwdPlan {
+  ConvGeom geom;
+  int chunks = 0, co_pad = 0;
+  size_t packed_bytes = 0, wt_bytes = 0;
+};
+
+FwdPlan fwd_plan(int B, int Cin, int Cout, int H, int W) {
+  FwdPlan p;
+  p.geom = conv_geom(B, H, W);
+  p.chunks = int(ceil_div(Cin, kKStep));
+  p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
+  p.packed_bytes = align256(size_t(p.geom.groups) * p.chunks * kGroupRows * kKStep * 2);
+  p.wt_bytes = align256(size_t(p.co_pad) * p.chunks * 9 * kKStep * 2);
+  return p;
+}
+
+bool shape_ok(const char* what, int B, int Cin, int Cout, int H, int W) {
+  if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1) {
+    set_error(std::string(what) + ": invalid shape");
+    return false;
+  }
+  return true;
+}
+
+int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, int chunks,
+                int dgrad, void* stream) {
+  if (!admit_launch("conv3x3 weight preparation")) return -1;
+  const int64_t n = int64_t(co_pad) * chunks * 9 * kKStep;
+  const int blocks = int(std::min<int64_t>(ceil_div(n, 256), 4096));
+  prep_weights_kernel<<<blocks, 256, 0, as_stream(stream)>>>(w, wt, Cout, Cin, co_pad, chunks, dgrad);
+  return check_launch("conv3x3 weight preparation");
+}
+
+// conv of packed input xp (cin channels) with prepared weights -> NCHW out (cout channels).
+int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
+                int B, int cin, int cout, int H, int W, void* stream) {
+  const ConvGeom geom = conv_geom(B, H, W);
+  RowsArgs a;
+  a.xp = xp;
+  a.wt = wt;
+  a.bias = bias;
+  a.out = out;
+  a.chunks = int(ceil_div(cin, kKStep));
+  a.cout = cout;
+  a.wp = geom.st.wp;
+  a.H = H;
+  a.W = W;
+  a.S = geom.st.S;
+  a.So = geom.st.So;
+  a.img = geom.img;
+  a.m_total = geom.m_total;
+  if (!admit_launch("conv3x3 rows")) return -1;
+  const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
+  // Small problems: 64-row tiles to put more workgroups on the 256 CUs.
+  const int64_t big_tiles = int64_t(geom.groups) * (kGroupOutRows / 128) * ytiles;
+  if (big_tiles >= 512) {
+    conv_rows_kernel<128><<<dim3(unsigned(geom.groups * (kGroupOutRows / 128)), ytiles), 256, 0,
+                            as_stream(stream)>>>(a);
+  } else {
+    conv_rows_kernel<64><<<dim3(unsigned(geom.groups * (kGroupOutRows / 64)), ytiles), 256, 0,
+                           as_stream(stream)>>>(a);
+  }
+  return check_launch("conv3x3 rows");
+}
+
+struct WgradPlan {
+  CmGeom cm;
+  int ci_pad = 0, co_pad = 0, splits = 0, kt_per = 0, xpitch = 0, wlen = 0;
+  size_t xt_bytes = 0, dt_bytes = 0, part_bytes = 0, bpart_bytes = 0;
+  size_t lds_bytes = 0;
+};
+
+WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
+  WgradPlan p;
+  p.cm = cm_geom(B, H, W);
+  p.ci_pad = int(ceil_div(Cin, 64) * 64);
+  p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
+  const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
+  const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
+  // Enough workgroups to cover the CUs twice, capped so the fp32 partials stay
+  // within ~32 MiB (they live in the MALL between the two kernels).
+  int64_t splits = ceil_div(512, tiles);
+  const int64_t cap = std::max<int64_t>(1, (int64_t(32) << 20) / (out_elems * 4));
+  splits = std::max<int64_t>(1, std::min({splits, cap, p.cm.ktiles}));
+  p.kt_per = int(ceil_div(p.cm.ktiles, splits));
+  p.splits = int(ceil_div(p.cm.ktiles, p.kt_per));
+  p.wlen = kTK + 2 * p.cm.wp8 + 8;
+  p.xpitch = int(ceil_div(p.wlen, 16) * 16 + 8);
+  p.xt_bytes = align256(size_t(p.ci_pad) * p.cm.q * 2);
+  p.dt_bytes = align256(size_t(p.co_pad) * p.cm.q * 2);
+  p.part_bytes = align256(size_t(p.splits) * out_elems * 4);
+  p.bpart_bytes = align256(size_t(p.splits) * p.co_pad * 4);
+  p.lds_bytes = size_t(kTCo) * kPitch * 2 + size_t(64) * p.xpitch * 2;
+  return p;
+}
+
+constexpr size_t kMaxWgradLds = 64 * 1024;
+
+}  // namespace
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" {
+
+size_t xdna_conv3x3_fwd_workspace_bytes(int B, int Cin, int Cout, int H, int W) {
+  if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1) return 0;
+  const FwdPlan p = fwd_plan(B, Cin, Cout, H, W);
+  return p.packed_bytes + p.wt_bytes;
+}
+
+int xdna_conv3x3_fwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* y,
+                          int B, int Cin, int Cout, int H, int W, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (!shape_ok("xdna_conv3x3_fwd_bf16", B, Cin, Cout, H, W)) return -1;
+  const FwdPlan p = fwd_plan(B, Cin, Cout, H, W);
+  if (!workspace || workspace_bytes < p.packed_bytes + p.wt_bytes) {
+    set_error("xdna_conv3x3_fwd_bf16: workspace too small");
+    return -1;
+  }
+  uint16_t* xp = static_cast<uint16_t*>(workspace);
+  uint16_t* wt = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.packed_bytes);
+  if (xdna_hip_memset_async(xp, 0, p.packed_bytes, stream)) return -1;
+  if (xdna_conv3x3w_pack_input_strips_range_bf16(x, xp, B, Cin, H, W, p.geom.st.S, p.geom.st.So, 0,
+                                                 p.chunks, 0, p.geom.groups, stream))
+    return -1;
+  if (launch_prep(w, wt, Cout, Cin, p.co_pad, p.chunks, 0, stream)) return -1;
+  return launch_rows(xp, wt, bias, y, B, Cin, Cout, H, W, stream);
+}
+
+size_t xdna_conv3x3_dgrad_workspace_bytes(int B, int Cin, int Cout, int H, int W) {
+  // dgrad is the forward conv of dY (Cout channels) into Cin channels.
+  return xdna_conv3x3_fwd_workspace_bytes(B, Cout, Cin, H, W);
+}
+
+int xdna_conv3x3_dgrad_bf16(const uint16_t* dy, const uint16_t* w, uint16_t* dx, int B, int Cin,
+                            int Cout, int H, int W, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  if (!shape_ok("xdna_conv3x3_dgrad_bf16", B, Cin, Cout, H, W)) return -1;
+  const FwdPlan p = fwd_plan(B, Cout, Cin, H, W);
+  if (!workspace || workspace_bytes < p.packed_bytes + p.wt_bytes) {
+    set_error("xdna_conv3x3_dgrad_bf16: workspace too small");
+    return -1;
+  }
+  uint16_t* dp = static_cast<uint16_t*>(workspace);
+  uint16_t* wt = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.packed_bytes);
+  if (xdna_hip_memset_async(dp, 0, p.packed_bytes, stream)) return -1;
+  if (xdna_conv3x3w_pack_input_strips_range_bf16(dy, dp, B, Cout, H, W, p.geom.st.S, p.geom.st.So,
+                                                 0, p.chunks, 0, p.geom.groups, stream))
+    return -1;
+  if (launch_prep(w, wt, Cout, Cin, p.co_pad, p.chunks, 1, stream)) return -1;
+  return launch_rows(dp, wt, nullptr, dx, B, Cout, Cin, H, W, stream);
+}
+
+size_t xdna_conv3x3_wgrad_workspace_bytes(int B, int Cin, int Cout, int H, int W) {
+  if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1) return 0;
+  const WgradPlan p = wgrad_plan(B, Cin, Cout, H, W);
+  return p.xt_bytes + p.dt_bytes + p.part_bytes + p.bpart_bytes;
+}
+
+int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, uint16_t* gb,
+                            int B, int Cin, int Cout, int H, int W, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (!shape_ok("xdna_conv3x3_wgrad_bf16", B, Cin, Cout, H, W)) return -1;
+  const WgradPlan p = wgrad_plan(B, Cin, Cout, H, W);
+  if (p.lds_bytes > kMaxWgradLds) {
+    set_error("xdna_conv3x3_wgrad_bf16: image too wide for the LDS window");
+    return -1;
+  }
+  const size_t need = p.xt_bytes + p.dt_bytes + p.part_bytes + p.bpart_bytes;
+  if (!workspace || workspace_bytes < need) {
+    set_error("xdna_conv3x3_wgrad_bf16: workspace too small");
+    return -1;
+  }
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* xt = reinterpret_cast<uint16_t*>(ws);
+  uint16_t* dt = reinterpret_cast<uint16_t*>(ws + p.xt_bytes);
+  float* part = reinterpret_cast<float*>(ws + p.xt_bytes + p.dt_bytes);
+  float* bpart = reinterpret_cast<float*>(ws + p.xt_bytes + p.dt_bytes + p.part_bytes);
+  hipStream_t st = as_stream(stream);
+
+  if (!admit_launch("conv3x3 wgrad pack")) return -1;
+  {
+    const int64_t nx = int64_t(p.ci_pad) * (p.cm.q / 8);
+    pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nx, 256), 16384)), 256, 0, st>>>(
+        x, xt, B, Cin, H, W, p.ci_pad, p.cm.wp8, p.cm.img, p.cm.q, 1);
+    const int64_t nd = int64_t(p.co_pad) * (p.cm.q / 8);
+    pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nd, 256), 16384)), 256, 0, st>>>(
+        dy, dt, B, Cout, H, W, p.co_pad, p.cm.wp8, p.cm.img, p.cm.q, 0);
+  }
+  if (check_launch("conv3x3 wgrad pack")) return -1;
+
+  if (!admit_launch("conv3x3 wgrad")) return -1;
+  WgradArgs a;
+  a.xt = xt;
+  a.dt = dt;
+  a.part = part;
+  a.bpart = gb ? bpart : nullptr;
+  a.q = p.cm.q;
+  a.wp8 = p.cm.wp8;
+  a.ci_pad = p.ci_pad;
+  a.co_pad = p.co_pad;
+  a.kt_per_split = p.kt_per;
+  a.ktiles = int(p.cm.ktiles);
+  a.xpitch = p.xpitch;
+  a.wlen = p.wlen;
+  wgrad_kernel<<<dim3(unsigned(p.co_pad / kTCo), unsigned(p.ci_pad / 64), unsigned(p.splits)), 256,
+                 p.lds_bytes, st>>>(a);
+  if (check_launch("conv3x3 wgrad")) return -1;
+
+  if (!admit_launch("conv3x3 wgrad reduce")) return -1;
+  const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
+  wgrad_reduce_kernel<<<int(std::min<int64_t>(ceil_div(n, 256), 8192)), 256, 0, st>>>(
+      part, bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  return check_launch("conv3x3 wgrad reduce");
+}
+
+int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H, int W,
+                                void* stream) {
+  if (B < 1 || C < 1 || H < 1 || W < 1) {
+    set_error("xdna_conv3x3_bias_grad_bf16: invalid shape");
+    return -1;
+  }
+  if (!admit_launch("xdna_conv3x3_bias_grad_bf16")) return -1;
+  bias_grad_kernel<<<C, 256, 0, as_stream(stream)>>>(dy, gb, B, C, int64_t(H) * W);
+  return check_launch("xdna_conv3x3_bias_grad_bf16");
+}
+
+}  // extern "C"

@@ -1,0 +1,224 @@
+// bf16 GEMM on gfx950 MFMA: C = alpha * A.B + beta * bias, fp32 accumulation, one
+// bf16 rounding.  Replaces the reference's fixed-shape NPU GEMM and its CPU mm/addmm/
+// bmm on aliases (torch_xdna_device.cpp:1330-1458, 3740-3790, 4360-4417): any shape,
+// any element strides, so Linear's forward (B = W^T, k-contiguous), dX (B = W,
+// n-contiguous) and dW (A = dY^T, m-contiguous) run without copies.
+//
+// Tiles: 128 x 128 x 32 per workgroup, four waves of 64 x 64 (2 x 2 MFMA 32x32x16).
+// Both LDS tiles are stored k-contiguous ([row][k], pitch 40 elements) so every MFMA
+// fragment is one 16-byte LDS read.  Staging picks per operand: 16-byte vector loads
+// along k (k-contiguous source), 16-byte loads along m/n written transposed into LDS
+// (m/n-contiguous source), or element loads (anything else, and the ragged edges).
+#include "common.h"
+#include "mfma.h"
+#include "../../include/xdna_hip.h"
+
+namespace xdna {
+namespace {
+
+constexpr int kTM = 128, kTN = 128, kTK = 32, kLdsPitch = 40;
+
+enum StageMode { kAlongK = 0, kAlongRow = 1, kScalar = 2 };
+
+struct GemmArgs {
+  const uint16_t* a;
+  const uint16_t* b;
+  uint16_t* c;
+  const uint16_t* bias;
+  int M, N, K;
+  int64_t a_r, a_k, a_batch;  // A element (row=m, k) strides
+  int64_t b_r, b_k, b_batch;  // B as [n][k]: element (row=n, k) strides
+  int64_t c_m, c_n, c_batch;
+  int bias_mode;
+  int64_t bias_sm, bias_sn;
+  float alpha, beta;
+};
+
+// Stages rows [r0, r0+128) x k [k0, k0+32) of a row-major-by-strides operand into
+// lds[row][k].  rows: valid row count; K: valid k count.
+template <int kMode>
+__device__ inline void stage(uint16_t* lds, const uint16_t* src, int64_t s_r, int64_t s_k, int r0,
+                             int rows, int k0, int K, int tid) {
+  if (kMode == kAlongK) {
+    // 128 rows x 4 vectors of 8 k.
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int i = tid + it * 256;
+      const int row = i >> 2, kv = (i & 3) * 8;
+      const int r = r0 + row, k = k0 + kv;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (r < rows) {
+        const uint16_t* p = src + int64_t(r) * s_r + k;
+        if (k + 8 <= K) {
+          v = *reinterpret_cast<const uint4*>(p);
+        } else {
+          uint32_t u[4] = {0, 0, 0, 0};
+          for (int e = 0; e < 8; ++e)
+            if (k + e < K) u[e >> 1] |= uint32_t(p[e]) << ((e & 1) * 16);
+          v = make_uint4(u[0], u[1], u[2], u[3]);
+        }
+      }
+      *reinterpret_cast<uint4*>(lds + row * kLdsPitch + kv) = v;
+    }
+  } else if (kMode == kAlongRow) {
+    // 32 k x 16 vectors of 8 rows; each vector is written transposed.
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int i = tid + it * 256;
+      const int kk = i >> 4, rv = (i & 15) * 8;
+      const int r = r0 + rv, k = k0 + kk;
+      uint32_t u[4] = {0, 0, 0, 0};
+      if (k < K) {
+        const uint16_t* p = src + int64_t(k) * s_k + r;
+        if (r + 8 <= rows) {
+          const uint4 v = *reinterpret_cast<const uint4*>(p);
+          u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+        } else {
+          for (int e = 0; e < 8; ++e)
+            if (r + e < rows) u[e >> 1] |= uint32_t(p[e]) << ((e & 1) * 16);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        lds[(rv + e) * kLdsPitch + kk] = uint16_t((e & 1) ? (u[e >> 1] >> 16) : (u[e >> 1] & 0xFFFF));
+    }
+  } else {
+    for (int i = tid; i < 128 * kTK; i += 256) {
+      const int row = i / kTK, kk = i - row * kTK;
+      const int r = r0 + row, k = k0 + kk;
+      lds[row * kLdsPitch + kk] = (r < rows && k < K) ? src[int64_t(r) * s_r + int64_t(k) * s_k] : 0;
+    }
+  }
+}
+
+template <int kModeA, int kModeB>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t as[kTM * kLdsPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t bs[kTN * kLdsPitch];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kTM, n0 = blockIdx.x * kTN;
+  const int batch = blockIdx.z;
+  const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
+  const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero_acc();
+
+  for (int k0 = 0; k0 < g.K; k0 += kTK) {
+    __syncthreads();
+    stage<kModeA>(as, A, g.a_r, g.a_k, m0, g.M, k0, g.K, tid);
+    stage<kModeB>(bs, B, g.b_r, g.b_k, n0, g.N, k0, g.K, tid);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ++ks) {
+      bf16x8_t af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = as_bf16x8(*reinterpret_cast<const uint4*>(as + (wm * 64 + i * 32 + lr) * kLdsPitch + ks * 16 + lk));
+        bfr[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn * 64 + i * 32 + lr) * kLdsPitch + ks * 16 + lk));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_32x32x16(af[i], bfr[j], acc[i][j]);
+    }
+  }
+
+  uint16_t* C = g.c + int64_t(batch) * g.c_batch;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 64 + j * 32 + lr;
+      if (n >= g.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + mfma_row(r, lane);
+        if (m >= g.M) continue;
+        float v = g.alpha * acc[i][j][r];
+        if (g.bias_mode && g.beta != 0.0f) {
+          float bv;
+          if (g.bias_mode == 1) bv = bf16_to_f32(g.bias[int64_t(n) * g.bias_sn]);
+          else if (g.bias_mode == 2) bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm + int64_t(n) * g.bias_sn]);
+          else bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm]);
+          v += g.beta * bv;
+        }
+        C[int64_t(m) * g.c_m + int64_t(n) * g.c_n] = f32_to_bf16(v);
+      }
+    }
+}
+
+// Operand described as [rows][k] with element strides (s_r, s_k).
+int stage_mode(const void* base, int64_t s_r, int64_t s_k, int64_t s_batch, int batch) {
+  const bool a16 = (reinterpret_cast<uintptr_t>(base) & 15) == 0;
+  const bool batch_ok = batch <= 1 || (s_batch % 8) == 0;
+  if (s_k == 1 && a16 && (s_r % 8) == 0 && batch_ok) return kAlongK;
+  if (s_r == 1 && a16 && (s_k % 8) == 0 && batch_ok) return kAlongRow;
+  return kScalar;
+}
+
+template <int MA>
+void launch_b(int mb, dim3 grid, hipStream_t st, const GemmArgs& g) {
+  if (mb == kAlongK) gemm_kernel<MA, kAlongK><<<grid, 256, 0, st>>>(g);
+  else if (mb == kAlongRow) gemm_kernel<MA, kAlongRow><<<grid, 256, 0, st>>>(g);
+  else gemm_kernel<MA, kScalar><<<grid, 256, 0, st>>>(g);
+}
+
+}  // namespace
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C,
+                              const uint16_t* bias, int batch, int M, int N, int K, int64_t lda_m,
+                              int64_t lda_k, int64_t stride_a, int64_t ldb_k, int64_t ldb_n,
+                              int64_t stride_b, int64_t ldc_m, int64_t ldc_n, int64_t stride_c,
+                              int bias_mode, int64_t bias_sm, int64_t bias_sn, float alpha,
+                              float beta, void* stream) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0 || bias_mode < 0 || bias_mode > 3 ||
+      (bias_mode && !bias)) {
+    set_error("xdna_gemm_bf16: invalid arguments");
+    return -1;
+  }
+  if (batch == 0 || M == 0 || N == 0) return 0;
+  if (batch > 65535) {
+    set_error("xdna_gemm_bf16: batch too large");
+    return -1;
+  }
+  GemmArgs g;
+  g.a = A;
+  g.b = Bm;
+  g.c = C;
+  g.bias = bias;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.a_r = lda_m;
+  g.a_k = lda_k;
+  g.a_batch = stride_a;
+  g.b_r = ldb_n;  // B is staged as [n][k]
+  g.b_k = ldb_k;
+  g.b_batch = stride_b;
+  g.c_m = ldc_m;
+  g.c_n = ldc_n;
+  g.c_batch = stride_c;
+  g.bias_mode = bias_mode;
+  g.bias_sm = bias_sm;
+  g.bias_sn = bias_sn;
+  g.alpha = alpha;
+  g.beta = beta;
+  const int ma = stage_mode(A, lda_m, lda_k, stride_a, batch);
+  const int mb = stage_mode(Bm, ldb_n, ldb_k, stride_b, batch);
+  if (!admit_launch("xdna_gemm_bf16")) return -1;
+  const dim3 grid(unsigned(ceil_div(N, kTN)), unsigned(ceil_div(M, kTM)), unsigned(batch));
+  hipStream_t st = as_stream(stream);
+  if (ma == kAlongK) launch_b<kAlongK>(mb, grid, st, g);
+  else if (ma == kAlongRow) launch_b<kAlongRow>(mb, grid, st, g);
+  else launch_b<kScalar>(mb, grid, st, g);
+  return check_launch("xdna_gemm_bf16");
+}

@@ -1,0 +1,342 @@
+// Device, memory, stream and event entry points of the C ABI, plus the error,
+// poisoning and failure-injection state every launcher goes through.
+//
+// The reference's XRT shim keeps a thread-local error string and poisons the process
+// when a dispatch cannot be aborted (xdna_train/_vendor/xrt_shim/xrt_shim.cpp:57-249);
+// this is the HIP counterpart.  The caching allocator plays the role of XdnaBoCache
+// (torch_xdna_device.cpp:205-296): size bins, reuse counters, a byte budget.
+#include "common.h"
+#include "../../include/xdna_hip.h"
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+
+namespace xdna {
+
+namespace {
+thread_local std::string t_error;
+std::atomic<bool> g_poisoned{false};
+std::atomic<int64_t> g_launches{0};
+std::atomic<int64_t> g_inject_at{0};     // absolute launch number that fails (0: off)
+std::atomic<int> g_inject_poison{0};
+}  // namespace
+
+void set_error(const std::string& msg) { t_error = msg; }
+void clear_error() { t_error.clear(); }
+
+bool admit_launch(const char* what) {
+  if (g_poisoned.load(std::memory_order_acquire)) {
+    set_error(std::string(what) + ": refused, the process is poisoned by an earlier failure");
+    return false;
+  }
+  const int64_t n = g_launches.fetch_add(1, std::memory_order_relaxed) + 1;
+  const int64_t at = g_inject_at.load(std::memory_order_relaxed);
+  if (at != 0 && n == at) {
+    g_inject_at.store(0, std::memory_order_relaxed);
+    if (g_inject_poison.load(std::memory_order_relaxed)) g_poisoned.store(true);
+    set_error(std::string(what) + ": injected failure");
+    return false;
+  }
+  return true;
+}
+
+int launch_failed(const char* what, hipError_t err) {
+  // Errors that can leave device work in flight poison the process: later frees
+  // leak and later launches are refused (xrt_shim.cpp:139-151).
+  if (err == hipErrorLaunchFailure || err == hipErrorIllegalAddress ||
+      err == hipErrorLaunchTimeOut || err == hipErrorAssert) {
+    g_poisoned.store(true);
+  }
+  set_error(std::string(what) + ": " + hipGetErrorString(err));
+  return -1;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return launch_failed(what, err);
+  return 0;
+}
+
+// ---- caching allocator ---------------------------------------------------------
+
+namespace {
+
+struct Cache {
+  std::mutex mu;
+  std::multimap<size_t, void*> free_blocks;       // rounded size -> block
+  std::unordered_map<void*, size_t> live;         // block -> rounded size
+  int64_t cached = 0, allocated = 0, max_allocated = 0;
+  int64_t fresh = 0, reuses = 0, frees = 0;
+};
+
+Cache& cache() {
+  static auto* c = new Cache();  // never destroyed: frees can run at exit
+  return *c;
+}
+
+size_t round_size(size_t n) {
+  if (n == 0) n = 1;
+  if (n <= (size_t(1) << 20)) return (n + 511) & ~size_t(511);
+  const size_t big = size_t(2) << 20;
+  return (n + big - 1) / big * big;
+}
+
+}  // namespace
+
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" {
+
+const char* xdna_hip_last_error(void) { return t_error.c_str(); }
+
+int xdna_hip_poisoned(void) { return g_poisoned.load() ? 1 : 0; }
+
+int xdna_hip_inject_failure(int64_t nth_launch, int poison) {
+  if (nth_launch < 0) {
+    set_error("xdna_hip_inject_failure: negative launch index");
+    return -1;
+  }
+  g_inject_poison.store(poison ? 1 : 0);
+  g_inject_at.store(nth_launch == 0 ? 0 : g_launches.load() + nth_launch);
+  return 0;
+}
+
+int xdna_hip_reset_failure_state(void) {
+  g_poisoned.store(false);
+  g_inject_at.store(0);
+  g_inject_poison.store(0);
+  return 0;
+}
+
+int64_t xdna_hip_launch_count(void) { return g_launches.load(); }
+
+int xdna_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+int xdna_hip_set_device(int device) {
+  const hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return launch_failed("hipSetDevice", e);
+  return 0;
+}
+
+int xdna_hip_get_device(int* device) {
+  const hipError_t e = hipGetDevice(device);
+  if (e != hipSuccess) return launch_failed("hipGetDevice", e);
+  return 0;
+}
+
+int xdna_hip_device_properties(char* name, size_t name_len, int* cu_count, size_t* total_mem,
+                               int* gcn_arch) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return launch_failed("hipGetDevice", e);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return launch_failed("hipGetDeviceProperties", e);
+  if (name && name_len) {
+    std::snprintf(name, name_len, "%s", prop.gcnArchName);
+  }
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (total_mem) *total_mem = prop.totalGlobalMem;
+  if (gcn_arch) *gcn_arch = prop.major * 100 + prop.minor * 10;  // gfx950 -> 950
+  return 0;
+}
+
+void* xdna_hip_malloc(size_t bytes) {
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    launch_failed("hipMalloc", e);
+    return nullptr;
+  }
+  return p;
+}
+
+int xdna_hip_free(void* ptr) {
+  if (!ptr) return 0;
+  if (g_poisoned.load()) return 0;  // device work may still use it: leak
+  const hipError_t e = hipFree(ptr);
+  if (e != hipSuccess) return launch_failed("hipFree", e);
+  return 0;
+}
+
+void* xdna_hip_cache_alloc(size_t bytes) {
+  Cache& c = cache();
+  const size_t n = round_size(bytes);
+  {
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto it = c.free_blocks.find(n);
+    if (it != c.free_blocks.end()) {
+      void* p = it->second;
+      c.free_blocks.erase(it);
+      c.cached -= int64_t(n);
+      c.live.emplace(p, n);
+      c.allocated += int64_t(n);
+      if (c.allocated > c.max_allocated) c.max_allocated = c.allocated;
+      ++c.reuses;
+      return p;
+    }
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, n);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    // Out of memory: give the cached blocks back and retry once.
+    xdna_hip_cache_empty();
+    e = hipMalloc(&p, n);
+    if (e != hipSuccess) {
+      launch_failed("xdna_hip_cache_alloc", e);
+      return nullptr;
+    }
+  }
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.live.emplace(p, n);
+  c.allocated += int64_t(n);
+  if (c.allocated > c.max_allocated) c.max_allocated = c.allocated;
+  ++c.fresh;
+  return p;
+}
+
+int xdna_hip_cache_free(void* ptr) {
+  if (!ptr) return 0;
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  auto it = c.live.find(ptr);
+  if (it == c.live.end()) {
+    set_error("xdna_hip_cache_free: pointer was not allocated by the cache");
+    return -1;
+  }
+  const size_t n = it->second;
+  c.live.erase(it);
+  c.allocated -= int64_t(n);
+  ++c.frees;
+  if (g_poisoned.load()) return 0;  // a stuck launch may still use it: never recycle
+  c.free_blocks.emplace(n, ptr);
+  c.cached += int64_t(n);
+  return 0;
+}
+
+int xdna_hip_cache_empty(void) {
+  Cache& c = cache();
+  std::multimap<size_t, void*> blocks;
+  {
+    std::lock_guard<std::mutex> lock(c.mu);
+    blocks.swap(c.free_blocks);
+    c.cached = 0;
+  }
+  if (blocks.empty()) return 0;
+  // Blocks may still be read by queued work on any stream.
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return launch_failed("xdna_hip_cache_empty", e);
+  for (auto& kv : blocks) {
+    e = hipFree(kv.second);
+    if (e != hipSuccess) return launch_failed("hipFree", e);
+  }
+  return 0;
+}
+
+int xdna_hip_cache_stats(int64_t* stats, int n) {
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  const int64_t v[6] = {c.cached, c.allocated, c.max_allocated, c.fresh, c.reuses, c.frees};
+  for (int i = 0; i < n && i < 6; ++i) stats[i] = v[i];
+  return 0;
+}
+
+int xdna_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+  if (bytes == 0) return 0;
+  hipMemcpyKind k = hipMemcpyDefault;
+  switch (kind) {
+    case 1: k = hipMemcpyHostToDevice; break;
+    case 2: k = hipMemcpyDeviceToHost; break;
+    case 3: k = hipMemcpyDeviceToDevice; break;
+    default: k = hipMemcpyDefault; break;
+  }
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, k, as_stream(stream));
+  if (e != hipSuccess) return launch_failed("hipMemcpyAsync", e);
+  return 0;
+}
+
+int xdna_hip_memset_async(void* dst, int value, size_t bytes, void* stream) {
+  if (bytes == 0) return 0;
+  const hipError_t e = hipMemsetAsync(dst, value, bytes, as_stream(stream));
+  if (e != hipSuccess) return launch_failed("hipMemsetAsync", e);
+  return 0;
+}
+
+int xdna_hip_stream_synchronize(void* stream) {
+  const hipError_t e = hipStreamSynchronize(as_stream(stream));
+  if (e != hipSuccess) return launch_failed("hipStreamSynchronize", e);
+  return 0;
+}
+
+int xdna_hip_device_synchronize(void) {
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return launch_failed("hipDeviceSynchronize", e);
+  return 0;
+}
+
+void* xdna_hip_event_create(int timing) {
+  hipEvent_t ev = nullptr;
+  const hipError_t e =
+      hipEventCreateWithFlags(&ev, timing ? hipEventDefault : hipEventDisableTiming);
+  if (e != hipSuccess) {
+    launch_failed("hipEventCreate", e);
+    return nullptr;
+  }
+  return ev;
+}
+
+int xdna_hip_event_destroy(void* event) {
+  if (!event) return 0;
+  const hipError_t e = hipEventDestroy(reinterpret_cast<hipEvent_t>(event));
+  if (e != hipSuccess) return launch_failed("hipEventDestroy", e);
+  return 0;
+}
+
+int xdna_hip_event_record(void* event, void* stream) {
+  const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream));
+  if (e != hipSuccess) return launch_failed("hipEventRecord", e);
+  return 0;
+}
+
+int xdna_hip_event_synchronize(void* event) {
+  const hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(event));
+  if (e != hipSuccess) return launch_failed("hipEventSynchronize", e);
+  return 0;
+}
+
+int xdna_hip_event_query(void* event) {
+  const hipError_t e = hipEventQuery(reinterpret_cast<hipEvent_t>(event));
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  return launch_failed("hipEventQuery", e);
+}
+
+int xdna_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+  const hipError_t e = hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                           reinterpret_cast<hipEvent_t>(stop));
+  if (e != hipSuccess) return launch_failed("hipEventElapsedTime", e);
+  return 0;
+}
+
+int xdna_hip_stream_wait_event(void* stream, void* event) {
+  const hipError_t e =
+      hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0);
+  if (e != hipSuccess) return launch_failed("hipStreamWaitEvent", e);
+  return 0;
+}
+
+}  // extern "C"

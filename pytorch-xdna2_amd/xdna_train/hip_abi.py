@@ -1,0 +1,114 @@
+"""ctypes binding of the C ABI in ``include/xdna_hip.h`` (``_lib/libxdna_hip.so``).
+
+The PrivateUse1 backend calls the same entry points from C++; this binding serves
+Python callers, benchmarks and the tests, mirroring how the reference's tests bind its
+host packing library (tests/run_conv3x3w_pack.py:16-27).  ``load()`` raises if the
+library was not built: there is no CPU substitute for any of these kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxdna_hip.so"
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+L = ctypes.c_int64
+Z = ctypes.c_size_t
+F = ctypes.c_float
+D = ctypes.c_double
+PP = ctypes.POINTER(ctypes.c_void_p)
+PL = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); every function declared in include/xdna_hip.h.
+SIGNATURES = {
+    "xdna_hip_last_error": (ctypes.c_char_p, []),
+    "xdna_hip_poisoned": (I, []),
+    "xdna_hip_inject_failure": (I, [L, I]),
+    "xdna_hip_reset_failure_state": (I, []),
+    "xdna_hip_launch_count": (L, []),
+    "xdna_hip_device_count": (I, []),
+    "xdna_hip_set_device": (I, [I]),
+    "xdna_hip_get_device": (I, [ctypes.POINTER(I)]),
+    "xdna_hip_device_properties": (I, [ctypes.c_char_p, Z, ctypes.POINTER(I), ctypes.POINTER(Z),
+                                       ctypes.POINTER(I)]),
+    "xdna_hip_malloc": (P, [Z]),
+    "xdna_hip_free": (I, [P]),
+    "xdna_hip_cache_alloc": (P, [Z]),
+    "xdna_hip_cache_free": (I, [P]),
+    "xdna_hip_cache_empty": (I, []),
+    "xdna_hip_cache_stats": (I, [PL, I]),
+    "xdna_hip_memcpy_async": (I, [P, P, Z, I, P]),
+    "xdna_hip_memset_async": (I, [P, I, Z, P]),
+    "xdna_hip_stream_synchronize": (I, [P]),
+    "xdna_hip_device_synchronize": (I, []),
+    "xdna_hip_event_create": (P, [I]),
+    "xdna_hip_event_destroy": (I, [P]),
+    "xdna_hip_event_record": (I, [P, P]),
+    "xdna_hip_event_synchronize": (I, [P]),
+    "xdna_hip_event_query": (I, [P]),
+    "xdna_hip_event_elapsed_ms": (I, [P, P, ctypes.POINTER(F)]),
+    "xdna_hip_stream_wait_event": (I, [P, P]),
+    "xdna_conv3x3w_pack_input_bf16": (I, [P, P, I, I, I, I, I, P]),
+    "xdna_conv3x3w_pack_input_range_bf16": (I, [P, P, I, I, I, I, I, I, I, P]),
+    "xdna_conv3x3w_pack_input_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
+    "xdna_conv3x3w_unpack_output_bf16": (I, [P, P, I, I, I, I, I, I, P]),
+    "xdna_conv3x3w_unpack_output_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, P]),
+    "xdna_conv3x3w_unpack_output_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
+    "xdna_conv3x3w_geometry": (I, [I, I, I, I, PL]),
+    "xdna_conv3x3_fwd_workspace_bytes": (Z, [I, I, I, I, I]),
+    "xdna_conv3x3_fwd_bf16": (I, [P, P, P, P, I, I, I, I, I, P, Z, P]),
+    "xdna_conv3x3_dgrad_workspace_bytes": (Z, [I, I, I, I, I]),
+    "xdna_conv3x3_dgrad_bf16": (I, [P, P, P, I, I, I, I, I, P, Z, P]),
+    "xdna_conv3x3_wgrad_workspace_bytes": (Z, [I, I, I, I, I]),
+    "xdna_conv3x3_wgrad_bf16": (I, [P, P, P, P, I, I, I, I, I, P, Z, P]),
+    "xdna_conv3x3_bias_grad_bf16": (I, [P, P, I, I, I, I, P]),
+    "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
+    "xdna_fused_adam": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, D, D, D, D, D, I, I, I, P, P, P]),
+}
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise HipError(
+                f"{LIB_PATH} is missing: build it with "
+                "`python pytorch-xdna2_amd/build_native.py` (no CPU fallback exists)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().xdna_hip_last_error().decode()
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        raise HipError(f"{what or 'xdna_hip'} failed: {last_error()}")
+
+
+def ptr_array(ptrs) -> ctypes.Array:
+    arr = (ctypes.c_void_p * len(ptrs))()
+    for i, p in enumerate(ptrs):
+        arr[i] = p
+    return arr
+
+
+def int64_array(vals) -> ctypes.Array:
+    arr = (ctypes.c_int64 * len(vals))()
+    for i, v in enumerate(vals):
+        arr[i] = int(v)
+    return arr

@@ -1,0 +1,113 @@
+"""HIP 3x3 conv forward / dgrad / wgrad (+ bias grad) vs the double-precision oracle.
+
+Bar: every output within 2 bf16 ulp of the exact sum of the bf16
+operands (with a floor at ulp(max|ref| * 2^-8) for outputs that cancel to ~0) and
+relative L2 <= 1e-2.  Shapes cover ragged channel counts (partial 64-chunks, partial
+128-blocks), one and several 2048-row groups, tiny channel counts (RGB-like), width
+strips (W > 36: S = 2, 3) and the C1 conv at B = 2.  wgrad is also checked for
+run-to-run bit equality (its split-K reduction is fixed-order).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import check_bf16, dev, dev_zeros, host, ptr, stream
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # B, Cin, Cout, H, W
+    (2, 64, 64, 12, 12),
+    (3, 70, 130, 9, 11),
+    (2, 3, 32, 7, 5),
+    (1, 64, 64, 8, 40),
+    (2, 128, 128, 36, 36),
+    (4, 64, 64, 36, 36),
+    (1, 128, 256, 18, 72),
+    (2, 256, 64, 5, 37),
+    (1, 1, 1, 1, 1),
+]
+
+
+def _data(B, Cin, Cout, H, W, seed):
+    rng = np.random.default_rng(seed)
+    bound = np.sqrt(6.0 / (9 * Cin))
+    x = oracle.rng_bf16(rng, (B, Cin, H, W))
+    w = oracle.bf16_bits(rng.uniform(-bound, bound, (Cout, Cin, 3, 3)).astype(np.float32))
+    b = oracle.bf16_bits(rng.uniform(-0.1, 0.1, (Cout,)).astype(np.float32))
+    dy = oracle.rng_bf16(rng, (B, Cout, H, W))
+    return x, w, b, dy
+
+
+def _ws(nbytes):
+    return dev_zeros((max(1, (nbytes + 1) // 2),))
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_forward(hip, shape):
+    B, Cin, Cout, H, W = shape
+    print(f"conv fwd {shape}", flush=True)
+    x, w, b, _ = _data(*shape, seed=sum(shape))
+    ref = oracle.conv3x3_fwd(x, w, b)
+    ws_bytes = hip.xdna_conv3x3_fwd_workspace_bytes(B, Cin, Cout, H, W)
+    ws = _ws(ws_bytes)
+    y = dev_zeros((B, Cout, H, W))
+    assert hip.xdna_conv3x3_fwd_bf16(ptr(dev(x)), ptr(dev(w)), ptr(dev(b)), ptr(y), B, Cin, Cout, H, W,
+                                     ptr(ws), ws_bytes, stream()) == 0
+    check_bf16(host(y), ref, what=f"fwd {shape}")
+    # without bias
+    y2 = dev_zeros((B, Cout, H, W))
+    assert hip.xdna_conv3x3_fwd_bf16(ptr(dev(x)), ptr(dev(w)), None, ptr(y2), B, Cin, Cout, H, W,
+                                     ptr(ws), ws_bytes, stream()) == 0
+    check_bf16(host(y2), oracle.conv3x3_fwd(x, w), what=f"fwd nobias {shape}")
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_dgrad(hip, shape):
+    B, Cin, Cout, H, W = shape
+    print(f"conv dgrad {shape}", flush=True)
+    _, w, _, dy = _data(*shape, seed=sum(shape) + 1)
+    ref = oracle.conv3x3_dgrad(dy, w)
+    ws_bytes = hip.xdna_conv3x3_dgrad_workspace_bytes(B, Cin, Cout, H, W)
+    ws = _ws(ws_bytes)
+    dx = dev_zeros((B, Cin, H, W))
+    assert hip.xdna_conv3x3_dgrad_bf16(ptr(dev(dy)), ptr(dev(w)), ptr(dx), B, Cin, Cout, H, W, ptr(ws),
+                                       ws_bytes, stream()) == 0
+    check_bf16(host(dx), ref, what=f"dgrad {shape}")
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_wgrad(hip, shape):
+    B, Cin, Cout, H, W = shape
+    print(f"conv wgrad {shape}", flush=True)
+    x, _, _, dy = _data(*shape, seed=sum(shape) + 2)
+    ref_w, ref_b = oracle.conv3x3_wgrad(x, dy)
+    ws_bytes = hip.xdna_conv3x3_wgrad_workspace_bytes(B, Cin, Cout, H, W)
+    ws = _ws(ws_bytes)
+    gw = dev_zeros((Cout, Cin, 3, 3))
+    gb = dev_zeros((Cout,))
+    dx_, ddy = dev(x), dev(dy)
+    assert hip.xdna_conv3x3_wgrad_bf16(ptr(dx_), ptr(ddy), ptr(gw), ptr(gb), B, Cin, Cout, H, W, ptr(ws),
+                                       ws_bytes, stream()) == 0
+    got_w, got_b = host(gw), host(gb)
+    check_bf16(got_w, ref_w, what=f"wgrad {shape}")
+    check_bf16(got_b, ref_b, what=f"bias grad {shape}")
+    # deterministic: a second call gives the same bits
+    gw2 = dev_zeros((Cout, Cin, 3, 3))
+    assert hip.xdna_conv3x3_wgrad_bf16(ptr(dx_), ptr(ddy), ptr(gw2), None, B, Cin, Cout, H, W, ptr(ws),
+                                       ws_bytes, stream()) == 0
+    np.testing.assert_array_equal(host(gw2), got_w)
+    # standalone bias gradient
+    gb2 = dev_zeros((Cout,))
+    assert hip.xdna_conv3x3_bias_grad_bf16(ptr(ddy), ptr(gb2), B, Cout, H, W, stream()) == 0
+    check_bf16(host(gb2), ref_b, what=f"bias grad kernel {shape}")
+
+
+def test_workspace_too_small_is_an_error(hip):
+    B, C, H, W = 1, 8, 4, 4
+    ws = _ws(64)
+    y = dev_zeros((B, C, H, W))
+    x = dev_zeros((B, C, H, W))
+    w = dev_zeros((C, C, 3, 3))
+    rc = hip.xdna_conv3x3_fwd_bf16(ptr(x), ptr(w), None, ptr(y), B, C, C, H, W, ptr(ws), 64, stream())
+    assert rc == -1
