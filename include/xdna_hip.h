@@ -179,6 +179,38 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
 int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H,
                                 int W, void* stream);
 
+/* --- the same convolutions as separate stages (the backend caches packed inputs and
+ * prepared weights across calls, like the reference's packed-buffer pool and weight
+ * cache, torch_xdna_device.cpp:1819-1914, 2200-2271) --- */
+
+/* Bytes of the packed input [groups][chunks][2126][64] of an NCHW [B][C][H][W]
+ * tensor in the strip layout the conv uses. */
+size_t xdna_conv3x3w_packed_bytes(int B, int C, int H, int W);
+
+/* Bytes of the prepared weights of a conv with `cin` input / `cout` output channels. */
+size_t xdna_conv3x3_prepared_weight_bytes(int cin, int cout);
+
+/* OIHW w[Cout][Cin][3][3] -> prepared A operand.  dgrad = 0: the forward conv
+ * (cin = Cin, cout = Cout).  dgrad = 1: the input-gradient conv (cin = Cout,
+ * cout = Cin) with the flip+swap map of conv_pack.cpp:470-473. */
+int xdna_conv3x3_prepare_weights_bf16(const uint16_t* w, uint16_t* wt, int Cout, int Cin,
+                                      int dgrad, void* stream);
+
+/* y[B][cout][H][W] = conv of the packed input xp (cin channels, strip layout of W)
+ * with prepared weights wt (+ bias[cout], may be NULL).  One kernel. */
+int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
+                           uint16_t* y, int B, int cin, int cout, int H, int W, void* stream);
+
+/* wgrad stage 1: x and dy re-laid out channel-major into the workspace (snapshots:
+ * stage 2 reads neither tensor).  Stage 2: the MFMA reduction over pixels and the
+ * fixed-order split reduction into gw (and gb when not NULL). */
+int xdna_conv3x3_wgrad_pack_bf16(const uint16_t* x, const uint16_t* dy, int B, int Cin,
+                                 int Cout, int H, int W, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+int xdna_conv3x3_wgrad_packed_bf16(uint16_t* gw, uint16_t* gb, int B, int Cin, int Cout,
+                                   int H, int W, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM: replaces mm_xdna / XdnaGemmRuntime::run (torch_xdna_device.cpp:      */
 /* 4387-4417, 1358-1457), addmm_out_xdna (:3740-3768) and bmm_out_xdna        */

@@ -71,7 +71,8 @@ def build_hip(jobs: int = 8) -> Path:
         objs = list(ex.map(lambda s: _compile_hip(s, headers), sources))
     out = LIBDIR / "libxdna_hip.so"
     tmp = LIBDIR / "libxdna_hip.so.tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libxdna_hip.so",
+           *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
@@ -84,8 +85,13 @@ def build_ext() -> Path | None:
     sources = sorted(NATIVE.glob("*.cpp"))
     if not sources:
         return None
+    import ctypes
+
     from torch.utils import cpp_extension
 
+    # the extension links libxdna_hip.so through $ORIGIN/_lib, which only resolves once
+    # it sits in xdna_train/; preload it for the import load() does from the build dir
+    ctypes.CDLL(str(LIBDIR / "libxdna_hip.so"), mode=ctypes.RTLD_GLOBAL)
     name = "_C"
     build_dir = BUILD / "ext"
     build_dir.mkdir(parents=True, exist_ok=True)

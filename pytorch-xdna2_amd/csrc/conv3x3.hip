@@ -538,44 +538,65 @@ size_t xdna_conv3x3_wgrad_workspace_bytes(int B, int Cin, int Cout, int H, int W
   return p.xt_bytes + p.dt_bytes + p.part_bytes + p.bpart_bytes;
 }
 
-int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, uint16_t* gb,
-                            int B, int Cin, int Cout, int H, int W, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-  if (!shape_ok("xdna_conv3x3_wgrad_bf16", B, Cin, Cout, H, W)) return -1;
-  const WgradPlan p = wgrad_plan(B, Cin, Cout, H, W);
+namespace {
+struct WgradBufs {
+  uint16_t* xt;
+  uint16_t* dt;
+  float* part;
+  float* bpart;
+};
+
+bool wgrad_bufs(const char* what, const WgradPlan& p, void* workspace, size_t workspace_bytes,
+                WgradBufs& b) {
   if (p.lds_bytes > kMaxWgradLds) {
-    set_error("xdna_conv3x3_wgrad_bf16: image too wide for the LDS window");
-    return -1;
+    set_error(std::string(what) + ": image too wide for the LDS window");
+    return false;
   }
   const size_t need = p.xt_bytes + p.dt_bytes + p.part_bytes + p.bpart_bytes;
   if (!workspace || workspace_bytes < need) {
-    set_error("xdna_conv3x3_wgrad_bf16: workspace too small");
-    return -1;
+    set_error(std::string(what) + ": workspace too small");
+    return false;
   }
   char* ws = static_cast<char*>(workspace);
-  uint16_t* xt = reinterpret_cast<uint16_t*>(ws);
-  uint16_t* dt = reinterpret_cast<uint16_t*>(ws + p.xt_bytes);
-  float* part = reinterpret_cast<float*>(ws + p.xt_bytes + p.dt_bytes);
-  float* bpart = reinterpret_cast<float*>(ws + p.xt_bytes + p.dt_bytes + p.part_bytes);
-  hipStream_t st = as_stream(stream);
+  b.xt = reinterpret_cast<uint16_t*>(ws);
+  b.dt = reinterpret_cast<uint16_t*>(ws + p.xt_bytes);
+  b.part = reinterpret_cast<float*>(ws + p.xt_bytes + p.dt_bytes);
+  b.bpart = reinterpret_cast<float*>(ws + p.xt_bytes + p.dt_bytes + p.part_bytes);
+  return true;
+}
+}  // namespace
 
+int xdna_conv3x3_wgrad_pack_bf16(const uint16_t* x, const uint16_t* dy, int B, int Cin, int Cout,
+                                 int H, int W, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (!shape_ok("xdna_conv3x3_wgrad_pack_bf16", B, Cin, Cout, H, W)) return -1;
+  const WgradPlan p = wgrad_plan(B, Cin, Cout, H, W);
+  WgradBufs bufs;
+  if (!wgrad_bufs("xdna_conv3x3_wgrad_pack_bf16", p, workspace, workspace_bytes, bufs)) return -1;
   if (!admit_launch("conv3x3 wgrad pack")) return -1;
-  {
-    const int64_t nx = int64_t(p.ci_pad) * (p.cm.q / 8);
-    pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nx, 256), 16384)), 256, 0, st>>>(
-        x, xt, B, Cin, H, W, p.ci_pad, p.cm.wp8, p.cm.img, p.cm.q, 1);
-    const int64_t nd = int64_t(p.co_pad) * (p.cm.q / 8);
-    pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nd, 256), 16384)), 256, 0, st>>>(
-        dy, dt, B, Cout, H, W, p.co_pad, p.cm.wp8, p.cm.img, p.cm.q, 0);
-  }
-  if (check_launch("conv3x3 wgrad pack")) return -1;
+  hipStream_t st = as_stream(stream);
+  const int64_t nx = int64_t(p.ci_pad) * (p.cm.q / 8);
+  pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nx, 256), 16384)), 256, 0, st>>>(
+      x, bufs.xt, B, Cin, H, W, p.ci_pad, p.cm.wp8, p.cm.img, p.cm.q, 1);
+  const int64_t nd = int64_t(p.co_pad) * (p.cm.q / 8);
+  pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nd, 256), 16384)), 256, 0, st>>>(
+      dy, bufs.dt, B, Cout, H, W, p.co_pad, p.cm.wp8, p.cm.img, p.cm.q, 0);
+  return check_launch("conv3x3 wgrad pack");
+}
 
+int xdna_conv3x3_wgrad_packed_bf16(uint16_t* gw, uint16_t* gb, int B, int Cin, int Cout, int H,
+                                   int W, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!shape_ok("xdna_conv3x3_wgrad_packed_bf16", B, Cin, Cout, H, W)) return -1;
+  const WgradPlan p = wgrad_plan(B, Cin, Cout, H, W);
+  WgradBufs bufs;
+  if (!wgrad_bufs("xdna_conv3x3_wgrad_packed_bf16", p, workspace, workspace_bytes, bufs)) return -1;
   if (!admit_launch("conv3x3 wgrad")) return -1;
+  hipStream_t st = as_stream(stream);
   WgradArgs a;
-  a.xt = xt;
-  a.dt = dt;
-  a.part = part;
-  a.bpart = gb ? bpart : nullptr;
+  a.xt = bufs.xt;
+  a.dt = bufs.dt;
+  a.part = bufs.part;
+  a.bpart = gb ? bufs.bpart : nullptr;
   a.q = p.cm.q;
   a.wp8 = p.cm.wp8;
   a.ci_pad = p.ci_pad;
@@ -586,13 +607,46 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
   a.wlen = p.wlen;
   wgrad_kernel<<<dim3(unsigned(p.co_pad / kTCo), unsigned(p.ci_pad / 64), unsigned(p.splits)), 256,
                  p.lds_bytes, st>>>(a);
-  if (check_launch("conv3x3 wgrad")) return -1;
-
-  if (!admit_launch("conv3x3 wgrad reduce")) return -1;
   const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
   wgrad_reduce_kernel<<<int(std::min<int64_t>(ceil_div(n, 256), 8192)), 256, 0, st>>>(
-      part, bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  return check_launch("conv3x3 wgrad reduce");
+      bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  return check_launch("conv3x3 wgrad");
+}
+
+int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, uint16_t* gb,
+                            int B, int Cin, int Cout, int H, int W, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (xdna_conv3x3_wgrad_pack_bf16(x, dy, B, Cin, Cout, H, W, workspace, workspace_bytes, stream))
+    return -1;
+  return xdna_conv3x3_wgrad_packed_bf16(gw, gb, B, Cin, Cout, H, W, workspace, workspace_bytes,
+                                        stream);
+}
+
+size_t xdna_conv3x3w_packed_bytes(int B, int C, int H, int W) {
+  if (B < 1 || C < 1 || H < 1 || W < 1) return 0;
+  return fwd_plan(B, C, 1, H, W).packed_bytes;
+}
+
+size_t xdna_conv3x3_prepared_weight_bytes(int cin, int cout) {
+  if (cin < 1 || cout < 1) return 0;
+  return fwd_plan(1, cin, cout, 1, 1).wt_bytes;
+}
+
+int xdna_conv3x3_prepare_weights_bf16(const uint16_t* w, uint16_t* wt, int Cout, int Cin,
+                                      int dgrad, void* stream) {
+  if (Cout < 1 || Cin < 1) {
+    set_error("xdna_conv3x3_prepare_weights_bf16: invalid shape");
+    return -1;
+  }
+  const int cin = dgrad ? Cout : Cin, cout = dgrad ? Cin : Cout;
+  const FwdPlan p = fwd_plan(1, cin, cout, 1, 1);
+  return launch_prep(w, wt, Cout, Cin, p.co_pad, p.chunks, dgrad ? 1 : 0, stream);
+}
+
+int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
+                           uint16_t* y, int B, int cin, int cout, int H, int W, void* stream) {
+  if (!shape_ok("xdna_conv3x3_rows_bf16", B, cin, cout, H, W)) return -1;
+  return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream);
 }
 
 int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H, int W,

@@ -1,0 +1,609 @@
+// PrivateUse1 "xdna" device over HIP memory: allocator, guard, hooks, tensor plumbing,
+// copies, and the boxed fallback.
+//
+// Reference counterparts (torch_xdna_device.cpp): XdnaBoCache/XdnaAllocator
+// (:205-296, 658-716), XdnaGuardImpl (:872-928), hooks (:964-997), empty/views/
+// resize_/set_ (:1001-1199), copy_ (:1201-1318), the registration table (:5021-5083)
+// and the zero-copy CPU fallback (:5109-5300).
+//
+// The reference's device memory is host memory, so its fallback runs CPU kernels on
+// CPU aliases.  Here device memory is HBM, and the MI355X counterpart is the same idea
+// one level over: an operator without an xdna kernel runs PyTorch-ROCm's own kernel
+// on ROCm ("cuda") tensors that alias the xdna buffers, on the same HIP stream as the
+// hot-path kernels.  No data moves; results are adopted as xdna tensors.
+#include "xdna.h"
+
+#include <ATen/CPUGeneratorImpl.h>
+#include <ATen/EmptyTensor.h>
+#include <ATen/core/dispatch/Dispatcher.h>
+#include <ATen/detail/PrivateUse1HooksInterface.h>
+#include <ATen/native/Resize.h>
+#include <ATen/ops/_conj_native.h>
+#include <ATen/ops/_neg_view_native.h>
+#include <ATen/ops/_reshape_alias_native.h>
+#include <ATen/ops/as_strided_native.h>
+#include <ATen/ops/unfold_native.h>
+#include <ATen/ops/view_as_complex_native.h>
+#include <ATen/ops/view_as_real_native.h>
+#include <ATen/ops/view_native.h>
+#include <c10/core/impl/DeviceGuardImplInterface.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <chrono>
+#include <mutex>
+#include <unordered_map>
+
+namespace xdna_backend {
+
+std::atomic<int> g_mode{2};
+
+namespace {
+
+int g_device_count = -1;
+
+int device_count() {
+  if (g_device_count < 0) g_device_count = xdna_hip_device_count() > 0 ? 1 : 0;
+  return g_device_count;
+}
+
+int64_t now_ns() {
+  return std::chrono::duration_cast<std::chrono::nanoseconds>(
+             std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+
+struct Stat {
+  int64_t calls = 0;
+  int64_t ns = 0;
+};
+
+std::mutex& stats_mu() {
+  static auto* m = new std::mutex();
+  return *m;
+}
+std::unordered_map<std::string, Stat>& path_stats() {
+  static auto* m = new std::unordered_map<std::string, Stat>();
+  return *m;
+}
+std::unordered_map<std::string, Stat>& fallback_stats() {
+  static auto* m = new std::unordered_map<std::string, Stat>();
+  return *m;
+}
+
+}  // namespace
+
+void count_call(const char* name, int64_t ns) {
+  std::lock_guard<std::mutex> lock(stats_mu());
+  auto& s = path_stats()[name];
+  ++s.calls;
+  s.ns += ns;
+}
+
+ScopedCount::ScopedCount(const char* n) : name(n), t0(now_ns()) {}
+ScopedCount::~ScopedCount() { count_call(name, now_ns() - t0); }
+
+void* current_stream() { return c10::hip::getCurrentHIPStream(0).stream(); }
+
+void check_abi(int rc, const char* what) {
+  TORCH_CHECK(rc == 0, "xdna: ", what, " failed: ", xdna_hip_last_error());
+}
+
+// ------------------------------------------------------------------------------------
+// Allocator: the C ABI's size-binned caching allocator.
+// ------------------------------------------------------------------------------------
+namespace {
+
+void xdna_delete(void* p) {
+  if (p) xdna_hip_cache_free(p);
+}
+
+struct XdnaAllocator final : c10::Allocator {
+  c10::DataPtr allocate(size_t n) override {
+    const c10::Device dev(kXdna, 0);
+    if (n == 0) return {nullptr, nullptr, &xdna_delete, dev};
+    void* p = xdna_hip_cache_alloc(n);
+    TORCH_CHECK(p, "xdna: out of device memory allocating ", n, " bytes: ", xdna_hip_last_error());
+    return {p, p, &xdna_delete, dev};
+  }
+  c10::DeleterFnPtr raw_deleter() const override { return &xdna_delete; }
+  void copy_data(void* dest, const void* src, std::size_t count) const override {
+    check_abi(xdna_hip_memcpy_async(dest, src, count, 3, current_stream()), "copy_data");
+  }
+};
+
+XdnaAllocator g_allocator;
+
+// Context of a DataPtr that borrows the memory of another storage (an xdna storage
+// seen as ROCm memory, or the reverse): the borrowed storage stays alive with it.
+void alias_ctx_delete(void* ctx) { delete static_cast<c10::Storage*>(ctx); }
+
+c10::Storage borrow_storage(const c10::Storage& src, c10::Device dev, c10::Allocator* alloc) {
+  c10::DataPtr dp(src.data_ptr().get(), new c10::Storage(src), &alias_ctx_delete, dev);
+  return c10::Storage(c10::make_intrusive<c10::StorageImpl>(c10::StorageImpl::use_byte_size_t(),
+                                                            src.nbytes(), std::move(dp), alloc,
+                                                            /*resizable=*/true));
+}
+
+at::Tensor make_view(c10::Storage st, c10::DispatchKey key, const at::Tensor& like) {
+  at::Tensor t = at::detail::make_tensor<c10::TensorImpl>(std::move(st), c10::DispatchKeySet(key),
+                                                          like.dtype());
+  t.unsafeGetTensorImpl()->set_sizes_and_strides(like.sizes(), like.strides(), like.storage_offset());
+  if (like.is_conj()) t._set_conj(true);
+  if (like.is_neg()) t._set_neg(true);
+  return t;
+}
+
+}  // namespace
+
+c10::Allocator* xdna_allocator() { return &g_allocator; }
+
+at::Tensor cuda_alias(const at::Tensor& t) {
+  // Always a fresh storage tagged cuda:0, also when the xdna storage borrows ROCm
+  // memory: storages PyTorch-ROCm resized itself carry "hip:0" DataPtrs, and a tensor
+  // built on one would not match the cuda:0 tensors it meets in kernels.
+  c10::Storage cs = borrow_storage(t.storage(), c10::Device(c10::DeviceType::CUDA, 0),
+                                   c10::GetAllocator(c10::DeviceType::CUDA));
+  return make_view(std::move(cs), c10::DispatchKey::CUDA, t);
+}
+
+at::Tensor xdna_from_cuda(const at::Tensor& t) {
+  const c10::Storage& cs = t.storage();
+  c10::Storage xs;
+  if (cs.data_ptr().get_deleter() == &alias_ctx_delete) {
+    xs = *static_cast<c10::Storage*>(cs.data_ptr().get_context());  // the xdna original
+  } else {
+    xs = borrow_storage(cs, c10::Device(kXdna, 0), &g_allocator);
+  }
+  return make_view(std::move(xs), c10::DispatchKey::PrivateUse1, t);
+}
+
+at::Tensor empty_xdna(at::IntArrayRef size, at::ScalarType dtype, c10::MemoryFormat fmt) {
+  return at::detail::empty_generic(size, &g_allocator, c10::DispatchKeySet(c10::DispatchKey::PrivateUse1),
+                                   dtype, fmt);
+}
+
+namespace {
+
+// ------------------------------------------------------------------------------------
+// Guard and hooks.  One device (xdna:0 = HIP device 0); its one stream is PyTorch-ROCm's
+// current stream, so the reported stream is the default one and event calls map to HIP
+// events on that stream.
+// ------------------------------------------------------------------------------------
+struct XdnaGuardImpl final : c10::impl::DeviceGuardImplInterface {
+  c10::DeviceType type() const override { return kXdna; }
+  c10::Device exchangeDevice(c10::Device d) const override {
+    TORCH_CHECK(d.index() <= 0, "xdna: only xdna:0 exists");
+    return c10::Device(kXdna, 0);
+  }
+  c10::Device getDevice() const override { return c10::Device(kXdna, 0); }
+  void setDevice(c10::Device d) const override {
+    TORCH_CHECK(d.index() <= 0, "xdna: only xdna:0 exists");
+  }
+  void uncheckedSetDevice(c10::Device) const noexcept override {}
+  c10::Stream getStream(c10::Device) const override {
+    return c10::Stream(c10::Stream::DEFAULT, c10::Device(kXdna, 0));
+  }
+  c10::Stream getDefaultStream(c10::Device) const override {
+    return c10::Stream(c10::Stream::DEFAULT, c10::Device(kXdna, 0));
+  }
+  c10::Stream getStreamFromGlobalPool(c10::Device, bool) const override {
+    return c10::Stream(c10::Stream::DEFAULT, c10::Device(kXdna, 0));
+  }
+  c10::Stream exchangeStream(c10::Stream) const override {
+    return c10::Stream(c10::Stream::DEFAULT, c10::Device(kXdna, 0));
+  }
+  c10::DeviceIndex deviceCount() const noexcept override {
+    return static_cast<c10::DeviceIndex>(device_count());
+  }
+  void destroyEvent(void* event, const c10::DeviceIndex) const noexcept override {
+    if (event) xdna_hip_event_destroy(event);
+  }
+  void record(void** event, const c10::Stream&, const c10::DeviceIndex,
+              const c10::EventFlag) const override {
+    if (!*event) {
+      *event = xdna_hip_event_create(0);
+      TORCH_CHECK(*event, "xdna: event creation failed: ", xdna_hip_last_error());
+    }
+    check_abi(xdna_hip_event_record(*event, current_stream()), "event record");
+  }
+  void block(void* event, const c10::Stream&) const override {
+    if (event) check_abi(xdna_hip_stream_wait_event(current_stream(), event), "event wait");
+  }
+  bool queryEvent(void* event) const override {
+    return !event || xdna_hip_event_query(event) == 1;
+  }
+  void synchronizeEvent(void* event) const override {
+    if (event) check_abi(xdna_hip_event_synchronize(event), "event synchronize");
+  }
+  bool queryStream(const c10::Stream&) const override { return true; }
+  void synchronizeStream(const c10::Stream&) const override {
+    check_abi(xdna_hip_stream_synchronize(current_stream()), "stream synchronize");
+  }
+  void synchronizeDevice(const c10::DeviceIndex) const override {
+    check_abi(xdna_hip_device_synchronize(), "device synchronize");
+  }
+  void recordDataPtrOnStream(const c10::DataPtr&, const c10::Stream&) const override {}
+};
+
+void resize_storage_bytes(const c10::Storage& storage, size_t newsize) {
+  c10::StorageImpl* impl = storage.unsafeGetStorageImpl();
+  TORCH_CHECK(impl->resizable(), "Trying to resize storage that is not resizable");
+  const size_t old = impl->nbytes();
+  if (newsize == old) return;
+  c10::DataPtr fresh = g_allocator.allocate(newsize);
+  const size_t n = std::min(old, newsize);
+  if (n > 0 && impl->data())
+    check_abi(xdna_hip_memcpy_async(fresh.get(), impl->data(), n, 3, current_stream()), "resize copy");
+  impl->set_data_ptr_noswap(std::move(fresh));
+  impl->set_nbytes(newsize);
+}
+
+struct XdnaHooks final : at::PrivateUse1HooksInterface {
+  bool isBuilt() const override { return true; }
+  bool isAvailable() const override { return device_count() > 0; }
+  const at::Generator& getDefaultGenerator(c10::DeviceIndex) const override {
+    return at::detail::getDefaultCPUGenerator();
+  }
+  at::Generator getNewGenerator(c10::DeviceIndex) const override {
+    return at::detail::createCPUGenerator();
+  }
+  at::Device getDeviceFromPtr(void*) const override { return at::Device(kXdna, 0); }
+  bool isPinnedPtr(const void*) const override { return false; }
+  c10::Allocator* getPinnedMemoryAllocator() const override { return at::getCPUAllocator(); }
+  bool hasPrimaryContext(c10::DeviceIndex) const override { return true; }
+  c10::DeviceIndex deviceCount() const override { return static_cast<c10::DeviceIndex>(device_count()); }
+  void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
+    resize_storage_bytes(storage, newsize);
+  }
+};
+
+// ------------------------------------------------------------------------------------
+// Factories, resize_, set_
+// ------------------------------------------------------------------------------------
+at::Tensor empty_memory_format(c10::SymIntArrayRef size, std::optional<at::ScalarType> dtype,
+                               std::optional<at::Layout> layout, std::optional<at::Device> device,
+                               std::optional<bool> pin_memory,
+                               std::optional<at::MemoryFormat> memory_format) {
+  TORCH_CHECK(!layout || *layout == at::Layout::Strided, "xdna: only strided tensors");
+  return at::detail::empty_generic(C10_AS_INTARRAYREF_SLOW(size), &g_allocator,
+                                   c10::DispatchKeySet(c10::DispatchKey::PrivateUse1),
+                                   c10::dtype_or_default(dtype), memory_format);
+}
+
+at::Tensor empty_strided(c10::SymIntArrayRef size, c10::SymIntArrayRef stride,
+                         std::optional<at::ScalarType> dtype, std::optional<at::Layout> layout,
+                         std::optional<at::Device> device, std::optional<bool> pin_memory) {
+  TORCH_CHECK(!layout || *layout == at::Layout::Strided, "xdna: only strided tensors");
+  return at::detail::empty_strided_generic(
+      C10_AS_INTARRAYREF_SLOW(size), C10_AS_INTARRAYREF_SLOW(stride), &g_allocator,
+      c10::DispatchKeySet(c10::DispatchKey::PrivateUse1), c10::dtype_or_default(dtype));
+}
+
+void ensure_storage(const at::Tensor& self) {
+  auto* impl = self.unsafeGetTensorImpl();
+  if (self.numel() == 0) return;
+  const size_t need = at::detail::computeStorageNbytes(impl->sizes(), impl->strides(),
+                                                       self.dtype().itemsize(),
+                                                       impl->storage_offset());
+  if (need > impl->storage().nbytes()) resize_storage_bytes(impl->storage(), need);
+}
+
+const at::Tensor& resize_xdna_(const at::Tensor& self, c10::SymIntArrayRef size,
+                               std::optional<at::MemoryFormat> fmt) {
+  auto* impl = self.unsafeGetTensorImpl();
+  const auto sizes = C10_AS_INTARRAYREF_SLOW(size);
+  if (impl->sizes() != sizes) impl->set_sizes_contiguous(sizes);
+  if (fmt && *fmt != at::MemoryFormat::Preserve) impl->empty_tensor_restride(*fmt);
+  ensure_storage(self);
+  return self;
+}
+
+at::Tensor& set_storage_offset_(at::Tensor& self, c10::Storage source, c10::SymInt offset,
+                                c10::SymIntArrayRef size, c10::SymIntArrayRef stride) {
+  const int64_t off = offset.guard_int(__FILE__, __LINE__);
+  const auto sz = C10_AS_INTARRAYREF_SLOW(size);
+  TORCH_CHECK(off >= 0, "Tensor: invalid storage offset ", off);
+  auto* impl = self.unsafeGetTensorImpl();
+  if (!impl->storage().is_alias_of(source)) impl->set_storage_keep_dtype(std::move(source));
+  impl->set_storage_offset(off);
+  if (stride.data() && !stride.empty()) {
+    impl->set_sizes_and_strides(sz, C10_AS_INTARRAYREF_SLOW(stride));
+  } else {
+    impl->set_sizes_contiguous(sz);
+  }
+  ensure_storage(self);
+  return self;
+}
+
+at::Tensor& set_storage_(at::Tensor& self, c10::Storage source) {
+  const int64_t n = int64_t(source.nbytes() / self.dtype().itemsize());
+  std::vector<c10::SymInt> size{c10::SymInt(n)}, stride{c10::SymInt(1)};
+  return set_storage_offset_(self, std::move(source), c10::SymInt(0), size, stride);
+}
+
+at::Tensor& set_tensor_(at::Tensor& self, const at::Tensor& src) {
+  if (self.is_same(src)) return self;
+  return set_storage_offset_(self, src.storage(), src.sym_storage_offset(), src.sym_sizes(),
+                             src.sym_strides());
+}
+
+at::Tensor& set_empty_(at::Tensor& self) {
+  c10::Storage st(c10::Storage::use_byte_size_t(), 0, &g_allocator, true);
+  std::vector<c10::SymInt> size{c10::SymInt(0)}, stride;
+  return set_storage_offset_(self, std::move(st), c10::SymInt(0), size, stride);
+}
+
+// ------------------------------------------------------------------------------------
+// Copies: host <-> xdna through hipMemcpy on the current stream (synchronized unless
+// non_blocking from a host tensor), xdna <-> xdna/ROCm through PyTorch-ROCm's copy
+// kernel on aliases (strides and dtype conversion included).
+// ------------------------------------------------------------------------------------
+bool is_devmem(const at::Tensor& t) { return t.device().type() == kXdna || t.is_cuda(); }
+
+at::Tensor as_rocm(const at::Tensor& t) { return t.device().type() == kXdna ? cuda_alias(t) : t; }
+
+at::Tensor copy_from_xdna(const at::Tensor& self, const at::Tensor& dst, bool non_blocking) {
+  ScopedCount sc("xdna.copy");
+  if (self.numel() == 0) return dst;
+  const at::Tensor& src = self;
+  if (is_devmem(src) && is_devmem(dst)) {
+    at::Tensor d = as_rocm(dst);
+    d.copy_(as_rocm(src), non_blocking);
+    return dst;
+  }
+  if (src.is_cpu() && dst.device().type() == kXdna) {
+    at::Tensor h = src.resolve_conj().resolve_neg().to(dst.scalar_type()).contiguous();
+    at::Tensor target = dst.is_contiguous() ? dst : empty_xdna(dst.sizes(), dst.scalar_type());
+    check_abi(xdna_hip_memcpy_async(target.data_ptr(), h.data_ptr(), h.nbytes(), 1, current_stream()),
+              "host to device copy");
+    // the host tensor may be freed right after return: wait for the copy
+    check_abi(xdna_hip_stream_synchronize(current_stream()), "host to device copy");
+    if (!target.is_same(dst)) cuda_alias(dst).copy_(cuda_alias(target));
+    return dst;
+  }
+  if (src.device().type() == kXdna && dst.is_cpu()) {
+    at::Tensor s = src;
+    if (!s.is_contiguous() || s.scalar_type() != dst.scalar_type() || s.is_conj() || s.is_neg()) {
+      at::Tensor tmp = empty_xdna(s.sizes(), dst.scalar_type());
+      cuda_alias(tmp).copy_(cuda_alias(s));
+      s = tmp;
+    }
+    at::Tensor h = dst.is_contiguous() ? dst : at::empty(dst.sizes(), dst.options());
+    check_abi(xdna_hip_memcpy_async(h.data_ptr(), s.data_ptr(), s.nbytes(), 2, current_stream()),
+              "device to host copy");
+    check_abi(xdna_hip_stream_synchronize(current_stream()), "device to host copy");
+    if (!h.is_same(dst)) dst.copy_(h);
+    return dst;
+  }
+  TORCH_CHECK(false, "xdna: unsupported copy from ", src.device(), " to ", dst.device());
+}
+
+at::Tensor copy_from_and_resize_xdna(const at::Tensor& self, const at::Tensor& dst) {
+  dst.resize_(self.sizes());
+  return copy_from_xdna(self, dst, false);
+}
+
+// ------------------------------------------------------------------------------------
+// Boxed fallback: PyTorch-ROCm kernels on aliases.
+// ------------------------------------------------------------------------------------
+bool& fallback_timing() {
+  static bool on = [] {
+    const char* e = std::getenv("XDNA_PROFILE_FALLBACK");
+    return e && e[0] && e[0] != '0';
+  }();
+  return on;
+}
+
+at::Tensor wrap_result(const at::Tensor& t,
+                       const std::vector<std::pair<at::Tensor, at::Tensor>>& written) {
+  if (!t.defined() || !t.is_cuda()) return t;
+  for (const auto& [alias, orig] : written)
+    if (t.unsafeGetTensorImpl() == alias.unsafeGetTensorImpl()) return orig;
+  return xdna_from_cuda(t);
+}
+
+// A mutated argument: adopt a storage the ROCm kernel resized or replaced, and any new
+// sizes/strides (out= arguments).
+void sync_back(const at::Tensor& alias, const at::Tensor& orig) {
+  auto* oi = orig.unsafeGetTensorImpl();
+  const c10::Storage& as = alias.storage();
+  const c10::Storage& os = oi->storage();
+  const bool same_mem = as.data_ptr().get() == os.data_ptr().get() && as.nbytes() == os.nbytes();
+  if (!same_mem) {
+    c10::StorageImpl* simpl = os.unsafeGetStorageImpl();
+    c10::DataPtr dp(as.data_ptr().get(), new c10::Storage(as), &alias_ctx_delete,
+                    c10::Device(kXdna, 0));
+    simpl->set_data_ptr_noswap(std::move(dp));
+    simpl->set_nbytes(as.nbytes());
+  }
+  if (oi->sizes() != alias.sizes() || oi->strides() != alias.strides() ||
+      oi->storage_offset() != alias.storage_offset()) {
+    oi->set_storage_offset(alias.storage_offset());
+    oi->set_sizes_and_strides(alias.sizes(), alias.strides());
+  }
+}
+
+void xdna_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
+  const bool timing = fallback_timing();
+  const int64_t t0 = timing ? now_ns() : 0;
+  const auto& schema = op.schema();
+  const auto& args = schema.arguments();
+  const size_t n = args.size();
+  TORCH_INTERNAL_ASSERT(stack->size() >= n);
+  const size_t base = stack->size() - n;
+  std::vector<std::pair<at::Tensor, at::Tensor>> written;  // {alias, xdna original}
+  for (size_t i = 0; i < n; ++i) {
+    c10::IValue& iv = (*stack)[base + i];
+    const auto* ai = args[i].alias_info();
+    const bool is_write = ai && ai->isWrite();
+    if (iv.isTensor()) {
+      const at::Tensor& t = iv.toTensor();
+      if (t.defined() && t.device().type() == kXdna) {
+        at::Tensor a = cuda_alias(t);
+        if (is_write) written.emplace_back(a, t);
+        iv = c10::IValue(std::move(a));
+      }
+    } else if (iv.isTensorList()) {
+      c10::List<at::Tensor> list = iv.toTensorList();
+      c10::List<at::Tensor> out;
+      out.reserve(list.size());
+      for (const at::Tensor t : list) {
+        if (t.defined() && t.device().type() == kXdna) {
+          at::Tensor a = cuda_alias(t);
+          if (is_write) written.emplace_back(a, t);
+          out.push_back(std::move(a));
+        } else {
+          out.push_back(t);
+        }
+      }
+      iv = c10::IValue(std::move(out));
+    } else if (iv.isOptionalTensorList()) {
+      auto list = iv.toOptionalTensorList();
+      c10::List<std::optional<at::Tensor>> out;
+      out.reserve(list.size());
+      for (const std::optional<at::Tensor> t : list) {
+        if (t && t->defined() && t->device().type() == kXdna) out.push_back(cuda_alias(*t));
+        else out.push_back(t);
+      }
+      iv = c10::IValue(std::move(out));
+    } else if (iv.isDevice()) {
+      if (iv.toDevice().type() == kXdna) iv = c10::IValue(c10::Device(c10::DeviceType::CUDA, 0));
+    }
+  }
+
+  op.redispatchBoxed(c10::DispatchKeySet(c10::DispatchKey::CUDA), stack);
+
+  for (const auto& [alias, orig] : written) sync_back(alias, orig);
+  const size_t r = schema.returns().size();
+  for (size_t j = 0; j < r; ++j) {
+    c10::IValue& iv = (*stack)[stack->size() - r + j];
+    if (iv.isTensor()) {
+      iv = c10::IValue(wrap_result(iv.toTensor(), written));
+    } else if (iv.isTensorList()) {
+      c10::List<at::Tensor> list = iv.toTensorList();
+      c10::List<at::Tensor> out;
+      out.reserve(list.size());
+      for (const at::Tensor t : list) out.push_back(wrap_result(t, written));
+      iv = c10::IValue(std::move(out));
+    }
+  }
+  {
+    std::string name = schema.name();
+    if (!schema.overload_name().empty()) name += "." + schema.overload_name();
+    std::lock_guard<std::mutex> lock(stats_mu());
+    auto& s = fallback_stats()[name];
+    ++s.calls;
+    if (timing) s.ns += now_ns() - t0;
+  }
+}
+
+}  // namespace
+}  // namespace xdna_backend
+
+using namespace xdna_backend;
+
+REGISTER_ALLOCATOR(c10::DeviceType::PrivateUse1, &g_allocator)
+C10_REGISTER_GUARD_IMPL(PrivateUse1, XdnaGuardImpl)
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  m.impl("empty.memory_format", TORCH_FN(empty_memory_format));
+  m.impl("empty_strided", TORCH_FN(empty_strided));
+  m.impl("as_strided", TORCH_FN(at::native::as_strided_tensorimpl));
+  m.impl("view", TORCH_FN(at::native::view));
+  m.impl("_reshape_alias", TORCH_FN(at::native::_reshape_alias));
+  m.impl("unfold", TORCH_FN(at::native::unfold));
+  m.impl("view_as_real", TORCH_FN(at::native::view_as_real));
+  m.impl("view_as_complex", TORCH_FN(at::native::view_as_complex));
+  m.impl("_conj", TORCH_FN(at::native::_conj));
+  m.impl("_neg_view", TORCH_FN(at::native::_neg_view));
+  m.impl("resize_", TORCH_FN(resize_xdna_));
+  m.impl("set_.source_Storage", TORCH_FN(set_storage_));
+  m.impl("set_.source_Storage_storage_offset", TORCH_FN(set_storage_offset_));
+  m.impl("set_.source_Tensor", TORCH_FN(set_tensor_));
+  m.impl("set_", TORCH_FN(set_empty_));
+  m.impl("_copy_from", TORCH_FN(copy_from_xdna));
+  m.impl("_copy_from_and_resize", TORCH_FN(copy_from_and_resize_xdna));
+  register_hot_ops(m);
+}
+
+TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
+  m.fallback(torch::CppFunction::makeFromBoxedFunction<&xdna_fallback>());
+}
+
+// ------------------------------------------------------------------------------------
+// Python module _C (the reference's pybind surface, torch_xdna_device.cpp:5346-5767,
+// restricted to the hot path).
+// ------------------------------------------------------------------------------------
+namespace {
+
+py::dict stats_dict(std::unordered_map<std::string, Stat>& m) {
+  py::dict d;
+  std::lock_guard<std::mutex> lock(stats_mu());
+  for (const auto& [k, s] : m) {
+    py::dict e;
+    e["calls"] = s.calls;
+    e["total_ms"] = double(s.ns) / 1e6;
+    e["avg_ms"] = s.calls ? double(s.ns) / 1e6 / double(s.calls) : 0.0;
+    d[py::str(k)] = e;
+  }
+  return d;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
+  at::RegisterPrivateUse1HooksInterface(new XdnaHooks());
+  mod.def("is_available", [] { return device_count() > 0; });
+  mod.def("device_count", [] { return device_count(); });
+  mod.def("current_device", [] { return 0; });
+  mod.def("set_device", [](int d) { TORCH_CHECK(d == 0, "xdna: only xdna:0 exists"); });
+  mod.def("synchronize", [] { check_abi(xdna_hip_device_synchronize(), "synchronize"); });
+  mod.def("empty_cache", [] {
+    check_abi(xdna_hip_device_synchronize(), "synchronize");
+    check_abi(xdna_hip_cache_empty(), "empty_cache");
+  });
+  mod.def("allocator_stats", [] {
+    int64_t s[6] = {0, 0, 0, 0, 0, 0};
+    xdna_hip_cache_stats(s, 6);
+    py::dict d;
+    d["cached_bytes"] = s[0];
+    d["allocated_bytes"] = s[1];
+    d["max_allocated_bytes"] = s[2];
+    d["fresh_allocations"] = s[3];
+    d["reuses"] = s[4];
+    d["frees"] = s[5];
+    return d;
+  });
+  mod.def("set_npu_mode", [](int m) {
+    TORCH_CHECK(m >= 0 && m <= 2, "xdna: mode must be 0, 1 or 2");
+    g_mode.store(m);
+  });
+  mod.def("npu_mode", [] { return g_mode.load(); });
+  mod.def("mapped_cpu_stats", [] { return stats_dict(path_stats()); });
+  mod.def("reset_mapped_cpu_stats", [] {
+    std::lock_guard<std::mutex> lock(stats_mu());
+    path_stats().clear();
+  });
+  mod.def("fallback_stats", [] { return stats_dict(fallback_stats()); });
+  mod.def("reset_fallback_stats", [] {
+    std::lock_guard<std::mutex> lock(stats_mu());
+    fallback_stats().clear();
+  });
+  mod.def("cuda_alias", [](const at::Tensor& t) { return cuda_alias(t); });
+  mod.def("from_cuda", [](const at::Tensor& t) { return xdna_from_cuda(t); });
+  mod.def("data_ptr", [](const at::Tensor& t) { return reinterpret_cast<uintptr_t>(t.data_ptr()); });
+  mod.def("launch_count", [] { return xdna_hip_launch_count(); });
+  mod.def("async_dw_stats", [] {
+    py::dict d;
+    d["jobs"] = dw_jobs();
+    d["kicks"] = 0;
+    d["learned_k"] = 0;
+    return d;
+  });
+  mod.def("poisoned", [] { return xdna_hip_poisoned() != 0; });
+  mod.def("inject_failure", [](int64_t n, bool poison) {
+    check_abi(xdna_hip_inject_failure(n, poison ? 1 : 0), "inject_failure");
+  });
+  mod.def("reset_failure_state", [] { xdna_hip_reset_failure_state(); });
+}

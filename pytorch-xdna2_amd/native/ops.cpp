@@ -1,0 +1,506 @@
+// Hot-path operators of the xdna backend: 3x3 conv forward / backward, mm / addmm /
+// bmm, fused Adam / AdamW.  Every kernel runs through the C ABI (include/xdna_hip.h)
+// on PyTorch-ROCm's current HIP stream; shapes outside the hot path go to the generic
+// fallback (PyTorch-ROCm kernels on aliases), as the reference sends them to its CPU
+// kernels (torch_xdna_device.cpp:4524-4606, 4608-4885, 4360-4417, 3740-3790).
+#include "xdna.h"
+
+#include <ATen/native/Resize.h>
+#include <ATen/ops/_fused_adam_native.h>
+#include <c10/core/impl/LocalDispatchKeySet.h>
+
+#include <array>
+#include <map>
+#include <mutex>
+#include <optional>
+#include <vector>
+
+namespace xdna_backend {
+namespace {
+
+at::Tensor rocm(const at::Tensor& t) {
+  return t.defined() && t.device().type() == kXdna ? cuda_alias(t) : t;
+}
+std::optional<at::Tensor> rocm(const std::optional<at::Tensor>& t) {
+  if (!t || !t->defined()) return t;
+  return rocm(*t);
+}
+at::Tensor back(const at::Tensor& t) { return t.defined() && t.is_cuda() ? xdna_from_cuda(t) : t; }
+
+// Dispatch below autograd: the aliases never carry autograd state.
+struct BelowAutograd {
+  at::AutoDispatchBelowADInplaceOrView guard;
+};
+
+at::Tensor alloc_bytes(size_t n) {
+  return empty_xdna({int64_t(std::max<size_t>(n, 1))}, at::kByte);
+}
+
+// ---------------------------------------------------------------------------------------
+// Packed-input pool (the reference's acquire_packed, torch_xdna_device.cpp:1819-1914).
+// Packing writes only real pixels/channels, so a buffer is zero-filled when created and
+// whenever the packed shape changes; all use is ordered on one stream, so a released
+// buffer can serve the next call at once.
+// ---------------------------------------------------------------------------------------
+struct PackedBuf {
+  at::Tensor mem;
+  std::array<int64_t, 4> shape{};
+};
+
+struct PackedPool {
+  std::mutex mu;
+  std::multimap<size_t, PackedBuf> free;
+  size_t bytes = 0;
+  static constexpr size_t kMaxBytes = size_t(8) << 30;
+};
+
+PackedPool& packed_pool() {
+  static auto* p = new PackedPool();
+  return *p;
+}
+
+PackedBuf acquire_packed(size_t bytes, const std::array<int64_t, 4>& shape) {
+  PackedPool& pool = packed_pool();
+  PackedBuf b;
+  {
+    std::lock_guard<std::mutex> lock(pool.mu);
+    auto range = pool.free.equal_range(bytes);
+    auto pick = range.second;
+    for (auto it = range.first; it != range.second; ++it) {
+      if (it->second.shape == shape) { pick = it; break; }
+      if (pick == range.second) pick = it;
+    }
+    if (pick != range.second) {
+      b = std::move(pick->second);
+      pool.free.erase(pick);
+      pool.bytes -= bytes;
+    }
+  }
+  if (!b.mem.defined()) b.mem = alloc_bytes(bytes);
+  if (b.shape != shape) {
+    cuda_alias(b.mem).zero_();  // a fill kernel (no memset node in captured graphs)
+    b.shape = shape;
+  }
+  return b;
+}
+
+void release_packed(PackedBuf&& b) {
+  PackedPool& pool = packed_pool();
+  const size_t bytes = size_t(b.mem.nbytes());
+  std::lock_guard<std::mutex> lock(pool.mu);
+  if (pool.bytes + bytes > PackedPool::kMaxBytes) {
+    pool.free.clear();
+    pool.bytes = 0;
+  }
+  pool.free.emplace(bytes, std::move(b));
+  pool.bytes += bytes;
+}
+
+// ---------------------------------------------------------------------------------------
+// 3x3 conv
+// ---------------------------------------------------------------------------------------
+bool is_one(c10::SymIntArrayRef v, int64_t x) {
+  return v.size() == 2 && v[0] == x && v[1] == x;
+}
+
+// The reference's eligibility gate (XdnaConv3x3wRuntime::plan, torch_xdna_device.cpp:
+// 2112-2157): bf16, 4-D, 3x3, stride 1, pad 1, dilation 1, groups 1, not transposed.
+bool conv_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
+                   c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation, bool transposed,
+                   c10::SymIntArrayRef output_padding, const c10::SymInt& groups) {
+  if (g_mode.load() < 1) return false;
+  if (x.scalar_type() != at::kBFloat16 || w.scalar_type() != at::kBFloat16) return false;
+  if (x.dim() != 4 || w.dim() != 4 || w.size(2) != 3 || w.size(3) != 3) return false;
+  if (!is_one(stride, 1) || !is_one(padding, 1) || !is_one(dilation, 1) || transposed) return false;
+  if (!is_one(output_padding, 0) || groups != 1) return false;
+  if (x.size(0) < 1 || x.size(2) < 1 || x.size(3) < 1 || w.size(0) < 1 || w.size(1) < 1) return false;
+  if (x.device().type() != kXdna || w.device().type() != kXdna) return false;
+  return true;
+}
+
+// Runs the conv of `src` (NCHW, cin channels) with `w` (forward: w as given; dgrad:
+// flip+swap) into a new NCHW tensor of cout channels.
+at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor* bias,
+                    bool dgrad) {
+  const int64_t B = src.size(0), cin = src.size(1), H = src.size(2), W = src.size(3);
+  const int64_t cout = dgrad ? w.size(1) : w.size(0);
+  at::Tensor x = src.contiguous();
+  at::Tensor wc = w.contiguous();
+  void* st = current_stream();
+  const size_t pbytes = xdna_conv3x3w_packed_bytes(int(B), int(cin), int(H), int(W));
+  PackedBuf packed = acquire_packed(pbytes, {B, cin, H, W});
+  int64_t geo[7];
+  check_abi(xdna_conv3x3w_geometry(int(B), int(cin), int(H), int(W), geo), "conv geometry");
+  check_abi(xdna_conv3x3w_pack_input_strips_range_bf16(
+                static_cast<const uint16_t*>(x.const_data_ptr()), static_cast<uint16_t*>(packed.mem.data_ptr()),
+                int(B), int(cin), int(H), int(W), int(geo[0]), int(geo[1]), 0, int(geo[5]), 0, int(geo[4]), st),
+            "conv pack");
+  at::Tensor wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
+  check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
+                                              static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
+                                              int(w.size(1)), dgrad ? 1 : 0, st),
+            "conv weights");
+  at::Tensor out = empty_xdna({B, cout, H, W}, at::kBFloat16);
+  at::Tensor bc;
+  if (bias) bc = bias->contiguous();
+  check_abi(xdna_conv3x3_rows_bf16(static_cast<const uint16_t*>(packed.mem.const_data_ptr()),
+                                   static_cast<const uint16_t*>(wt.const_data_ptr()),
+                                   bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                                   static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout),
+                                   int(H), int(W), st),
+            "conv rows");
+  release_packed(std::move(packed));
+  return out;
+}
+
+at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tensor& weight,
+                                         const std::optional<at::Tensor>& bias,
+                                         c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
+                                         c10::SymIntArrayRef dilation, bool transposed,
+                                         c10::SymIntArrayRef output_padding, c10::SymInt groups) {
+  const bool has_bias = bias && bias->defined();
+  if (conv_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
+      input.size(1) == weight.size(1) &&
+      (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
+                     bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
+    ScopedCount sc("hip_conv3x3.fwd.run");
+    return hip_conv(input, weight, has_bias ? &*bias : nullptr, false);
+  }
+  ScopedCount sc("aten::convolution.rocm");
+  BelowAutograd g;
+  return back(at::_ops::convolution::call(rocm(input), rocm(weight), rocm(bias), stride, padding,
+                                          dilation, transposed, output_padding, groups));
+}
+
+// Weight gradient (+ bias gradient) through the two wgrad stages.  Stage 1 takes
+// snapshots of x and dY, so later writes to either cannot change the gradient (the
+// reference's deferred-dW contract, run_deferred_dw.py:62-71); stage 2 is ordered
+// before every reader of gw by the stream.
+void hip_wgrad(const at::Tensor& input, const at::Tensor& dy, at::Tensor& gw, at::Tensor* gb) {
+  const int64_t B = input.size(0), Cin = input.size(1), H = input.size(2), W = input.size(3);
+  const int64_t Cout = dy.size(1);
+  at::Tensor x = input.contiguous();
+  at::Tensor d = dy.contiguous();
+  void* st = current_stream();
+  const size_t wsb = xdna_conv3x3_wgrad_workspace_bytes(int(B), int(Cin), int(Cout), int(H), int(W));
+  at::Tensor ws = alloc_bytes(wsb);
+  gw = empty_xdna({Cout, Cin, 3, 3}, at::kBFloat16);
+  if (gb) *gb = empty_xdna({Cout}, at::kBFloat16);
+  check_abi(xdna_conv3x3_wgrad_pack_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                         static_cast<const uint16_t*>(d.const_data_ptr()), int(B),
+                                         int(Cin), int(Cout), int(H), int(W), ws.data_ptr(), wsb, st),
+            "conv wgrad pack");
+  check_abi(xdna_conv3x3_wgrad_packed_bf16(static_cast<uint16_t*>(gw.data_ptr()),
+                                           gb ? static_cast<uint16_t*>(gb->data_ptr()) : nullptr,
+                                           int(B), int(Cin), int(Cout), int(H), int(W), ws.data_ptr(),
+                                           wsb, st),
+            "conv wgrad");
+}
+
+std::atomic<int64_t> g_dw_jobs{0};
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable_xdna(
+    const at::Tensor& grad_output, const at::Tensor& input, const at::Tensor& weight,
+    c10::SymIntArrayRef stride, c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation,
+    bool transposed, c10::SymIntArrayRef output_padding, c10::SymInt groups,
+    std::array<bool, 3> output_mask) {
+  at::Tensor gi, gw, gb;
+  const bool hip = conv_eligible(input, weight, stride, padding, dilation, transposed,
+                                 output_padding, groups) &&
+                   grad_output.scalar_type() == at::kBFloat16 && grad_output.dim() == 4 &&
+                   grad_output.device().type() == kXdna && input.size(1) == weight.size(1) &&
+                   grad_output.size(1) == weight.size(0) && grad_output.size(0) == input.size(0) &&
+                   grad_output.size(2) == input.size(2) && grad_output.size(3) == input.size(3);
+  auto mask = output_mask;
+  if (hip && mask[0]) {
+    ScopedCount sc("hip_conv3x3.dx.run");
+    gi = hip_conv(grad_output, weight, nullptr, true);
+    mask[0] = false;
+  }
+  if (hip && mask[1] && g_mode.load() >= 2 && input.size(3) <= 142) {
+    ScopedCount sc("hip_conv3x3.dw.run");
+    hip_wgrad(input, grad_output, gw, mask[2] ? &gb : nullptr);
+    g_dw_jobs.fetch_add(1);
+    mask[1] = false;
+    mask[2] = false;
+  }
+  if (hip && mask[2]) {
+    ScopedCount sc("hip_conv3x3.bias_grad.run");
+    at::Tensor d = grad_output.contiguous();
+    gb = empty_xdna({grad_output.size(1)}, at::kBFloat16);
+    check_abi(xdna_conv3x3_bias_grad_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                          static_cast<uint16_t*>(gb.data_ptr()), int(d.size(0)),
+                                          int(d.size(1)), int(d.size(2)), int(d.size(3)),
+                                          current_stream()),
+              "conv bias grad");
+    mask[2] = false;
+  }
+  if (mask[0] || mask[1] || mask[2]) {
+    ScopedCount sc("aten::convolution_backward.rocm");
+    BelowAutograd g;
+    std::vector<c10::SymInt> bias_sizes;
+    std::optional<c10::SymIntArrayRef> bs;
+    if (mask[2]) {
+      bias_sizes.push_back(transposed ? weight.sym_size(1) * groups : weight.sym_size(0));
+      bs = c10::SymIntArrayRef(bias_sizes);
+    }
+    auto r = at::_ops::convolution_backward::call(rocm(grad_output), rocm(input), rocm(weight), bs,
+                                                  stride, padding, dilation, transposed,
+                                                  output_padding, groups, mask);
+    if (mask[0]) gi = back(std::get<0>(r));
+    if (mask[1]) gw = back(std::get<1>(r));
+    if (mask[2]) gb = back(std::get<2>(r));
+  }
+  return {gi, gw, gb};
+}
+
+// ---------------------------------------------------------------------------------------
+// GEMM
+// ---------------------------------------------------------------------------------------
+bool gemm_dtype_ok(std::initializer_list<const at::Tensor*> ts) {
+  if (g_mode.load() < 1) return false;
+  for (const at::Tensor* t : ts)
+    if (t->scalar_type() != at::kBFloat16 || t->device().type() != kXdna) return false;
+  return true;
+}
+
+bool fits_int(const at::Tensor& t) {
+  for (int64_t s : t.sizes())
+    if (s > (int64_t(1) << 30)) return false;
+  return true;
+}
+
+// c[b] = alpha * a[b].m[b] + beta * bias  (bias: an [M][N] view, may be broadcast)
+void run_gemm(const at::Tensor& a, const at::Tensor& m, at::Tensor& c, const at::Tensor* bias,
+              float alpha, float beta) {
+  const bool batched = a.dim() == 3;
+  const int64_t batch = batched ? a.size(0) : 1;
+  const int ia = batched ? 1 : 0;
+  const int64_t M = a.size(ia), K = a.size(ia + 1), N = m.size(ia + 1);
+  const uint16_t* bp = nullptr;
+  int mode = 0;
+  int64_t bsm = 0, bsn = 0;
+  at::Tensor be;
+  if (bias && beta != 0.0f) {
+    be = bias->expand({M, N});
+    bp = static_cast<const uint16_t*>(be.const_data_ptr());
+    mode = 2;
+    bsm = be.stride(0);
+    bsn = be.stride(1);
+  }
+  check_abi(xdna_gemm_bf16(static_cast<const uint16_t*>(a.const_data_ptr()),
+                           static_cast<const uint16_t*>(m.const_data_ptr()),
+                           static_cast<uint16_t*>(c.data_ptr()), bp, int(batch), int(M), int(N), int(K),
+                           a.stride(ia), a.stride(ia + 1), batched ? a.stride(0) : 0, m.stride(ia),
+                           m.stride(ia + 1), batched ? m.stride(0) : 0, c.stride(ia), c.stride(ia + 1),
+                           batched ? c.stride(0) : 0, mode, bsm, bsn, alpha, beta, current_stream()),
+            "gemm");
+}
+
+at::Tensor mm_xdna(const at::Tensor& a, const at::Tensor& b) {
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2, "mm: expected 2-D tensors");
+  TORCH_CHECK(a.size(1) == b.size(0), "mm: mat1 and mat2 shapes cannot be multiplied (",
+              a.size(0), "x", a.size(1), " and ", b.size(0), "x", b.size(1), ")");
+  if (gemm_dtype_ok({&a, &b}) && fits_int(a) && fits_int(b)) {
+    ScopedCount sc("hip_gemm.mm.run");
+    at::Tensor c = empty_xdna({a.size(0), b.size(1)}, at::kBFloat16);
+    run_gemm(a, b, c, nullptr, 1.0f, 0.0f);
+    return c;
+  }
+  ScopedCount sc("aten::mm.rocm");
+  BelowAutograd g;
+  return back(at::_ops::mm::call(rocm(a), rocm(b)));
+}
+
+at::Tensor& mm_out_xdna(const at::Tensor& a, const at::Tensor& b, at::Tensor& out) {
+  at::Tensor r = mm_xdna(a, b);
+  at::native::resize_output(out, r.sizes());
+  out.copy_(r);
+  return out;
+}
+
+at::Tensor addmm_xdna(const at::Tensor& self, const at::Tensor& a, const at::Tensor& b,
+                      const at::Scalar& beta, const at::Scalar& alpha) {
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2, "addmm: expected 2-D matrices");
+  TORCH_CHECK(a.size(1) == b.size(0), "addmm: mat1 and mat2 shapes cannot be multiplied (",
+              a.size(0), "x", a.size(1), " and ", b.size(0), "x", b.size(1), ")");
+  const int64_t M = a.size(0), N = b.size(1);
+  const bool self_ok = self.dim() <= 2 && self.scalar_type() == at::kBFloat16 &&
+                       self.device().type() == kXdna && at::is_expandable_to(self.sizes(), {M, N});
+  if (gemm_dtype_ok({&a, &b}) && self_ok && fits_int(a) && fits_int(b)) {
+    ScopedCount sc("hip_gemm.addmm.run");
+    at::Tensor c = empty_xdna({M, N}, at::kBFloat16);
+    run_gemm(a, b, c, &self, alpha.to<float>(), beta.to<float>());
+    return c;
+  }
+  ScopedCount sc("aten::addmm.rocm");
+  BelowAutograd g;
+  return back(at::_ops::addmm::call(rocm(self), rocm(a), rocm(b), beta, alpha));
+}
+
+at::Tensor& addmm_out_xdna(const at::Tensor& self, const at::Tensor& a, const at::Tensor& b,
+                           const at::Scalar& beta, const at::Scalar& alpha, at::Tensor& out) {
+  at::Tensor r = addmm_xdna(self, a, b, beta, alpha);
+  at::native::resize_output(out, r.sizes());
+  out.copy_(r);
+  return out;
+}
+
+at::Tensor bmm_xdna(const at::Tensor& a, const at::Tensor& b) {
+  TORCH_CHECK(a.dim() == 3 && b.dim() == 3, "batch1 and batch2 must be 3D tensors");
+  TORCH_CHECK(a.size(0) == b.size(0) && a.size(2) == b.size(1), "bmm: shape mismatch");
+  if (gemm_dtype_ok({&a, &b}) && fits_int(a) && fits_int(b) && a.size(0) <= 65535) {
+    ScopedCount sc("hip_gemm.bmm.run");
+    at::Tensor c = empty_xdna({a.size(0), a.size(1), b.size(2)}, at::kBFloat16);
+    run_gemm(a, b, c, nullptr, 1.0f, 0.0f);
+    return c;
+  }
+  ScopedCount sc("aten::bmm.rocm");
+  BelowAutograd g;
+  return back(at::_ops::bmm::call(rocm(a), rocm(b)));
+}
+
+at::Tensor& bmm_out_xdna(const at::Tensor& a, const at::Tensor& b, at::Tensor& out) {
+  at::Tensor r = bmm_xdna(a, b);
+  at::native::resize_output(out, r.sizes());
+  out.copy_(r);
+  return out;
+}
+
+// ---------------------------------------------------------------------------------------
+// Fused Adam / AdamW (PyTorch's _fused_adam_ schema; the reference runs the CPU kernel
+// of this op through its fallback).
+// ---------------------------------------------------------------------------------------
+bool adam_eligible(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                   at::TensorList mx, at::TensorList steps, bool amsgrad, int& dtype) {
+  if (g_mode.load() < 1 || p.empty()) return false;
+  const auto st = p[0].scalar_type();
+  if (st != at::kBFloat16 && st != at::kFloat) return false;
+  dtype = st == at::kBFloat16 ? 1 : 0;
+  if (g.size() != p.size() || m.size() != p.size() || v.size() != p.size() ||
+      steps.size() != p.size() || (amsgrad && mx.size() != p.size()))
+    return false;
+  auto ok = [&](const at::Tensor& t, int64_t n) {
+    return t.defined() && t.device().type() == kXdna && t.scalar_type() == st && t.is_contiguous() &&
+           t.numel() == n;
+  };
+  for (size_t i = 0; i < p.size(); ++i) {
+    const int64_t n = p[i].numel();
+    if (!ok(p[i], n) || !ok(g[i], n) || !ok(m[i], n) || !ok(v[i], n)) return false;
+    if (amsgrad && !ok(mx[i], n)) return false;
+    const at::Tensor& s = steps[i];
+    if (s.device().type() != kXdna || s.scalar_type() != at::kFloat || s.numel() != 1) return false;
+  }
+  return true;
+}
+
+std::vector<at::Tensor> rocm_list(at::TensorList l) {
+  std::vector<at::Tensor> out;
+  out.reserve(l.size());
+  for (const auto& t : l) out.push_back(rocm(t));
+  return out;
+}
+
+void fused_adam_common(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                       at::TensorList mx, at::TensorList steps, double lr, double beta1,
+                       double beta2, double wd, double eps, bool amsgrad, bool maximize,
+                       const std::optional<at::Tensor>& grad_scale,
+                       const std::optional<at::Tensor>& found_inf, bool adamw) {
+  int dtype = 1;
+  const bool scalars_ok =
+      (!grad_scale || (grad_scale->device().type() == kXdna && grad_scale->scalar_type() == at::kFloat)) &&
+      (!found_inf || (found_inf->device().type() == kXdna && found_inf->scalar_type() == at::kFloat));
+  if (scalars_ok && adam_eligible(p, g, m, v, mx, steps, amsgrad, dtype)) {
+    ScopedCount sc(adamw ? "hip_adamw.run" : "hip_adam.run");
+    const size_t n = p.size();
+    std::vector<void*> pp(n), gp(n), mp(n), vp(n), xp(n);
+    std::vector<const float*> sp(n);
+    std::vector<int64_t> numel(n);
+    for (size_t i = 0; i < n; ++i) {
+      pp[i] = p[i].data_ptr();
+      gp[i] = g[i].data_ptr();
+      mp[i] = m[i].data_ptr();
+      vp[i] = v[i].data_ptr();
+      xp[i] = amsgrad ? mx[i].data_ptr() : nullptr;
+      sp[i] = static_cast<const float*>(steps[i].const_data_ptr());
+      numel[i] = p[i].numel();
+    }
+    check_abi(xdna_fused_adam(int(n), pp.data(), gp.data(), mp.data(), vp.data(),
+                              amsgrad ? xp.data() : nullptr, sp.data(), numel.data(), dtype, lr, beta1,
+                              beta2, wd, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, adamw ? 1 : 0,
+                              grad_scale ? static_cast<const float*>(grad_scale->const_data_ptr()) : nullptr,
+                              found_inf ? static_cast<const float*>(found_inf->const_data_ptr()) : nullptr,
+                              current_stream()),
+              "fused adam");
+    return;
+  }
+  ScopedCount sc("aten::_fused_adam_.rocm");
+  BelowAutograd guard;
+  auto rp = rocm_list(p), rg = rocm_list(g), rm = rocm_list(m), rv = rocm_list(v), rx = rocm_list(mx),
+       rs = rocm_list(steps);
+  if (adamw)
+    at::_ops::_fused_adamw_::call(rp, rg, rm, rv, rx, rs, lr, beta1, beta2, wd, eps, amsgrad, maximize,
+                                  rocm(grad_scale), rocm(found_inf));
+  else
+    at::_ops::_fused_adam_::call(rp, rg, rm, rv, rx, rs, lr, beta1, beta2, wd, eps, amsgrad, maximize,
+                                 rocm(grad_scale), rocm(found_inf));
+}
+
+void fused_adam_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                     at::TensorList mx, at::TensorList steps, double lr, double beta1, double beta2,
+                     double wd, double eps, bool amsgrad, bool maximize,
+                     const std::optional<at::Tensor>& grad_scale,
+                     const std::optional<at::Tensor>& found_inf) {
+  fused_adam_common(p, g, m, v, mx, steps, lr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
+                    found_inf, false);
+}
+
+void fused_adamw_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                      at::TensorList mx, at::TensorList steps, double lr, double beta1, double beta2,
+                      double wd, double eps, bool amsgrad, bool maximize,
+                      const std::optional<at::Tensor>& grad_scale,
+                      const std::optional<at::Tensor>& found_inf) {
+  fused_adam_common(p, g, m, v, mx, steps, lr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
+                    found_inf, true);
+}
+
+double lr_value(const at::Tensor& lr) { return lr.item<double>(); }
+
+void fused_adam_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                         at::TensorList mx, at::TensorList steps, const at::Tensor& lr, double beta1,
+                         double beta2, double wd, double eps, bool amsgrad, bool maximize,
+                         const std::optional<at::Tensor>& grad_scale,
+                         const std::optional<at::Tensor>& found_inf) {
+  fused_adam_common(p, g, m, v, mx, steps, lr_value(lr), beta1, beta2, wd, eps, amsgrad, maximize,
+                    grad_scale, found_inf, false);
+}
+
+void fused_adamw_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                          at::TensorList mx, at::TensorList steps, const at::Tensor& lr, double beta1,
+                          double beta2, double wd, double eps, bool amsgrad, bool maximize,
+                          const std::optional<at::Tensor>& grad_scale,
+                          const std::optional<at::Tensor>& found_inf) {
+  fused_adam_common(p, g, m, v, mx, steps, lr_value(lr), beta1, beta2, wd, eps, amsgrad, maximize,
+                    grad_scale, found_inf, true);
+}
+
+}  // namespace
+
+int64_t dw_jobs() { return g_dw_jobs.load(); }
+
+void register_hot_ops(torch::Library& m) {
+  m.impl("convolution_overrideable", TORCH_FN(convolution_overrideable_xdna));
+  m.impl("convolution_backward_overrideable", TORCH_FN(convolution_backward_overrideable_xdna));
+  m.impl("mm", TORCH_FN(mm_xdna));
+  m.impl("mm.out", TORCH_FN(mm_out_xdna));
+  m.impl("addmm", TORCH_FN(addmm_xdna));
+  m.impl("addmm.out", TORCH_FN(addmm_out_xdna));
+  m.impl("bmm", TORCH_FN(bmm_xdna));
+  m.impl("bmm.out", TORCH_FN(bmm_out_xdna));
+  m.impl("_fused_adam_", TORCH_FN(fused_adam_xdna));
+  m.impl("_fused_adamw_", TORCH_FN(fused_adamw_xdna));
+  m.impl("_fused_adam_.tensor_lr", TORCH_FN(fused_adam_tlr_xdna));
+  m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tlr_xdna));
+}
+
+}  // namespace xdna_backend

@@ -1,0 +1,63 @@
+// Shared declarations of the PrivateUse1 "xdna" backend over HIP device memory.
+//
+// Layer map (reference torch_xdna_device.cpp): device memory, guard and hooks
+// (:131-1318) are device.cpp; the hot operators (:1814-2771, 3740-3790, 4360-4885)
+// are ops.cpp; every kernel is reached through the C ABI of include/xdna_hip.h.
+#pragma once
+
+#include <ATen/ATen.h>
+#include <c10/core/Allocator.h>
+#include <torch/library.h>
+
+#include <atomic>
+#include <cstdint>
+#include <string>
+
+#include "xdna_hip.h"
+
+namespace xdna_backend {
+
+constexpr c10::DeviceType kXdna = c10::DeviceType::PrivateUse1;
+
+// HIP stream all backend work is ordered on: the current stream of device 0, the same
+// one PyTorch-ROCm kernels launched by the fallback use.
+void* current_stream();
+
+// Throws c10::Error with the C ABI's last error when rc != 0.
+void check_abi(int rc, const char* what);
+
+c10::Allocator* xdna_allocator();
+
+// A new xdna tensor (contiguous).
+at::Tensor empty_xdna(at::IntArrayRef size, at::ScalarType dtype,
+                      c10::MemoryFormat fmt = c10::MemoryFormat::Contiguous);
+
+// A ROCm ("cuda") tensor aliasing the memory of an xdna tensor (same sizes, strides,
+// offset); its storage keeps the xdna storage alive.
+at::Tensor cuda_alias(const at::Tensor& t);
+// An xdna tensor sharing the memory of a ROCm tensor (its storage keeps the ROCm
+// storage alive); the inverse of cuda_alias when t's storage is an alias.
+at::Tensor xdna_from_cuda(const at::Tensor& t);
+
+// 0: every op through the generic ROCm fallback; 1: HIP hot path without the HIP weight
+// gradient; 2: all HIP paths (default).  Mirrors the reference's npu mode
+// (xdna_train/device.py:526-650).
+extern std::atomic<int> g_mode;
+
+// Per-path counters (the reference's ScopedMappedCpu, torch_xdna_device.cpp:1470-1521).
+void count_call(const char* name, int64_t ns);
+
+struct ScopedCount {
+  const char* name;
+  int64_t t0;
+  explicit ScopedCount(const char* n);
+  ~ScopedCount();
+};
+
+// Hot-path registrations (ops.cpp).
+void register_hot_ops(torch::Library& m);
+
+// Weight-gradient launches so far (ops.cpp).
+int64_t dw_jobs();
+
+}  // namespace xdna_backend

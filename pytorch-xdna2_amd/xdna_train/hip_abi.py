@@ -64,6 +64,12 @@ SIGNATURES = {
     "xdna_conv3x3_wgrad_workspace_bytes": (Z, [I, I, I, I, I]),
     "xdna_conv3x3_wgrad_bf16": (I, [P, P, P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_bias_grad_bf16": (I, [P, P, I, I, I, I, P]),
+    "xdna_conv3x3w_packed_bytes": (Z, [I, I, I, I]),
+    "xdna_conv3x3_prepared_weight_bytes": (Z, [I, I]),
+    "xdna_conv3x3_prepare_weights_bf16": (I, [P, P, I, I, I, P]),
+    "xdna_conv3x3_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
+    "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_fused_adam": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, D, D, D, D, D, I, I, I, P, P, P]),
 }
