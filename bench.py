@@ -1,0 +1,376 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X xdna hot path on BASELINE.json's workloads.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-style]
+
+Headline (`value`): BASELINE config 2, the 3x3 conv sweep (stride 1, pad 1, bias, bf16;
+N {16,40,64} x C_in = C_out {64,128,256,512} x H = W {18,36,72}, 36 shapes).  One step =
+forward, dgrad and wgrad (+ bias grad) of every shape through the xdna backend's
+convolution ops (the reference's aten::convolution_overrideable /
+convolution_backward_overrideable surface).  value = algorithmic fwd+dgrad+wgrad FLOP of
+the step (2*N*H*W*C*C*9 per direction, real MACs only) / step time, in TFLOP/s.
+
+Also reported, from the same run:
+* "style_net": BASELINE config 4 (Johnson generator + frozen random VGG19 through
+  relu4_1, content + Gram style loss, B40 36x36, Adam) in it/s, beside the same step on
+  the host CPU in bf16 (the reference's CPU BF16 path: stock PyTorch CPU kernels);
+* "adam": fused Adam over config 3's 25,175,040 bf16 parameters (14 B/param), GB/s;
+* "kernels": per-kernel launches / time / achieved rate from HIP events recorded on the
+  launch stream around every hot-kernel launch of the timed region;
+* "roofline": the dominant kernel of the timed region against the MI355X dense bf16
+  MFMA peak (2.5 PFLOP/s), or HBM (8 TB/s) for byte-bound kernels;
+* "cpu_baseline": PyTorch CPU bf16 conv fwd+dgrad+wgrad (the reference's CPU path) on a
+  bounded sample of the sweep, TFLOP/s.
+
+Synthetic data: model seed 0, data seed 1, style image seed 2, sweep shape i seed 1000+i.
+One GPU: --gpus above 1 exits.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "pytorch-xdna2_amd"))
+
+METRIC = "it/s style-net b40@36x36; 3x3-conv fwd+dgrad+wgrad BF16 TFLOP/s"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SWEEP = [(n, c, h) for n in (16, 40, 64) for c in (64, 128, 256, 512) for h in (18, 36, 72)]
+ADAM_PARAMS = 25_175_040    # BASELINE config 3 (Linear 1024->4096->4096->1024)
+
+
+# ---------------------------------------------------------------------------------------
+# style-transfer step
+# ---------------------------------------------------------------------------------------
+def style_models(torch, nn):
+    class ConvIN(nn.Sequential):
+        def __init__(self, cin, cout, k, stride=1, relu=True):
+            layers = [nn.Conv2d(cin, cout, k, stride=stride, padding=k // 2),
+                      nn.InstanceNorm2d(cout, affine=True)]
+            if relu:
+                layers.append(nn.ReLU())
+            super().__init__(*layers)
+
+    class Residual(nn.Module):
+        def __init__(self, c):
+            super().__init__()
+            self.body = nn.Sequential(ConvIN(c, c, 3), ConvIN(c, c, 3, relu=False))
+
+        def forward(self, x):
+            return x + self.body(x)
+
+    class UpConv(nn.Sequential):
+        def __init__(self, cin, cout):
+            super().__init__(nn.Upsample(scale_factor=2, mode="nearest"), ConvIN(cin, cout, 3))
+
+    class Generator(nn.Sequential):
+        """9x9 3->32, 3x3 s2 32->64, 3x3 s2 64->128, 5 residual blocks, 2 x (nearest x2 +
+        3x3 conv) to 64, 32, 9x9 32->3."""
+
+        def __init__(self):
+            super().__init__(ConvIN(3, 32, 9), ConvIN(32, 64, 3, 2), ConvIN(64, 128, 3, 2),
+                             *[Residual(128) for _ in range(5)], UpConv(128, 64), UpConv(64, 32),
+                             nn.Conv2d(32, 3, 9, padding=4))
+
+    # VGG19 conv stack through relu4_1 (random init, frozen)
+    cfg = [(3, 64), (64, 64), "M", (64, 128), (128, 128), "M", (128, 256), (256, 256),
+           (256, 256), (256, 256), "M", (256, 512)]
+    names = ["relu1_1", "relu1_2", "pool1", "relu2_1", "relu2_2", "pool2", "relu3_1",
+             "relu3_2", "relu3_3", "relu3_4", "pool3", "relu4_1"]
+
+    class VGGFeatures(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = nn.ModuleList()
+            for c in cfg:
+                if c == "M":
+                    self.layers.append(nn.MaxPool2d(2))
+                else:
+                    self.layers.append(nn.Sequential(nn.Conv2d(c[0], c[1], 3, padding=1), nn.ReLU()))
+
+        def forward(self, x, taps):
+            out = {}
+            for name, layer in zip(names, self.layers):
+                x = layer(x)
+                if name in taps:
+                    out[name] = x
+            return out
+
+    return Generator, VGGFeatures
+
+
+STYLE_TAPS = ("relu1_1", "relu2_1", "relu3_1", "relu4_1")
+CONTENT_TAP = "relu2_2"
+
+
+def gram(f):
+    b, c, h, w = f.shape
+    x = f.reshape(b, c, h * w)
+    return (x @ x.transpose(1, 2)).float() / float(c * h * w)
+
+
+def build_style(torch, device, batch=40, size=36):
+    nn = torch.nn
+    Generator, VGG = style_models(torch, nn)
+    torch.manual_seed(0)
+    gen = Generator().bfloat16()
+    vgg = VGG().bfloat16()
+    for p in vgg.parameters():
+        p.requires_grad_(False)
+    g1 = torch.Generator().manual_seed(1)
+    content = torch.rand(batch, 3, size, size, generator=g1).bfloat16()
+    g2 = torch.Generator().manual_seed(2)
+    style = torch.rand(1, 3, size, size, generator=g2).bfloat16()
+    gen.to(device)
+    vgg.to(device)
+    content = content.to(device)
+    style = style.to(device)
+    with torch.no_grad():
+        sf = vgg(style, STYLE_TAPS)
+        style_grams = {k: gram(v) for k, v in sf.items()}
+    opt = torch.optim.Adam(gen.parameters(), lr=1e-3, fused=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        out = gen(content)
+        with torch.no_grad():
+            target = vgg(content, (CONTENT_TAP,))[CONTENT_TAP]
+        feats = vgg(out, STYLE_TAPS + (CONTENT_TAP,))
+        loss = torch.nn.functional.mse_loss(feats[CONTENT_TAP].float(), target.float())
+        for k in STYLE_TAPS:
+            g = gram(feats[k])
+            loss = loss + 1e5 * torch.nn.functional.mse_loss(g, style_grams[k].expand_as(g))
+        loss.backward()
+        opt.step()
+        return loss
+
+    return step, gen
+
+
+# ---------------------------------------------------------------------------------------
+def sync(torch):
+    torch.xdna.synchronize()
+
+
+def conv_sweep_data(torch, device, shapes):
+    data = []
+    for idx, (n, c, h) in enumerate(shapes):
+        torch.manual_seed(1000 + idx)
+        bound = math.sqrt(6.0 / (9 * c))
+        x = torch.randn(n, c, h, h, device=device).bfloat16()
+        w = ((torch.rand(c, c, 3, 3, device=device) * 2 - 1) * bound).bfloat16()
+        b = ((torch.rand(c, device=device) * 2 - 1) / math.sqrt(9 * c)).bfloat16()
+        dy = torch.randn(n, c, h, h, device=device).bfloat16()
+        data.append((x, w, b, dy))
+    return data
+
+
+def conv_step(torch, data):
+    aten = torch.ops.aten
+    s, p, d, op = [1, 1], [1, 1], [1, 1], [0, 0]
+    for x, w, b, dy in data:
+        aten.convolution_overrideable(x, w, b, s, p, d, False, op, 1)
+        aten.convolution_backward_overrideable(dy, x, w, s, p, d, False, op, 1, [True, True, True])
+
+
+def sweep_flops(shapes):
+    return sum(3 * 2.0 * n * h * h * c * c * 9 for n, c, h in shapes)
+
+
+def cpu_conv_baseline(torch, budget_s=12.0):
+    """PyTorch CPU bf16 conv fwd + dgrad + wgrad (+ bias grad) over N=16 sweep shapes,
+    repeated until ~budget_s of CPU work."""
+    shapes = [(16, c, h) for c in (64, 128, 256) for h in (18, 36)]
+    flops, t_total = 0.0, 0.0
+    cpu = torch.device("cpu")
+    data = conv_sweep_data(torch, cpu, shapes)
+    reps = 0
+    while t_total < budget_s and reps < 50:
+        for (x, w, b, dy), (n, c, h) in zip(data, shapes):
+            xr = x.clone().requires_grad_()
+            wr = w.clone().requires_grad_()
+            br = b.clone().requires_grad_()
+            t0 = time.perf_counter()
+            y = torch.nn.functional.conv2d(xr, wr, br, padding=1)
+            y.backward(dy)
+            t_total += time.perf_counter() - t0
+            flops += 3 * 2.0 * n * h * h * c * c * 9
+        reps += 1
+    return flops / t_total / 1e12, reps, shapes
+
+
+def kernel_summary(report):
+    out = {}
+    for name, e in report.items():
+        ms = e["total_ms"]
+        rate = e["work"] / (ms * 1e-3) if ms > 0 else 0.0
+        is_bytes = name in ("conv3x3w_pack", "fused_adam")
+        out[name] = {"launches": e["launches"], "total_ms": round(ms, 4),
+                     "avg_us": round(1e3 * ms / max(1, e["launches"]), 3),
+                     ("GB/s" if is_bytes else "TFLOP/s"): round(rate / (1e9 if is_bytes else 1e12), 2)}
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--style-steps", type=int, default=20)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-style", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="small subset (profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one MI355X only (one process, one GPU); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import xdna_train
+
+    assert xdna_train.is_available(), "xdna device not available"
+    from xdna_train import device as xdev
+
+    C = xdev._C
+    X = torch.device("xdna")
+    log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+
+    # --- headline: conv sweep --------------------------------------------------------
+    shapes = SWEEP if not args.quick else [(16, 128, 36), (64, 256, 36)]
+    log(f"conv sweep: {len(shapes)} shapes, building data")
+    data = conv_sweep_data(torch, X, shapes)
+    for _ in range(args.warmup):
+        conv_step(torch, data)
+    sync(torch)
+    log("conv sweep: warm")
+    C.kernel_timing(True)
+    sync(torch)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        conv_step(torch, data)
+    sync(torch)
+    dt = time.perf_counter() - t0
+    kreport = dict(C.kernel_timing_report())
+    C.kernel_timing(False)
+    flops_step = sweep_flops(shapes)
+    value = flops_step * args.steps / dt / 1e12
+    kernels = kernel_summary(kreport)
+    log(f"conv sweep: {value:.1f} TFLOP/s, {1e3 * dt / args.steps:.2f} ms/step")
+
+    # dominant kernel of the timed region (largest total time among the MFMA kernels)
+    groups = {"conv3x3_rows": ["conv3x3_rows.fwd", "conv3x3_rows.dgrad"], "conv3x3_wgrad": ["conv3x3_wgrad"]}
+    tot = {g: sum(kreport.get(n, {}).get("total_ms", 0.0) for n in ns) for g, ns in groups.items()}
+    dom = max(tot, key=tot.get)
+    work = sum(kreport.get(n, {}).get("work", 0.0) for n in groups[dom])
+    launches = sum(kreport.get(n, {}).get("launches", 0) for n in groups[dom])
+    achieved = work / (tot[dom] * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": None, "launches": launches,
+                "avg_launch_us": round(1e3 * tot[dom] / max(1, launches), 3),
+                "flop_per_launch_avg": work / max(1, launches)}
+    per_dir = {}
+    for name in ("conv3x3_rows.fwd", "conv3x3_rows.dgrad", "conv3x3_wgrad"):
+        e = kreport.get(name)
+        if e:
+            per_dir[name] = round(e["work"] / (e["total_ms"] * 1e-3) / 1e12, 1)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations and dY, Kaiming-uniform weights)",
+        "config": {"workload": "BASELINE config 2: 3x3 conv sweep, stride 1, pad 1, bias, bf16, "
+                               "N{16,40,64} x C{64,128,256,512} x H=W{18,36,72}; step = fwd + dgrad + "
+                               "wgrad(+bias grad) of every shape via aten convolution(_backward)_overrideable",
+                   "shapes": len(shapes), "gflop_per_step": round(flops_step / 1e9, 1),
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "kernel_tflops_by_direction": per_dir,
+        "kernels": kernels,
+    }
+
+    # --- fused Adam at config 3's parameter count --------------------------------------
+    params = [torch.nn.Parameter(torch.randn(ADAM_PARAMS, device=X).bfloat16())]
+    params[0].grad = (torch.randn(ADAM_PARAMS, device=X) * 1e-2).bfloat16()
+    opt = torch.optim.Adam(params, lr=1e-3, fused=True)
+    for _ in range(3):
+        opt.step()
+    sync(torch)
+    C.kernel_timing(True)
+    for _ in range(10):
+        opt.step()
+    ar = dict(C.kernel_timing_report()).get("fused_adam", {})
+    C.kernel_timing(False)
+    if ar:
+        gbs = ar["work"] / (ar["total_ms"] * 1e-3) / 1e9
+        result["adam"] = {"params": ADAM_PARAMS, "bytes_per_param": 14, "GB/s": round(gbs, 1),
+                          "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                          "avg_launch_us": round(1e3 * ar["total_ms"] / ar["launches"], 2)}
+        log(f"adam: {gbs:.0f} GB/s")
+    del params, opt
+
+    # --- style step (config 4) ---------------------------------------------------------
+    if not args.skip_style:
+        log("style net: building")
+        step, _ = build_style(torch, X)
+        for _ in range(3):
+            step()
+        sync(torch)
+        t0 = time.perf_counter()
+        for _ in range(args.style_steps):
+            loss = step()
+        loss.item()
+        dts = time.perf_counter() - t0
+        it_s = args.style_steps / dts
+        result["style_net"] = {"it_s": round(it_s, 2), "ms_per_step": round(1e3 * dts / args.style_steps, 3),
+                               "steps": args.style_steps, "loss": float(loss.item())}
+        log(f"style net: {it_s:.1f} it/s")
+        if not args.skip_cpu:
+            cpu_step, _ = build_style(torch, torch.device("cpu"))
+            cpu_step()
+            times = []
+            t_end = time.perf_counter() + 20.0
+            while time.perf_counter() < t_end and len(times) < 20:
+                t1 = time.perf_counter()
+                cpu_step().item()
+                times.append(time.perf_counter() - t1)
+            cpu_it_s = 1.0 / statistics.median(times)
+            result["style_net"].update({"cpu_it_s": round(cpu_it_s, 3), "cpu_steps": len(times),
+                                        "speedup_vs_cpu": round(it_s / cpu_it_s, 1)})
+            log(f"style net CPU: {cpu_it_s:.2f} it/s")
+
+    # --- CPU baseline of the headline ---------------------------------------------------
+    if not args.skip_cpu:
+        log("cpu baseline: conv sweep sample")
+        cpu_tf, reps, cpu_shapes = cpu_conv_baseline(torch)
+        result["cpu_baseline"] = {
+            "value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "reference",
+            "sample": f"PyTorch CPU bf16 conv2d fwd+dgrad+wgrad(+bias grad), the reference's CPU BF16 "
+                      f"path, on {len(cpu_shapes)} sweep shapes (N16, C 64-256, H 18/36) x {reps} reps",
+        }
+        log(f"cpu baseline: {cpu_tf:.3f} TFLOP/s on {torch.get_num_threads()} threads")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -48,11 +48,11 @@ def _digest(paths) -> str:
     return h.hexdigest()[:16]
 
 
-def _compile_hip(src: Path, headers) -> Path:
+def _compile_hip(src: Path, headers, force: bool = False) -> Path:
     obj = BUILD / (src.stem + ".o")
     stamp = BUILD / (src.stem + ".stamp")
     key = _digest([src, *headers])
-    if obj.exists() and stamp.exists() and stamp.read_text() == key:
+    if not force and obj.exists() and stamp.exists() and stamp.read_text() == key:
         return obj
     cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -62,13 +62,13 @@ def _compile_hip(src: Path, headers) -> Path:
     return obj
 
 
-def build_hip(jobs: int = 8) -> Path:
+def build_hip(jobs: int = 8, force: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     LIBDIR.mkdir(parents=True, exist_ok=True)
     headers = list(CSRC.glob("*.h")) + [REPO / "include" / "xdna_hip.h"]
     sources = sorted(CSRC.glob("*.hip"))
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(lambda s: _compile_hip(s, headers), sources))
+        objs = list(ex.map(lambda s: _compile_hip(s, headers, force), sources))
     out = LIBDIR / "libxdna_hip.so"
     tmp = LIBDIR / "libxdna_hip.so.tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libxdna_hip.so",
@@ -80,7 +80,7 @@ def build_hip(jobs: int = 8) -> Path:
     return out
 
 
-def build_ext() -> Path | None:
+def build_ext(force: bool = False) -> Path | None:
     """The PrivateUse1 extension (C++ only; calls the kernels through the C ABI)."""
     sources = sorted(NATIVE.glob("*.cpp"))
     if not sources:
@@ -94,6 +94,8 @@ def build_ext() -> Path | None:
     ctypes.CDLL(str(LIBDIR / "libxdna_hip.so"), mode=ctypes.RTLD_GLOBAL)
     name = "_C"
     build_dir = BUILD / "ext"
+    if force and build_dir.exists():
+        shutil.rmtree(build_dir)
     build_dir.mkdir(parents=True, exist_ok=True)
     torch_lib = Path(cpp_extension.library_paths()[0])
     extra_ldflags = [
@@ -124,12 +126,13 @@ def build_ext() -> Path | None:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--hip-only", action="store_true")
+    ap.add_argument("--force", action="store_true", help="recompile everything")
     ap.add_argument("-j", type=int, default=int(os.environ.get("MAX_JOBS", "8")))
     args = ap.parse_args()
-    lib = build_hip(args.j)
+    lib = build_hip(args.j, args.force)
     print(f"built {lib}")
     if not args.hip_only:
-        ext = build_ext()
+        ext = build_ext(args.force)
         if ext:
             print(f"built {ext}")
     return 0

@@ -594,6 +594,18 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   mod.def("from_cuda", [](const at::Tensor& t) { return xdna_from_cuda(t); });
   mod.def("data_ptr", [](const at::Tensor& t) { return reinterpret_cast<uintptr_t>(t.data_ptr()); });
   mod.def("launch_count", [] { return xdna_hip_launch_count(); });
+  mod.def("kernel_timing", [](bool on) { kernel_timing_enable(on); });
+  mod.def("kernel_timing_report", [] {
+    py::dict d;
+    for (const auto& [name, n, ms, work] : kernel_timing_report()) {
+      py::dict e;
+      e["launches"] = n;
+      e["total_ms"] = ms;
+      e["work"] = work;
+      d[py::str(name)] = e;
+    }
+    return d;
+  });
   mod.def("async_dw_stats", [] {
     py::dict d;
     d["jobs"] = dw_jobs();

@@ -131,10 +131,14 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
   PackedBuf packed = acquire_packed(pbytes, {B, cin, H, W});
   int64_t geo[7];
   check_abi(xdna_conv3x3w_geometry(int(B), int(cin), int(H), int(W), geo), "conv geometry");
-  check_abi(xdna_conv3x3w_pack_input_strips_range_bf16(
-                static_cast<const uint16_t*>(x.const_data_ptr()), static_cast<uint16_t*>(packed.mem.data_ptr()),
-                int(B), int(cin), int(H), int(W), int(geo[0]), int(geo[1]), 0, int(geo[5]), 0, int(geo[4]), st),
-            "conv pack");
+  {
+    const double bytes = 2.0 * double(x.numel()) + double(geo[4]) * double(geo[5]) * 2126.0 * 64.0 * 2.0;
+    KernelTimer kt("conv3x3w_pack", bytes);
+    check_abi(xdna_conv3x3w_pack_input_strips_range_bf16(
+                  static_cast<const uint16_t*>(x.const_data_ptr()), static_cast<uint16_t*>(packed.mem.data_ptr()),
+                  int(B), int(cin), int(H), int(W), int(geo[0]), int(geo[1]), 0, int(geo[5]), 0, int(geo[4]), st),
+              "conv pack");
+  }
   at::Tensor wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
   check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
                                               static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
@@ -143,6 +147,8 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
   at::Tensor out = empty_xdna({B, cout, H, W}, at::kBFloat16);
   at::Tensor bc;
   if (bias) bc = bias->contiguous();
+  const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
+  KernelTimer kt(dgrad ? "conv3x3_rows.dgrad" : "conv3x3_rows.fwd", flops);
   check_abi(xdna_conv3x3_rows_bf16(static_cast<const uint16_t*>(packed.mem.const_data_ptr()),
                                    static_cast<const uint16_t*>(wt.const_data_ptr()),
                                    bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
@@ -190,6 +196,7 @@ void hip_wgrad(const at::Tensor& input, const at::Tensor& dy, at::Tensor& gw, at
                                          static_cast<const uint16_t*>(d.const_data_ptr()), int(B),
                                          int(Cin), int(Cout), int(H), int(W), ws.data_ptr(), wsb, st),
             "conv wgrad pack");
+  KernelTimer kt("conv3x3_wgrad", 2.0 * double(B) * double(H) * double(W) * double(Cin) * double(Cout) * 9.0);
   check_abi(xdna_conv3x3_wgrad_packed_bf16(static_cast<uint16_t*>(gw.data_ptr()),
                                            gb ? static_cast<uint16_t*>(gb->data_ptr()) : nullptr,
                                            int(B), int(Cin), int(Cout), int(H), int(W), ws.data_ptr(),
@@ -288,6 +295,7 @@ void run_gemm(const at::Tensor& a, const at::Tensor& m, at::Tensor& c, const at:
     bsm = be.stride(0);
     bsn = be.stride(1);
   }
+  KernelTimer kt("gemm", 2.0 * double(batch) * double(M) * double(N) * double(K));
   check_abi(xdna_gemm_bf16(static_cast<const uint16_t*>(a.const_data_ptr()),
                            static_cast<const uint16_t*>(m.const_data_ptr()),
                            static_cast<uint16_t*>(c.data_ptr()), bp, int(batch), int(M), int(N), int(K),
@@ -425,6 +433,10 @@ void fused_adam_common(at::TensorList p, at::TensorList g, at::TensorList m, at:
       sp[i] = static_cast<const float*>(steps[i].const_data_ptr());
       numel[i] = p[i].numel();
     }
+    double bytes = 0.0;
+    for (size_t i = 0; i < n; ++i)
+      bytes += double(numel[i]) * double(p[i].element_size()) * (amsgrad ? 9.0 : 7.0);
+    KernelTimer kt("fused_adam", bytes);
     check_abi(xdna_fused_adam(int(n), pp.data(), gp.data(), mp.data(), vp.data(),
                               amsgrad ? xp.data() : nullptr, sp.data(), numel.data(), dtype, lr, beta1,
                               beta2, wd, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, adamw ? 1 : 0,
@@ -484,7 +496,61 @@ void fused_adamw_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, 
                     grad_scale, found_inf, true);
 }
 
+struct TimedLaunch {
+  std::string name;
+  void* start;
+  void* stop;
+  double work;
+};
+std::mutex g_kt_mu;
+std::atomic<bool> g_kt_on{false};
+std::vector<TimedLaunch>& timed() {
+  static auto* v = new std::vector<TimedLaunch>();
+  return *v;
+}
+
 }  // namespace
+
+KernelTimer::KernelTimer(const char* n, double w) : name(n), work(w) {
+  if (!g_kt_on.load(std::memory_order_relaxed)) return;
+  start = xdna_hip_event_create(1);
+  stop = xdna_hip_event_create(1);
+  if (start && stop) xdna_hip_event_record(start, current_stream());
+}
+
+KernelTimer::~KernelTimer() {
+  if (!start || !stop) return;
+  xdna_hip_event_record(stop, current_stream());
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  timed().push_back({name, start, stop, work});
+}
+
+void kernel_timing_enable(bool on) {
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  for (auto& t : timed()) {
+    xdna_hip_event_destroy(t.start);
+    xdna_hip_event_destroy(t.stop);
+  }
+  timed().clear();
+  g_kt_on.store(on);
+}
+
+std::vector<std::tuple<std::string, int64_t, double, double>> kernel_timing_report() {
+  check_abi(xdna_hip_device_synchronize(), "kernel timing");
+  std::map<std::string, std::tuple<int64_t, double, double>> acc;
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  for (const auto& t : timed()) {
+    float ms = 0.0f;
+    if (xdna_hip_event_elapsed_ms(t.start, t.stop, &ms) != 0) continue;
+    auto& a = acc[t.name];
+    std::get<0>(a) += 1;
+    std::get<1>(a) += ms;
+    std::get<2>(a) += t.work;
+  }
+  std::vector<std::tuple<std::string, int64_t, double, double>> out;
+  for (const auto& [k, v] : acc) out.emplace_back(k, std::get<0>(v), std::get<1>(v), std::get<2>(v));
+  return out;
+}
 
 int64_t dw_jobs() { return g_dw_jobs.load(); }
 

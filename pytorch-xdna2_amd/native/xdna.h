@@ -12,6 +12,8 @@
 #include <atomic>
 #include <cstdint>
 #include <string>
+#include <tuple>
+#include <vector>
 
 #include "xdna_hip.h"
 
@@ -59,5 +61,19 @@ void register_hot_ops(torch::Library& m);
 
 // Weight-gradient launches so far (ops.cpp).
 int64_t dw_jobs();
+
+// Live kernel timing: HIP events around hot-kernel launches on the launch stream,
+// with the algorithmic work (FLOP or bytes) of each launch.
+struct KernelTimer {
+  const char* name;
+  double work;
+  void* start = nullptr;
+  void* stop = nullptr;
+  KernelTimer(const char* n, double w);
+  ~KernelTimer();
+};
+void kernel_timing_enable(bool on);
+// name -> (launches, total ms, total work); synchronizes the device.
+std::vector<std::tuple<std::string, int64_t, double, double>> kernel_timing_report();
 
 }  // namespace xdna_backend
