@@ -82,11 +82,19 @@ struct RowsArgs {
   int64_t img, m_total;
 };
 
+// One workgroup: 128 output channels x TP grid rows of one group; wave (wm, wn) owns
+// channels [wm*64, +64) x rows [wn*TP/2, +TP/2) (2 x TP/64 MFMA tiles).  Per input chunk
+// the TP + 2*wp + 2 rows of the halo window sit in LDS (double-buffered: the next chunk's
+// window is fetched into registers while this one is multiplied, one barrier per chunk);
+// the nine taps are row offsets into it.  Weight fragments come straight from L2 into
+// registers, one tap ahead (they are shared by every workgroup and stay L2-resident).
 template <int TP>
-__global__ __launch_bounds__(256) void conv_rows_kernel(RowsArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void conv_rows_kernel(RowsArgs a) {
   constexpr int kXRows = TP + kMaxHalo;
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kXRows * kPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[kTCo * kPitch];
+  constexpr int NT = TP / 64;                       // 32-row MFMA tiles per wave along N
+  constexpr int kXv = (kXRows * 8 + 255) / 256;     // window vectors per thread
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kXRows * kPitch];
 
   constexpr int tiles_per_group = kGroupOutRows / TP;
   const int g = blockIdx.x / tiles_per_group;
@@ -94,61 +102,109 @@ __global__ __launch_bounds__(256) void conv_rows_kernel(RowsArgs a) {
   if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;  // tail tile: no valid row
   const int co0 = blockIdx.y * kTCo;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;  // wave tile: 64 channels x TP/2 rows
-  constexpr int NT = TP / 64;               // 32-row MFMA tiles per wave along N
+  const int wm = wave & 1, wn = wave >> 1;
   const int K = a.chunks * 9 * kKStep;
-  const int nrows = TP + 2 * a.wp + 2;
+  const int nvec = (TP + 2 * a.wp + 2) * 8;         // window vectors actually needed
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
 
   f32x16_t acc[2][NT];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = zero_acc();
+    for (int n = 0; n < NT; ++n) acc[m][n] = zero_acc();
 
-  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  // weight fragments of (chunk, tap): rows co0 + wm*64 + m*32 + lr, k = (ch*9+tap)*64 + ks*16 + lk
+  const uint16_t* wrow0 = a.wt + int64_t(co0 + wm * 64 + lr) * K + lk;
+  const uint16_t* wrow1 = wrow0 + int64_t(32) * K;
+  u32x4_t wa[3][2][4];   // [set][m][ks]: tap t uses set t % 3 (9 taps per chunk keep the rotation)
+  u32x4_t xr[kXv];
+
+#define XDNA_ROWS_LOADW(set_, ch_, tap_)                                                     \
+  do {                                                                                       \
+    const int kb_ = ((ch_) * 9 + (tap_)) * kKStep;                                           \
+    _Pragma("unroll") for (int ks = 0; ks < 4; ++ks) {                                       \
+      wa[set_][0][ks] = *reinterpret_cast<const u32x4_t*>(wrow0 + kb_ + ks * 16);            \
+      wa[set_][1][ks] = *reinterpret_cast<const u32x4_t*>(wrow1 + kb_ + ks * 16);            \
+    }                                                                                        \
+  } while (0)
+#define XDNA_ROWS_LOADX(ch_)                                                                 \
+  do {                                                                                       \
+    const uint16_t* src_ = a.xp + ((int64_t(g) * a.chunks + (ch_)) * kGroupRows + r0) * kKStep; \
+    _Pragma("unroll") for (int j = 0; j < kXv; ++j) {                                        \
+      const int i = tid + j * 256;                                                           \
+      if (i < nvec) xr[j] = *reinterpret_cast<const u32x4_t*>(src_ + (i >> 3) * kKStep + (i & 7) * 8); \
+    }                                                                                        \
+  } while (0)
+#define XDNA_ROWS_STOREX(buf_)                                                               \
+  do {                                                                                       \
+    _Pragma("unroll") for (int j = 0; j < kXv; ++j) {                                        \
+      const int i = tid + j * 256;                                                           \
+      if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[buf_][(i >> 3) * kPitch + (i & 7) * 8]) = xr[j]; \
+    }                                                                                        \
+  } while (0)
+
+  // weights two taps ahead
+  XDNA_ROWS_LOADW(0, 0, 0);
+  XDNA_ROWS_LOADW(1, 0, 1);
+  XDNA_ROWS_LOADX(0);
+  XDNA_ROWS_STOREX(0);
+  __syncthreads();
+
   for (int ch = 0; ch < a.chunks; ++ch) {
-    __syncthreads();
-    const uint16_t* xsrc = a.xp + ((int64_t(g) * a.chunks + ch) * kGroupRows + r0) * kKStep;
-    for (int i = tid; i < nrows * 8; i += 256) {
-      const int row = i >> 3, q = i & 7;
-      *reinterpret_cast<uint4*>(xs + row * kPitch + q * 8) =
-          *reinterpret_cast<const uint4*>(xsrc + row * kKStep + q * 8);
-    }
+    const int cur = ch & 1;
+    const bool more = ch + 1 < a.chunks;
+    const uint16_t* xb = &xs[cur][(wn * (TP / 2) + lr) * kPitch + lk];
+    // B fragments are software-pipelined one 16-wide k-step ahead (36 steps per chunk:
+    // 9 taps x 4), so LDS latency hides behind the 2*NT MFMAs of the current step.
+    u32x4_t bq[2][NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+      bq[0][n] = *reinterpret_cast<const u32x4_t*>(xb + n * 32 * kPitch);
+#pragma unroll
     for (int tap = 0; tap < 9; ++tap) {
-      if (tap) __syncthreads();
-      const uint16_t* wsrc = a.wt + int64_t(co0) * K + (ch * 9 + tap) * kKStep;
-      for (int i = tid; i < kTCo * 8; i += 256) {
-        const int row = i >> 3, q = i & 7;
-        *reinterpret_cast<uint4*>(ws + row * kPitch + q * 8) =
-            *reinterpret_cast<const uint4*>(wsrc + int64_t(row) * K + q * 8);
+      const int set = tap % 3;
+      // weights of tap + 2 first, so the window prefetch below can stay in flight
+      if (tap < 7) {
+        XDNA_ROWS_LOADW((tap + 2) % 3, ch, tap + 2);
+      } else if (more) {
+        XDNA_ROWS_LOADW((tap + 2) % 3, ch + 1, tap - 7);
       }
-      __syncthreads();
-      const int off = (tap / 3) * a.wp + (tap % 3);
+      if (tap == 0 && more) XDNA_ROWS_LOADX(ch + 1);
 #pragma unroll
-      for (int ks = 0; ks < kKStep / 16; ++ks) {
-        bf16x8_t af[2], bfr[NT];
+      for (int ks = 0; ks < 4; ++ks) {
+        const int step = tap * 4 + ks;
+        if (step + 1 < 36) {
+          const int ntap = (step + 1) >> 2, nks = (step + 1) & 3;
+          const int noff = ((ntap / 3) * a.wp + (ntap % 3)) * kPitch + nks * 16;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          af[mt] = as_bf16x8(*reinterpret_cast<const uint4*>(
-              ws + (wm * 64 + mt * 32 + lr) * kPitch + ks * 16 + lk));
+          for (int n = 0; n < NT; ++n)
+            bq[(step + 1) & 1][n] = *reinterpret_cast<const u32x4_t*>(xb + noff + n * 32 * kPitch);
+        }
+        // keep the next step's LDS reads ahead of this step's MFMAs (the scheduler would
+        // otherwise sink each read next to its use and expose its latency)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          bfr[nt] = as_bf16x8(*reinterpret_cast<const uint4*>(
-              xs + (wn * (TP / 2) + nt * 32 + lr + off) * kPitch + ks * 16 + lk));
+        for (int n = 0; n < NT; ++n) {
+          const bf16x8_t bfr = as_bf16x8(bq[step & 1][n]);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma_32x32x16(af[mt], bfr[nt], acc[mt][nt]);
+          for (int m = 0; m < 2; ++m) acc[m][n] = mfma_32x32x16(as_bf16x8(wa[set][m][ks]), bfr, acc[m][n]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (more) XDNA_ROWS_STOREX(cur ^ 1);
+    __syncthreads();
   }
+#undef XDNA_ROWS_LOADW
+#undef XDNA_ROWS_LOADX
+#undef XDNA_ROWS_STOREX
 
   // Epilogue: grid row -> NCHW pixel, bias in fp32, one rounding.
   const int first = a.S == 1 ? 0 : 1;
   const int64_t plane = int64_t(a.H) * a.W;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + nt * 32 + lr;
+  for (int n = 0; n < NT; ++n) {
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
     if (p >= a.m_total) continue;
     const int64_t vb = p / a.img;
     const int64_t rem = p - vb * a.img;
@@ -161,12 +217,12 @@ __global__ __launch_bounds__(256) void conv_rows_kernel(RowsArgs a) {
     const int x = (a.S == 1 ? 0 : s * a.So) + col;
     uint16_t* obase = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int co = co0 + wm * 64 + mt * 32 + mfma_row(i, lane);
+        const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
         if (co < a.cout) {
-          float v = acc[mt][nt][i];
+          float v = acc[m][n][i];
           if (a.bias) v += bf16_to_f32(a.bias[co]);
           obase[int64_t(co) * plane] = f32_to_bf16(v);
         }
@@ -241,87 +297,152 @@ struct WgradArgs {
   int wlen;            // staged window length (elements): kTK + 2*wp8 + 8
 };
 
-// LDS: dY tile [128][kPitch] then the x window [64][xpitch].
-__global__ __launch_bounds__(256) void wgrad_kernel(WgradArgs a) {
+// One workgroup (8 waves, 512 threads): 128 output channels x 64 input channels x 9 taps
+// over the k-tiles of one split.  Wave (wm, wn) owns channels [wm*32, +32) x input
+// channels [wn*32, +32) x all 9 taps (9 accumulator tiles), fed per 16-pixel step by one
+// dY fragment and 3 x (16 + 4)-byte LDS reads of the x window (dx = 0, 1, 2 are built from
+// each read with alignbit).  Fragments are software-pipelined one step ahead; the next
+// k-tile is fetched into registers while the current one is multiplied, and LDS is
+// double-buffered ([dY 128 x kPitch][x 64 x xpitch] per buffer): one barrier per k-tile.
+// Two waves per SIMD.
+constexpr int kWgThreads = 512;
+constexpr int kWgMaxXv = 6;  // x-window vectors per thread (64 * wlen/8 <= 3072: wlen <= 384)
+
+// XV: x-window vectors per thread (4: wlen <= 256, i.e. W <= 90; 6: wlen <= 384)
+template <int XV>
+__global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void wgrad_kernel(WgradArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* ds = smem;
-  uint16_t* xs = smem + kTCo * kPitch;
+  const int buf_elems = kTCo * kPitch + 64 * a.xpitch;
   const int co0 = blockIdx.x * kTCo;
   const int ci0 = blockIdx.y * 64;
   const int split = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
   const int lr = lane & 31, lk = (lane >> 5) * 8;
   const int kt0 = split * a.kt_per_split;
   const int kt1 = min(a.ktiles, kt0 + a.kt_per_split);
-
-  f32x16_t acc[9][2];
-#pragma unroll
-  for (int t = 0; t < 9; ++t) {
-    acc[t][0] = zero_acc();
-    acc[t][1] = zero_acc();
-  }
-  float bsum = 0.0f;
-  const bool do_bias = a.bpart && blockIdx.y == 0;
   const int nvec_w = a.wlen / 8;
+  const int nx = 64 * nvec_w;
 
+  f32x16_t acc[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) acc[t] = zero_acc();
+  float bsum = 0.0f;
+  const bool do_bias = a.bpart && blockIdx.y == 0 && wn == 0;
+
+  u32x4_t dreg[2];
+  u32x4_t xreg[XV];
+  // global -> registers (k-tile kt), registers -> LDS buffer; macros keep the prefetch
+  // arrays in registers (fully unrolled, constant indices)
+#define XDNA_WG_LOAD(kt_)                                                                    \
+  do {                                                                                       \
+    const int64_t k0_ = int64_t(kt_) * kTK;                                                  \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+      const int i = tid + j * kWgThreads;                                                    \
+      dreg[j] = *reinterpret_cast<const u32x4_t*>(a.dt + int64_t(co0 + (i >> 3)) * a.q + k0_ + \
+                                                  (i & 7) * 8);                              \
+    }                                                                                        \
+    _Pragma("unroll") for (int j = 0; j < XV; ++j) {                                         \
+      const int i = tid + j * kWgThreads;                                                    \
+      const int row = i / nvec_w, qv = i - row * nvec_w;                                     \
+      if (i < nx)                                                                            \
+        xreg[j] = *reinterpret_cast<const u32x4_t*>(a.xt + int64_t(ci0 + row) * a.q + k0_ +  \
+                                                    qv * 8);                                 \
+    }                                                                                        \
+  } while (0)
+#define XDNA_WG_STORE(buf_)                                                                  \
+  do {                                                                                       \
+    uint16_t* ds_ = smem + (buf_) * buf_elems;                                               \
+    uint16_t* xs_ = ds_ + kTCo * kPitch;                                                     \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+      const int i = tid + j * kWgThreads;                                                    \
+      *reinterpret_cast<u32x4_t*>(ds_ + (i >> 3) * kPitch + (i & 7) * 8) = dreg[j];          \
+    }                                                                                        \
+    _Pragma("unroll") for (int j = 0; j < XV; ++j) {                                         \
+      const int i = tid + j * kWgThreads;                                                    \
+      const int row = i / nvec_w, qv = i - row * nvec_w;                                     \
+      if (i < nx) *reinterpret_cast<u32x4_t*>(xs_ + row * a.xpitch + qv * 8) = xreg[j];      \
+    }                                                                                        \
+  } while (0)
+
+  if (kt0 < kt1) {
+    XDNA_WG_LOAD(kt0);
+    XDNA_WG_STORE(0);
+  }
+  __syncthreads();
   for (int kt = kt0; kt < kt1; ++kt) {
-    const int64_t k0 = int64_t(kt) * kTK;
-    __syncthreads();
-    for (int i = tid; i < kTCo * 8; i += 256) {
-      const int row = i >> 3, qv = i & 7;
-      *reinterpret_cast<uint4*>(ds + row * kPitch + qv * 8) =
-          *reinterpret_cast<const uint4*>(a.dt + int64_t(co0 + row) * a.q + k0 + qv * 8);
-    }
-    for (int i = tid; i < 64 * nvec_w; i += 256) {
-      const int row = i / nvec_w, qv = i - row * nvec_w;
-      *reinterpret_cast<uint4*>(xs + row * a.xpitch + qv * 8) =
-          *reinterpret_cast<const uint4*>(a.xt + int64_t(ci0 + row) * a.q + k0 + qv * 8);
-    }
-    __syncthreads();
+    const int cur = (kt - kt0) & 1;
+    const bool more = kt + 1 < kt1;
+    if (more) XDNA_WG_LOAD(kt + 1);
+    const uint16_t* ds = smem + cur * buf_elems;
+    const uint16_t* xs = ds + kTCo * kPitch;
+    const uint16_t* arow = ds + (wm * 32 + lr) * kPitch + lk;
+    const uint16_t* xrow = xs + (wn * 32 + lr) * a.xpitch + lk;
+    u32x4_t av[2], lo[2][3];
+    uint32_t hi[2][3];
+#define XDNA_WG_FRAGS(slot_, ks_)                                                            \
+  do {                                                                                       \
+    av[slot_] = *reinterpret_cast<const u32x4_t*>(arow + (ks_) * 16);                        \
+    _Pragma("unroll") for (int dy = 0; dy < 3; ++dy) {                                       \
+      const uint16_t* src_ = xrow + (ks_) * 16 + dy * a.wp8;                                 \
+      lo[slot_][dy] = *reinterpret_cast<const u32x4_t*>(src_);                               \
+      hi[slot_][dy] = *reinterpret_cast<const uint32_t*>(src_ + 8);                          \
+    }                                                                                        \
+  } while (0)
+    XDNA_WG_FRAGS(0, 0);
 #pragma unroll
     for (int ks = 0; ks < kTK / 16; ++ks) {
-      const uint4 av = *reinterpret_cast<const uint4*>(ds + (wave * 32 + lr) * kPitch + ks * 16 + lk);
+      const int sl = ks & 1;
+      if (ks + 1 < kTK / 16) XDNA_WG_FRAGS(sl ^ 1, ks + 1);
+      // keep the next step's LDS reads ahead of this step's MFMAs
+      __builtin_amdgcn_sched_barrier(0);
       if (do_bias) {
-        const uint32_t u[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bsum += __uint_as_float(u[e] << 16) + __uint_as_float(u[e] & 0xFFFF0000u);
+        for (int e = 0; e < 4; ++e)
+          bsum += __uint_as_float(av[sl][e] << 16) + __uint_as_float(av[sl][e] & 0xFFFF0000u);
       }
-      const bf16x8_t af = as_bf16x8(av);
+      const bf16x8_t af = as_bf16x8(av[sl]);
 #pragma unroll
-      for (int dy = 0; dy < 3; ++dy)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint16_t* src = xs + (h * 32 + lr) * a.xpitch + ks * 16 + lk + dy * a.wp8;
-          const uint4 lo = *reinterpret_cast<const uint4*>(src);
-          const uint32_t hi = *reinterpret_cast<const uint32_t*>(src + 8);
-          const uint4 s1 = make_uint4(__builtin_amdgcn_alignbit(lo.y, lo.x, 16),
-                                      __builtin_amdgcn_alignbit(lo.z, lo.y, 16),
-                                      __builtin_amdgcn_alignbit(lo.w, lo.z, 16),
-                                      __builtin_amdgcn_alignbit(hi, lo.w, 16));
-          const uint4 s2 = make_uint4(lo.y, lo.z, lo.w, hi);
-          acc[dy * 3 + 0][h] = mfma_32x32x16(af, as_bf16x8(lo), acc[dy * 3 + 0][h]);
-          acc[dy * 3 + 1][h] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1][h]);
-          acc[dy * 3 + 2][h] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2][h]);
-        }
+      for (int dy = 0; dy < 3; ++dy) {
+        const u32x4_t l = lo[sl][dy];
+        const uint32_t h = hi[sl][dy];
+        u32x4_t s1, s2;
+        s1[0] = __builtin_amdgcn_alignbit(l[1], l[0], 16);
+        s1[1] = __builtin_amdgcn_alignbit(l[2], l[1], 16);
+        s1[2] = __builtin_amdgcn_alignbit(l[3], l[2], 16);
+        s1[3] = __builtin_amdgcn_alignbit(h, l[3], 16);
+        s2[0] = l[1];
+        s2[1] = l[2];
+        s2[2] = l[3];
+        s2[3] = h;
+        acc[dy * 3 + 0] = mfma_32x32x16(af, as_bf16x8(l), acc[dy * 3 + 0]);
+        acc[dy * 3 + 1] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1]);
+        acc[dy * 3 + 2] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+#undef XDNA_WG_FRAGS
+    if (more) XDNA_WG_STORE(cur ^ 1);
+    __syncthreads();
   }
+#undef XDNA_WG_LOAD
+#undef XDNA_WG_STORE
 
   // Partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci.
   float* pbase = a.part + int64_t(split) * a.co_pad * 9 * a.ci_pad;
+  const int ci = ci0 + wn * 32 + lr;
 #pragma unroll
   for (int t = 0; t < 9; ++t)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int co = co0 + wave * 32 + mfma_row(i, lane);
-        const int ci = ci0 + h * 32 + lr;
-        pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][h][i];
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 32 + mfma_row(i, lane);
+      pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][i];
+    }
   if (do_bias) {
-    // lane l and l+32 hold the two k-halves of channel row l%32.
+    // lanes l and l+32 hold the two k-halves of channel row l % 32
     const float other = __shfl_down(bsum, 32, 64);
-    if (lane < 32) a.bpart[int64_t(split) * a.co_pad + co0 + wave * 32 + lane] = bsum + other;
+    if (lane < 32) a.bpart[int64_t(split) * a.co_pad + co0 + wm * 32 + lane] = bsum + other;
   }
 }
 
@@ -431,14 +552,17 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.m_total = geom.m_total;
   if (!admit_launch("conv3x3 rows")) return -1;
   const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
-  // Small problems: 64-row tiles to put more workgroups on the 256 CUs.
-  const int64_t big_tiles = int64_t(geom.groups) * (kGroupOutRows / 128) * ytiles;
-  if (big_tiles >= 512) {
-    conv_rows_kernel<128><<<dim3(unsigned(geom.groups * (kGroupOutRows / 128)), ytiles), 256, 0,
-                            as_stream(stream)>>>(a);
+  // Tile rows per workgroup: the largest of 256 / 128 / 64 that still puts a few
+  // hundred workgroups on the 256 CUs.
+  const int64_t wg256 = int64_t(geom.groups) * (kGroupOutRows / 256) * ytiles;
+  const int64_t wg128 = int64_t(geom.groups) * (kGroupOutRows / 128) * ytiles;
+  hipStream_t st = as_stream(stream);
+  if (wg256 >= 384) {
+    conv_rows_kernel<256><<<dim3(unsigned(geom.groups * (kGroupOutRows / 256)), ytiles), 256, 0, st>>>(a);
+  } else if (wg128 >= 384) {
+    conv_rows_kernel<128><<<dim3(unsigned(geom.groups * (kGroupOutRows / 128)), ytiles), 256, 0, st>>>(a);
   } else {
-    conv_rows_kernel<64><<<dim3(unsigned(geom.groups * (kGroupOutRows / 64)), ytiles), 256, 0,
-                           as_stream(stream)>>>(a);
+    conv_rows_kernel<64><<<dim3(unsigned(geom.groups * (kGroupOutRows / 64)), ytiles), 256, 0, st>>>(a);
   }
   return check_launch("conv3x3 rows");
 }
@@ -457,12 +581,24 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
   p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
   const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
   const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
-  // Enough workgroups to cover the CUs twice, capped so the fp32 partials stay
-  // within ~32 MiB (they live in the MALL between the two kernels).
-  int64_t splits = ceil_div(512, tiles);
-  const int64_t cap = std::max<int64_t>(1, (int64_t(32) << 20) / (out_elems * 4));
-  splits = std::max<int64_t>(1, std::min({splits, cap, p.cm.ktiles}));
-  p.kt_per = int(ceil_div(p.cm.ktiles, splits));
+  // Split-K: pick the split count s that minimizes a simple model of the two kernels,
+  //   flops / (min(tiles*s, CUs) * per-CU rate) + (write + read of s fp32 partials) / BW,
+  // i.e. enough workgroups to fill the 256 CUs without drowning small problems in
+  // partial-sum traffic.
+  const double flops = 2.0 * 9.0 * double(B) * H * W * double(Cin) * double(Cout);
+  const double cu_rate = 4.0e12, bw = 5.0e12;
+  int64_t best = 1;
+  double best_t = 1e30;
+  const int64_t smax = std::min<int64_t>(p.cm.ktiles, 4096);
+  for (int64_t s = 1; s <= smax; s = s < 16 ? s + 1 : s + s / 8) {
+    const double wgs = double(std::min<int64_t>(tiles * s, 256));
+    const double t = flops / (wgs * cu_rate) + 2.0 * double(s) * double(out_elems) * 4.0 / bw;
+    if (t < best_t) {
+      best_t = t;
+      best = s;
+    }
+  }
+  p.kt_per = int(ceil_div(p.cm.ktiles, best));
   p.splits = int(ceil_div(p.cm.ktiles, p.kt_per));
   p.wlen = kTK + 2 * p.cm.wp8 + 8;
   p.xpitch = int(ceil_div(p.wlen, 16) * 16 + 8);
@@ -470,11 +606,11 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
   p.dt_bytes = align256(size_t(p.co_pad) * p.cm.q * 2);
   p.part_bytes = align256(size_t(p.splits) * out_elems * 4);
   p.bpart_bytes = align256(size_t(p.splits) * p.co_pad * 4);
-  p.lds_bytes = size_t(kTCo) * kPitch * 2 + size_t(64) * p.xpitch * 2;
+  p.lds_bytes = 2 * (size_t(kTCo) * kPitch * 2 + size_t(64) * p.xpitch * 2);  // double-buffered
   return p;
 }
 
-constexpr size_t kMaxWgradLds = 64 * 1024;
+constexpr size_t kMaxWgradLds = 160 * 1024;
 
 }  // namespace
 }  // namespace xdna
@@ -548,7 +684,7 @@ struct WgradBufs {
 
 bool wgrad_bufs(const char* what, const WgradPlan& p, void* workspace, size_t workspace_bytes,
                 WgradBufs& b) {
-  if (p.lds_bytes > kMaxWgradLds) {
+  if (p.lds_bytes > kMaxWgradLds || 64 * (p.wlen / 8) > kWgMaxXv * kWgThreads) {
     set_error(std::string(what) + ": image too wide for the LDS window");
     return false;
   }
@@ -605,8 +741,22 @@ int xdna_conv3x3_wgrad_packed_bf16(uint16_t* gw, uint16_t* gb, int B, int Cin, i
   a.ktiles = int(p.cm.ktiles);
   a.xpitch = p.xpitch;
   a.wlen = p.wlen;
-  wgrad_kernel<<<dim3(unsigned(p.co_pad / kTCo), unsigned(p.ci_pad / 64), unsigned(p.splits)), 256,
-                 p.lds_bytes, st>>>(a);
+  static bool lds_attr = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_kernel<4>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
+           hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_kernel<6>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess;
+  }();
+  if (!lds_attr) {
+    (void)hipGetLastError();
+    set_error("conv3x3 wgrad: cannot raise the dynamic LDS limit");
+    return -1;
+  }
+  const dim3 grid(unsigned(p.co_pad / kTCo), unsigned(p.ci_pad / 64), unsigned(p.splits));
+  if (64 * (p.wlen / 8) <= 4 * kWgThreads)
+    wgrad_kernel<4><<<grid, kWgThreads, p.lds_bytes, st>>>(a);
+  else
+    wgrad_kernel<6><<<grid, kWgThreads, p.lds_bytes, st>>>(a);
   const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
   wgrad_reduce_kernel<<<int(std::min<int64_t>(ceil_div(n, 256), 8192)), 256, 0, st>>>(
       bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);

@@ -16,12 +16,16 @@ namespace xdna {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+// 16-byte register vector (HIP's uint4 is a struct over a union, which keeps arrays of it
+// in scratch memory; this native vector type stays in VGPRs)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ inline f32x16_t mfma_32x32x16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ inline bf16x8_t as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8_t, u); }
+__device__ inline bf16x8_t as_bf16x8(const u32x4_t& u) { return __builtin_bit_cast(bf16x8_t, u); }
 
 // Row (within a 32x32 tile) of accumulator register i for lane l.
 __device__ inline int mfma_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
