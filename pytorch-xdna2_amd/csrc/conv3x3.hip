@@ -107,11 +107,21 @@ void conv_rows_kernel(RowsArgs a) {
   const int nvec = (TP + 2 * a.wp + 2) * 8;         // window vectors actually needed
   const int lr = lane & 31, lk = (lane >> 5) * 8;
 
+  // accumulators start at the bias (fp32), so the epilogue is one rounding and a store
   f32x16_t acc[2][NT];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+  for (int m = 0; m < 2; ++m) {
+    f32x16_t init = zero_acc();
+    if (a.bias) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n) acc[m][n] = zero_acc();
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
+        init[i] = co < a.cout ? bf16_to_f32(a.bias[co]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[m][n] = init;
+  }
 
   // weight fragments of (chunk, tap): rows co0 + wm*64 + m*32 + lr, k = (ch*9+tap)*64 + ks*16 + lk
   const uint16_t* wrow0 = a.wt + int64_t(co0 + wm * 64 + lr) * K + lk;
@@ -199,11 +209,14 @@ void conv_rows_kernel(RowsArgs a) {
 #undef XDNA_ROWS_LOADX
 #undef XDNA_ROWS_STOREX
 
-  // Epilogue: grid row -> NCHW pixel, bias in fp32, one rounding.
+  // Epilogue: grid row -> NCHW pixel, one rounding; lanes 0..31 store 32 consecutive
+  // grid rows (mostly consecutive image columns) of one channel.
   const int first = a.S == 1 ? 0 : 1;
   const int64_t plane = int64_t(a.H) * a.W;
+  uint16_t* obase[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
+    obase[n] = nullptr;
     const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
     if (p >= a.m_total) continue;
     const int64_t vb = p / a.img;
@@ -215,19 +228,18 @@ void conv_rows_kernel(RowsArgs a) {
     const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
     if (col >= cols) continue;
     const int x = (a.S == 1 ? 0 : s * a.So) + col;
-    uint16_t* obase = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
-        if (co < a.cout) {
-          float v = acc[m][n][i];
-          if (a.bias) v += bf16_to_f32(a.bias[co]);
-          obase[int64_t(co) * plane] = f32_to_bf16(v);
-        }
-      }
+    obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
   }
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
+      if (co >= a.cout) continue;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
+    }
 }
 
 // ---------------------------------------------------------------------------------
@@ -253,36 +265,120 @@ CmGeom cm_geom(int B, int H, int W) {
 // dst[c][q] for c < c_pad, q < qlen; shift = 1 places pixel (y, x) at grid (y+1, x+1)
 // (the conv input), shift = 0 at (y, x) (the output gradient).  Every element is
 // written (zeros outside the image and for c >= C).
+//
+// Workgroups [0, nmain) each take grid rows [gy0, gy0 + rows_per) of planes_per
+// consecutive (b, c) planes (planes_per > 1 only when whole planes fit): the source rows
+// they need are one contiguous run of NCHW, read with 16-byte loads into LDS (placed so
+// that 16-byte aligned global addresses stay 16-byte aligned in LDS), then written as
+// 16-byte pieces of padded grid rows.  The remaining workgroups zero the rows c >= C and
+// the tail of every row past the last image.
+constexpr int kCmLdsElems = 8192;  // 16 KiB of staged source rows
+
 __global__ __launch_bounds__(256) void pack_cm_kernel(const uint16_t* __restrict__ src,
                                                       uint16_t* __restrict__ dst, int B, int C,
                                                       int H, int W, int c_pad, int wp8,
-                                                      int64_t img, int64_t qlen, int shift) {
-  const int64_t nvec_row = qlen / 8;
-  const int64_t n = int64_t(c_pad) * nvec_row;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += int64_t(gridDim.x) * blockDim.x) {
-    const int c = int(i / nvec_row);
-    const int64_t q0 = (i - int64_t(c) * nvec_row) * 8;
-    uint32_t u[4] = {0, 0, 0, 0};
-    const int64_t b = q0 / img;
-    if (c < C && b < B) {
-      const int64_t rem = q0 - b * img;
-      const int yy = int(rem / wp8) - shift;
-      const int xx0 = int(rem - int64_t(yy + shift) * wp8) - shift;
-      if (yy >= 0 && yy < H) {
-        const uint16_t* row = src + ((b * C + c) * H + yy) * W;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int xx = xx0 + e;
-          if (xx >= 0 && xx < W) {
-            const uint32_t h = row[xx];
-            u[e >> 1] |= (e & 1) ? (h << 16) : h;
-          }
-        }
+                                                      int64_t img, int64_t qlen, int shift,
+                                                      int rows_per, int rblocks, int planes_per,
+                                                      int64_t nmain) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[kCmLdsElems + 16];
+  const int64_t bid = blockIdx.x;
+  const int64_t tail0 = int64_t(B) * img;  // first q past the last image
+  if (bid >= nmain) {
+    // zero fill: rows c < C from tail0 (a multiple of 8), rows c >= C whole
+    const int64_t tvec = (qlen - tail0) / 8, rvec = qlen / 8;
+    const int64_t n = int64_t(C) * tvec + int64_t(c_pad - C) * rvec;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    for (int64_t i = (bid - nmain) * 256 + threadIdx.x; i < n; i += (int64_t(gridDim.x) - nmain) * 256) {
+      int64_t o;
+      if (i < int64_t(C) * tvec) {
+        const int64_t c = i / tvec;
+        o = c * qlen + tail0 + (i - c * tvec) * 8;
+      } else {
+        const int64_t k = i - int64_t(C) * tvec;
+        const int64_t c = C + k / rvec;
+        o = c * qlen + (k - (c - C) * rvec) * 8;
+      }
+      *reinterpret_cast<uint4*>(dst + o) = z;
+    }
+    return;
+  }
+  const int rb = int(bid % rblocks);
+  const int64_t pl0 = (bid / rblocks) * planes_per;  // first source plane b*C + c
+  const int np = int(std::min<int64_t>(planes_per, int64_t(B) * C - pl0));
+  const int gy0 = rb * rows_per;
+  const int gy1 = min(gy0 + rows_per, H + 2);
+  const int vrow = wp8 / 8;
+  const int nout_pl = (gy1 - gy0) * vrow;
+  // source rows needed: yy = gy - shift for gy in [gy0, gy1), clipped to [0, H)
+  const int ylo = max(gy0 - shift, 0), yhi = min(gy1 - shift, H);
+  if (yhi > ylo) {
+    const int64_t off = (pl0 * H + ylo) * W;  // element offset of the run
+    const int len = ((np - 1) * H + yhi - ylo) * W;
+    const int lead = int(off & 7);            // LDS index of element 0
+    const int64_t abase = off - lead;         // 16-byte aligned start
+    const int nvec = (lead + len + 7) >> 3;
+    const bool full_ok = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    for (int v = threadIdx.x; v < nvec; v += 256) {
+      const int e0 = v * 8;
+      if (full_ok && e0 >= lead && e0 + 8 <= lead + len) {
+        *reinterpret_cast<uint4*>(lds + e0) = *reinterpret_cast<const uint4*>(src + abase + e0);
+      } else {
+        for (int e = e0; e < e0 + 8; ++e)
+          if (e >= lead && e < lead + len) lds[e] = src[abase + e];
       }
     }
-    *reinterpret_cast<uint4*>(dst + int64_t(c) * qlen + q0) = make_uint4(u[0], u[1], u[2], u[3]);
+    __syncthreads();
+    for (int v = threadIdx.x; v < np * nout_pl; v += 256) {
+      const int k = v / nout_pl;
+      const int vv = v - k * nout_pl;
+      const int r = vv / vrow;
+      const int x0 = (vv - r * vrow) * 8 - shift;
+      const int yy = gy0 + r - shift;
+      uint32_t u[4] = {0, 0, 0, 0};
+      if (yy >= 0 && yy < H) {
+        const uint16_t* lr = lds + lead + (k * H + yy - ylo) * W;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int xx = x0 + e;
+          if (xx >= 0 && xx < W) u[e >> 1] |= uint32_t(lr[xx]) << (16 * (e & 1));
+        }
+      }
+      const int64_t pl = pl0 + k;
+      const int64_t b = pl / C, c = pl - b * C;
+      uint16_t* d = dst + c * qlen + b * img + int64_t(gy0) * wp8 + int64_t(vv) * 8;
+      *reinterpret_cast<uint4*>(d) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+  } else {
+    // grid rows with no source row (a single plane): all zero
+    const int64_t b = pl0 / C, c = pl0 - b * C;
+    uint16_t* drow = dst + c * qlen + b * img + int64_t(gy0) * wp8;
+    for (int v = threadIdx.x; v < nout_pl; v += 256)
+      *reinterpret_cast<uint4*>(drow + int64_t(v) * 8) = make_uint4(0, 0, 0, 0);
   }
+}
+
+// Launches pack_cm_kernel for one operand.
+int pack_cm_launch(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W, int c_pad,
+                   const CmGeom& cm, int shift, hipStream_t st) {
+  // grid rows per workgroup: the source run (rows_per rows of W, plus alignment lead)
+  // must fit the LDS buffer; small planes are batched while the grid stays large
+  const int rows_per = std::max(1, std::min(H + 2, (kCmLdsElems - 8) / std::max(W, 1)));
+  const int rblocks = int(ceil_div(H + 2, rows_per));
+  const int64_t planes = int64_t(B) * C;
+  int planes_per = 1;
+  if (rblocks == 1)
+    planes_per = int(std::max<int64_t>(1, std::min<int64_t>((kCmLdsElems - 8) / (int64_t(H) * W), planes / 2048)));
+  const int64_t nmain = ceil_div(planes, planes_per) * rblocks;
+  const int64_t nzero = int64_t(C) * ((cm.q - int64_t(B) * cm.img) / 8) + int64_t(c_pad - C) * (cm.q / 8);
+  const int64_t zblocks = std::min<int64_t>(std::max<int64_t>(ceil_div(nzero, 256 * 4), 1), 4096);
+  const int64_t blocks = nmain + zblocks;
+  if (blocks > int64_t(0x7fffffff)) {
+    set_error("conv3x3 wgrad pack: too many planes");
+    return -1;
+  }
+  pack_cm_kernel<<<dim3(unsigned(blocks)), 256, 0, st>>>(src, dst, B, C, H, W, c_pad, cm.wp8, cm.img, cm.q,
+                                                          shift, rows_per, rblocks, planes_per, nmain);
+  return 0;
 }
 
 struct WgradArgs {
@@ -711,12 +807,8 @@ int xdna_conv3x3_wgrad_pack_bf16(const uint16_t* x, const uint16_t* dy, int B, i
   if (!wgrad_bufs("xdna_conv3x3_wgrad_pack_bf16", p, workspace, workspace_bytes, bufs)) return -1;
   if (!admit_launch("conv3x3 wgrad pack")) return -1;
   hipStream_t st = as_stream(stream);
-  const int64_t nx = int64_t(p.ci_pad) * (p.cm.q / 8);
-  pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nx, 256), 16384)), 256, 0, st>>>(
-      x, bufs.xt, B, Cin, H, W, p.ci_pad, p.cm.wp8, p.cm.img, p.cm.q, 1);
-  const int64_t nd = int64_t(p.co_pad) * (p.cm.q / 8);
-  pack_cm_kernel<<<int(std::min<int64_t>(ceil_div(nd, 256), 16384)), 256, 0, st>>>(
-      dy, bufs.dt, B, Cout, H, W, p.co_pad, p.cm.wp8, p.cm.img, p.cm.q, 0);
+  if (pack_cm_launch(x, bufs.xt, B, Cin, H, W, p.ci_pad, p.cm, 1, st) != 0) return -1;
+  if (pack_cm_launch(dy, bufs.dt, B, Cout, H, W, p.co_pad, p.cm, 0, st) != 0) return -1;
   return check_launch("conv3x3 wgrad pack");
 }
 

@@ -81,6 +81,117 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
   }
 }
 
+// LDS-staged variant: a workgroup packs R full image rows of one image and one chunk,
+// for every strip of those rows.  Phase 1: each item is (source pixel, 8-channel piece);
+// consecutive threads take consecutive pixels, so each of the 8 channel loads of a wave
+// reads a contiguous run of NCHW, and the 8 values land in LDS as one 16-byte write
+// ([pixel][64 channels], pitch kLdsPitch).  Phase 2: consecutive threads take consecutive
+// 16-byte pieces of packed rows, so a wave store covers 8 whole rows (1 KB contiguous).
+constexpr int kLdsPitch = 72;      // elements per staged pixel (64 + 8: 16-byte aligned rows)
+constexpr int kMaxTilePix = 256;   // pixels per workgroup (LDS 36 KiB: four workgroups per CU)
+
+template <int VP>
+__global__ __launch_bounds__(256) void pack_rows_lds_kernel(
+    const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int C, int H, int W, int S,
+    int So, int Wg, int wp, int halo_zero, int chunks, int g0, int ng, int b0, int64_t plo,
+    int64_t phi, int R, int ybl) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t tile[];
+  int bid = blockIdx.x;
+  const int yb = bid % ybl;
+  bid /= ybl;
+  const int chunk = bid % chunks;
+  const int b = b0 + bid / chunks;
+  const int cc = min(C - chunk * kKStep, kKStep);
+  if (cc <= 0) return;
+  const int y0 = yb * R;
+  const int rows = min(R, H - y0);
+  const int npix = rows * W;
+  const int64_t plane = int64_t(H) * W;
+  const uint16_t* sbase = src + (int64_t(b) * C + chunk * kKStep) * plane + int64_t(y0) * W;
+  // phase 1: NCHW rows [y0, y0 + rows) -> tile[pix][c], pix = yy * W + x.  An item is
+  // VP consecutive pixels x 16 channels: 16 loads of VP pixels each (one per channel, all
+  // issued before the first LDS write), then VP x two 16-byte LDS writes.
+  const int nseg16 = (cc + 15) >> 4;
+  const int ngrp = (npix + VP - 1) / VP;
+  const int nitem = nseg16 * ngrp;
+  for (int it = threadIdx.x; it < nitem; it += 256) {
+    const int seg = it / ngrp;
+    const int pix0 = (it - seg * ngrp) * VP;
+    const uint16_t* sp = sbase + int64_t(seg * 16) * plane + pix0;
+    uint32_t d[16][(VP + 1) / 2];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const bool ok = seg * 16 + k < cc;
+      if (VP == 4) {
+        uint2 t = make_uint2(0, 0);
+        if (ok) t = *reinterpret_cast<const uint2*>(sp + k * plane);
+        d[k][0] = t.x;
+        d[k][1] = t.y;
+      } else if (VP == 2) {
+        d[k][0] = ok ? *reinterpret_cast<const uint32_t*>(sp + k * plane) : 0u;
+      } else {
+        d[k][0] = ok ? uint32_t(sp[k * plane]) : 0u;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+      if (pix0 + i < npix) {
+        // dword m of pixel i: channel 2m (low half) and channel 2m + 1 (high half)
+        uint32_t o[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const uint32_t a = d[2 * m][i >> 1], b = d[2 * m + 1][i >> 1];
+          // v_perm_b32 selector: bytes 0-3 come from the second operand, 4-7 from the first
+          o[m] = VP == 1 ? (a | (b << 16))
+                         : ((i & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
+                                    : __builtin_amdgcn_perm(b, a, 0x05040100u));
+        }
+        uint4* tp = reinterpret_cast<uint4*>(tile + (pix0 + i) * kLdsPitch + seg * 16);
+        tp[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        tp[1] = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // phase 2: packed rows of every strip (and the halo copies into the previous group)
+  const int nseg = (cc + 7) >> 3;
+  const int spix = rows * Wg;  // packed rows per strip
+  const int nst = S * spix * nseg;
+  for (int t = threadIdx.x; t < nst; t += 256) {
+    const int opix = t / nseg;
+    const int q = t - opix * nseg;
+    const int s = opix / spix;
+    const int rem = opix - s * spix;
+    const int yy = rem / Wg, j = rem - yy * Wg;
+    const int x = (S == 1 ? 0 : s * So - 1) + j;  // source column of data column j
+    if (x < 0 || x >= W) continue;                // no source pixel: left as the caller's zero fill
+    const int64_t p = ((int64_t(b) * S + s) * (H + 2) + y0 + yy + 1) * wp + 1 + j;
+    if (p < plo || p >= phi) continue;
+    const int64_t g = p / kGroupOutRows;
+    const int r = int(p - g * kGroupOutRows);
+    const bool main_w = g >= g0 && g < int64_t(g0) + ng;
+    const bool halo_w = g > g0 && g <= int64_t(g0) + ng && r + kGroupOutRows < kGroupRows;
+    const bool zero = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
+    const uint16_t* tp = tile + (yy * W + x) * kLdsPitch + q * 8;
+    const bool full = (q + 1) * 8 <= cc;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (!zero) v = *reinterpret_cast<const uint4*>(tp);
+    for (int k = 0; k < 2; ++k) {
+      if (k == 0 && !main_w) continue;
+      if (k == 1 && !halo_w) continue;
+      uint16_t* d = k == 0 ? dst + ((int64_t(g - g0) * chunks + chunk) * kGroupRows + r) * kKStep
+                           : dst + ((int64_t(g - 1 - g0) * chunks + chunk) * kGroupRows + r +
+                                    kGroupOutRows) * kKStep;
+      if (full) {
+        *reinterpret_cast<uint4*>(d + q * 8) = v;
+      } else {
+        for (int c = q * 8; c < cc; ++c) d[c] = zero ? uint16_t(0) : tp[c - q * 8];
+      }
+    }
+  }
+}
+
 template <bool kVecLoad>
 __global__ __launch_bounds__(256) void unpack_rows_kernel(
     const uint16_t* __restrict__ c, uint16_t* __restrict__ dst, int H, int W, int S, int So,
@@ -141,6 +252,38 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
   const int64_t v1 = std::min<int64_t>((phi - 1) / img + 1, Bv);
   if (v1 <= v0) return 0;
   if (!admit_launch(what)) return -1;
+  if (aligned16(dst) && W <= kMaxTilePix) {
+    // whole images b0 .. b1-1 cover virtual images v0 .. v1-1; rows outside [plo, phi)
+    // are skipped in the kernel
+    const int64_t b0 = v0 / S, b1 = ceil_div(v1, S);
+    // tile height: as many rows as the LDS tile holds, lowered until the grid has
+    // enough workgroups to fill the chip
+    const int64_t row_tasks = (b1 - b0) * chunks * H;
+    const int R = int(std::max<int64_t>(1, std::min<int64_t>({int64_t(H), kMaxTilePix / W, row_tasks / 2048})));
+    const int ybl = int(ceil_div(H, R));
+    const int64_t blocks = (b1 - b0) * chunks * ybl;
+    const size_t lds = size_t(R) * W * kLdsPitch * 2;
+    // pixels per lane load: every channel run (plane offset + y0 * W) must keep the
+    // alignment of the load for every tile row start; the last group of a run is cut
+    // short by the tile's pixel count only, and runs are padded in LDS to the group size
+    const int64_t plane = int64_t(H) * W;
+    const int64_t step = std::gcd<int64_t>(plane, int64_t(R) * W);  // all run offsets are multiples
+    const uintptr_t sa = reinterpret_cast<uintptr_t>(src);
+    const int VP = (sa % 8 == 0 && step % 4 == 0 && (R * W) % 4 == 0) ? 4
+                   : (sa % 4 == 0 && step % 2 == 0 && (R * W) % 2 == 0) ? 2 : 1;
+    const dim3 grid{unsigned(blocks)};
+    hipStream_t st = as_stream(stream);
+    if (VP == 4)
+      pack_rows_lds_kernel<4><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks,
+                                                      g0, ng, int(b0), plo, phi, R, ybl);
+    else if (VP == 2)
+      pack_rows_lds_kernel<2><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks,
+                                                      g0, ng, int(b0), plo, phi, R, ybl);
+    else
+      pack_rows_lds_kernel<1><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks,
+                                                      g0, ng, int(b0), plo, phi, R, ybl);
+    return check_launch(what);
+  }
   const int64_t n = (v1 - v0) * chunks * H * Wg;
   const int threads = 256;
   const int64_t blocks = ceil_div(n, threads);
