@@ -74,6 +74,18 @@ int xdna_hip_cache_empty(void);
  * fresh_allocations, reuses, frees. */
 int xdna_hip_cache_stats(int64_t* stats, int n);
 
+/* Private pools of the cache, for graph capture (the role of PyTorch's graph memory
+ * pools; no reference counterpart, the reference has no graph capture).  Between
+ * pool_begin(pool) and pool_end() the calling thread's cache_alloc calls are served from
+ * `pool` (new hipMalloc calls run with the thread's capture mode relaxed), and blocks of
+ * the pool return to it when freed, so they are never handed to other work while a graph
+ * that uses them can be replayed.  pool_release(pool) gives the pool's blocks back to
+ * the shared pool (call it after the last replay). */
+int64_t xdna_hip_cache_pool_create(void);
+int xdna_hip_cache_pool_begin(int64_t pool);
+int xdna_hip_cache_pool_end(void);
+int xdna_hip_cache_pool_release(int64_t pool);
+
 int xdna_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
                           void* stream); /* kind: 1 H2D, 2 D2H, 3 D2D, 4 default */
 int xdna_hip_memset_async(void* dst, int value, size_t bytes, void* stream);
@@ -117,6 +129,16 @@ int xdna_conv3x3w_pack_input_strips_range_bf16(const uint16_t* src, uint16_t* ds
                                                int C, int H, int W, int S, int So,
                                                int halo_zero, int chunks, int g0, int ng,
                                                void* stream);
+
+/* The whole packed input of xdna_conv3x3w_geometry (all groups and chunks, the strip
+ * layout for W > 36) with every element written: the bytes at pixel rows and real
+ * channels equal xdna_conv3x3w_pack_input_strips_range_bf16's, every other byte is zero.
+ * No reference counterpart: the reference zero-fills a packed buffer once per shape
+ * (torch_xdna_device.cpp:1848-1872) and packs real pixels only; this form serves callers
+ * that recycle one buffer across shapes or replay captured graphs.  dst must be 16-byte
+ * aligned and W <= 256. */
+int xdna_conv3x3w_pack_input_dense_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H,
+                                        int W, void* stream);
 
 /* Replaces xdna_conv3x3w_unpack_output_bf16 (conv_pack.cpp:447-466):
  * [groups*2048][128] bf16 rows -> channel slice [c_start, c_start+cout_valid)
@@ -249,6 +271,20 @@ int xdna_fused_adam(int n_tensors, void* const* params, void* const* grads,
                     double beta2, double weight_decay, double eps, int amsgrad,
                     int maximize, int mode, const float* grad_scale,
                     const float* found_inf, void* stream);
+
+/* Batch norm in training mode without running statistics over x[N][C][L] bf16 (the form
+ * PyTorch's instance_norm takes: [B, C, H, W] as [1, B*C, H*W]).  Replaces PyTorch's CPU
+ * native_batch_norm / native_batch_norm_backward, which the reference reaches through
+ * its zero-copy fallback (torch_xdna_device.cpp:5124-5260).  weight / bias: param_dtype
+ * 0 (absent: weight 1, bias 0), 1 (bf16), 2 (fp32); save_mean / save_invstd fp32 [C];
+ * invstd = 1 / sqrt(biased var + eps).  Backward: dx, dweight, dbias may each be NULL;
+ * dweight / dbias are of param_dtype (1 or 2). */
+int xdna_batch_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                             uint16_t* y, float* save_mean, float* save_invstd, int64_t N, int64_t C,
+                             int64_t L, double eps, void* stream);
+int xdna_batch_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
+                             const float* save_mean, const float* save_invstd, uint16_t* dx,
+                             void* dweight, void* dbias, int64_t N, int64_t C, int64_t L, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,162 @@
+// Batch-norm statistics, normalisation and backward for bf16 activations, in the form
+// instance_norm reaches them: PyTorch's instance_norm views [B, C, H, W] as
+// [1, B*C, H, W] and calls native_batch_norm (training, no running statistics), so a
+// "channel" here is one (image, channel) plane of H*W elements.  The reference serves
+// these operators from PyTorch's CPU kernels through its zero-copy fallback
+// (torch_xdna_device.cpp:5124-5260); on the GPU they decide the style step's time once
+// the convolutions are fast (a wide, shallow reduction PyTorch-ROCm runs at ~35 us).
+//
+// Layout: x[n][c][l], n < N, c < C, l < L (contiguous).  One 64-lane wave per channel,
+// four channels per workgroup; a channel's N*L elements are read from HBM once and
+// re-read from cache by the later passes.  Statistics in fp32: mean, then the centred
+// sum of squares (two passes), biased variance, invstd = 1 / sqrt(var + eps), as
+// PyTorch's batch_norm_collect_statistics; y = (x - mean) * invstd * w + b rounded
+// once to bf16.
+#include "common.h"
+#include "../../include/xdna_hip.h"
+
+namespace xdna {
+namespace {
+
+constexpr int kNormWaves = 4;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// weight / bias element c of dtype wd (0 none -> default, 1 bf16, 2 fp32)
+__device__ inline float param_at(const void* p, int wd, int64_t c, float dflt) {
+  if (!p || wd == 0) return dflt;
+  return wd == 1 ? bf16_to_f32(static_cast<const uint16_t*>(p)[c]) : static_cast<const float*>(p)[c];
+}
+
+__device__ inline void param_put(void* p, int wd, int64_t c, float v) {
+  if (!p) return;
+  if (wd == 1) static_cast<uint16_t*>(p)[c] = f32_to_bf16(v);
+  else static_cast<float*>(p)[c] = v;
+}
+
+__global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const void* __restrict__ b, int wd,
+    uint16_t* __restrict__ y, float* __restrict__ save_mean, float* __restrict__ save_invstd,
+    int64_t N, int64_t C, int64_t L, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+  if (c >= C) return;
+  const int64_t cnt = N * L;
+  float s = 0.f;
+  for (int64_t n = 0; n < N; ++n) {
+    const uint16_t* xp = x + (n * C + c) * L;
+    for (int64_t l = lane; l < L; l += 64) s += bf16_to_f32(xp[l]);
+  }
+  const float mean = wave_sum(s) / float(cnt);
+  float q = 0.f;
+  for (int64_t n = 0; n < N; ++n) {
+    const uint16_t* xp = x + (n * C + c) * L;
+    for (int64_t l = lane; l < L; l += 64) {
+      const float d = bf16_to_f32(xp[l]) - mean;
+      q += d * d;
+    }
+  }
+  const float var = wave_sum(q) / float(cnt);
+  const float invstd = 1.0f / sqrtf(var + eps);
+  if (lane == 0) {
+    save_mean[c] = mean;
+    save_invstd[c] = invstd;
+  }
+  const float scale = param_at(w, wd, c, 1.f) * invstd;
+  const float shift = param_at(b, wd, c, 0.f) - mean * scale;
+  for (int64_t n = 0; n < N; ++n) {
+    const uint16_t* xp = x + (n * C + c) * L;
+    uint16_t* yp = y + (n * C + c) * L;
+    for (int64_t l = lane; l < L; l += 64) yp[l] = f32_to_bf16(fmaf(bf16_to_f32(xp[l]), scale, shift));
+  }
+}
+
+// dx = (dy - mean(dy) - (x - mean) * invstd^2 * mean(dy * (x - mean))) * invstd * w
+// dw = invstd * sum(dy * (x - mean)),  db = sum(dy)   (PyTorch's batch_norm_backward)
+__global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
+    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const void* __restrict__ w, int wd,
+    const float* __restrict__ mean_in, const float* __restrict__ invstd_in, uint16_t* __restrict__ dx,
+    void* __restrict__ dw, void* __restrict__ db, int64_t N, int64_t C, int64_t L) {
+  const int lane = threadIdx.x & 63;
+  const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+  if (c >= C) return;
+  const float mean = mean_in[c], invstd = invstd_in[c];
+  float sdy = 0.f, sdot = 0.f;
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t o = (n * C + c) * L;
+    for (int64_t l = lane; l < L; l += 64) {
+      const float g = bf16_to_f32(dy[o + l]);
+      sdy += g;
+      sdot += g * (bf16_to_f32(x[o + l]) - mean);
+    }
+  }
+  sdy = wave_sum(sdy);
+  sdot = wave_sum(sdot);
+  if (lane == 0) {
+    param_put(dw, wd, c, sdot * invstd);
+    param_put(db, wd, c, sdy);
+  }
+  if (!dx) return;
+  const float inv_cnt = 1.0f / float(N * L);
+  const float gmean = sdy * inv_cnt;
+  const float proj = sdot * inv_cnt * invstd * invstd;
+  const float gscale = invstd * param_at(w, wd, c, 1.f);
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t o = (n * C + c) * L;
+    for (int64_t l = lane; l < L; l += 64) {
+      const float xm = bf16_to_f32(x[o + l]) - mean;
+      dx[o + l] = f32_to_bf16((bf16_to_f32(dy[o + l]) - gmean - xm * proj) * gscale);
+    }
+  }
+}
+
+bool norm_shape_ok(const char* what, int64_t N, int64_t C, int64_t L, int wd) {
+  if (N < 0 || C < 0 || L < 0 || wd < 0 || wd > 2) {
+    set_error(std::string(what) + ": invalid arguments");
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" {
+
+int xdna_batch_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                             uint16_t* y, float* save_mean, float* save_invstd, int64_t N, int64_t C,
+                             int64_t L, double eps, void* stream) {
+  if (!norm_shape_ok("xdna_batch_norm_fwd_bf16", N, C, L, param_dtype)) return -1;
+  if (C == 0) return 0;
+  if (N * L == 0) {
+    set_error("xdna_batch_norm_fwd_bf16: empty reduction");
+    return -1;
+  }
+  if (!admit_launch("batch_norm fwd")) return -1;
+  bn_fwd_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
+      x, weight, bias, param_dtype, y, save_mean, save_invstd, N, C, L, float(eps));
+  return check_launch("batch_norm fwd");
+}
+
+int xdna_batch_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
+                             const float* save_mean, const float* save_invstd, uint16_t* dx,
+                             void* dweight, void* dbias, int64_t N, int64_t C, int64_t L, void* stream) {
+  if (!norm_shape_ok("xdna_batch_norm_bwd_bf16", N, C, L, param_dtype)) return -1;
+  if (C == 0) return 0;
+  if ((dweight || dbias) && param_dtype == 0) {
+    set_error("xdna_batch_norm_bwd_bf16: parameter gradients need param_dtype 1 or 2");
+    return -1;
+  }
+  if (!admit_launch("batch_norm bwd")) return -1;
+  bn_bwd_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
+      dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, N, C, L);
+  return check_launch("batch_norm bwd");
+}
+
+}  // extern "C"

@@ -90,13 +90,45 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
 constexpr int kLdsPitch = 72;      // elements per staged pixel (64 + 8: 16-byte aligned rows)
 constexpr int kMaxTilePix = 256;   // pixels per workgroup (LDS 36 KiB: four workgroups per CU)
 
-template <int VP>
+// Writes the 16-byte piece q of packed row p (main copy and, for the first 78 rows of a
+// group, the halo copy at the end of the previous group), when p is in [plo, phi).
+__device__ inline void put_row_piece(uint16_t* __restrict__ dst, int64_t p, int q, uint4 v,
+                                     int chunks, int chunk, int g0, int ng, int64_t plo,
+                                     int64_t phi) {
+  if (p < plo || p >= phi) return;
+  const int64_t g = p / kGroupOutRows;
+  const int r = int(p - g * kGroupOutRows);
+  if (g >= g0 && g < int64_t(g0) + ng)
+    *reinterpret_cast<uint4*>(dst + ((int64_t(g - g0) * chunks + chunk) * kGroupRows + r) * kKStep + q * 8) = v;
+  if (g > g0 && g <= int64_t(g0) + ng && r + kGroupOutRows < kGroupRows)
+    *reinterpret_cast<uint4*>(dst + ((int64_t(g - 1 - g0) * chunks + chunk) * kGroupRows + r + kGroupOutRows) *
+                                        kKStep + q * 8) = v;
+}
+
+// kDense = false: only rows of real pixels and only the real channels are written (the
+// reference's contract: the caller zero-fills once per shape).  kDense = true: every
+// element of groups [g0, g0 + ng) is written, zeros included (border rows and columns,
+// padded channels, the rows past the last image), so a buffer needs no fill; workgroups
+// from nimg on write the rows past the last image.
+template <int VP, bool kDense>
 __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int C, int H, int W, int S,
     int So, int Wg, int wp, int halo_zero, int chunks, int g0, int ng, int b0, int64_t plo,
-    int64_t phi, int R, int ybl) {
+    int64_t phi, int R, int ybl, int nimg, int64_t tail0) {
   extern __shared__ __attribute__((aligned(16))) uint16_t tile[];
   int bid = blockIdx.x;
+  if (kDense && bid >= nimg) {
+    // rows [tail0, phi) hold no image: zeros for every chunk
+    const int64_t n = (phi - tail0) * chunks * 8;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    for (int64_t i = int64_t(bid - nimg) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x - nimg) * 256) {
+      const int q = int(i & 7);
+      const int64_t rc = i >> 3;
+      const int chunk = int(rc % chunks);
+      put_row_piece(dst, tail0 + rc / chunks, q, z, chunks, chunk, g0, ng, plo, phi);
+    }
+    return;
+  }
   const int yb = bid % ybl;
   bid /= ybl;
   const int chunk = bid % chunks;
@@ -155,6 +187,31 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
   __syncthreads();
 
   // phase 2: packed rows of every strip (and the halo copies into the previous group)
+  if (kDense) {
+    // grid rows y0+1 .. y0+rows (plus the top / bottom border row for the first / last
+    // tile), all wp columns, all 64 channels
+    const int gy_lo = y0 == 0 ? 0 : y0 + 1;
+    const int gy_hi = y0 + rows == H ? H + 2 : y0 + rows + 1;
+    const int grows = gy_hi - gy_lo;
+    const int nst = S * grows * wp * 8;
+    for (int t = threadIdx.x; t < nst; t += 256) {
+      const int q = t & 7;
+      const int opix = t >> 3;
+      const int s = opix / (grows * wp);
+      const int rem = opix - s * (grows * wp);
+      const int gr = rem / wp, gx = rem - gr * wp;
+      const int gy = gy_lo + gr;
+      const int j = gx - 1;
+      const int x = (S == 1 ? 0 : s * So - 1) + j;
+      const bool zero_col = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (gy >= 1 && gy <= H && j >= 0 && j < Wg && x >= 0 && x < W && !zero_col && q * 8 < cc)
+        v = *reinterpret_cast<const uint4*>(tile + ((gy - 1 - y0) * W + x) * kLdsPitch + q * 8);
+      const int64_t p = ((int64_t(b) * S + s) * (H + 2) + gy) * wp + gx;
+      put_row_piece(dst, p, q, v, chunks, chunk, g0, ng, plo, phi);
+    }
+    return;
+  }
   const int nseg = (cc + 7) >> 3;
   const int spix = rows * Wg;  // packed rows per strip
   const int nst = S * spix * nseg;
@@ -235,7 +292,8 @@ __global__ __launch_bounds__(256) void unpack_rows_kernel(
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
-                int S, int So, int halo_zero, int chunks, int g0, int ng, void* stream) {
+                int S, int So, int halo_zero, int chunks, int g0, int ng, void* stream,
+                bool dense = false) {
   if (B < 0 || C < 0 || H < 0 || W < 0 || chunks < 0 || S < 1 || g0 < 0 || ng < 0 ||
       (S > 1 && So < 1)) {
     set_error(std::string(what) + ": invalid geometry");
@@ -250,18 +308,27 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
   const int64_t phi = int64_t(g0 + ng) * kGroupOutRows + (kGroupRows - kGroupOutRows);
   const int64_t v0 = plo / img;
   const int64_t v1 = std::min<int64_t>((phi - 1) / img + 1, Bv);
-  if (v1 <= v0) return 0;
+  if (dense && (!aligned16(dst) || W > kMaxTilePix)) {
+    set_error(std::string(what) + ": dense packing needs a 16-byte aligned destination and W <= 256");
+    return -1;
+  }
+  if (v1 <= v0 && !dense) return 0;
   if (!admit_launch(what)) return -1;
   if (aligned16(dst) && W <= kMaxTilePix) {
     // whole images b0 .. b1-1 cover virtual images v0 .. v1-1; rows outside [plo, phi)
     // are skipped in the kernel
-    const int64_t b0 = v0 / S, b1 = ceil_div(v1, S);
+    const int64_t b0 = v1 > v0 ? v0 / S : 0, b1 = v1 > v0 ? ceil_div(v1, S) : 0;
     // tile height: as many rows as the LDS tile holds, lowered until the grid has
     // enough workgroups to fill the chip
     const int64_t row_tasks = (b1 - b0) * chunks * H;
     const int R = int(std::max<int64_t>(1, std::min<int64_t>({int64_t(H), kMaxTilePix / W, row_tasks / 2048})));
     const int ybl = int(ceil_div(H, R));
-    const int64_t blocks = (b1 - b0) * chunks * ybl;
+    const int64_t nimg = (b1 - b0) * chunks * ybl;
+    // dense: rows [tail0, phi) past the last image get workgroups of their own
+    const int64_t tail0 = std::max(plo, Bv * img);
+    const int64_t ntail = dense && phi > tail0 ? std::min<int64_t>(ceil_div((phi - tail0) * chunks * 8, 256), 1024) : 0;
+    const int64_t blocks = nimg + ntail;
+    if (blocks == 0) return 0;
     const size_t lds = size_t(R) * W * kLdsPitch * 2;
     // pixels per lane load: every channel run (plane offset + y0 * W) must keep the
     // alignment of the load for every tile row start; the last group of a run is cut
@@ -273,15 +340,20 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
                    : (sa % 4 == 0 && step % 2 == 0 && (R * W) % 2 == 0) ? 2 : 1;
     const dim3 grid{unsigned(blocks)};
     hipStream_t st = as_stream(stream);
-    if (VP == 4)
-      pack_rows_lds_kernel<4><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks,
-                                                      g0, ng, int(b0), plo, phi, R, ybl);
-    else if (VP == 2)
-      pack_rows_lds_kernel<2><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks,
-                                                      g0, ng, int(b0), plo, phi, R, ybl);
-    else
-      pack_rows_lds_kernel<1><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks,
-                                                      g0, ng, int(b0), plo, phi, R, ybl);
+#define XDNA_PACK_LAUNCH(vp, dn)                                                                  \
+  pack_rows_lds_kernel<vp, dn><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, \
+                                                      chunks, g0, ng, int(b0), plo, phi, R, ybl,   \
+                                                      int(nimg), tail0)
+    if (dense) {
+      if (VP == 4) XDNA_PACK_LAUNCH(4, true);
+      else if (VP == 2) XDNA_PACK_LAUNCH(2, true);
+      else XDNA_PACK_LAUNCH(1, true);
+    } else {
+      if (VP == 4) XDNA_PACK_LAUNCH(4, false);
+      else if (VP == 2) XDNA_PACK_LAUNCH(2, false);
+      else XDNA_PACK_LAUNCH(1, false);
+    }
+#undef XDNA_PACK_LAUNCH
     return check_launch(what);
   }
   const int64_t n = (v1 - v0) * chunks * H * Wg;
@@ -352,6 +424,17 @@ int xdna_conv3x3w_pack_input_strips_range_bf16(const uint16_t* src, uint16_t* ds
                                                int chunks, int g0, int ng, void* stream) {
   return pack_launch("xdna_conv3x3w_pack_input_strips_range_bf16", src, dst, B, C, H, W, S, So,
                      halo_zero, chunks, g0, ng, stream);
+}
+
+int xdna_conv3x3w_pack_input_dense_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H,
+                                         int W, void* stream) {
+  if (B < 1 || C < 1 || H < 1 || W < 1) {
+    set_error("xdna_conv3x3w_pack_input_dense_bf16: invalid shape");
+    return -1;
+  }
+  const ConvGeom cg = conv_geom(B, H, W);
+  return pack_launch("xdna_conv3x3w_pack_input_dense_bf16", src, dst, B, C, H, W, cg.st.S, cg.st.So, 0,
+                     int(ceil_div(C, kKStep)), 0, cg.groups, stream, /*dense=*/true);
 }
 
 int xdna_conv3x3w_unpack_output_bf16(const uint16_t* c, uint16_t* dst, int B, int H, int W,

@@ -65,10 +65,21 @@ int check_launch(const char* what) {
 
 namespace {
 
+// Blocks belong to the shared pool (id 0) or to a private pool.  A private pool serves the
+// allocations a thread makes between pool_begin and pool_end (a graph capture), and keeps
+// every block it ever handed out: freed blocks return to it, never to the shared pool, so
+// memory a captured graph reads or writes is not given to other work while the graph may
+// be replayed.  pool_release hands the pool's blocks back to the shared pool.
 struct Cache {
   std::mutex mu;
-  std::multimap<size_t, void*> free_blocks;       // rounded size -> block
-  std::unordered_map<void*, size_t> live;         // block -> rounded size
+  std::multimap<size_t, void*> free_blocks;  // shared pool: rounded size -> block
+  struct Live {
+    size_t size;
+    int64_t pool;
+  };
+  std::unordered_map<void*, Live> live;                                  // block -> size, pool
+  std::unordered_map<int64_t, std::multimap<size_t, void*>> pool_free;   // private pools
+  int64_t next_pool = 1;
   int64_t cached = 0, allocated = 0, max_allocated = 0;
   int64_t fresh = 0, reuses = 0, frees = 0;
 };
@@ -76,6 +87,18 @@ struct Cache {
 Cache& cache() {
   static auto* c = new Cache();  // never destroyed: frees can run at exit
   return *c;
+}
+
+thread_local int64_t t_pool = 0;  // private pool of this thread's allocations (0: shared)
+
+// hipMalloc with the thread's stream-capture mode relaxed, so that it is legal while this
+// thread captures a graph (the allocation itself is not a stream operation).
+hipError_t malloc_relaxed(void** p, size_t n) {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  const hipError_t e = hipMalloc(p, n);
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  return e;
 }
 
 size_t round_size(size_t n) {
@@ -175,14 +198,20 @@ int xdna_hip_free(void* ptr) {
 void* xdna_hip_cache_alloc(size_t bytes) {
   Cache& c = cache();
   const size_t n = round_size(bytes);
+  const int64_t pool = t_pool;
   {
     std::lock_guard<std::mutex> lock(c.mu);
-    auto it = c.free_blocks.find(n);
-    if (it != c.free_blocks.end()) {
+    std::multimap<size_t, void*>* fl = &c.free_blocks;
+    if (pool != 0) {
+      auto pit = c.pool_free.find(pool);
+      fl = pit == c.pool_free.end() ? nullptr : &pit->second;
+    }
+    auto it = fl ? fl->find(n) : std::multimap<size_t, void*>::iterator();
+    if (fl && it != fl->end()) {
       void* p = it->second;
-      c.free_blocks.erase(it);
+      fl->erase(it);
       c.cached -= int64_t(n);
-      c.live.emplace(p, n);
+      c.live.emplace(p, Cache::Live{n, pool});
       c.allocated += int64_t(n);
       if (c.allocated > c.max_allocated) c.max_allocated = c.allocated;
       ++c.reuses;
@@ -190,19 +219,20 @@ void* xdna_hip_cache_alloc(size_t bytes) {
     }
   }
   void* p = nullptr;
-  hipError_t e = hipMalloc(&p, n);
-  if (e != hipSuccess) {
+  hipError_t e = malloc_relaxed(&p, n);
+  if (e != hipSuccess && pool == 0) {
     (void)hipGetLastError();
-    // Out of memory: give the cached blocks back and retry once.
+    // Out of memory: give the cached blocks back and retry once (not while capturing:
+    // emptying synchronizes the device).
     xdna_hip_cache_empty();
-    e = hipMalloc(&p, n);
-    if (e != hipSuccess) {
-      launch_failed("xdna_hip_cache_alloc", e);
-      return nullptr;
-    }
+    e = malloc_relaxed(&p, n);
+  }
+  if (e != hipSuccess) {
+    launch_failed("xdna_hip_cache_alloc", e);
+    return nullptr;
   }
   std::lock_guard<std::mutex> lock(c.mu);
-  c.live.emplace(p, n);
+  c.live.emplace(p, Cache::Live{n, pool});
   c.allocated += int64_t(n);
   if (c.allocated > c.max_allocated) c.max_allocated = c.allocated;
   ++c.fresh;
@@ -218,13 +248,17 @@ int xdna_hip_cache_free(void* ptr) {
     set_error("xdna_hip_cache_free: pointer was not allocated by the cache");
     return -1;
   }
-  const size_t n = it->second;
+  const Cache::Live b = it->second;
   c.live.erase(it);
-  c.allocated -= int64_t(n);
+  c.allocated -= int64_t(b.size);
   ++c.frees;
   if (g_poisoned.load()) return 0;  // a stuck launch may still use it: never recycle
-  c.free_blocks.emplace(n, ptr);
-  c.cached += int64_t(n);
+  auto pit = b.pool != 0 ? c.pool_free.find(b.pool) : c.pool_free.end();
+  if (pit != c.pool_free.end())
+    pit->second.emplace(b.size, ptr);
+  else
+    c.free_blocks.emplace(b.size, ptr);
+  c.cached += int64_t(b.size);
   return 0;
 }
 
@@ -234,7 +268,7 @@ int xdna_hip_cache_empty(void) {
   {
     std::lock_guard<std::mutex> lock(c.mu);
     blocks.swap(c.free_blocks);
-    c.cached = 0;
+    for (const auto& kv : blocks) c.cached -= int64_t(kv.first);
   }
   if (blocks.empty()) return 0;
   // Blocks may still be read by queued work on any stream.
@@ -244,6 +278,45 @@ int xdna_hip_cache_empty(void) {
     e = hipFree(kv.second);
     if (e != hipSuccess) return launch_failed("hipFree", e);
   }
+  return 0;
+}
+
+int64_t xdna_hip_cache_pool_create(void) {
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  const int64_t id = c.next_pool++;
+  c.pool_free.emplace(id, std::multimap<size_t, void*>());
+  return id;
+}
+
+int xdna_hip_cache_pool_begin(int64_t pool) {
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  if (c.pool_free.find(pool) == c.pool_free.end()) {
+    set_error("xdna_hip_cache_pool_begin: no such pool");
+    return -1;
+  }
+  t_pool = pool;
+  return 0;
+}
+
+int xdna_hip_cache_pool_end(void) {
+  t_pool = 0;
+  return 0;
+}
+
+int xdna_hip_cache_pool_release(int64_t pool) {
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  auto pit = c.pool_free.find(pool);
+  if (pit == c.pool_free.end()) {
+    set_error("xdna_hip_cache_pool_release: no such pool");
+    return -1;
+  }
+  for (const auto& kv : pit->second) c.free_blocks.emplace(kv.first, kv.second);
+  c.pool_free.erase(pit);
+  for (auto& kv : c.live)
+    if (kv.second.pool == pool) kv.second.pool = 0;  // freed later into the shared pool
   return 0;
 }
 

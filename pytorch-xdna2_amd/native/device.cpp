@@ -563,6 +563,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     check_abi(xdna_hip_device_synchronize(), "synchronize");
     check_abi(xdna_hip_cache_empty(), "empty_cache");
   });
+  mod.def("pool_create", [] { return xdna_hip_cache_pool_create(); });
+  mod.def("pool_begin", [](int64_t pool) { check_abi(xdna_hip_cache_pool_begin(pool), "pool_begin"); });
+  mod.def("pool_end", [] { check_abi(xdna_hip_cache_pool_end(), "pool_end"); });
+  mod.def("pool_release", [](int64_t pool) { check_abi(xdna_hip_cache_pool_release(pool), "pool_release"); });
   mod.def("allocator_stats", [] {
     int64_t s[6] = {0, 0, 0, 0, 0, 0};
     xdna_hip_cache_stats(s, 6);

@@ -10,7 +10,6 @@
 #include <c10/core/impl/LocalDispatchKeySet.h>
 
 #include <array>
-#include <map>
 #include <mutex>
 #include <optional>
 #include <vector>
@@ -34,66 +33,6 @@ struct BelowAutograd {
 
 at::Tensor alloc_bytes(size_t n) {
   return empty_xdna({int64_t(std::max<size_t>(n, 1))}, at::kByte);
-}
-
-// ---------------------------------------------------------------------------------------
-// Packed-input pool (the reference's acquire_packed, torch_xdna_device.cpp:1819-1914).
-// Packing writes only real pixels/channels, so a buffer is zero-filled when created and
-// whenever the packed shape changes; all use is ordered on one stream, so a released
-// buffer can serve the next call at once.
-// ---------------------------------------------------------------------------------------
-struct PackedBuf {
-  at::Tensor mem;
-  std::array<int64_t, 4> shape{};
-};
-
-struct PackedPool {
-  std::mutex mu;
-  std::multimap<size_t, PackedBuf> free;
-  size_t bytes = 0;
-  static constexpr size_t kMaxBytes = size_t(8) << 30;
-};
-
-PackedPool& packed_pool() {
-  static auto* p = new PackedPool();
-  return *p;
-}
-
-PackedBuf acquire_packed(size_t bytes, const std::array<int64_t, 4>& shape) {
-  PackedPool& pool = packed_pool();
-  PackedBuf b;
-  {
-    std::lock_guard<std::mutex> lock(pool.mu);
-    auto range = pool.free.equal_range(bytes);
-    auto pick = range.second;
-    for (auto it = range.first; it != range.second; ++it) {
-      if (it->second.shape == shape) { pick = it; break; }
-      if (pick == range.second) pick = it;
-    }
-    if (pick != range.second) {
-      b = std::move(pick->second);
-      pool.free.erase(pick);
-      pool.bytes -= bytes;
-    }
-  }
-  if (!b.mem.defined()) b.mem = alloc_bytes(bytes);
-  if (b.shape != shape) {
-    cuda_alias(b.mem).zero_();  // a fill kernel (no memset node in captured graphs)
-    b.shape = shape;
-  }
-  return b;
-}
-
-void release_packed(PackedBuf&& b) {
-  PackedPool& pool = packed_pool();
-  const size_t bytes = size_t(b.mem.nbytes());
-  std::lock_guard<std::mutex> lock(pool.mu);
-  if (pool.bytes + bytes > PackedPool::kMaxBytes) {
-    pool.free.clear();
-    pool.bytes = 0;
-  }
-  pool.free.emplace(bytes, std::move(b));
-  pool.bytes += bytes;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -127,17 +66,29 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
   at::Tensor x = src.contiguous();
   at::Tensor wc = w.contiguous();
   void* st = current_stream();
+  // The packed input is transient: the dense pack writes every element (zeros in the
+  // borders and padded channels), so a recycled allocation needs no fill.  (The reference
+  // keeps a pool of zero-filled buffers per shape, torch_xdna_device.cpp:1848-1872.)
   const size_t pbytes = xdna_conv3x3w_packed_bytes(int(B), int(cin), int(H), int(W));
-  PackedBuf packed = acquire_packed(pbytes, {B, cin, H, W});
+  at::Tensor packed = alloc_bytes(pbytes);
   int64_t geo[7];
   check_abi(xdna_conv3x3w_geometry(int(B), int(cin), int(H), int(W), geo), "conv geometry");
   {
     const double bytes = 2.0 * double(x.numel()) + double(geo[4]) * double(geo[5]) * 2126.0 * 64.0 * 2.0;
     KernelTimer kt("conv3x3w_pack", bytes);
-    check_abi(xdna_conv3x3w_pack_input_strips_range_bf16(
-                  static_cast<const uint16_t*>(x.const_data_ptr()), static_cast<uint16_t*>(packed.mem.data_ptr()),
-                  int(B), int(cin), int(H), int(W), int(geo[0]), int(geo[1]), 0, int(geo[5]), 0, int(geo[4]), st),
-              "conv pack");
+    if (W <= 256) {
+      check_abi(xdna_conv3x3w_pack_input_dense_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                                    static_cast<uint16_t*>(packed.data_ptr()), int(B), int(cin),
+                                                    int(H), int(W), st),
+                "conv pack");
+    } else {
+      // wider than one LDS tile row: fill, then pack the real pixels
+      cuda_alias(packed).zero_();
+      check_abi(xdna_conv3x3w_pack_input_strips_range_bf16(
+                    static_cast<const uint16_t*>(x.const_data_ptr()), static_cast<uint16_t*>(packed.data_ptr()),
+                    int(B), int(cin), int(H), int(W), int(geo[0]), int(geo[1]), 0, int(geo[5]), 0, int(geo[4]), st),
+                "conv pack");
+    }
   }
   at::Tensor wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
   check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
@@ -149,13 +100,12 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
   if (bias) bc = bias->contiguous();
   const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
   KernelTimer kt(dgrad ? "conv3x3_rows.dgrad" : "conv3x3_rows.fwd", flops);
-  check_abi(xdna_conv3x3_rows_bf16(static_cast<const uint16_t*>(packed.mem.const_data_ptr()),
+  check_abi(xdna_conv3x3_rows_bf16(static_cast<const uint16_t*>(packed.const_data_ptr()),
                                    static_cast<const uint16_t*>(wt.const_data_ptr()),
                                    bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
                                    static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout),
                                    int(H), int(W), st),
             "conv rows");
-  release_packed(std::move(packed));
   return out;
 }
 
@@ -554,6 +504,105 @@ std::vector<std::tuple<std::string, int64_t, double, double>> kernel_timing_repo
 
 int64_t dw_jobs() { return g_dw_jobs.load(); }
 
+// ---------------------------------------------------------------------------------------
+// Batch norm in training mode without running statistics: the form instance_norm takes
+// ([B, C, H, W] viewed as [1, B*C, H, W]).  The reference runs it on the CPU through the
+// zero-copy fallback (torch_xdna_device.cpp:5124-5260); here one HIP kernel per direction.
+// Other forms (running statistics, eval mode, very long channels) use PyTorch-ROCm.
+// ---------------------------------------------------------------------------------------
+constexpr int64_t kNormMaxPerChannel = 65536;  // one wave per channel up to this many elements
+
+int norm_param_dtype(const std::optional<at::Tensor>& w, const std::optional<at::Tensor>& b) {
+  const bool hw = w && w->defined(), hb = b && b->defined();
+  if (!hw && !hb) return 0;
+  const at::ScalarType t = hw ? w->scalar_type() : b->scalar_type();
+  if (hw && hb && w->scalar_type() != b->scalar_type()) return -1;
+  return t == at::kBFloat16 ? 1 : t == at::kFloat ? 2 : -1;
+}
+
+bool norm_param_ok(const std::optional<at::Tensor>& t, int64_t C) {
+  return !t || !t->defined() ||
+         (t->dim() == 1 && t->size(0) == C && t->is_contiguous() && t->device().type() == kXdna);
+}
+
+bool norm_eligible(const at::Tensor& input, const std::optional<at::Tensor>& weight,
+                   const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& rm,
+                   const std::optional<at::Tensor>& rv, bool training) {
+  if (g_mode.load() < 1 || !training) return false;
+  if ((rm && rm->defined()) || (rv && rv->defined())) return false;
+  if (input.scalar_type() != at::kBFloat16 || input.dim() < 2 || input.device().type() != kXdna) return false;
+  const int64_t C = input.size(1);
+  if (C < 1 || input.numel() == 0 || input.numel() / C > kNormMaxPerChannel) return false;
+  return norm_param_dtype(weight, bias) >= 0 && norm_param_ok(weight, C) && norm_param_ok(bias, C);
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> native_batch_norm_xdna(
+    const at::Tensor& input, const std::optional<at::Tensor>& weight, const std::optional<at::Tensor>& bias,
+    const std::optional<at::Tensor>& running_mean, const std::optional<at::Tensor>& running_var, bool training,
+    double momentum, double eps) {
+  if (norm_eligible(input, weight, bias, running_mean, running_var, training)) {
+    ScopedCount sc("hip_batch_norm.fwd.run");
+    const at::Tensor x = input.contiguous();
+    const int64_t N = x.size(0), C = x.size(1), L = x.numel() / (N * C);
+    const int wd = norm_param_dtype(weight, bias);
+    at::Tensor y = empty_xdna(x.sizes(), at::kBFloat16);
+    at::Tensor mean = empty_xdna({C}, at::kFloat), invstd = empty_xdna({C}, at::kFloat);
+    check_abi(xdna_batch_norm_fwd_bf16(
+                  static_cast<const uint16_t*>(x.const_data_ptr()),
+                  weight && weight->defined() ? weight->const_data_ptr() : nullptr,
+                  bias && bias->defined() ? bias->const_data_ptr() : nullptr, wd,
+                  static_cast<uint16_t*>(y.data_ptr()), mean.data_ptr<float>(), invstd.data_ptr<float>(), N, C, L,
+                  eps, current_stream()),
+              "batch_norm fwd");
+    return {y, mean, invstd};
+  }
+  ScopedCount sc("aten::native_batch_norm.rocm");
+  BelowAutograd g;
+  auto r = at::_ops::native_batch_norm::call(rocm(input), rocm(weight), rocm(bias), rocm(running_mean),
+                                             rocm(running_var), training, momentum, eps);
+  return {back(std::get<0>(r)), back(std::get<1>(r)), back(std::get<2>(r))};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> native_batch_norm_backward_xdna(
+    const at::Tensor& grad_out, const at::Tensor& input, const std::optional<at::Tensor>& weight,
+    const std::optional<at::Tensor>& running_mean, const std::optional<at::Tensor>& running_var,
+    const std::optional<at::Tensor>& save_mean, const std::optional<at::Tensor>& save_invstd, bool train,
+    double eps, std::array<bool, 3> mask) {
+  const bool stats_ok = save_mean && save_mean->defined() && save_invstd && save_invstd->defined() &&
+                        save_mean->scalar_type() == at::kFloat && save_invstd->scalar_type() == at::kFloat &&
+                        save_mean->is_contiguous() && save_invstd->is_contiguous() &&
+                        save_mean->device().type() == kXdna && save_invstd->device().type() == kXdna;
+  const bool param_grads_ok = !(mask[1] || mask[2]) || (weight && weight->defined());
+  if (stats_ok && param_grads_ok && norm_eligible(input, weight, std::nullopt, running_mean, running_var, train) &&
+      grad_out.scalar_type() == at::kBFloat16 && grad_out.sizes() == input.sizes() &&
+      grad_out.device().type() == kXdna && save_mean->numel() == input.size(1) &&
+      save_invstd->numel() == input.size(1)) {
+    ScopedCount sc("hip_batch_norm.bwd.run");
+    const at::Tensor x = input.contiguous(), dy = grad_out.contiguous();
+    const int64_t N = x.size(0), C = x.size(1), L = x.numel() / (N * C);
+    const int wd = norm_param_dtype(weight, std::nullopt);
+    at::Tensor dx, dw, db;
+    if (mask[0]) dx = empty_xdna(x.sizes(), at::kBFloat16);
+    const at::ScalarType pt = wd == 2 ? at::kFloat : at::kBFloat16;
+    if (mask[1]) dw = empty_xdna({C}, pt);
+    if (mask[2]) db = empty_xdna({C}, pt);
+    check_abi(xdna_batch_norm_bwd_bf16(
+                  static_cast<const uint16_t*>(dy.const_data_ptr()), static_cast<const uint16_t*>(x.const_data_ptr()),
+                  weight && weight->defined() ? weight->const_data_ptr() : nullptr, wd,
+                  save_mean->const_data_ptr<float>(), save_invstd->const_data_ptr<float>(),
+                  mask[0] ? static_cast<uint16_t*>(dx.data_ptr()) : nullptr, mask[1] ? dw.data_ptr() : nullptr,
+                  mask[2] ? db.data_ptr() : nullptr, N, C, L, current_stream()),
+              "batch_norm bwd");
+    return {dx, dw, db};
+  }
+  ScopedCount sc("aten::native_batch_norm_backward.rocm");
+  BelowAutograd g;
+  auto r = at::_ops::native_batch_norm_backward::call(rocm(grad_out), rocm(input), rocm(weight),
+                                                      rocm(running_mean), rocm(running_var), rocm(save_mean),
+                                                      rocm(save_invstd), train, eps, mask);
+  return {back(std::get<0>(r)), back(std::get<1>(r)), back(std::get<2>(r))};
+}
+
 void register_hot_ops(torch::Library& m) {
   m.impl("convolution_overrideable", TORCH_FN(convolution_overrideable_xdna));
   m.impl("convolution_backward_overrideable", TORCH_FN(convolution_backward_overrideable_xdna));
@@ -567,6 +616,8 @@ void register_hot_ops(torch::Library& m) {
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_xdna));
   m.impl("_fused_adam_.tensor_lr", TORCH_FN(fused_adam_tlr_xdna));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tlr_xdna));
+  m.impl("native_batch_norm", TORCH_FN(native_batch_norm_xdna));
+  m.impl("native_batch_norm_backward", TORCH_FN(native_batch_norm_backward_xdna));
 }
 
 }  // namespace xdna_backend

@@ -25,6 +25,8 @@ from .device import (
     wait_for_builds,
 )
 
+from .graphs import Graph, graph
+
 __version__ = "0.1.0"
 
 try_register_xdna_device()
@@ -50,4 +52,6 @@ __all__ = [
     "is_xrt_backed",
     "bo_handle",
     "coherency_state",
+    "Graph",
+    "graph",
 ]

@@ -39,6 +39,10 @@ SIGNATURES = {
     "xdna_hip_cache_free": (I, [P]),
     "xdna_hip_cache_empty": (I, []),
     "xdna_hip_cache_stats": (I, [PL, I]),
+    "xdna_hip_cache_pool_create": (L, []),
+    "xdna_hip_cache_pool_begin": (I, [L]),
+    "xdna_hip_cache_pool_end": (I, []),
+    "xdna_hip_cache_pool_release": (I, [L]),
     "xdna_hip_memcpy_async": (I, [P, P, Z, I, P]),
     "xdna_hip_memset_async": (I, [P, I, Z, P]),
     "xdna_hip_stream_synchronize": (I, [P]),
@@ -53,6 +57,7 @@ SIGNATURES = {
     "xdna_conv3x3w_pack_input_bf16": (I, [P, P, I, I, I, I, I, P]),
     "xdna_conv3x3w_pack_input_range_bf16": (I, [P, P, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_pack_input_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
+    "xdna_conv3x3w_pack_input_dense_bf16": (I, [P, P, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_bf16": (I, [P, P, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
@@ -71,6 +76,8 @@ SIGNATURES = {
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
+    "xdna_batch_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, P]),
+    "xdna_batch_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
     "xdna_fused_adam": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, D, D, D, D, D, I, I, I, P, P, P]),
 }
 
