@@ -223,6 +223,16 @@ int xdna_conv3x3_prepare_weights_bf16(const uint16_t* w, uint16_t* wt, int Cout,
 int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
                            uint16_t* y, int B, int cin, int cout, int H, int W, void* stream);
 
+/* Kernel selection of xdna_conv3x3_rows_bf16 (and the conv calls built on it), for
+ * measurements and tests: 0 automatic (default), 1 the main kernel (128 output channels
+ * x 64-256 rows per workgroup, weights streamed from L2 per tap), 2 / 3 the small-grid
+ * kernel (64 output channels x 64 / 128 rows, whole chunks staged in LDS, split-K when
+ * the grid is smaller than the CU count).  Results agree to the same tolerance; only the
+ * summation grouping differs.  No reference counterpart (a tuning knob, like the
+ * reference's XDNA_* performance environment variables).  XDNA_ROWS_VARIANT sets the
+ * initial value. */
+int xdna_conv3x3_set_rows_variant(int variant);
+
 /* wgrad stage 1: x and dy re-laid out channel-major into the workspace (snapshots:
  * stage 2 reads neither tensor).  Stage 2: the MFMA reduction over pixels and the
  * fixed-order split reduction into gw (and gb when not NULL). */

@@ -31,6 +31,8 @@
 #include "../../include/xdna_hip.h"
 
 #include <algorithm>
+#include <atomic>
+#include <cstdlib>
 
 namespace xdna {
 namespace {
@@ -78,8 +80,10 @@ struct RowsArgs {
   const uint16_t* wt;    // [co_pad][K]
   const uint16_t* bias;  // [cout] or null
   uint16_t* out;         // NCHW [B][cout][H][W]
+  float* part;           // split-K: fp32 partial sums [nsplit][cout][m_pad], else null
   int chunks, cout, wp, H, W, S, So;
-  int64_t img, m_total;
+  int ch_per;            // input chunks per split (blockIdx.z)
+  int64_t img, m_total, m_pad;
 };
 
 // One workgroup: 128 output channels x TP grid rows of one group; wave (wm, wn) owns
@@ -87,7 +91,11 @@ struct RowsArgs {
 // the TP + 2*wp + 2 rows of the halo window sit in LDS (double-buffered: the next chunk's
 // window is fetched into registers while this one is multiplied, one barrier per chunk);
 // the nine taps are row offsets into it.  Weight fragments come straight from L2 into
-// registers, one tap ahead (they are shared by every workgroup and stay L2-resident).
+// registers, two taps ahead (they are shared by every workgroup and stay L2-resident).
+// The window prefetch is spread over taps 0..6, each slice issued after that tap's weight
+// loads: the memory counter is in order, so a weight load never waits on a window load
+// issued less than three taps earlier.  blockIdx.z selects a range of ch_per input chunks
+// (split-K for small grids); a split writes fp32 partial sums for rows_reduce_kernel.
 template <int TP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void conv_rows_kernel(RowsArgs a) {
@@ -101,6 +109,8 @@ void conv_rows_kernel(RowsArgs a) {
   const int r0 = (blockIdx.x % tiles_per_group) * TP;
   if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;  // tail tile: no valid row
   const int co0 = blockIdx.y * kTCo;
+  const int ch0 = blockIdx.z * a.ch_per;
+  const int ch1 = min(a.chunks, ch0 + a.ch_per);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int K = a.chunks * 9 * kKStep;
@@ -112,7 +122,7 @@ void conv_rows_kernel(RowsArgs a) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     f32x16_t init = zero_acc();
-    if (a.bias) {
+    if (a.bias && !a.part) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
@@ -137,12 +147,14 @@ void conv_rows_kernel(RowsArgs a) {
       wa[set_][1][ks] = *reinterpret_cast<const u32x4_t*>(wrow1 + kb_ + ks * 16);            \
     }                                                                                        \
   } while (0)
-#define XDNA_ROWS_LOADX(ch_)                                                                 \
+// window vectors j with j * 7 / kXv == part_ (part_ < 0: all of them)
+#define XDNA_ROWS_LOADX(ch_, part_)                                                          \
   do {                                                                                       \
     const uint16_t* src_ = a.xp + ((int64_t(g) * a.chunks + (ch_)) * kGroupRows + r0) * kKStep; \
     _Pragma("unroll") for (int j = 0; j < kXv; ++j) {                                        \
       const int i = tid + j * 256;                                                           \
-      if (i < nvec) xr[j] = *reinterpret_cast<const u32x4_t*>(src_ + (i >> 3) * kKStep + (i & 7) * 8); \
+      if (((part_) < 0 || j * 7 / kXv == (part_)) && i < nvec)                               \
+        xr[j] = *reinterpret_cast<const u32x4_t*>(src_ + (i >> 3) * kKStep + (i & 7) * 8);   \
     }                                                                                        \
   } while (0)
 #define XDNA_ROWS_STOREX(buf_)                                                               \
@@ -154,15 +166,15 @@ void conv_rows_kernel(RowsArgs a) {
   } while (0)
 
   // weights two taps ahead
-  XDNA_ROWS_LOADW(0, 0, 0);
-  XDNA_ROWS_LOADW(1, 0, 1);
-  XDNA_ROWS_LOADX(0);
+  XDNA_ROWS_LOADW(0, ch0, 0);
+  XDNA_ROWS_LOADW(1, ch0, 1);
+  XDNA_ROWS_LOADX(ch0, -1);
   XDNA_ROWS_STOREX(0);
   __syncthreads();
 
-  for (int ch = 0; ch < a.chunks; ++ch) {
-    const int cur = ch & 1;
-    const bool more = ch + 1 < a.chunks;
+  for (int ch = ch0; ch < ch1; ++ch) {
+    const int cur = (ch - ch0) & 1;
+    const bool more = ch + 1 < ch1;
     const uint16_t* xb = &xs[cur][(wn * (TP / 2) + lr) * kPitch + lk];
     // B fragments are software-pipelined one 16-wide k-step ahead (36 steps per chunk:
     // 9 taps x 4), so LDS latency hides behind the 2*NT MFMAs of the current step.
@@ -179,7 +191,7 @@ void conv_rows_kernel(RowsArgs a) {
       } else if (more) {
         XDNA_ROWS_LOADW((tap + 2) % 3, ch + 1, tap - 7);
       }
-      if (tap == 0 && more) XDNA_ROWS_LOADX(ch + 1);
+      if (tap < 7 && more) XDNA_ROWS_LOADX(ch + 1, tap);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int step = tap * 4 + ks;
@@ -208,6 +220,24 @@ void conv_rows_kernel(RowsArgs a) {
 #undef XDNA_ROWS_LOADW
 #undef XDNA_ROWS_LOADX
 #undef XDNA_ROWS_STOREX
+
+  if (a.part) {
+    // split-K: fp32 partial sums, rows of 32 consecutive grid rows per store
+    float* pz = a.part + int64_t(blockIdx.z) * a.cout * a.m_pad;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
+      if (p >= a.m_total) continue;
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
+          if (co < a.cout) pz[int64_t(co) * a.m_pad + p] = acc[m][n][i];
+        }
+    }
+    return;
+  }
 
   // Epilogue: grid row -> NCHW pixel, one rounding; lanes 0..31 store 32 consecutive
   // grid rows (mostly consecutive image columns) of one channel.
@@ -240,6 +270,177 @@ void conv_rows_kernel(RowsArgs a) {
       for (int n = 0; n < NT; ++n)
         if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
     }
+}
+
+// Small-grid variant: 64 output channels x TP grid rows per workgroup.  Per input chunk
+// the halo window AND all nine taps of the workgroup's weights (64 x 576 bf16, 72 KiB)
+// are staged in LDS with every load of the chunk in flight at once, so a chunk costs one
+// memory latency instead of one per tap; the next chunk's loads are issued into
+// registers before the current chunk is multiplied.  Wave (wm, wn) owns channels
+// [wm*32, +32) x rows [wn*TP/2, +TP/2).  For convs whose grid is a few hundred
+// workgroups or less, where the main kernel waits on its per-tap weight loads.
+constexpr int kSCo = 64;                  // output channels per workgroup
+constexpr int kSWPitch = 9 * kKStep + 8;  // LDS pitch of a staged weight row (584)
+
+template <int TP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void conv_small_kernel(RowsArgs a) {
+  constexpr int kXRows = TP + kMaxHalo;
+  constexpr int NT = TP / 64;                     // 32-row MFMA tiles per wave
+  constexpr int kXv = (kXRows * 8 + 255) / 256;   // window vectors per thread
+  constexpr int kWv = kSCo * 9 * 8 / 256;         // weight vectors per thread (18)
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs = smem;                            // [kXRows][kPitch]
+  uint16_t* ws = smem + kXRows * kPitch;          // [kSCo][kSWPitch]
+
+  constexpr int tiles_per_group = kGroupOutRows / TP;
+  const int g = blockIdx.x / tiles_per_group;
+  const int r0 = (blockIdx.x % tiles_per_group) * TP;
+  if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;
+  const int co0 = blockIdx.y * kSCo;
+  const int ch0 = blockIdx.z * a.ch_per;
+  const int ch1 = min(a.chunks, ch0 + a.ch_per);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int K = a.chunks * 9 * kKStep;
+  const int nvec = (TP + 2 * a.wp + 2) * 8;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc[NT];
+  {
+    f32x16_t init = zero_acc();
+    if (a.bias && !a.part) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * 32 + mfma_row(i, lane);
+        init[i] = co < a.cout ? bf16_to_f32(a.bias[co]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[n] = init;
+  }
+
+  u32x4_t xr[kXv], wr[kWv];
+  // weight vector v of the workgroup's chunk slab: row v / 72, piece v % 72 (8 elements)
+  auto load_chunk = [&](int ch) {
+    const uint16_t* xsrc = a.xp + ((int64_t(g) * a.chunks + ch) * kGroupRows + r0) * kKStep;
+#pragma unroll
+    for (int j = 0; j < kXv; ++j) {
+      const int i = tid + j * 256;
+      if (i < nvec) xr[j] = *reinterpret_cast<const u32x4_t*>(xsrc + (i >> 3) * kKStep + (i & 7) * 8);
+    }
+    const uint16_t* wsrc = a.wt + int64_t(co0) * K + int64_t(ch) * 9 * kKStep;
+#pragma unroll
+    for (int j = 0; j < kWv; ++j) {
+      const int v = tid + j * 256;
+      const int row = v / 72, piece = v - row * 72;
+      wr[j] = *reinterpret_cast<const u32x4_t*>(wsrc + int64_t(row) * K + piece * 8);
+    }
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int j = 0; j < kXv; ++j) {
+      const int i = tid + j * 256;
+      if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[(i >> 3) * kPitch + (i & 7) * 8]) = xr[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kWv; ++j) {
+      const int v = tid + j * 256;
+      const int row = v / 72, piece = v - row * 72;
+      *reinterpret_cast<u32x4_t*>(&ws[row * kSWPitch + piece * 8]) = wr[j];
+    }
+  };
+
+  load_chunk(ch0);
+  const uint16_t* wa_base = ws + (wm * 32 + lr) * kSWPitch + lk;
+  const uint16_t* xb = xs + (wn * (TP / 2) + lr) * kPitch + lk;
+  for (int ch = ch0; ch < ch1; ++ch) {
+    __syncthreads();  // the previous chunk's reads of xs / ws are done
+    store_chunk();
+    __syncthreads();
+    if (ch + 1 < ch1) load_chunk(ch + 1);
+    u32x4_t aq[2], bq[2][NT];
+    aq[0] = *reinterpret_cast<const u32x4_t*>(wa_base);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) bq[0][n] = *reinterpret_cast<const u32x4_t*>(xb + n * 32 * kPitch);
+#pragma unroll
+    for (int step = 0; step < 36; ++step) {
+      if (step + 1 < 36) {
+        const int ntap = (step + 1) >> 2, nks = (step + 1) & 3;
+        const int noff = ((ntap / 3) * a.wp + (ntap % 3)) * kPitch + nks * 16;
+        aq[(step + 1) & 1] = *reinterpret_cast<const u32x4_t*>(wa_base + ntap * kKStep + nks * 16);
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          bq[(step + 1) & 1][n] = *reinterpret_cast<const u32x4_t*>(xb + noff + n * 32 * kPitch);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const bf16x8_t af = as_bf16x8(aq[step & 1]);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[n] = mfma_32x32x16(af, as_bf16x8(bq[step & 1][n]), acc[n]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  if (a.part) {
+    float* pz = a.part + int64_t(blockIdx.z) * a.cout * a.m_pad;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
+      if (p >= a.m_total) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * 32 + mfma_row(i, lane);
+        if (co < a.cout) pz[int64_t(co) * a.m_pad + p] = acc[n][i];
+      }
+    }
+    return;
+  }
+  const int first = a.S == 1 ? 0 : 1;
+  const int64_t plane = int64_t(a.H) * a.W;
+  uint16_t* obase[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    obase[n] = nullptr;
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
+    if (p >= a.m_total) continue;
+    const int64_t vb = p / a.img;
+    const int64_t rem = p - vb * a.img;
+    const int y = int(rem / a.wp);
+    const int col = int(rem - int64_t(y) * a.wp) - first;
+    if (y >= a.H || col < 0) continue;
+    const int b = int(vb / a.S), s = int(vb % a.S);
+    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+    if (col >= cols) continue;
+    const int x = (a.S == 1 ? 0 : s * a.So) + col;
+    obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int co = co0 + wm * 32 + mfma_row(i, lane);
+    if (co >= a.cout) continue;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+      if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[n][i]);
+  }
+}
+
+// Split-K epilogue: out[b][co][y][x] = bf16(bias[co] + sum over splits, in split order,
+// of part[z][co][p(b, y, x)]).  blockIdx.y = plane b * cout + co (plane0 + that), threads
+// over the plane's pixels (32-bit index math).
+__global__ __launch_bounds__(256) void rows_reduce_kernel(RowsArgs a, int nsplit, int plane0) {
+  const int plane = plane0 + int(blockIdx.y);
+  const int b = plane / a.cout, co = plane - b * a.cout;
+  const int pix = int(blockIdx.x) * 256 + int(threadIdx.x);
+  if (pix >= a.H * a.W) return;
+  const int y = pix / a.W, x = pix - y * a.W;
+  const int s = a.S == 1 ? 0 : x / a.So;
+  const int col = x - s * a.So + (a.S == 1 ? 0 : 1);
+  const int64_t p = (int64_t(b) * a.S + s) * a.img + int64_t(y) * a.wp + col;
+  float v = a.bias ? bf16_to_f32(a.bias[co]) : 0.0f;
+  const float* pp = a.part + int64_t(co) * a.m_pad + p;
+  const int64_t zstride = int64_t(a.cout) * a.m_pad;
+  for (int z = 0; z < nsplit; ++z) v += pp[z * zstride];
+  a.out[int64_t(plane) * a.H * a.W + pix] = f32_to_bf16(v);
 }
 
 // ---------------------------------------------------------------------------------
@@ -629,6 +830,11 @@ int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, 
 }
 
 // conv of packed input xp (cin channels) with prepared weights -> NCHW out (cout channels).
+std::atomic<int> g_rows_variant{[] {
+  const char* e = std::getenv("XDNA_ROWS_VARIANT");
+  return e ? std::atoi(e) : 0;
+}()};
+
 int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
                 int B, int cin, int cout, int H, int W, void* stream) {
   const ConvGeom geom = conv_geom(B, H, W);
@@ -637,6 +843,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.wt = wt;
   a.bias = bias;
   a.out = out;
+  a.part = nullptr;
   a.chunks = int(ceil_div(cin, kKStep));
   a.cout = cout;
   a.wp = geom.st.wp;
@@ -644,21 +851,76 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.W = W;
   a.S = geom.st.S;
   a.So = geom.st.So;
+  a.ch_per = a.chunks;
   a.img = geom.img;
   a.m_total = geom.m_total;
+  a.m_pad = int64_t(geom.groups) * kGroupOutRows;
   if (!admit_launch("conv3x3 rows")) return -1;
-  const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
-  // Tile rows per workgroup: the largest of 256 / 128 / 64 that still puts a few
-  // hundred workgroups on the 256 CUs.
-  const int64_t wg256 = int64_t(geom.groups) * (kGroupOutRows / 256) * ytiles;
-  const int64_t wg128 = int64_t(geom.groups) * (kGroupOutRows / 128) * ytiles;
   hipStream_t st = as_stream(stream);
-  if (wg256 >= 384) {
-    conv_rows_kernel<256><<<dim3(unsigned(geom.groups * (kGroupOutRows / 256)), ytiles), 256, 0, st>>>(a);
-  } else if (wg128 >= 384) {
-    conv_rows_kernel<128><<<dim3(unsigned(geom.groups * (kGroupOutRows / 128)), ytiles), 256, 0, st>>>(a);
-  } else {
-    conv_rows_kernel<64><<<dim3(unsigned(geom.groups * (kGroupOutRows / 64)), ytiles), 256, 0, st>>>(a);
+  // Kernel choice (xdna_conv3x3_set_rows_variant, or XDNA_ROWS_VARIANT at start-up,
+  // overrides it: 1 main kernel, 2 / 3 small-grid kernel with 64 / 128-row tiles).  The
+  // main kernel needs a grid of several workgroups per CU to hide its per-tap weight
+  // loads; below that the small-grid kernel, which stages whole chunks, is faster.
+  const int variant = g_rows_variant.load();
+  const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
+  const int64_t big128 = ceil_div(geom.m_total, 128) * ytiles;
+  const bool small = variant == 2 || variant == 3 || (variant == 0 && big128 < 512);
+  if (!small) {
+    // Tile rows per workgroup: the largest of 256 / 128 / 64 that still puts a few
+    // hundred workgroups on the 256 CUs.
+    const int64_t wg256 = int64_t(geom.groups) * (kGroupOutRows / 256) * ytiles;
+    const int64_t wg128 = int64_t(geom.groups) * (kGroupOutRows / 128) * ytiles;
+    const int TP = wg256 >= 384 ? 256 : wg128 >= 384 ? 128 : 64;
+    const dim3 grid(unsigned(int64_t(geom.groups) * (kGroupOutRows / TP)), ytiles, 1);
+    if (TP == 256)
+      conv_rows_kernel<256><<<grid, 256, 0, st>>>(a);
+    else if (TP == 128)
+      conv_rows_kernel<128><<<grid, 256, 0, st>>>(a);
+    else
+      conv_rows_kernel<64><<<grid, 256, 0, st>>>(a);
+    return check_launch("conv3x3 rows");
+  }
+  static const bool lds_ok = [] {
+    const int b64 = (64 + kMaxHalo) * kPitch * 2 + kSCo * kSWPitch * 2;
+    const int b128 = (128 + kMaxHalo) * kPitch * 2 + kSCo * kSWPitch * 2;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<64>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, b64) == hipSuccess &&
+           hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, b128) == hipSuccess;
+  }();
+  if (!lds_ok) {
+    set_error("conv3x3 rows: cannot enable the small-grid kernel's LDS size");
+    return -1;
+  }
+  const unsigned stiles = unsigned(ceil_div(cout, kSCo));
+  const int TP = variant == 2 ? 64 : variant == 3 ? 128 : (ceil_div(geom.m_total, 128) * stiles >= 256 ? 128 : 64);
+  const int64_t valid = ceil_div(geom.m_total, TP) * stiles;
+  // Fewer workgroups than CUs: split the input chunks over blockIdx.z and sum the fp32
+  // partials in a second pass (in split order).
+  int nsplit = 1;
+  if (valid < 256 && a.chunks >= 2) {
+    nsplit = int(std::min<int64_t>(a.chunks, ceil_div(256, valid)));
+    a.ch_per = int(ceil_div(a.chunks, nsplit));
+    nsplit = int(ceil_div(a.chunks, a.ch_per));
+  }
+  if (nsplit > 1) {
+    const size_t pbytes = size_t(nsplit) * size_t(cout) * size_t(a.m_pad) * sizeof(float);
+    a.part = static_cast<float*>(xdna_hip_cache_alloc(pbytes));
+    if (!a.part) return -1;
+  }
+  const dim3 grid(unsigned(int64_t(geom.groups) * (kGroupOutRows / TP)), stiles, unsigned(nsplit));
+  const size_t lds = size_t(TP + kMaxHalo) * kPitch * 2 + size_t(kSCo) * kSWPitch * 2;
+  if (TP == 128)
+    conv_small_kernel<128><<<grid, 256, lds, st>>>(a);
+  else
+    conv_small_kernel<64><<<grid, 256, lds, st>>>(a);
+  if (nsplit > 1) {
+    const unsigned pix_blocks = unsigned(ceil_div(int64_t(H) * W, 256));
+    const int planes = B * cout;
+    for (int p0 = 0; p0 < planes; p0 += 65535)
+      rows_reduce_kernel<<<dim3(pix_blocks, unsigned(std::min(65535, planes - p0))), 256, 0, st>>>(a, nsplit, p0);
+    // stream-ordered reuse: the next user of the block runs after the reduce
+    xdna_hip_cache_free(a.part);
   }
   return check_launch("conv3x3 rows");
 }
@@ -889,6 +1151,15 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
                            uint16_t* y, int B, int cin, int cout, int H, int W, void* stream) {
   if (!shape_ok("xdna_conv3x3_rows_bf16", B, cin, cout, H, W)) return -1;
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream);
+}
+
+int xdna_conv3x3_set_rows_variant(int variant) {
+  if (variant < 0 || variant > 3) {
+    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..3");
+    return -1;
+  }
+  g_rows_variant.store(variant);
+  return 0;
 }
 
 int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H, int W,

@@ -72,6 +72,7 @@ SIGNATURES = {
     "xdna_conv3x3w_packed_bytes": (Z, [I, I, I, I]),
     "xdna_conv3x3_prepared_weight_bytes": (Z, [I, I]),
     "xdna_conv3x3_prepare_weights_bf16": (I, [P, P, I, I, I, P]),
+    "xdna_conv3x3_set_rows_variant": (I, [I]),
     "xdna_conv3x3_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),

@@ -4,8 +4,10 @@ Bar: every output within 2 bf16 ulp of the exact sum of th
 operands (with a floor at ulp(max|ref| * 2^-8) for outputs that cancel to ~0) and
 relative L2 <= 1e-2.  Shapes cover ragged channel counts (partial 64-chunks, partial
 128-blocks), one and several 2048-row groups, tiny channel counts (RGB-like), width
-strips (W > 36: S = 2, 3) and the C1 conv at B = 2.  wgrad is also checked for
-run-to-run bit equality (its split-K reduction is fixed-order).
+strips (W > 36: S = 2, 3) and the C1 conv at B = 2.  Forward and dgrad run through each
+rows-kernel variant (main kernel; small-grid kernel with 64 / 128-row tiles, split-K over
+chunks on small grids).  wgrad is also checked for run-to-run bit equality (its split-K
+reduction is fixed-order).
 """
 import numpy as np
 import pytest
@@ -43,10 +45,23 @@ def _ws(nbytes):
     return dev_zeros((max(1, (nbytes + 1) // 2),))
 
 
+# rows-kernel variants (xdna_conv3x3_set_rows_variant): main kernel, small-grid kernel
+# with 64- and 128-row tiles (split-K over chunks where the grid is small)
+VARIANTS = [1, 2, 3]
+
+
+@pytest.fixture
+def variant(hip, request):
+    assert hip.xdna_conv3x3_set_rows_variant(request.param) == 0
+    yield request.param
+    assert hip.xdna_conv3x3_set_rows_variant(0) == 0
+
+
+@pytest.mark.parametrize("variant", VARIANTS, indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_forward(hip, shape):
+def test_forward(hip, shape, variant):
     B, Cin, Cout, H, W = shape
-    print(f"conv fwd {shape}", flush=True)
+    print(f"conv fwd {shape} variant {variant}", flush=True)
     x, w, b, _ = _data(*shape, seed=sum(shape))
     ref = oracle.conv3x3_fwd(x, w, b)
     ws_bytes = hip.xdna_conv3x3_fwd_workspace_bytes(B, Cin, Cout, H, W)
@@ -62,10 +77,11 @@ def test_forward(hip, shape):
     check_bf16(host(y2), oracle.conv3x3_fwd(x, w), what=f"fwd nobias {shape}")
 
 
+@pytest.mark.parametrize("variant", VARIANTS, indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_dgrad(hip, shape):
+def test_dgrad(hip, shape, variant):
     B, Cin, Cout, H, W = shape
-    print(f"conv dgrad {shape}", flush=True)
+    print(f"conv dgrad {shape} variant {variant}", flush=True)
     _, w, _, dy = _data(*shape, seed=sum(shape) + 1)
     ref = oracle.conv3x3_dgrad(dy, w)
     ws_bytes = hip.xdna_conv3x3_dgrad_workspace_bytes(B, Cin, Cout, H, W)
