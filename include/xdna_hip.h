@@ -282,6 +282,14 @@ int xdna_fused_adam(int n_tensors, void* const* params, void* const* grads,
                     int maximize, int mode, const float* grad_scale,
                     const float* found_inf, void* stream);
 
+/* tensors[i][j] += value (fp32, computed as t + value in fp32) for every element of
+ * n_tensors device tensors: torch._foreach_add_(state_steps, 1), which the optimizers
+ * call before the fused Adam step (torch/optim/adam.py _fused_adam; the reference runs
+ * it on the CPU through its fallback, torch_xdna_device.cpp:5124-5260).  One launch per
+ * 64 tensors. */
+int xdna_foreach_add_scalar_f32(int n_tensors, float* const* tensors, const int64_t* numels,
+                                float value, void* stream);
+
 /* Batch norm in training mode without running statistics over x[N][C][L] bf16 (the form
  * PyTorch's instance_norm takes: [B, C, H, W] as [1, B*C, H*W]).  Replaces PyTorch's CPU
  * native_batch_norm / native_batch_norm_backward, which the reference reaches through

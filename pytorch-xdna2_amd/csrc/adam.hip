@@ -23,6 +23,7 @@
 #include "common.h"
 #include "../../include/xdna_hip.h"
 
+#include <algorithm>
 #include <cmath>
 #include <vector>
 
@@ -194,6 +195,21 @@ __global__ __launch_bounds__(kThreads) void fused_adam_kernel(AdamArgs a, AdamSc
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// t[i][j] += value for every element of up to kForeachMax fp32 tensors, one launch
+// (workgroup i takes tensor i): the optimizers' per-step counter bump
+// (torch._foreach_add_(state_steps, 1)) in one kernel instead of one per tensor.
+constexpr int kForeachMax = 64;
+struct ForeachArgs {
+  float* t[kForeachMax];
+  int64_t numel[kForeachMax];
+};
+
+__global__ __launch_bounds__(256) void foreach_add_f32_kernel(ForeachArgs a, float value) {
+  float* t = a.t[blockIdx.x];
+  const int64_t n = a.numel[blockIdx.x];
+  for (int64_t j = threadIdx.x; j < n; j += 256) t[j] = t[j] + value;
+}
+
 }  // namespace
 }  // namespace xdna
 
@@ -253,6 +269,31 @@ extern "C" int xdna_fused_adam(int n_tensors, void* const* params, void* const* 
       fused_adam_kernel<float><<<dim3(unsigned(blocks)), kThreads, 0, as_stream(stream)>>>(
           a, s, grad_scale, found_inf);
     if (check_launch("xdna_fused_adam")) return -1;
+  }
+  return 0;
+}
+
+extern "C" int xdna_foreach_add_scalar_f32(int n_tensors, float* const* tensors, const int64_t* numels,
+                                           float value, void* stream) {
+  if (n_tensors < 0 || (n_tensors > 0 && (!tensors || !numels))) {
+    set_error("xdna_foreach_add_scalar_f32: invalid arguments");
+    return -1;
+  }
+  for (int done = 0; done < n_tensors;) {
+    ForeachArgs a;
+    const int n = std::min(kForeachMax, n_tensors - done);
+    for (int i = 0; i < n; ++i) {
+      a.t[i] = tensors[done + i];
+      a.numel[i] = numels[done + i];
+      if (a.numel[i] < 0 || (a.numel[i] > 0 && !a.t[i])) {
+        set_error("xdna_foreach_add_scalar_f32: invalid tensor");
+        return -1;
+      }
+    }
+    if (!admit_launch("xdna_foreach_add_scalar_f32")) return -1;
+    foreach_add_f32_kernel<<<dim3(unsigned(n)), 256, 0, as_stream(stream)>>>(a, value);
+    if (check_launch("xdna_foreach_add_scalar_f32")) return -1;
+    done += n;
   }
   return 0;
 }

@@ -11,6 +11,8 @@
 // (m/n-contiguous source), or element loads (anything else, and the ragged edges).
 #include "common.h"
 #include "mfma.h"
+
+#include <algorithm>
 #include "../../include/xdna_hip.h"
 
 namespace xdna {
@@ -32,6 +34,10 @@ struct GemmArgs {
   int bias_mode;
   int64_t bias_sm, bias_sn;
   float alpha, beta;
+  int batch;
+  int kt_per;   // k-tiles per split (blockIdx.z = batch index * nsplit + split)
+  int nsplit;
+  float* part;  // split-K: fp32 partial products [nsplit][batch][M][N], else null
 };
 
 // Stages rows [r0, r0+128) x k [k0, k0+32) of a row-major-by-strides operand into
@@ -98,7 +104,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int m0 = blockIdx.y * kTM, n0 = blockIdx.x * kTN;
-  const int batch = blockIdx.z;
+  const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
+  const int kbeg = split * g.kt_per * kTK, kend = min(g.K, kbeg + g.kt_per * kTK);
   const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
   const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
   const int lr = lane & 31, lk = (lane >> 5) * 8;
@@ -109,10 +116,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = zero_acc();
 
-  for (int k0 = 0; k0 < g.K; k0 += kTK) {
+  for (int k0 = kbeg; k0 < kend; k0 += kTK) {
     __syncthreads();
-    stage<kModeA>(as, A, g.a_r, g.a_k, m0, g.M, k0, g.K, tid);
-    stage<kModeB>(bs, B, g.b_r, g.b_k, n0, g.N, k0, g.K, tid);
+    stage<kModeA>(as, A, g.a_r, g.a_k, m0, g.M, k0, kend, tid);
+    stage<kModeB>(bs, B, g.b_r, g.b_k, n0, g.N, k0, kend, tid);
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < kTK / 16; ++ks) {
@@ -129,6 +136,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     }
   }
 
+  if (g.part) {
+    float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + lr;
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 64 + i * 32 + mfma_row(r, lane);
+          if (m < g.M) P[int64_t(m) * g.N + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
   uint16_t* C = g.c + int64_t(batch) * g.c_batch;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -151,6 +174,29 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         C[int64_t(m) * g.c_m + int64_t(n) * g.c_n] = f32_to_bf16(v);
       }
     }
+}
+
+// Split-K epilogue: C[b][m][n] = bf16(alpha * sum over splits (in split order) of the fp32
+// partials + beta * bias term), consecutive threads on consecutive n.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs g) {
+  const int64_t mn = int64_t(g.M) * g.N;
+  const int64_t n_all = mn * g.batch;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n_all; i += int64_t(gridDim.x) * 256) {
+    const int b = int(i / mn);
+    const int64_t r = i - int64_t(b) * mn;
+    const int m = int(r / g.N), n = int(r - int64_t(m) * g.N);
+    float acc = 0.0f;
+    for (int z = 0; z < g.nsplit; ++z) acc += g.part[int64_t(z) * n_all + i];
+    float v = g.alpha * acc;
+    if (g.bias_mode && g.beta != 0.0f) {
+      float bv;
+      if (g.bias_mode == 1) bv = bf16_to_f32(g.bias[int64_t(n) * g.bias_sn]);
+      else if (g.bias_mode == 2) bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm + int64_t(n) * g.bias_sn]);
+      else bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm]);
+      v += g.beta * bv;
+    }
+    g.c[int64_t(b) * g.c_batch + int64_t(m) * g.c_m + int64_t(n) * g.c_n] = f32_to_bf16(v);
+  }
 }
 
 // Operand described as [rows][k] with element strides (s_r, s_k).
@@ -215,10 +261,35 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   const int ma = stage_mode(A, lda_m, lda_k, stride_a, batch);
   const int mb = stage_mode(Bm, ldb_n, ldb_k, stride_b, batch);
   if (!admit_launch("xdna_gemm_bf16")) return -1;
-  const dim3 grid(unsigned(ceil_div(N, kTN)), unsigned(ceil_div(M, kTM)), unsigned(batch));
+  g.batch = batch;
+  // Few output tiles and a long K (Gram matrices: [C x HW] x [HW x C]): split K over
+  // blockIdx.z so the grid covers the CUs; fp32 partials are summed in split order.
+  const int64_t tiles = ceil_div(N, kTN) * ceil_div(M, kTM) * int64_t(batch);
+  const int ktiles = int(ceil_div(K, kTK));
+  g.nsplit = 1;
+  g.kt_per = std::max(ktiles, 1);
+  g.part = nullptr;
+  if (tiles < 256 && ktiles >= 8) {
+    int s = int(std::min<int64_t>(ktiles / 4, ceil_div(512, tiles)));
+    s = std::max(1, std::min(s, 65535 / std::max(batch, 1)));
+    g.kt_per = int(ceil_div(ktiles, s));
+    g.nsplit = int(ceil_div(ktiles, g.kt_per));
+  }
   hipStream_t st = as_stream(stream);
+  if (g.nsplit > 1) {
+    g.part = static_cast<float*>(
+        xdna_hip_cache_alloc(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float)));
+    if (!g.part) return -1;
+  }
+  const dim3 grid(unsigned(ceil_div(N, kTN)), unsigned(ceil_div(M, kTM)), unsigned(batch * g.nsplit));
   if (ma == kAlongK) launch_b<kAlongK>(mb, grid, st, g);
   else if (ma == kAlongRow) launch_b<kAlongRow>(mb, grid, st, g);
   else launch_b<kScalar>(mb, grid, st, g);
+  if (g.nsplit > 1) {
+    const int64_t n_all = int64_t(batch) * M * N;
+    gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st>>>(g);
+    // stream-ordered reuse: the next user of the block runs after the reduce
+    xdna_hip_cache_free(g.part);
+  }
   return check_launch("xdna_gemm_bf16");
 }

@@ -9,6 +9,7 @@
 #include <ATen/ops/_fused_adam_native.h>
 #include <c10/core/impl/LocalDispatchKeySet.h>
 
+#include <algorithm>
 #include <array>
 #include <mutex>
 #include <optional>
@@ -57,6 +58,76 @@ bool conv_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef
   return true;
 }
 
+// Prepared weights of frozen tensors (requires_grad false: a loss network's weights),
+// keyed by storage, offset, shape, version and direction, the role of the reference's
+// weight slots (torch_xdna_device.cpp:2208-2271).  A weak reference to the storage tells
+// a live tensor from a new one at a recycled address; in-place writes bump the version.
+// Trainable weights are prepared on every call: the optimizer changes them in place
+// (also inside replayed graphs, where no version is bumped).
+struct PreparedWeights {
+  c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
+  int64_t offset = 0, version = 0;
+  std::array<int64_t, 4> sizes{};
+  bool dgrad = false;
+  at::Tensor wt;
+  uint64_t last_use = 0;
+};
+
+struct WeightCache {
+  std::mutex mu;
+  std::vector<PreparedWeights> entries;
+  uint64_t tick = 0;
+  static constexpr size_t kMaxEntries = 64;
+};
+
+WeightCache& weight_cache() {
+  static auto* c = new WeightCache();
+  return *c;
+}
+
+bool weight_cacheable(const at::Tensor& w) {
+  return !w.requires_grad() && !w.is_inference() && w.dim() == 4;
+}
+
+std::array<int64_t, 4> sizes4(const at::Tensor& w) { return {w.size(0), w.size(1), w.size(2), w.size(3)}; }
+
+at::Tensor cached_weights(const at::Tensor& w, bool dgrad) {
+  WeightCache& c = weight_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  const int64_t ver = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
+  for (auto& e : c.entries) {
+    if (e.dgrad != dgrad || e.offset != w.storage_offset() || e.version != ver || e.sizes != sizes4(w)) continue;
+    auto live = e.storage.lock();
+    if (!live || live.get() != w.storage().unsafeGetStorageImpl()) continue;
+    e.last_use = ++c.tick;
+    return e.wt;
+  }
+  return at::Tensor();
+}
+
+void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
+  WeightCache& c = weight_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  // drop entries of dead storages, then the least recently used one when full
+  c.entries.erase(std::remove_if(c.entries.begin(), c.entries.end(),
+                                 [](const PreparedWeights& e) { return e.storage.expired(); }),
+                  c.entries.end());
+  if (c.entries.size() >= WeightCache::kMaxEntries) {
+    auto lru = std::min_element(c.entries.begin(), c.entries.end(),
+                                [](const auto& a, const auto& b) { return a.last_use < b.last_use; });
+    c.entries.erase(lru);
+  }
+  PreparedWeights e;
+  e.storage = c10::weak_intrusive_ptr<c10::StorageImpl>(w.storage().getWeakStorageImpl());
+  e.offset = w.storage_offset();
+  e.version = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
+  e.sizes = sizes4(w);
+  e.dgrad = dgrad;
+  e.wt = wt;
+  e.last_use = ++c.tick;
+  c.entries.push_back(std::move(e));
+}
+
 // Runs the conv of `src` (NCHW, cin channels) with `w` (forward: w as given; dgrad:
 // flip+swap) into a new NCHW tensor of cout channels.
 at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor* bias,
@@ -90,11 +161,16 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
                 "conv pack");
     }
   }
-  at::Tensor wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
-  check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
-                                              static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
-                                              int(w.size(1)), dgrad ? 1 : 0, st),
-            "conv weights");
+  const bool cacheable = weight_cacheable(w);
+  at::Tensor wt = cacheable ? cached_weights(w, dgrad) : at::Tensor();
+  if (!wt.defined()) {
+    wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
+    check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
+                                                static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
+                                                int(w.size(1)), dgrad ? 1 : 0, st),
+              "conv weights");
+    if (cacheable) remember_weights(w, dgrad, wt);
+  }
   at::Tensor out = empty_xdna({B, cout, H, W}, at::kBFloat16);
   at::Tensor bc;
   if (bias) bc = bias->contiguous();
@@ -426,6 +502,30 @@ void fused_adamw_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::
                     found_inf, true);
 }
 
+// torch._foreach_add_(state_steps, 1) before every fused Adam step: one HIP launch for
+// the whole list of fp32 xdna tensors; other forms go to PyTorch-ROCm on aliases.
+void foreach_add_scalar_xdna(at::TensorList self, const at::Scalar& scalar) {
+  bool ok = g_mode.load() >= 1 && !scalar.isComplex();
+  for (const auto& t : self)
+    ok = ok && t.defined() && t.device().type() == kXdna && t.scalar_type() == at::kFloat && t.is_contiguous();
+  if (ok) {
+    ScopedCount sc("hip_foreach_add.run");
+    std::vector<float*> ptrs(self.size());
+    std::vector<int64_t> numels(self.size());
+    for (size_t i = 0; i < self.size(); ++i) {
+      ptrs[i] = self[i].data_ptr<float>();
+      numels[i] = self[i].numel();
+    }
+    check_abi(xdna_foreach_add_scalar_f32(int(self.size()), ptrs.data(), numels.data(), scalar.toFloat(),
+                                          current_stream()),
+              "foreach add");
+    return;
+  }
+  ScopedCount sc("aten::_foreach_add_.rocm");
+  BelowAutograd g;
+  at::_ops::_foreach_add__Scalar::call(rocm_list(self), scalar);
+}
+
 double lr_value(const at::Tensor& lr) { return lr.item<double>(); }
 
 void fused_adam_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
@@ -616,6 +716,7 @@ void register_hot_ops(torch::Library& m) {
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_xdna));
   m.impl("_fused_adam_.tensor_lr", TORCH_FN(fused_adam_tlr_xdna));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tlr_xdna));
+  m.impl("_foreach_add_.Scalar", TORCH_FN(foreach_add_scalar_xdna));
   m.impl("native_batch_norm", TORCH_FN(native_batch_norm_xdna));
   m.impl("native_batch_norm_backward", TORCH_FN(native_batch_norm_backward_xdna));
 }

@@ -239,3 +239,48 @@ def test_launch_errors_raise(xdna):
     finally:
         dev._C.reset_failure_state()
     assert conv(x).shape == (1, 16, 8, 8)
+
+
+def test_foreach_add_steps_one_launch():
+    ts = [torch.zeros((), device=X) for _ in range(70)] + [torch.arange(5.0).to(X)]
+    xdna_train.reset_mapped_cpu_stats()
+    torch._foreach_add_(ts, 1)
+    torch._foreach_add_(ts, 0.5)
+    stats = xdna_train.mapped_cpu_stats()
+    assert stats.get("hip_foreach_add.run", {}).get("calls", 0) == 2, stats
+    assert all(float(t) == 1.5 for t in ts[:70])
+    assert torch.equal(ts[70].cpu(), torch.arange(5.0) + 1.5)
+    # bf16 lists take the ROCm path
+    b = [torch.ones(3, device=X).bfloat16()]
+    torch._foreach_add_(b, 2)
+    assert torch.equal(b[0].cpu().float(), torch.full((3,), 3.0))
+
+
+def test_frozen_weights_prepared_once_and_refreshed_on_write():
+    torch.manual_seed(3)
+    conv = torch.nn.Conv2d(64, 64, 3, padding=1).bfloat16()
+    for p in conv.parameters():
+        p.requires_grad_(False)
+    x = torch.randn(2, 64, 10, 10).bfloat16()
+    cd = torch.nn.Conv2d(64, 64, 3, padding=1).bfloat16()
+    cd.load_state_dict(conv.state_dict())
+    for p in cd.parameters():
+        p.requires_grad_(False)
+    cd = cd.to(X)
+    xd = x.to(X)
+    y1 = cd(xd)
+    n0 = xdna_train.device._C.launch_count()
+    y2 = cd(xd)
+    n1 = xdna_train.device._C.launch_count()
+    assert torch.equal(y1.cpu(), y2.cpu())
+    # the second call reuses the prepared weights: pack + conv only (no preparation launch)
+    assert n1 - n0 == 2, (n0, n1)
+    ref = conv(x).float()
+    assert torch.allclose(y2.cpu().float(), ref, atol=5e-2, rtol=5e-2)
+    # an in-place write bumps the version: the new weights are used
+    with torch.no_grad():
+        cd.weight.mul_(-1)
+        conv.weight.mul_(-1)
+    y3 = cd(xd)
+    assert torch.allclose(y3.cpu().float(), conv(x).float(), atol=5e-2, rtol=5e-2)
+    assert not torch.allclose(y3.cpu().float(), y2.cpu().float(), atol=5e-2, rtol=5e-2)
