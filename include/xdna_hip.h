@@ -86,6 +86,11 @@ int xdna_hip_cache_pool_begin(int64_t pool);
 int xdna_hip_cache_pool_end(void);
 int xdna_hip_cache_pool_release(int64_t pool);
 
+/* out[i] = bf16 rounding of in[i] as every kernel of the library applies it: round to
+ * nearest even, NaN -> 0x7FC0 (c10::BFloat16's convention, which the reference's CPU
+ * path uses).  A diagnostic that lets tests pin the rounding; no reference counterpart. */
+int xdna_round_bf16(const float* in, uint16_t* out, int64_t n, void* stream);
+
 int xdna_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
                           void* stream); /* kind: 1 H2D, 2 D2H, 3 D2D, 4 default */
 int xdna_hip_memset_async(void* dst, int value, size_t bytes, void* stream);

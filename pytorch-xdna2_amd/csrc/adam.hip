@@ -61,6 +61,8 @@ template <typename T> __device__ inline void st(T* p, int64_t i, float v);
 template <> __device__ inline void st<float>(float* p, int64_t i, float v) { p[i] = v; }
 template <> __device__ inline void st<uint16_t>(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 // 8 consecutive elements <-> fp32 registers.
 template <typename T> struct Vec8;
 template <> struct Vec8<uint16_t> {
@@ -117,35 +119,61 @@ __device__ inline void adam_elem(float& p, float& g, float& m, float& v, float& 
   p = p - (k.step_size * m) / den;
 }
 
+// Bias corrections of this tensor's step, in double as torch's _fused_adam_ computes
+// them (step_size = lr / (1 - beta1^t), sqrt(1 - beta2^t)).
+__device__ inline StepConsts step_consts(const AdamScalars& s, float step_f) {
+  const double step = double(step_f);
+  const double bc1 = 1.0 - pow(s.beta1, step);
+  const double bc2 = 1.0 - pow(s.beta2, step);
+  StepConsts k;
+  k.step_size = float(s.lr / bc1);
+  k.bc2_sqrt = float(sqrt(bc2));
+  k.eps = float(s.eps);
+  k.beta2 = float(s.beta2);
+  k.one_minus_beta2 = float(1.0 - s.beta2);
+  k.w = float(1.0 - s.beta1);
+  k.one_minus_w = 1.0f - k.w;
+  k.wd = float(s.wd);
+  k.decay = float(1.0 - s.lr * s.wd);
+  return k;
+}
+
+// 16-byte raw vector <-> 8 fp32 values (bf16: 8 elements; fp32: 4 elements per vector,
+// two vectors per 8).
+template <typename T> struct Raw;
+template <> struct Raw<uint16_t> {
+  static constexpr int kVecs = 1;
+  __device__ static inline void to_f32(const u32x4& w, const u32x4&, float* f) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = __uint_as_float(w[e] << 16);
+      f[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+    }
+  }
+};
+template <> struct Raw<float> {
+  static constexpr int kVecs = 2;
+  __device__ static inline void to_f32(const u32x4& a, const u32x4& b, float* f) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = __uint_as_float(a[e]);
+      f[4 + e] = __uint_as_float(b[e]);
+    }
+  }
+};
+
+// One workgroup per kBlockElems elements of one tensor (block_start prefix).  A full
+// item issues all its loads (kIters vectors each of p, g, m, v per thread, raw) before
+// thread 0 computes the step constants (double-precision bias corrections) and the
+// workgroup waits for them: the loads' latency covers that work.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void fused_adam_kernel(AdamArgs a, AdamScalars s,
                                                               const float* grad_scale,
                                                               const float* found_inf) {
   if (found_inf && *found_inf == 1.0f) return;
   __shared__ StepConsts sk;
-  __shared__ int s_tensor;
-  if (threadIdx.x == 0) {
-    int t = 0;
-    while (t + 1 < a.n && int(blockIdx.x) >= a.block_start[t + 1]) ++t;
-    s_tensor = t;
-    const double step = double(*a.step[t]);
-    const double bc1 = 1.0 - pow(s.beta1, step);
-    const double bc2 = 1.0 - pow(s.beta2, step);
-    StepConsts k;
-    k.step_size = float(s.lr / bc1);
-    k.bc2_sqrt = float(sqrt(bc2));
-    k.eps = float(s.eps);
-    k.beta2 = float(s.beta2);
-    k.one_minus_beta2 = float(1.0 - s.beta2);
-    k.w = float(1.0 - s.beta1);
-    k.one_minus_w = 1.0f - k.w;
-    k.wd = float(s.wd);
-    k.decay = float(1.0 - s.lr * s.wd);
-    sk = k;
-  }
-  __syncthreads();
-  const int t = s_tensor;
-  const StepConsts k = sk;
+  int t = 0;
+  while (t + 1 < a.n && int(blockIdx.x) >= a.block_start[t + 1]) ++t;
   T* P = static_cast<T*>(a.p[t]);
   T* G = static_cast<T*>(a.g[t]);
   T* M = static_cast<T*>(a.m[t]);
@@ -153,30 +181,68 @@ __global__ __launch_bounds__(kThreads) void fused_adam_kernel(AdamArgs a, AdamSc
   T* MX = static_cast<T*>(a.mx[t]);
   const int64_t n = a.numel[t];
   const int64_t base = int64_t(blockIdx.x - a.block_start[t]) * kBlockElems;
+  const int64_t i0 = base + int64_t(threadIdx.x) * kVec;
+  constexpr int64_t kStride = int64_t(kThreads) * kVec;
+  constexpr int RV = Raw<T>::kVecs;
+  const bool full = a.vec_ok[t] && base + kBlockElems <= n && !s.amsgrad && !grad_scale;
+  u32x4 rp[kIters][RV], rg[kIters][RV], rm[kIters][RV], rv[kIters][RV];
+  if (full) {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it)
+#pragma unroll
+      for (int q = 0; q < RV; ++q) {
+        const int64_t j = i0 + it * kStride + q * (8 / RV);
+        rp[it][q] = *reinterpret_cast<const u32x4*>(P + j);
+        rg[it][q] = *reinterpret_cast<const u32x4*>(G + j);
+        rm[it][q] = *reinterpret_cast<const u32x4*>(M + j);
+        rv[it][q] = *reinterpret_cast<const u32x4*>(V + j);
+      }
+  }
+  if (threadIdx.x == 0) sk = step_consts(s, *a.step[t]);
+  __syncthreads();
+  const StepConsts k = sk;
+  if (full) {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      float p[kVec], g[kVec], m[kVec], v[kVec];
+      Raw<T>::to_f32(rp[it][0], rp[it][RV - 1], p);
+      Raw<T>::to_f32(rg[it][0], rg[it][RV - 1], g);
+      Raw<T>::to_f32(rm[it][0], rm[it][RV - 1], m);
+      Raw<T>::to_f32(rv[it][0], rv[it][RV - 1], v);
+      float mx_unused = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) adam_elem(p[e], g[e], m[e], v[e], mx_unused, k, s);
+      const int64_t j = i0 + it * kStride;
+      Vec8<T>::store(P, j, p);
+      Vec8<T>::store(M, j, m);
+      Vec8<T>::store(V, j, v);
+    }
+    return;
+  }
   const float inv_scale_div = grad_scale ? *grad_scale : 1.0f;
   for (int it = 0; it < kIters; ++it) {
-    const int64_t i0 = base + (int64_t(it) * kThreads + threadIdx.x) * kVec;
-    if (i0 >= n) break;
-    if (a.vec_ok[t] && i0 + kVec <= n) {
+    const int64_t j0 = i0 + it * kStride;
+    if (j0 >= n) break;
+    if (a.vec_ok[t] && j0 + kVec <= n) {
       float p[kVec], g[kVec], m[kVec], v[kVec], mx[kVec];
-      Vec8<T>::load(P, i0, p);
-      Vec8<T>::load(G, i0, g);
-      Vec8<T>::load(M, i0, m);
-      Vec8<T>::load(V, i0, v);
-      if (s.amsgrad) Vec8<T>::load(MX, i0, mx);
+      Vec8<T>::load(P, j0, p);
+      Vec8<T>::load(G, j0, g);
+      Vec8<T>::load(M, j0, m);
+      Vec8<T>::load(V, j0, v);
+      if (s.amsgrad) Vec8<T>::load(MX, j0, mx);
       if (grad_scale) {
 #pragma unroll
         for (int e = 0; e < kVec; ++e) g[e] = g[e] / inv_scale_div;
-        Vec8<T>::store(G, i0, g);
+        Vec8<T>::store(G, j0, g);
       }
 #pragma unroll
       for (int e = 0; e < kVec; ++e) adam_elem(p[e], g[e], m[e], v[e], mx[e], k, s);
-      Vec8<T>::store(P, i0, p);
-      Vec8<T>::store(M, i0, m);
-      Vec8<T>::store(V, i0, v);
-      if (s.amsgrad) Vec8<T>::store(MX, i0, mx);
+      Vec8<T>::store(P, j0, p);
+      Vec8<T>::store(M, j0, m);
+      Vec8<T>::store(V, j0, v);
+      if (s.amsgrad) Vec8<T>::store(MX, j0, mx);
     } else {
-      for (int64_t i = i0; i < i0 + kVec && i < n; ++i) {
+      for (int64_t i = j0; i < j0 + kVec && i < n; ++i) {
         float p = ld(P, i), g = ld(G, i), m = ld(M, i), v = ld(V, i);
         float mx = s.amsgrad ? ld(MX, i) : 0.0f;
         if (grad_scale) {

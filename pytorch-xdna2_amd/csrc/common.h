@@ -80,11 +80,12 @@ __host__ __device__ inline float bf16_to_f32(uint16_t h) {
 }
 
 // Round to nearest even; NaN -> quiet NaN 0x7FC0 (the c10::BFloat16 convention).
+// gfx950 converts with v_cvt_pk_bf16_f32, which rounds to nearest even exactly as
+// (u + 0x7FFF + lsb) >> 16 for every non-NaN input, subnormals included (checked over
+// all 2^32 patterns on an MI355X); it keeps a NaN's sign and payload, hence the select.
 __device__ inline uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t(0x7FC0);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  return f != f ? uint16_t(0x7FC0) : h;
 }
 
 }  // namespace xdna

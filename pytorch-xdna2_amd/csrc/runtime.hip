@@ -8,6 +8,7 @@
 #include "common.h"
 #include "../../include/xdna_hip.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -109,6 +110,13 @@ size_t round_size(size_t n) {
 }
 
 }  // namespace
+
+// out[i] = the bf16 rounding every kernel of the library applies to in[i].
+__global__ __launch_bounds__(256) void round_bf16_kernel(const float* __restrict__ in,
+                                                         uint16_t* __restrict__ out, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+    out[i] = f32_to_bf16(in[i]);
+}
 
 }  // namespace xdna
 
@@ -413,3 +421,14 @@ int xdna_hip_stream_wait_event(void* stream, void* event) {
 }
 
 }  // extern "C"
+
+extern "C" int xdna_round_bf16(const float* in, uint16_t* out, int64_t n, void* stream) {
+  if (n < 0 || (n > 0 && (!in || !out))) {
+    set_error("xdna_round_bf16: invalid arguments");
+    return -1;
+  }
+  if (n == 0) return 0;
+  if (!admit_launch("xdna_round_bf16")) return -1;
+  round_bf16_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 16384)), 256, 0, as_stream(stream)>>>(in, out, n);
+  return check_launch("xdna_round_bf16");
+}

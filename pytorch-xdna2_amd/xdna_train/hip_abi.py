@@ -43,6 +43,7 @@ SIGNATURES = {
     "xdna_hip_cache_pool_begin": (I, [L]),
     "xdna_hip_cache_pool_end": (I, []),
     "xdna_hip_cache_pool_release": (I, [L]),
+    "xdna_round_bf16": (I, [P, P, L, P]),
     "xdna_hip_memcpy_async": (I, [P, P, Z, I, P]),
     "xdna_hip_memset_async": (I, [P, I, Z, P]),
     "xdna_hip_stream_synchronize": (I, [P]),
