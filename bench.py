@@ -207,6 +207,34 @@ def cpu_conv_baseline(torch, budget_s=12.0):
     return flops / t_total / 1e12, reps, shapes
 
 
+CALIB_BYTES = 256 << 20     # plain device copy whose PMC byte counts calibrate FETCH/WRITE_SIZE
+TRAFFIC_FILE = REPO / "profiles" / "conv_sweep_hbm_traffic.json"
+
+
+def calibration_copy(torch, C):
+    """One D2D copy of CALIB_BYTES through the C ABI (hipMemcpyAsync's blit kernel): the
+    reference kernel of known size for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
+    from xdna_train import hip_abi
+    lib = hip_abi.load()
+    src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device="xdna")
+    dst = torch.empty_like(src)
+    rc = lib.xdna_hip_memcpy_async(C.data_ptr(dst), C.data_ptr(src), CALIB_BYTES, 3,
+                                   torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    sync(torch)
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary (two rocprofv3 --pmc
+    runs of this script over the sweep, FETCH_SIZE then WRITE_SIZE, each scaled by the
+    calibration copy's reading), or None."""
+    try:
+        d = json.loads(TRAFFIC_FILE.read_text())
+        return d["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def kernel_summary(report):
     out = {}
     for name, e in report.items():
@@ -245,6 +273,8 @@ def main() -> int:
     X = torch.device("xdna")
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    calibration_copy(torch, C)
+
     # --- headline: conv sweep --------------------------------------------------------
     shapes = SWEEP if not args.quick else [(16, 128, 36), (64, 256, 36)]
     log(f"conv sweep: {len(shapes)} shapes, building data")
@@ -276,7 +306,7 @@ def main() -> int:
     achieved = work / (tot[dom] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": None, "launches": launches,
+                "traffic": measured_traffic(dom) if not args.quick else None, "launches": launches,
                 "avg_launch_us": round(1e3 * tot[dom] / max(1, launches), 3),
                 "flop_per_launch_avg": work / max(1, launches)}
     per_dir = {}

@@ -83,8 +83,23 @@ struct RowsArgs {
   float* part;           // split-K: fp32 partial sums [nsplit][cout][m_pad], else null
   int chunks, cout, wp, H, W, S, So;
   int ch_per;            // input chunks per split (blockIdx.z)
+  int nrt, ncot;         // row tiles, channel tiles (blockIdx.x decodes to both)
   int64_t img, m_total, m_pad;
 };
+
+constexpr int kXcds = 8;  // MI355X: workgroups go round-robin to 8 XCDs, each with its own L2
+
+// blockIdx.x -> (row tile, channel tile).  Workgroup L runs on XCD L % 8; on each XCD the
+// consecutive workgroups take all channel tiles of one row tile, so a window read from
+// HBM once serves every channel tile from that XCD's L2 (row tile r lives on XCD r % 8;
+// nrt is padded to a multiple of 8 in the grid, padding workgroups exit).
+__device__ inline bool rows_tile(const RowsArgs& a, int& rt, int& ct) {
+  const int L = blockIdx.x;
+  const int x = L % kXcds, k = L / kXcds;
+  rt = (k / a.ncot) * kXcds + x;
+  ct = k % a.ncot;
+  return rt < a.nrt;
+}
 
 // One workgroup: 128 output channels x TP grid rows of one group; wave (wm, wn) owns
 // channels [wm*64, +64) x rows [wn*TP/2, +TP/2) (2 x TP/64 MFMA tiles).  Per input chunk
@@ -105,10 +120,12 @@ void conv_rows_kernel(RowsArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][kXRows * kPitch];
 
   constexpr int tiles_per_group = kGroupOutRows / TP;
-  const int g = blockIdx.x / tiles_per_group;
-  const int r0 = (blockIdx.x % tiles_per_group) * TP;
+  int rt, ct;
+  if (!rows_tile(a, rt, ct)) return;
+  const int g = rt / tiles_per_group;
+  const int r0 = (rt % tiles_per_group) * TP;
   if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;  // tail tile: no valid row
-  const int co0 = blockIdx.y * kTCo;
+  const int co0 = ct * kTCo;
   const int ch0 = blockIdx.z * a.ch_per;
   const int ch1 = min(a.chunks, ch0 + a.ch_per);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -294,10 +311,12 @@ void conv_small_kernel(RowsArgs a) {
   uint16_t* ws = smem + kXRows * kPitch;          // [kSCo][kSWPitch]
 
   constexpr int tiles_per_group = kGroupOutRows / TP;
-  const int g = blockIdx.x / tiles_per_group;
-  const int r0 = (blockIdx.x % tiles_per_group) * TP;
+  int rt, ct;
+  if (!rows_tile(a, rt, ct)) return;
+  const int g = rt / tiles_per_group;
+  const int r0 = (rt % tiles_per_group) * TP;
   if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;
-  const int co0 = blockIdx.y * kSCo;
+  const int co0 = ct * kSCo;
   const int ch0 = blockIdx.z * a.ch_per;
   const int ch1 = min(a.chunks, ch0 + a.ch_per);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -871,7 +890,9 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     const int64_t wg256 = int64_t(geom.groups) * (kGroupOutRows / 256) * ytiles;
     const int64_t wg128 = int64_t(geom.groups) * (kGroupOutRows / 128) * ytiles;
     const int TP = wg256 >= 384 ? 256 : wg128 >= 384 ? 128 : 64;
-    const dim3 grid(unsigned(int64_t(geom.groups) * (kGroupOutRows / TP)), ytiles, 1);
+    a.nrt = int(ceil_div(geom.m_total, TP));
+    a.ncot = int(ytiles);
+    const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
     if (TP == 256)
       conv_rows_kernel<256><<<grid, 256, 0, st>>>(a);
     else if (TP == 128)
@@ -908,7 +929,9 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     a.part = static_cast<float*>(xdna_hip_cache_alloc(pbytes));
     if (!a.part) return -1;
   }
-  const dim3 grid(unsigned(int64_t(geom.groups) * (kGroupOutRows / TP)), stiles, unsigned(nsplit));
+  a.nrt = int(ceil_div(geom.m_total, TP));
+  a.ncot = int(stiles);
+  const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, unsigned(nsplit));
   const size_t lds = size_t(TP + kMaxHalo) * kPitch * 2 + size_t(kSCo) * kSWPitch * 2;
   if (TP == 128)
     conv_small_kernel<128><<<grid, 256, lds, st>>>(a);
