@@ -560,6 +560,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   mod.def("set_device", [](int d) { TORCH_CHECK(d == 0, "xdna: only xdna:0 exists"); });
   mod.def("synchronize", [] { check_abi(xdna_hip_device_synchronize(), "synchronize"); });
   mod.def("empty_cache", [] {
+    clear_weight_cache();
     check_abi(xdna_hip_device_synchronize(), "synchronize");
     check_abi(xdna_hip_cache_empty(), "empty_cache");
   });

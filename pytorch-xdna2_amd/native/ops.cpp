@@ -85,6 +85,16 @@ WeightCache& weight_cache() {
   return *c;
 }
 
+}  // namespace
+
+void clear_weight_cache() {
+  WeightCache& c = weight_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.entries.clear();
+}
+
+namespace {
+
 bool weight_cacheable(const at::Tensor& w) {
   return !w.requires_grad() && !w.is_inference() && w.dim() == 4;
 }

@@ -59,6 +59,9 @@ struct ScopedCount {
 // Hot-path registrations (ops.cpp).
 void register_hot_ops(torch::Library& m);
 
+// Drops the prepared weights of frozen tensors (ops.cpp).
+void clear_weight_cache();
+
 // Weight-gradient launches so far (ops.cpp).
 int64_t dw_jobs();
 
