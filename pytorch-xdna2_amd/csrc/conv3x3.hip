@@ -289,6 +289,171 @@ void conv_rows_kernel(RowsArgs a) {
     }
 }
 
+// Wide variant for cout >= 256: 256 output channels x 256 grid rows per workgroup, 8 waves
+// (two per SIMD, so one wave's MFMAs run while the other waits).  Wave (wm, wn) owns
+// channels [wm*64, +64) x rows [wn*128, +128): 2 x 4 MFMA tiles per 16-wide k-step.
+// Both operands come from LDS: the chunk's halo window (single buffer, the next chunk's
+// window prefetched into registers over taps 0..6) and the weights of one (chunk, tap)
+// slab at a time in a 3-slot ring.  Slab T is loaded into registers at tap T-2 (16-byte
+// coalesced loads, 256 rows x 128 bytes), stored to slot T % 3 at the start of tap T-1
+// and read at tap T; a barrier opens every tap.  Fragments are read right before their
+// MFMAs: the other wave of the SIMD covers the LDS latency.  Needs prepared weights
+// padded to a multiple of 256 rows (fwd_plan pads so for cout > 128).
+constexpr int kWCo = 256;                              // output channels per workgroup
+constexpr int kWTp = 256;                              // grid rows per workgroup
+constexpr int kWXRows = kWTp + kMaxHalo;
+constexpr int kWSlot = kWCo * kPitch;                  // elements of one weight slot
+constexpr size_t kWideLds = size_t(kWXRows * kPitch + 3 * kWSlot) * 2;
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void conv_rows2_kernel(RowsArgs a) {
+  constexpr int kXv = (kWXRows * 8 + 511) / 512;       // window vectors per thread (6)
+  constexpr int kWv = kWCo * 8 / 512;                  // weight vectors per thread per slab (4)
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs = smem;                                 // [kWXRows][kPitch]
+  uint16_t* wsl = smem + kWXRows * kPitch;             // [3][kWCo][kPitch]
+
+  constexpr int tiles_per_group = kGroupOutRows / kWTp;
+  int rt, ct;
+  if (!rows_tile(a, rt, ct)) return;
+  const int g = rt / tiles_per_group;
+  const int r0 = (rt % tiles_per_group) * kWTp;
+  if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;
+  const int co0 = ct * kWCo;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int K = a.chunks * 9 * kKStep;
+  const int nvec = (kWTp + 2 * a.wp + 2) * 8;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  const int T0 = 0, T1 = a.chunks * 9;
+
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    f32x16_t init = zero_acc();
+    if (a.bias) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
+        init[i] = co < a.cout ? bf16_to_f32(a.bias[co]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[m][n] = init;
+  }
+
+  // weight slab T: rows co0 .. co0+255, k = [T*64, T*64+64); vector v = row v/8, piece v%8
+  const uint16_t* wbase = a.wt + int64_t(co0) * K;
+  u32x4_t wreg[kWv];
+  u32x4_t xr[kXv];
+#define XDNA_W2_LOAD(T_)                                                                     \
+  do {                                                                                       \
+    _Pragma("unroll") for (int j = 0; j < kWv; ++j) {                                        \
+      const int v = tid + j * 512;                                                           \
+      wreg[j] = *reinterpret_cast<const u32x4_t*>(wbase + int64_t(v >> 3) * K + (T_) * kKStep + (v & 7) * 8); \
+    }                                                                                        \
+  } while (0)
+#define XDNA_W2_STORE(slot_)                                                                 \
+  do {                                                                                       \
+    _Pragma("unroll") for (int j = 0; j < kWv; ++j) {                                        \
+      const int v = tid + j * 512;                                                           \
+      *reinterpret_cast<u32x4_t*>(&wsl[(slot_) * kWSlot + (v >> 3) * kPitch + (v & 7) * 8]) = wreg[j]; \
+    }                                                                                        \
+  } while (0)
+#define XDNA_X2_LOAD(ch_, part_)                                                             \
+  do {                                                                                       \
+    const uint16_t* src_ = a.xp + ((int64_t(g) * a.chunks + (ch_)) * kGroupRows + r0) * kKStep; \
+    _Pragma("unroll") for (int j = 0; j < kXv; ++j) {                                        \
+      const int i = tid + j * 512;                                                           \
+      if (((part_) < 0 || j * 7 / kXv == (part_)) && i < nvec)                               \
+        xr[j] = *reinterpret_cast<const u32x4_t*>(src_ + (i >> 3) * kKStep + (i & 7) * 8);   \
+    }                                                                                        \
+  } while (0)
+#define XDNA_X2_STORE()                                                                      \
+  do {                                                                                       \
+    _Pragma("unroll") for (int j = 0; j < kXv; ++j) {                                        \
+      const int i = tid + j * 512;                                                           \
+      if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[(i >> 3) * kPitch + (i & 7) * 8]) = xr[j]; \
+    }                                                                                        \
+  } while (0)
+
+  // prologue: slab 0 to slot 0, slab 1 in registers, window of chunk 0 in LDS
+  XDNA_W2_LOAD(T0);
+  XDNA_X2_LOAD(0, -1);
+  XDNA_W2_STORE(0);
+  XDNA_X2_STORE();
+  if (T0 + 1 < T1) XDNA_W2_LOAD(T0 + 1);
+
+  const uint16_t* xb = xs + (wn * 128 + lr) * kPitch + lk;
+  for (int ch = 0; ch < a.chunks; ++ch) {
+    const bool more = ch + 1 < a.chunks;
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+      const int T = ch * 9 + tap;
+      __syncthreads();  // tap T-1 done everywhere; slot T % 3 and the window are visible
+      // slab T+1 (in registers since tap T-1) to its slot (last read at tap T-2), then
+      // slab T+2 into the registers
+      if (T + 1 < T1) XDNA_W2_STORE((T + 1) % 3);
+      if (T + 2 < T1) XDNA_W2_LOAD(T + 2);
+      if (tap < 7 && more) XDNA_X2_LOAD(ch + 1, tap);
+      const uint16_t* wa = wsl + (T % 3) * kWSlot + (wm * 64 + lr) * kPitch + lk;
+      const int toff = ((tap / 3) * a.wp + (tap % 3)) * kPitch;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4_t aq[2], bq[4];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) aq[m] = *reinterpret_cast<const u32x4_t*>(wa + m * 32 * kPitch + ks * 16);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) bq[n] = *reinterpret_cast<const u32x4_t*>(xb + toff + n * 32 * kPitch + ks * 16);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const bf16x8_t bfr = as_bf16x8(bq[n]);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) acc[m][n] = mfma_32x32x16(as_bf16x8(aq[m]), bfr, acc[m][n]);
+        }
+      }
+    }
+    if (more) {
+      __syncthreads();  // every wave is done reading this chunk's window
+      XDNA_X2_STORE();
+    }
+  }
+#undef XDNA_W2_LOAD
+#undef XDNA_W2_STORE
+#undef XDNA_X2_LOAD
+#undef XDNA_X2_STORE
+
+  const int first = a.S == 1 ? 0 : 1;
+  const int64_t plane = int64_t(a.H) * a.W;
+  uint16_t* obase[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    obase[n] = nullptr;
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * 128 + n * 32 + lr;
+    if (p >= a.m_total) continue;
+    const int64_t vb = p / a.img;
+    const int64_t rem = p - vb * a.img;
+    const int y = int(rem / a.wp);
+    const int col = int(rem - int64_t(y) * a.wp) - first;
+    if (y >= a.H || col < 0) continue;
+    const int b = int(vb / a.S), s = int(vb % a.S);
+    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+    if (col >= cols) continue;
+    const int x = (a.S == 1 ? 0 : s * a.So) + col;
+    obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 64 + m * 32 + mfma_row(i, lane);
+      if (co >= a.cout) continue;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
+    }
+}
+
 // Small-grid variant: 64 output channels x TP grid rows per workgroup.  Per input chunk
 // the halo window AND all nine taps of the workgroup's weights (64 x 576 bf16, 72 KiB)
 // are staged in LDS with every load of the chunk in flight at once, so a chunk costs one
@@ -825,7 +990,8 @@ FwdPlan fwd_plan(int B, int Cin, int Cout, int H, int W) {
   FwdPlan p;
   p.geom = conv_geom(B, H, W);
   p.chunks = int(ceil_div(Cin, kKStep));
-  p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
+  // 128-row channel tiles; beyond 128 channels, a multiple of 256 for the wide kernel
+  p.co_pad = Cout <= kTCo ? kTCo : int(ceil_div(Cout, kWCo) * kWCo);
   p.packed_bytes = align256(size_t(p.geom.groups) * p.chunks * kGroupRows * kKStep * 2);
   p.wt_bytes = align256(size_t(p.co_pad) * p.chunks * 9 * kKStep * 2);
   return p;
@@ -884,6 +1050,23 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
   const int64_t big128 = ceil_div(geom.m_total, 128) * ytiles;
   const bool small = variant == 2 || variant == 3 || (variant == 0 && big128 < 512);
+  // the wide kernel: 256-channel tiles (cout > 128 only: the weights are padded to 256
+  // rows from there on)
+  const bool wide = cout > kTCo && (variant == 4 || (variant == 0 && !small && cout >= kWCo));
+  if (wide) {
+    static const bool lds_wide = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows2_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     int(kWideLds)) == hipSuccess;
+    if (!lds_wide) {
+      set_error("conv3x3 rows: cannot enable the wide kernel's LDS size");
+      return -1;
+    }
+    a.nrt = int(ceil_div(geom.m_total, kWTp));
+    a.ncot = int(ceil_div(cout, kWCo));
+    const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
+    conv_rows2_kernel<<<grid, 512, kWideLds, st>>>(a);
+    return check_launch("conv3x3 rows");
+  }
   if (!small) {
     // Tile rows per workgroup: the largest of 256 / 128 / 64 that still puts a few
     // hundred workgroups on the 256 CUs.
@@ -959,7 +1142,8 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
   WgradPlan p;
   p.cm = cm_geom(B, H, W);
   p.ci_pad = int(ceil_div(Cin, 64) * 64);
-  p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
+  // 128-row channel tiles; beyond 128 channels, a multiple of 256 for the wide kernel
+  p.co_pad = Cout <= kTCo ? kTCo : int(ceil_div(Cout, kWCo) * kWCo);
   const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
   const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
   // Split-K: pick the split count s that minimizes a simple model of the two kernels,
@@ -1177,8 +1361,8 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {
-  if (variant < 0 || variant > 3) {
-    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..3");
+  if (variant < 0 || variant > 4) {
+    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..4");
     return -1;
   }
   g_rows_variant.store(variant);

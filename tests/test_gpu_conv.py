@@ -28,6 +28,7 @@ SHAPES = [
     (1, 128, 256, 18, 72),
     (2, 256, 64, 5, 37),
     (1, 1, 1, 1, 1),
+    (1, 64, 384, 6, 40),    # 384 output channels: a partial 256-channel tile
 ]
 
 
@@ -46,8 +47,9 @@ def _ws(nbytes):
 
 
 # rows-kernel variants (xdna_conv3x3_set_rows_variant): main kernel, small-grid kernel
-# with 64- and 128-row tiles (split-K over chunks where the grid is small)
-VARIANTS = [1, 2, 3]
+# with 64- and 128-row tiles (split-K over chunks where the grid is small), wide kernel
+# (256-channel tiles, for cout > 128; the main kernel otherwise)
+VARIANTS = [1, 2, 3, 4]
 
 
 @pytest.fixture
