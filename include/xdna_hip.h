@@ -270,6 +270,13 @@ int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uin
                    int bias_mode, int64_t bias_sm, int64_t bias_sn,
                    float alpha, float beta, void* stream);
 
+/* Kernel selection of xdna_gemm_bf16, for measurements and tests: 0 automatic (default),
+ * 1 the 128 x 128 kernel (any strides, split-K for few long-K tiles), 2 the 256 x 256
+ * kernel (8 waves; operands with a unit stride along k or along rows only, else 1 is
+ * used).  No reference counterpart (a tuning knob).  XDNA_GEMM_VARIANT sets the initial
+ * value. */
+int xdna_gemm_set_variant(int variant);
+
 /* ------------------------------------------------------------------------ */
 /* Fused Adam / AdamW: replaces torch._fused_adam_ reached through the        */
 /* boxed CPU fallback (xdna_cpu_fallback, torch_xdna_device.cpp:5273-5295;    */

@@ -13,6 +13,8 @@
 #include "mfma.h"
 
 #include <algorithm>
+#include <atomic>
+#include <cstdlib>
 #include "../../include/xdna_hip.h"
 
 namespace xdna {
@@ -176,6 +178,183 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Large-tile variant: 256 x 256 output tile, k-tile 64, 8 waves (two per SIMD); wave
+// (wm, wn) owns rows [wm*128, +128) x columns [wn*64, +64) (4 x 2 MFMA tiles).  Both
+// operands are staged k-contiguous in LDS ([256][72] each, double-buffered, 144 KiB);
+// the next k-tile is loaded into registers while the current one is multiplied.
+// An operand whose rows are contiguous (kAlongRow: A = dY^T, B = W in dX) is read as
+// 4 (k) x 8 (rows) blocks with 16-byte loads and transposed in registers (v_perm) into
+// 8-byte LDS writes.
+// ---------------------------------------------------------------------------------------
+constexpr int kT2 = 256, kK2 = 64, kP2 = 72;
+constexpr size_t kGemm2Lds = size_t(2) * 2 * kT2 * kP2 * 2;  // 2 buffers x (A, B)
+
+typedef unsigned int g2u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int g2u2 __attribute__((ext_vector_type(2)));
+
+// Registers of one operand's k-tile: 4 x 16 bytes per thread.
+template <int kMode>
+__device__ inline void g2_load(g2u4 (&r)[4], const uint16_t* src, int64_t s_r, int64_t s_k, int r0,
+                               int rows, int k0, int K, int tid) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (kMode == kAlongK) {
+      // vector v: row v / 8, k [k0 + (v % 8) * 8, +8)
+      const int v = tid + j * 512;
+      const int row = v >> 3, k = k0 + (v & 7) * 8;
+      const int rr = r0 + row;
+      g2u4 x = {0u, 0u, 0u, 0u};
+      if (rr < rows) {
+        const uint16_t* p = src + int64_t(rr) * s_r + k;
+        if (k + 8 <= K) {
+          x = *reinterpret_cast<const g2u4*>(p);
+        } else {
+          for (int e = 0; e < 8; ++e)
+            if (k + e < K) x[e >> 1] |= uint32_t(p[e]) << ((e & 1) * 16);
+        }
+      }
+      r[j] = x;
+    } else {
+      // thread t: rows [r0 + (t % 32) * 8, +8), k = k0 + (t / 32) * 4 + j (one 16-byte row run)
+      const int rg = tid & 31, k = k0 + (tid >> 5) * 4 + j;
+      const int rr = r0 + rg * 8;
+      g2u4 x = {0u, 0u, 0u, 0u};
+      if (k < K) {
+        const uint16_t* p = src + int64_t(k) * s_k + rr;
+        if (rr + 8 <= rows) {
+          x = *reinterpret_cast<const g2u4*>(p);
+        } else {
+          for (int e = 0; e < 8; ++e)
+            if (rr + e < rows) x[e >> 1] |= uint32_t(p[e]) << ((e & 1) * 16);
+        }
+      }
+      r[j] = x;
+    }
+  }
+}
+
+template <int kMode>
+__device__ inline void g2_store(uint16_t* lds, const g2u4 (&r)[4], int tid) {
+  if (kMode == kAlongK) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int v = tid + j * 512;
+      *reinterpret_cast<g2u4*>(lds + (v >> 3) * kP2 + (v & 7) * 8) = r[j];
+    }
+  } else {
+    // r[j] holds rows rg*8 .. +7 at k = kq*4 + j; row e gets (k0..k3) as two dwords
+    const int rg = tid & 31, kq = tid >> 5;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high / low halves
+      g2u2 w;
+      w[0] = __builtin_amdgcn_perm(r[1][e >> 1], r[0][e >> 1], sel);
+      w[1] = __builtin_amdgcn_perm(r[3][e >> 1], r[2][e >> 1], sel);
+      *reinterpret_cast<g2u2*>(lds + (rg * 8 + e) * kP2 + kq * 4) = w;
+    }
+  }
+}
+
+template <int kModeA, int kModeB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm2_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kT2, n0 = blockIdx.x * kT2;
+  const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
+  const int kbeg = split * g.kt_per * kK2, kend = min(g.K, kbeg + g.kt_per * kK2);
+  const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
+  const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero_acc();
+
+  g2u4 ra[4], rb[4];
+  if (kbeg < kend) {
+    g2_load<kModeA>(ra, A, g.a_r, g.a_k, m0, g.M, kbeg, kend, tid);
+    g2_load<kModeB>(rb, B, g.b_r, g.b_k, n0, g.N, kbeg, kend, tid);
+    g2_store<kModeA>(smem, ra, tid);
+    g2_store<kModeB>(smem + kT2 * kP2, rb, tid);
+  }
+  __syncthreads();
+  int cur = 0;
+  for (int k0 = kbeg; k0 < kend; k0 += kK2) {
+    const bool more = k0 + kK2 < kend;
+    if (more) {
+      g2_load<kModeA>(ra, A, g.a_r, g.a_k, m0, g.M, k0 + kK2, kend, tid);
+      g2_load<kModeB>(rb, B, g.b_r, g.b_k, n0, g.N, k0 + kK2, kend, tid);
+    }
+    const uint16_t* as = smem + cur * 2 * kT2 * kP2;
+    const uint16_t* bs = as + kT2 * kP2;
+#pragma unroll
+    for (int ks = 0; ks < kK2 / 16; ++ks) {
+      bf16x8_t af[4], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(as + (wm * 128 + i * 32 + lr) * kP2 + ks * 16 + lk));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bfr[j] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(bs + (wn * 64 + j * 32 + lr) * kP2 + ks * 16 + lk));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_32x32x16(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      uint16_t* nxt = smem + (cur ^ 1) * 2 * kT2 * kP2;
+      g2_store<kModeA>(nxt, ra, tid);
+      g2_store<kModeB>(nxt + kT2 * kP2, rb, tid);
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+
+  if (g.part) {
+    float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + lr;
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 128 + i * 32 + mfma_row(r, lane);
+          if (m < g.M) P[int64_t(m) * g.N + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
+  uint16_t* C = g.c + int64_t(batch) * g.c_batch;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 64 + j * 32 + lr;
+      if (n >= g.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 128 + i * 32 + mfma_row(r, lane);
+        if (m >= g.M) continue;
+        float v = g.alpha * acc[i][j][r];
+        if (g.bias_mode && g.beta != 0.0f) {
+          float bv;
+          if (g.bias_mode == 1) bv = bf16_to_f32(g.bias[int64_t(n) * g.bias_sn]);
+          else if (g.bias_mode == 2) bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm + int64_t(n) * g.bias_sn]);
+          else bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm]);
+          v += g.beta * bv;
+        }
+        C[int64_t(m) * g.c_m + int64_t(n) * g.c_n] = f32_to_bf16(v);
+      }
+    }
+}
+
 // Split-K epilogue: C[b][m][n] = bf16(alpha * sum over splits (in split order) of the fp32
 // partials + beta * bias term), consecutive threads on consecutive n.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs g) {
@@ -207,6 +386,26 @@ int stage_mode(const void* base, int64_t s_r, int64_t s_k, int64_t s_batch, int 
   if (s_r == 1 && a16 && (s_k % 8) == 0 && batch_ok) return kAlongRow;
   return kScalar;
 }
+
+template <int MA, int MB>
+bool gemm2_lds_ok() {
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm2_kernel<MA, MB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(kGemm2Lds)) == hipSuccess;
+  return ok;
+}
+
+template <int MA, int MB>
+bool launch2(dim3 grid, hipStream_t st, const GemmArgs& g) {
+  if (!gemm2_lds_ok<MA, MB>()) return false;
+  gemm2_kernel<MA, MB><<<grid, 512, kGemm2Lds, st>>>(g);
+  return true;
+}
+
+std::atomic<int> g_gemm_variant{[] {
+  const char* e = std::getenv("XDNA_GEMM_VARIANT");
+  return e ? std::atoi(e) : 0;
+}()};
 
 template <int MA>
 void launch_b(int mb, dim3 grid, hipStream_t st, const GemmArgs& g) {
@@ -262,6 +461,46 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   const int mb = stage_mode(Bm, ldb_n, ldb_k, stride_b, batch);
   if (!admit_launch("xdna_gemm_bf16")) return -1;
   g.batch = batch;
+  hipStream_t st2 = as_stream(stream);
+  // Large tiles (256 x 256, 8 waves) when neither operand needs scalar staging and the
+  // grid still has enough tiles; xdna_gemm_set_variant overrides (1 small, 2 large).
+  const int variant = g_gemm_variant.load();
+  const int64_t tiles2 = ceil_div(N, kT2) * ceil_div(M, kT2) * int64_t(batch);
+  const bool vec_ok = ma != kScalar && mb != kScalar;
+  if (vec_ok && K > 0 && (variant == 2 || (variant == 0 && tiles2 >= 64))) {
+    // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
+    const int kt2 = int(ceil_div(K, kK2));
+    g.nsplit = 1;
+    g.kt_per = std::max(kt2, 1);
+    g.part = nullptr;
+    if (tiles2 < 256 && kt2 >= 8) {
+      int sp = int(std::min<int64_t>(kt2 / 4, ceil_div(256, tiles2)));
+      sp = std::max(1, std::min(sp, 65535 / std::max(batch, 1)));
+      g.kt_per = int(ceil_div(kt2, sp));
+      g.nsplit = int(ceil_div(kt2, g.kt_per));
+    }
+    if (g.nsplit > 1) {
+      g.part = static_cast<float*>(
+          xdna_hip_cache_alloc(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float)));
+      if (!g.part) return -1;
+    }
+    const dim3 grid2(unsigned(ceil_div(N, kT2)), unsigned(ceil_div(M, kT2)), unsigned(batch * g.nsplit));
+    bool ok;
+    if (ma == kAlongK) ok = mb == kAlongK ? launch2<kAlongK, kAlongK>(grid2, st2, g) : launch2<kAlongK, kAlongRow>(grid2, st2, g);
+    else ok = mb == kAlongK ? launch2<kAlongRow, kAlongK>(grid2, st2, g) : launch2<kAlongRow, kAlongRow>(grid2, st2, g);
+    if (!ok) {
+      if (g.part) xdna_hip_cache_free(g.part);
+      set_error("xdna_gemm_bf16: cannot enable the large-tile kernel's LDS size");
+      return -1;
+    }
+    if (g.nsplit > 1) {
+      const int64_t n_all = int64_t(batch) * M * N;
+      gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st2>>>(g);
+      // stream-ordered reuse: the next user of the block runs after the reduce
+      xdna_hip_cache_free(g.part);
+    }
+    return check_launch("xdna_gemm_bf16");
+  }
   // Few output tiles and a long K (Gram matrices: [C x HW] x [HW x C]): split K over
   // blockIdx.z so the grid covers the CUs; fp32 partials are summed in split order.
   const int64_t tiles = ceil_div(N, kTN) * ceil_div(M, kTM) * int64_t(batch);
@@ -292,4 +531,13 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
     xdna_hip_cache_free(g.part);
   }
   return check_launch("xdna_gemm_bf16");
+}
+
+extern "C" int xdna_gemm_set_variant(int variant) {
+  if (variant < 0 || variant > 2) {
+    set_error("xdna_gemm_set_variant: variant must be 0..2");
+    return -1;
+  }
+  g_gemm_variant.store(variant);
+  return 0;
 }

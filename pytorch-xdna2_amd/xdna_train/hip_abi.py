@@ -77,6 +77,7 @@ SIGNATURES = {
     "xdna_conv3x3_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
+    "xdna_gemm_set_variant": (I, [I]),
     "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_batch_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, P]),
     "xdna_batch_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),

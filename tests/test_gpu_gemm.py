@@ -29,11 +29,20 @@ def _run(hip, a_t, b_t, M, N, K, a_s, b_s, bias=None, bias_mode=0, bias_s=(0, 0)
     return host(c)
 
 
+@pytest.fixture
+def variant(hip, request):
+    assert hip.xdna_gemm_set_variant(request.param) == 0
+    yield request.param
+    assert hip.xdna_gemm_set_variant(0) == 0
+
+
+# kernel variants (xdna_gemm_set_variant): 128 x 128 tiles, 256 x 256 tiles
+@pytest.mark.parametrize("variant", [1, 2], indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("M,N,K", [(256, 384, 512), (130, 70, 33), (1, 1, 1), (64, 257, 8),
-                                   (300, 128, 1000)])
+                                   (300, 128, 1000), (520, 264, 136)])
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn", "tt"])
-def test_layouts(hip, M, N, K, layout):
-    print(f"gemm {layout} {M}x{N}x{K}", flush=True)
+def test_layouts(hip, M, N, K, layout, variant):
+    print(f"gemm {layout} {M}x{N}x{K} variant {variant}", flush=True)
     rng = np.random.default_rng(M + N + K)
     a = _mat(rng, M, K)
     b = _mat(rng, K, N)
@@ -78,8 +87,9 @@ def test_k_zero_gives_beta_bias(hip):
     np.testing.assert_array_equal(oracle.bf16_value(host(c)), np.broadcast_to(2 * oracle.bf16_value(bias), (M, N)))
 
 
+@pytest.mark.parametrize("variant", [1, 2], indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("mode", [1, 2, 3])
-def test_bias_modes_alpha_beta(hip, mode):
+def test_bias_modes_alpha_beta(hip, mode, variant):
     rng = np.random.default_rng(3 + mode)
     M, N, K = 96, 160, 64
     a, b = _mat(rng, M, K), _mat(rng, K, N)
@@ -96,7 +106,8 @@ def test_bias_modes_alpha_beta(hip, mode):
     check_bf16(got, ref, what=f"bias mode {mode}")
 
 
-def test_batched(hip):
+@pytest.mark.parametrize("variant", [1, 2], indirect=True, ids=lambda v: f"v{v}")
+def test_batched(hip, variant):
     rng = np.random.default_rng(5)
     Bt, M, N, K = 6, 40, 72, 96
     a = oracle.rng_bf16(rng, (Bt, M, K))
@@ -111,7 +122,8 @@ def test_batched(hip):
     check_bf16(got_g, ref_g, what="gram")
 
 
-def test_mlp_shape(hip):
+@pytest.mark.parametrize("variant", [1, 2], indirect=True, ids=lambda v: f"v{v}")
+def test_mlp_shape(hip, variant):
     """One of config 3's GEMMs (x [8192,1024] . W^T [1024,4096]) on a row subset."""
     rng = np.random.default_rng(6)
     M, N, K = 512, 4096, 1024
