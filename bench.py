@@ -15,6 +15,8 @@ Also reported, from the same run:
   relu4_1, content + Gram style loss, B40 36x36, Adam) in it/s, beside the same step on
   the host CPU in bf16 (the reference's CPU BF16 path: stock PyTorch CPU kernels);
 * "adam": fused Adam over config 3's 25,175,040 bf16 parameters (14 B/param), GB/s;
+* "mlp": config 3's training step (Linear 1024->4096->4096->1024 with GELU, x [8192,1024],
+  MSE, Adam): ms/step and its 1168.2 GFLOP of GEMM per step as TFLOP/s;
 * "kernels": per-kernel launches / time / achieved rate from HIP events recorded on the
   launch stream around every hot-kernel launch of the timed region;
 * "roofline": the dominant kernel of the timed region against the MI355X dense bf16
@@ -255,6 +257,8 @@ def main() -> int:
     ap.add_argument("--style-steps", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-style", action="store_true")
+    ap.add_argument("--skip-mlp", action="store_true")
+    ap.add_argument("--mlp-steps", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="small subset (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -357,6 +361,50 @@ def main() -> int:
                           "avg_launch_us": round(1e3 * ar["total_ms"] / ar["launches"], 2)}
         log(f"adam: {gbs:.0f} GB/s")
     del params, opt
+
+    # --- MLP training step (config 3): mm / addmm fwd + both backward GEMMs + Adam -------
+    if not args.skip_mlp:
+        log("mlp: building")
+        torch.manual_seed(0)
+        mlp = torch.nn.Sequential(torch.nn.Linear(1024, 4096), torch.nn.GELU(), torch.nn.Linear(4096, 4096),
+                                  torch.nn.GELU(), torch.nn.Linear(4096, 1024)).bfloat16().to(X)
+        gm = torch.Generator().manual_seed(1)
+        xm = torch.randn(8192, 1024, generator=gm).bfloat16().to(X)
+        tm = torch.randn(8192, 1024, generator=gm).bfloat16().to(X)
+        mopt = torch.optim.Adam(mlp.parameters(), lr=1e-3, fused=True)
+
+        def mlp_step():
+            mopt.zero_grad(set_to_none=True)
+            loss = torch.nn.functional.mse_loss(mlp(xm).float(), tm.float())
+            loss.backward()
+            mopt.step()
+            return loss
+
+        for _ in range(3):
+            mlp_step()
+        sync(torch)
+        C.kernel_timing(True)
+        t0 = time.perf_counter()
+        for _ in range(args.mlp_steps):
+            mloss = mlp_step()
+        sync(torch)
+        dtm = time.perf_counter() - t0
+        mrep = dict(C.kernel_timing_report())
+        C.kernel_timing(False)
+        # fwd 3 GEMMs + dW 3 + dX 2 (the input needs no gradient): 2*T*(sum of in*out) each
+        gemm_flop = 2.0 * 8192 * (1024 * 4096 + 4096 * 4096 + 4096 * 1024) * 3 - 2.0 * 8192 * 1024 * 4096
+        ge = mrep.get("gemm", {})
+        result["mlp"] = {
+            "steps": args.mlp_steps, "ms_per_step": round(1e3 * dtm / args.mlp_steps, 3),
+            "step_gemm_tflops": round(gemm_flop * args.mlp_steps / dtm / 1e12, 1),
+            "gemm_kernel_tflops": round(ge["work"] / (ge["total_ms"] * 1e-3) / 1e12, 1) if ge else None,
+            "gemm_launches_per_step": ge.get("launches", 0) // max(1, args.mlp_steps),
+            "loss": float(mloss.item()),
+            "workload": "BASELINE config 3: Linear 1024->4096->4096->1024, GELU, bias, x [8192,1024], MSE, Adam; "
+                        "step_gemm_tflops = 1168.2 GFLOP of GEMM per step / wall time of the whole step",
+        }
+        log(f"mlp: {result['mlp']['ms_per_step']} ms/step, {result['mlp']['step_gemm_tflops']} TFLOP/s")
+        del mlp, mopt, xm, tm
 
     # --- style step (config 4) ---------------------------------------------------------
     if not args.skip_style:
