@@ -1049,7 +1049,8 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   const int variant = g_rows_variant.load();
   const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
   const int64_t big128 = ceil_div(geom.m_total, 128) * ytiles;
-  const bool small = variant == 2 || variant == 3 || (variant == 0 && big128 < 512);
+  // 64 or fewer output channels: the small-grid kernel's 64-channel tiles waste no MFMA work
+  const bool small = variant == 2 || variant == 3 || (variant == 0 && (big128 < 512 || cout <= kSCo));
   // the wide kernel: 256-channel tiles (cout > 128 only: the weights are padded to 256
   // rows from there on)
   const bool wide = cout > kTCo && (variant == 4 || (variant == 0 && !small && cout >= kWCo));
@@ -1097,7 +1098,8 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     return -1;
   }
   const unsigned stiles = unsigned(ceil_div(cout, kSCo));
-  const int TP = variant == 2 ? 64 : variant == 3 ? 128 : (ceil_div(geom.m_total, 128) * stiles >= 256 ? 128 : 64);
+  const int64_t tp128_min = cout <= kSCo ? 128 : 256;  // measured on the sweep shapes
+  const int TP = variant == 2 ? 64 : variant == 3 ? 128 : (ceil_div(geom.m_total, 128) * stiles >= tp128_min ? 128 : 64);
   const int64_t valid = ceil_div(geom.m_total, TP) * stiles;
   // Fewer workgroups than CUs: split the input chunks over blockIdx.z and sum the fp32
   // partials in a second pass (in split order).
