@@ -659,21 +659,37 @@ CmGeom cm_geom(int B, int H, int W) {
 // the tail of every row past the last image.
 constexpr int kCmLdsElems = 8192;  // 16 KiB of staged source rows
 
-__global__ __launch_bounds__(256) void pack_cm_kernel(const uint16_t* __restrict__ src,
-                                                      uint16_t* __restrict__ dst, int B, int C,
-                                                      int H, int W, int c_pad, int wp8,
-                                                      int64_t img, int64_t qlen, int shift,
-                                                      int rows_per, int rblocks, int planes_per,
-                                                      int64_t nmain) {
+// One operand of the channel-major pack (x with shift 1, or dY with shift 0).
+struct CmOp {
+  const uint16_t* src;
+  uint16_t* dst;
+  int C, c_pad, shift, rows_per, rblocks, planes_per;
+  int64_t nmain, blocks;  // workgroups [0, nmain) pack planes, [nmain, blocks) zero-fill
+};
+struct CmArgs {
+  CmOp op[2];
+  int B, H, W, wp8;
+  int64_t img, qlen;
+};
+
+__global__ __launch_bounds__(256) void pack_cm_kernel(CmArgs ca) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[kCmLdsElems + 16];
-  const int64_t bid = blockIdx.x;
+  int64_t bid = blockIdx.x;
+  const int which = bid < ca.op[0].blocks ? 0 : 1;
+  if (which) bid -= ca.op[0].blocks;
+  const CmOp& op = ca.op[which];
+  const uint16_t* __restrict__ src = op.src;
+  uint16_t* __restrict__ dst = op.dst;
+  const int B = ca.B, C = op.C, H = ca.H, W = ca.W, c_pad = op.c_pad, wp8 = ca.wp8, shift = op.shift;
+  const int rows_per = op.rows_per, rblocks = op.rblocks, planes_per = op.planes_per;
+  const int64_t img = ca.img, qlen = ca.qlen, nmain = op.nmain;
   const int64_t tail0 = int64_t(B) * img;  // first q past the last image
   if (bid >= nmain) {
     // zero fill: rows c < C from tail0 (a multiple of 8), rows c >= C whole
     const int64_t tvec = (qlen - tail0) / 8, rvec = qlen / 8;
     const int64_t n = int64_t(C) * tvec + int64_t(c_pad - C) * rvec;
     const uint4 z = make_uint4(0, 0, 0, 0);
-    for (int64_t i = (bid - nmain) * 256 + threadIdx.x; i < n; i += (int64_t(gridDim.x) - nmain) * 256) {
+    for (int64_t i = (bid - nmain) * 256 + threadIdx.x; i < n; i += (op.blocks - nmain) * 256) {
       int64_t o;
       if (i < int64_t(C) * tvec) {
         const int64_t c = i / tvec;
@@ -742,27 +758,47 @@ __global__ __launch_bounds__(256) void pack_cm_kernel(const uint16_t* __restrict
   }
 }
 
-// Launches pack_cm_kernel for one operand.
-int pack_cm_launch(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W, int c_pad,
-                   const CmGeom& cm, int shift, hipStream_t st) {
+// Plans one operand of pack_cm_kernel.
+CmOp pack_cm_plan(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W, int c_pad,
+                  const CmGeom& cm, int shift) {
   // grid rows per workgroup: the source run (rows_per rows of W, plus alignment lead)
   // must fit the LDS buffer; small planes are batched while the grid stays large
-  const int rows_per = std::max(1, std::min(H + 2, (kCmLdsElems - 8) / std::max(W, 1)));
-  const int rblocks = int(ceil_div(H + 2, rows_per));
+  CmOp o;
+  o.src = src;
+  o.dst = dst;
+  o.C = C;
+  o.c_pad = c_pad;
+  o.shift = shift;
+  o.rows_per = std::max(1, std::min(H + 2, (kCmLdsElems - 8) / std::max(W, 1)));
+  o.rblocks = int(ceil_div(H + 2, o.rows_per));
   const int64_t planes = int64_t(B) * C;
-  int planes_per = 1;
-  if (rblocks == 1)
-    planes_per = int(std::max<int64_t>(1, std::min<int64_t>((kCmLdsElems - 8) / (int64_t(H) * W), planes / 2048)));
-  const int64_t nmain = ceil_div(planes, planes_per) * rblocks;
+  o.planes_per = 1;
+  if (o.rblocks == 1)
+    o.planes_per = int(std::max<int64_t>(1, std::min<int64_t>((kCmLdsElems - 8) / (int64_t(H) * W), planes / 2048)));
+  o.nmain = ceil_div(planes, o.planes_per) * o.rblocks;
   const int64_t nzero = int64_t(C) * ((cm.q - int64_t(B) * cm.img) / 8) + int64_t(c_pad - C) * (cm.q / 8);
-  const int64_t zblocks = std::min<int64_t>(std::max<int64_t>(ceil_div(nzero, 256 * 4), 1), 4096);
-  const int64_t blocks = nmain + zblocks;
+  o.blocks = o.nmain + std::min<int64_t>(std::max<int64_t>(ceil_div(nzero, 256 * 4), 1), 4096);
+  return o;
+}
+
+// Packs x (shift 1) and dY (shift 0) in one launch.
+int pack_cm_launch2(const uint16_t* x, uint16_t* xt, int Cin, int ci_pad, const uint16_t* dy, uint16_t* dt,
+                    int Cout, int co_pad, int B, int H, int W, const CmGeom& cm, hipStream_t st) {
+  CmArgs ca;
+  ca.op[0] = pack_cm_plan(x, xt, B, Cin, H, W, ci_pad, cm, 1);
+  ca.op[1] = pack_cm_plan(dy, dt, B, Cout, H, W, co_pad, cm, 0);
+  ca.B = B;
+  ca.H = H;
+  ca.W = W;
+  ca.wp8 = cm.wp8;
+  ca.img = cm.img;
+  ca.qlen = cm.q;
+  const int64_t blocks = ca.op[0].blocks + ca.op[1].blocks;
   if (blocks > int64_t(0x7fffffff)) {
     set_error("conv3x3 wgrad pack: too many planes");
     return -1;
   }
-  pack_cm_kernel<<<dim3(unsigned(blocks)), 256, 0, st>>>(src, dst, B, C, H, W, c_pad, cm.wp8, cm.img, cm.q,
-                                                          shift, rows_per, rblocks, planes_per, nmain);
+  pack_cm_kernel<<<dim3(unsigned(blocks)), 256, 0, st>>>(ca);
   return 0;
 }
 
@@ -1104,7 +1140,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   // Fewer workgroups than CUs: split the input chunks over blockIdx.z and sum the fp32
   // partials in a second pass (in split order).
   int nsplit = 1;
-  if (valid < 256 && a.chunks >= 2) {
+  if (valid <= 64 && a.chunks >= 2) {
     nsplit = int(std::min<int64_t>(a.chunks, ceil_div(256, valid)));
     a.ch_per = int(ceil_div(a.chunks, nsplit));
     nsplit = int(ceil_div(a.chunks, a.ch_per));
@@ -1278,8 +1314,7 @@ int xdna_conv3x3_wgrad_pack_bf16(const uint16_t* x, const uint16_t* dy, int B, i
   if (!wgrad_bufs("xdna_conv3x3_wgrad_pack_bf16", p, workspace, workspace_bytes, bufs)) return -1;
   if (!admit_launch("conv3x3 wgrad pack")) return -1;
   hipStream_t st = as_stream(stream);
-  if (pack_cm_launch(x, bufs.xt, B, Cin, H, W, p.ci_pad, p.cm, 1, st) != 0) return -1;
-  if (pack_cm_launch(dy, bufs.dt, B, Cout, H, W, p.co_pad, p.cm, 0, st) != 0) return -1;
+  if (pack_cm_launch2(x, bufs.xt, Cin, p.ci_pad, dy, bufs.dt, Cout, p.co_pad, B, H, W, p.cm, st) != 0) return -1;
   return check_launch("conv3x3 wgrad pack");
 }
 
