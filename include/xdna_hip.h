@@ -233,7 +233,10 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
  * x 64-256 rows per workgroup, weights streamed from L2 per tap), 2 / 3 the small-grid
  * kernel (64 output channels x 64 / 128 rows, whole chunks staged in LDS, split-K when
  * the grid is smaller than the CU count), 4 the wide kernel (256 output channels x 256
- * rows, 8 waves, weights staged in LDS; used for cout > 128 only, else the main kernel).
+ * rows, 8 waves, weights staged in LDS; used for cout > 128 only, else the main kernel),
+ * 5 its four-wave form (one wave per SIMD with 128 x 128 wave tiles, fragments
+ * software-pipelined; cout > 128 only; the automatic choice for cout >= 256 on large
+ * grids).
  * Results agree to the same tolerance; only the
  * summation grouping differs.  No reference counterpart (a tuning knob, like the
  * reference's XDNA_* performance environment variables).  XDNA_ROWS_VARIANT sets the

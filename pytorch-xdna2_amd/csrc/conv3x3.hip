@@ -454,6 +454,219 @@ void conv_rows2_kernel(RowsArgs a) {
     }
 }
 
+// Four-wave form of the 256 x 256 tile: one wave per SIMD, each owning 128 channels x 128
+// rows (4 x 4 MFMA tiles, accumulators in the AGPR half of the register file), so a 16-wide
+// k-step reads 8 fragments for 16 MFMAs — half the LDS traffic per MFMA of the eight-wave
+// form.  With one wave per SIMD nothing else covers latency, so the kernel pipelines it:
+//   * fragments are read one k-step ahead, across tap boundaries too: the slab of tap T+1
+//     is in its slot two barriers before the last k-step of tap T reads its first
+//     fragments (only a chunk boundary, where the window changes, waits);
+//   * the one barrier per tap opens the last k-step, where slab T+3 replaces slab T in
+//     LDS; slabs are loaded two taps before they are stored (register set = slab % 3, and
+//     9 taps per chunk keep the rotation static);
+//   * every LDS access and global load issues between two MFMAs (scheduling groups), so
+//     the matrix cores do not idle while the wave issues memory instructions;
+//   * every load and store is unconditional (slab and chunk indexes clamped, window rows
+//     clamped to the window), so the memory counters the compiler waits on are static.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void conv_rows4_kernel(RowsArgs a) {
+  constexpr int kXv = (kWXRows * 8 + 255) / 256;       // window vectors per thread (11)
+  constexpr int kWv = kWCo * 8 / 256;                  // weight vectors per thread per slab (8)
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs = smem;                                 // [kWXRows][kPitch]
+  uint16_t* wsl = smem + kWXRows * kPitch;             // [3][kWCo][kPitch]
+
+  constexpr int tiles_per_group = kGroupOutRows / kWTp;
+  int rt, ct;
+  if (!rows_tile(a, rt, ct)) return;
+  const int g = rt / tiles_per_group;
+  const int r0 = (rt % tiles_per_group) * kWTp;
+  if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;
+  const int co0 = ct * kWCo;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int K = a.chunks * 9 * kKStep;
+  const int T1 = a.chunks * 9;
+  const int nrows = kWTp + 2 * a.wp + 2;               // window rows (<= kWXRows)
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    f32x16_t init = zero_acc();
+    if (a.bias) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * 128 + m * 32 + mfma_row(i, lane);
+        init[i] = co < a.cout ? bf16_to_f32(a.bias[co]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[m][n] = init;
+  }
+
+  // weight vector j of a slab: row (tid >> 3) + 32 j, 8-element piece tid & 7
+  const uint16_t* wsrc = a.wt + (int64_t(co0) + (tid >> 3)) * K + (tid & 7) * 8;
+  const int wdst = (tid >> 3) * kPitch + (tid & 7) * 8;
+  // window vector j: row min((tid + 256 j) >> 3, nrows - 1), piece tid & 7
+  auto xoff = [&](int j) { return min((tid + j * 256) >> 3, nrows - 1) * 8 + (tid & 7); };
+  const uint16_t* xsrc0 = a.xp + (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
+
+  u32x4_t wreg[3][kWv];
+  u32x4_t xr[kXv];
+  u32x4_t fa[2][4], fb[2][4];
+
+#define XDNA_W4_LOAD(set_, T_)                                                               \
+  do {                                                                                       \
+    const uint16_t* s_ = wsrc + int64_t(min((T_), T1 - 1)) * kKStep;                         \
+    _Pragma("unroll") for (int j = 0; j < kWv; ++j)                                          \
+      wreg[set_][j] = *reinterpret_cast<const u32x4_t*>(s_ + int64_t(j * 32) * K);           \
+  } while (0)
+#define XDNA_W4_STORE(set_, slot_)                                                           \
+  do {                                                                                       \
+    uint16_t* d_ = wsl + (slot_) * kWSlot + wdst;                                            \
+    _Pragma("unroll") for (int j = 0; j < kWv; ++j)                                          \
+      *reinterpret_cast<u32x4_t*>(d_ + j * 32 * kPitch) = wreg[set_][j];                     \
+  } while (0)
+// window vectors j of chunk ch_ with j * 7 / kXv == part_ (part_ < 0: all of them)
+#define XDNA_X4_LOAD(ch_, part_)                                                             \
+  do {                                                                                       \
+    const uint16_t* s_ = xsrc0 + int64_t(ch_) * kGroupRows * kKStep;                         \
+    _Pragma("unroll") for (int j = 0; j < kXv; ++j)                                          \
+      if ((part_) < 0 || j * 7 / kXv == (part_))                                             \
+        xr[j] = *reinterpret_cast<const u32x4_t*>(s_ + xoff(j) * 8);                         \
+  } while (0)
+#define XDNA_X4_STORE()                                                                      \
+  do {                                                                                       \
+    _Pragma("unroll") for (int j = 0; j < kXv; ++j)                                          \
+      *reinterpret_cast<u32x4_t*>(&xs[(xoff(j) >> 3) * kPitch + (xoff(j) & 7) * 8]) = xr[j]; \
+  } while (0)
+// fragments of (slot_, tap_, ks_) into buffer buf_
+#define XDNA_F4_LOAD(buf_, slot_, tap_, ks_)                                                 \
+  do {                                                                                       \
+    const uint16_t* wa_ = wsl + (slot_) * kWSlot + (wm * 128 + lr) * kPitch + lk + (ks_) * 16; \
+    const uint16_t* xb_ = xs + (wn * 128 + lr + ((tap_) / 3) * a.wp + ((tap_) % 3)) * kPitch + lk + (ks_) * 16; \
+    _Pragma("unroll") for (int m = 0; m < 4; ++m)                                            \
+      fa[buf_][m] = *reinterpret_cast<const u32x4_t*>(wa_ + m * 32 * kPitch);                \
+    _Pragma("unroll") for (int n = 0; n < 4; ++n)                                            \
+      fb[buf_][n] = *reinterpret_cast<const u32x4_t*>(xb_ + n * 32 * kPitch);                \
+  } while (0)
+
+#define XDNA_M4(buf_)                                                                        \
+  do {                                                                                       \
+    _Pragma("unroll") for (int m = 0; m < 4; ++m)                                            \
+      _Pragma("unroll") for (int n = 0; n < 4; ++n)                                          \
+        acc[m][n] = mfma_32x32x16(as_bf16x8(fa[buf_][m]), as_bf16x8(fb[buf_][n]), acc[m][n]); \
+  } while (0)
+
+  // prologue: slabs 0..2 and the window of chunk 0 in LDS; slabs 3..5 in registers
+  XDNA_W4_LOAD(0, 0);
+  XDNA_W4_LOAD(1, 1);
+  XDNA_W4_LOAD(2, 2);
+  XDNA_X4_LOAD(0, -1);
+  XDNA_W4_STORE(0, 0);
+  XDNA_W4_STORE(1, 1);
+  XDNA_W4_STORE(2, 2);
+  XDNA_X4_STORE();
+  XDNA_W4_LOAD(0, 3);
+  XDNA_W4_LOAD(1, 4);
+  __syncthreads();
+  XDNA_F4_LOAD(0, 0, 0, 0);
+
+  // Slab S lives in slot S % 3 and, before that, in register set S % 3 (loaded at tap
+  // S-5, two taps before it is stored; at most two sets hold data at a time); (tap % 3) ==
+  // (T % 3), so every slot and set index below is a compile-time constant.  Slot T % 3 is
+  // read for the last time at tap T, k-step 2 (the fragments of k-step 3): the barrier
+  // that opens k-step 3 frees it for slab T+3, which is first read at tap T+2, k-step 3,
+  // two barriers later.  Instruction order is pinned with scheduling groups so that every
+  // LDS access and global load issues between two MFMAs of the current k-step.
+  for (int ch = 0; ch < a.chunks; ++ch) {
+    const int chn = min(ch + 1, a.chunks - 1);
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+      const int T = ch * 9 + tap;
+      constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100, kDsWr = 0x200;
+#pragma unroll
+      for (int ks = 0; ks < 3; ++ks) {
+        const int cur = ks & 1;
+        XDNA_F4_LOAD(cur ^ 1, tap % 3, tap, ks + 1);
+        if (ks == 1 && tap < 7) XDNA_X4_LOAD(chn, tap);
+        XDNA_M4(cur);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+          if (ks == 1 && i < 2) __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __syncthreads();
+      if (tap < 8) XDNA_F4_LOAD(0, (tap + 1) % 3, tap + 1, 0);
+      else XDNA_X4_STORE();                 // chunk boundary: the next window
+      XDNA_W4_STORE(tap % 3, tap % 3);      // slab T+3
+      XDNA_W4_LOAD((tap + 2) % 3, T + 5);
+      XDNA_M4(1);
+      // the next tap's fragment reads first (their slot is not the one being written)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        if (tap < 8)
+          __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+        else
+          __builtin_amdgcn_sched_group_barrier(kDsWr, 2, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsWr, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (tap == 8) {
+        __syncthreads();
+        XDNA_F4_LOAD(0, 0, 0, 0);
+      }
+    }
+  }
+#undef XDNA_W4_LOAD
+#undef XDNA_W4_STORE
+#undef XDNA_X4_LOAD
+#undef XDNA_X4_STORE
+#undef XDNA_F4_LOAD
+#undef XDNA_M4
+
+  const int first = a.S == 1 ? 0 : 1;
+  const int64_t plane = int64_t(a.H) * a.W;
+  uint16_t* obase[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    obase[n] = nullptr;
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * 128 + n * 32 + lr;
+    if (p >= a.m_total) continue;
+    const int64_t vb = p / a.img;
+    const int64_t rem = p - vb * a.img;
+    const int y = int(rem / a.wp);
+    const int col = int(rem - int64_t(y) * a.wp) - first;
+    if (y >= a.H || col < 0) continue;
+    const int b = int(vb / a.S), s = int(vb % a.S);
+    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+    if (col >= cols) continue;
+    const int x = (a.S == 1 ? 0 : s * a.So) + col;
+    obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 128 + m * 32 + mfma_row(i, lane);
+      if (co >= a.cout) continue;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
+    }
+}
+
 // Small-grid variant: 64 output channels x TP grid rows per workgroup.  Per input chunk
 // the halo window AND all nine taps of the workgroup's weights (64 x 576 bf16, 72 KiB)
 // are staged in LDS with every load of the chunk in flight at once, so a chunk costs one
@@ -1087,13 +1300,15 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   const int64_t big128 = ceil_div(geom.m_total, 128) * ytiles;
   // 64 or fewer output channels: the small-grid kernel's 64-channel tiles waste no MFMA work
   const bool small = variant == 2 || variant == 3 || (variant == 0 && (big128 < 512 || cout <= kSCo));
-  // the wide kernel: 256-channel tiles (cout > 128 only: the weights are padded to 256
-  // rows from there on)
-  const bool wide = cout > kTCo && (variant == 4 || (variant == 0 && !small && cout >= kWCo));
+  // the wide kernels: 256-channel tiles (cout > 128 only: the weights are padded to 256
+  // rows from there on); the four-wave form unless the eight-wave one is asked for
+  const bool wide = cout > kTCo && (variant == 4 || variant == 5 || (variant == 0 && !small && cout >= kWCo));
   if (wide) {
-    static const bool lds_wide = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows2_kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     int(kWideLds)) == hipSuccess;
+    static const bool lds_wide =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows2_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(kWideLds)) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(kWideLds)) == hipSuccess;
     if (!lds_wide) {
       set_error("conv3x3 rows: cannot enable the wide kernel's LDS size");
       return -1;
@@ -1101,7 +1316,10 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     a.nrt = int(ceil_div(geom.m_total, kWTp));
     a.ncot = int(ceil_div(cout, kWCo));
     const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
-    conv_rows2_kernel<<<grid, 512, kWideLds, st>>>(a);
+    if (variant == 4)
+      conv_rows2_kernel<<<grid, 512, kWideLds, st>>>(a);
+    else
+      conv_rows4_kernel<<<grid, 256, kWideLds, st>>>(a);
     return check_launch("conv3x3 rows");
   }
   if (!small) {
@@ -1398,8 +1616,8 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {
-  if (variant < 0 || variant > 4) {
-    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..4");
+  if (variant < 0 || variant > 5) {
+    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..5");
     return -1;
   }
   g_rows_variant.store(variant);
