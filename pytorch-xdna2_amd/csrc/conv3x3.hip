@@ -1025,7 +1025,22 @@ struct WgradArgs {
   int kt_per_split, ktiles;
   int xpitch;          // LDS pitch of the staged x window (elements)
   int wlen;            // staged window length (elements): kTK + 2*wp8 + 8
+  int nco_t, ntiles, splits;  // channel tiles (co tiles x ci tiles) and pixel splits
 };
+
+// blockIdx.x -> (co tile, ci tile, split).  Workgroup L runs on XCD L % 8; on each XCD the
+// consecutive workgroups take every channel tile of one pixel split, so the split's x
+// window and dY rows come from HBM once and serve all its tiles from that XCD's L2
+// (split s lives on XCD s % 8; the grid is padded to a multiple of 8 splits).
+__device__ inline bool wgrad_tile(const WgradArgs& a, int& co_t, int& ci_t, int& split) {
+  const int L = blockIdx.x;
+  const int x = L % kXcds, k = L / kXcds;
+  const int tile = k % a.ntiles;
+  split = (k / a.ntiles) * kXcds + x;
+  co_t = tile % a.nco_t;
+  ci_t = tile / a.nco_t;
+  return split < a.splits;
+}
 
 // One workgroup (8 waves, 512 threads): 128 output channels x 64 input channels x 9 taps
 // over the k-tiles of one split.  Wave (wm, wn) owns channels [wm*32, +32) x input
@@ -1044,9 +1059,10 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 void wgrad_kernel(WgradArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   const int buf_elems = kTCo * kPitch + 64 * a.xpitch;
-  const int co0 = blockIdx.x * kTCo;
-  const int ci0 = blockIdx.y * 64;
-  const int split = blockIdx.z;
+  int co_t, ci_t, split;
+  if (!wgrad_tile(a, co_t, ci_t, split)) return;
+  const int co0 = co_t * kTCo;
+  const int ci0 = ci_t * 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 3, wn = wave >> 2;
   const int lr = lane & 31, lk = (lane >> 5) * 8;
@@ -1059,7 +1075,7 @@ void wgrad_kernel(WgradArgs a) {
 #pragma unroll
   for (int t = 0; t < 9; ++t) acc[t] = zero_acc();
   float bsum = 0.0f;
-  const bool do_bias = a.bpart && blockIdx.y == 0 && wn == 0;
+  const bool do_bias = a.bpart && ci_t == 0 && wn == 0;
 
   u32x4_t dreg[2];
   u32x4_t xreg[XV];
@@ -1403,17 +1419,17 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
   const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
   const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
   // Split-K: pick the split count s that minimizes a simple model of the two kernels,
-  //   flops / (min(tiles*s, CUs) * per-CU rate) + (write + read of s fp32 partials) / BW,
-  // i.e. enough workgroups to fill the 256 CUs without drowning small problems in
-  // partial-sum traffic.
+  //   rounds(s) * flops / (tiles * s * per-CU rate) + (write + read of s fp32 partials) / BW,
+  // with rounds(s) = ceil(tiles * s / 256): one workgroup fits a CU (its LDS and 8 waves
+  // of 256 registers), so a grid of 257 workgroups takes two full workgroup times.
   const double flops = 2.0 * 9.0 * double(B) * H * W * double(Cin) * double(Cout);
   const double cu_rate = 4.0e12, bw = 5.0e12;
   int64_t best = 1;
   double best_t = 1e30;
   const int64_t smax = std::min<int64_t>(p.cm.ktiles, 4096);
-  for (int64_t s = 1; s <= smax; s = s < 16 ? s + 1 : s + s / 8) {
-    const double wgs = double(std::min<int64_t>(tiles * s, 256));
-    const double t = flops / (wgs * cu_rate) + 2.0 * double(s) * double(out_elems) * 4.0 / bw;
+  for (int64_t s = 1; s <= smax; s = s < 512 ? s + 1 : s + s / 8) {
+    const double rounds = double(ceil_div(tiles * s, 256));
+    const double t = rounds * flops / (double(tiles * s) * cu_rate) + 2.0 * double(s) * double(out_elems) * 4.0 / bw;
     if (t < best_t) {
       best_t = t;
       best = s;
@@ -1568,7 +1584,15 @@ int xdna_conv3x3_wgrad_packed_bf16(uint16_t* gw, uint16_t* gb, int B, int Cin, i
     set_error("conv3x3 wgrad: cannot raise the dynamic LDS limit");
     return -1;
   }
-  const dim3 grid(unsigned(p.co_pad / kTCo), unsigned(p.ci_pad / 64), unsigned(p.splits));
+  a.nco_t = p.co_pad / kTCo;
+  a.ntiles = a.nco_t * (p.ci_pad / 64);
+  a.splits = p.splits;
+  const int64_t nblocks = ceil_div(p.splits, kXcds) * kXcds * int64_t(a.ntiles);
+  if (nblocks > int64_t(0x7fffffff)) {
+    set_error("conv3x3 wgrad: grid too large");
+    return -1;
+  }
+  const dim3 grid(unsigned(nblocks), 1, 1);
   if (64 * (p.wlen / 8) <= 4 * kWgThreads)
     wgrad_kernel<4><<<grid, kWgThreads, p.lds_bytes, st>>>(a);
   else
