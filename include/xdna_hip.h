@@ -236,7 +236,8 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
  * rows, 8 waves, weights staged in LDS; used for cout > 128 only, else the main kernel),
  * 5 its four-wave form (one wave per SIMD with 128 x 128 wave tiles, fragments
  * software-pipelined; cout > 128 only; the automatic choice for cout >= 256 on large
- * grids).
+ * grids), 6 / 7 / 8 four-wave kernels with 128 channels x 256 rows, 128 channels x 512
+ * rows and 64 channels x 512 rows per workgroup (any cout).
  * Results agree to the same tolerance; only the
  * summation grouping differs.  No reference counterpart (a tuning knob, like the
  * reference's XDNA_* performance environment variables).  XDNA_ROWS_VARIANT sets the

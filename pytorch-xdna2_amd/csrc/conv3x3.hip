@@ -454,10 +454,13 @@ void conv_rows2_kernel(RowsArgs a) {
     }
 }
 
-// Four-wave form of the 256 x 256 tile: one wave per SIMD, each owning 128 channels x 128
-// rows (4 x 4 MFMA tiles, accumulators in the AGPR half of the register file), so a 16-wide
-// k-step reads 8 fragments for 16 MFMAs — half the LDS traffic per MFMA of the eight-wave
-// form.  With one wave per SIMD nothing else covers latency, so the kernel pipelines it:
+// Four-wave kernels: one wave per SIMD, wave (wm, wn) of a WM x (4/WM) grid owning MT*32
+// channels x NT*32 rows (MT x NT MFMA tiles, accumulators in the AGPR half of the
+// register file).  A workgroup covers CO = WM*MT*32 channels x TP = (4/WM)*NT*32 rows:
+//   <4,4,2>  256 channels x 256 rows (cout > 128): a 16-wide k-step reads 8 fragments for
+//            16 MFMAs, half the LDS traffic per MFMA of the eight-wave form;
+//   <2,4,2>  128 x 256 and <4,4,1> 128 x 512 (cout <= 128), <2,4,1> 64 x 512 (cout <= 64).
+// With one wave per SIMD nothing else covers latency, so the kernel pipelines it:
 //   * fragments are read one k-step ahead, across tap boundaries too: the slab of tap T+1
 //     is in its slot two barriers before the last k-step of tap T reads its first
 //     fragments (only a chunk boundary, where the window changes, waits);
@@ -468,41 +471,55 @@ void conv_rows2_kernel(RowsArgs a) {
 //     the matrix cores do not idle while the wave issues memory instructions;
 //   * every load and store is unconditional (slab and chunk indexes clamped, window rows
 //     clamped to the window), so the memory counters the compiler waits on are static.
+template <int MT, int NT, int WM>
+struct Q4 {
+  static constexpr int WN = 4 / WM;
+  static constexpr int CO = WM * MT * 32;                    // channels per workgroup
+  static constexpr int TP = WN * NT * 32;                    // grid rows per workgroup
+  static constexpr int XRows = TP + kMaxHalo;                // window rows
+  static constexpr int Slot = CO * kPitch;                   // elements of one weight slot
+  static constexpr size_t Lds = size_t(XRows * kPitch + 3 * Slot) * 2;
+};
+
+template <int MT, int NT, int WM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void conv_rows4_kernel(RowsArgs a) {
-  constexpr int kXv = (kWXRows * 8 + 255) / 256;       // window vectors per thread (11)
-  constexpr int kWv = kWCo * 8 / 256;                  // weight vectors per thread per slab (8)
+  using Q = Q4<MT, NT, WM>;
+  constexpr int kXv = (Q::XRows * 8 + 255) / 256;      // window vectors per thread
+  constexpr int kWv = Q::CO * 8 / 256;                 // weight vectors per thread per slab
+  constexpr int kR = MT + NT, kM = MT * NT;            // fragment reads, MFMAs per k-step
+  static_assert(kM >= kR && kWv >= 1, "tile too small for the schedule");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* xs = smem;                                 // [kWXRows][kPitch]
-  uint16_t* wsl = smem + kWXRows * kPitch;             // [3][kWCo][kPitch]
+  uint16_t* xs = smem;                                 // [XRows][kPitch]
+  uint16_t* wsl = smem + Q::XRows * kPitch;            // [3][CO][kPitch]
 
-  constexpr int tiles_per_group = kGroupOutRows / kWTp;
+  constexpr int tiles_per_group = kGroupOutRows / Q::TP;
   int rt, ct;
   if (!rows_tile(a, rt, ct)) return;
   const int g = rt / tiles_per_group;
-  const int r0 = (rt % tiles_per_group) * kWTp;
+  const int r0 = (rt % tiles_per_group) * Q::TP;
   if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;
-  const int co0 = ct * kWCo;
+  const int co0 = ct * Q::CO;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WM, wn = wave / WM;
   const int K = a.chunks * 9 * kKStep;
   const int T1 = a.chunks * 9;
-  const int nrows = kWTp + 2 * a.wp + 2;               // window rows (<= kWXRows)
+  const int nrows = Q::TP + 2 * a.wp + 2;              // window rows (<= XRows)
   const int lr = lane & 31, lk = (lane >> 5) * 8;
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[MT][NT];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < MT; ++m) {
     f32x16_t init = zero_acc();
     if (a.bias) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int co = co0 + wm * 128 + m * 32 + mfma_row(i, lane);
+        const int co = co0 + wm * MT * 32 + m * 32 + mfma_row(i, lane);
         init[i] = co < a.cout ? bf16_to_f32(a.bias[co]) : 0.0f;
       }
     }
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[m][n] = init;
+    for (int n = 0; n < NT; ++n) acc[m][n] = init;
   }
 
   // weight vector j of a slab: row (tid >> 3) + 32 j, 8-element piece tid & 7
@@ -514,7 +531,7 @@ void conv_rows4_kernel(RowsArgs a) {
 
   u32x4_t wreg[3][kWv];
   u32x4_t xr[kXv];
-  u32x4_t fa[2][4], fb[2][4];
+  u32x4_t fa[2][MT], fb[2][NT];
 
 #define XDNA_W4_LOAD(set_, T_)                                                               \
   do {                                                                                       \
@@ -524,7 +541,7 @@ void conv_rows4_kernel(RowsArgs a) {
   } while (0)
 #define XDNA_W4_STORE(set_, slot_)                                                           \
   do {                                                                                       \
-    uint16_t* d_ = wsl + (slot_) * kWSlot + wdst;                                            \
+    uint16_t* d_ = wsl + (slot_) * Q::Slot + wdst;                                           \
     _Pragma("unroll") for (int j = 0; j < kWv; ++j)                                          \
       *reinterpret_cast<u32x4_t*>(d_ + j * 32 * kPitch) = wreg[set_][j];                     \
   } while (0)
@@ -544,22 +561,21 @@ void conv_rows4_kernel(RowsArgs a) {
 // fragments of (slot_, tap_, ks_) into buffer buf_
 #define XDNA_F4_LOAD(buf_, slot_, tap_, ks_)                                                 \
   do {                                                                                       \
-    const uint16_t* wa_ = wsl + (slot_) * kWSlot + (wm * 128 + lr) * kPitch + lk + (ks_) * 16; \
-    const uint16_t* xb_ = xs + (wn * 128 + lr + ((tap_) / 3) * a.wp + ((tap_) % 3)) * kPitch + lk + (ks_) * 16; \
-    _Pragma("unroll") for (int m = 0; m < 4; ++m)                                            \
+    const uint16_t* wa_ = wsl + (slot_) * Q::Slot + (wm * MT * 32 + lr) * kPitch + lk + (ks_) * 16; \
+    const uint16_t* xb_ = xs + (wn * NT * 32 + lr + ((tap_) / 3) * a.wp + ((tap_) % 3)) * kPitch + lk + (ks_) * 16; \
+    _Pragma("unroll") for (int m = 0; m < MT; ++m)                                           \
       fa[buf_][m] = *reinterpret_cast<const u32x4_t*>(wa_ + m * 32 * kPitch);                \
-    _Pragma("unroll") for (int n = 0; n < 4; ++n)                                            \
+    _Pragma("unroll") for (int n = 0; n < NT; ++n)                                           \
       fb[buf_][n] = *reinterpret_cast<const u32x4_t*>(xb_ + n * 32 * kPitch);                \
   } while (0)
-
 #define XDNA_M4(buf_)                                                                        \
   do {                                                                                       \
-    _Pragma("unroll") for (int m = 0; m < 4; ++m)                                            \
-      _Pragma("unroll") for (int n = 0; n < 4; ++n)                                          \
+    _Pragma("unroll") for (int m = 0; m < MT; ++m)                                           \
+      _Pragma("unroll") for (int n = 0; n < NT; ++n)                                         \
         acc[m][n] = mfma_32x32x16(as_bf16x8(fa[buf_][m]), as_bf16x8(fb[buf_][n]), acc[m][n]); \
   } while (0)
 
-  // prologue: slabs 0..2 and the window of chunk 0 in LDS; slabs 3..5 in registers
+  // prologue: slabs 0..2 and the window of chunk 0 in LDS; slabs 3, 4 in registers
   XDNA_W4_LOAD(0, 0);
   XDNA_W4_LOAD(1, 1);
   XDNA_W4_LOAD(2, 2);
@@ -580,12 +596,15 @@ void conv_rows4_kernel(RowsArgs a) {
   // that opens k-step 3 frees it for slab T+3, which is first read at tap T+2, k-step 3,
   // two barriers later.  Instruction order is pinned with scheduling groups so that every
   // LDS access and global load issues between two MFMAs of the current k-step.
+  constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100, kDsWr = 0x200;
+  constexpr int kRest = kM - kR;                                   // MFMAs after the reads
+  constexpr int kPerRest = kRest > 0 ? (kWv + kRest - 1) / kRest : kWv;
+  constexpr int kXwPer = (kXv + kR - 1) / kR;                      // window writes per MFMA
   for (int ch = 0; ch < a.chunks; ++ch) {
     const int chn = min(ch + 1, a.chunks - 1);
 #pragma unroll
     for (int tap = 0; tap < 9; ++tap) {
       const int T = ch * 9 + tap;
-      constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100, kDsWr = 0x200;
 #pragma unroll
       for (int ks = 0; ks < 3; ++ks) {
         const int cur = ks & 1;
@@ -593,12 +612,12 @@ void conv_rows4_kernel(RowsArgs a) {
         if (ks == 1 && tap < 7) XDNA_X4_LOAD(chn, tap);
         XDNA_M4(cur);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kR; ++i) {
           __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
           __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
-          if (ks == 1 && i < 2) __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
+          if (ks == 1 && i < 3) __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+        if (kRest > 0) __builtin_amdgcn_sched_group_barrier(kMfma, kRest, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
       __syncthreads();
@@ -609,18 +628,18 @@ void conv_rows4_kernel(RowsArgs a) {
       XDNA_M4(1);
       // the next tap's fragment reads first (their slot is not the one being written)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kR; ++i) {
         __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
         if (tap < 8)
           __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
         else
-          __builtin_amdgcn_sched_group_barrier(kDsWr, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(kDsWr, kXwPer, 0);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kDsWr, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
+      for (int i = 0; i < (kRest > 0 ? kRest : 1); ++i) {
+        if (kRest > 0) __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsWr, kPerRest, 0);
+        __builtin_amdgcn_sched_group_barrier(kVmemRd, kPerRest, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (tap == 8) {
@@ -638,11 +657,11 @@ void conv_rows4_kernel(RowsArgs a) {
 
   const int first = a.S == 1 ? 0 : 1;
   const int64_t plane = int64_t(a.H) * a.W;
-  uint16_t* obase[4];
+  uint16_t* obase[NT];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int n = 0; n < NT; ++n) {
     obase[n] = nullptr;
-    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * 128 + n * 32 + lr;
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NT * 32 + n * 32 + lr;
     if (p >= a.m_total) continue;
     const int64_t vb = p / a.img;
     const int64_t rem = p - vb * a.img;
@@ -656,13 +675,13 @@ void conv_rows4_kernel(RowsArgs a) {
     obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
   }
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int co = co0 + wm * 128 + m * 32 + mfma_row(i, lane);
+      const int co = co0 + wm * MT * 32 + m * 32 + mfma_row(i, lane);
       if (co >= a.cout) continue;
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
+      for (int n = 0; n < NT; ++n)
         if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
     }
 }
@@ -1279,6 +1298,23 @@ int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, 
   return check_launch("conv3x3 weight preparation");
 }
 
+template <int MT, int NT, int WM>
+int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
+  using Q = Q4<MT, NT, WM>;
+  static const bool lds_ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess;
+  if (!lds_ok) {
+    set_error("conv3x3 rows: cannot enable the four-wave kernel's LDS size");
+    return -1;
+  }
+  a.nrt = int(ceil_div(geom.m_total, Q::TP));
+  a.ncot = int(ceil_div(cout, Q::CO));
+  const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
+  conv_rows4_kernel<MT, NT, WM><<<grid, 256, Q::Lds, st>>>(a);
+  return check_launch("conv3x3 rows");
+}
+
 // conv of packed input xp (cin channels) with prepared weights -> NCHW out (cout channels).
 std::atomic<int> g_rows_variant{[] {
   const char* e = std::getenv("XDNA_ROWS_VARIANT");
@@ -1311,19 +1347,50 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   // overrides it: 1 main kernel, 2 / 3 small-grid kernel with 64 / 128-row tiles).  The
   // main kernel needs a grid of several workgroups per CU to hide its per-tap weight
   // loads; below that the small-grid kernel, which stages whole chunks, is faster.
-  const int variant = g_rows_variant.load();
+  int variant = g_rows_variant.load();
   const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
   const int64_t big128 = ceil_div(geom.m_total, 128) * ytiles;
-  // 64 or fewer output channels: the small-grid kernel's 64-channel tiles waste no MFMA work
-  const bool small = variant == 2 || variant == 3 || (variant == 0 && (big128 < 512 || cout <= kSCo));
+  if (variant == 0) {
+    // Automatic choice (fitted to the sweep shapes on an MI355X).  Grids of a few hundred
+    // 128-row tiles or less: the small-grid kernel (whole chunks staged per workgroup,
+    // split-K below the CU count).  Otherwise the four-wave kernel whose modelled time
+    //   ceil(workgroups / 256) * (tile channels * tile rows) * per-MFMA cost
+    // is least (one workgroup per CU; the 128 x 256 and 64 x 512 tiles issue 8 MFMAs per 6
+    // fragment reads instead of 16 per 8: cost 1.1).  Ties go to the first candidate.
+    const bool small = cout <= kSCo ? ceil_div(geom.m_total, 512) < 150 : big128 < 300;
+    if (small) {
+      variant = -1;
+    } else {
+      struct Cand { int v, co, tp; double cost; };
+      const Cand all[] = {{7, 128, 512, 1.0}, {5, 256, 256, 1.0}, {6, 128, 256, 1.1}, {8, 64, 512, 1.1}};
+      double best = 1e300;
+      for (const Cand& c : all) {
+        if (c.v == 5 && cout <= kTCo) continue;            // 256-channel tiles: cout > 128 only
+        if (c.v == 8 && cout > kTCo) continue;
+        if (c.v == 7 && cout <= kSCo) continue;            // <= 64 channels: 64-channel tiles only
+        if (c.v == 6 && cout <= kSCo) continue;
+        const int64_t wgs = ceil_div(geom.m_total, c.tp) * ceil_div(cout, c.co);
+        const double t = double(ceil_div(wgs, 256)) * double(c.co) * c.tp * c.cost;
+        if (t < best) {
+          best = t;
+          variant = c.v;
+        }
+      }
+    }
+  }
+  const bool small = variant == 2 || variant == 3 || variant == -1;
+  // four-wave kernels with 128- or 64-channel tiles: any cout (the prepared weights cover
+  // every tile: 128 rows up to 128 channels, a multiple of 256 beyond)
+  if (variant == 6) return launch_rows4<2, 4, 2>(a, geom, cout, st);
+  if (variant == 7) return launch_rows4<4, 4, 1>(a, geom, cout, st);
+  if (variant == 8) return launch_rows4<2, 4, 1>(a, geom, cout, st);
   // the wide kernels: 256-channel tiles (cout > 128 only: the weights are padded to 256
   // rows from there on); the four-wave form unless the eight-wave one is asked for
-  const bool wide = cout > kTCo && (variant == 4 || variant == 5 || (variant == 0 && !small && cout >= kWCo));
+  const bool wide = cout > kTCo && (variant == 4 || variant == 5);
   if (wide) {
+    if (variant != 4) return launch_rows4<4, 4, 2>(a, geom, cout, st);
     static const bool lds_wide =
         hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows2_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, int(kWideLds)) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(kWideLds)) == hipSuccess;
     if (!lds_wide) {
       set_error("conv3x3 rows: cannot enable the wide kernel's LDS size");
@@ -1332,10 +1399,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     a.nrt = int(ceil_div(geom.m_total, kWTp));
     a.ncot = int(ceil_div(cout, kWCo));
     const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
-    if (variant == 4)
-      conv_rows2_kernel<<<grid, 512, kWideLds, st>>>(a);
-    else
-      conv_rows4_kernel<<<grid, 256, kWideLds, st>>>(a);
+    conv_rows2_kernel<<<grid, 512, kWideLds, st>>>(a);
     return check_launch("conv3x3 rows");
   }
   if (!small) {
@@ -1640,8 +1704,8 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {
-  if (variant < 0 || variant > 5) {
-    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..5");
+  if (variant < 0 || variant > 8) {
+    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..8");
     return -1;
   }
   g_rows_variant.store(variant);

@@ -6,7 +6,8 @@ relative L2 <= 1e-2.  Shapes cover ragged channel counts (partial 64-chunks, par
 128-blocks), one and several 2048-row groups, tiny channel counts (RGB-like), width
 strips (W > 36: S = 2, 3) and the C1 conv at B = 2.  Forward and dgrad run through each
 rows-kernel variant (main kernel; small-grid kernel with 64 / 128-row tiles, split-K over
-chunks on small grids; wide kernels with 256-channel tiles in eight- and four-wave forms).  wgrad is also checked for run-to-run bit equality (its split-K
+chunks on small grids; wide kernels with 256-channel tiles in eight- and four-wave forms;
+four-wave kernels with 128- and 64-channel tiles).  wgrad is also checked for run-to-run bit equality (its split-K
 reduction is fixed-order).
 """
 import numpy as np
@@ -50,8 +51,8 @@ def _ws(nbytes):
 # rows-kernel variants (xdna_conv3x3_set_rows_variant): main kernel, small-grid kernel
 # with 64- and 128-row tiles (split-K over chunks where the grid is small), wide kernel
 # with eight and with four waves (256-channel tiles, for cout > 128; the main kernel
-# otherwise)
-VARIANTS = [1, 2, 3, 4, 5]
+# otherwise), four-wave kernels with 128 x 256, 128 x 512 and 64 x 512 tiles
+VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8]
 
 
 @pytest.fixture
