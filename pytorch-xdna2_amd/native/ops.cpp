@@ -568,14 +568,29 @@ std::vector<TimedLaunch>& timed() {
   static auto* v = new std::vector<TimedLaunch>();
   return *v;
 }
+// Events are created when timing is switched on, not per launch: creating two events per
+// launch costs the host more than the small launches take on the GPU.  They live until
+// the process ends and are reused by the next timing session; launches past the pool's
+// end are not timed.
+constexpr size_t kTimingEvents = 16384;
+std::vector<void*>& event_pool() {
+  static auto* v = new std::vector<void*>();
+  return *v;
+}
+size_t g_pool_next = 0;
 
 }  // namespace
 
 KernelTimer::KernelTimer(const char* n, double w) : name(n), work(w) {
   if (!g_kt_on.load(std::memory_order_relaxed)) return;
-  start = xdna_hip_event_create(1);
-  stop = xdna_hip_event_create(1);
-  if (start && stop) xdna_hip_event_record(start, current_stream());
+  {
+    std::lock_guard<std::mutex> lock(g_kt_mu);
+    if (g_pool_next + 2 > event_pool().size()) return;
+    start = event_pool()[g_pool_next];
+    stop = event_pool()[g_pool_next + 1];
+    g_pool_next += 2;
+  }
+  xdna_hip_event_record(start, current_stream());
 }
 
 KernelTimer::~KernelTimer() {
@@ -587,11 +602,14 @@ KernelTimer::~KernelTimer() {
 
 void kernel_timing_enable(bool on) {
   std::lock_guard<std::mutex> lock(g_kt_mu);
-  for (auto& t : timed()) {
-    xdna_hip_event_destroy(t.start);
-    xdna_hip_event_destroy(t.stop);
+  auto& pool = event_pool();
+  while (on && pool.size() < kTimingEvents) {
+    void* e = xdna_hip_event_create(1);
+    if (!e) break;
+    pool.push_back(e);
   }
   timed().clear();
+  g_pool_next = 0;
   g_kt_on.store(on);
 }
 
