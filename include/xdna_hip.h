@@ -277,8 +277,10 @@ int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uin
 /* Kernel selection of xdna_gemm_bf16, for measurements and tests: 0 automatic (default),
  * 1 the 128 x 128 kernel (any strides, split-K for few long-K tiles), 2 the 256 x 256
  * kernel (8 waves; operands with a unit stride along k or along rows only, else 1 is
- * used).  No reference counterpart (a tuning knob).  XDNA_GEMM_VARIANT sets the initial
- * value. */
+ * used), 3 its four-wave form (one wave per SIMD with 128 x 128 wave tiles, software-
+ * pipelined; also needs K % 8 == 0 and rows % 8 == 0 for row-contiguous operands, else 2
+ * or 1; the automatic choice where it applies).  No reference counterpart (a tuning
+ * knob).  XDNA_GEMM_VARIANT sets the initial value. */
 int xdna_gemm_set_variant(int variant);
 
 /* ------------------------------------------------------------------------ */

@@ -355,6 +355,233 @@ void gemm2_kernel(GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Four-wave variant: the same 256 x 256 tile with k-tile 64, one wave per SIMD owning a
+// 128 x 128 block (4 x 4 MFMA tiles, accumulators in the AGPR half of the register
+// file): 8 fragment reads per 16 MFMAs.  Latency is covered by pipelining, not by a
+// second wave: fragments are read one k-step ahead (across k-tiles too), the global loads
+// of k-tile t+2 issue between the MFMAs of k-tile t's first two k-steps, and the barrier
+// that opens k-step 3 frees this k-tile's LDS buffer for them.  Loads are unconditional
+// (clamped addresses, zero-masked results), so the memory counters are static.  Needs
+// whole 8-element vectors: K % 8 == 0 for k-contiguous operands, rows % 8 == 0 for
+// row-contiguous ones (checked by the launcher).
+// ---------------------------------------------------------------------------------------
+constexpr int kT4 = 256, kK4 = 64, kP4 = 72;
+constexpr size_t kGemm4Lds = size_t(2) * 2 * kT4 * kP4 * 2;  // 2 buffers x (A, B)
+
+// One operand's loads through a buffer resource: per thread 8 vectors of 16 bytes per
+// k-tile.  The row part of each vector's offset is fixed for the workgroup (-1 for rows
+// past the operand); the k part moves with the k-tile.  A vector outside the operand gets
+// an offset past the resource's size, and the buffer load returns zeros for it: no
+// branch and no select on the data.
+struct G4Operand {
+  __amdgpu_buffer_rsrc_t rs;
+  int roff[8];   // row * s_r (elements), or -1
+  int kq[8];     // k offset of vector j within a k-tile
+  int s_k;
+};
+
+template <int kMode>
+__device__ inline G4Operand g4_operand(const uint16_t* src, int64_t s_r, int64_t s_k, int r0, int rows,
+                                       int K, int tid) {
+  G4Operand o;
+  // bytes up to the last element of the operand (< 2^31: checked by the launcher)
+  const int64_t extent = ((int64_t(rows) - 1) * s_r + (int64_t(K) - 1) * s_k + 1) * 2;
+  o.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), 0, int(extent), 0x00020000);
+  o.s_k = int(s_k);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int row;
+    if (kMode == kAlongK) {
+      // vector v = tid + 256 j: row v / 8, k [(v % 8) * 8, +8)
+      const int v = tid + j * 256;
+      row = r0 + (v >> 3);
+      o.kq[j] = (v & 7) * 8;
+    } else {
+      // rows [r0 + (tid % 32) * 8, +8) at k = ((tid / 32) + 8 (j / 4)) * 4 + j % 4
+      row = r0 + (tid & 31) * 8;
+      o.kq[j] = ((tid >> 5) + 8 * (j >> 2)) * 4 + (j & 3);
+    }
+    o.roff[j] = row < rows ? int(int64_t(row) * s_r) : -1;
+  }
+  return o;
+}
+
+__device__ inline void g4_load(u32x4_t (&r)[8], const G4Operand& o, int k0, int K) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k = k0 + o.kq[j];
+    const bool ok = o.roff[j] >= 0 && k < K;
+    const int off = ok ? (o.roff[j] + k * o.s_k) * 2 : 0x7FFFFFF0;
+    r[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(o.rs, off, 0, 0));
+  }
+}
+
+template <int kMode>
+__device__ inline void g4_store(uint16_t* lds, const u32x4_t (&r)[8], int tid) {
+  if (kMode == kAlongK) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int v = tid + j * 256;
+      *reinterpret_cast<u32x4_t*>(lds + (v >> 3) * kP4 + (v & 7) * 8) = r[j];
+    }
+  } else {
+    // r[4h + i] holds rows rg*8 .. +7 at k = (kq + 8h) * 4 + i: row e gets 4 k as two dwords
+    const int rg = tid & 31, kq = tid >> 5;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high / low halves
+        g2u2 w;
+        w[0] = __builtin_amdgcn_perm(r[4 * h + 1][e >> 1], r[4 * h][e >> 1], sel);
+        w[1] = __builtin_amdgcn_perm(r[4 * h + 3][e >> 1], r[4 * h + 2][e >> 1], sel);
+        *reinterpret_cast<g2u2*>(lds + (rg * 8 + e) * kP4 + (kq + 8 * h) * 4) = w;
+      }
+  }
+}
+
+template <int kModeA, int kModeB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm4_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kT4, n0 = blockIdx.x * kT4;
+  const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
+  const int kbeg = split * g.kt_per * kK4, kend = min(g.K, kbeg + g.kt_per * kK4);
+  const int ntiles = kend > kbeg ? (kend - kbeg + kK4 - 1) / kK4 : 0;
+  const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
+  const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = zero_acc();
+
+  u32x4_t ra[8], rb[8];
+  u32x4_t fa[2][4], fb[2][4];
+  const G4Operand oa = g4_operand<kModeA>(A, g.a_r, g.a_k, m0, g.M, g.K, tid);
+  const G4Operand ob = g4_operand<kModeB>(B, g.b_r, g.b_k, n0, g.N, g.K, tid);
+  // k-tile t lives in LDS buffer t % 2: A at [256][kP4], then B
+  auto abuf = [&](int t) { return smem + (t & 1) * 2 * kT4 * kP4; };
+#define XDNA_G4_LOAD(t_)                                                                     \
+  do {                                                                                       \
+    const int k_ = kbeg + min((t_), ntiles - 1) * kK4;                                       \
+    g4_load(ra, oa, k_, kend);                                                               \
+    g4_load(rb, ob, k_, kend);                                                               \
+  } while (0)
+#define XDNA_G4_STORE(t_)                                                                    \
+  do {                                                                                       \
+    g4_store<kModeA>(abuf(t_), ra, tid);                                                     \
+    g4_store<kModeB>(abuf(t_) + kT4 * kP4, rb, tid);                                         \
+  } while (0)
+#define XDNA_G4_FRAGS(buf_, t_, ks_)                                                         \
+  do {                                                                                       \
+    const uint16_t* as_ = abuf(t_) + (wm * 128 + lr) * kP4 + lk + (ks_) * 16;                 \
+    const uint16_t* bs_ = abuf(t_) + kT4 * kP4 + (wn * 128 + lr) * kP4 + lk + (ks_) * 16;     \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                            \
+      fa[buf_][i] = *reinterpret_cast<const u32x4_t*>(as_ + i * 32 * kP4);                   \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j)                                            \
+      fb[buf_][j] = *reinterpret_cast<const u32x4_t*>(bs_ + j * 32 * kP4);                   \
+  } while (0)
+#define XDNA_G4_MFMA(buf_)                                                                   \
+  do {                                                                                       \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                            \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j)                                          \
+        acc[i][j] = mfma_32x32x16(as_bf16x8(fa[buf_][i]), as_bf16x8(fb[buf_][j]), acc[i][j]); \
+  } while (0)
+
+  if (ntiles > 0) {
+    // prologue: k-tiles 0 and 1 in LDS
+    XDNA_G4_LOAD(0);
+    XDNA_G4_STORE(0);
+    XDNA_G4_LOAD(1);
+    XDNA_G4_STORE(1);
+    __syncthreads();
+    XDNA_G4_FRAGS(0, 0, 0);
+    constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100, kDsWr = 0x200;
+    for (int t = 0; t < ntiles; ++t) {
+#pragma unroll
+      for (int ks = 0; ks < 3; ++ks) {
+        const int cur = ks & 1;
+        XDNA_G4_FRAGS(cur ^ 1, t, ks + 1);
+        if (ks == 0) XDNA_G4_LOAD(t + 2);    // k-tile t+2 into registers
+        XDNA_G4_MFMA(cur);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+          if (ks == 0) __builtin_amdgcn_sched_group_barrier(kVmemRd, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // every wave has read this k-tile's buffer for the last time (k-step 3's fragments)
+      __syncthreads();
+      XDNA_G4_FRAGS(0, t + 1, 0);            // k-tile t+1: stored one k-tile ago
+      XDNA_G4_STORE(t + 2);                  // into this k-tile's buffer
+      XDNA_G4_MFMA(1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsWr, kModeA == kAlongK && kModeB == kAlongK ? 2 : 4, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#undef XDNA_G4_LOAD
+#undef XDNA_G4_STORE
+#undef XDNA_G4_FRAGS
+#undef XDNA_G4_MFMA
+
+  if (g.part) {
+    float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 128 + j * 32 + lr;
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 128 + i * 32 + mfma_row(r, lane);
+          if (m < g.M) P[int64_t(m) * g.N + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
+  uint16_t* C = g.c + int64_t(batch) * g.c_batch;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 128 + j * 32 + lr;
+      if (n >= g.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 128 + i * 32 + mfma_row(r, lane);
+        if (m >= g.M) continue;
+        float v = g.alpha * acc[i][j][r];
+        if (g.bias_mode && g.beta != 0.0f) {
+          float bv;
+          if (g.bias_mode == 1) bv = bf16_to_f32(g.bias[int64_t(n) * g.bias_sn]);
+          else if (g.bias_mode == 2) bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm + int64_t(n) * g.bias_sn]);
+          else bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm]);
+          v += g.beta * bv;
+        }
+        C[int64_t(m) * g.c_m + int64_t(n) * g.c_n] = f32_to_bf16(v);
+      }
+    }
+}
+
 // Split-K epilogue: C[b][m][n] = bf16(alpha * sum over splits (in split order) of the fp32
 // partials + beta * bias term), consecutive threads on consecutive n.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs g) {
@@ -399,6 +626,16 @@ template <int MA, int MB>
 bool launch2(dim3 grid, hipStream_t st, const GemmArgs& g) {
   if (!gemm2_lds_ok<MA, MB>()) return false;
   gemm2_kernel<MA, MB><<<grid, 512, kGemm2Lds, st>>>(g);
+  return true;
+}
+
+template <int MA, int MB>
+bool launch4(dim3 grid, hipStream_t st, const GemmArgs& g) {
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm4_kernel<MA, MB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(kGemm4Lds)) == hipSuccess;
+  if (!ok) return false;
+  gemm4_kernel<MA, MB><<<grid, 256, kGemm4Lds, st>>>(g);
   return true;
 }
 
@@ -462,12 +699,23 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   if (!admit_launch("xdna_gemm_bf16")) return -1;
   g.batch = batch;
   hipStream_t st2 = as_stream(stream);
-  // Large tiles (256 x 256, 8 waves) when neither operand needs scalar staging and the
-  // grid still has enough tiles; xdna_gemm_set_variant overrides (1 small, 2 large).
+  // Large tiles (256 x 256) when neither operand needs scalar staging and the grid still
+  // has enough tiles: the four-wave kernel where its whole-vector loads fit the shape, else
+  // the eight-wave one; xdna_gemm_set_variant overrides (1 small, 2 eight-wave, 3 four-wave).
   const int variant = g_gemm_variant.load();
   const int64_t tiles2 = ceil_div(N, kT2) * ceil_div(M, kT2) * int64_t(batch);
   const bool vec_ok = ma != kScalar && mb != kScalar;
-  if (vec_ok && K > 0 && (variant == 2 || (variant == 0 && tiles2 >= 64))) {
+  // buffer-resource offsets are 32-bit: each operand (one batch element) under 2 GiB
+  const auto extent = [](int rows, int64_t s_r, int64_t s_k, int k) {
+    return ((int64_t(rows) - 1) * s_r + (int64_t(k) - 1) * s_k + 1) * 2;
+  };
+  const bool fits4 = vec_ok && K > 0 && (K % 8) == 0 && (ma != kAlongRow || (M % 8) == 0) &&
+                     (mb != kAlongRow || (N % 8) == 0) && extent(M, lda_m, lda_k, K) < (int64_t(1) << 31) &&
+                     extent(N, ldb_n, ldb_k, K) < (int64_t(1) << 31);
+  // the four-wave kernel's longer prologue and epilogue (one wave per SIMD) only pay off
+  // over a long K (measured on config 3's GEMMs: ahead from K = 4096, behind at 1024)
+  const bool use4 = fits4 && (variant == 3 || (variant == 0 && tiles2 >= 64 && K >= 2048));
+  if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && tiles2 >= 64))) {
     // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
     const int kt2 = int(ceil_div(K, kK2));
     g.nsplit = 1;
@@ -486,11 +734,17 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
     }
     const dim3 grid2(unsigned(ceil_div(N, kT2)), unsigned(ceil_div(M, kT2)), unsigned(batch * g.nsplit));
     bool ok;
-    if (ma == kAlongK) ok = mb == kAlongK ? launch2<kAlongK, kAlongK>(grid2, st2, g) : launch2<kAlongK, kAlongRow>(grid2, st2, g);
-    else ok = mb == kAlongK ? launch2<kAlongRow, kAlongK>(grid2, st2, g) : launch2<kAlongRow, kAlongRow>(grid2, st2, g);
+    if (use4) {
+      if (ma == kAlongK) ok = mb == kAlongK ? launch4<kAlongK, kAlongK>(grid2, st2, g) : launch4<kAlongK, kAlongRow>(grid2, st2, g);
+      else ok = mb == kAlongK ? launch4<kAlongRow, kAlongK>(grid2, st2, g) : launch4<kAlongRow, kAlongRow>(grid2, st2, g);
+    } else if (ma == kAlongK) {
+      ok = mb == kAlongK ? launch2<kAlongK, kAlongK>(grid2, st2, g) : launch2<kAlongK, kAlongRow>(grid2, st2, g);
+    } else {
+      ok = mb == kAlongK ? launch2<kAlongRow, kAlongK>(grid2, st2, g) : launch2<kAlongRow, kAlongRow>(grid2, st2, g);
+    }
     if (!ok) {
       if (g.part) xdna_hip_cache_free(g.part);
-      set_error("xdna_gemm_bf16: cannot enable the large-tile kernel's LDS size");
+      set_error("xdna_gemm_bf16: cannot enable a large-tile kernel's LDS size");
       return -1;
     }
     if (g.nsplit > 1) {
@@ -534,8 +788,8 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
 }
 
 extern "C" int xdna_gemm_set_variant(int variant) {
-  if (variant < 0 || variant > 2) {
-    set_error("xdna_gemm_set_variant: variant must be 0..2");
+  if (variant < 0 || variant > 3) {
+    set_error("xdna_gemm_set_variant: variant must be 0..3");
     return -1;
   }
   g_gemm_variant.store(variant);
