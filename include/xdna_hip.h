@@ -145,6 +145,30 @@ int xdna_conv3x3w_pack_input_strips_range_bf16(const uint16_t* src, uint16_t* ds
 int xdna_conv3x3w_pack_input_dense_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H,
                                         int W, void* stream);
 
+/* BFP16 weight codec (the reference's NPU weight wire format, bit-exact).
+ * Replaces xdna_conv3x3w_pack_weights_bfp16 (conv_pack.cpp:398-443; spec
+ * conv3x3w_host.py:49-82): OIHW bf16 [Cout][Cin][3][3] -> bfp16ebs8 bytes for output
+ * channels [128*n_block, +128), blocks [chunk*9+tap][n/16][k/8][2][8 n][8 k] of 9 bytes
+ * (largest biased exponent, then 8 int8 mantissas round(v * 2^(133-e)) clamped to
+ * [-128, 127]); channels past Cin / Cout encode as zeros.  Same arguments as the
+ * reference plus the stream; dst holds xdna_conv3x3w_weights_bfp16_bytes(chunks) bytes,
+ * 16-byte aligned. */
+int xdna_conv3x3w_pack_weights_bfp16(const uint16_t* w, uint8_t* dst, int Cout, int Cin, int chunks,
+                                     int n_block, void* stream);
+/* Replaces xdna_conv3x3w_pack_weights_dx_bfp16 (conv_pack.cpp:474-519): the same bytes
+ * for the dX conv's weights w'[ci][co][dy][dx] = w[co][ci][2-dy][2-dx], read from the
+ * forward weight w [Cout_fwd][Cin_fwd][3][3]; chunks = ceil(Cout_fwd / 64), n_block over
+ * Cin_fwd. */
+int xdna_conv3x3w_pack_weights_dx_bfp16(const uint16_t* w, uint8_t* dst, int Cout_fwd, int Cin_fwd,
+                                        int chunks, int n_block, void* stream);
+/* Bytes of one 128-channel block of BFP16 weights: chunks * 9 * 64 * 128 * 9 / 8
+ * (the reference's b_bytes, torch_xdna_device.cpp:2352-2367). */
+size_t xdna_conv3x3w_weights_bfp16_bytes(int chunks);
+/* No reference counterpart (the reference decodes inside its NPU kernel): 9-byte BFP16
+ * blocks -> 8 floats each, v = int8 mantissa * 2^(e - 133); for tests and for
+ * reproducing the NPU's weight rounding. */
+int xdna_bfp16_decode_f32(const uint8_t* src, float* dst, int64_t nblocks, void* stream);
+
 /* Replaces xdna_conv3x3w_unpack_output_bf16 (conv_pack.cpp:447-466):
  * [groups*2048][128] bf16 rows -> channel slice [c_start, c_start+cout_valid)
  * of NCHW [B][C_total][H][W] (valid pixels only). */

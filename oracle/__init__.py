@@ -7,9 +7,9 @@ product path (``pytorch-xdna2_amd/``) never imports, links or runs it.
 Contents:
 
 * ``liboracle.so`` (``oracle.c``): plain-C restatements of the conv3x3w layouts
-  (pack / unpack, with strips, halo_zero and group ranges), the direct 3x3
-  convolution forward / input-gradient / weight-gradient / bias-gradient in double
-  precision, and the fused Adam step.
+  (pack / unpack, with strips, halo_zero and group ranges), the BFP16 weight codec
+  (forward and dX forms), the direct 3x3 convolution forward / input-gradient /
+  weight-gradient / bias-gradient in double precision, and the fused Adam step.
 * numpy helpers: bf16 rounding, the GEMM reference (float64 products of bf16 values),
   and the layout geometry.
 * ``ref_pack()``: the reference's own ``conv_pack.cpp`` compiled in place into
@@ -19,7 +19,8 @@ Contents:
 Pinning (what proves each function right) is recorded in the tests that use it:
 ``tests/test_oracle_layouts.py`` (reference build + committed golden digests + layout
 invariants), ``tests/test_oracle_conv.py`` (brute force, closed forms, linearity,
-torch CPU fp32 convolution), ``tests/test_oracle_adam.py`` (golden vectors from
+torch CPU fp32 convolution), ``tests/test_oracle_bfp16.py`` (reference build + committed
+golden digests + closed forms), ``tests/test_oracle_adam.py`` (golden vectors from
 torch's CPU ``_fused_adam_`` + known-answer steps), ``tests/test_oracle_gemm.py``.
 """
 from __future__ import annotations
@@ -61,6 +62,7 @@ def lib():
         _lib.oracle_conv3x3_wgrad.argtypes = [P, P, P, P, I, I, I, I, I]
         _lib.oracle_adam.argtypes = [P, P, P, P, P, L, I, D, D, D, D, D, D, I, I, I, D, I]
         _lib.oracle_strip_geometry.argtypes = [I, ctypes.POINTER(I), ctypes.POINTER(I)]
+        _lib.oracle_pack_weights_bfp16.argtypes = [P, P, I, I, I, I, I, I]
     return _lib
 
 
@@ -77,6 +79,8 @@ def ref_pack():
         _ref.xdna_conv3x3w_pack_input_bf16.argtypes = [P, P, I, I, I, I, I]
         _ref.xdna_conv3x3w_unpack_output_bf16.argtypes = [P, P, I, I, I, I, I, I]
         _ref.xdna_conv_set_threads.argtypes = [I]
+        _ref.xdna_conv3x3w_pack_weights_bfp16.argtypes = [P, P, I, I, I, I]
+        _ref.xdna_conv3x3w_pack_weights_dx_bfp16.argtypes = [P, P, I, I, I, I]
     return _ref
 
 
@@ -215,3 +219,37 @@ def adam_(p, g, m, v, mx, step, lr=1e-3, beta1=0.9, beta2=0.999, weight_decay=0.
                       mx.ctypes.data if amsgrad else None, p.size, dtype, float(step), lr, beta1,
                       beta2, weight_decay, eps, int(amsgrad), int(maximize), int(adamw),
                       0.0 if grad_scale is None else float(grad_scale), int(grad_scale is not None))
+
+
+# ---------------------------------------------------------------------------
+# BFP16 weight codec
+# ---------------------------------------------------------------------------
+
+BFP16_BYTES_PER_CHUNK = 9 * 8 * 8 * 2 * 8 * 9   # one 128-channel block: 82,944 per chunk
+
+
+def pack_weights_bfp16(w_bits: np.ndarray, chunks: int, n_block: int) -> np.ndarray:
+    """OIHW bf16 bits -> bfp16ebs8 bytes of output channels [128 n_block, +128)."""
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    cout, cin = w.shape[:2]
+    out = np.zeros(chunks * BFP16_BYTES_PER_CHUNK, np.uint8)
+    lib().oracle_pack_weights_bfp16(w.ctypes.data, out.ctypes.data, cout, cin, cin, chunks, n_block, 0)
+    return out
+
+
+def pack_weights_dx_bfp16(w_bits: np.ndarray, chunks: int, n_block: int) -> np.ndarray:
+    """The dX conv's bfp16 weights, read from the forward weight [Cout_fwd][Cin_fwd][3][3]."""
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    cout_fwd, cin_fwd = w.shape[:2]
+    out = np.zeros(chunks * BFP16_BYTES_PER_CHUNK, np.uint8)
+    lib().oracle_pack_weights_bfp16(w.ctypes.data, out.ctypes.data, cin_fwd, cout_fwd, cin_fwd, chunks,
+                                    n_block, 1)
+    return out
+
+
+def bfp16_decode(blocks: np.ndarray) -> np.ndarray:
+    """9-byte blocks -> float64 values (int8 mantissa * 2^(e - 133))."""
+    b = np.asarray(blocks, np.uint8).reshape(-1, 9)
+    e = b[:, :1].astype(np.int64)
+    m = b[:, 1:].view(np.int8).astype(np.float64)
+    return np.ldexp(m, e - 133).reshape(-1)

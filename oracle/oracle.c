@@ -281,3 +281,48 @@ void oracle_adam(void* p_, void* g_, void* m_, void* v_, void* mx_, int64_t n, i
     }
   }
 }
+
+/*
+ * BFP16 ("bfp16ebs8") weight encoding for output channels [128 n_block, +128).
+ * Spec: conv3x3w_host.py:49-82 (bfp16_encode: per 8 consecutive values, exponent byte =
+ * largest biased fp32 exponent, mantissas = clip(rint(v / 2^(e-127-6)), -128, 127);
+ * atb_shuffle: blocks [kb][n/16][k/8][2][8 n][8 k]; pack_weights: K order (chunk, dy, dx,
+ * c), zero padding past Cin / Cout).  Host code: conv_pack.cpp:398-443 (forward: element
+ * (n, c, t) = w[n][c][t], ld = Cin) and :474-519 (dx = 1: the dX conv's weights
+ * w'[ci][co][t] = w[co][ci][8-t] read from the forward weight; Cout and Cin are the dX
+ * conv's own channel counts, i.e. Cin_fwd and Cout_fwd, and ld = Cin_fwd).
+ * The rounding is done in double, where v * 2^(133-e) is exact; NaN encodes as 0 (the
+ * reference's int conversion of NaN on x86 gives INT_MIN, whose low byte is 0).
+ */
+void oracle_pack_weights_bfp16(const uint16_t* w, uint8_t* dst, int Cout, int Cin, int ld, int chunks,
+                               int n_block, int dx) {
+  uint8_t* out = dst;
+  for (int kb = 0; kb < chunks * 9; ++kb) {
+    const int chunk = kb / 9, tap = kb % 9;
+    for (int n16 = 0; n16 < 8; ++n16)
+      for (int k8 = 0; k8 < 8; ++k8)
+        for (int two = 0; two < 2; ++two)
+          for (int nl = 0; nl < 8; ++nl) {
+            const int n = 128 * n_block + n16 * 16 + two * 8 + nl;
+            float v[8];
+            int emax = 0;
+            for (int kl = 0; kl < 8; ++kl) {
+              const int c = chunk * KSTEP + k8 * 8 + kl;
+              uint16_t h = 0;
+              if (c < Cin && n < Cout)
+                h = dx ? w[((size_t)c * ld + n) * 9 + (8 - tap)] : w[((size_t)n * ld + c) * 9 + tap];
+              v[kl] = bf16f(h);
+              const int e = (h >> 7) & 0xFF;
+              if (e > emax) emax = e;
+            }
+            *out++ = (uint8_t)emax;
+            for (int kl = 0; kl < 8; ++kl) {
+              double q = nearbyint(ldexp((double)v[kl], 133 - emax));
+              if (isnan(q)) q = 0.0;
+              if (q < -128.0) q = -128.0;
+              if (q > 127.0) q = 127.0;
+              *out++ = (uint8_t)(int8_t)(int)q;
+            }
+          }
+  }
+}

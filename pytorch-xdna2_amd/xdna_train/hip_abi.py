@@ -59,6 +59,10 @@ SIGNATURES = {
     "xdna_conv3x3w_pack_input_range_bf16": (I, [P, P, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_pack_input_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_pack_input_dense_bf16": (I, [P, P, I, I, I, I, P]),
+    "xdna_conv3x3w_pack_weights_bfp16": (I, [P, P, I, I, I, I, P]),
+    "xdna_conv3x3w_pack_weights_dx_bfp16": (I, [P, P, I, I, I, I, P]),
+    "xdna_conv3x3w_weights_bfp16_bytes": (Z, [I]),
+    "xdna_bfp16_decode_f32": (I, [P, P, L, P]),
     "xdna_conv3x3w_unpack_output_bf16": (I, [P, P, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),

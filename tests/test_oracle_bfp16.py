@@ -1,0 +1,138 @@
+"""Pins the oracle's BFP16 weight codec restatement (oracle_pack_weights_bfp16).
+
+1. Golden digests of the reference's own conv_pack.cpp (tests/golden/bfp16_golden.json,
+   written by tests/golden/make_bfp16_golden.py from oracle/_ref): the reference test's
+   channel counts and weight recipe (run_conv3x3w_pack.py:63-67: mixed scales, zeros,
+   exact ties, all-zero blocks), plus +-inf / NaN / subnormal values and every bf16 bit
+   pattern, forward and dX forms.
+2. The reference build itself, where present, on other seeds.
+3. What the format fixes on its own: an all-zero block is nine zero bytes; a block's
+   largest element lands in [64, 127] (its exponent byte is that element's exponent);
+   powers of two and exact ties round to even; decode(encode(w)) is within half a step
+   of w (one step = 2^(e_max - 133)) except where the 127 clamp applies; the dX form is
+   the forward form of the flipped, transposed weight.
+"""
+import hashlib
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+
+sys.path.insert(0, str(Path(__file__).parent / "golden"))
+from make_bfp16_golden import bfp16_weights  # noqa: E402
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "bfp16_golden.json").read_text())["cases"]
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.mark.parametrize("case", GOLDEN, ids=lambda c: f"ci{c['cin']}co{c['cout']}{c['kind']}")
+def test_matches_reference_digests(case):
+    cin, cout = case["cin"], case["cout"]
+    w = bfp16_weights(cin, cout, case["kind"], case["seed"])
+    chunks = -(-cin // 64)
+    for nb, digest in enumerate(case["fwd"]):
+        assert _sha(oracle.pack_weights_bfp16(w, chunks, nb)) == digest, f"fwd block {nb}"
+    for nb, digest in enumerate(case["dx"]):
+        assert _sha(oracle.pack_weights_dx_bfp16(w, -(-cout // 64), nb)) == digest, f"dx block {nb}"
+
+
+@pytest.mark.skipif(oracle.ref_pack() is None, reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("cin,cout,kind", [(130, 200, "recipe"), (64, 72, "special"), (9, 300, "recipe")])
+def test_matches_reference_build(cin, cout, kind):
+    ref = oracle.ref_pack()
+    w = np.ascontiguousarray(bfp16_weights(cin, cout, kind, 77))
+    chunks = -(-cin // 64)
+    for nb in range(-(-cout // 128)):
+        want = np.zeros(chunks * oracle.BFP16_BYTES_PER_CHUNK, np.uint8)
+        ref.xdna_conv3x3w_pack_weights_bfp16(w.ctypes.data, want.ctypes.data, cout, cin, chunks, nb)
+        np.testing.assert_array_equal(oracle.pack_weights_bfp16(w, chunks, nb), want)
+    dchunks = -(-cout // 64)
+    for nb in range(-(-cin // 128)):
+        want = np.zeros(dchunks * oracle.BFP16_BYTES_PER_CHUNK, np.uint8)
+        ref.xdna_conv3x3w_pack_weights_dx_bfp16(w.ctypes.data, want.ctypes.data, cout, cin, dchunks, nb)
+        np.testing.assert_array_equal(oracle.pack_weights_dx_bfp16(w, dchunks, nb), want)
+
+
+def _blocks(w_bits, chunks=1, nb=0):
+    return oracle.pack_weights_bfp16(w_bits, chunks, nb).reshape(-1, 9)
+
+
+def _block_values(w_bits, cin):
+    """Values of every block of a one-chunk encoding, in block order (zero-padded)."""
+    cout = w_bits.shape[0]
+    v = np.zeros((9, 8, 8, 2, 8, 8), np.float64)  # [tap][n16][k8][two][nl][kl]
+    f = oracle.bf16_value(w_bits).astype(np.float64)
+    for tap in range(9):
+        for n in range(min(cout, 128)):
+            for c in range(min(cin, 64)):
+                v[tap, n // 16, c // 8, (n % 16) // 8, n % 8, c % 8] = f[n, c, tap // 3, tap % 3]
+    return v.reshape(-1, 8)
+
+
+def test_zero_blocks_are_zero_bytes():
+    w = np.zeros((128, 64, 3, 3), np.uint16)
+    assert not _blocks(w).any()
+
+
+def test_block_maximum_and_round_trip():
+    rng = np.random.default_rng(5)
+    w = oracle.bf16_bits((rng.standard_normal((128, 64, 3, 3)) * np.exp(rng.uniform(-8, 8, (128, 64, 1, 1))))
+                         .astype(np.float32))
+    blk = _blocks(w)
+    vals = _block_values(w, 64)
+    e = blk[:, 0].astype(np.int64)
+    m = blk[:, 1:].view(np.int8).astype(np.int64)
+    # the exponent byte is the largest element's biased exponent ...
+    want_e = np.frexp(np.abs(vals).max(axis=1))[1] + 126
+    want_e[np.abs(vals).max(axis=1) == 0] = 0
+    np.testing.assert_array_equal(e, want_e)
+    # ... whose mantissa lands in [64, 127] (or -128 after rounding a negative up)
+    big = np.abs(m).max(axis=1)
+    assert ((big >= 64) & (big <= 128)).all()
+    # decode within half a step, where no clamp applied
+    step = np.ldexp(1.0, e - 133)[:, None]
+    dec = oracle.bfp16_decode(blk).reshape(-1, 8)
+    free = (m > -128) & (m < 127)
+    assert (np.abs(dec - vals)[free] <= step.repeat(8, 1)[free] / 2).all()
+
+
+def test_ties_round_to_even():
+    # block maximum 1.0 (exponent 127): one step is 2^-6; values k/128 are exact ties
+    w = np.zeros((128, 64, 3, 3), np.float32)
+    w[0, :8, 1, 1] = [1.0, 1.5 / 64, 2.5 / 64, -1.5 / 64, 0.5 / 64, 3.5 / 64, 127.5 / 64, 126.5 / 64]
+    blk = _blocks(oracle.bf16_bits(w))
+    # tap 4, n = 0, k8 = 0 -> block index ((4 * 8 + 0) * 8 + 0) * 16 + 0
+    b = blk[(4 * 8 * 8) * 16]
+    assert b[0] == 127
+    np.testing.assert_array_equal(b[1:].view(np.int8), [64, 2, 2, -2, 0, 4, 127, 126])
+
+
+def test_special_values():
+    w = np.zeros((128, 64, 3, 3), np.uint16)
+    w[0, :8, 0, 0] = [0x7F80, 0xFF80, 0x7FC0, 0x3F80, 0x0000, 0x8000, 0x0001, 0xC000]  # +inf -inf nan 1 0 -0 sub -2
+    b = _blocks(w)[0]
+    assert b[0] == 255
+    # +inf saturates to 127, -inf to -128, NaN gives 0; finite values vanish next to 2^128
+    np.testing.assert_array_equal(b[1:].view(np.int8), [127, -128, 0, 0, 0, 0, 0, 0])
+    w2 = np.zeros((128, 64, 3, 3), np.uint16)
+    w2[0, :8, 0, 0] = [0x0001, 0x007F, 0x8040, 0, 0, 0, 0, 0]     # bf16 subnormals only
+    b2 = _blocks(w2)[0]
+    assert b2[0] == 0                                           # exponent field 0
+    np.testing.assert_array_equal(b2[1:].view(np.int8), [1, 127, -64, 0, 0, 0, 0, 0])
+
+
+def test_dx_form_is_forward_form_of_flipped_transpose():
+    rng = np.random.default_rng(9)
+    w = oracle.bf16_bits(rng.standard_normal((96, 80, 3, 3)).astype(np.float32))
+    wdx = np.ascontiguousarray(w[:, :, ::-1, ::-1].transpose(1, 0, 2, 3))   # [Cin_fwd][Cout_fwd]
+    chunks = -(-96 // 64)
+    for nb in range(1):
+        np.testing.assert_array_equal(oracle.pack_weights_dx_bfp16(w, chunks, nb),
+                                      oracle.pack_weights_bfp16(wdx, chunks, nb))
