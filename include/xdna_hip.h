@@ -252,6 +252,25 @@ int xdna_conv3x3_prepare_weights_bf16(const uint16_t* w, uint16_t* wt, int Cout,
 int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
                            uint16_t* y, int B, int cin, int cout, int H, int W, void* stream);
 
+/* General 2-D convolution, bf16 in/out, fp32 accumulation: any kernel size, stride and
+ * padding (dilation 1, groups 1), NCHW activations and OIHW weights.  Replaces the
+ * reference's CPU route for convolutions outside its 3x3 path
+ * (convolution_overrideable_xdna / convolution_backward_overrideable_xdna falling back to
+ * aten::convolution on host aliases, torch_xdna_device.cpp:4594-4604, 4862-4874).
+ * Output size Ho = (H + 2 ph - KH) / sh + 1 (likewise Wo).  Forward: y [B][Cout][Ho][Wo]
+ * (+ bias [Cout] or null).  dgrad: dx [B][Cin][H][W] from dy [B][Cout][Ho][Wo].  wgrad:
+ * gw [Cout][Cin][KH][KW] and, when gb is not null, the bias gradient [Cout]; its pixel
+ * reduction is split over workgroups and summed in a fixed order (same bits every call).
+ * Every tensor below 2^31 elements. */
+int xdna_conv2d_fwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* y, int B,
+                         int Cin, int Cout, int H, int W, int KH, int KW, int sh, int sw, int ph, int pw,
+                         void* stream);
+int xdna_conv2d_dgrad_bf16(const uint16_t* dy, const uint16_t* w, uint16_t* dx, int B, int Cin, int Cout,
+                           int H, int W, int KH, int KW, int sh, int sw, int ph, int pw, void* stream);
+int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, uint16_t* gb, int B, int Cin,
+                           int Cout, int H, int W, int KH, int KW, int sh, int sw, int ph, int pw,
+                           void* stream);
+
 /* Kernel selection of xdna_conv3x3_rows_bf16 (and the conv calls built on it), for
  * measurements and tests: 0 automatic (default), 1 the main kernel (128 output channels
  * x 64-256 rows per workgroup, weights streamed from L2 per tap), 2 / 3 the small-grid

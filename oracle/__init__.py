@@ -253,3 +253,66 @@ def bfp16_decode(blocks: np.ndarray) -> np.ndarray:
     e = b[:, :1].astype(np.int64)
     m = b[:, 1:].view(np.int8).astype(np.float64)
     return np.ldexp(m, e - 133).reshape(-1)
+
+
+# ---------------------------------------------------------------------------
+# General 2-D convolution (any kernel, stride, padding; dilation 1, groups 1), float64
+# of bf16 operands.  The reference runs these on PyTorch's CPU kernels
+# (torch_xdna_device.cpp:4524-4606, 4608-4885); restated here as sums over the kernel
+# taps of strided slices of the zero-padded input.
+# ---------------------------------------------------------------------------
+
+def _f64(bits):
+    return bf16_value(bits).astype(np.float64)
+
+
+def conv2d_out_size(H, W, KH, KW, sh, sw, ph, pw):
+    return (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+
+
+def conv2d_fwd(x_bits, w_bits, bias_bits=None, stride=(1, 1), padding=(0, 0)):
+    x, w = _f64(x_bits), _f64(w_bits)
+    B, Cin, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    (sh, sw), (ph, pw) = stride, padding
+    Ho, Wo = conv2d_out_size(H, W, KH, KW, sh, sw, ph, pw)
+    xp = np.zeros((B, Cin, H + 2 * ph, W + 2 * pw))
+    xp[:, :, ph:ph + H, pw:pw + W] = x
+    y = np.zeros((B, Cout, Ho, Wo))
+    for ky in range(KH):
+        for kx in range(KW):
+            sl = xp[:, :, ky:ky + sh * (Ho - 1) + 1:sh, kx:kx + sw * (Wo - 1) + 1:sw]
+            y += np.einsum("bchw,oc->bohw", sl, w[:, :, ky, kx], optimize=True)
+    if bias_bits is not None:
+        y += _f64(bias_bits)[None, :, None, None]
+    return y
+
+
+def conv2d_dgrad(dy_bits, w_bits, in_hw, stride=(1, 1), padding=(0, 0)):
+    dy, w = _f64(dy_bits), _f64(w_bits)
+    B, Cout, Ho, Wo = dy.shape
+    _, Cin, KH, KW = w.shape
+    (sh, sw), (ph, pw) = stride, padding
+    H, W = in_hw
+    dxp = np.zeros((B, Cin, max(H + 2 * ph, sh * (Ho - 1) + KH), max(W + 2 * pw, sw * (Wo - 1) + KW)))
+    for ky in range(KH):
+        for kx in range(KW):
+            dxp[:, :, ky:ky + sh * (Ho - 1) + 1:sh, kx:kx + sw * (Wo - 1) + 1:sw] += np.einsum(
+                "bohw,oc->bchw", dy, w[:, :, ky, kx], optimize=True)
+    return dxp[:, :, ph:ph + H, pw:pw + W]
+
+
+def conv2d_wgrad(x_bits, dy_bits, kernel, stride=(1, 1), padding=(0, 0)):
+    x, dy = _f64(x_bits), _f64(dy_bits)
+    B, Cin, H, W = x.shape
+    _, Cout, Ho, Wo = dy.shape
+    KH, KW = kernel
+    (sh, sw), (ph, pw) = stride, padding
+    xp = np.zeros((B, Cin, H + 2 * ph, W + 2 * pw))
+    xp[:, :, ph:ph + H, pw:pw + W] = x
+    gw = np.zeros((Cout, Cin, KH, KW))
+    for ky in range(KH):
+        for kx in range(KW):
+            sl = xp[:, :, ky:ky + sh * (Ho - 1) + 1:sh, kx:kx + sw * (Wo - 1) + 1:sw]
+            gw[:, :, ky, kx] = np.einsum("bohw,bchw->oc", dy, sl, optimize=True)
+    return gw, dy.sum(axis=(0, 2, 3))

@@ -63,6 +63,9 @@ SIGNATURES = {
     "xdna_conv3x3w_pack_weights_dx_bfp16": (I, [P, P, I, I, I, I, P]),
     "xdna_conv3x3w_weights_bfp16_bytes": (Z, [I]),
     "xdna_bfp16_decode_f32": (I, [P, P, L, P]),
+    "xdna_conv2d_fwd_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),
+    "xdna_conv2d_dgrad_bf16": (I, [P, P, P] + [I] * 11 + [P]),
+    "xdna_conv2d_wgrad_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),
     "xdna_conv3x3w_unpack_output_bf16": (I, [P, P, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_unpack_output_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
