@@ -43,7 +43,7 @@ struct GArgs {
 // Element (row, k) of operand A and (col, k) of operand B, with the per-thread row state
 // precomputed once.  Out-of-range elements are zero.
 struct RowState {
-  int valid;
+  bool valid;
   int b, y0, x0;   // fwd B: image, oy*sh-ph, ox*sw-pw;  dgrad B: image, iy+ph, ix+pw
   int ci, ky, kx;  // wgrad B: the (ci, ky, kx) of the column
 };
@@ -75,39 +75,54 @@ __device__ inline RowState b_row(const GArgs& a, int n) {
   return r;
 }
 
-// B operand: elements (n, k0 .. k0+15) packed as bf16 pairs into u[8]
-template <int DIR>
+// Every gather below is branch-free: the address of an out-of-range element is replaced by
+// the operand's first element and the loaded value is masked, so all loads of a k-tile
+// are in flight together (a branch per element would serialise them, one memory latency
+// each).
+// offsets are 32-bit: every operand holds fewer than 2^31 elements (checked on entry)
+__device__ inline uint32_t ld_masked(const uint16_t* base, int off, bool ok) {
+  const uint32_t v = base[ok ? off : 0];
+  return ok ? v : 0u;
+}
+
+// B operand: elements (n, k0 .. k0+15) packed as bf16 pairs into u[8].  S1: unit strides
+// (dgrad needs no division then).
+template <int DIR, bool S1>
 __device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint32_t (&u)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) u[i] = 0;
-  if (!r.valid) return;
   if (DIR == kGFwd) {
     const int khw = a.KH * a.KW;
     int ci = k0 / khw, rem = k0 - ci * khw;
     int ky = rem / a.KW, kx = rem - ky * a.KW;
+    const int img = r.b * a.Cin;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int iy = r.y0 + ky, ix = r.x0 + kx;
-      uint32_t v = 0;
-      if (k0 + e < a.K && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
-        v = a.x[((int64_t(r.b) * a.Cin + ci) * a.H + iy) * a.W + ix];
-      u[e >> 1] |= v << ((e & 1) * 16);
+      const bool ok = r.valid & (k0 + e < a.K) & (iy >= 0) & (iy < a.H) & (ix >= 0) & (ix < a.W);
+      u[e >> 1] |= ld_masked(a.x, ((img + ci) * a.H + iy) * a.W + ix, ok) << ((e & 1) * 16);
       if (++kx == a.KW) { kx = 0; if (++ky == a.KH) { ky = 0; ++ci; } }
     }
   } else if (DIR == kGDgrad) {
     const int khw = a.KH * a.KW;
     int co = k0 / khw, rem = k0 - co * khw;
     int ky = rem / a.KW, kx = rem - ky * a.KW;
+    const int img = r.b * a.Cout;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int ty = r.y0 - ky, tx = r.x0 - kx;
-      uint32_t v = 0;
-      if (k0 + e < a.K && ty >= 0 && tx >= 0) {
-        const int oy = ty / a.sh, ox = tx / a.sw;
-        if (oy * a.sh == ty && ox * a.sw == tx && oy < a.Ho && ox < a.Wo)
-          v = a.dy[((int64_t(r.b) * a.Cout + co) * a.Ho + oy) * a.Wo + ox];
+      int oy, ox;
+      bool ok = r.valid & (k0 + e < a.K) & (ty >= 0) & (tx >= 0);
+      if (S1) {
+        oy = ty;
+        ox = tx;
+      } else {
+        oy = ty / a.sh;
+        ox = tx / a.sw;
+        ok = ok & (oy * a.sh == ty) & (ox * a.sw == tx);
       }
-      u[e >> 1] |= v << ((e & 1) * 16);
+      ok = ok & (oy < a.Ho) & (ox < a.Wo);
+      u[e >> 1] |= ld_masked(a.dy, ((img + co) * a.Ho + oy) * a.Wo + ox, ok) << ((e & 1) * 16);
       if (++kx == a.KW) { kx = 0; if (++ky == a.KH) { ky = 0; ++co; } }
     }
   } else {
@@ -117,10 +132,8 @@ __device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint3
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int iy = oy * a.sh - a.ph + r.ky, ix = ox * a.sw - a.pw + r.kx;
-      uint32_t v = 0;
-      if (k0 + e < a.K && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
-        v = a.x[((int64_t(b) * a.Cin + r.ci) * a.H + iy) * a.W + ix];
-      u[e >> 1] |= v << ((e & 1) * 16);
+      const bool ok = r.valid & (k0 + e < a.K) & (iy >= 0) & (iy < a.H) & (ix >= 0) & (ix < a.W);
+      u[e >> 1] |= ld_masked(a.x, ((b * a.Cin + r.ci) * a.H + iy) * a.W + ix, ok) << ((e & 1) * 16);
       if (++ox == a.Wo) { ox = 0; if (++oy == a.Ho) { oy = 0; ++b; } }
     }
   }
@@ -131,23 +144,19 @@ template <int DIR, int KPT>
 __device__ inline void gather_a(const GArgs& a, int m, int k0, uint32_t (&u)[KPT / 2]) {
 #pragma unroll
   for (int i = 0; i < KPT / 2; ++i) u[i] = 0;
-  if (m >= a.M) return;
+  const bool mok = m < a.M;
   if (DIR == kGFwd) {
-    const uint16_t* src = a.w + int64_t(m) * a.K;
+    const int row = m * a.K;
 #pragma unroll
-    for (int e = 0; e < KPT; ++e) {
-      const uint32_t v = k0 + e < a.K ? uint32_t(src[k0 + e]) : 0u;
-      u[e >> 1] |= v << ((e & 1) * 16);
-    }
+    for (int e = 0; e < KPT; ++e)
+      u[e >> 1] |= ld_masked(a.w, row + k0 + e, mok & (k0 + e < a.K)) << ((e & 1) * 16);
   } else if (DIR == kGDgrad) {
     // w[co][m][ky][kx] for k = (co, ky, kx)
     const int khw = a.KH * a.KW;
     int co = k0 / khw, r = k0 - co * khw;
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      uint32_t v = 0;
-      if (k0 + e < a.K) v = a.w[(int64_t(co) * a.Cin + m) * khw + r];
-      u[e >> 1] |= v << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(a.w, (co * a.Cin + m) * khw + r, mok & (k0 + e < a.K)) << ((e & 1) * 16);
       if (++r == khw) { r = 0; ++co; }
     }
   } else {
@@ -156,15 +165,13 @@ __device__ inline void gather_a(const GArgs& a, int m, int k0, uint32_t (&u)[KPT
     int b = k0 / hw, rem = k0 - b * hw;
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      uint32_t v = 0;
-      if (k0 + e < a.K) v = a.dy[(int64_t(b) * a.Cout + m) * hw + rem];
-      u[e >> 1] |= v << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(a.dy, (b * a.Cout + m) * hw + rem, mok & (k0 + e < a.K)) << ((e & 1) * 16);
       if (++rem == hw) { rem = 0; ++b; }
     }
   }
 }
 
-template <int DIR, int TM>
+template <int DIR, int TM, bool S1>
 __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
   constexpr int WMW = TM == 32 ? 1 : 2;        // waves along M
   constexpr int WNW = 4 / WMW;                 // waves along N
@@ -209,7 +216,7 @@ __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
 
   if (kt0 < kt1) {
     gather_a<DIR, KPT>(a, am, kt0 * kGTK + ak, ua);
-    gather_b<DIR>(a, br, kt0 * kGTK + bk, ub);
+    gather_b<DIR, S1>(a, br, kt0 * kGTK + bk, ub);
     store(0);
   }
   __syncthreads();
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
     const bool more = kt + 1 < kt1;
     if (more) {
       gather_a<DIR, KPT>(a, am, (kt + 1) * kGTK + ak, ua);
-      gather_b<DIR>(a, br, (kt + 1) * kGTK + bk, ub);
+      gather_b<DIR, S1>(a, br, (kt + 1) * kGTK + bk, ub);
     }
 #pragma unroll
     for (int ks = 0; ks < kGTK / 16; ++ks) {
@@ -298,8 +305,9 @@ bool gconv_args(const char* what, GArgs& a, int B, int Cin, int Cout, int H, int
     set_error(std::string(what) + ": kernel larger than the padded input");
     return false;
   }
-  // element counts and offsets inside each operand must fit the kernel's int arithmetic
-  const int64_t lim = int64_t(1) << 31;
+  // element counts and offsets inside each operand must fit the kernel's int arithmetic,
+  // with headroom for the (masked) offsets of out-of-range elements
+  const int64_t lim = int64_t(1) << 30;
   if (int64_t(B) * Cin * H * W >= lim || int64_t(B) * Cout * a.Ho * a.Wo >= lim ||
       int64_t(Cout) * Cin * KH * KW >= lim) {
     set_error(std::string(what) + ": tensor too large");
@@ -310,13 +318,20 @@ bool gconv_args(const char* what, GArgs& a, int B, int Cin, int Cout, int H, int
 
 int tile_m(int M) { return M <= 32 ? 32 : M <= 64 ? 64 : 128; }
 
+template <int DIR, bool S1>
+void launch_gather_s(GArgs& a, dim3 grid, int tm, hipStream_t st) {
+  if (tm == 32) conv_gather_kernel<DIR, 32, S1><<<grid, 256, 0, st>>>(a);
+  else if (tm == 64) conv_gather_kernel<DIR, 64, S1><<<grid, 256, 0, st>>>(a);
+  else conv_gather_kernel<DIR, 128, S1><<<grid, 256, 0, st>>>(a);
+}
+
 template <int DIR>
 int launch_gather(GArgs& a, hipStream_t st) {
   const int tm = tile_m(a.M);
   const dim3 grid(unsigned(ceil_div(a.N, kGTN)), unsigned(ceil_div(a.M, tm)), unsigned(a.nsplit));
-  if (tm == 32) conv_gather_kernel<DIR, 32><<<grid, 256, 0, st>>>(a);
-  else if (tm == 64) conv_gather_kernel<DIR, 64><<<grid, 256, 0, st>>>(a);
-  else conv_gather_kernel<DIR, 128><<<grid, 256, 0, st>>>(a);
+  // unit strides only change the dgrad gather (no division); one instantiation otherwise
+  if (DIR == kGDgrad && a.sh == 1 && a.sw == 1) launch_gather_s<DIR, true>(a, grid, tm, st);
+  else launch_gather_s<DIR, false>(a, grid, tm, st);
   return check_launch("conv gather");
 }
 

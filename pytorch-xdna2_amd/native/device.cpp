@@ -37,6 +37,13 @@
 namespace xdna_backend {
 
 std::atomic<int> g_mode{2};
+// Convolutions outside the 3x3 path: 0 PyTorch-ROCm, 1 (default) the general HIP kernels
+// where they measured faster than MIOpen, 2 the general HIP kernels always.
+std::atomic<int> g_gconv_mode{[] {
+  const char* e = std::getenv("XDNA_GENERAL_CONV");
+  const int v = e ? std::atoi(e) : 1;
+  return v < 0 || v > 2 ? 1 : v;
+}()};
 
 namespace {
 
@@ -585,6 +592,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     g_mode.store(m);
   });
   mod.def("npu_mode", [] { return g_mode.load(); });
+  mod.def("set_general_conv_mode", [](int m) {
+    TORCH_CHECK(m >= 0 && m <= 2, "xdna: general conv mode must be 0, 1 or 2");
+    g_gconv_mode.store(m);
+  });
+  mod.def("general_conv_mode", [] { return g_gconv_mode.load(); });
   mod.def("mapped_cpu_stats", [] { return stats_dict(path_stats()); });
   mod.def("reset_mapped_cpu_stats", [] {
     std::lock_guard<std::mutex> lock(stats_mu());

@@ -195,6 +195,72 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
   return out;
 }
 
+// ---------------------------------------------------------------------------------------
+// Other 2-D convolutions (any kernel size, stride and padding; dilation 1, groups 1, bf16):
+// the general HIP kernels.  The reference runs these on the CPU (its fallback to
+// aten::convolution, torch_xdna_device.cpp:4594-4604, 4862-4874).
+// ---------------------------------------------------------------------------------------
+bool gconv_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
+                    c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation, bool transposed,
+                    c10::SymIntArrayRef output_padding, const c10::SymInt& groups) {
+  if (g_mode.load() < 1) return false;
+  if (x.scalar_type() != at::kBFloat16 || w.scalar_type() != at::kBFloat16) return false;
+  if (x.dim() != 4 || w.dim() != 4 || x.size(1) != w.size(1)) return false;
+  if (stride.size() != 2 || padding.size() != 2 || !is_one(dilation, 1) || transposed) return false;
+  if (!is_one(output_padding, 0) || groups != 1) return false;
+  if (stride[0] < 1 || stride[1] < 1 || padding[0] < 0 || padding[1] < 0) return false;
+  if (x.device().type() != kXdna || w.device().type() != kXdna) return false;
+  const int64_t lim = int64_t(1) << 30;
+  for (const at::Tensor* t : {&x, &w})
+    if (t->numel() >= lim) return false;
+  for (int64_t d = 0; d < 4; ++d)
+    if (x.size(d) < 1 || w.size(d) < 1) return false;
+  const int64_t H = x.size(2), W = x.size(3), KH = w.size(2), KW = w.size(3);
+  const int64_t ph = padding[0].expect_int(), pw = padding[1].expect_int();
+  if (H + 2 * ph < KH || W + 2 * pw < KW) return false;
+  const int64_t Ho = (H + 2 * ph - KH) / stride[0].expect_int() + 1, Wo = (W + 2 * pw - KW) / stride[1].expect_int() + 1;
+  return x.size(0) * w.size(0) * Ho * Wo < lim;
+}
+
+struct GeomArgs {
+  int B, Cin, Cout, H, W, KH, KW, sh, sw, ph, pw, Ho, Wo;
+};
+
+// Where the general kernels beat MIOpen (measured on the style network's layers, B40
+// 36x36): stride-1 layers with 32 or more output channels, forward and weight gradient
+// (9x9 3->32: 23 vs 39 us forward).  Strided layers and their input gradients, and layers
+// with a few output channels (9x9 32->3), stay on MIOpen unless mode 2 asks otherwise.
+bool gconv_auto(int cout, int sh, int sw) { return cout >= 32 && sh == 1 && sw == 1; }
+
+GeomArgs gconv_geom(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
+                    c10::SymIntArrayRef padding) {
+  GeomArgs g;
+  g.B = int(x.size(0)); g.Cin = int(x.size(1)); g.H = int(x.size(2)); g.W = int(x.size(3));
+  g.Cout = int(w.size(0)); g.KH = int(w.size(2)); g.KW = int(w.size(3));
+  g.sh = int(stride[0].expect_int()); g.sw = int(stride[1].expect_int());
+  g.ph = int(padding[0].expect_int()); g.pw = int(padding[1].expect_int());
+  g.Ho = (g.H + 2 * g.ph - g.KH) / g.sh + 1;
+  g.Wo = (g.W + 2 * g.pw - g.KW) / g.sw + 1;
+  return g;
+}
+
+at::Tensor hip_gconv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias,
+                         c10::SymIntArrayRef stride, c10::SymIntArrayRef padding) {
+  const GeomArgs g = gconv_geom(input, weight, stride, padding);
+  at::Tensor x = input.contiguous(), w = weight.contiguous();
+  at::Tensor bc;
+  if (bias) bc = bias->contiguous();
+  at::Tensor y = empty_xdna({g.B, g.Cout, g.Ho, g.Wo}, at::kBFloat16);
+  KernelTimer kt("conv2d.fwd", 2.0 * g.B * g.Ho * g.Wo * double(g.Cout) * g.Cin * g.KH * g.KW);
+  check_abi(xdna_conv2d_fwd_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                 static_cast<const uint16_t*>(w.const_data_ptr()),
+                                 bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                                 static_cast<uint16_t*>(y.data_ptr()), g.B, g.Cin, g.Cout, g.H, g.W, g.KH,
+                                 g.KW, g.sh, g.sw, g.ph, g.pw, current_stream()),
+            "conv2d forward");
+  return y;
+}
+
 at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tensor& weight,
                                          const std::optional<at::Tensor>& bias,
                                          c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
@@ -207,6 +273,15 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv3x3.fwd.run");
     return hip_conv(input, weight, has_bias ? &*bias : nullptr, false);
+  }
+  const int gmode = g_gconv_mode.load();
+  if (gmode > 0 &&
+      gconv_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
+      (gmode == 2 || gconv_auto(int(weight.size(0)), int(stride[0].expect_int()), int(stride[1].expect_int()))) &&
+      (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
+                     bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
+    ScopedCount sc("hip_conv2d.fwd.run");
+    return hip_gconv_fwd(input, weight, has_bias ? &*bias : nullptr, stride, padding);
   }
   ScopedCount sc("aten::convolution.rocm");
   BelowAutograd g;
@@ -277,6 +352,58 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
                                           current_stream()),
               "conv bias grad");
     mask[2] = false;
+  }
+  const int gmode = g_gconv_mode.load();
+  const bool ghip = !hip && gmode > 0 &&
+                    gconv_eligible(input, weight, stride, padding, dilation, transposed,
+                                   output_padding, groups) &&
+                    grad_output.scalar_type() == at::kBFloat16 && grad_output.dim() == 4 &&
+                    grad_output.device().type() == kXdna && grad_output.size(0) == input.size(0) &&
+                    grad_output.size(1) == weight.size(0);
+  if (ghip) {
+    const GeomArgs g = gconv_geom(input, weight, stride, padding);
+    TORCH_CHECK(grad_output.size(2) == g.Ho && grad_output.size(3) == g.Wo,
+                "convolution_backward: grad_output has the wrong spatial size");
+    at::Tensor d = grad_output.contiguous();
+    const double flops = 2.0 * g.B * g.Ho * g.Wo * double(g.Cout) * g.Cin * g.KH * g.KW;
+    const bool auto_ok = gconv_auto(g.Cout, g.sh, g.sw);
+    if (mask[0] && gmode == 2) {
+      ScopedCount sc("hip_conv2d.dx.run");
+      at::Tensor w = weight.contiguous();
+      gi = empty_xdna({g.B, g.Cin, g.H, g.W}, at::kBFloat16);
+      KernelTimer kt("conv2d.dgrad", flops);
+      check_abi(xdna_conv2d_dgrad_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                       static_cast<const uint16_t*>(w.const_data_ptr()),
+                                       static_cast<uint16_t*>(gi.data_ptr()), g.B, g.Cin, g.Cout, g.H, g.W,
+                                       g.KH, g.KW, g.sh, g.sw, g.ph, g.pw, current_stream()),
+                "conv2d dgrad");
+      mask[0] = false;
+    }
+    if (mask[1] && g_mode.load() >= 2 && (gmode == 2 || auto_ok)) {
+      ScopedCount sc("hip_conv2d.dw.run");
+      at::Tensor x = input.contiguous();
+      gw = empty_xdna({g.Cout, g.Cin, g.KH, g.KW}, at::kBFloat16);
+      if (mask[2]) gb = empty_xdna({g.Cout}, at::kBFloat16);
+      KernelTimer kt("conv2d.wgrad", flops);
+      check_abi(xdna_conv2d_wgrad_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                       static_cast<const uint16_t*>(d.const_data_ptr()),
+                                       static_cast<uint16_t*>(gw.data_ptr()),
+                                       mask[2] ? static_cast<uint16_t*>(gb.data_ptr()) : nullptr, g.B, g.Cin,
+                                       g.Cout, g.H, g.W, g.KH, g.KW, g.sh, g.sw, g.ph, g.pw, current_stream()),
+                "conv2d wgrad");
+      g_dw_jobs.fetch_add(1);
+      mask[1] = false;
+      mask[2] = false;
+    }
+    if (mask[2] && !mask[1]) {
+      ScopedCount sc("hip_conv2d.bias_grad.run");
+      gb = empty_xdna({g.Cout}, at::kBFloat16);
+      check_abi(xdna_conv3x3_bias_grad_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                            static_cast<uint16_t*>(gb.data_ptr()), g.B, g.Cout, g.Ho, g.Wo,
+                                            current_stream()),
+                "conv2d bias grad");
+      mask[2] = false;
+    }
   }
   if (mask[0] || mask[1] || mask[2]) {
     ScopedCount sc("aten::convolution_backward.rocm");

@@ -45,6 +45,7 @@ at::Tensor xdna_from_cuda(const at::Tensor& t);
 // gradient; 2: all HIP paths (default).  Mirrors the reference's npu mode
 // (xdna_train/device.py:526-650).
 extern std::atomic<int> g_mode;
+extern std::atomic<int> g_gconv_mode;
 
 // Per-path counters (the reference's ScopedMappedCpu, torch_xdna_device.cpp:1470-1521).
 void count_call(const char* name, int64_t ns);

@@ -11,6 +11,7 @@ from .device import (
     coherency_state,
     empty_cache,
     fallback_stats,
+    general_conv_mode,
     is_available,
     is_xrt_backed,
     mapped_cpu_stats,
@@ -19,6 +20,7 @@ from .device import (
     register_xdna_device,
     reset_fallback_stats,
     reset_mapped_cpu_stats,
+    set_general_conv_mode,
     set_npu_mode,
     synchronize,
     try_register_xdna_device,
@@ -43,6 +45,8 @@ __all__ = [
     "autotune_result",
     "set_npu_mode",
     "npu_mode",
+    "set_general_conv_mode",
+    "general_conv_mode",
     "wait_for_builds",
     "reset_fallback_stats",
     "fallback_stats",

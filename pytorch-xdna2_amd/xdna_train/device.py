@@ -320,6 +320,20 @@ def npu_mode() -> int:
     return int(_C.npu_mode())
 
 
+def set_general_conv_mode(mode: int) -> None:
+    """Convolutions outside the 3x3 / stride-1 path (strided, 1x1, 9x9, ...): 0 on
+    PyTorch-ROCm (MIOpen), 1 (default) on the general HIP kernels where those measured
+    faster, 2 on the general HIP kernels always.  XDNA_GENERAL_CONV sets the initial value.
+    No reference counterpart (the reference runs these on its CPU)."""
+    register_xdna_device()
+    _C.set_general_conv_mode(int(mode))
+
+
+def general_conv_mode() -> int:
+    register_xdna_device()
+    return int(_C.general_conv_mode())
+
+
 def wait_for_builds(timeout: float | None = None) -> bool:
     """Kernels are compiled ahead of time: nothing is ever pending."""
     del timeout

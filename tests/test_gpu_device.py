@@ -88,19 +88,61 @@ def test_conv_forward_backward_matches_cpu_and_oracle(xdna):
         assert (g - r).norm() / r.norm() < 1e-2
 
 
-def test_ineligible_convs_fall_back(xdna):
+def test_other_convs_run_on_general_kernels(xdna):
+    """5x5, strided 3x3, 1x1, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on
+    the general HIP kernels (mode 2: always) and match the CPU bf16 path and the float64
+    oracle."""
     xdna.reset_mapped_cpu_stats()
-    for conv in (nn.Conv2d(8, 16, 5, padding=2), nn.Conv2d(8, 16, 3, stride=2, padding=1),
-                 nn.Conv2d(8, 16, 1)):
-        conv = conv.bfloat16()
-        x = torch.randn(2, 8, 10, 10).bfloat16()
-        cd = type(conv)(8, 16, conv.kernel_size, stride=conv.stride, padding=conv.padding).bfloat16().to(X)
+    xdna.set_general_conv_mode(2)
+    specs = [(8, 16, 5, 1, 2), (8, 16, 3, 2, 1), (8, 16, 1, 1, 0), (3, 32, 9, 1, 4), (3, 16, 7, 2, 3),
+             (16, 24, 1, 2, 0)]
+    for cin, cout, k, s, pd in specs:
+        torch.manual_seed(k * 10 + s)
+        conv = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16()
+        x = torch.randn(2, cin, 14, 13).bfloat16()
+        cd = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16().to(X)
+        cd.load_state_dict(conv.state_dict())
+        xd = x.to(X).requires_grad_()
+        yd = cd(xd)
+        dy = torch.randn(yd.shape).bfloat16()
+        yd.backward(dy.to(X))
+        xb, wb, bb, dyb = (bits(t) for t in (x, conv.weight, conv.bias, dy))
+        what = f"k{k} s{s} {cin}->{cout}"
+        check_bf16(bits(yd), oracle.conv2d_fwd(xb, wb, bb, (s, s), (pd, pd)), what=f"fwd {what}")
+        check_bf16(bits(xd.grad), oracle.conv2d_dgrad(dyb, wb, (14, 13), (s, s), (pd, pd)), what=f"dgrad {what}")
+        gw, gb = oracle.conv2d_wgrad(xb, dyb, (k, k), (s, s), (pd, pd))
+        check_bf16(bits(cd.weight.grad), gw, what=f"wgrad {what}")
+        check_bf16(bits(cd.bias.grad), gb, what=f"bias grad {what}")
+        xc = x.clone().requires_grad_()
+        yc = conv(xc)
+        yc.backward(dy)
+        for got, ref in ((yd, yc), (xd.grad, xc.grad), (cd.weight.grad, conv.weight.grad)):
+            g, r = got.detach().cpu().float(), ref.detach().float()
+            assert (g - r).norm() / r.norm() < 1e-2, what
+    xdna.set_general_conv_mode(1)
+    st = xdna.mapped_cpu_stats()
+    n = len(specs)
+    for key in ("hip_conv2d.fwd.run", "hip_conv2d.dx.run", "hip_conv2d.dw.run"):
+        assert st.get(key, {}).get("calls", 0) == n, (key, st)
+    assert "aten::convolution.rocm" not in st and "hip_conv3x3.fwd.run" not in st
+
+
+def test_ineligible_convs_fall_back(xdna):
+    """Dilated, grouped and fp32 convolutions stay on PyTorch-ROCm."""
+    xdna.reset_mapped_cpu_stats()
+    for conv, dt in ((nn.Conv2d(8, 16, 3, padding=2, dilation=2), torch.bfloat16),
+                     (nn.Conv2d(8, 16, 3, padding=1, groups=2), torch.bfloat16),
+                     (nn.Conv2d(8, 16, 3, padding=1), torch.float32)):
+        conv = conv.to(dt)
+        x = torch.randn(2, 8, 10, 10).to(dt)
+        cd = nn.Conv2d(8, 16, 3, padding=conv.padding, dilation=conv.dilation, groups=conv.groups).to(dt).to(X)
         cd.load_state_dict(conv.state_dict())
         y = cd(x.to(X))
         ref = conv(x)
         assert (y.cpu().float() - ref.float()).norm() / ref.float().norm() < 1e-2
     st = xdna.mapped_cpu_stats()
-    assert "hip_conv3x3.fwd.run" not in st and st["aten::convolution.rocm"]["calls"] == 3
+    assert "hip_conv3x3.fwd.run" not in st and "hip_conv2d.fwd.run" not in st
+    assert st["aten::convolution.rocm"]["calls"] == 3
 
 
 def test_deferred_wgrad_snapshots_inputs(xdna):
