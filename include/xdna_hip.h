@@ -367,6 +367,21 @@ int xdna_batch_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* 
                              const float* save_mean, const float* save_invstd, uint16_t* dx,
                              void* dweight, void* dbias, int64_t N, int64_t C, int64_t L, void* stream);
 
+/* Instance norm over x [B][C][L] (training statistics, no running statistics): each
+ * (image, channel) plane normalised on its own, y = (x - mean) * invstd * w[c] + b[c]
+ * with C-element parameters (param_dtype 0 none, 1 bf16, 2 fp32); save_mean /
+ * save_invstd hold B*C floats.  The backward writes dx (if not null) and, when dweight
+ * and dbias are given, the parameter gradients summed over the images in a fixed order.
+ * Replaces PyTorch's instance_norm composite on the device (repeat of the parameters,
+ * native_batch_norm on [1, B*C, L], and the repeat's backward sums), which the reference
+ * runs on its CPU through the fallback (torch_xdna_device.cpp:5124-5260). */
+int xdna_instance_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                uint16_t* y, float* save_mean, float* save_invstd, int64_t B, int64_t C,
+                                int64_t L, double eps, void* stream);
+int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
+                                const float* save_mean, const float* save_invstd, uint16_t* dx, void* dweight,
+                                void* dbias, int64_t B, int64_t C, int64_t L, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,10 @@
 // Batch-norm statistics, normalisation and backward for bf16 activations, in the form
 // instance_norm reaches them: PyTorch's instance_norm views [B, C, H, W] as
 // [1, B*C, H, W] and calls native_batch_norm (training, no running statistics), so a
-// "channel" here is one (image, channel) plane of H*W elements.  The reference serves
+// "channel" here is one (image, channel) plane of H*W elements.  The instance-norm entry
+// points take the C-element weight and bias directly (parameter index = channel % C) and
+// sum the parameter gradients over the images themselves, which replaces PyTorch's
+// repeat of the parameters and the reductions of its backward.  The reference serves
 // these operators from PyTorch's CPU kernels through its zero-copy fallback
 // (torch_xdna_device.cpp:5124-5260); on the GPU they decide the style step's time once
 // the convolutions are fast (a wide, shallow reduction PyTorch-ROCm runs at ~35 us).
@@ -38,10 +41,12 @@ __device__ inline void param_put(void* p, int wd, int64_t c, float v) {
   else static_cast<float*>(p)[c] = v;
 }
 
+// Parameters are indexed by channel % pC: pC = C for batch norm, the per-image channel
+// count for instance norm (whose B*C "channels" share C weights; no repeated copies).
 __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const void* __restrict__ b, int wd,
     uint16_t* __restrict__ y, float* __restrict__ save_mean, float* __restrict__ save_invstd,
-    int64_t N, int64_t C, int64_t L, float eps) {
+    int64_t N, int64_t C, int64_t L, float eps, int64_t pC) {
   const int lane = threadIdx.x & 63;
   const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
   if (c >= C) return;
@@ -66,8 +71,8 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
     save_mean[c] = mean;
     save_invstd[c] = invstd;
   }
-  const float scale = param_at(w, wd, c, 1.f) * invstd;
-  const float shift = param_at(b, wd, c, 0.f) - mean * scale;
+  const float scale = param_at(w, wd, c % pC, 1.f) * invstd;
+  const float shift = param_at(b, wd, c % pC, 0.f) - mean * scale;
   for (int64_t n = 0; n < N; ++n) {
     const uint16_t* xp = x + (n * C + c) * L;
     uint16_t* yp = y + (n * C + c) * L;
@@ -77,10 +82,13 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
 
 // dx = (dy - mean(dy) - (x - mean) * invstd^2 * mean(dy * (x - mean))) * invstd * w
 // dw = invstd * sum(dy * (x - mean)),  db = sum(dy)   (PyTorch's batch_norm_backward)
+// With pw / pb set (instance norm), each channel's dw / db terms go there in fp32 for a
+// fixed-order sum over the images (norm_param_reduce_kernel) instead of to dw / db.
 __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const void* __restrict__ w, int wd,
     const float* __restrict__ mean_in, const float* __restrict__ invstd_in, uint16_t* __restrict__ dx,
-    void* __restrict__ dw, void* __restrict__ db, int64_t N, int64_t C, int64_t L) {
+    void* __restrict__ dw, void* __restrict__ db, int64_t N, int64_t C, int64_t L, int64_t pC,
+    float* __restrict__ pw, float* __restrict__ pb) {
   const int lane = threadIdx.x & 63;
   const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
   if (c >= C) return;
@@ -97,20 +105,48 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
   sdy = wave_sum(sdy);
   sdot = wave_sum(sdot);
   if (lane == 0) {
-    param_put(dw, wd, c, sdot * invstd);
-    param_put(db, wd, c, sdy);
+    if (pw) {
+      pw[c] = sdot * invstd;
+      pb[c] = sdy;
+    } else {
+      param_put(dw, wd, c, sdot * invstd);
+      param_put(db, wd, c, sdy);
+    }
   }
   if (!dx) return;
   const float inv_cnt = 1.0f / float(N * L);
   const float gmean = sdy * inv_cnt;
   const float proj = sdot * inv_cnt * invstd * invstd;
-  const float gscale = invstd * param_at(w, wd, c, 1.f);
+  const float gscale = invstd * param_at(w, wd, c % pC, 1.f);
   for (int64_t n = 0; n < N; ++n) {
     const int64_t o = (n * C + c) * L;
     for (int64_t l = lane; l < L; l += 64) {
       const float xm = bf16_to_f32(x[o + l]) - mean;
       dx[o + l] = f32_to_bf16((bf16_to_f32(dy[o + l]) - gmean - xm * proj) * gscale);
     }
+  }
+}
+
+// dw[c] = sum_b pw[b*C + c], db likewise, stored in dtype wd: one wave per parameter,
+// lane l sums images l, l+64, ... and the wave adds the lanes in a fixed order (the
+// result does not depend on timing).
+__global__ __launch_bounds__(64 * kNormWaves) void norm_param_reduce_kernel(const float* __restrict__ pw,
+                                                                           const float* __restrict__ pb,
+                                                                           void* dw, void* db, int wd, int64_t B,
+                                                                           int64_t C) {
+  const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (c >= C) return;
+  float sw = 0.f, sb = 0.f;
+  for (int64_t b = lane; b < B; b += 64) {
+    sw += pw[b * C + c];
+    sb += pb[b * C + c];
+  }
+  sw = wave_sum(sw);
+  sb = wave_sum(sb);
+  if (lane == 0) {
+    param_put(dw, wd, c, sw);
+    param_put(db, wd, c, sb);
   }
 }
 
@@ -140,7 +176,7 @@ int xdna_batch_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* 
   }
   if (!admit_launch("batch_norm fwd")) return -1;
   bn_fwd_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
-      x, weight, bias, param_dtype, y, save_mean, save_invstd, N, C, L, float(eps));
+      x, weight, bias, param_dtype, y, save_mean, save_invstd, N, C, L, float(eps), C);
   return check_launch("batch_norm fwd");
 }
 
@@ -155,8 +191,62 @@ int xdna_batch_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* 
   }
   if (!admit_launch("batch_norm bwd")) return -1;
   bn_bwd_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
-      dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, N, C, L);
+      dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, N, C, L, C, nullptr, nullptr);
   return check_launch("batch_norm bwd");
+}
+
+int xdna_instance_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                uint16_t* y, float* save_mean, float* save_invstd, int64_t B, int64_t C,
+                                int64_t L, double eps, void* stream) {
+  if (!norm_shape_ok("xdna_instance_norm_fwd_bf16", B, C, L, param_dtype)) return -1;
+  if (B == 0 || C == 0) return 0;
+  if (L == 0) {
+    set_error("xdna_instance_norm_fwd_bf16: empty reduction");
+    return -1;
+  }
+  const int64_t ch = B * C;
+  if (ceil_div(ch, kNormWaves) > 0x7fffffff) {
+    set_error("xdna_instance_norm_fwd_bf16: too many planes");
+    return -1;
+  }
+  if (!admit_launch("instance_norm fwd")) return -1;
+  bn_fwd_kernel<<<dim3(unsigned(ceil_div(ch, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
+      x, weight, bias, param_dtype, y, save_mean, save_invstd, 1, ch, L, float(eps), C);
+  return check_launch("instance_norm fwd");
+}
+
+int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
+                                const float* save_mean, const float* save_invstd, uint16_t* dx, void* dweight,
+                                void* dbias, int64_t B, int64_t C, int64_t L, void* stream) {
+  if (!norm_shape_ok("xdna_instance_norm_bwd_bf16", B, C, L, param_dtype)) return -1;
+  if (B == 0 || C == 0) return 0;
+  const bool params = dweight || dbias;
+  if (params && (param_dtype == 0 || !dweight || !dbias)) {
+    set_error("xdna_instance_norm_bwd_bf16: parameter gradients need both outputs and param_dtype 1 or 2");
+    return -1;
+  }
+  const int64_t ch = B * C;
+  if (ceil_div(ch, kNormWaves) > 0x7fffffff) {
+    set_error("xdna_instance_norm_bwd_bf16: too many planes");
+    return -1;
+  }
+  if (!admit_launch("instance_norm bwd")) return -1;
+  float* part = nullptr;
+  if (params) {
+    part = static_cast<float*>(xdna_hip_cache_alloc(size_t(2 * ch) * sizeof(float)));
+    if (!part) return -1;
+  }
+  hipStream_t st = as_stream(stream);
+  bn_bwd_kernel<<<dim3(unsigned(ceil_div(ch, kNormWaves))), 64 * kNormWaves, 0, st>>>(
+      dy, x, weight, param_dtype, save_mean, save_invstd, dx, nullptr, nullptr, 1, ch, L, C, part,
+      part ? part + ch : nullptr);
+  if (params) {
+    norm_param_reduce_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, st>>>(
+        part, part + ch, dweight, dbias, param_dtype, B, C);
+    // stream-ordered reuse: the next user of the block runs after the reduce
+    xdna_hip_cache_free(part);
+  }
+  return check_launch("instance_norm bwd");
 }
 
 }  // extern "C"

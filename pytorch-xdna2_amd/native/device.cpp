@@ -534,6 +534,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   register_hot_ops(m);
 }
 
+TORCH_LIBRARY_IMPL(aten, AutogradPrivateUse1, m) { register_autograd_ops(m); }
+
 TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
   m.fallback(torch::CppFunction::makeFromBoxedFunction<&xdna_fallback>());
 }

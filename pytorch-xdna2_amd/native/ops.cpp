@@ -7,6 +7,8 @@
 
 #include <ATen/native/Resize.h>
 #include <ATen/ops/_fused_adam_native.h>
+#include <ATen/ops/instance_norm_native.h>
+#include <torch/csrc/autograd/custom_function.h>
 #include <c10/core/impl/LocalDispatchKeySet.h>
 
 #include <algorithm>
@@ -856,6 +858,94 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> native_batch_norm_backward_xdna(
                                                       rocm(running_mean), rocm(running_var), rocm(save_mean),
                                                       rocm(save_invstd), train, eps, mask);
   return {back(std::get<0>(r)), back(std::get<1>(r)), back(std::get<2>(r))};
+}
+
+// ---------------------------------------------------------------------------------------
+// instance_norm with training statistics, registered for AutogradPrivateUse1 so that it
+// replaces PyTorch's composite (repeat of weight and bias to B*C elements, batch norm on
+// [1, B*C, L], and the sums over the images the repeat's backward runs): one kernel
+// forward, a kernel plus a parameter-gradient reduce backward.  Other forms (no affine
+// parameters or a lone one, running or eval statistics, non-bf16 input) keep the
+// composite, whose native_batch_norm calls reach the batch-norm kernels above.
+// The reference reaches the same operator through its CPU fallback
+// (torch_xdna_device.cpp:5124-5260).
+// ---------------------------------------------------------------------------------------
+bool instance_norm_eligible(const at::Tensor& input, const std::optional<at::Tensor>& weight,
+                            const std::optional<at::Tensor>& bias, const std::optional<at::Tensor>& rm,
+                            const std::optional<at::Tensor>& rv, bool use_input_stats) {
+  if (g_mode.load() < 1 || !use_input_stats) return false;
+  if ((rm && rm->defined()) || (rv && rv->defined())) return false;
+  if (input.scalar_type() != at::kBFloat16 || input.dim() < 3 || input.device().type() != kXdna) return false;
+  if (input.numel() == 0) return false;
+  const int64_t C = input.size(1), L = input.numel() / (input.size(0) * C);
+  if (L > kNormMaxPerChannel) return false;
+  // affine only: without parameters the composite adds no work around the batch norm
+  if (!weight || !weight->defined() || !bias || !bias->defined()) return false;
+  if (weight->requires_grad() != bias->requires_grad()) return false;
+  return norm_param_dtype(weight, bias) >= 0 && norm_param_ok(weight, C) && norm_param_ok(bias, C);
+}
+
+struct InstanceNormFn : public torch::autograd::Function<InstanceNormFn> {
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& input,
+                            const at::Tensor& weight, const at::Tensor& bias, double eps) {
+    ScopedCount sc("hip_instance_norm.fwd.run");
+    const at::Tensor x = input.contiguous();
+    const int64_t B = x.size(0), C = x.size(1), L = x.numel() / (B * C);
+    const int wd = norm_param_dtype(weight, bias);
+    at::Tensor y = empty_xdna(x.sizes(), at::kBFloat16);
+    at::Tensor mean = empty_xdna({B * C}, at::kFloat), invstd = empty_xdna({B * C}, at::kFloat);
+    check_abi(xdna_instance_norm_fwd_bf16(
+                  static_cast<const uint16_t*>(x.const_data_ptr()), weight.const_data_ptr(), bias.const_data_ptr(),
+                  wd, static_cast<uint16_t*>(y.data_ptr()),
+                  mean.data_ptr<float>(), invstd.data_ptr<float>(), B, C, L, eps, current_stream()),
+              "instance_norm fwd");
+    ctx->save_for_backward({x, weight, mean, invstd});
+    ctx->saved_data["wd"] = int64_t(wd);
+    return y;
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor &x = saved[0], &weight = saved[1], &mean = saved[2], &invstd = saved[3];
+    const int wd = int(ctx->saved_data["wd"].toInt());
+    const bool need_x = ctx->needs_input_grad(0);
+    const bool need_p = ctx->needs_input_grad(1) || ctx->needs_input_grad(2);
+    at::Tensor dx, dw, db;
+    if (!grads[0].defined() || (!need_x && !need_p)) return {dx, dw, db, at::Tensor()};
+    ScopedCount sc("hip_instance_norm.bwd.run");
+    const int64_t B = x.size(0), C = x.size(1), L = x.numel() / (B * C);
+    at::Tensor dy = grads[0].to(at::kBFloat16).contiguous();
+    if (need_x) dx = empty_xdna(x.sizes(), at::kBFloat16);
+    if (need_p) {
+      const at::ScalarType pt = wd == 2 ? at::kFloat : at::kBFloat16;
+      dw = empty_xdna({C}, pt);
+      db = empty_xdna({C}, pt);
+    }
+    check_abi(xdna_instance_norm_bwd_bf16(
+                  static_cast<const uint16_t*>(dy.const_data_ptr()), static_cast<const uint16_t*>(x.const_data_ptr()),
+                  weight.const_data_ptr(), wd, mean.const_data_ptr<float>(),
+                  invstd.const_data_ptr<float>(), need_x ? static_cast<uint16_t*>(dx.data_ptr()) : nullptr,
+                  need_p ? dw.data_ptr() : nullptr, need_p ? db.data_ptr() : nullptr, B, C, L, current_stream()),
+              "instance_norm bwd");
+    return {dx, dw, db, at::Tensor()};
+  }
+};
+
+at::Tensor instance_norm_autograd_xdna(const at::Tensor& input, const std::optional<at::Tensor>& weight,
+                                       const std::optional<at::Tensor>& bias,
+                                       const std::optional<at::Tensor>& running_mean,
+                                       const std::optional<at::Tensor>& running_var, bool use_input_stats,
+                                       double momentum, double eps, bool cudnn_enabled) {
+  if (instance_norm_eligible(input, weight, bias, running_mean, running_var, use_input_stats)) {
+    return InstanceNormFn::apply(input, *weight, *bias, eps);
+  }
+  return at::native::instance_norm(input, weight, bias, running_mean, running_var, use_input_stats, momentum,
+                                   eps, cudnn_enabled);
+}
+
+void register_autograd_ops(torch::Library& m) {
+  m.impl("instance_norm", TORCH_FN(instance_norm_autograd_xdna));
 }
 
 void register_hot_ops(torch::Library& m) {

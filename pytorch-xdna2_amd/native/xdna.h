@@ -59,6 +59,8 @@ struct ScopedCount {
 
 // Hot-path registrations (ops.cpp).
 void register_hot_ops(torch::Library& m);
+// Autograd-level overrides for the backend (ops.cpp): instance_norm.
+void register_autograd_ops(torch::Library& m);
 
 // Drops the prepared weights of frozen tensors (ops.cpp).
 void clear_weight_cache();

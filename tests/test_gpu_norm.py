@@ -1,8 +1,11 @@
-"""InstanceNorm on the xdna device: the HIP batch-norm kernels (reached through
-native_batch_norm / native_batch_norm_backward, as PyTorch's instance_norm calls them)
-against an fp64 autograd reference computed from the same bf16 inputs on the CPU.
+"""InstanceNorm on the xdna device: the HIP instance-norm kernels (the backend's
+instance_norm override at the autograd level) and the HIP batch-norm kernels (reached
+through native_batch_norm / native_batch_norm_backward, by batch_norm and by the
+instance_norm forms the override leaves to PyTorch's composite) against an fp64 autograd
+reference computed from the same bf16 inputs on the CPU.
 Tolerance: bf16 outputs within 2 bf16 ulp (floor at 2^-8 of the largest magnitude) and
-relative L2 <= 1e-2; fp32 statistics within 1e-5 relative."""
+relative L2 <= 1e-2; parameter gradients within 2 bf16 ulp (bf16 parameters: one
+rounding of an fp32 sum) or 1e-4 relative (fp32 parameters)."""
 import numpy as np
 import pytest
 import torch
@@ -48,20 +51,114 @@ def test_instance_norm_matches_fp64(shape, affine, pdtype):
     yd.backward(dy.to(X))
     torch.xdna.synchronize()
     stats = xdna_train.mapped_cpu_stats()
-    assert stats.get("hip_batch_norm.fwd.run", {}).get("calls", 0) == 1, stats
-    assert stats.get("hip_batch_norm.bwd.run", {}).get("calls", 0) == 1, stats
+    # affine norms take the instance-norm kernels, the others PyTorch's composite over
+    # the batch-norm kernels
+    kind = "hip_instance_norm" if affine else "hip_batch_norm"
+    assert stats.get(f"{kind}.fwd.run", {}).get("calls", 0) == 1, stats
+    assert stats.get(f"{kind}.bwd.run", {}).get("calls", 0) == 1, stats
+    assert "aten::native_batch_norm.rocm" not in stats, stats
     check_bf16(bits(yd), yr.detach().numpy(), what="instance_norm out")
     check_bf16(bits(xd.grad), xr.grad.numpy(), what="instance_norm dx")
     if affine:
-        for got, ref, name in ((wd.grad, wr.grad, "dweight"), (bd.grad, br.grad, "dbias")):
-            gv = got.detach().cpu().double().numpy()
-            rv = ref.numpy()
-            if pdtype == torch.bfloat16:
-                # per-image sums rounded to bf16, then summed over the batch by autograd
-                tol = shape[0] * 2 * oracle.bf16_ulp(np.abs(rv) + np.abs(ref.numpy()).max() * 2.0 ** -8)
-            else:
-                tol = 1e-4 * (np.abs(rv) + np.abs(rv).max())
-            assert (np.abs(gv - rv) <= tol).all(), (name, np.abs(gv - rv).max(), tol.max())
+        assert wd.grad.dtype == pdtype and bd.grad.dtype == pdtype
+        check_param_grads(((wd.grad, wr.grad, "dweight"), (bd.grad, br.grad, "dbias")), pdtype)
+
+
+def check_param_grads(pairs, pdtype):
+    for got, ref, name in pairs:
+        gv = got.detach().cpu().double().numpy()
+        rv = ref.numpy()
+        if pdtype == torch.bfloat16:
+            tol = 2 * oracle.bf16_ulp(np.abs(rv) + np.abs(rv).max() * 2.0 ** -8)
+        else:
+            tol = 1e-4 * (np.abs(rv) + np.abs(rv).max())
+        assert (np.abs(gv - rv) <= tol).all(), (name, np.abs(gv - rv).max(), tol.max())
+
+
+@pytest.mark.parametrize("need", ["x", "params"])
+def test_instance_norm_partial_grads(need):
+    """Only the input, or only the parameters, require gradients."""
+    g = torch.Generator().manual_seed(11)
+    shape = (6, 24, 10, 11)
+    x = torch.randn(shape, generator=g).bfloat16()
+    dy = torch.randn(shape, generator=g).bfloat16()
+    w = (torch.rand(24, generator=g) + 0.5).bfloat16()
+    b = torch.randn(24, generator=g).bfloat16()
+    xr = x.double().requires_grad_(need == "x")
+    wr = w.double().requires_grad_(need == "params")
+    br = b.double().requires_grad_(need == "params")
+    torch.nn.functional.instance_norm(xr, weight=wr, bias=br).backward(dy.double())
+    xd = x.to(X).requires_grad_(need == "x")
+    wd = w.to(X).requires_grad_(need == "params")
+    bd = b.to(X).requires_grad_(need == "params")
+    xdna_train.reset_mapped_cpu_stats()
+    torch.nn.functional.instance_norm(xd, weight=wd, bias=bd).backward(dy.to(X))
+    torch.xdna.synchronize()
+    stats = xdna_train.mapped_cpu_stats()
+    assert stats.get("hip_instance_norm.bwd.run", {}).get("calls", 0) == 1, stats
+    if need == "x":
+        assert wd.grad is None and bd.grad is None
+        check_bf16(bits(xd.grad), xr.grad.numpy(), what="instance_norm dx")
+    else:
+        assert xd.grad is None
+        check_param_grads(((wd.grad, wr.grad, "dweight"), (bd.grad, br.grad, "dbias")), torch.bfloat16)
+
+
+def test_instance_norm_module_channels_last_and_no_grad():
+    """nn.InstanceNorm2d(affine) on a channels-last input, then under no_grad."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 16, 9, 13, generator=g).bfloat16()
+    m = torch.nn.InstanceNorm2d(16, affine=True).bfloat16()
+    with torch.no_grad():
+        m.weight.copy_(torch.rand(16, generator=g) + 0.5)
+        m.bias.copy_(torch.randn(16, generator=g))
+    ref = torch.nn.functional.instance_norm(x.double(), weight=m.weight.double(), bias=m.bias.double())
+    md = m.to(X)
+    xd = x.to(X).contiguous(memory_format=torch.channels_last)
+    y = md(xd)
+    check_bf16(bits(y), ref.detach().numpy(), what="channels-last instance_norm out")
+    with torch.no_grad():
+        y2 = md(x.to(X))
+    assert y2.grad_fn is None
+    check_bf16(bits(y2), ref.detach().numpy(), what="no_grad instance_norm out")
+
+
+def test_instance_norm_lone_weight_uses_batch_norm_kernels():
+    """A weight without a bias leaves instance_norm to PyTorch's composite, whose
+    native_batch_norm calls still reach the HIP batch-norm kernels."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 8, 7, 7, generator=g).bfloat16()
+    w = (torch.rand(8, generator=g) + 0.5).bfloat16()
+    ref = torch.nn.functional.instance_norm(x.double(), weight=w.double())
+    xdna_train.reset_mapped_cpu_stats()
+    y = torch.nn.functional.instance_norm(x.to(X), weight=w.to(X))
+    torch.xdna.synchronize()
+    stats = xdna_train.mapped_cpu_stats()
+    assert "hip_instance_norm.fwd.run" not in stats, stats
+    assert stats.get("hip_batch_norm.fwd.run", {}).get("calls", 0) == 1, stats
+    check_bf16(bits(y), ref.numpy(), what="composite instance_norm out")
+
+
+@pytest.mark.parametrize("pdtype", [torch.bfloat16, torch.float32])
+def test_batch_norm_training_without_running_stats(pdtype):
+    g = torch.Generator().manual_seed(9)
+    shape = (5, 12, 6, 7)
+    x = (torch.randn(shape, generator=g) * 2 - 1).bfloat16()
+    dy = torch.randn(shape, generator=g).bfloat16()
+    w = (torch.rand(12, generator=g) + 0.5).to(pdtype)
+    b = torch.randn(12, generator=g).to(pdtype)
+    xr, wr, br = (t.double().requires_grad_(True) for t in (x, w, b))
+    torch.nn.functional.batch_norm(xr, None, None, wr, br, training=True).backward(dy.double())
+    xd, wd, bd = (t.to(X).requires_grad_(True) for t in (x, w, b))
+    xdna_train.reset_mapped_cpu_stats()
+    yd = torch.nn.functional.batch_norm(xd, None, None, wd, bd, training=True)
+    yd.backward(dy.to(X))
+    torch.xdna.synchronize()
+    stats = xdna_train.mapped_cpu_stats()
+    assert stats.get("hip_batch_norm.fwd.run", {}).get("calls", 0) == 1, stats
+    assert stats.get("hip_batch_norm.bwd.run", {}).get("calls", 0) == 1, stats
+    check_bf16(bits(xd.grad), xr.grad.numpy(), what="batch_norm dx")
+    check_param_grads(((wd.grad, wr.grad, "dweight"), (bd.grad, br.grad, "dbias")), pdtype)
 
 
 def test_batch_norm_with_running_stats_falls_back():
