@@ -85,7 +85,48 @@ struct RowsArgs {
   int ch_per;            // input chunks per split (blockIdx.z)
   int nrt, ncot;         // row tiles, channel tiles (blockIdx.x decodes to both)
   int64_t img, m_total, m_pad;
+  int B;                 // images
+  int out_rs;            // 1: stores through a buffer resource (every tile's span < 2^30 bytes)
 };
+
+// Branch-free NCHW epilogue.  The resource starts at the first image a tile touches; a
+// store whose pixel or channel lies outside the output gets an offset of kOutSkip or more,
+// past the resource's record count, and the hardware drops it, so no store waits behind a
+// branch.  Valid offsets stay below kOutSkip (checked on the host), so the sum of a valid
+// and a skipped part, or of two skipped parts, is dropped too.
+constexpr int kOutSkip = 0x40000000;
+
+struct OutMap {
+  __amdgpu_buffer_rsrc_t rs;
+  int b0;
+  int64_t cp;  // elements of one image (cout * H * W)
+};
+
+__device__ inline OutMap out_map(const RowsArgs& a, int64_t p_first) {
+  OutMap o;
+  o.b0 = int(p_first / a.img / a.S);
+  o.cp = int64_t(a.cout) * a.H * a.W;
+  const int64_t left = (int64_t(a.B) - o.b0) * o.cp * 2;
+  o.rs = __builtin_amdgcn_make_buffer_rsrc(a.out + o.b0 * o.cp, 0, int(left < kOutSkip ? left : kOutSkip - 1),
+                                           0x00020000);
+  return o;
+}
+
+// byte offset of padded-grid row p's output pixel (channel 0) from the map's base, or
+// kOutSkip for a border / padding row
+__device__ inline int out_pixel_off(const RowsArgs& a, const OutMap& o, int64_t p) {
+  if (p >= a.m_total) return kOutSkip;
+  const int first = a.S == 1 ? 0 : 1;
+  const int64_t vb = p / a.img;
+  const int64_t rem = p - vb * a.img;
+  const int y = int(rem / a.wp);
+  const int col = int(rem - int64_t(y) * a.wp) - first;
+  const int b = int(vb / a.S), s = int(vb % a.S);
+  const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+  if (y >= a.H || col < 0 || col >= cols) return kOutSkip;
+  const int x = (a.S == 1 ? 0 : s * a.So) + col;
+  return int(((int64_t(b - o.b0)) * o.cp + int64_t(y) * a.W + x) * 2);
+}
 
 constexpr int kXcds = 8;  // MI355X: workgroups go round-robin to 8 XCDs, each with its own L2
 
@@ -655,6 +696,25 @@ void conv_rows4_kernel(RowsArgs a) {
 #undef XDNA_F4_LOAD
 #undef XDNA_M4
 
+  if (a.out_rs) {
+    const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
+    const int plane2 = a.H * a.W * 2;
+    int poff[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+      poff[n] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * NT * 32 + n * 32 + lr);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * MT * 32 + m * 32 + mfma_row(i, lane);
+        const int coff = co < a.cout ? co * plane2 : kOutSkip;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(acc[m][n][i]), om.rs, poff[n] + coff, 0, 0);
+      }
+    return;
+  }
   const int first = a.S == 1 ? 0 : 1;
   const int64_t plane = int64_t(a.H) * a.W;
   uint16_t* obase[NT];
@@ -808,6 +868,23 @@ void conv_small_kernel(RowsArgs a) {
         const int co = co0 + wm * 32 + mfma_row(i, lane);
         if (co < a.cout) pz[int64_t(co) * a.m_pad + p] = acc[n][i];
       }
+    }
+    return;
+  }
+  if (a.out_rs) {
+    const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
+    const int plane2 = a.H * a.W * 2;
+    int poff[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+      poff[n] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 32 + mfma_row(i, lane);
+      const int coff = co < a.cout ? co * plane2 : kOutSkip;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(acc[n][i]), om.rs, poff[n] + coff, 0, 0);
     }
     return;
   }
@@ -1341,6 +1418,12 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.img = geom.img;
   a.m_total = geom.m_total;
   a.m_pad = int64_t(geom.groups) * kGroupOutRows;
+  a.B = B;
+  {
+    // images a tile of up to 512 grid rows can touch, and the bytes they span
+    const int64_t span = (512 - 1) / geom.img + 2;
+    a.out_rs = span * cout * int64_t(H) * W * 2 < kOutSkip ? 1 : 0;
+  }
   if (!admit_launch("conv3x3 rows")) return -1;
   hipStream_t st = as_stream(stream);
   // Kernel choice (xdna_conv3x3_set_rows_variant, or XDNA_ROWS_VARIANT at start-up,
