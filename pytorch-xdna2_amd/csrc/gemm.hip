@@ -40,7 +40,81 @@ struct GemmArgs {
   int kt_per;   // k-tiles per split (blockIdx.z = batch index * nsplit + split)
   int nsplit;
   float* part;  // split-K: fp32 partial products [nsplit][batch][M][N], else null
+  int rs_ok;    // 1: the epilogue stores through buffer resources (extents host-checked)
+  int c_bytes, bias_bytes, part_bytes;  // byte extents of one batch's C / bias / partials
 };
+
+// Branch-free epilogue of one wave's MI x NJ block of 32 x 32 MFMA tiles (rows mb + i*32 +
+// mfma_row(r, lane), columns nb + j*32 + lane % 32), through buffer resources: an element
+// outside M x N gets an offset of kSkip or more, past the record count, so the hardware
+// drops its store (and reads its bias as zero) and no store waits behind a branch.  Valid
+// offsets stay below kSkip (rs_ok, checked on the host), so a valid row offset plus a
+// skipped column offset, or two skipped ones, are dropped as well.
+constexpr int kSkip = 0x40000000;
+
+template <int MI, int NJ>
+__device__ inline void store_block(const GemmArgs& g, int batch, int split, const f32x16_t (&acc)[MI][NJ],
+                                   int mb, int nb, int lane) {
+  const int lr = lane & 31;
+  if (g.part) {
+    float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
+    const auto prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, g.part_bytes, 0x00020000);
+    int noff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = nb + j * 32 + lr;
+      noff[j] = n < g.N ? n * 4 : kSkip;
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mb + i * 32 + mfma_row(r, lane);
+        const int moff = m < g.M ? m * g.N * 4 : kSkip;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), prs, moff + noff[j], 0, 0);
+        // one row of stores at a time: keeps the accumulators in place (no spills)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    return;
+  }
+  const auto crs = __builtin_amdgcn_make_buffer_rsrc(g.c + int64_t(batch) * g.c_batch, 0, g.c_bytes, 0x00020000);
+  const bool bias = g.bias_mode != 0 && g.beta != 0.0f;
+  const auto brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.bias), 0, bias ? g.bias_bytes : 0,
+                                                     0x00020000);
+  int noff[NJ], nbo[NJ];
+  float bn[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = nb + j * 32 + lr;
+    noff[j] = n < g.N ? int(n * g.c_n * 2) : kSkip;
+    nbo[j] = n < g.N ? int(n * g.bias_sn * 2) : kSkip;
+    bn[j] = bias && g.bias_mode == 1 ? bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, nbo[j], 0, 0)) : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mb + i * 32 + mfma_row(r, lane);
+      const bool mok = m < g.M;
+      const int moff = mok ? int(m * g.c_m * 2) : kSkip;
+      const int mbo = mok ? int(m * g.bias_sm * 2) : kSkip;
+      float bm = 0.0f;
+      if (bias && g.bias_mode == 3) bm = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, mbo, 0, 0));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        float v = g.alpha * acc[i][j][r];
+        if (bias) {
+          float bv = g.bias_mode == 1 ? bn[j] : bm;
+          if (g.bias_mode == 2) bv = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, mbo + nbo[j], 0, 0));
+          v += g.beta * bv;
+        }
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), crs, moff + noff[j], 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
 
 // Stages rows [r0, r0+128) x k [k0, k0+32) of a row-major-by-strides operand into
 // lds[row][k].  rows: valid row count; K: valid k count.
@@ -138,6 +212,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     }
   }
 
+  if (g.rs_ok) {
+    store_block<2, 2>(g, batch, split, acc, m0 + wm * 64, n0 + wn * 64, lane);
+    return;
+  }
   if (g.part) {
     float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
 #pragma unroll
@@ -315,6 +393,10 @@ void gemm2_kernel(GemmArgs g) {
     cur ^= 1;
   }
 
+  if (g.rs_ok) {
+    store_block<4, 2>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 64, lane);
+    return;
+  }
   if (g.part) {
     float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
 #pragma unroll
@@ -542,44 +624,9 @@ void gemm4_kernel(GemmArgs g) {
 #undef XDNA_G4_FRAGS
 #undef XDNA_G4_MFMA
 
-  if (g.part) {
-    float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 128 + j * 32 + lr;
-        if (n >= g.N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 128 + i * 32 + mfma_row(r, lane);
-          if (m < g.M) P[int64_t(m) * g.N + n] = acc[i][j][r];
-        }
-      }
-    return;
-  }
-  uint16_t* C = g.c + int64_t(batch) * g.c_batch;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 128 + j * 32 + lr;
-      if (n >= g.N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + i * 32 + mfma_row(r, lane);
-        if (m >= g.M) continue;
-        float v = g.alpha * acc[i][j][r];
-        if (g.bias_mode && g.beta != 0.0f) {
-          float bv;
-          if (g.bias_mode == 1) bv = bf16_to_f32(g.bias[int64_t(n) * g.bias_sn]);
-          else if (g.bias_mode == 2) bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm + int64_t(n) * g.bias_sn]);
-          else bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm]);
-          v += g.beta * bv;
-        }
-        C[int64_t(m) * g.c_m + int64_t(n) * g.c_n] = f32_to_bf16(v);
-      }
-    }
+  // buffer-resource epilogue only (the launcher checks rs_ok): a second, per-element
+  // path would keep every accumulator live across both and spill them
+  store_block<4, 4>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
 }
 
 // Split-K epilogue: C[b][m][n] = bf16(alpha * sum over splits (in split order) of the fp32
@@ -694,6 +741,24 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   g.bias_sn = bias_sn;
   g.alpha = alpha;
   g.beta = beta;
+  {
+    // byte extents of one batch element's C, bias and partials: the buffer-resource
+    // epilogue needs every offset below kSkip (else the per-element form runs)
+    const auto ext = [](int64_t rows, int64_t s_r, int64_t cols, int64_t s_c) {
+      return ((rows - 1) * s_r + (cols - 1) * s_c + 1) * 2;
+    };
+    const int64_t cb = ext(M, ldc_m, N, ldc_n);
+    int64_t bb = 0;
+    bool nonneg = ldc_m >= 0 && ldc_n >= 0;
+    if (bias_mode == 1) bb = ext(1, 0, N, bias_sn), nonneg = nonneg && bias_sn >= 0;
+    if (bias_mode == 2) bb = ext(M, bias_sm, N, bias_sn), nonneg = nonneg && bias_sm >= 0 && bias_sn >= 0;
+    if (bias_mode == 3) bb = ext(M, bias_sm, 1, 0), nonneg = nonneg && bias_sm >= 0;
+    const int64_t pb = int64_t(M) * N * 4;
+    g.rs_ok = nonneg && cb < kSkip && bb < kSkip && pb < kSkip ? 1 : 0;
+    g.c_bytes = int(std::min<int64_t>(cb, kSkip));
+    g.bias_bytes = int(std::min<int64_t>(bb, kSkip));
+    g.part_bytes = int(std::min<int64_t>(pb, kSkip));
+  }
   const int ma = stage_mode(A, lda_m, lda_k, stride_a, batch);
   const int mb = stage_mode(Bm, ldb_n, ldb_k, stride_b, batch);
   if (!admit_launch("xdna_gemm_bf16")) return -1;
@@ -712,10 +777,13 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   const bool fits4 = vec_ok && K > 0 && (K % 8) == 0 && (ma != kAlongRow || (M % 8) == 0) &&
                      (mb != kAlongRow || (N % 8) == 0) && extent(M, lda_m, lda_k, K) < (int64_t(1) << 31) &&
                      extent(N, ldb_n, ldb_k, K) < (int64_t(1) << 31);
-  // the four-wave kernel's longer prologue and epilogue (one wave per SIMD) only pay off
-  // over a long K (measured on config 3's GEMMs: ahead from K = 4096, behind at 1024)
-  const bool use4 = fits4 && (variant == 3 || (variant == 0 && tiles2 >= 64 && K >= 2048));
-  if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && tiles2 >= 64))) {
+  // Large tiles when the grid has enough of them, or when a long K can be split into
+  // enough work (Gram-like products: measured 1.5x the small kernel at K = 51840).  The
+  // four-wave kernel's longer prologue (one wave per SIMD) pays off from K = 1024 on
+  // config 3's GEMMs (even there, ahead of the eight-wave kernel from K = 4096).
+  const bool big = tiles2 >= 64 || K >= 16384;
+  const bool use4 = fits4 && g.rs_ok && (variant == 3 || (variant == 0 && big && K >= 1024));
+  if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && big))) {
     // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
     const int kt2 = int(ceil_div(K, kK2));
     g.nsplit = 1;
