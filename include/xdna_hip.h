@@ -280,7 +280,9 @@ int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, 
  * 5 its four-wave form (one wave per SIMD with 128 x 128 wave tiles, fragments
  * software-pipelined; cout > 128 only; the automatic choice for cout >= 256 on large
  * grids), 6 / 7 / 8 four-wave kernels with 128 channels x 256 rows, 128 channels x 512
- * rows and 64 channels x 512 rows per workgroup (any cout).
+ * rows and 64 channels x 512 rows per workgroup (any cout), 9 the four-wave kernel with
+ * 64 channels x 256 rows and two workgroups per CU (the automatic choice up to 256
+ * output channels on all but the smallest grids).
  * Results agree to the same tolerance; only the
  * summation grouping differs.  No reference counterpart (a tuning knob, like the
  * reference's XDNA_* performance environment variables).  XDNA_ROWS_VARIANT sets the

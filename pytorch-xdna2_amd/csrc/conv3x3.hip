@@ -522,8 +522,8 @@ struct Q4 {
   static constexpr size_t Lds = size_t(XRows * kPitch + 3 * Slot) * 2;
 };
 
-template <int MT, int NT, int WM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int MT, int NT, int WM, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 void conv_rows4_kernel(RowsArgs a) {
   using Q = Q4<MT, NT, WM>;
   constexpr int kXv = (Q::XRows * 8 + 255) / 256;      // window vectors per thread
@@ -1375,11 +1375,11 @@ int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, 
   return check_launch("conv3x3 weight preparation");
 }
 
-template <int MT, int NT, int WM>
+template <int MT, int NT, int WM, int OCC = 1>
 int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   using Q = Q4<MT, NT, WM>;
   static const bool lds_ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM, OCC>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess;
   if (!lds_ok) {
     set_error("conv3x3 rows: cannot enable the four-wave kernel's LDS size");
@@ -1388,7 +1388,7 @@ int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   a.nrt = int(ceil_div(geom.m_total, Q::TP));
   a.ncot = int(ceil_div(cout, Q::CO));
   const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
-  conv_rows4_kernel<MT, NT, WM><<<grid, 256, Q::Lds, st>>>(a);
+  conv_rows4_kernel<MT, NT, WM, OCC><<<grid, 256, Q::Lds, st>>>(a);
   return check_launch("conv3x3 rows");
 }
 
@@ -1432,7 +1432,6 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   // loads; below that the small-grid kernel, which stages whole chunks, is faster.
   int variant = g_rows_variant.load();
   const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
-  const int64_t big128 = ceil_div(geom.m_total, 128) * ytiles;
   if (variant == 0) {
     // Automatic choice (fitted to the sweep shapes on an MI355X).  Grids of a few hundred
     // 128-row tiles or less: the small-grid kernel (whole chunks staged per workgroup,
@@ -1440,20 +1439,24 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     //   ceil(workgroups / 256) * (tile channels * tile rows) * per-MFMA cost
     // is least (one workgroup per CU; the 128 x 256 and 64 x 512 tiles issue 8 MFMAs per 6
     // fragment reads instead of 16 per 8: cost 1.1).  Ties go to the first candidate.
-    const bool small = cout <= kSCo ? ceil_div(geom.m_total, 512) < 150 : big128 < 300;
-    if (small) {
+    // Below ~150 workgroups of the 64 x 256 two-per-CU kernel: the small-grid kernel.  Up
+    // to 256 output channels: the two-per-CU kernel (its second workgroup hides the
+    // per-tap weight loads and the prologue of the other; measured 7 % ahead of the
+    // one-per-CU tiles over the sweep's C <= 256 shapes).  Wider: the modelled choice.
+    const int64_t wgs9 = ceil_div(geom.m_total, 256) * ceil_div(cout, kSCo);
+    if (wgs9 < 150) {
       variant = -1;
+    } else if (cout <= 2 * kTCo) {
+      variant = 9;
     } else {
-      struct Cand { int v, co, tp; double cost; };
-      const Cand all[] = {{7, 128, 512, 1.0}, {5, 256, 256, 1.0}, {6, 128, 256, 1.1}, {8, 64, 512, 1.1}};
+      // slots: workgroups one round holds (256 CUs x workgroups per CU)
+      struct Cand { int v, co, tp, slots; double cost; };
+      const Cand all[] = {{7, 128, 512, 256, 1.0}, {5, 256, 256, 256, 1.0}, {6, 128, 256, 256, 1.1},
+                          {9, 64, 256, 512, 1.05}};
       double best = 1e300;
       for (const Cand& c : all) {
-        if (c.v == 5 && cout <= kTCo) continue;            // 256-channel tiles: cout > 128 only
-        if (c.v == 8 && cout > kTCo) continue;
-        if (c.v == 7 && cout <= kSCo) continue;            // <= 64 channels: 64-channel tiles only
-        if (c.v == 6 && cout <= kSCo) continue;
         const int64_t wgs = ceil_div(geom.m_total, c.tp) * ceil_div(cout, c.co);
-        const double t = double(ceil_div(wgs, 256)) * double(c.co) * c.tp * c.cost;
+        const double t = double(ceil_div(wgs, c.slots)) * (c.slots / 256) * double(c.co) * c.tp * c.cost;
         if (t < best) {
           best = t;
           variant = c.v;
@@ -1467,6 +1470,8 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   if (variant == 6) return launch_rows4<2, 4, 2>(a, geom, cout, st);
   if (variant == 7) return launch_rows4<4, 4, 1>(a, geom, cout, st);
   if (variant == 8) return launch_rows4<2, 4, 1>(a, geom, cout, st);
+  // 64 x 256 tiles, two workgroups per CU (76 KB of LDS each)
+  if (variant == 9) return launch_rows4<2, 2, 1, 2>(a, geom, cout, st);
   // the wide kernels: 256-channel tiles (cout > 128 only: the weights are padded to 256
   // rows from there on); the four-wave form unless the eight-wave one is asked for
   const bool wide = cout > kTCo && (variant == 4 || variant == 5);
@@ -1515,7 +1520,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     return -1;
   }
   const unsigned stiles = unsigned(ceil_div(cout, kSCo));
-  const int64_t tp128_min = cout <= kSCo ? 128 : 256;  // measured on the sweep shapes
+  const int64_t tp128_min = 128;  // measured on the sweep shapes
   const int TP = variant == 2 ? 64 : variant == 3 ? 128 : (ceil_div(geom.m_total, 128) * stiles >= tp128_min ? 128 : 64);
   const int64_t valid = ceil_div(geom.m_total, TP) * stiles;
   // Fewer workgroups than CUs: split the input chunks over blockIdx.z and sum the fp32
@@ -1787,7 +1792,7 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {
-  if (variant < 0 || variant > 8) {
+  if (variant < 0 || variant > 9) {
     set_error("xdna_conv3x3_set_rows_variant: variant must be 0..8");
     return -1;
   }
