@@ -384,6 +384,15 @@ int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const voi
                                 const float* save_mean, const float* save_invstd, uint16_t* dx, void* dweight,
                                 void* dbias, int64_t B, int64_t C, int64_t L, void* stream);
 
+/* Nearest-neighbour upsampling by exactly 2 of `planes` NCHW bf16 planes of H x W (the
+ * input size): y[p][oy][ox] = x[p][oy/2][ox/2] into 2H x 2W planes; the backward writes
+ * dx[p][iy][ix] = bf16(fp32 sum of the 2x2 block of dy, row-major order).  Buffers
+ * 4-byte aligned.  Replaces upsample_nearest2d(_backward) through the zero-copy CPU
+ * fallback (torch_xdna_device.cpp:5124-5260). */
+int xdna_upsample_nearest2x_bf16(const uint16_t* x, uint16_t* y, int64_t planes, int H, int W, void* stream);
+int xdna_upsample_nearest2x_bwd_bf16(const uint16_t* dy, uint16_t* dx, int64_t planes, int H, int W,
+                                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,8 +15,8 @@
 // operands are staged k-contiguous in LDS ([row][k], pitch 40) so every MFMA fragment is
 // one 16-byte read; the next k-tile's gathers are issued into registers while the
 // current one is multiplied (double-buffered LDS, one barrier per k-tile).  The weight
-// gradient splits its pixel reduction over blockIdx.z into fp32 partials, summed in split
-// order by a second kernel (deterministic).
+// gradient splits its pixel reduction over blockIdx.z into fp32 partials, summed in a
+// fixed order by a second kernel (deterministic).
 #include "common.h"
 #include "mfma.h"
 #include "../../include/xdna_hip.h"
@@ -279,14 +279,28 @@ __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
   }
 }
 
-// gw[m][n] = bf16(sum over splits, in split order, of part[s][m][n])
+// gw[m][n] = bf16(sum over splits of part[s][m][n]): the 256 threads are 8 groups of 32
+// consecutive outputs; group z sums splits z, z + 8, ... and the groups are added in
+// order through LDS (a fixed association per output, so the result is deterministic;
+// eight loads in flight per output where one thread per output waited on each split).
 __global__ __launch_bounds__(256) void gather_reduce_kernel(const float* __restrict__ part,
                                                             uint16_t* __restrict__ gw, int64_t mn,
                                                             int nsplit) {
-  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < mn; i += int64_t(gridDim.x) * 256) {
+  constexpr int ZG = 8, EPB = 256 / ZG;
+  const int z = threadIdx.x / EPB, e = threadIdx.x % EPB;
+  __shared__ float red[256];
+  for (int64_t base = int64_t(blockIdx.x) * EPB; base < mn; base += int64_t(gridDim.x) * EPB) {
+    const int64_t i = base + e;
     float s = 0.0f;
-    for (int z = 0; z < nsplit; ++z) s += part[int64_t(z) * mn + i];
-    gw[i] = f32_to_bf16(s);
+    if (i < mn)
+      for (int k = z; k < nsplit; k += ZG) s += part[int64_t(k) * mn + i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    if (z == 0) {
+      for (int q = 1; q < ZG; ++q) s += red[q * EPB + e];
+      if (i < mn) gw[i] = f32_to_bf16(s);
+    }
+    __syncthreads();
   }
 }
 
@@ -394,8 +408,8 @@ int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, 
     xdna_hip_cache_free(a.part);
     return -1;
   }
-  gather_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(mn, 256), 4096)), 256, 0, st>>>(a.part, gw, mn,
-                                                                                          a.nsplit);
+  gather_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(mn, 32), 8192)), 256, 0, st>>>(a.part, gw, mn,
+                                                                                         a.nsplit);
   // stream-ordered reuse: the next user of the block runs after the reduce
   xdna_hip_cache_free(a.part);
   if (check_launch("xdna_conv2d_wgrad_bf16")) return -1;

@@ -1,0 +1,91 @@
+// Nearest-neighbour 2x upsampling of NCHW bf16 planes and its gradient: the style
+// generator's "nearest up x2" layers.  For an exact factor of 2, PyTorch's nearest source
+// index floor(dst * 0.5) is dst / 2 (its scale 1/2 is exact in fp32), so
+//   y[p][oy][ox] = x[p][oy / 2][ox / 2],
+// and the gradient sums each 2x2 block of dy in fp32 in row-major order, (0,0), (0,1),
+// (1,0), (1,1), then rounds once to bf16, as PyTorch's backward accumulates in float.
+// The reference runs both from PyTorch's CPU kernels through its zero-copy fallback
+// (torch_xdna_device.cpp:5124-5260).
+//
+// One thread per input pixel: the forward reads 2 bytes and writes two 4-byte pairs, the
+// backward reads two 4-byte pairs and writes 2 bytes (output columns 2*ix are even, so
+// the pairs are 4-byte aligned).  HBM-bound.
+#include "common.h"
+#include "../../include/xdna_hip.h"
+
+namespace xdna {
+namespace {
+
+__global__ __launch_bounds__(256) void upsample2x_kernel(const uint16_t* __restrict__ x,
+                                                         uint16_t* __restrict__ y, int64_t n, int H,
+                                                         int W) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const int64_t row = i / W;  // plane * H + iy
+    const int ix = int(i - row * W);
+    const uint32_t v = x[i];
+    const uint32_t pair = v | (v << 16);
+    uint32_t* o = reinterpret_cast<uint32_t*>(y + (2 * row) * (2 * int64_t(W)) + 2 * ix);
+    o[0] = pair;
+    o[W] = pair;  // the next output row: 2W elements = W pairs further
+  }
+  (void)H;
+}
+
+__global__ __launch_bounds__(256) void upsample2x_bwd_kernel(const uint16_t* __restrict__ dy,
+                                                             uint16_t* __restrict__ dx, int64_t n, int H,
+                                                             int W) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const int64_t row = i / W;
+    const int ix = int(i - row * W);
+    const uint32_t* g = reinterpret_cast<const uint32_t*>(dy + (2 * row) * (2 * int64_t(W)) + 2 * ix);
+    const uint32_t a = g[0], b = g[W];
+    float s = __uint_as_float(a << 16);
+    s += __uint_as_float(a & 0xFFFF0000u);
+    s += __uint_as_float(b << 16);
+    s += __uint_as_float(b & 0xFFFF0000u);
+    dx[i] = f32_to_bf16(s);
+  }
+  (void)H;
+}
+
+bool resample_args(const char* what, const void* src, const void* dst, int64_t planes, int H, int W) {
+  if (planes < 0 || H < 0 || W < 0 || ((planes * H * W) > 0 && (!src || !dst))) {
+    set_error(std::string(what) + ": invalid arguments");
+    return false;
+  }
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 3) {
+    set_error(std::string(what) + ": buffers must be 4-byte aligned");
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" {
+
+int xdna_upsample_nearest2x_bf16(const uint16_t* x, uint16_t* y, int64_t planes, int H, int W, void* stream) {
+  if (!resample_args("xdna_upsample_nearest2x_bf16", x, y, planes, H, W)) return -1;
+  const int64_t n = planes * H * W;
+  if (n == 0) return 0;
+  if (!admit_launch("xdna_upsample_nearest2x_bf16")) return -1;
+  upsample2x_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(x, y, n,
+                                                                                                          H, W);
+  return check_launch("xdna_upsample_nearest2x_bf16");
+}
+
+int xdna_upsample_nearest2x_bwd_bf16(const uint16_t* dy, uint16_t* dx, int64_t planes, int H, int W,
+                                     void* stream) {
+  if (!resample_args("xdna_upsample_nearest2x_bwd_bf16", dy, dx, planes, H, W)) return -1;
+  const int64_t n = planes * H * W;
+  if (n == 0) return 0;
+  if (!admit_launch("xdna_upsample_nearest2x_bwd_bf16")) return -1;
+  upsample2x_bwd_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(
+      dy, dx, n, H, W);
+  return check_launch("xdna_upsample_nearest2x_bwd_bf16");
+}
+
+}  // extern "C"

@@ -944,6 +944,64 @@ at::Tensor instance_norm_autograd_xdna(const at::Tensor& input, const std::optio
                                    eps, cudnn_enabled);
 }
 
+// ---------------------------------------------------------------------------------------
+// Nearest 2x upsampling (the style generator's decoder) and its gradient: one HIP kernel
+// each for bf16 NCHW-contiguous tensors upsampled by exactly 2 (no scale, or scale 2);
+// other forms run PyTorch-ROCm's kernels on aliases.  The reference runs both on its CPU
+// through the fallback (torch_xdna_device.cpp:5124-5260).
+// ---------------------------------------------------------------------------------------
+bool nearest2x_ok(const at::Tensor& t, int64_t oh, int64_t ow, int64_t ih, int64_t iw,
+                  std::optional<double> sh, std::optional<double> sw) {
+  if (g_mode.load() < 1 || t.scalar_type() != at::kBFloat16 || t.dim() != 4 || t.device().type() != kXdna)
+    return false;
+  if (oh != 2 * ih || ow != 2 * iw || ih < 1 || iw < 1) return false;
+  if ((sh && *sh != 2.0) || (sw && *sw != 2.0)) return false;
+  return t.is_contiguous() && (reinterpret_cast<uintptr_t>(t.const_data_ptr()) & 3) == 0;
+}
+
+at::Tensor upsample_nearest2d_xdna(const at::Tensor& self, c10::SymIntArrayRef output_size,
+                                   std::optional<double> scales_h, std::optional<double> scales_w) {
+  if (output_size.size() == 2 && self.dim() == 4 &&
+      nearest2x_ok(self, output_size[0].expect_int(), output_size[1].expect_int(), self.size(2), self.size(3),
+                   scales_h, scales_w)) {
+    ScopedCount sc("hip_upsample_nearest2x.fwd.run");
+    const int64_t B = self.size(0), C = self.size(1), H = self.size(2), W = self.size(3);
+    at::Tensor y = empty_xdna({B, C, 2 * H, 2 * W}, at::kBFloat16);
+    check_abi(xdna_upsample_nearest2x_bf16(static_cast<const uint16_t*>(self.const_data_ptr()),
+                                           static_cast<uint16_t*>(y.data_ptr()), B * C, int(H), int(W),
+                                           current_stream()),
+              "upsample_nearest2d");
+    return y;
+  }
+  ScopedCount sc("aten::upsample_nearest2d.rocm");
+  BelowAutograd g;
+  return back(at::_ops::upsample_nearest2d::call(rocm(self), output_size, scales_h, scales_w));
+}
+
+at::Tensor upsample_nearest2d_backward_xdna(const at::Tensor& grad_output, c10::SymIntArrayRef output_size,
+                                            c10::SymIntArrayRef input_size, std::optional<double> scales_h,
+                                            std::optional<double> scales_w) {
+  if (output_size.size() == 2 && input_size.size() == 4 && grad_output.dim() == 4) {
+    const int64_t B = input_size[0].expect_int(), C = input_size[1].expect_int();
+    const int64_t H = input_size[2].expect_int(), W = input_size[3].expect_int();
+    const int64_t oh = output_size[0].expect_int(), ow = output_size[1].expect_int();
+    if (grad_output.size(0) == B && grad_output.size(1) == C && grad_output.size(2) == oh &&
+        grad_output.size(3) == ow && nearest2x_ok(grad_output, oh, ow, H, W, scales_h, scales_w)) {
+      ScopedCount sc("hip_upsample_nearest2x.bwd.run");
+      at::Tensor dx = empty_xdna({B, C, H, W}, at::kBFloat16);
+      check_abi(xdna_upsample_nearest2x_bwd_bf16(static_cast<const uint16_t*>(grad_output.const_data_ptr()),
+                                                 static_cast<uint16_t*>(dx.data_ptr()), B * C, int(H), int(W),
+                                                 current_stream()),
+                "upsample_nearest2d_backward");
+      return dx;
+    }
+  }
+  ScopedCount sc("aten::upsample_nearest2d_backward.rocm");
+  BelowAutograd g;
+  return back(at::_ops::upsample_nearest2d_backward::call(rocm(grad_output), output_size, input_size, scales_h,
+                                                          scales_w));
+}
+
 void register_autograd_ops(torch::Library& m) {
   m.impl("instance_norm", TORCH_FN(instance_norm_autograd_xdna));
 }
@@ -964,6 +1022,8 @@ void register_hot_ops(torch::Library& m) {
   m.impl("_foreach_add_.Scalar", TORCH_FN(foreach_add_scalar_xdna));
   m.impl("native_batch_norm", TORCH_FN(native_batch_norm_xdna));
   m.impl("native_batch_norm_backward", TORCH_FN(native_batch_norm_backward_xdna));
+  m.impl("upsample_nearest2d", TORCH_FN(upsample_nearest2d_xdna));
+  m.impl("upsample_nearest2d_backward", TORCH_FN(upsample_nearest2d_backward_xdna));
 }
 
 }  // namespace xdna_backend

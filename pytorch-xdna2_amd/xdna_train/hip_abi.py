@@ -66,6 +66,8 @@ SIGNATURES = {
     "xdna_conv2d_fwd_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),
     "xdna_instance_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, ctypes.c_double, P]),
     "xdna_instance_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
+    "xdna_upsample_nearest2x_bf16": (I, [P, P, L, I, I, P]),
+    "xdna_upsample_nearest2x_bwd_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_dgrad_bf16": (I, [P, P, P] + [I] * 11 + [P]),
     "xdna_conv2d_wgrad_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),
     "xdna_conv3x3w_unpack_output_bf16": (I, [P, P, I, I, I, I, I, I, P]),
