@@ -271,6 +271,13 @@ int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, 
                            int Cout, int H, int W, int KH, int KW, int sh, int sw, int ph, int pw,
                            void* stream);
 
+/* Kernel selection of xdna_conv2d_fwd_bf16 / xdna_conv2d_dgrad_bf16, for measurements and
+ * tests: 0 automatic (default: at stride 1 with at most 32 output and at least 16 input
+ * channels of the direction, and a padded output width up to 128, the direct form, which stages the
+ * input rows of 4 output rows in LDS as a zero-padded grid and reads every tap as a row
+ * offset; else the gather GEMM), 1 the gather GEMM only.  No reference counterpart. */
+int xdna_conv2d_set_variant(int variant);
+
 /* Kernel selection of xdna_conv3x3_rows_bf16 (and the conv calls built on it), for
  * measurements and tests: 0 automatic (default), 1 the main kernel (128 output channels
  * x 64-256 rows per workgroup, weights streamed from L2 per tap), 2 / 3 the small-grid
@@ -392,6 +399,16 @@ int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const voi
 int xdna_upsample_nearest2x_bf16(const uint16_t* x, uint16_t* y, int64_t planes, int H, int W, void* stream);
 int xdna_upsample_nearest2x_bwd_bf16(const uint16_t* dy, uint16_t* dx, int64_t planes, int H, int W,
                                      void* stream);
+
+/* Stride-2 sampling of `planes` NCHW bf16 planes whose full size is H x W: subsample2
+ * writes y[p][oy][ox] = full[p][2oy][2ox] into ceil(H/2) x ceil(W/2) planes; dilate2
+ * writes full[p][y][x] = dy[p][y/2][x/2] at even (y, x) and 0 elsewhere.  A 3x3 / stride-2
+ * / pad-1 conv is the stride-1 conv subsampled this way, and its input and weight
+ * gradients are the stride-1 ones of the dilated gradient.  No reference counterpart (the
+ * reference runs strided convs on its CPU through the fallback, torch_xdna_device.cpp:
+ * 4524-4606, 4608-4885). */
+int xdna_subsample2_bf16(const uint16_t* full, uint16_t* y, int64_t planes, int H, int W, void* stream);
+int xdna_dilate2_bf16(const uint16_t* dy, uint16_t* full, int64_t planes, int H, int W, void* stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@
 #include "../../include/xdna_hip.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace xdna {
 namespace {
@@ -38,7 +39,22 @@ struct GArgs {
   float* part;           // wgrad: [nsplit][M][N]
   int B, Cin, Cout, H, W, KH, KW, sh, sw, ph, pw, Ho, Wo;
   int M, N, K, kt_per, nsplit;
+  int x_bytes, w_bytes, dy_bytes;  // operand extents (each under 2^31 bytes)
 };
+
+// Buffer resources over the three operands: a load at an out-of-range offset returns
+// zero without a memory access, which is how every masked element below is read.
+struct GRs {
+  __amdgpu_buffer_rsrc_t x, w, dy;
+};
+
+__device__ inline GRs g_rs(const GArgs& a) {
+  GRs r;
+  r.x = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), 0, a.x_bytes, 0x00020000);
+  r.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.w), 0, a.w_bytes, 0x00020000);
+  r.dy = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.dy), 0, a.dy_bytes, 0x00020000);
+  return r;
+}
 
 // Element (row, k) of operand A and (col, k) of operand B, with the per-thread row state
 // precomputed once.  Out-of-range elements are zero.
@@ -75,20 +91,22 @@ __device__ inline RowState b_row(const GArgs& a, int n) {
   return r;
 }
 
-// Every gather below is branch-free: the address of an out-of-range element is replaced by
-// the operand's first element and the loaded value is masked, so all loads of a k-tile
-// are in flight together (a branch per element would serialise them, one memory latency
-// each).
-// offsets are 32-bit: every operand holds fewer than 2^31 elements (checked on entry)
-__device__ inline uint32_t ld_masked(const uint16_t* base, int off, bool ok) {
-  const uint32_t v = base[ok ? off : 0];
-  return ok ? v : 0u;
+// Every gather below is branch-free: a masked element's offset is replaced by one past
+// the resource's end, so the hardware returns zero without a memory access, and all loads
+// of a k-tile are in flight together (a branch per element would serialise them, one
+// memory latency each; redirecting masked loads to element 0 instead queued them all on
+// that one address).  Offsets are 32-bit: every operand holds fewer than 2^30 elements
+// (checked on entry).
+constexpr int kOob = int(0x80000000u);
+
+__device__ inline uint32_t ld_masked(__amdgpu_buffer_rsrc_t rs, int off, bool ok) {
+  return __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? off * 2 : kOob, 0, 0);
 }
 
 // B operand: elements (n, k0 .. k0+15) packed as bf16 pairs into u[8].  S1: unit strides
 // (dgrad needs no division then).
 template <int DIR, bool S1>
-__device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint32_t (&u)[8]) {
+__device__ inline void gather_b(const GArgs& a, const GRs& rs, const RowState& r, int k0, uint32_t (&u)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) u[i] = 0;
   if (DIR == kGFwd) {
@@ -100,7 +118,7 @@ __device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint3
     for (int e = 0; e < 16; ++e) {
       const int iy = r.y0 + ky, ix = r.x0 + kx;
       const bool ok = r.valid & (k0 + e < a.K) & (iy >= 0) & (iy < a.H) & (ix >= 0) & (ix < a.W);
-      u[e >> 1] |= ld_masked(a.x, ((img + ci) * a.H + iy) * a.W + ix, ok) << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(rs.x, ((img + ci) * a.H + iy) * a.W + ix, ok) << ((e & 1) * 16);
       if (++kx == a.KW) { kx = 0; if (++ky == a.KH) { ky = 0; ++ci; } }
     }
   } else if (DIR == kGDgrad) {
@@ -122,7 +140,7 @@ __device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint3
         ok = ok & (oy * a.sh == ty) & (ox * a.sw == tx);
       }
       ok = ok & (oy < a.Ho) & (ox < a.Wo);
-      u[e >> 1] |= ld_masked(a.dy, ((img + co) * a.Ho + oy) * a.Wo + ox, ok) << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(rs.dy, ((img + co) * a.Ho + oy) * a.Wo + ox, ok) << ((e & 1) * 16);
       if (++kx == a.KW) { kx = 0; if (++ky == a.KH) { ky = 0; ++co; } }
     }
   } else {
@@ -133,7 +151,7 @@ __device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint3
     for (int e = 0; e < 16; ++e) {
       const int iy = oy * a.sh - a.ph + r.ky, ix = ox * a.sw - a.pw + r.kx;
       const bool ok = r.valid & (k0 + e < a.K) & (iy >= 0) & (iy < a.H) & (ix >= 0) & (ix < a.W);
-      u[e >> 1] |= ld_masked(a.x, ((b * a.Cin + r.ci) * a.H + iy) * a.W + ix, ok) << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(rs.x, ((b * a.Cin + r.ci) * a.H + iy) * a.W + ix, ok) << ((e & 1) * 16);
       if (++ox == a.Wo) { ox = 0; if (++oy == a.Ho) { oy = 0; ++b; } }
     }
   }
@@ -141,7 +159,7 @@ __device__ inline void gather_b(const GArgs& a, const RowState& r, int k0, uint3
 
 // A operand: row m, KPT consecutive k from k0, packed as bf16 pairs
 template <int DIR, int KPT>
-__device__ inline void gather_a(const GArgs& a, int m, int k0, uint32_t (&u)[KPT / 2]) {
+__device__ inline void gather_a(const GArgs& a, const GRs& rs, int m, int k0, uint32_t (&u)[KPT / 2]) {
 #pragma unroll
   for (int i = 0; i < KPT / 2; ++i) u[i] = 0;
   const bool mok = m < a.M;
@@ -149,14 +167,14 @@ __device__ inline void gather_a(const GArgs& a, int m, int k0, uint32_t (&u)[KPT
     const int row = m * a.K;
 #pragma unroll
     for (int e = 0; e < KPT; ++e)
-      u[e >> 1] |= ld_masked(a.w, row + k0 + e, mok & (k0 + e < a.K)) << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(rs.w, row + k0 + e, mok & (k0 + e < a.K)) << ((e & 1) * 16);
   } else if (DIR == kGDgrad) {
     // w[co][m][ky][kx] for k = (co, ky, kx)
     const int khw = a.KH * a.KW;
     int co = k0 / khw, r = k0 - co * khw;
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      u[e >> 1] |= ld_masked(a.w, (co * a.Cin + m) * khw + r, mok & (k0 + e < a.K)) << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(rs.w, (co * a.Cin + m) * khw + r, mok & (k0 + e < a.K)) << ((e & 1) * 16);
       if (++r == khw) { r = 0; ++co; }
     }
   } else {
@@ -165,7 +183,7 @@ __device__ inline void gather_a(const GArgs& a, int m, int k0, uint32_t (&u)[KPT
     int b = k0 / hw, rem = k0 - b * hw;
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      u[e >> 1] |= ld_masked(a.dy, (b * a.Cout + m) * hw + rem, mok & (k0 + e < a.K)) << ((e & 1) * 16);
+      u[e >> 1] |= ld_masked(rs.dy, (b * a.Cout + m) * hw + rem, mok & (k0 + e < a.K)) << ((e & 1) * 16);
       if (++rem == hw) { rem = 0; ++b; }
     }
   }
@@ -194,6 +212,7 @@ __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
   const int am = m0 + tid / TPR, ak = (tid % TPR) * KPT;
   const int bn = tid >> 1, bk = (tid & 1) * 16;
   const RowState br = b_row<DIR>(a, n0 + bn);
+  const GRs rs = g_rs(a);
 
   f32x16_t acc[MT][NT];
 #pragma unroll
@@ -215,8 +234,8 @@ __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
   };
 
   if (kt0 < kt1) {
-    gather_a<DIR, KPT>(a, am, kt0 * kGTK + ak, ua);
-    gather_b<DIR, S1>(a, br, kt0 * kGTK + bk, ub);
+    gather_a<DIR, KPT>(a, rs, am, kt0 * kGTK + ak, ua);
+    gather_b<DIR, S1>(a, rs, br, kt0 * kGTK + bk, ub);
     store(0);
   }
   __syncthreads();
@@ -224,8 +243,8 @@ __global__ __launch_bounds__(256) void conv_gather_kernel(GArgs a) {
     const int cur = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
     if (more) {
-      gather_a<DIR, KPT>(a, am, (kt + 1) * kGTK + ak, ua);
-      gather_b<DIR, S1>(a, br, (kt + 1) * kGTK + bk, ub);
+      gather_a<DIR, KPT>(a, rs, am, (kt + 1) * kGTK + ak, ua);
+      gather_b<DIR, S1>(a, rs, br, (kt + 1) * kGTK + bk, ub);
     }
 #pragma unroll
     for (int ks = 0; ks < kGTK / 16; ++ks) {
@@ -327,6 +346,9 @@ bool gconv_args(const char* what, GArgs& a, int B, int Cin, int Cout, int H, int
     set_error(std::string(what) + ": tensor too large");
     return false;
   }
+  a.x_bytes = int(int64_t(B) * Cin * H * W * 2);
+  a.w_bytes = int(int64_t(Cout) * Cin * KH * KW * 2);
+  a.dy_bytes = int(int64_t(B) * Cout * a.Ho * a.Wo * 2);
   return true;
 }
 
@@ -347,6 +369,269 @@ int launch_gather(GArgs& a, hipStream_t st) {
   if (DIR == kGDgrad && a.sh == 1 && a.sw == 1) launch_gather_s<DIR, true>(a, grid, tm, st);
   else launch_gather_s<DIR, false>(a, grid, tm, st);
   return check_launch("conv gather");
+}
+
+// ---------------------------------------------------------------------------------------
+// Direct form for few output channels (<= 32) at stride 1: the style network's 9x9 input
+// and output layers (3 -> 32, 32 -> 3, and the 32 -> 3 layer's input gradient), where the
+// gather GEMM pads M to 32 rows and fetches every operand element from global memory.
+// Workgroup = (image, kDTR output rows, all columns).  The input rows it needs sit in LDS
+// as a zero-padded grid of Wp = Wo + KW - 1 columns, pixel-major with 32 channels per
+// position; output pixel (oy, ox) is grid position q = (oy - oy0) * Wp + ox and tap
+// (ky, kx) reads position q + ky * Wp + kx, so a B fragment (32 consecutive q x 8
+// channels) is one 16-byte LDS read per lane (columns ox >= Wo are computed and dropped).
+// Prepared weights [chunk][ky][32 co][KW][32 ci] are staged one kernel row at a time; the
+// next row is loaded into registers during the current row's MFMAs.  Two workgroups fit
+// a CU (67 KB of LDS for the 9x9 layers at 36 x 36).
+// ---------------------------------------------------------------------------------------
+constexpr int kDTR = 4;        // output rows per workgroup
+constexpr int kDCK = 32;       // channels per chunk
+constexpr int kDPitch = 40;    // LDS pitch (elements) of one grid position / weight row
+constexpr int kDMaxNB = 16;    // grid blocks of 32 positions (kDTR * Wp <= 512)
+constexpr int kDXItems = 16;   // staging items (position x 8 channels) per thread
+
+// 16-byte weight vectors per thread per kernel row: 32 rows x KW taps x 4 vectors,
+// rounded up to whole rounds of 256 threads (the prepared rows are zero-padded to that, so
+// every load and LDS write is unconditional); KW <= 16
+__host__ __device__ constexpr int direct_wv(int kw) { return (32 * kw * 4 + 255) / 256; }
+
+struct DArgs {
+  const uint16_t* x;     // [B][Cin][H][W]
+  const uint16_t* wp;    // prepared [chunks][KH][wv * 256 vectors of 8]: rows (co, kx) of 32 ci
+  const uint16_t* bias;  // [Cout] or null
+  uint16_t* out;         // [B][Cout][Ho][Wo]
+  int B, Cin, Cout, H, W, KH, KW, ph, pw, Ho, Wo, Wp, chunks, nb, xpos, rtiles, wv;
+  int x_bytes;           // under 2^31
+};
+
+// Prepared weights, one block of wv * 256 vectors per (chunk, ky): row r = co * KW + kx holds
+// the 32 channels ci of w[co][ch*32+ci][ky][kx] (forward) or, flipped for the input
+// gradient as a forward conv, of w[ch*32+ci][co][KH-1-ky][KW-1-kx]; zero padding.
+__global__ __launch_bounds__(256) void direct_prep_kernel(const uint16_t* __restrict__ w,
+                                                          uint16_t* __restrict__ wp, int Cin, int Cout,
+                                                          int KH, int KW, int flip, int blk, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const int e = int(i % blk);
+    const int64_t cb = i / blk;  // ch * KH + ky
+    const int ky = int(cb % KH), ch = int(cb / KH);
+    const int ci = e % kDCK, row = e / kDCK;
+    const int co = row / KW, kx = row - co * KW;
+    const int c = ch * kDCK + ci;
+    uint16_t v = 0;
+    if (co < 32 && co < Cout && c < Cin) {
+      // flipped: the forward conv's weight tensor is [Cin][Cout][KH][KW] in this
+      // direction's terms (its output channels are this conv's inputs)
+      v = flip ? w[((int64_t(c) * Cout + co) * KH + (KH - 1 - ky)) * KW + (KW - 1 - kx)]
+               : w[((int64_t(co) * Cin + c) * KH + ky) * KW + kx];
+    }
+    wp[i] = v;
+  }
+}
+
+// KWT: the kernel width when known at compile time (the tap loop unrolls), 0: any width.
+// NBW: grid blocks per wave (blocks wave, wave + 4, ...; a wave past the last block
+// recomputes the last one and drops it, so no MFMA or LDS read sits behind a branch).
+template <int KWT, int NBW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_direct_kernel(DArgs a) {
+  constexpr int WV = KWT > 0 ? direct_wv(KWT) : direct_wv(16);
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs = smem;                               // [xpos][kDPitch]
+  uint16_t* ws = smem + a.xpos * kDPitch;            // [WV * 256 / 4][kDPitch]
+  const int b = blockIdx.x / a.rtiles, oy0 = (blockIdx.x % a.rtiles) * kDTR;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  const int trh = kDTR + a.KH - 1;                   // input rows staged
+  const int KW = KWT > 0 ? KWT : a.KW;
+
+  f32x16_t acc[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) acc[j] = zero_acc();
+  int bpos[NBW];  // first grid position of each of this wave's blocks (clamped)
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) bpos[j] = min(wave + 4 * j, a.nb - 1) * 32 + lr;
+
+  u32x4_t wr[WV];
+  auto load_w = [&](int ch, int ky) {
+    const uint16_t* src = a.wp + (int64_t(ch) * a.KH + ky) * (a.wv * 256 * 8) + tid * 8;
+#pragma unroll
+    for (int j = 0; j < WV; ++j)
+      if (KWT > 0 || j < a.wv) wr[j] = *reinterpret_cast<const u32x4_t*>(src + j * 256 * 8);
+  };
+  auto store_w = [&]() {
+#pragma unroll
+    for (int j = 0; j < WV; ++j) {
+      // vector v = tid + 256 j: row v / 4, channels (v % 4) * 8
+      const int v = tid + j * 256;
+      if (KWT > 0 || j < a.wv) *reinterpret_cast<u32x4_t*>(ws + (v >> 2) * kDPitch + (v & 3) * 8) = wr[j];
+    }
+  };
+  // masked elements (borders, padding channels, unused items) read through an
+  // out-of-range offset: zero, no memory access
+  const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), 0, a.x_bytes, 0x00020000);
+  const int plane = a.H * a.W;
+  auto stage_x = [&](int ch) {
+    const int items = a.xpos * (kDCK / 8);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t v[kDXItems / 2][4];
+#pragma unroll
+      for (int j = 0; j < kDXItems / 2; ++j) {
+        const int i = tid + (half * (kDXItems / 2) + j) * 256;
+        const int pos = i % a.xpos, cg = i / a.xpos;
+        const int t = pos / a.Wp, c = pos - t * a.Wp;
+        const int iy = oy0 - a.ph + t, ix = c - a.pw;
+        const bool pok = i < items && t < trh && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+        const int c0 = ch * kDCK + cg * 8;
+        const int base = ((b * a.Cin + c0) * plane + iy * a.W + ix) * 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool ok0 = pok && c0 + 2 * e < a.Cin, ok1 = pok && c0 + 2 * e + 1 < a.Cin;
+          const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(xrs, ok0 ? base + (2 * e) * plane * 2 : kOob, 0, 0);
+          const uint32_t hi =
+              __builtin_amdgcn_raw_buffer_load_b16(xrs, ok1 ? base + (2 * e + 1) * plane * 2 : kOob, 0, 0);
+          v[j][e] = lo | (hi << 16);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kDXItems / 2; ++j) {
+        const int i = tid + (half * (kDXItems / 2) + j) * 256;
+        if (i < items) {
+          const int pos = i % a.xpos, cg = i / a.xpos;
+          *reinterpret_cast<u32x4_t*>(xs + pos * kDPitch + cg * 8) = u32x4_t{v[j][0], v[j][1], v[j][2], v[j][3]};
+        }
+      }
+    }
+  };
+
+  for (int ch = 0; ch < a.chunks; ++ch) {
+    __syncthreads();  // the previous chunk's reads of xs / ws are done
+    stage_x(ch);
+    load_w(ch, 0);
+    for (int ky = 0; ky < a.KH; ++ky) {
+      if (ky > 0) __syncthreads();  // the previous kernel row's reads of ws are done
+      store_w();
+      __syncthreads();
+      if (ky + 1 < a.KH) load_w(ch, ky + 1);
+      const uint16_t* wa = ws + lr * KW * kDPitch + lk;
+      const uint16_t* xb = xs + (ky * a.Wp) * kDPitch + lk;
+#pragma unroll
+      for (int kx = 0; kx < KW; ++kx) {
+#pragma unroll
+        for (int ks = 0; ks < kDCK / 16; ++ks) {
+          const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(wa + kx * kDPitch + ks * 16));
+#pragma unroll
+          for (int j = 0; j < NBW; ++j) {
+            const bf16x8_t bf =
+                as_bf16x8(*reinterpret_cast<const u32x4_t*>(xb + (bpos[j] + kx) * kDPitch + ks * 16));
+            acc[j] = mfma_32x32x16(af, bf, acc[j]);
+          }
+        }
+      }
+    }
+  }
+
+  // lanes 0..31 hold 32 consecutive grid positions of one output channel per value
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    const int nbk = wave + 4 * j;
+    if (nbk >= a.nb) continue;
+    const int q = nbk * 32 + lr;
+    const int orow = q / a.Wp, ox = q - orow * a.Wp, oy = oy0 + orow;
+    if (orow >= kDTR || oy >= a.Ho || ox >= a.Wo) continue;
+    uint16_t* o = a.out + (int64_t(b) * a.Cout * a.Ho + oy) * a.Wo + ox;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int co = mfma_row(r, lane);
+      if (co < a.Cout) {
+        float v = acc[j][r];
+        if (a.bias) v += bf16_to_f32(a.bias[co]);
+        o[int64_t(co) * a.Ho * a.Wo] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+size_t direct_lds(const DArgs& d);
+
+// The direct form's geometry for a stride-1 conv of x [B][Cin][H][W] into Cout channels,
+// or false when it does not apply (more than 32 outputs, fewer than 16 inputs, a grid
+// wider than 128 columns, more staging than the fixed per-thread budget, or LDS beyond
+// one CU).
+bool direct_args(DArgs& d, int B, int Cin, int Cout, int H, int W, int KH, int KW, int ph, int pw) {
+  // fewer than 16 input channels: the 32-channel chunk would be mostly padding (the
+  // gather GEMM's k runs over the real channels only; measured faster for 3 channels)
+  if (Cout > 32 || Cin < 16 || KW > 16 || KH < 1 || KW < 1 || ph < 0 || pw < 0) return false;
+  d.B = B; d.Cin = Cin; d.Cout = Cout; d.H = H; d.W = W; d.KH = KH; d.KW = KW; d.ph = ph; d.pw = pw;
+  d.Ho = H + 2 * ph - KH + 1;
+  d.Wo = W + 2 * pw - KW + 1;
+  if (d.Ho < 1 || d.Wo < 1) return false;
+  d.Wp = d.Wo + KW - 1;
+  d.nb = int(ceil_div(int64_t(kDTR) * d.Wp, 32));
+  if (d.nb > kDMaxNB) return false;
+  d.xpos = d.nb * 32 + (KH - 1) * d.Wp + KW - 1;
+  if (d.xpos * (kDCK / 8) > kDXItems * 256) return false;
+  d.chunks = int(ceil_div(Cin, kDCK));
+  d.rtiles = int(ceil_div(d.Ho, kDTR));
+  d.wv = direct_wv(KW == 9 ? 9 : 16);  // the generic kernel pads every width to 16
+  if (direct_lds(d) > 160 * 1024) return false;
+  if (int64_t(B) * d.rtiles > 0x7fffffff) return false;
+  return true;
+}
+
+size_t direct_lds(const DArgs& d) { return size_t(d.xpos + d.wv * 256 / 4) * kDPitch * 2; }
+
+std::atomic<int> g_conv2d_variant{0};  // 0 automatic, 1 gather GEMM only
+
+// Runs the direct form (weights prepared into the cache allocator) or returns 1 when it
+// does not apply.
+int run_direct(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int B, int Cin,
+               int Cout, int H, int W, int KH, int KW, int ph, int pw, int flip, hipStream_t st) {
+  DArgs d{};
+  if (g_conv2d_variant.load() == 1 || !direct_args(d, B, Cin, Cout, H, W, KH, KW, ph, pw)) return 1;
+  d.x_bytes = int(int64_t(B) * Cin * H * W * 2);  // the callers' operands are under 2^30 elements
+  static const bool lds_ok = [] {
+    bool ok = true;
+    for (const void* f : {reinterpret_cast<const void*>(&conv_direct_kernel<0, 1>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<0, 2>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<0, 3>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<0, 4>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<9, 1>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<9, 2>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<9, 3>),
+                          reinterpret_cast<const void*>(&conv_direct_kernel<9, 4>)})
+      ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    return ok;
+  }();
+  if (!lds_ok) return 1;
+  const int blk = d.wv * 256 * 8;
+  const int64_t n = int64_t(d.chunks) * KH * blk;
+  uint16_t* wp = static_cast<uint16_t*>(xdna_hip_cache_alloc(size_t(n) * 2));
+  if (!wp) return -1;
+  direct_prep_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 4096)), 256, 0, st>>>(w, wp, Cin, Cout, KH, KW,
+                                                                                          flip, blk, n);
+  d.x = x;
+  d.wp = wp;
+  d.bias = bias;
+  d.out = out;
+  const unsigned grid = unsigned(int64_t(B) * d.rtiles);
+  const size_t lds = direct_lds(d);
+  const int nbw = int(ceil_div(d.nb, 4));
+#define XDNA_DIRECT(kw_, nbw_) conv_direct_kernel<kw_, nbw_><<<grid, 256, lds, st>>>(d)
+  if (KW == 9) {
+    if (nbw == 1) XDNA_DIRECT(9, 1);
+    else if (nbw == 2) XDNA_DIRECT(9, 2);
+    else if (nbw == 3) XDNA_DIRECT(9, 3);
+    else XDNA_DIRECT(9, 4);
+  } else {
+    if (nbw == 1) XDNA_DIRECT(0, 1);
+    else if (nbw == 2) XDNA_DIRECT(0, 2);
+    else if (nbw == 3) XDNA_DIRECT(0, 3);
+    else XDNA_DIRECT(0, 4);
+  }
+#undef XDNA_DIRECT
+  // stream-ordered reuse: the next user of the block runs after the conv
+  xdna_hip_cache_free(wp);
+  return check_launch("conv direct");
 }
 
 }  // namespace
@@ -370,6 +655,10 @@ int xdna_conv2d_fwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* b
   a.nsplit = 1;
   a.kt_per = int(ceil_div(a.K, kGTK));
   if (!admit_launch("xdna_conv2d_fwd_bf16")) return -1;
+  if (sh == 1 && sw == 1) {
+    const int rc = run_direct(x, w, bias, y, B, Cin, Cout, H, W, KH, KW, ph, pw, 0, as_stream(stream));
+    if (rc <= 0) return rc;
+  }
   return launch_gather<kGFwd>(a, as_stream(stream));
 }
 
@@ -382,6 +671,13 @@ int xdna_conv2d_dgrad_bf16(const uint16_t* dy, const uint16_t* w, uint16_t* dx, 
   a.nsplit = 1;
   a.kt_per = int(ceil_div(a.K, kGTK));
   if (!admit_launch("xdna_conv2d_dgrad_bf16")) return -1;
+  if (sh == 1 && sw == 1 && ph <= KH - 1 && pw <= KW - 1) {
+    // at stride 1 the input gradient is the forward conv of dy with the flipped,
+    // transposed weights and padding K - 1 - p, which gives back H x W
+    const int rc = run_direct(dy, w, nullptr, dx, B, Cout, Cin, a.Ho, a.Wo, KH, KW, KH - 1 - ph, KW - 1 - pw, 1,
+                              as_stream(stream));
+    if (rc <= 0) return rc;
+  }
   return launch_gather<kGDgrad>(a, as_stream(stream));
 }
 
@@ -414,6 +710,15 @@ int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, 
   xdna_hip_cache_free(a.part);
   if (check_launch("xdna_conv2d_wgrad_bf16")) return -1;
   if (gb) return xdna_conv3x3_bias_grad_bf16(dy, gb, B, Cout, a.Ho, a.Wo, stream);
+  return 0;
+}
+
+int xdna_conv2d_set_variant(int variant) {
+  if (variant < 0 || variant > 1) {
+    set_error("xdna_conv2d_set_variant: variant must be 0 or 1");
+    return -1;
+  }
+  g_conv2d_variant.store(variant);
   return 0;
 }
 

@@ -165,10 +165,29 @@ __device__ inline void stage(uint16_t* lds, const uint16_t* src, int64_t s_r, in
         lds[(rv + e) * kLdsPitch + kk] = uint16_t((e & 1) ? (u[e >> 1] >> 16) : (u[e >> 1] & 0xFFFF));
     }
   } else {
-    for (int i = tid; i < 128 * kTK; i += 256) {
-      const int row = i / kTK, kk = i - row * kTK;
+    // Element by element (strides without 16-byte vectors): all 16 loads of a thread are
+    // issued before the first LDS write (a load-store loop waited one memory latency per
+    // element), out-of-range elements read element 0 and are masked (no branches), and
+    // consecutive lanes take the operand's unit-stride direction where it has one.
+    constexpr int kPer = 128 * kTK / 256;
+    const bool rows_fast = s_r == 1 && s_k != 1;
+    uint32_t v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * 256;
+      const int row = rows_fast ? (i & 127) : i / kTK;
+      const int kk = rows_fast ? (i >> 7) : i % kTK;
       const int r = r0 + row, k = k0 + kk;
-      lds[row * kLdsPitch + kk] = (r < rows && k < K) ? src[int64_t(r) * s_r + int64_t(k) * s_k] : 0;
+      const bool ok = r < rows && k < K;
+      const uint32_t e = src[ok ? int64_t(r) * s_r + int64_t(k) * s_k : 0];
+      v[j] = ok ? e : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * 256;
+      const int row = rows_fast ? (i & 127) : i / kTK;
+      const int kk = rows_fast ? (i >> 7) : i % kTK;
+      lds[row * kLdsPitch + kk] = uint16_t(v[j]);
     }
   }
 }

@@ -1,6 +1,9 @@
-// Nearest-neighbour 2x upsampling of NCHW bf16 planes and its gradient: the style
-// generator's "nearest up x2" layers.  For an exact factor of 2, PyTorch's nearest source
-// index floor(dst * 0.5) is dst / 2 (its scale 1/2 is exact in fp32), so
+// Resampling of NCHW bf16 planes: nearest-neighbour 2x upsampling and its gradient (the
+// style generator's "nearest up x2" layers), and the stride-2 sampling that runs 3x3 /
+// stride-2 convs through the stride-1 conv kernels (below).
+//
+// Upsampling: for an exact factor of 2, PyTorch's nearest source index floor(dst * 0.5) is
+// dst / 2 (its scale 1/2 is exact in fp32), so
 //   y[p][oy][ox] = x[p][oy / 2][ox / 2],
 // and the gradient sums each 2x2 block of dy in fp32 in row-major order, (0,0), (0,1),
 // (1,0), (1,1), then rounds once to bf16, as PyTorch's backward accumulates in float.
@@ -48,6 +51,37 @@ __global__ __launch_bounds__(256) void upsample2x_bwd_kernel(const uint16_t* __r
   (void)H;
 }
 
+// Stride-2 sampling for 3x3 / stride-2 / pad-1 convs run through the stride-1 kernels:
+// y[p][oy][ox] = full[p][2 oy][2 ox] (forward: every other output of the stride-1 conv),
+// and the spread of a gradient onto the stride-1 grid, full[p][y][x] = dy[p][y/2][x/2] at
+// even (y, x) and 0 elsewhere (the input / weight gradients then run at stride 1; the
+// zeros add nothing to their sums).  Full planes H x W, sampled ceil(H/2) x ceil(W/2).
+__global__ __launch_bounds__(256) void subsample2_kernel(const uint16_t* __restrict__ full,
+                                                         uint16_t* __restrict__ y, int64_t n, int H, int W) {
+  const int Ho = (H + 1) / 2, Wo = (W + 1) / 2;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const int64_t row = i / Wo;  // plane * Ho + oy
+    const int ox = int(i - row * Wo);
+    const int64_t p = row / Ho;
+    const int oy = int(row - p * Ho);
+    y[i] = full[(p * H + 2 * oy) * int64_t(W) + 2 * ox];
+  }
+}
+
+__global__ __launch_bounds__(256) void dilate2_kernel(const uint16_t* __restrict__ dy,
+                                                      uint16_t* __restrict__ full, int64_t n, int H, int W) {
+  const int Ho = (H + 1) / 2, Wo = (W + 1) / 2;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const int64_t row = i / W;  // plane * H + y
+    const int x = int(i - row * W);
+    const int64_t p = row / H;
+    const int y = int(row - p * H);
+    const bool even = ((x | y) & 1) == 0;
+    const uint16_t v = dy[even ? (p * Ho + y / 2) * int64_t(Wo) + x / 2 : 0];
+    full[i] = even ? v : uint16_t(0);
+  }
+}
+
 bool resample_args(const char* what, const void* src, const void* dst, int64_t planes, int H, int W) {
   if (planes < 0 || H < 0 || W < 0 || ((planes * H * W) > 0 && (!src || !dst))) {
     set_error(std::string(what) + ": invalid arguments");
@@ -86,6 +120,32 @@ int xdna_upsample_nearest2x_bwd_bf16(const uint16_t* dy, uint16_t* dx, int64_t p
   upsample2x_bwd_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(
       dy, dx, n, H, W);
   return check_launch("xdna_upsample_nearest2x_bwd_bf16");
+}
+
+int xdna_subsample2_bf16(const uint16_t* full, uint16_t* y, int64_t planes, int H, int W, void* stream) {
+  if (planes < 0 || H < 0 || W < 0 || (planes * H * W > 0 && (!full || !y))) {
+    set_error("xdna_subsample2_bf16: invalid arguments");
+    return -1;
+  }
+  const int64_t n = planes * ((H + 1) / 2) * ((W + 1) / 2);
+  if (n == 0) return 0;
+  if (!admit_launch("xdna_subsample2_bf16")) return -1;
+  subsample2_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(full, y, n,
+                                                                                                          H, W);
+  return check_launch("xdna_subsample2_bf16");
+}
+
+int xdna_dilate2_bf16(const uint16_t* dy, uint16_t* full, int64_t planes, int H, int W, void* stream) {
+  if (planes < 0 || H < 0 || W < 0 || (planes * H * W > 0 && (!full || !dy))) {
+    set_error("xdna_dilate2_bf16: invalid arguments");
+    return -1;
+  }
+  const int64_t n = planes * H * W;
+  if (n == 0) return 0;
+  if (!admit_launch("xdna_dilate2_bf16")) return -1;
+  dilate2_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(dy, full, n, H,
+                                                                                                       W);
+  return check_launch("xdna_dilate2_bf16");
 }
 
 }  // extern "C"

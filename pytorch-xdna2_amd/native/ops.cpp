@@ -60,6 +60,26 @@ bool conv_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef
   return true;
 }
 
+// 3x3 / stride-2 / pad-1 convs (the style encoder, ResNet's downsampling blocks) run
+// through the stride-1 kernels: the forward is the stride-1 conv at every other row and
+// column, and both gradients are the stride-1 ones of the gradient spread onto the
+// stride-1 grid with zeros (which add nothing to any sum), so the numerics are those of
+// the hot path.  4x the MACs of the strided conv, on kernels several times faster than
+// MIOpen's on these shapes, and within the conv bar where MIOpen is not.  The reference
+// runs them on its CPU through the fallback (torch_xdna_device.cpp:4524-4606, 4608-4885).
+bool conv_s2_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
+                      c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation, bool transposed,
+                      c10::SymIntArrayRef output_padding, const c10::SymInt& groups) {
+  if (g_mode.load() < 1) return false;
+  if (x.scalar_type() != at::kBFloat16 || w.scalar_type() != at::kBFloat16) return false;
+  if (x.dim() != 4 || w.dim() != 4 || w.size(2) != 3 || w.size(3) != 3) return false;
+  if (!is_one(stride, 2) || !is_one(padding, 1) || !is_one(dilation, 1) || transposed) return false;
+  if (!is_one(output_padding, 0) || groups != 1) return false;
+  if (x.size(0) < 1 || x.size(2) < 1 || x.size(3) < 1 || w.size(0) < 1 || w.size(1) < 1) return false;
+  if (x.size(1) != w.size(1)) return false;
+  return x.device().type() == kXdna && w.device().type() == kXdna;
+}
+
 // Prepared weights of frozen tensors (requires_grad false: a loss network's weights),
 // keyed by storage, offset, shape, version and direction, the role of the reference's
 // weight slots (torch_xdna_device.cpp:2208-2271).  A weak reference to the storage tells
@@ -230,9 +250,20 @@ struct GeomArgs {
 
 // Where the general kernels beat MIOpen (measured on the style network's layers, B40
 // 36x36): stride-1 layers with 32 or more output channels, forward and weight gradient
-// (9x9 3->32: 23 vs 39 us forward).  Strided layers and their input gradients, and layers
-// with a few output channels (9x9 32->3), stay on MIOpen unless mode 2 asks otherwise.
+// (9x9 3->32: 22 vs 38 us forward), and the forward of stride-1 layers with a few output
+// channels and 16 or more inputs, which takes the direct form (9x9 32->3: 28 vs 147 us).
+// Strided layers, other input gradients, and the weight gradient of few-output layers
+// stay on MIOpen unless mode 2 asks otherwise.
 bool gconv_auto(int cout, int sh, int sw) { return cout >= 32 && sh == 1 && sw == 1; }
+bool gconv_auto_fwd(int cin, int cout, int sh, int sw) {
+  return gconv_auto(cout, sh, sw) || (cout <= 32 && cin >= 16 && sh == 1 && sw == 1);
+}
+// The input gradient where the direct form takes it (stride 1, at most 32 input channels
+// of the layer and 16 or more outputs: 9x9 3->32 in 29 us); MIOpen's input gradient of
+// that layer also misses the 2-ulp bar on some elements.
+bool gconv_auto_dgrad(const GeomArgs& g) {
+  return g.sh == 1 && g.sw == 1 && g.Cin <= 32 && g.Cout >= 16 && g.ph <= g.KH - 1 && g.pw <= g.KW - 1;
+}
 
 GeomArgs gconv_geom(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
                     c10::SymIntArrayRef padding) {
@@ -276,10 +307,23 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
     ScopedCount sc("hip_conv3x3.fwd.run");
     return hip_conv(input, weight, has_bias ? &*bias : nullptr, false);
   }
+  if (conv_s2_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
+      (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
+                     bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
+    ScopedCount sc("hip_conv3x3_s2.fwd.run");
+    const at::Tensor full = hip_conv(input, weight, has_bias ? &*bias : nullptr, false);
+    const int64_t B = full.size(0), C = full.size(1), H = full.size(2), W = full.size(3);
+    at::Tensor y = empty_xdna({B, C, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16);
+    check_abi(xdna_subsample2_bf16(static_cast<const uint16_t*>(full.const_data_ptr()),
+                                   static_cast<uint16_t*>(y.data_ptr()), B * C, int(H), int(W), current_stream()),
+              "conv stride-2 subsample");
+    return y;
+  }
   const int gmode = g_gconv_mode.load();
   if (gmode > 0 &&
       gconv_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
-      (gmode == 2 || gconv_auto(int(weight.size(0)), int(stride[0].expect_int()), int(stride[1].expect_int()))) &&
+      (gmode == 2 || gconv_auto_fwd(int(weight.size(1)), int(weight.size(0)), int(stride[0].expect_int()),
+                                    int(stride[1].expect_int()))) &&
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv2d.fwd.run");
@@ -325,29 +369,41 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     bool transposed, c10::SymIntArrayRef output_padding, c10::SymInt groups,
     std::array<bool, 3> output_mask) {
   at::Tensor gi, gw, gb;
-  const bool hip = conv_eligible(input, weight, stride, padding, dilation, transposed,
-                                 output_padding, groups) &&
-                   grad_output.scalar_type() == at::kBFloat16 && grad_output.dim() == 4 &&
-                   grad_output.device().type() == kXdna && input.size(1) == weight.size(1) &&
-                   grad_output.size(1) == weight.size(0) && grad_output.size(0) == input.size(0) &&
-                   grad_output.size(2) == input.size(2) && grad_output.size(3) == input.size(3);
+  const bool go_ok = grad_output.scalar_type() == at::kBFloat16 && grad_output.dim() == 4 &&
+                     grad_output.device().type() == kXdna && input.size(1) == weight.size(1) &&
+                     grad_output.size(1) == weight.size(0) && grad_output.size(0) == input.size(0);
+  bool hip = conv_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
+             go_ok && grad_output.size(2) == input.size(2) && grad_output.size(3) == input.size(3);
+  // stride 2: the stride-1 gradients of the gradient spread onto the stride-1 grid
+  at::Tensor go = grad_output;
+  if (!hip && go_ok && conv_s2_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
+      grad_output.size(2) == (input.size(2) + 1) / 2 && grad_output.size(3) == (input.size(3) + 1) / 2) {
+    ScopedCount sc("hip_conv3x3_s2.bwd.run");
+    const at::Tensor d = grad_output.contiguous();
+    const int64_t B = input.size(0), C = weight.size(0), H = input.size(2), W = input.size(3);
+    go = empty_xdna({B, C, H, W}, at::kBFloat16);
+    check_abi(xdna_dilate2_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                static_cast<uint16_t*>(go.data_ptr()), B * C, int(H), int(W), current_stream()),
+              "conv stride-2 dilate");
+    hip = true;
+  }
   auto mask = output_mask;
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
-    gi = hip_conv(grad_output, weight, nullptr, true);
+    gi = hip_conv(go, weight, nullptr, true);
     mask[0] = false;
   }
   if (hip && mask[1] && g_mode.load() >= 2 && input.size(3) <= 142) {
     ScopedCount sc("hip_conv3x3.dw.run");
-    hip_wgrad(input, grad_output, gw, mask[2] ? &gb : nullptr);
+    hip_wgrad(input, go, gw, mask[2] ? &gb : nullptr);
     g_dw_jobs.fetch_add(1);
     mask[1] = false;
     mask[2] = false;
   }
   if (hip && mask[2]) {
     ScopedCount sc("hip_conv3x3.bias_grad.run");
-    at::Tensor d = grad_output.contiguous();
-    gb = empty_xdna({grad_output.size(1)}, at::kBFloat16);
+    at::Tensor d = go.contiguous();
+    gb = empty_xdna({go.size(1)}, at::kBFloat16);
     check_abi(xdna_conv3x3_bias_grad_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
                                           static_cast<uint16_t*>(gb.data_ptr()), int(d.size(0)),
                                           int(d.size(1)), int(d.size(2)), int(d.size(3)),
@@ -369,7 +425,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     at::Tensor d = grad_output.contiguous();
     const double flops = 2.0 * g.B * g.Ho * g.Wo * double(g.Cout) * g.Cin * g.KH * g.KW;
     const bool auto_ok = gconv_auto(g.Cout, g.sh, g.sw);
-    if (mask[0] && gmode == 2) {
+    if (mask[0] && (gmode == 2 || gconv_auto_dgrad(g))) {
       ScopedCount sc("hip_conv2d.dx.run");
       at::Tensor w = weight.contiguous();
       gi = empty_xdna({g.B, g.Cin, g.H, g.W}, at::kBFloat16);

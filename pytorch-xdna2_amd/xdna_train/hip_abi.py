@@ -67,6 +67,9 @@ SIGNATURES = {
     "xdna_instance_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, ctypes.c_double, P]),
     "xdna_instance_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
     "xdna_upsample_nearest2x_bf16": (I, [P, P, L, I, I, P]),
+    "xdna_conv2d_set_variant": (I, [I]),
+    "xdna_subsample2_bf16": (I, [P, P, L, I, I, P]),
+    "xdna_dilate2_bf16": (I, [P, P, L, I, I, P]),
     "xdna_upsample_nearest2x_bwd_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_dgrad_bf16": (I, [P, P, P] + [I] * 11 + [P]),
     "xdna_conv2d_wgrad_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),

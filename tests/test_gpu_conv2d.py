@@ -6,7 +6,10 @@ Shapes: the style network's 9x9 input / output layers and stride-2 encoder convs
 ResNet's 7x7 stride-2 stem and 1x1 stride-2 downsampling, non-square kernels and
 strides, odd sizes, channel counts that leave partial 32 / 64 / 128-row tiles, and a
 pixel count beyond one 128-column tile row.  The weight gradient is checked for
-run-to-run bit equality (fixed-order split reduction).
+run-to-run bit equality (fixed-order split reduction).  Forward and input gradient run
+in both kernel forms: automatic (the direct form at stride 1 with <= 32 output and >= 16
+input channels of the direction, up to the widest padded row it stages) and the gather
+GEMM alone.
 """
 import numpy as np
 import pytest
@@ -27,7 +30,18 @@ CASES = [
     (3, 40, 70, 9, 11, 1, 1, 1, 1, 0, 0),     # 1x1, partial tiles
     (2, 5, 130, 7, 9, 3, 2, 1, 3, 1, 0),      # non-square kernel and stride
     (1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 0),
+    (2, 70, 20, 13, 17, 5, 3, 1, 1, 2, 1),    # direct form: 3 channel chunks (partial), 5x3
+    (3, 16, 32, 40, 50, 3, 3, 1, 1, 0, 0),    # direct form: no padding, 7 grid blocks
+    (2, 16, 5, 30, 90, 7, 7, 1, 1, 3, 3),     # direct form: wide row (12 grid blocks, 95 KB LDS)
+    (2, 6, 4, 20, 200, 3, 3, 1, 1, 1, 1),     # too wide for the direct form: gather GEMM
 ]
+
+
+@pytest.fixture(params=[0, 1], ids=["auto", "gather"])
+def cvar(request, hip):
+    assert hip.xdna_conv2d_set_variant(request.param) == 0
+    yield request.param
+    hip.xdna_conv2d_set_variant(0)
 
 
 def _data(case, seed):
@@ -43,9 +57,9 @@ def _data(case, seed):
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
-def test_forward(hip, case):
+def test_forward(hip, case, cvar):
     B, Cin, Cout, H, W, KH, KW, sh, sw, ph, pw = case
-    print(f"conv2d fwd {case}", flush=True)
+    print(f"conv2d fwd {case} variant {cvar}", flush=True)
     x, w, b, _, Ho, Wo = _data(case, sum(case))
     y = dev_zeros((B, Cout, Ho, Wo))
     assert hip.xdna_conv2d_fwd_bf16(ptr(dev(x)), ptr(dev(w)), ptr(dev(b)), ptr(y), B, Cin, Cout, H, W, KH, KW,
@@ -58,9 +72,9 @@ def test_forward(hip, case):
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
-def test_dgrad(hip, case):
+def test_dgrad(hip, case, cvar):
     B, Cin, Cout, H, W, KH, KW, sh, sw, ph, pw = case
-    print(f"conv2d dgrad {case}", flush=True)
+    print(f"conv2d dgrad {case} variant {cvar}", flush=True)
     _, w, _, dy, Ho, Wo = _data(case, sum(case) + 1)
     dx = dev_zeros((B, Cin, H, W))
     assert hip.xdna_conv2d_dgrad_bf16(ptr(dev(dy)), ptr(dev(w)), ptr(dx), B, Cin, Cout, H, W, KH, KW, sh, sw,

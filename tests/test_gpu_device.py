@@ -89,9 +89,9 @@ def test_conv_forward_backward_matches_cpu_and_oracle(xdna):
 
 
 def test_other_convs_run_on_general_kernels(xdna):
-    """5x5, strided 3x3, 1x1, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on
-    the general HIP kernels (mode 2: always) and match the CPU bf16 path and the float64
-    oracle."""
+    """5x5, 1x1, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on the general
+    HIP kernels (mode 2: always), the 3x3 / stride-2 / pad-1 one on the stride-1 3x3 path,
+    and all match the CPU bf16 path and the float64 oracle."""
     xdna.reset_mapped_cpu_stats()
     xdna.set_general_conv_mode(2)
     specs = [(8, 16, 5, 1, 2), (8, 16, 3, 2, 1), (8, 16, 1, 1, 0), (3, 32, 9, 1, 4), (3, 16, 7, 2, 3),
@@ -121,10 +121,52 @@ def test_other_convs_run_on_general_kernels(xdna):
             assert (g - r).norm() / r.norm() < 1e-2, what
     xdna.set_general_conv_mode(1)
     st = xdna.mapped_cpu_stats()
-    n = len(specs)
+    n = len(specs) - 1  # all but the 3x3 / stride-2 / pad-1 conv
     for key in ("hip_conv2d.fwd.run", "hip_conv2d.dx.run", "hip_conv2d.dw.run"):
         assert st.get(key, {}).get("calls", 0) == n, (key, st)
-    assert "aten::convolution.rocm" not in st and "hip_conv3x3.fwd.run" not in st
+    for key in ("hip_conv3x3_s2.fwd.run", "hip_conv3x3_s2.bwd.run"):
+        assert st.get(key, {}).get("calls", 0) == 1, (key, st)
+    assert "aten::convolution.rocm" not in st and "aten::convolution_backward.rocm" not in st
+
+
+def test_default_routing_of_general_convs(xdna):
+    """Mode 1 (default) routes each conv direction where it was measured faster: the 9x9
+    32->3 forward and the 9x9 3->32 input gradient to the direct form, the 9x9 3->32
+    forward and weight gradient to the gather GEMM, 3x3 / stride-2 layers to the stride-1
+    3x3 path, the 9x9 32->3 gradients to MIOpen; every result matches the float64
+    oracle."""
+    assert xdna.general_conv_mode() == 1
+    specs = [  # cin, cout, k, s, p, expected counters
+        (32, 3, 9, 1, 4, {"hip_conv2d.fwd.run": 1, "aten::convolution_backward.rocm": 1}),
+        (3, 32, 9, 1, 4, {"hip_conv2d.fwd.run": 1, "hip_conv2d.dw.run": 1, "hip_conv2d.dx.run": 1,
+                          "aten::convolution_backward.rocm": 0}),
+        (32, 64, 3, 2, 1, {"hip_conv3x3_s2.fwd.run": 1, "hip_conv3x3_s2.bwd.run": 1,
+                           "aten::convolution.rocm": 0, "aten::convolution_backward.rocm": 0}),
+    ]
+    for cin, cout, k, s, pd, expect in specs:
+        torch.manual_seed(cin + cout)
+        conv = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16()
+        x = torch.randn(2, cin, 12, 10).bfloat16()
+        cd = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16().to(X)
+        cd.load_state_dict(conv.state_dict())
+        xdna.reset_mapped_cpu_stats()
+        xd = x.to(X).requires_grad_()
+        yd = cd(xd)
+        dy = torch.randn(yd.shape).bfloat16()
+        yd.backward(dy.to(X))
+        torch.xdna.synchronize()
+        st = xdna.mapped_cpu_stats()
+        for key, n in expect.items():
+            assert st.get(key, {}).get("calls", 0) == n, (cin, cout, key, st)
+        xb, wb, bb, dyb = (bits(t) for t in (x, conv.weight, conv.bias, dy))
+        what = f"k{k} s{s} {cin}->{cout}"
+        check_bf16(bits(yd), oracle.conv2d_fwd(xb, wb, bb, (s, s), (pd, pd)), what=f"fwd {what}")
+        check_bf16(bits(xd.grad), oracle.conv2d_dgrad(dyb, wb, (12, 10), (s, s), (pd, pd)), what=f"dgrad {what}")
+        gw, gb = oracle.conv2d_wgrad(xb, dyb, (k, k), (s, s), (pd, pd))
+        check_bf16(bits(cd.weight.grad), gw, what=f"wgrad {what}")
+        # bias gradients from MIOpen sum in another order: relative bar
+        g, r = oracle.bf16_value(bits(cd.bias.grad)), gb
+        assert np.abs(g - r).max() <= 2 * oracle.bf16_ulp(np.abs(r).max()) + 1e-6, what
 
 
 def test_ineligible_convs_fall_back(xdna):
