@@ -247,6 +247,13 @@ size_t xdna_conv3x3_prepared_weight_bytes(int cin, int cout);
 int xdna_conv3x3_prepare_weights_bf16(const uint16_t* w, uint16_t* wt, int Cout, int Cin,
                                       int dgrad, void* stream);
 
+/* Both prepared forms of one weight in one launch: wt as xdna_conv3x3_prepare_weights_bf16
+ * with dgrad = 0, wt_dgrad as with dgrad = 1 (each sized by
+ * xdna_conv3x3_prepared_weight_bytes of its direction).  For trainable weights, whose
+ * forward prepares the input gradient's form too.  No reference counterpart. */
+int xdna_conv3x3_prepare_weights_both_bf16(const uint16_t* w, uint16_t* wt, uint16_t* wt_dgrad, int Cout,
+                                           int Cin, void* stream);
+
 /* y[B][cout][H][W] = conv of the packed input xp (cin channels, strip layout of W)
  * with prepared weights wt (+ bias[cout], may be NULL).  One kernel. */
 int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,

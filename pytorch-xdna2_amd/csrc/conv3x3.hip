@@ -1404,6 +1404,37 @@ bool shape_ok(const char* what, int B, int Cin, int Cout, int H, int W) {
   return true;
 }
 
+// Both forms of a trainable weight in one launch: the forward one into wt and the
+// flip+swap one of the input gradient into wtd (workgroups past the first form's take the
+// second), so the backward need not launch its own preparation.
+__global__ __launch_bounds__(256) void prep_weights_both_kernel(const uint16_t* __restrict__ w,
+                                                                uint16_t* __restrict__ wt,
+                                                                uint16_t* __restrict__ wtd, int Cout, int Cin,
+                                                                int co_pad_f, int chunks_f, int co_pad_d,
+                                                                int chunks_d, int blocks_f) {
+  const bool d = int(blockIdx.x) >= blocks_f;
+  const int co_pad = d ? co_pad_d : co_pad_f, chunks = d ? chunks_d : chunks_f;
+  const int b0 = d ? int(blockIdx.x) - blocks_f : int(blockIdx.x);
+  const int nb = d ? int(gridDim.x) - blocks_f : blocks_f;
+  uint16_t* out = d ? wtd : wt;
+  const int64_t K = int64_t(chunks) * 9 * kKStep;
+  const int64_t n = int64_t(co_pad) * K;
+  for (int64_t i = int64_t(b0) * 256 + threadIdx.x; i < n; i += int64_t(nb) * 256) {
+    const int row = int(i / K);
+    const int k = int(i - int64_t(row) * K);
+    const int c = k % kKStep;
+    const int tap = (k / kKStep) % 9;
+    const int col = (k / (kKStep * 9)) * kKStep + c;
+    uint16_t v = 0;
+    if (!d) {
+      if (row < Cout && col < Cin) v = w[(int64_t(row) * Cin + col) * 9 + tap];
+    } else {
+      if (row < Cin && col < Cout) v = w[(int64_t(col) * Cin + row) * 9 + (8 - tap)];
+    }
+    out[i] = v;
+  }
+}
+
 int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, int chunks,
                 int dgrad, void* stream) {
   if (!admit_launch("conv3x3 weight preparation")) return -1;
@@ -1829,6 +1860,21 @@ int xdna_conv3x3_prepare_weights_bf16(const uint16_t* w, uint16_t* wt, int Cout,
   const int cin = dgrad ? Cout : Cin, cout = dgrad ? Cin : Cout;
   const FwdPlan p = fwd_plan(1, cin, cout, 1, 1);
   return launch_prep(w, wt, Cout, Cin, p.co_pad, p.chunks, dgrad ? 1 : 0, stream);
+}
+
+int xdna_conv3x3_prepare_weights_both_bf16(const uint16_t* w, uint16_t* wt, uint16_t* wt_dgrad, int Cout,
+                                           int Cin, void* stream) {
+  if (Cout < 1 || Cin < 1 || !w || !wt || !wt_dgrad) {
+    set_error("xdna_conv3x3_prepare_weights_both_bf16: invalid arguments");
+    return -1;
+  }
+  const FwdPlan pf = fwd_plan(1, Cin, Cout, 1, 1), pd = fwd_plan(1, Cout, Cin, 1, 1);
+  const int64_t nf = int64_t(pf.co_pad) * pf.chunks * 9 * kKStep, nd = int64_t(pd.co_pad) * pd.chunks * 9 * kKStep;
+  const int bf = int(std::min<int64_t>(ceil_div(nf, 256), 2048)), bd = int(std::min<int64_t>(ceil_div(nd, 256), 2048));
+  if (!admit_launch("conv3x3 weight preparation")) return -1;
+  prep_weights_both_kernel<<<bf + bd, 256, 0, as_stream(stream)>>>(w, wt, wt_dgrad, Cout, Cin, pf.co_pad, pf.chunks,
+                                                                   pd.co_pad, pd.chunks, bf);
+  return check_launch("conv3x3 weight preparation");
 }
 
 int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,

@@ -149,6 +149,13 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
                                 [](const auto& a, const auto& b) { return a.last_use < b.last_use; });
     c.entries.erase(lru);
   }
+  // an entry for the same tensor and direction (an older version) is replaced
+  const auto same = [&](const PreparedWeights& e) {
+    auto live = e.storage.lock();
+    return e.dgrad == dgrad && e.offset == w.storage_offset() && e.sizes == sizes4(w) && live &&
+           live.get() == w.storage().unsafeGetStorageImpl();
+  };
+  c.entries.erase(std::remove_if(c.entries.begin(), c.entries.end(), same), c.entries.end());
   PreparedWeights e;
   e.storage = c10::weak_intrusive_ptr<c10::StorageImpl>(w.storage().getWeakStorageImpl());
   e.offset = w.storage_offset();
@@ -193,15 +200,30 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
                 "conv pack");
     }
   }
+  // Frozen weights: both forms cached by storage and version.  Trainable weights: the
+  // forward prepares the input gradient's form in the same launch and leaves it in the
+  // cache under the weight's current version, where the backward of the same step finds
+  // it (an optimizer step bumps the version; a stale entry is never read).
   const bool cacheable = weight_cacheable(w);
-  at::Tensor wt = cacheable ? cached_weights(w, dgrad) : at::Tensor();
+  const bool trainable = w.requires_grad() && !w.is_inference();
+  at::Tensor wt = cacheable || (trainable && dgrad) ? cached_weights(w, dgrad) : at::Tensor();
   if (!wt.defined()) {
     wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
-    check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
-                                                static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
-                                                int(w.size(1)), dgrad ? 1 : 0, st),
-              "conv weights");
-    if (cacheable) remember_weights(w, dgrad, wt);
+    if (trainable && !dgrad) {
+      at::Tensor wtd = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cout), int(cin)));
+      check_abi(xdna_conv3x3_prepare_weights_both_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
+                                                       static_cast<uint16_t*>(wt.data_ptr()),
+                                                       static_cast<uint16_t*>(wtd.data_ptr()), int(w.size(0)),
+                                                       int(w.size(1)), st),
+                "conv weights");
+      remember_weights(w, true, wtd);
+    } else {
+      check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
+                                                  static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
+                                                  int(w.size(1)), dgrad ? 1 : 0, st),
+                "conv weights");
+      if (cacheable) remember_weights(w, dgrad, wt);
+    }
   }
   at::Tensor out = empty_xdna({B, cout, H, W}, at::kBFloat16);
   at::Tensor bc;

@@ -69,6 +69,7 @@ SIGNATURES = {
     "xdna_upsample_nearest2x_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_set_variant": (I, [I]),
     "xdna_subsample2_bf16": (I, [P, P, L, I, I, P]),
+    "xdna_conv3x3_prepare_weights_both_bf16": (I, [P, P, P, I, I, P]),
     "xdna_dilate2_bf16": (I, [P, P, L, I, I, P]),
     "xdna_upsample_nearest2x_bwd_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_dgrad_bf16": (I, [P, P, P] + [I] * 11 + [P]),

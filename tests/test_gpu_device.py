@@ -169,6 +169,26 @@ def test_default_routing_of_general_convs(xdna):
         assert np.abs(g - r).max() <= 2 * oracle.bf16_ulp(np.abs(r).max()) + 1e-6, what
 
 
+def test_trainable_weight_forms_follow_the_version(xdna):
+    """The forward of a trainable weight prepares the input gradient's weight form too and
+    leaves it for the backward; an in-place update of the weight (a version bump) between
+    the two makes the backward prepare it again, so dx always uses the current weight."""
+    torch.manual_seed(3)
+    x = torch.randn(2, 64, 10, 10).bfloat16()
+    dy = torch.randn(2, 64, 10, 10).bfloat16()
+    w = (torch.randn(64, 64, 3, 3) * 0.05).bfloat16()
+    wd = w.to(X).requires_grad_()
+    xd, dyd = x.to(X), dy.to(X)
+    args = ([1, 1], [1, 1], [1, 1], False, [0, 0], 1)
+    with torch.no_grad():
+        torch.ops.aten.convolution(xd, wd, None, *args)
+        for step in range(2):
+            dx = torch.ops.aten.convolution_backward(dyd, xd, wd, None, *args, [True, False, False])[0]
+            ref = oracle.conv2d_dgrad(bits(dy), bits(wd), (10, 10), (1, 1), (1, 1))
+            check_bf16(bits(dx), ref, what=f"dgrad after update {step}")
+            wd.mul_(-0.5)  # version bump, no new forward
+
+
 def test_ineligible_convs_fall_back(xdna):
     """Dilated, grouped and fp32 convolutions stay on PyTorch-ROCm."""
     xdna.reset_mapped_cpu_stats()
