@@ -468,6 +468,12 @@ void gemm2_kernel(GemmArgs g) {
 // row-contiguous ones (checked by the launcher).
 // ---------------------------------------------------------------------------------------
 constexpr int kT4 = 256, kK4 = 64, kP4 = 72;
+// A row-contiguous operand's k-tile stays in its own layout, [k][row] with pitch kPR4
+// (consecutive k rows start 8 banks apart), and its MFMA fragments are read with the
+// transposing LDS read; it fits the region of a k-contiguous tile.
+constexpr int kPR4 = kT4 + 16;
+static_assert(kK4 * kPR4 <= kT4 * kP4, "a [k][row] tile fits the operand region");
+typedef short g4i16x4 __attribute__((ext_vector_type(4)));
 constexpr size_t kGemm4Lds = size_t(2) * 2 * kT4 * kP4 * 2;  // 2 buffers x (A, B)
 
 // One operand's loads through a buffer resource: per thread 8 vectors of 16 bytes per
@@ -499,9 +505,10 @@ __device__ inline G4Operand g4_operand(const uint16_t* src, int64_t s_r, int64_t
       row = r0 + (v >> 3);
       o.kq[j] = (v & 7) * 8;
     } else {
-      // rows [r0 + (tid % 32) * 8, +8) at k = ((tid / 32) + 8 (j / 4)) * 4 + j % 4
-      row = r0 + (tid & 31) * 8;
-      o.kq[j] = ((tid >> 5) + 8 * (j >> 2)) * 4 + (j & 3);
+      // vector v = tid + 256 j: rows [r0 + (v % 32) * 8, +8) at k = v / 32
+      const int v = tid + j * 256;
+      row = r0 + (v & 31) * 8;
+      o.kq[j] = v >> 5;
     }
     o.roff[j] = row < rows ? int(int64_t(row) * s_r) : -1;
   }
@@ -527,19 +534,30 @@ __device__ inline void g4_store(uint16_t* lds, const u32x4_t (&r)[8], int tid) {
       *reinterpret_cast<u32x4_t*>(lds + (v >> 3) * kP4 + (v & 7) * 8) = r[j];
     }
   } else {
-    // r[4h + i] holds rows rg*8 .. +7 at k = (kq + 8h) * 4 + i: row e gets 4 k as two dwords
-    const int rg = tid & 31, kq = tid >> 5;
+    // as loaded: 8 rows at one k per vector, into the [k][row] tile
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high / low halves
-        g2u2 w;
-        w[0] = __builtin_amdgcn_perm(r[4 * h + 1][e >> 1], r[4 * h][e >> 1], sel);
-        w[1] = __builtin_amdgcn_perm(r[4 * h + 3][e >> 1], r[4 * h + 2][e >> 1], sel);
-        *reinterpret_cast<g2u2*>(lds + (rg * 8 + e) * kP4 + (kq + 8 * h) * 4) = w;
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int v = tid + j * 256;
+      *reinterpret_cast<u32x4_t*>(lds + (v >> 5) * kPR4 + (v & 31) * 8) = r[j];
+    }
   }
+}
+
+// MFMA fragment of a k-tile: row rb + lane % 32, k = kk + 8 (lane / 32) .. +8.  From a
+// [k][row] tile with two transposing reads: in 16-lane group g = lane / 16 (rows
+// +16 (g % 2), k +8 (g / 2)), lane j supplies (k + j / 4, row + 4 (j % 4)) and every lane
+// receives 4 consecutive k of its own row (layout measured on the MI355X).
+template <int kMode>
+__device__ inline u32x4_t g4_frag(const uint16_t* tile, int rb, int kk, int lane) {
+  if (kMode == kAlongK)
+    return *reinterpret_cast<const u32x4_t*>(tile + (rb + (lane & 31)) * kP4 + kk + (lane >> 5) * 8);
+  const int g = lane >> 4, j = lane & 15;
+  const uint16_t* p = tile + (kk + 8 * (g >> 1) + (j >> 2)) * kPR4 + rb + 16 * (g & 1) + 4 * (j & 3);
+  const g4i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) g4i16x4*)(p));
+  const g4i16x4 hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) g4i16x4*)(p + 4 * kPR4));
+  const g2u2 a = __builtin_bit_cast(g2u2, lo), b = __builtin_bit_cast(g2u2, hi);
+  return u32x4_t{a[0], a[1], b[0], b[1]};
 }
 
 template <int kModeA, int kModeB>
@@ -581,12 +599,10 @@ void gemm4_kernel(GemmArgs g) {
   } while (0)
 #define XDNA_G4_FRAGS(buf_, t_, ks_)                                                         \
   do {                                                                                       \
-    const uint16_t* as_ = abuf(t_) + (wm * 128 + lr) * kP4 + lk + (ks_) * 16;                 \
-    const uint16_t* bs_ = abuf(t_) + kT4 * kP4 + (wn * 128 + lr) * kP4 + lk + (ks_) * 16;     \
     _Pragma("unroll") for (int i = 0; i < 4; ++i)                                            \
-      fa[buf_][i] = *reinterpret_cast<const u32x4_t*>(as_ + i * 32 * kP4);                   \
+      fa[buf_][i] = g4_frag<kModeA>(abuf(t_), wm * 128 + i * 32, (ks_) * 16, lane);          \
     _Pragma("unroll") for (int j = 0; j < 4; ++j)                                            \
-      fb[buf_][j] = *reinterpret_cast<const u32x4_t*>(bs_ + j * 32 * kP4);                   \
+      fb[buf_][j] = g4_frag<kModeB>(abuf(t_) + kT4 * kP4, wn * 128 + j * 32, (ks_) * 16, lane); \
   } while (0)
 #define XDNA_G4_MFMA(buf_)                                                                   \
   do {                                                                                       \
@@ -604,6 +620,8 @@ void gemm4_kernel(GemmArgs g) {
     __syncthreads();
     XDNA_G4_FRAGS(0, 0, 0);
     constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100, kDsWr = 0x200;
+    // LDS reads per k-step: one per fragment, two for a row-contiguous operand's
+    constexpr int kRd = (kModeA == kAlongK ? 4 : 8) + (kModeB == kAlongK ? 4 : 8);
     for (int t = 0; t < ntiles; ++t) {
 #pragma unroll
       for (int ks = 0; ks < 3; ++ks) {
@@ -612,12 +630,11 @@ void gemm4_kernel(GemmArgs g) {
         if (ks == 0) XDNA_G4_LOAD(t + 2);    // k-tile t+2 into registers
         XDNA_G4_MFMA(cur);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 16; ++i) {
           __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
-          if (ks == 0) __builtin_amdgcn_sched_group_barrier(kVmemRd, 2, 0);
+          if (i < kRd) __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+          if (ks == 0 && i < 8) __builtin_amdgcn_sched_group_barrier(kVmemRd, 2, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
       // every wave has read this k-tile's buffer for the last time (k-step 3's fragments)
@@ -626,14 +643,10 @@ void gemm4_kernel(GemmArgs g) {
       XDNA_G4_STORE(t + 2);                  // into this k-tile's buffer
       XDNA_G4_MFMA(1);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 16; ++i) {
         __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kDsWr, kModeA == kAlongK && kModeB == kAlongK ? 2 : 4, 0);
+        if (i < kRd) __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+        if (i >= 8) __builtin_amdgcn_sched_group_barrier(kDsWr, 2, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
