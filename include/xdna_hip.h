@@ -226,6 +226,19 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
                             uint16_t* gb, int B, int Cin, int Cout, int H, int W,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* Weight gradient (+ bias gradient when gb is not null) from the packed row layouts the
+ * forward and input-gradient convs use: xp = x packed by
+ * xdna_conv3x3w_pack_input_dense_bf16 (Cin channels), dp = dY packed the same way (Cout
+ * channels; the input gradient's own packed operand).  No channel-major copy of either
+ * is made, and any width works (strips).  Same split-K partials and fixed-order reduce
+ * as xdna_conv3x3_wgrad_bf16 (workspace: xdna_conv3x3_wgrad_rows_workspace_bytes).
+ * Replaces the same reference stages as xdna_conv3x3_wgrad_bf16
+ * (XdnaConv3x3wDwRuntime::pack_operands / compute, torch_xdna_device.cpp:2660-2751). */
+size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W);
+int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_t* gw, uint16_t* gb, int B,
+                                 int Cin, int Cout, int H, int W, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* Bias gradient alone: gb[c] = sum_{b,y,x} dy[b][c][y][x] (fp32 sum, one rounding). */
 int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H,
                                 int W, void* stream);

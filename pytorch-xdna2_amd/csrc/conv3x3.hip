@@ -1670,6 +1670,227 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
 
 constexpr size_t kMaxWgradLds = 160 * 1024;
 
+// ---------------------------------------------------------------------------------------
+// Weight gradient on the packed row layout: x and dY as the forward and input-gradient
+// convolutions already pack them ([group][chunk][2126 rows][64 channels], one padded-grid
+// position per row), so no channel-major copy of either is made.  Output row p of group g
+// (the centre of its pixel is packed row p + wp + 1) pairs dY there with x rows
+// p + dy*wp + dx, all inside the group's 2126 rows, as in the forward kernel.
+//
+// One workgroup (8 waves): 128 output channels x 64 input channels x 9 taps over the
+// k-tiles (64 output rows) of one split.  The dY tile ([64 rows][128 channels]) and the
+// x window ([64 + 2wp + 2 rows][64 channels]) sit in LDS in that row-major form and every
+// MFMA fragment (8 consecutive rows of one channel) is read with two transposing LDS
+// reads (ds_read_tr16_b64); any row offset is aligned, so a tap is a row offset.  Per
+// 16-row step a wave reads its dY fragment once and 12 consecutive x rows per kernel row
+// (three reads), building dx = 0, 1, 2 from them with alignbit.  Strip halo columns
+// (images wider than 36 are packed as strips with one real column on each side) are
+// zeroed in the dY tile: those pixels belong to the neighbouring strip.
+constexpr int kWrA = 128 + 16;   // LDS pitch (elements) of the dY tile: rows 8 banks apart
+constexpr int kWrX = 64 + 16;    // LDS pitch of the x window
+constexpr int kWrXv = 3;         // x-window vectors per thread (8 * (64 + 2*38 + 2) <= 3 * 512)
+
+struct WgRowsArgs {
+  const uint16_t* xp;  // packed x  [groups][ci_chunks][2126][64]
+  const uint16_t* dp;  // packed dY [groups][co_chunks][2126][64]
+  float* part;         // [splits][co_pad][9][ci_pad]
+  float* bpart;        // [splits][co_pad]
+  int ci_chunks, co_chunks, ci_pad, co_pad;
+  int wp, S, Wg;
+  int64_t img, m_total;
+  int ktiles, kt_per_split, splits, nco_t, ntiles;
+};
+
+typedef short wr_i16x4 __attribute__((ext_vector_type(4)));
+
+// rows q .. q+3 of column c of a row-major LDS tile, as two dwords: in 16-lane group
+// g = lane / 16 (columns +16 (g % 2), rows +8 (g / 2)), lane j supplies (row + j / 4,
+// column + 4 (j % 4)) and every lane receives 4 consecutive rows of its own column
+__device__ inline uint2 wr_tr4(const uint16_t* tile, int pitch, int q, int cb, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const uint16_t* p = tile + (q + 8 * (g >> 1) + (j >> 2)) * pitch + cb + 16 * (g & 1) + 4 * (j & 3);
+  const wr_i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) wr_i16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void wgrad_rows_kernel(WgRowsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int xrows = 64 + 2 * a.wp + 2;
+  // the third read of a kernel row reaches up to 2 rows past the window (values never
+  // used): the buffer holds 4 more rows
+  const int buf_elems = 64 * kWrA + (xrows + 4) * kWrX;
+  // blockIdx.x -> (co tile, ci tile, split): a split's channel tiles share one XCD
+  const int L = blockIdx.x;
+  const int xcd = L % kXcds, kq = L / kXcds;
+  const int tile = kq % a.ntiles;
+  const int split = (kq / a.ntiles) * kXcds + xcd;
+  if (split >= a.splits) return;
+  const int co_t = tile % a.nco_t, ci_t = tile / a.nco_t;
+  const int co0 = co_t * kTCo, ci0 = ci_t * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int kt0 = split * a.kt_per_split;
+  const int kt1 = min(a.ktiles, kt0 + a.kt_per_split);
+  const int nxv = xrows * 8;
+
+  f32x16_t acc[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) acc[t] = zero_acc();
+  float bsum = 0.0f;
+  const bool do_bias = a.bpart && ci_t == 0 && wn == 0;
+
+  u32x4_t dreg[2];
+  u32x4_t xreg[kWrXv];
+  bool dok[2];
+  // k-tile kt: group kt / 32, output rows r0 = (kt % 32) * 64 of it
+  auto load = [&](int kt) {
+    const int g = kt >> 5, r0 = (kt & 31) * 64;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      // vector i: row i / 16, channels (i % 16) * 8 of the 128
+      const int i = tid + j * 512;
+      const int row = i >> 4, ch = (i >> 3) & 1, piece = i & 7;
+      const int chunk = co0 / 64 + ch;
+      const int64_t p = int64_t(g) * kGroupOutRows + r0 + row;  // output row
+      bool ok = chunk < a.co_chunks && p < a.m_total;
+      if (a.S > 1) {
+        const int jcol = int((p % a.img) % a.wp);
+        ok = ok && jcol != 0 && jcol != a.Wg - 1;
+      }
+      dok[j] = ok;
+      const int cchunk = min(chunk, a.co_chunks - 1);
+      dreg[j] = *reinterpret_cast<const u32x4_t*>(
+          a.dp + ((int64_t(g) * a.co_chunks + cchunk) * kGroupRows + r0 + row + a.wp + 1) * kKStep + piece * 8);
+    }
+    const uint16_t* xs = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
+#pragma unroll
+    for (int j = 0; j < kWrXv; ++j) {
+      const int i = min(tid + j * 512, nxv - 1);
+      xreg[j] = *reinterpret_cast<const u32x4_t*>(xs + (i >> 3) * kKStep + (i & 7) * 8);
+    }
+  };
+  auto store = [&](int buf) {
+    uint16_t* as = smem + buf * buf_elems;
+    uint16_t* xs = as + 64 * kWrA;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + j * 512;
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(as + (i >> 4) * kWrA + (i & 15) * 8) = dok[j] ? dreg[j] : z;
+    }
+#pragma unroll
+    for (int j = 0; j < kWrXv; ++j) {
+      const int i = tid + j * 512;
+      if (i < nxv) *reinterpret_cast<u32x4_t*>(xs + (i >> 3) * kWrX + (i & 7) * 8) = xreg[j];
+    }
+  };
+
+  if (kt0 < kt1) {
+    load(kt0);
+    store(0);
+  }
+  __syncthreads();
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int cur = (kt - kt0) & 1;
+    const bool more = kt + 1 < kt1;
+    if (more) load(kt + 1);
+    const uint16_t* as = smem + cur * buf_elems;
+    const uint16_t* xs = as + 64 * kWrA;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int q = ks * 16;
+      const uint2 a0 = wr_tr4(as, kWrA, q, wm * 32, lane), a1 = wr_tr4(as, kWrA, q + 4, wm * 32, lane);
+      const u32x4_t av = {a0.x, a0.y, a1.x, a1.y};
+      if (do_bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          bsum += __uint_as_float(av[e] << 16) + __uint_as_float(av[e] & 0xFFFF0000u);
+      }
+      const bf16x8_t af = as_bf16x8(av);
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy) {
+        const int qx = q + dy * a.wp;
+        const uint2 r0 = wr_tr4(xs, kWrX, qx, wn * 32, lane);
+        const uint2 r1 = wr_tr4(xs, kWrX, qx + 4, wn * 32, lane);
+        const uint2 r2 = wr_tr4(xs, kWrX, qx + 8, wn * 32, lane);
+        const u32x4_t l = {r0.x, r0.y, r1.x, r1.y};
+        u32x4_t s1, s2;
+        s1[0] = __builtin_amdgcn_alignbit(r0.y, r0.x, 16);
+        s1[1] = __builtin_amdgcn_alignbit(r1.x, r0.y, 16);
+        s1[2] = __builtin_amdgcn_alignbit(r1.y, r1.x, 16);
+        s1[3] = __builtin_amdgcn_alignbit(r2.x, r1.y, 16);
+        s2[0] = r0.y;
+        s2[1] = r1.x;
+        s2[2] = r1.y;
+        s2[3] = r2.x;
+        acc[dy * 3 + 0] = mfma_32x32x16(af, as_bf16x8(l), acc[dy * 3 + 0]);
+        acc[dy * 3 + 1] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1]);
+        acc[dy * 3 + 2] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2]);
+      }
+    }
+    if (more) store(cur ^ 1);
+    __syncthreads();
+  }
+
+  // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci
+  const int lr = lane & 31;
+  float* pbase = a.part + int64_t(split) * a.co_pad * 9 * a.ci_pad;
+  const int ci = ci0 + wn * 32 + lr;
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 32 + mfma_row(i, lane);
+      pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][i];
+    }
+  if (do_bias) {
+    // lanes l and l+32 hold the two 8-row halves of channel row l % 32
+    const float other = __shfl_down(bsum, 32, 64);
+    if (lane < 32) a.bpart[int64_t(split) * a.co_pad + co0 + wm * 32 + lane] = bsum + other;
+  }
+}
+
+struct WgRowsPlan {
+  ConvGeom geom;
+  int ci_chunks = 0, co_chunks = 0, ci_pad = 0, co_pad = 0;
+  int ktiles = 0, splits = 0, kt_per = 0;
+  size_t part_bytes = 0, bpart_bytes = 0, lds_bytes = 0;
+};
+
+WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W) {
+  WgRowsPlan p;
+  p.geom = conv_geom(B, H, W);
+  p.ci_chunks = int(ceil_div(Cin, kKStep));
+  p.co_chunks = int(ceil_div(Cout, kKStep));
+  p.ci_pad = p.ci_chunks * kKStep;
+  p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
+  p.ktiles = int(ceil_div(p.geom.m_total, 64));
+  const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
+  const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
+  // split count: the channel-major path's model (rounds of 256 workgroups x per-CU rate,
+  // plus the write and read of the fp32 partials)
+  const double flops = 2.0 * 9.0 * double(B) * H * W * double(Cin) * double(Cout);
+  const double cu_rate = 4.0e12, bw = 5.0e12;
+  int64_t best = 1;
+  double best_t = 1e30;
+  const int64_t smax = std::min<int64_t>(p.ktiles, 4096);
+  for (int64_t s = 1; s <= smax; s = s < 512 ? s + 1 : s + s / 8) {
+    const double rounds = double(ceil_div(tiles * s, 256));
+    const double t = rounds * flops / (double(tiles * s) * cu_rate) + 2.0 * double(s) * double(out_elems) * 4.0 / bw;
+    if (t < best_t) {
+      best_t = t;
+      best = s;
+    }
+  }
+  p.kt_per = int(ceil_div(p.ktiles, best));
+  p.splits = int(ceil_div(p.ktiles, p.kt_per));
+  p.part_bytes = align256(size_t(p.splits) * out_elems * 4);
+  p.bpart_bytes = align256(size_t(p.splits) * p.co_pad * 4);
+  p.lds_bytes = 2 * (size_t(64) * kWrA + size_t(64 + 2 * p.geom.st.wp + 2 + 4) * kWrX) * 2;
+  return p;
+}
+
 }  // namespace
 }  // namespace xdna
 
@@ -1839,6 +2060,75 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
     return -1;
   return xdna_conv3x3_wgrad_packed_bf16(gw, gb, B, Cin, Cout, H, W, workspace, workspace_bytes,
                                         stream);
+}
+
+size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W) {
+  if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1) return 0;
+  const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W);
+  return p.part_bytes + p.bpart_bytes;
+}
+
+int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_t* gw, uint16_t* gb, int B,
+                                 int Cin, int Cout, int H, int W, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (!shape_ok("xdna_conv3x3_wgrad_rows_bf16", B, Cin, Cout, H, W)) return -1;
+  if (!xp || !dp || !gw) {
+    set_error("xdna_conv3x3_wgrad_rows_bf16: null operand");
+    return -1;
+  }
+  const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W);
+  if (!workspace || workspace_bytes < p.part_bytes + p.bpart_bytes) {
+    set_error("xdna_conv3x3_wgrad_rows_bf16: workspace too small");
+    return -1;
+  }
+  if (!admit_launch("conv3x3 wgrad rows")) return -1;
+  static const bool lds_attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          int(kMaxWgradLds)) == hipSuccess;
+  if (!lds_attr || p.lds_bytes > kMaxWgradLds) {
+    (void)hipGetLastError();
+    set_error("conv3x3 wgrad rows: cannot raise the dynamic LDS limit");
+    return -1;
+  }
+  WgRowsArgs a;
+  a.xp = xp;
+  a.dp = dp;
+  a.part = static_cast<float*>(workspace);
+  a.bpart = gb ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.part_bytes) : nullptr;
+  a.ci_chunks = p.ci_chunks;
+  a.co_chunks = p.co_chunks;
+  a.ci_pad = p.ci_pad;
+  a.co_pad = p.co_pad;
+  a.wp = p.geom.st.wp;
+  a.S = p.geom.st.S;
+  a.Wg = p.geom.st.Wg;
+  a.img = p.geom.img;
+  a.m_total = p.geom.m_total;
+  a.ktiles = p.ktiles;
+  a.kt_per_split = p.kt_per;
+  a.splits = p.splits;
+  a.nco_t = p.co_pad / kTCo;
+  a.ntiles = a.nco_t * (p.ci_pad / 64);
+  const int64_t nblocks = ceil_div(p.splits, kXcds) * kXcds * int64_t(a.ntiles);
+  if (nblocks > int64_t(0x7fffffff)) {
+    set_error("conv3x3 wgrad rows: grid too large");
+    return -1;
+  }
+  hipStream_t st = as_stream(stream);
+  wgrad_rows_kernel<<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
+  const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
+  const int zg = p.splits >= 64 ? 8 : p.splits >= 16 ? 4 : p.splits >= 4 ? 2 : 1;
+  const unsigned rgrid = unsigned(std::min<int64_t>(ceil_div(n, 256 / zg), 8192));
+  float* bp = gb ? a.bpart : nullptr;
+  if (zg == 8)
+    wgrad_reduce_kernel<8><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  else if (zg == 4)
+    wgrad_reduce_kernel<4><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  else if (zg == 2)
+    wgrad_reduce_kernel<2><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  else
+    wgrad_reduce_kernel<1><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  return check_launch("conv3x3 wgrad rows");
 }
 
 size_t xdna_conv3x3w_packed_bytes(int B, int C, int H, int W) {

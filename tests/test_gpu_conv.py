@@ -124,6 +124,35 @@ def test_wgrad(hip, shape):
     check_bf16(host(gb2), ref_b, what=f"bias grad kernel {shape}")
 
 
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_rows(hip, shape):
+    """Weight gradient from the packed row layouts (x and dY packed as the forward and
+    input-gradient convs pack them) vs the oracle; run-to-run bit equality."""
+    B, Cin, Cout, H, W = shape
+    print(f"conv wgrad rows {shape}", flush=True)
+    x, _, _, dy = _data(*shape, seed=sum(shape) + 3)
+    ref_w, ref_b = oracle.conv3x3_wgrad(x, dy)
+    xp = _ws(hip.xdna_conv3x3w_packed_bytes(B, Cin, H, W))
+    dp = _ws(hip.xdna_conv3x3w_packed_bytes(B, Cout, H, W))
+    assert hip.xdna_conv3x3w_pack_input_dense_bf16(ptr(dev(x)), ptr(xp), B, Cin, H, W, stream()) == 0
+    assert hip.xdna_conv3x3w_pack_input_dense_bf16(ptr(dev(dy)), ptr(dp), B, Cout, H, W, stream()) == 0
+    ws_bytes = hip.xdna_conv3x3_wgrad_rows_workspace_bytes(B, Cin, Cout, H, W)
+    ws = _ws(ws_bytes)
+    gw = dev_zeros((Cout, Cin, 3, 3))
+    gb = dev_zeros((Cout,))
+    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw), ptr(gb), B, Cin, Cout, H, W, ptr(ws),
+                                            ws_bytes, stream()) == 0
+    got_w = host(gw)
+    check_bf16(got_w, ref_w, what=f"wgrad rows {shape}")
+    check_bf16(host(gb), ref_b, what=f"bias grad rows {shape}")
+    gw2 = dev_zeros((Cout, Cin, 3, 3))
+    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, ptr(ws),
+                                            ws_bytes, stream()) == 0
+    np.testing.assert_array_equal(host(gw2), got_w)
+    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, ptr(ws),
+                                            ws_bytes - 1, stream()) == -1
+
+
 def test_workspace_too_small_is_an_error(hip):
     B, C, H, W = 1, 8, 4, 4
     ws = _ws(64)
