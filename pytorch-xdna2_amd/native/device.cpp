@@ -44,6 +44,11 @@ std::atomic<int> g_gconv_mode{[] {
   const int v = e ? std::atoi(e) : 1;
   return v < 0 || v > 2 ? 1 : v;
 }()};
+std::atomic<int> g_wgrad_form{[] {
+  const char* e = std::getenv("XDNA_WGRAD_FORM");
+  const int v = e ? std::atoi(e) : 0;
+  return v < 0 || v > 2 ? 0 : v;
+}()};
 
 namespace {
 
@@ -599,6 +604,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     g_gconv_mode.store(m);
   });
   mod.def("general_conv_mode", [] { return g_gconv_mode.load(); });
+  mod.def("set_wgrad_form", [](int m) {
+    TORCH_CHECK(m >= 0 && m <= 2, "xdna: weight-gradient form must be 0, 1 or 2");
+    g_wgrad_form.store(m);
+  });
+  mod.def("wgrad_form", [] { return g_wgrad_form.load(); });
   mod.def("mapped_cpu_stats", [] { return stats_dict(path_stats()); });
   mod.def("reset_mapped_cpu_stats", [] {
     std::lock_guard<std::mutex> lock(stats_mu());

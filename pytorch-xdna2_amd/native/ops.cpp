@@ -167,14 +167,12 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
   c.entries.push_back(std::move(e));
 }
 
-// Runs the conv of `src` (NCHW, cin channels) with `w` (forward: w as given; dgrad:
-// flip+swap) into a new NCHW tensor of cout channels.
-at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor* bias,
-                    bool dgrad) {
+// The packed row layout of an NCHW bf16 tensor ([groups][chunks][2126 rows][64 channels],
+// images wider than 36 as strips), as the rows conv kernels and the rows weight gradient
+// read it.
+at::Tensor pack_rows(const at::Tensor& src) {
   const int64_t B = src.size(0), cin = src.size(1), H = src.size(2), W = src.size(3);
-  const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor x = src.contiguous();
-  at::Tensor wc = w.contiguous();
   void* st = current_stream();
   // The packed input is transient: the dense pack writes every element (zeros in the
   // borders and padded channels), so a recycled allocation needs no fill.  (The reference
@@ -200,6 +198,17 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
                 "conv pack");
     }
   }
+  return packed;
+}
+
+// Runs the conv of a packed input (NCHW shape `src`, cin channels) with `w` (forward: w as
+// given; dgrad: flip+swap) into a new NCHW tensor of cout channels.
+at::Tensor hip_conv_packed(const at::Tensor& packed, at::IntArrayRef src, const at::Tensor& w,
+                           const at::Tensor* bias, bool dgrad) {
+  const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
+  const int64_t cout = dgrad ? w.size(1) : w.size(0);
+  at::Tensor wc = w.contiguous();
+  void* st = current_stream();
   // Frozen weights: both forms cached by storage and version.  Trainable weights: the
   // forward prepares the input gradient's form in the same launch and leaves it in the
   // cache under the weight's current version, where the backward of the same step finds
@@ -237,6 +246,10 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
                                    int(H), int(W), st),
             "conv rows");
   return out;
+}
+
+at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor* bias, bool dgrad) {
+  return hip_conv_packed(pack_rows(src), src.sizes(), w, bias, dgrad);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -383,6 +396,39 @@ void hip_wgrad(const at::Tensor& input, const at::Tensor& dy, at::Tensor& gw, at
             "conv wgrad");
 }
 
+// Weight gradient (+ bias gradient) on the packed row layout: x packed here, dY in the
+// packed form its input gradient already read (`dpacked`), so neither is copied
+// channel-major.  The packs are snapshots, as in the channel-major form.
+void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int64_t Cout, at::Tensor& gw,
+                    at::Tensor* gb) {
+  const int64_t B = input.size(0), Cin = input.size(1), H = input.size(2), W = input.size(3);
+  const at::Tensor xpacked = pack_rows(input);
+  void* st = current_stream();
+  const size_t wsb = xdna_conv3x3_wgrad_rows_workspace_bytes(int(B), int(Cin), int(Cout), int(H), int(W));
+  at::Tensor ws = alloc_bytes(wsb);
+  gw = empty_xdna({Cout, Cin, 3, 3}, at::kBFloat16);
+  if (gb) *gb = empty_xdna({Cout}, at::kBFloat16);
+  KernelTimer kt("conv3x3_wgrad", 2.0 * double(B) * double(H) * double(W) * double(Cin) * double(Cout) * 9.0);
+  check_abi(xdna_conv3x3_wgrad_rows_bf16(static_cast<const uint16_t*>(xpacked.const_data_ptr()),
+                                         static_cast<const uint16_t*>(dpacked.const_data_ptr()),
+                                         static_cast<uint16_t*>(gw.data_ptr()),
+                                         gb ? static_cast<uint16_t*>(gb->data_ptr()) : nullptr, int(B), int(Cin),
+                                         int(Cout), int(H), int(W), ws.data_ptr(), wsb, st),
+            "conv wgrad rows");
+}
+
+// Which weight-gradient form a 3x3 layer takes (measured over the 36 sweep shapes, packs
+// included): the rows form wherever the image fits one strip, and for wider images with
+// at most 128 x 128 channels; wider images with more channels take the channel-major form,
+// since the rows form also multiplies the strip halo rows (17% of the rows at 72 x 72).
+// Images wider than 142 exceed the channel-major form's window and always take the rows form.
+bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W) {
+  const int form = g_wgrad_form.load();
+  if (W > 142 || form == 2) return true;
+  if (form == 1) return false;
+  return W <= 36 || Cin * Cout <= 128 * 128;
+}
+
 std::atomic<int64_t> g_dw_jobs{0};
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable_xdna(
@@ -410,14 +456,24 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     hip = true;
   }
   auto mask = output_mask;
+  const bool dw = hip && mask[1] && g_mode.load() >= 2;
+  const bool dw_rows = dw && wgrad_rows_pick(input.size(1), weight.size(0), input.size(3));
+  // dY packed once: the input gradient's conv and the rows weight gradient read it
+  at::Tensor gop;
+  if (hip && (mask[0] || dw_rows)) gop = pack_rows(go);
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
-    gi = hip_conv(go, weight, nullptr, true);
+    gi = hip_conv_packed(gop, go.sizes(), weight, nullptr, true);
     mask[0] = false;
   }
-  if (hip && mask[1] && g_mode.load() >= 2 && input.size(3) <= 142) {
+  if (dw) {
     ScopedCount sc("hip_conv3x3.dw.run");
-    hip_wgrad(input, go, gw, mask[2] ? &gb : nullptr);
+    if (dw_rows) {
+      ScopedCount sr("hip_conv3x3.dw_rows.run");
+      hip_wgrad_rows(input, gop, weight.size(0), gw, mask[2] ? &gb : nullptr);
+    } else {
+      hip_wgrad(input, go, gw, mask[2] ? &gb : nullptr);
+    }
     g_dw_jobs.fetch_add(1);
     mask[1] = false;
     mask[2] = false;

@@ -46,6 +46,8 @@ at::Tensor xdna_from_cuda(const at::Tensor& t);
 // (xdna_train/device.py:526-650).
 extern std::atomic<int> g_mode;
 extern std::atomic<int> g_gconv_mode;
+// 3x3 weight gradient: 0 (default) per layer shape, 1 channel-major form, 2 rows form.
+extern std::atomic<int> g_wgrad_form;
 
 // Per-path counters (the reference's ScopedMappedCpu, torch_xdna_device.cpp:1470-1521).
 void count_call(const char* name, int64_t ns);

@@ -22,9 +22,11 @@ from .device import (
     reset_mapped_cpu_stats,
     set_general_conv_mode,
     set_npu_mode,
+    set_wgrad_form,
     synchronize,
     try_register_xdna_device,
     wait_for_builds,
+    wgrad_form,
 )
 
 from .graphs import Graph, graph
@@ -47,6 +49,8 @@ __all__ = [
     "npu_mode",
     "set_general_conv_mode",
     "general_conv_mode",
+    "set_wgrad_form",
+    "wgrad_form",
     "wait_for_builds",
     "reset_fallback_stats",
     "fallback_stats",

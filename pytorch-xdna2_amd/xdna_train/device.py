@@ -334,6 +334,21 @@ def general_conv_mode() -> int:
     return int(_C.general_conv_mode())
 
 
+def set_wgrad_form(form: int) -> None:
+    """Weight gradient of the 3x3 / stride-1 convs: 0 (default) chosen per layer shape,
+    1 the channel-major form (x and dY copied channel-major), 2 the packed-rows form (dY
+    read in the packed form its input gradient used, x packed the same way).  Both sum in
+    fp32 and round once to bf16, in different orders.  Images wider than 142 always take
+    the rows form.  XDNA_WGRAD_FORM sets the initial value.  No reference counterpart."""
+    register_xdna_device()
+    _C.set_wgrad_form(int(form))
+
+
+def wgrad_form() -> int:
+    register_xdna_device()
+    return int(_C.wgrad_form())
+
+
 def wait_for_builds(timeout: float | None = None) -> bool:
     """Kernels are compiled ahead of time: nothing is ever pending."""
     del timeout

@@ -88,6 +88,41 @@ def test_conv_forward_backward_matches_cpu_and_oracle(xdna):
         assert (g - r).norm() / r.norm() < 1e-2
 
 
+@pytest.mark.parametrize("shape", [(4, 64, 96, 20, 24), (2, 32, 48, 12, 72), (1, 160, 144, 5, 72),
+                                   (1, 16, 24, 6, 150), (1, 8, 16, 3, 300)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_forms(xdna, shape):
+    """Both 3x3 weight-gradient forms (channel-major copies; packed rows sharing the input
+    gradient's packed dY) through the op path against the oracle, and the per-shape choice;
+    images wider than 142 take the rows form whatever the setting."""
+    B, Cin, Cout, H, W = shape
+    print(f"wgrad forms {shape}", flush=True)
+    g = torch.Generator().manual_seed(sum(shape))
+    x = torch.randn(B, Cin, H, W, generator=g).bfloat16()
+    dy = torch.randn(B, Cout, H, W, generator=g).bfloat16()
+    w = (torch.randn(Cout, Cin, 3, 3, generator=g) * 0.05).bfloat16()
+    gw_ref, gb_ref = oracle.conv3x3_wgrad(bits(x), bits(dy))
+    gx_ref = oracle.conv3x3_dgrad(bits(dy), bits(w))
+    expect_rows = {1: W > 142, 2: True, 0: W <= 36 or W > 142 or Cin * Cout <= 128 * 128}
+    try:
+        for form in (1, 2, 0):
+            xdna.set_wgrad_form(form)
+            assert xdna.wgrad_form() == form
+            xdna.reset_mapped_cpu_stats()
+            wd = w.to(X).requires_grad_()
+            bd = torch.zeros(Cout, dtype=torch.bfloat16).to(X).requires_grad_()
+            xd = x.to(X).requires_grad_()
+            torch.nn.functional.conv2d(xd, wd, bd, padding=1).backward(dy.to(X))
+            st = xdna.mapped_cpu_stats()
+            assert st.get("hip_conv3x3.dw.run", {}).get("calls", 0) == 1, st
+            assert st.get("hip_conv3x3.dw_rows.run", {}).get("calls", 0) == int(expect_rows[form]), (form, st)
+            check_bf16(bits(wd.grad), gw_ref, what=f"wgrad form {form}")
+            check_bf16(bits(bd.grad), gb_ref, what=f"bias grad form {form}")
+            check_bf16(bits(xd.grad), gx_ref, what=f"dgrad form {form}")
+    finally:
+        xdna.set_wgrad_form(0)
+
+
 def test_other_convs_run_on_general_kernels(xdna):
     """5x5, 1x1, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on the general
     HIP kernels (mode 2: always), the 3x3 / stride-2 / pad-1 one on the stride-1 3x3 path,
