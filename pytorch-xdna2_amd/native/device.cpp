@@ -575,6 +575,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   mod.def("synchronize", [] { check_abi(xdna_hip_device_synchronize(), "synchronize"); });
   mod.def("empty_cache", [] {
     clear_weight_cache();
+    clear_packed_inputs();
     check_abi(xdna_hip_device_synchronize(), "synchronize");
     check_abi(xdna_hip_cache_empty(), "empty_cache");
   });

@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <array>
+#include <deque>
 #include <mutex>
 #include <optional>
 #include <vector>
@@ -252,6 +253,100 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
   return hip_conv_packed(pack_rows(src), src.sizes(), w, bias, dgrad);
 }
 
+// Packed inputs of forward convs kept for the rows weight gradient of the same layer, so
+// that the backward does not pack x again.  Keyed by the input's storage, offset, sizes,
+// strides and version (autograd keeps the input alive and unchanged until the backward);
+// the backward takes its entry out.  Entries whose input storage has died are dropped,
+// and the oldest go once the kept bytes pass a cap.
+struct PackedInput {
+  c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
+  int64_t offset = 0, version = 0;
+  std::vector<int64_t> sizes, strides;
+  at::Tensor packed;
+};
+
+struct PackedInputCache {
+  std::mutex mu;
+  std::deque<PackedInput> entries;
+  size_t bytes = 0;
+  static constexpr size_t kMaxBytes = size_t(16) << 30;
+};
+
+PackedInputCache& packed_input_cache() {
+  static auto* c = new PackedInputCache();
+  return *c;
+}
+
+bool same_input(const PackedInput& e, const at::Tensor& x) {
+  if (e.offset != x.storage_offset() || e.sizes != x.sizes().vec() || e.strides != x.strides().vec() ||
+      e.version != int64_t(x.unsafeGetTensorImpl()->version_counter().current_version()))
+    return false;
+  auto live = e.storage.lock();
+  return live && live.get() == x.storage().unsafeGetStorageImpl();
+}
+
+void remember_packed_input(const at::Tensor& x, const at::Tensor& packed) {
+  PackedInputCache& c = packed_input_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (auto it = c.entries.begin(); it != c.entries.end();) {
+    if (it->storage.expired() || same_input(*it, x)) {
+      c.bytes -= size_t(it->packed.nbytes());
+      it = c.entries.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  PackedInput e;
+  e.storage = c10::weak_intrusive_ptr<c10::StorageImpl>(x.storage().getWeakStorageImpl());
+  e.offset = x.storage_offset();
+  e.version = int64_t(x.unsafeGetTensorImpl()->version_counter().current_version());
+  e.sizes = x.sizes().vec();
+  e.strides = x.strides().vec();
+  e.packed = packed;
+  c.bytes += size_t(packed.nbytes());
+  c.entries.push_back(std::move(e));
+  while (c.bytes > PackedInputCache::kMaxBytes && c.entries.size() > 1) {
+    c.bytes -= size_t(c.entries.front().packed.nbytes());
+    c.entries.pop_front();
+  }
+}
+
+at::Tensor take_packed_input(const at::Tensor& x) {
+  PackedInputCache& c = packed_input_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (auto it = c.entries.begin(); it != c.entries.end(); ++it) {
+    if (!same_input(*it, x)) continue;
+    at::Tensor p = it->packed;
+    c.bytes -= size_t(p.nbytes());
+    c.entries.erase(it);
+    return p;
+  }
+  return at::Tensor();
+}
+
+}  // namespace
+
+void clear_packed_inputs() {
+  PackedInputCache& c = packed_input_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.entries.clear();
+  c.bytes = 0;
+}
+
+namespace {
+
+bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W);
+
+// Forward of a 3x3 / stride-1 conv; the packed input is kept when this layer's weight
+// gradient will take the rows form.
+at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias) {
+  at::Tensor packed = pack_rows(input);
+  if (g_mode.load() >= 2 && at::GradMode::is_enabled() && weight.requires_grad() &&
+      wgrad_rows_pick(input.size(1), weight.size(0), input.size(3)))
+    remember_packed_input(input, packed);
+  return hip_conv_packed(packed, input.sizes(), weight, bias, false);
+}
+
 // ---------------------------------------------------------------------------------------
 // Other 2-D convolutions (any kernel size, stride and padding; dilation 1, groups 1, bf16):
 // the general HIP kernels.  The reference runs these on the CPU (its fallback to
@@ -340,13 +435,13 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv3x3.fwd.run");
-    return hip_conv(input, weight, has_bias ? &*bias : nullptr, false);
+    return hip_conv_fwd(input, weight, has_bias ? &*bias : nullptr);
   }
   if (conv_s2_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv3x3_s2.fwd.run");
-    const at::Tensor full = hip_conv(input, weight, has_bias ? &*bias : nullptr, false);
+    const at::Tensor full = hip_conv_fwd(input, weight, has_bias ? &*bias : nullptr);
     const int64_t B = full.size(0), C = full.size(1), H = full.size(2), W = full.size(3);
     at::Tensor y = empty_xdna({B, C, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16);
     check_abi(xdna_subsample2_bf16(static_cast<const uint16_t*>(full.const_data_ptr()),
@@ -402,7 +497,12 @@ void hip_wgrad(const at::Tensor& input, const at::Tensor& dy, at::Tensor& gw, at
 void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int64_t Cout, at::Tensor& gw,
                     at::Tensor* gb) {
   const int64_t B = input.size(0), Cin = input.size(1), H = input.size(2), W = input.size(3);
-  const at::Tensor xpacked = pack_rows(input);
+  at::Tensor xpacked = take_packed_input(input);
+  if (xpacked.defined()) {
+    ScopedCount sk("hip_conv3x3.dw_rows.kept_pack");
+  } else {
+    xpacked = pack_rows(input);
+  }
   void* st = current_stream();
   const size_t wsb = xdna_conv3x3_wgrad_rows_workspace_bytes(int(B), int(Cin), int(Cout), int(H), int(W));
   at::Tensor ws = alloc_bytes(wsb);

@@ -66,6 +66,8 @@ void register_autograd_ops(torch::Library& m);
 
 // Drops the prepared weights of frozen tensors (ops.cpp).
 void clear_weight_cache();
+// Drops the packed conv inputs kept for weight gradients (ops.cpp).
+void clear_packed_inputs();
 
 // Weight-gradient launches so far (ops.cpp).
 int64_t dw_jobs();

@@ -116,11 +116,40 @@ def test_wgrad_forms(xdna, shape):
             st = xdna.mapped_cpu_stats()
             assert st.get("hip_conv3x3.dw.run", {}).get("calls", 0) == 1, st
             assert st.get("hip_conv3x3.dw_rows.run", {}).get("calls", 0) == int(expect_rows[form]), (form, st)
+            # the rows form reads the forward's packed input
+            assert st.get("hip_conv3x3.dw_rows.kept_pack", {}).get("calls", 0) == int(expect_rows[form]), st
             check_bf16(bits(wd.grad), gw_ref, what=f"wgrad form {form}")
             check_bf16(bits(bd.grad), gb_ref, what=f"bias grad form {form}")
             check_bf16(bits(xd.grad), gx_ref, what=f"dgrad form {form}")
     finally:
         xdna.set_wgrad_form(0)
+
+
+def test_kept_packed_input_shared_and_stale(xdna):
+    """Two convs reading one input (one kept pack, taken by the first backward; the second
+    packs again), and a forward whose backward never runs: gradients still match the
+    oracle."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(2, 32, 10, 12, generator=g).bfloat16()
+    w1 = (torch.randn(48, 32, 3, 3, generator=g) * 0.05).bfloat16()
+    w2 = (torch.randn(40, 32, 3, 3, generator=g) * 0.05).bfloat16()
+    d1 = torch.randn(2, 48, 10, 12, generator=g).bfloat16()
+    d2 = torch.randn(2, 40, 10, 12, generator=g).bfloat16()
+    xd = x.to(X)
+    w1d, w2d = w1.to(X).requires_grad_(), w2.to(X).requires_grad_()
+    # a forward without a backward leaves an entry behind
+    F.conv2d(xd, w1d, padding=1)
+    xdna.reset_mapped_cpu_stats()
+    y1 = F.conv2d(xd, w1d, padding=1)
+    y2 = F.conv2d(xd, w2d, padding=1)
+    torch.autograd.backward([y1, y2], [d1.to(X), d2.to(X)])
+    st = xdna.mapped_cpu_stats()
+    assert st.get("hip_conv3x3.dw_rows.run", {}).get("calls", 0) == 2, st
+    assert st.get("hip_conv3x3.dw_rows.kept_pack", {}).get("calls", 0) == 1, st
+    for wd, d in ((w1d, d1), (w2d, d2)):
+        gw_ref, _ = oracle.conv3x3_wgrad(bits(x), bits(d))
+        check_bf16(bits(wd.grad), gw_ref, what="wgrad shared input")
+    xdna.empty_cache()
 
 
 def test_other_convs_run_on_general_kernels(xdna):
