@@ -227,17 +227,17 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Weight gradient (+ bias gradient when gb is not null) from the packed row layouts the
- * forward and input-gradient convs use: xp = x packed by
- * xdna_conv3x3w_pack_input_dense_bf16 (Cin channels), dp = dY packed the same way (Cout
- * channels; the input gradient's own packed operand).  No channel-major copy of either
- * is made, and any width works (strips).  Same split-K partials and fixed-order reduce
- * as xdna_conv3x3_wgrad_bf16 (workspace: xdna_conv3x3_wgrad_rows_workspace_bytes).
- * Replaces the same reference stages as xdna_conv3x3_wgrad_bf16
- * (XdnaConv3x3wDwRuntime::pack_operands / compute, torch_xdna_device.cpp:2660-2751). */
-size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W);
+ * forward and input-gradient convs use: xp = x packed in row layout `layout` (Cin
+ * channels), dp = dY packed the same way (Cout channels; the input gradient's own packed
+ * operand).  No channel-major copy of either is made, and any width works (strips).  Same
+ * split-K partials and fixed-order reduce as xdna_conv3x3_wgrad_bf16 (workspace:
+ * xdna_conv3x3_wgrad_rows_workspace_bytes, 0 for an invalid shape or layout).  Replaces
+ * the same reference stages as xdna_conv3x3_wgrad_bf16 (XdnaConv3x3wDwRuntime::
+ * pack_operands / compute, torch_xdna_device.cpp:2660-2751). */
+size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W, int layout);
 int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_t* gw, uint16_t* gb, int B,
-                                 int Cin, int Cout, int H, int W, void* workspace, size_t workspace_bytes,
-                                 void* stream);
+                                 int Cin, int Cout, int H, int W, int layout, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* Bias gradient alone: gb[c] = sum_{b,y,x} dy[b][c][y][x] (fp32 sum, one rounding). */
 int xdna_conv3x3_bias_grad_bf16(const uint16_t* dy, uint16_t* gb, int B, int C, int H,
@@ -271,6 +271,31 @@ int xdna_conv3x3_prepare_weights_both_bf16(const uint16_t* w, uint16_t* wt, uint
  * with prepared weights wt (+ bias[cout], may be NULL).  One kernel. */
 int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
                            uint16_t* y, int B, int cin, int cout, int H, int W, void* stream);
+
+/* Row layouts of the packed operands.  XDNA_CONV3X3_LAYOUT_REF: the reference's conv3x3w
+ * layout above (images wider than 36 as strips of up to 34 columns, each strip row with
+ * one neighbour column per side and two zero columns: wp = So + 4).
+ * XDNA_CONV3X3_LAYOUT_TIGHT: identical up to 36 columns; wider images as strips of up to
+ * 36 columns whose rows hold the strip's columns and one neighbour column per side and
+ * nothing else (wp = So + 2, data column j at row position j): the zero columns are never
+ * a tap of a real output, and 72 columns take 2 strips of 38 positions instead of 3 of
+ * 28.  Same groups of 2126 rows.  The backend's conv ops use the tight layout; no
+ * reference counterpart (an internal layout of the same kernels). */
+#define XDNA_CONV3X3_LAYOUT_REF 0
+#define XDNA_CONV3X3_LAYOUT_TIGHT 1
+
+/* Bytes of the packed input in `layout` (0 for an invalid shape or layout). */
+size_t xdna_conv3x3_layout_packed_bytes(int B, int C, int H, int W, int layout);
+
+/* Packs NCHW src into `layout`, writing every element (zeros included: the buffer needs
+ * no fill; images wider than 256 are zero-filled by a kernel first).  dst 16-byte aligned.
+ * For XDNA_CONV3X3_LAYOUT_REF the result equals xdna_conv3x3w_pack_input_dense_bf16's. */
+int xdna_conv3x3_layout_pack_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W, int layout,
+                                  void* stream);
+
+/* xdna_conv3x3_rows_bf16 on an input packed in `layout`. */
+int xdna_conv3x3_layout_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                  int B, int cin, int cout, int H, int W, int layout, void* stream);
 
 /* General 2-D convolution, bf16 in/out, fp32 accumulation: any kernel size, stride and
  * padding (dilation 1, groups 1), NCHW activations and OIHW weights.  Replaces the

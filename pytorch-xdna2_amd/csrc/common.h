@@ -38,20 +38,46 @@ constexpr int kRawN = 128;         // channels per raw output row block
 constexpr int kMaxWidth = 36;
 constexpr int kMaxStrip = 34;
 
+// Two row layouts share the group structure above.
+//  kLayoutRef: the reference's conv3x3w layout.  Images wider than 36 are cut into S strips
+//    of So <= 34 columns; a strip row holds Wg = So + 2 data columns (the strip's columns
+//    and one neighbour column each side, zero at the image border) between two zero
+//    columns (wp = Wg + 2, data column j at row position j + 1).
+//  kLayoutTight: the same up to 36 columns; wider images as strips of So <= 36 columns
+//    whose rows hold only the Wg = So + 2 data columns (wp = Wg, data column j at row
+//    position j).  The taps of a real output column stay inside its strip row, so the
+//    zero columns are never read: for 72 columns, 2 strips of 38 positions instead of 3
+//    of 28 (8.5% more rows than pixels instead of 20%).
+// Output column c of a strip is output row position c + first of its image row.
+constexpr int kLayoutRef = 0;
+constexpr int kLayoutTight = 1;
+constexpr int kMaxStripTight = 36;
+
 struct StripGeom {
   int S = 1, So = 0, Wg = 0, wp = 0;
+  int lead = 1;   // row position of data column 0
+  int first = 0;  // output row position of output column 0
 };
 
-inline StripGeom strip_geom(int W) {
+inline StripGeom strip_geom(int W, int layout = kLayoutRef) {
   StripGeom g;
   if (W <= kMaxWidth) {
-    g.S = 1; g.So = W; g.Wg = W;
+    g.S = 1; g.So = W; g.Wg = W; g.wp = W + 2;
+  } else if (layout == kLayoutTight) {
+    g.S = int(ceil_div(W, kMaxStripTight));
+    g.So = int(ceil_div(W, g.S));
+    g.Wg = g.So + 2;
+    g.wp = g.Wg;
+    g.lead = 0;
   } else {
     g.S = int(ceil_div(W, kMaxStrip));
     g.So = int(ceil_div(W, g.S));
     g.Wg = g.So + 2;
+    g.wp = g.Wg + 2;
   }
-  g.wp = g.Wg + 2;
+  // output row p is centred on packed row p + wp + 1; output column c reads data column
+  // c + (S > 1) at row position c + (S > 1) + lead
+  g.first = (g.S > 1 ? 1 : 0) + g.lead - 1;
   return g;
 }
 
@@ -63,9 +89,9 @@ struct ConvGeom {
   int groups = 0;
 };
 
-inline ConvGeom conv_geom(int B, int H, int W) {
+inline ConvGeom conv_geom(int B, int H, int W, int layout = kLayoutRef) {
   ConvGeom g;
-  g.st = strip_geom(W);
+  g.st = strip_geom(W, layout);
   g.B = B; g.H = H; g.W = W;
   g.img = int64_t(H + 2) * g.st.wp;
   g.m_total = int64_t(B) * g.st.S * g.img;

@@ -82,6 +82,7 @@ struct RowsArgs {
   uint16_t* out;         // NCHW [B][cout][H][W]
   float* part;           // split-K: fp32 partial sums [nsplit][cout][m_pad], else null
   int chunks, cout, wp, H, W, S, So;
+  int first;             // output row position of output column 0 (the layout's)
   int ch_per;            // input chunks per split (blockIdx.z)
   int nrt, ncot;         // row tiles, channel tiles (blockIdx.x decodes to both)
   int64_t img, m_total, m_pad;
@@ -116,7 +117,7 @@ __device__ inline OutMap out_map(const RowsArgs& a, int64_t p_first) {
 // kOutSkip for a border / padding row
 __device__ inline int out_pixel_off(const RowsArgs& a, const OutMap& o, int64_t p) {
   if (p >= a.m_total) return kOutSkip;
-  const int first = a.S == 1 ? 0 : 1;
+  const int first = a.first;
   const int64_t vb = p / a.img;
   const int64_t rem = p - vb * a.img;
   const int y = int(rem / a.wp);
@@ -299,7 +300,7 @@ void conv_rows_kernel(RowsArgs a) {
 
   // Epilogue: grid row -> NCHW pixel, one rounding; lanes 0..31 store 32 consecutive
   // grid rows (mostly consecutive image columns) of one channel.
-  const int first = a.S == 1 ? 0 : 1;
+  const int first = a.first;
   const int64_t plane = int64_t(a.H) * a.W;
   uint16_t* obase[NT];
 #pragma unroll
@@ -464,7 +465,7 @@ void conv_rows2_kernel(RowsArgs a) {
 #undef XDNA_X2_LOAD
 #undef XDNA_X2_STORE
 
-  const int first = a.S == 1 ? 0 : 1;
+  const int first = a.first;
   const int64_t plane = int64_t(a.H) * a.W;
   uint16_t* obase[4];
 #pragma unroll
@@ -715,7 +716,7 @@ void conv_rows4_kernel(RowsArgs a) {
       }
     return;
   }
-  const int first = a.S == 1 ? 0 : 1;
+  const int first = a.first;
   const int64_t plane = int64_t(a.H) * a.W;
   uint16_t* obase[NT];
 #pragma unroll
@@ -888,7 +889,7 @@ void conv_small_kernel(RowsArgs a) {
     }
     return;
   }
-  const int first = a.S == 1 ? 0 : 1;
+  const int first = a.first;
   const int64_t plane = int64_t(a.H) * a.W;
   uint16_t* obase[NT];
 #pragma unroll
@@ -927,7 +928,7 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(RowsArgs a, int nsplit
   if (pix >= a.H * a.W) return;
   const int y = pix / a.W, x = pix - y * a.W;
   const int s = a.S == 1 ? 0 : x / a.So;
-  const int col = x - s * a.So + (a.S == 1 ? 0 : 1);
+  const int col = x - s * a.So + a.first;
   const int64_t p = (int64_t(b) * a.S + s) * a.img + int64_t(y) * a.wp + col;
   float v = a.bias ? bf16_to_f32(a.bias[co]) : 0.0f;
   const float* pp = a.part + int64_t(co) * a.m_pad + p;
@@ -1468,8 +1469,8 @@ std::atomic<int> g_rows_variant{[] {
 }()};
 
 int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
-                int B, int cin, int cout, int H, int W, void* stream) {
-  const ConvGeom geom = conv_geom(B, H, W);
+                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef) {
+  const ConvGeom geom = conv_geom(B, H, W, layout);
   RowsArgs a;
   a.xp = xp;
   a.wt = wt;
@@ -1483,6 +1484,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.W = W;
   a.S = geom.st.S;
   a.So = geom.st.So;
+  a.first = geom.st.first;
   a.ch_per = a.chunks;
   a.img = geom.img;
   a.m_total = geom.m_total;
@@ -1685,7 +1687,8 @@ constexpr size_t kMaxWgradLds = 160 * 1024;
 // 16-row step a wave reads its dY fragment once and 12 consecutive x rows per kernel row
 // (three reads), building dx = 0, 1, 2 from them with alignbit.  Strip halo columns
 // (images wider than 36 are packed as strips with one real column on each side) are
-// zeroed in the dY tile: those pixels belong to the neighbouring strip.
+// zeroed in the dY tile: those pixels belong to the neighbouring strip.  Either row layout
+// (the reference's, or the tight one without zero columns).
 constexpr int kWrA = 128 + 16;   // LDS pitch (elements) of the dY tile: rows 8 banks apart
 constexpr int kWrX = 64 + 16;    // LDS pitch of the x window
 constexpr int kWrXv = 3;         // x-window vectors per thread (8 * (64 + 2*38 + 2) <= 3 * 512)
@@ -1696,7 +1699,7 @@ struct WgRowsArgs {
   float* part;         // [splits][co_pad][9][ci_pad]
   float* bpart;        // [splits][co_pad]
   int ci_chunks, co_chunks, ci_pad, co_pad;
-  int wp, S, Wg;
+  int wp, S, Wg, lead;
   int64_t img, m_total;
   int ktiles, kt_per_split, splits, nco_t, ntiles;
 };
@@ -1755,8 +1758,11 @@ void wgrad_rows_kernel(WgRowsArgs a) {
       const int64_t p = int64_t(g) * kGroupOutRows + r0 + row;  // output row
       bool ok = chunk < a.co_chunks && p < a.m_total;
       if (a.S > 1) {
-        const int jcol = int((p % a.img) % a.wp);
-        ok = ok && jcol != 0 && jcol != a.Wg - 1;
+        // data column of the centre row p + wp + 1 (row position jcol + 1, wrapping to the
+        // next row's position 0)
+        int j = int((p % a.img) % a.wp) + 1 - a.lead;
+        if (j == a.wp) j = 0;
+        ok = ok && j != 0 && j != a.Wg - 1;
       }
       dok[j] = ok;
       const int cchunk = min(chunk, a.co_chunks - 1);
@@ -1858,9 +1864,9 @@ struct WgRowsPlan {
   size_t part_bytes = 0, bpart_bytes = 0, lds_bytes = 0;
 };
 
-WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W) {
+WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   WgRowsPlan p;
-  p.geom = conv_geom(B, H, W);
+  p.geom = conv_geom(B, H, W, layout);
   p.ci_chunks = int(ceil_div(Cin, kKStep));
   p.co_chunks = int(ceil_div(Cout, kKStep));
   p.ci_pad = p.ci_chunks * kKStep;
@@ -2062,21 +2068,21 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
                                         stream);
 }
 
-size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W) {
-  if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1) return 0;
-  const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W);
+size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W, int layout) {
+  if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1 || (layout != kLayoutRef && layout != kLayoutTight)) return 0;
+  const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W, layout);
   return p.part_bytes + p.bpart_bytes;
 }
 
 int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_t* gw, uint16_t* gb, int B,
-                                 int Cin, int Cout, int H, int W, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 int Cin, int Cout, int H, int W, int layout, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   if (!shape_ok("xdna_conv3x3_wgrad_rows_bf16", B, Cin, Cout, H, W)) return -1;
-  if (!xp || !dp || !gw) {
-    set_error("xdna_conv3x3_wgrad_rows_bf16: null operand");
+  if (!xp || !dp || !gw || (layout != kLayoutRef && layout != kLayoutTight)) {
+    set_error("xdna_conv3x3_wgrad_rows_bf16: null operand or unknown layout");
     return -1;
   }
-  const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W);
+  const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W, layout);
   if (!workspace || workspace_bytes < p.part_bytes + p.bpart_bytes) {
     set_error("xdna_conv3x3_wgrad_rows_bf16: workspace too small");
     return -1;
@@ -2102,6 +2108,7 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
   a.wp = p.geom.st.wp;
   a.S = p.geom.st.S;
   a.Wg = p.geom.st.Wg;
+  a.lead = p.geom.st.lead;
   a.img = p.geom.img;
   a.m_total = p.geom.m_total;
   a.ktiles = p.ktiles;
@@ -2171,6 +2178,16 @@ int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_
                            uint16_t* y, int B, int cin, int cout, int H, int W, void* stream) {
   if (!shape_ok("xdna_conv3x3_rows_bf16", B, cin, cout, H, W)) return -1;
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream);
+}
+
+int xdna_conv3x3_layout_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                  int B, int cin, int cout, int H, int W, int layout, void* stream) {
+  if (!shape_ok("xdna_conv3x3_layout_rows_bf16", B, cin, cout, H, W)) return -1;
+  if (layout != kLayoutRef && layout != kLayoutTight) {
+    set_error("xdna_conv3x3_layout_rows_bf16: unknown layout");
+    return -1;
+  }
+  return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout);
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {

@@ -9,6 +9,9 @@
 //   the tail of the last group are never written (the caller zero-fills once).
 //   raw output rows [p][128]: output pixel (y, t) of virtual image vb sits at row
 //   (vb*(H+2) + y)*wp + first + t, first = 0 (S == 1) or 1 (strips).
+// The tight layout (images wider than 36 as strips of up to 36 columns with no zero
+// columns: wp = Wg, data column j at row position j) is packed by the same kernels with
+// the row position of data column 0 (`lead`) as a parameter.
 //
 // Both kernels are HBM-bound byte moves.  One thread per packed row (pixel x chunk):
 // consecutive threads take consecutive image columns, so each of the (up to) 64
@@ -23,7 +26,7 @@ namespace {
 template <bool kVecStore>
 __global__ __launch_bounds__(256) void pack_rows_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int C, int H, int W, int S,
-    int So, int Wg, int wp, int halo_zero, int chunks, int g0, int ng, int v0, int64_t plo,
+    int So, int Wg, int wp, int lead, int halo_zero, int chunks, int g0, int ng, int v0, int64_t plo,
     int64_t phi, int64_t n_threads) {
   int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= n_threads) return;
@@ -38,7 +41,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
   const int b = vb / S, s = vb % S;
   const int x = (S == 1 ? 0 : s * So - 1) + j;  // source column of data column j
   if (x < 0 || x >= W) return;
-  const int64_t p = (int64_t(vb) * (H + 2) + y + 1) * wp + 1 + j;
+  const int64_t p = (int64_t(vb) * (H + 2) + y + 1) * wp + lead + j;
   if (p < plo || p >= phi) return;
   const int64_t g = p / kGroupOutRows;
   const int r = int(p - g * kGroupOutRows);
@@ -113,7 +116,7 @@ __device__ inline void put_row_piece(uint16_t* __restrict__ dst, int64_t p, int 
 template <int VP, bool kDense>
 __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int C, int H, int W, int S,
-    int So, int Wg, int wp, int halo_zero, int chunks, int g0, int ng, int b0, int64_t plo,
+    int So, int Wg, int wp, int lead, int halo_zero, int chunks, int g0, int ng, int b0, int64_t plo,
     int64_t phi, int R, int ybl, int nimg, int64_t tail0) {
   extern __shared__ __attribute__((aligned(16))) uint16_t tile[];
   int bid = blockIdx.x;
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
       const int rem = opix - s * (grows * wp);
       const int gr = rem / wp, gx = rem - gr * wp;
       const int gy = gy_lo + gr;
-      const int j = gx - 1;
+      const int j = gx - lead;
       const int x = (S == 1 ? 0 : s * So - 1) + j;
       const bool zero_col = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
       uint4 v = make_uint4(0, 0, 0, 0);
@@ -223,7 +226,7 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
     const int yy = rem / Wg, j = rem - yy * Wg;
     const int x = (S == 1 ? 0 : s * So - 1) + j;  // source column of data column j
     if (x < 0 || x >= W) continue;                // no source pixel: left as the caller's zero fill
-    const int64_t p = ((int64_t(b) * S + s) * (H + 2) + y0 + yy + 1) * wp + 1 + j;
+    const int64_t p = ((int64_t(b) * S + s) * (H + 2) + y0 + yy + 1) * wp + lead + j;
     if (p < plo || p >= phi) continue;
     const int64_t g = p / kGroupOutRows;
     const int r = int(p - g * kGroupOutRows);
@@ -247,6 +250,13 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
       }
     }
   }
+}
+
+// Zero fill of n 16-byte pieces (a kernel, not a memset, so that graph capture records a
+// kernel node).
+__global__ __launch_bounds__(256) void zero16_kernel(uint4* __restrict__ dst, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+    dst[i] = make_uint4(0, 0, 0, 0);
 }
 
 template <bool kVecLoad>
@@ -293,15 +303,17 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
                 int S, int So, int halo_zero, int chunks, int g0, int ng, void* stream,
-                bool dense = false) {
+                bool dense = false, int layout = kLayoutRef) {
   if (B < 0 || C < 0 || H < 0 || W < 0 || chunks < 0 || S < 1 || g0 < 0 || ng < 0 ||
       (S > 1 && So < 1)) {
     set_error(std::string(what) + ": invalid geometry");
     return -1;
   }
   if (B == 0 || C == 0 || H == 0 || W == 0 || chunks == 0 || ng == 0) return 0;
+  const bool tight = layout == kLayoutTight && S > 1;
   const int Wg = S == 1 ? W : So + 2;
-  const int wp = Wg + 2;
+  const int wp = tight ? Wg : Wg + 2;
+  const int lead = tight ? 0 : 1;
   const int64_t Bv = int64_t(B) * S;
   const int64_t img = int64_t(H + 2) * wp;
   const int64_t plo = int64_t(g0) * kGroupOutRows;
@@ -341,7 +353,7 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
     const dim3 grid{unsigned(blocks)};
     hipStream_t st = as_stream(stream);
 #define XDNA_PACK_LAUNCH(vp, dn)                                                                  \
-  pack_rows_lds_kernel<vp, dn><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, halo_zero, \
+  pack_rows_lds_kernel<vp, dn><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, lead, halo_zero, \
                                                       chunks, g0, ng, int(b0), plo, phi, R, ybl,   \
                                                       int(nimg), tail0)
     if (dense) {
@@ -361,10 +373,10 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
   const int64_t blocks = ceil_div(n, threads);
   if (aligned16(dst))
     pack_rows_kernel<true><<<dim3(unsigned(blocks)), threads, 0, as_stream(stream)>>>(
-        src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks, g0, ng, int(v0), plo, phi, n);
+        src, dst, C, H, W, S, So, Wg, wp, lead, halo_zero, chunks, g0, ng, int(v0), plo, phi, n);
   else
     pack_rows_kernel<false><<<dim3(unsigned(blocks)), threads, 0, as_stream(stream)>>>(
-        src, dst, C, H, W, S, So, Wg, wp, halo_zero, chunks, g0, ng, int(v0), plo, phi, n);
+        src, dst, C, H, W, S, So, Wg, wp, lead, halo_zero, chunks, g0, ng, int(v0), plo, phi, n);
   return check_launch(what);
 }
 
@@ -435,6 +447,37 @@ int xdna_conv3x3w_pack_input_dense_bf16(const uint16_t* src, uint16_t* dst, int 
   const ConvGeom cg = conv_geom(B, H, W);
   return pack_launch("xdna_conv3x3w_pack_input_dense_bf16", src, dst, B, C, H, W, cg.st.S, cg.st.So, 0,
                      int(ceil_div(C, kKStep)), 0, cg.groups, stream, /*dense=*/true);
+}
+
+size_t xdna_conv3x3_layout_packed_bytes(int B, int C, int H, int W, int layout) {
+  if (B < 1 || C < 1 || H < 1 || W < 1 || (layout != kLayoutRef && layout != kLayoutTight)) return 0;
+  const ConvGeom cg = conv_geom(B, H, W, layout);
+  return size_t(cg.groups) * size_t(ceil_div(C, kKStep)) * kGroupRows * kKStep * 2;
+}
+
+int xdna_conv3x3_layout_pack_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W, int layout,
+                                  void* stream) {
+  if (B < 1 || C < 1 || H < 1 || W < 1 || (layout != kLayoutRef && layout != kLayoutTight) || !src || !dst) {
+    set_error("xdna_conv3x3_layout_pack_bf16: invalid arguments");
+    return -1;
+  }
+  if (!aligned16(dst)) {
+    set_error("xdna_conv3x3_layout_pack_bf16: the destination must be 16-byte aligned");
+    return -1;
+  }
+  const ConvGeom cg = conv_geom(B, H, W, layout);
+  const int chunks = int(ceil_div(C, kKStep));
+  if (W <= kMaxTilePix)
+    return pack_launch("xdna_conv3x3_layout_pack_bf16", src, dst, B, C, H, W, cg.st.S, cg.st.So, 0, chunks, 0,
+                       cg.groups, stream, /*dense=*/true, layout);
+  // wider rows than the LDS tile: zero fill, then the real pixels
+  const int64_t n16 = int64_t(cg.groups) * chunks * kGroupRows * kKStep * 2 / 16;
+  if (!admit_launch("xdna_conv3x3_layout_pack_bf16")) return -1;
+  zero16_kernel<<<unsigned(std::min<int64_t>(ceil_div(n16, 256), 16384)), 256, 0, as_stream(stream)>>>(
+      reinterpret_cast<uint4*>(dst), n16);
+  if (check_launch("xdna_conv3x3_layout_pack_bf16")) return -1;
+  return pack_launch("xdna_conv3x3_layout_pack_bf16", src, dst, B, C, H, W, cg.st.S, cg.st.So, 0, chunks, 0,
+                     cg.groups, stream, /*dense=*/false, layout);
 }
 
 int xdna_conv3x3w_unpack_output_bf16(const uint16_t* c, uint16_t* dst, int B, int H, int W,

@@ -44,6 +44,11 @@ std::atomic<int> g_gconv_mode{[] {
   const int v = e ? std::atoi(e) : 1;
   return v < 0 || v > 2 ? 1 : v;
 }()};
+std::atomic<int> g_conv_layout{[] {
+  const char* e = std::getenv("XDNA_CONV_LAYOUT");
+  const int v = e ? std::atoi(e) : 1;
+  return v < 0 || v > 1 ? 1 : v;
+}()};
 std::atomic<int> g_wgrad_form{[] {
   const char* e = std::getenv("XDNA_WGRAD_FORM");
   const int v = e ? std::atoi(e) : 0;
@@ -610,6 +615,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     g_wgrad_form.store(m);
   });
   mod.def("wgrad_form", [] { return g_wgrad_form.load(); });
+  mod.def("set_conv_layout", [](int m) {
+    TORCH_CHECK(m >= 0 && m <= 1, "xdna: conv layout must be 0 or 1");
+    g_conv_layout.store(m);
+  });
+  mod.def("conv_layout", [] { return g_conv_layout.load(); });
   mod.def("mapped_cpu_stats", [] { return stats_dict(path_stats()); });
   mod.def("reset_mapped_cpu_stats", [] {
     std::lock_guard<std::mutex> lock(stats_mu());

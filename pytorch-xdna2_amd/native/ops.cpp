@@ -170,41 +170,28 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
 
 // The packed row layout of an NCHW bf16 tensor ([groups][chunks][2126 rows][64 channels],
 // images wider than 36 as strips), as the rows conv kernels and the rows weight gradient
-// read it.
-at::Tensor pack_rows(const at::Tensor& src) {
+// read it: the tight layout (strips of up to 36 columns without zero columns) unless
+// XDNA_CONV_LAYOUT / set_conv_layout asks for the reference's.
+at::Tensor pack_rows(const at::Tensor& src, int layout) {
   const int64_t B = src.size(0), cin = src.size(1), H = src.size(2), W = src.size(3);
   at::Tensor x = src.contiguous();
-  void* st = current_stream();
-  // The packed input is transient: the dense pack writes every element (zeros in the
-  // borders and padded channels), so a recycled allocation needs no fill.  (The reference
-  // keeps a pool of zero-filled buffers per shape, torch_xdna_device.cpp:1848-1872.)
-  const size_t pbytes = xdna_conv3x3w_packed_bytes(int(B), int(cin), int(H), int(W));
+  // The packed input is transient: the pack writes every element (zeros in the borders
+  // and padded channels), so a recycled allocation needs no fill.  (The reference keeps a
+  // pool of zero-filled buffers per shape, torch_xdna_device.cpp:1848-1872.)
+  const size_t pbytes = xdna_conv3x3_layout_packed_bytes(int(B), int(cin), int(H), int(W), layout);
+  TORCH_CHECK(pbytes > 0, "xdna conv: invalid packed layout");
   at::Tensor packed = alloc_bytes(pbytes);
-  int64_t geo[7];
-  check_abi(xdna_conv3x3w_geometry(int(B), int(cin), int(H), int(W), geo), "conv geometry");
-  {
-    const double bytes = 2.0 * double(x.numel()) + double(geo[4]) * double(geo[5]) * 2126.0 * 64.0 * 2.0;
-    KernelTimer kt("conv3x3w_pack", bytes);
-    if (W <= 256) {
-      check_abi(xdna_conv3x3w_pack_input_dense_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
-                                                    static_cast<uint16_t*>(packed.data_ptr()), int(B), int(cin),
-                                                    int(H), int(W), st),
-                "conv pack");
-    } else {
-      // wider than one LDS tile row: fill, then pack the real pixels
-      cuda_alias(packed).zero_();
-      check_abi(xdna_conv3x3w_pack_input_strips_range_bf16(
-                    static_cast<const uint16_t*>(x.const_data_ptr()), static_cast<uint16_t*>(packed.data_ptr()),
-                    int(B), int(cin), int(H), int(W), int(geo[0]), int(geo[1]), 0, int(geo[5]), 0, int(geo[4]), st),
-                "conv pack");
-    }
-  }
+  KernelTimer kt("conv3x3w_pack", 2.0 * double(x.numel()) + double(pbytes));
+  check_abi(xdna_conv3x3_layout_pack_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                          static_cast<uint16_t*>(packed.data_ptr()), int(B), int(cin), int(H),
+                                          int(W), layout, current_stream()),
+            "conv pack");
   return packed;
 }
 
 // Runs the conv of a packed input (NCHW shape `src`, cin channels) with `w` (forward: w as
 // given; dgrad: flip+swap) into a new NCHW tensor of cout channels.
-at::Tensor hip_conv_packed(const at::Tensor& packed, at::IntArrayRef src, const at::Tensor& w,
+at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef src, const at::Tensor& w,
                            const at::Tensor* bias, bool dgrad) {
   const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
@@ -240,17 +227,18 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, at::IntArrayRef src, const 
   if (bias) bc = bias->contiguous();
   const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
   KernelTimer kt(dgrad ? "conv3x3_rows.dgrad" : "conv3x3_rows.fwd", flops);
-  check_abi(xdna_conv3x3_rows_bf16(static_cast<const uint16_t*>(packed.const_data_ptr()),
-                                   static_cast<const uint16_t*>(wt.const_data_ptr()),
-                                   bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
-                                   static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout),
-                                   int(H), int(W), st),
+  check_abi(xdna_conv3x3_layout_rows_bf16(static_cast<const uint16_t*>(packed.const_data_ptr()),
+                                          static_cast<const uint16_t*>(wt.const_data_ptr()),
+                                          bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                                          static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout),
+                                          int(H), int(W), layout, st),
             "conv rows");
   return out;
 }
 
 at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor* bias, bool dgrad) {
-  return hip_conv_packed(pack_rows(src), src.sizes(), w, bias, dgrad);
+  const int layout = g_conv_layout.load();
+  return hip_conv_packed(pack_rows(src, layout), layout, src.sizes(), w, bias, dgrad);
 }
 
 // Packed inputs of forward convs kept for the rows weight gradient of the same layer, so
@@ -262,6 +250,7 @@ struct PackedInput {
   c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
   int64_t offset = 0, version = 0;
   std::vector<int64_t> sizes, strides;
+  int layout = 0;
   at::Tensor packed;
 };
 
@@ -277,19 +266,19 @@ PackedInputCache& packed_input_cache() {
   return *c;
 }
 
-bool same_input(const PackedInput& e, const at::Tensor& x) {
-  if (e.offset != x.storage_offset() || e.sizes != x.sizes().vec() || e.strides != x.strides().vec() ||
+bool same_input(const PackedInput& e, const at::Tensor& x, int layout) {
+  if (e.layout != layout || e.offset != x.storage_offset() || e.sizes != x.sizes().vec() || e.strides != x.strides().vec() ||
       e.version != int64_t(x.unsafeGetTensorImpl()->version_counter().current_version()))
     return false;
   auto live = e.storage.lock();
   return live && live.get() == x.storage().unsafeGetStorageImpl();
 }
 
-void remember_packed_input(const at::Tensor& x, const at::Tensor& packed) {
+void remember_packed_input(const at::Tensor& x, const at::Tensor& packed, int layout) {
   PackedInputCache& c = packed_input_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   for (auto it = c.entries.begin(); it != c.entries.end();) {
-    if (it->storage.expired() || same_input(*it, x)) {
+    if (it->storage.expired() || same_input(*it, x, layout)) {
       c.bytes -= size_t(it->packed.nbytes());
       it = c.entries.erase(it);
     } else {
@@ -302,6 +291,7 @@ void remember_packed_input(const at::Tensor& x, const at::Tensor& packed) {
   e.version = int64_t(x.unsafeGetTensorImpl()->version_counter().current_version());
   e.sizes = x.sizes().vec();
   e.strides = x.strides().vec();
+  e.layout = layout;
   e.packed = packed;
   c.bytes += size_t(packed.nbytes());
   c.entries.push_back(std::move(e));
@@ -311,11 +301,11 @@ void remember_packed_input(const at::Tensor& x, const at::Tensor& packed) {
   }
 }
 
-at::Tensor take_packed_input(const at::Tensor& x) {
+at::Tensor take_packed_input(const at::Tensor& x, int layout) {
   PackedInputCache& c = packed_input_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   for (auto it = c.entries.begin(); it != c.entries.end(); ++it) {
-    if (!same_input(*it, x)) continue;
+    if (!same_input(*it, x, layout)) continue;
     at::Tensor p = it->packed;
     c.bytes -= size_t(p.nbytes());
     c.entries.erase(it);
@@ -340,11 +330,12 @@ bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W);
 // Forward of a 3x3 / stride-1 conv; the packed input is kept when this layer's weight
 // gradient will take the rows form.
 at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias) {
-  at::Tensor packed = pack_rows(input);
+  const int layout = g_conv_layout.load();
+  at::Tensor packed = pack_rows(input, layout);
   if (g_mode.load() >= 2 && at::GradMode::is_enabled() && weight.requires_grad() &&
       wgrad_rows_pick(input.size(1), weight.size(0), input.size(3)))
-    remember_packed_input(input, packed);
-  return hip_conv_packed(packed, input.sizes(), weight, bias, false);
+    remember_packed_input(input, packed, layout);
+  return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -494,17 +485,18 @@ void hip_wgrad(const at::Tensor& input, const at::Tensor& dy, at::Tensor& gw, at
 // Weight gradient (+ bias gradient) on the packed row layout: x packed here, dY in the
 // packed form its input gradient already read (`dpacked`), so neither is copied
 // channel-major.  The packs are snapshots, as in the channel-major form.
-void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int64_t Cout, at::Tensor& gw,
+void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int layout, int64_t Cout, at::Tensor& gw,
                     at::Tensor* gb) {
   const int64_t B = input.size(0), Cin = input.size(1), H = input.size(2), W = input.size(3);
-  at::Tensor xpacked = take_packed_input(input);
+  at::Tensor xpacked = take_packed_input(input, layout);
   if (xpacked.defined()) {
     ScopedCount sk("hip_conv3x3.dw_rows.kept_pack");
   } else {
-    xpacked = pack_rows(input);
+    xpacked = pack_rows(input, layout);
   }
   void* st = current_stream();
-  const size_t wsb = xdna_conv3x3_wgrad_rows_workspace_bytes(int(B), int(Cin), int(Cout), int(H), int(W));
+  const size_t wsb =
+      xdna_conv3x3_wgrad_rows_workspace_bytes(int(B), int(Cin), int(Cout), int(H), int(W), layout);
   at::Tensor ws = alloc_bytes(wsb);
   gw = empty_xdna({Cout, Cin, 3, 3}, at::kBFloat16);
   if (gb) *gb = empty_xdna({Cout}, at::kBFloat16);
@@ -513,7 +505,7 @@ void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int64_t 
                                          static_cast<const uint16_t*>(dpacked.const_data_ptr()),
                                          static_cast<uint16_t*>(gw.data_ptr()),
                                          gb ? static_cast<uint16_t*>(gb->data_ptr()) : nullptr, int(B), int(Cin),
-                                         int(Cout), int(H), int(W), ws.data_ptr(), wsb, st),
+                                         int(Cout), int(H), int(W), layout, ws.data_ptr(), wsb, st),
             "conv wgrad rows");
 }
 
@@ -559,18 +551,19 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   const bool dw = hip && mask[1] && g_mode.load() >= 2;
   const bool dw_rows = dw && wgrad_rows_pick(input.size(1), weight.size(0), input.size(3));
   // dY packed once: the input gradient's conv and the rows weight gradient read it
+  const int layout = g_conv_layout.load();
   at::Tensor gop;
-  if (hip && (mask[0] || dw_rows)) gop = pack_rows(go);
+  if (hip && (mask[0] || dw_rows)) gop = pack_rows(go, layout);
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
-    gi = hip_conv_packed(gop, go.sizes(), weight, nullptr, true);
+    gi = hip_conv_packed(gop, layout, go.sizes(), weight, nullptr, true);
     mask[0] = false;
   }
   if (dw) {
     ScopedCount sc("hip_conv3x3.dw.run");
     if (dw_rows) {
       ScopedCount sr("hip_conv3x3.dw_rows.run");
-      hip_wgrad_rows(input, gop, weight.size(0), gw, mask[2] ? &gb : nullptr);
+      hip_wgrad_rows(input, gop, layout, weight.size(0), gw, mask[2] ? &gb : nullptr);
     } else {
       hip_wgrad(input, go, gw, mask[2] ? &gb : nullptr);
     }

@@ -48,6 +48,8 @@ extern std::atomic<int> g_mode;
 extern std::atomic<int> g_gconv_mode;
 // 3x3 weight gradient: 0 (default) per layer shape, 1 channel-major form, 2 rows form.
 extern std::atomic<int> g_wgrad_form;
+// Row layout of the 3x3 conv operands: 1 (default) tight strips, 0 the reference's layout.
+extern std::atomic<int> g_conv_layout;
 
 // Per-path counters (the reference's ScopedMappedCpu, torch_xdna_device.cpp:1470-1521).
 void count_call(const char* name, int64_t ns);

@@ -8,6 +8,7 @@ from .device import (
     async_dw_stats,
     autotune_result,
     bo_handle,
+    conv_layout,
     coherency_state,
     empty_cache,
     fallback_stats,
@@ -21,6 +22,7 @@ from .device import (
     reset_fallback_stats,
     reset_mapped_cpu_stats,
     set_general_conv_mode,
+    set_conv_layout,
     set_npu_mode,
     set_wgrad_form,
     synchronize,
@@ -50,6 +52,8 @@ __all__ = [
     "set_general_conv_mode",
     "general_conv_mode",
     "set_wgrad_form",
+    "set_conv_layout",
+    "conv_layout",
     "wgrad_form",
     "wait_for_builds",
     "reset_fallback_stats",

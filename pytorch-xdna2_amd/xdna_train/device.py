@@ -349,6 +349,21 @@ def wgrad_form() -> int:
     return int(_C.wgrad_form())
 
 
+def set_conv_layout(layout: int) -> None:
+    """Row layout of the packed operands of the 3x3 convs: 1 (default) tight strips
+    (images wider than 36 as strips of up to 36 columns without zero columns), 0 the
+    reference's conv3x3w layout (strips of up to 34 columns between zero columns).  The
+    results agree to the conv tolerance (the sums run in other orders).  XDNA_CONV_LAYOUT
+    sets the initial value.  No reference counterpart."""
+    register_xdna_device()
+    _C.set_conv_layout(int(layout))
+
+
+def conv_layout() -> int:
+    register_xdna_device()
+    return int(_C.conv_layout())
+
+
 def wait_for_builds(timeout: float | None = None) -> bool:
     """Kernels are compiled ahead of time: nothing is ever pending."""
     del timeout

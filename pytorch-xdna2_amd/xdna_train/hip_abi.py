@@ -21,6 +21,10 @@ D = ctypes.c_double
 PP = ctypes.POINTER(ctypes.c_void_p)
 PL = ctypes.POINTER(ctypes.c_int64)
 
+# row layouts of the packed conv operands (XDNA_CONV3X3_LAYOUT_*)
+LAYOUT_REF = 0
+LAYOUT_TIGHT = 1
+
 # name -> (restype, argtypes); every function declared in include/xdna_hip.h.
 SIGNATURES = {
     "xdna_hip_last_error": (ctypes.c_char_p, []),
@@ -70,8 +74,8 @@ SIGNATURES = {
     "xdna_conv2d_set_variant": (I, [I]),
     "xdna_subsample2_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv3x3_prepare_weights_both_bf16": (I, [P, P, P, I, I, P]),
-    "xdna_conv3x3_wgrad_rows_workspace_bytes": (Z, [I, I, I, I, I]),
-    "xdna_conv3x3_wgrad_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, P, Z, P]),
+    "xdna_conv3x3_wgrad_rows_workspace_bytes": (Z, [I, I, I, I, I, I]),
+    "xdna_conv3x3_wgrad_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, I, P, Z, P]),
     "xdna_dilate2_bf16": (I, [P, P, L, I, I, P]),
     "xdna_upsample_nearest2x_bwd_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_dgrad_bf16": (I, [P, P, P] + [I] * 11 + [P]),
@@ -92,6 +96,9 @@ SIGNATURES = {
     "xdna_conv3x3_prepare_weights_bf16": (I, [P, P, I, I, I, P]),
     "xdna_conv3x3_set_rows_variant": (I, [I]),
     "xdna_conv3x3_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "xdna_conv3x3_layout_packed_bytes": (Z, [I, I, I, I, I]),
+    "xdna_conv3x3_layout_pack_bf16": (I, [P, P, I, I, I, I, I, P]),
+    "xdna_conv3x3_layout_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_gemm_set_variant": (I, [I]),

@@ -13,6 +13,7 @@ reduction is fixed-order).
 import numpy as np
 import pytest
 
+import layout_util
 import oracle
 from gpu_util import check_bf16, dev, dev_zeros, host, ptr, stream
 
@@ -124,33 +125,76 @@ def test_wgrad(hip, shape):
     check_bf16(host(gb2), ref_b, what=f"bias grad kernel {shape}")
 
 
-@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_rows(hip, shape):
+# shapes whose layouts differ (W > 36), one where they agree, and one past the LDS tile
+LAYOUT_SHAPES = [(1, 64, 64, 8, 40), (1, 128, 256, 18, 72), (2, 256, 64, 5, 37), (1, 64, 384, 6, 40),
+                 (1, 32, 48, 5, 110), (1, 16, 24, 3, 300), (2, 64, 64, 12, 12)]
+
+
+def _pack(hip, bits, layout):
+    """bits packed on the device in `layout` into a buffer pre-filled with a non-zero pattern."""
+    B, C, H, W = bits.shape
+    n = hip.xdna_conv3x3_layout_packed_bytes(B, C, H, W, layout)
+    assert n > 0
+    buf = dev(np.full((n // 2,), 0xBEEF, np.uint16))
+    assert hip.xdna_conv3x3_layout_pack_bf16(ptr(dev(bits)), ptr(buf), B, C, H, W, layout, stream()) == 0
+    return buf
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("shape", LAYOUT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_layout_pack(hip, shape, layout):
+    """Both row layouts written whole (zeros included) and bit-exact against the host
+    construction (itself pinned to the oracle's reference pack on the CPU)."""
+    B, Cin, _, H, W = shape
+    print(f"layout pack {shape} layout {layout}", flush=True)
+    x = _data(*shape, seed=sum(shape) + 5)[0]
+    got = host(_pack(hip, x, layout)).reshape(-1)
+    np.testing.assert_array_equal(got, layout_util.pack_expected(x, layout).reshape(-1))
+    assert hip.xdna_conv3x3_layout_packed_bytes(B, Cin, H, W, 2) == 0
+
+
+@pytest.mark.parametrize("variant", VARIANTS, indirect=True, ids=lambda v: f"v{v}")
+@pytest.mark.parametrize("shape", LAYOUT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_forward_tight_layout(hip, shape, variant):
+    """The rows kernels on the tight layout (every variant) vs the oracle."""
+    B, Cin, Cout, H, W = shape
+    print(f"conv fwd tight {shape} variant {variant}", flush=True)
+    x, w, b, _ = _data(*shape, seed=sum(shape) + 6)
+    xp = _pack(hip, x, 1)
+    wt = _ws(hip.xdna_conv3x3_prepared_weight_bytes(Cin, Cout))
+    assert hip.xdna_conv3x3_prepare_weights_bf16(ptr(dev(w)), ptr(wt), Cout, Cin, 0, stream()) == 0
+    y = dev_zeros((B, Cout, H, W))
+    assert hip.xdna_conv3x3_layout_rows_bf16(ptr(xp), ptr(wt), ptr(dev(b)), ptr(y), B, Cin, Cout, H, W, 1,
+                                             stream()) == 0
+    check_bf16(host(y), oracle.conv3x3_fwd(x, w, b), what=f"fwd tight {shape}")
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("shape", SHAPES + LAYOUT_SHAPES[4:6], ids=lambda s: "x".join(map(str, s)))
+def test_wgrad_rows(hip, shape, layout):
     """Weight gradient from the packed row layouts (x and dY packed as the forward and
     input-gradient convs pack them) vs the oracle; run-to-run bit equality."""
     B, Cin, Cout, H, W = shape
-    print(f"conv wgrad rows {shape}", flush=True)
+    print(f"conv wgrad rows {shape} layout {layout}", flush=True)
     x, _, _, dy = _data(*shape, seed=sum(shape) + 3)
     ref_w, ref_b = oracle.conv3x3_wgrad(x, dy)
-    xp = _ws(hip.xdna_conv3x3w_packed_bytes(B, Cin, H, W))
-    dp = _ws(hip.xdna_conv3x3w_packed_bytes(B, Cout, H, W))
-    assert hip.xdna_conv3x3w_pack_input_dense_bf16(ptr(dev(x)), ptr(xp), B, Cin, H, W, stream()) == 0
-    assert hip.xdna_conv3x3w_pack_input_dense_bf16(ptr(dev(dy)), ptr(dp), B, Cout, H, W, stream()) == 0
-    ws_bytes = hip.xdna_conv3x3_wgrad_rows_workspace_bytes(B, Cin, Cout, H, W)
+    xp = _pack(hip, x, layout)
+    dp = _pack(hip, dy, layout)
+    ws_bytes = hip.xdna_conv3x3_wgrad_rows_workspace_bytes(B, Cin, Cout, H, W, layout)
     ws = _ws(ws_bytes)
     gw = dev_zeros((Cout, Cin, 3, 3))
     gb = dev_zeros((Cout,))
-    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw), ptr(gb), B, Cin, Cout, H, W, ptr(ws),
-                                            ws_bytes, stream()) == 0
+    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw), ptr(gb), B, Cin, Cout, H, W, layout,
+                                            ptr(ws), ws_bytes, stream()) == 0
     got_w = host(gw)
     check_bf16(got_w, ref_w, what=f"wgrad rows {shape}")
     check_bf16(host(gb), ref_b, what=f"bias grad rows {shape}")
     gw2 = dev_zeros((Cout, Cin, 3, 3))
-    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, ptr(ws),
-                                            ws_bytes, stream()) == 0
+    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, layout,
+                                            ptr(ws), ws_bytes, stream()) == 0
     np.testing.assert_array_equal(host(gw2), got_w)
-    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, ptr(ws),
-                                            ws_bytes - 1, stream()) == -1
+    assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, layout,
+                                            ptr(ws), ws_bytes - 1, stream()) == -1
 
 
 def test_workspace_too_small_is_an_error(hip):
