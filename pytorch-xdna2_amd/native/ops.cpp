@@ -302,6 +302,7 @@ void remember_packed_input(const at::Tensor& x, const at::Tensor& packed, int la
 }
 
 at::Tensor take_packed_input(const at::Tensor& x, int layout) {
+  if (x.is_inference()) return at::Tensor();
   PackedInputCache& c = packed_input_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   for (auto it = c.entries.begin(); it != c.entries.end(); ++it) {
@@ -327,12 +328,14 @@ namespace {
 
 bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W);
 
-// Forward of a 3x3 / stride-1 conv; the packed input is kept when this layer's weight
-// gradient will take the rows form.
+// Forward of a 3x3 / stride-1 conv; the packed input is kept when the weight is trainable
+// and its gradient takes the rows form (whether or not autograd records this call: a
+// caller may run the aten backward itself).  A kept pack whose backward never comes goes
+// when its input dies.  Inference tensors keep nothing (they have no version counter).
 at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias) {
   const int layout = g_conv_layout.load();
   at::Tensor packed = pack_rows(input, layout);
-  if (g_mode.load() >= 2 && at::GradMode::is_enabled() && weight.requires_grad() &&
+  if (g_mode.load() >= 2 && weight.requires_grad() && !weight.is_inference() && !input.is_inference() &&
       wgrad_rows_pick(input.size(1), weight.size(0), input.size(3)))
     remember_packed_input(input, packed, layout);
   return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false);
@@ -509,16 +512,15 @@ void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int layo
             "conv wgrad rows");
 }
 
-// Which weight-gradient form a 3x3 layer takes (measured over the 36 sweep shapes, packs
-// included): the rows form wherever the image fits one strip, and for wider images with
-// at most 128 x 128 channels; wider images with more channels take the channel-major form,
-// since the rows form also multiplies the strip halo rows (17% of the rows at 72 x 72).
-// Images wider than 142 exceed the channel-major form's window and always take the rows form.
+// Which weight-gradient form a 3x3 layer takes: the rows form (its x operand is the
+// forward's kept pack, its dY operand the input gradient's) unless the channel-major form
+// is asked for; on the tight layout the rows form measured faster on all 36 sweep shapes
+// (6.7 vs 7.8 ms per sweep step, the channel-major copies included).  Images wider than
+// 142 exceed the channel-major form's window and always take the rows form.
 bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W) {
-  const int form = g_wgrad_form.load();
-  if (W > 142 || form == 2) return true;
-  if (form == 1) return false;
-  return W <= 36 || Cin * Cout <= 128 * 128;
+  (void)Cin;
+  (void)Cout;
+  return W > 142 || g_wgrad_form.load() != 1;
 }
 
 std::atomic<int64_t> g_dw_jobs{0};

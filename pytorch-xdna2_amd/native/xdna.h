@@ -46,7 +46,7 @@ at::Tensor xdna_from_cuda(const at::Tensor& t);
 // (xdna_train/device.py:526-650).
 extern std::atomic<int> g_mode;
 extern std::atomic<int> g_gconv_mode;
-// 3x3 weight gradient: 0 (default) per layer shape, 1 channel-major form, 2 rows form.
+// 3x3 weight gradient: 0 (default) and 2 the rows form, 1 the channel-major form.
 extern std::atomic<int> g_wgrad_form;
 // Row layout of the 3x3 conv operands: 1 (default) tight strips, 0 the reference's layout.
 extern std::atomic<int> g_conv_layout;

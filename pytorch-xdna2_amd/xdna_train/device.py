@@ -335,9 +335,9 @@ def general_conv_mode() -> int:
 
 
 def set_wgrad_form(form: int) -> None:
-    """Weight gradient of the 3x3 / stride-1 convs: 0 (default) chosen per layer shape,
-    1 the channel-major form (x and dY copied channel-major), 2 the packed-rows form (dY
-    read in the packed form its input gradient used, x packed the same way).  Both sum in
+    """Weight gradient of the 3x3 / stride-1 convs: 0 (default) and 2 the packed-rows
+    form (dY read in the packed form its input gradient used, x in the packed form its
+    forward used), 1 the channel-major form (x and dY copied channel-major).  Both sum in
     fp32 and round once to bf16, in different orders.  Images wider than 142 always take
     the rows form.  XDNA_WGRAD_FORM sets the initial value.  No reference counterpart."""
     register_xdna_device()
