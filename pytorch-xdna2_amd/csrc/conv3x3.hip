@@ -1706,12 +1706,15 @@ struct WgRowsArgs {
 
 typedef short wr_i16x4 __attribute__((ext_vector_type(4)));
 
-// rows q .. q+3 of column c of a row-major LDS tile, as two dwords: in 16-lane group
-// g = lane / 16 (columns +16 (g % 2), rows +8 (g / 2)), lane j supplies (row + j / 4,
-// column + 4 (j % 4)) and every lane receives 4 consecutive rows of its own column
-__device__ inline uint2 wr_tr4(const uint16_t* tile, int pitch, int q, int cb, int lane) {
+// Lane part of a transposing LDS read of a row-major tile: in 16-lane group g = lane / 16
+// (columns +16 (g % 2), rows +8 (g / 2)), lane j supplies (row + j / 4, column + 4 (j % 4)),
+// and every lane receives 4 consecutive rows of its own column as two dwords.
+__device__ inline int wr_lane_off(int pitch, int lane) {
   const int g = lane >> 4, j = lane & 15;
-  const uint16_t* p = tile + (q + 8 * (g >> 1) + (j >> 2)) * pitch + cb + 16 * (g & 1) + 4 * (j & 3);
+  return (8 * (g >> 1) + (j >> 2)) * pitch + 16 * (g & 1) + 4 * (j & 3);
+}
+
+__device__ inline uint2 wr_tr(const uint16_t* p) {
   const wr_i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) wr_i16x4*)(p));
   return __builtin_bit_cast(uint2, v);
 }
@@ -1743,38 +1746,59 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   float bsum = 0.0f;
   const bool do_bias = a.bpart && ci_t == 0 && wn == 0;
 
+  // Per-thread load offsets (elements from the k-tile's base), fixed over the k-tiles.
+  // dY vector j: row i / 16, channels (i % 16) * 8 of the tile's 128; x vector j: window
+  // row i / 8, channels (i % 8) * 8.
+  int d_off[2], d_row[2];
+  bool d_chunk[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = tid + j * 512;
+    const int row = i >> 4, ch = (i >> 3) & 1, piece = i & 7;
+    const int chunk = co0 / 64 + ch;
+    d_chunk[j] = chunk < a.co_chunks;
+    d_row[j] = row;
+    d_off[j] = (min(chunk, a.co_chunks - 1) * kGroupRows + row + a.wp + 1) * kKStep + piece * 8;
+  }
+  int x_off[kWrXv];
+#pragma unroll
+  for (int j = 0; j < kWrXv; ++j) {
+    const int i = min(tid + j * 512, nxv - 1);
+    x_off[j] = (i >> 3) * kKStep + (i & 7) * 8;
+  }
+
   u32x4_t dreg[2];
   u32x4_t xreg[kWrXv];
   bool dok[2];
-  // k-tile kt: group kt / 32, output rows r0 = (kt % 32) * 64 of it
+  // k-tile kt: group kt / 32, output rows (kt % 32) * 64 of it, i.e. global output rows
+  // p = 64 kt + row
   auto load = [&](int kt) {
     const int g = kt >> 5, r0 = (kt & 31) * 64;
+    const int64_t rem = a.m_total - int64_t(kt) * 64;  // rows of this tile before the end
+    // strip halo columns: p % wp from (64 kt) % wp (wave-uniform) plus the row, reduced by
+    // at most three subtractions (strips are at least 21 positions wide)
+    const int base = a.S > 1 ? int((uint32_t(kt) * 64u) % uint32_t(a.wp)) : 0;
+    const uint16_t* db = a.dp + (int64_t(g) * a.co_chunks * kGroupRows + r0) * kKStep;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      // vector i: row i / 16, channels (i % 16) * 8 of the 128
-      const int i = tid + j * 512;
-      const int row = i >> 4, ch = (i >> 3) & 1, piece = i & 7;
-      const int chunk = co0 / 64 + ch;
-      const int64_t p = int64_t(g) * kGroupOutRows + r0 + row;  // output row
-      bool ok = chunk < a.co_chunks && p < a.m_total;
+      bool ok = d_chunk[j] && d_row[j] < rem;
       if (a.S > 1) {
-        // data column of the centre row p + wp + 1 (row position jcol + 1, wrapping to the
+        int jc = base + d_row[j];
+        jc -= jc >= a.wp ? a.wp : 0;
+        jc -= jc >= a.wp ? a.wp : 0;
+        jc -= jc >= a.wp ? a.wp : 0;
+        // data column of the centre row p + wp + 1 (row position jc + 1, wrapping to the
         // next row's position 0)
-        int j = int((p % a.img) % a.wp) + 1 - a.lead;
-        if (j == a.wp) j = 0;
-        ok = ok && j != 0 && j != a.Wg - 1;
+        int dj = jc + 1 - a.lead;
+        dj = dj == a.wp ? 0 : dj;
+        ok = ok && dj != 0 && dj != a.Wg - 1;
       }
       dok[j] = ok;
-      const int cchunk = min(chunk, a.co_chunks - 1);
-      dreg[j] = *reinterpret_cast<const u32x4_t*>(
-          a.dp + ((int64_t(g) * a.co_chunks + cchunk) * kGroupRows + r0 + row + a.wp + 1) * kKStep + piece * 8);
+      dreg[j] = *reinterpret_cast<const u32x4_t*>(db + d_off[j]);
     }
-    const uint16_t* xs = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
+    const uint16_t* xb = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
 #pragma unroll
-    for (int j = 0; j < kWrXv; ++j) {
-      const int i = min(tid + j * 512, nxv - 1);
-      xreg[j] = *reinterpret_cast<const u32x4_t*>(xs + (i >> 3) * kKStep + (i & 7) * 8);
-    }
+    for (int j = 0; j < kWrXv; ++j) xreg[j] = *reinterpret_cast<const u32x4_t*>(xb + x_off[j]);
   };
   auto store = [&](int buf) {
     uint16_t* as = smem + buf * buf_elems;
@@ -1792,6 +1816,12 @@ void wgrad_rows_kernel(WgRowsArgs a) {
     }
   };
 
+  // LDS read bases of this lane: dY rows at + q * kWrA, x rows of kernel row dy at
+  // + dy * wp * kWrX + q * kWrX (q a compile-time row: an immediate offset)
+  const int a_lane = wr_lane_off(kWrA, lane) + wm * 32;
+  const int x_lane = 64 * kWrA + wr_lane_off(kWrX, lane) + wn * 32;
+  const int wrow = a.wp * kWrX;
+
   if (kt0 < kt1) {
     load(kt0);
     store(0);
@@ -1801,12 +1831,13 @@ void wgrad_rows_kernel(WgRowsArgs a) {
     const int cur = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
     if (more) load(kt + 1);
-    const uint16_t* as = smem + cur * buf_elems;
-    const uint16_t* xs = as + 64 * kWrA;
+    const uint16_t* ab = smem + cur * buf_elems + a_lane;
+    const uint16_t* xb0 = smem + cur * buf_elems + x_lane;
+    const uint16_t* xbr[3] = {xb0, xb0 + wrow, xb0 + 2 * wrow};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int q = ks * 16;
-      const uint2 a0 = wr_tr4(as, kWrA, q, wm * 32, lane), a1 = wr_tr4(as, kWrA, q + 4, wm * 32, lane);
+      const uint2 a0 = wr_tr(ab + q * kWrA), a1 = wr_tr(ab + (q + 4) * kWrA);
       const u32x4_t av = {a0.x, a0.y, a1.x, a1.y};
       if (do_bias) {
 #pragma unroll
@@ -1816,11 +1847,12 @@ void wgrad_rows_kernel(WgRowsArgs a) {
       const bf16x8_t af = as_bf16x8(av);
 #pragma unroll
       for (int dy = 0; dy < 3; ++dy) {
-        const int qx = q + dy * a.wp;
-        const uint2 r0 = wr_tr4(xs, kWrX, qx, wn * 32, lane);
-        const uint2 r1 = wr_tr4(xs, kWrX, qx + 4, wn * 32, lane);
-        const uint2 r2 = wr_tr4(xs, kWrX, qx + 8, wn * 32, lane);
+        const uint16_t* xr = xbr[dy] + q * kWrX;
+        const uint2 r0 = wr_tr(xr), r1 = wr_tr(xr + 4 * kWrX);
         const u32x4_t l = {r0.x, r0.y, r1.x, r1.y};
+        // dx = 1, 2: the same 12 rows shifted by one and two (reading the dx = 2 operand
+        // directly instead measured the same)
+        const uint2 r2 = wr_tr(xr + 8 * kWrX);
         u32x4_t s1, s2;
         s1[0] = __builtin_amdgcn_alignbit(r0.y, r0.x, 16);
         s1[1] = __builtin_amdgcn_alignbit(r1.x, r0.y, 16);
@@ -2083,6 +2115,12 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
     return -1;
   }
   const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W, layout);
+  // the kernel's 32-bit row arithmetic and its strip-column reduction (strips of 21 or
+  // more positions)
+  if (int64_t(p.ktiles) * 64 >= (int64_t(1) << 31) || (p.geom.st.S > 1 && p.geom.st.wp < 21)) {
+    set_error("xdna_conv3x3_wgrad_rows_bf16: shape outside the kernel's range");
+    return -1;
+  }
   if (!workspace || workspace_bytes < p.part_bytes + p.bpart_bytes) {
     set_error("xdna_conv3x3_wgrad_rows_bf16: workspace too small");
     return -1;
