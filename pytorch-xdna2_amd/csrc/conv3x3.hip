@@ -1672,6 +1672,12 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
 
 constexpr size_t kMaxWgradLds = 160 * 1024;
 
+// Output rows per k-tile of the rows weight gradient (64 or 128; XDNA_WGRAD_KT).
+std::atomic<int> g_wgrad_rows_kt{[] {
+  const char* e = std::getenv("XDNA_WGRAD_KT");
+  return e && std::atoi(e) == 64 ? 64 : 128;
+}()};
+
 // ---------------------------------------------------------------------------------------
 // Weight gradient on the packed row layout: x and dY as the forward and input-gradient
 // convolutions already pack them ([group][chunk][2126 rows][64 channels], one padded-grid
@@ -1691,7 +1697,9 @@ constexpr size_t kMaxWgradLds = 160 * 1024;
 // (the reference's, or the tight one without zero columns).
 constexpr int kWrA = 128 + 16;   // LDS pitch (elements) of the dY tile: rows 8 banks apart
 constexpr int kWrX = 64 + 16;    // LDS pitch of the x window
-constexpr int kWrXv = 3;         // x-window vectors per thread (8 * (64 + 2*38 + 2) <= 3 * 512)
+// x-window vectors per thread for k-tiles of KT rows (8 * (KT + 2*38 + 2) vectors per window)
+template <int KT>
+constexpr int wr_xv() { return (8 * (KT + 2 * 38 + 2) + 511) / 512; }
 
 struct WgRowsArgs {
   const uint16_t* xp;  // packed x  [groups][ci_chunks][2126][64]
@@ -1719,13 +1727,18 @@ __device__ inline uint2 wr_tr(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// KT: output rows per k-tile (64 or 128).
+template <int KT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void wgrad_rows_kernel(WgRowsArgs a) {
+  constexpr int kDv = KT / 32;          // dY vectors per thread
+  constexpr int kXv = wr_xv<KT>();      // x-window vectors per thread
+  constexpr int kTilesPerGroup = kGroupOutRows / KT;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  const int xrows = 64 + 2 * a.wp + 2;
+  const int xrows = KT + 2 * a.wp + 2;
   // the third read of a kernel row reaches up to 2 rows past the window (values never
   // used): the buffer holds 4 more rows
-  const int buf_elems = 64 * kWrA + (xrows + 4) * kWrX;
+  const int buf_elems = KT * kWrA + (xrows + 4) * kWrX;
   // blockIdx.x -> (co tile, ci tile, split): a split's channel tiles share one XCD
   const int L = blockIdx.x;
   const int xcd = L % kXcds, kq = L / kXcds;
@@ -1749,43 +1762,41 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   // Per-thread load offsets (elements from the k-tile's base), fixed over the k-tiles.
   // dY vector j: row i / 16, channels (i % 16) * 8 of the tile's 128; x vector j: window
   // row i / 8, channels (i % 8) * 8.
-  int d_off[2], d_row[2];
-  bool d_chunk[2];
+  int d_off[kDv], d_row[kDv], d_rmod[kDv];
+  bool d_chunk[kDv];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < kDv; ++j) {
     const int i = tid + j * 512;
     const int row = i >> 4, ch = (i >> 3) & 1, piece = i & 7;
     const int chunk = co0 / 64 + ch;
     d_chunk[j] = chunk < a.co_chunks;
     d_row[j] = row;
+    d_rmod[j] = row % a.wp;
     d_off[j] = (min(chunk, a.co_chunks - 1) * kGroupRows + row + a.wp + 1) * kKStep + piece * 8;
   }
-  int x_off[kWrXv];
+  int x_off[kXv];
 #pragma unroll
-  for (int j = 0; j < kWrXv; ++j) {
+  for (int j = 0; j < kXv; ++j) {
     const int i = min(tid + j * 512, nxv - 1);
     x_off[j] = (i >> 3) * kKStep + (i & 7) * 8;
   }
 
-  u32x4_t dreg[2];
-  u32x4_t xreg[kWrXv];
-  bool dok[2];
-  // k-tile kt: group kt / 32, output rows (kt % 32) * 64 of it, i.e. global output rows
-  // p = 64 kt + row
+  u32x4_t dreg[kDv];
+  u32x4_t xreg[kXv];
+  bool dok[kDv];
+  // k-tile kt: group kt / kTilesPerGroup, output rows (kt % kTilesPerGroup) * KT of it,
+  // i.e. global output rows p = KT kt + row
   auto load = [&](int kt) {
-    const int g = kt >> 5, r0 = (kt & 31) * 64;
-    const int64_t rem = a.m_total - int64_t(kt) * 64;  // rows of this tile before the end
-    // strip halo columns: p % wp from (64 kt) % wp (wave-uniform) plus the row, reduced by
-    // at most three subtractions (strips are at least 21 positions wide)
-    const int base = a.S > 1 ? int((uint32_t(kt) * 64u) % uint32_t(a.wp)) : 0;
+    const int g = kt / kTilesPerGroup, r0 = (kt % kTilesPerGroup) * KT;
+    const int64_t rem = a.m_total - int64_t(kt) * KT;  // rows of this tile before the end
+    // strip halo columns: p % wp = ((KT kt) % wp (wave-uniform) + row % wp) reduced once
+    const int base = a.S > 1 ? int((uint32_t(kt) * uint32_t(KT)) % uint32_t(a.wp)) : 0;
     const uint16_t* db = a.dp + (int64_t(g) * a.co_chunks * kGroupRows + r0) * kKStep;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kDv; ++j) {
       bool ok = d_chunk[j] && d_row[j] < rem;
       if (a.S > 1) {
-        int jc = base + d_row[j];
-        jc -= jc >= a.wp ? a.wp : 0;
-        jc -= jc >= a.wp ? a.wp : 0;
+        int jc = base + d_rmod[j];
         jc -= jc >= a.wp ? a.wp : 0;
         // data column of the centre row p + wp + 1 (row position jc + 1, wrapping to the
         // next row's position 0)
@@ -1798,19 +1809,19 @@ void wgrad_rows_kernel(WgRowsArgs a) {
     }
     const uint16_t* xb = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
 #pragma unroll
-    for (int j = 0; j < kWrXv; ++j) xreg[j] = *reinterpret_cast<const u32x4_t*>(xb + x_off[j]);
+    for (int j = 0; j < kXv; ++j) xreg[j] = *reinterpret_cast<const u32x4_t*>(xb + x_off[j]);
   };
   auto store = [&](int buf) {
     uint16_t* as = smem + buf * buf_elems;
-    uint16_t* xs = as + 64 * kWrA;
+    uint16_t* xs = as + KT * kWrA;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kDv; ++j) {
       const int i = tid + j * 512;
       const u32x4_t z = {0u, 0u, 0u, 0u};
       *reinterpret_cast<u32x4_t*>(as + (i >> 4) * kWrA + (i & 15) * 8) = dok[j] ? dreg[j] : z;
     }
 #pragma unroll
-    for (int j = 0; j < kWrXv; ++j) {
+    for (int j = 0; j < kXv; ++j) {
       const int i = tid + j * 512;
       if (i < nxv) *reinterpret_cast<u32x4_t*>(xs + (i >> 3) * kWrX + (i & 7) * 8) = xreg[j];
     }
@@ -1819,7 +1830,7 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   // LDS read bases of this lane: dY rows at + q * kWrA, x rows of kernel row dy at
   // + dy * wp * kWrX + q * kWrX (q a compile-time row: an immediate offset)
   const int a_lane = wr_lane_off(kWrA, lane) + wm * 32;
-  const int x_lane = 64 * kWrA + wr_lane_off(kWrX, lane) + wn * 32;
+  const int x_lane = KT * kWrA + wr_lane_off(kWrX, lane) + wn * 32;
   const int wrow = a.wp * kWrX;
 
   if (kt0 < kt1) {
@@ -1835,7 +1846,7 @@ void wgrad_rows_kernel(WgRowsArgs a) {
     const uint16_t* xb0 = smem + cur * buf_elems + x_lane;
     const uint16_t* xbr[3] = {xb0, xb0 + wrow, xb0 + 2 * wrow};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < KT / 16; ++ks) {
       const int q = ks * 16;
       const uint2 a0 = wr_tr(ab + q * kWrA), a1 = wr_tr(ab + (q + 4) * kWrA);
       const u32x4_t av = {a0.x, a0.y, a1.x, a1.y};
@@ -1891,6 +1902,7 @@ void wgrad_rows_kernel(WgRowsArgs a) {
 
 struct WgRowsPlan {
   ConvGeom geom;
+  int kt_rows = 64;  // output rows per k-tile
   int ci_chunks = 0, co_chunks = 0, ci_pad = 0, co_pad = 0;
   int ktiles = 0, splits = 0, kt_per = 0;
   size_t part_bytes = 0, bpart_bytes = 0, lds_bytes = 0;
@@ -1903,7 +1915,8 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   p.co_chunks = int(ceil_div(Cout, kKStep));
   p.ci_pad = p.ci_chunks * kKStep;
   p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
-  p.ktiles = int(ceil_div(p.geom.m_total, 64));
+  p.kt_rows = g_wgrad_rows_kt.load() == 128 ? 128 : 64;
+  p.ktiles = int(ceil_div(p.geom.m_total, p.kt_rows));
   const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
   const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
   // split count: the channel-major path's model (rounds of 256 workgroups x per-CU rate,
@@ -1925,7 +1938,7 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   p.splits = int(ceil_div(p.ktiles, p.kt_per));
   p.part_bytes = align256(size_t(p.splits) * out_elems * 4);
   p.bpart_bytes = align256(size_t(p.splits) * p.co_pad * 4);
-  p.lds_bytes = 2 * (size_t(64) * kWrA + size_t(64 + 2 * p.geom.st.wp + 2 + 4) * kWrX) * 2;
+  p.lds_bytes = 2 * (size_t(p.kt_rows) * kWrA + size_t(p.kt_rows + 2 * p.geom.st.wp + 2 + 4) * kWrX) * 2;
   return p;
 }
 
@@ -2117,7 +2130,7 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
   const WgRowsPlan p = wgrad_rows_plan(B, Cin, Cout, H, W, layout);
   // the kernel's 32-bit row arithmetic and its strip-column reduction (strips of 21 or
   // more positions)
-  if (int64_t(p.ktiles) * 64 >= (int64_t(1) << 31) || (p.geom.st.S > 1 && p.geom.st.wp < 21)) {
+  if (int64_t(p.ktiles) * p.kt_rows >= (int64_t(1) << 31)) {
     set_error("xdna_conv3x3_wgrad_rows_bf16: shape outside the kernel's range");
     return -1;
   }
@@ -2127,8 +2140,10 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
   }
   if (!admit_launch("conv3x3 wgrad rows")) return -1;
   static const bool lds_attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          int(kMaxWgradLds)) == hipSuccess;
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel<64>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel<128>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess;
   if (!lds_attr || p.lds_bytes > kMaxWgradLds) {
     (void)hipGetLastError();
     set_error("conv3x3 wgrad rows: cannot raise the dynamic LDS limit");
@@ -2160,7 +2175,10 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
     return -1;
   }
   hipStream_t st = as_stream(stream);
-  wgrad_rows_kernel<<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
+  if (p.kt_rows == 128)
+    wgrad_rows_kernel<128><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
+  else
+    wgrad_rows_kernel<64><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
   const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
   const int zg = p.splits >= 64 ? 8 : p.splits >= 16 ? 4 : p.splits >= 4 ? 2 : 1;
   const unsigned rgrid = unsigned(std::min<int64_t>(ceil_div(n, 256 / zg), 8192));
