@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 #include <cstdlib>
 
 namespace xdna {
@@ -1696,7 +1697,10 @@ std::atomic<int> g_wgrad_rows_kt{[] {
 // zeroed in the dY tile: those pixels belong to the neighbouring strip.  Either row layout
 // (the reference's, or the tight one without zero columns).
 constexpr int kWrA = 128 + 16;   // LDS pitch (elements) of the dY tile: rows 8 banks apart
-constexpr int kWrX = 64 + 16;    // LDS pitch of the x window
+// LDS pitch of the x window: 96 elements (192 bytes, 64 mod 128) keeps the 32 lanes of a
+// half-wave transposing read on distinct banks of gfx950's 64 (5.5x fewer conflicts than
+// 80 on the largest sweep shape)
+constexpr int kWrX = 96;
 // x-window vectors per thread for k-tiles of KT rows (8 * (KT + 2*38 + 2) vectors per window)
 template <int KT>
 constexpr int wr_xv() { return (8 * (KT + 2 * 38 + 2) + 511) / 512; }
@@ -1760,26 +1764,17 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   const bool do_bias = a.bpart && ci_t == 0 && wn == 0;
 
   // Per-thread load offsets (elements from the k-tile's base), fixed over the k-tiles.
-  // dY vector j: row i / 16, channels (i % 16) * 8 of the tile's 128; x vector j: window
-  // row i / 8, channels (i % 8) * 8.
-  int d_off[kDv], d_row[kDv], d_rmod[kDv];
-  bool d_chunk[kDv];
-#pragma unroll
-  for (int j = 0; j < kDv; ++j) {
-    const int i = tid + j * 512;
-    const int row = i >> 4, ch = (i >> 3) & 1, piece = i & 7;
-    const int chunk = co0 / 64 + ch;
-    d_chunk[j] = chunk < a.co_chunks;
-    d_row[j] = row;
-    d_rmod[j] = row % a.wp;
-    d_off[j] = (min(chunk, a.co_chunks - 1) * kGroupRows + row + a.wp + 1) * kKStep + piece * 8;
-  }
-  int x_off[kXv];
-#pragma unroll
-  for (int j = 0; j < kXv; ++j) {
-    const int i = min(tid + j * 512, nxv - 1);
-    x_off[j] = (i >> 3) * kKStep + (i & 7) * 8;
-  }
+  // dY vector j: row tid / 16 + 32 j, channels (tid % 16) * 8 of the tile's 128; x vector
+  // j: window row tid / 8 + 64 j, channels (tid % 8) * 8.  Vector j is vector 0 plus a
+  // compile-time offset, so one register of each kind is kept.
+  const bool strips = a.S > 1;
+  const int d_row0 = tid >> 4;
+  const int d_chunk = co0 / 64 + ((tid >> 3) & 1);
+  const bool d_chunk_ok = d_chunk < a.co_chunks;
+  const int d_off0 = (min(d_chunk, a.co_chunks - 1) * kGroupRows + d_row0 + a.wp + 1) * kKStep + (tid & 7) * 8;
+  const int d_rmod0 = d_row0 % a.wp;
+  const int x_off0 = (tid >> 3) * kKStep + (tid & 7) * 8;
+  const int x_offmax = ((nxv - 1) >> 3) * kKStep + ((nxv - 1) & 7) * 8;
 
   u32x4_t dreg[kDv];
   u32x4_t xreg[kXv];
@@ -1789,27 +1784,27 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   auto load = [&](int kt) {
     const int g = kt / kTilesPerGroup, r0 = (kt % kTilesPerGroup) * KT;
     const int64_t rem = a.m_total - int64_t(kt) * KT;  // rows of this tile before the end
-    // strip halo columns: p % wp = ((KT kt) % wp (wave-uniform) + row % wp) reduced once
-    const int base = a.S > 1 ? int((uint32_t(kt) * uint32_t(KT)) % uint32_t(a.wp)) : 0;
+    // strip halo columns: p % wp = ((KT kt) % wp + (32 j) % wp (both wave-uniform) +
+    // row0 % wp), each term below wp, reduced by two subtractions
+    const int base = int((uint32_t(kt) * uint32_t(KT)) % uint32_t(a.wp));
     const uint16_t* db = a.dp + (int64_t(g) * a.co_chunks * kGroupRows + r0) * kKStep;
 #pragma unroll
     for (int j = 0; j < kDv; ++j) {
-      bool ok = d_chunk[j] && d_row[j] < rem;
-      if (a.S > 1) {
-        int jc = base + d_rmod[j];
-        jc -= jc >= a.wp ? a.wp : 0;
-        // data column of the centre row p + wp + 1 (row position jc + 1, wrapping to the
-        // next row's position 0)
-        int dj = jc + 1 - a.lead;
-        dj = dj == a.wp ? 0 : dj;
-        ok = ok && dj != 0 && dj != a.Wg - 1;
-      }
-      dok[j] = ok;
-      dreg[j] = *reinterpret_cast<const u32x4_t*>(db + d_off[j]);
+      // branch-free: data column of the centre row p + wp + 1 (row position jc + 1,
+      // wrapping to the next row's position 0); a strip's halo columns are masked
+      int jc = base + int(uint32_t(32 * j) % uint32_t(a.wp)) + d_rmod0;
+      jc -= jc >= a.wp ? a.wp : 0;
+      jc -= jc >= a.wp ? a.wp : 0;
+      int dj = jc + 1 - a.lead;
+      dj = dj == a.wp ? 0 : dj;
+      const bool halo = strips && (dj == 0 || dj == a.Wg - 1);
+      dok[j] = d_chunk_ok && d_row0 + 32 * j < rem && !halo;
+      dreg[j] = *reinterpret_cast<const u32x4_t*>(db + d_off0 + 32 * j * kKStep);
     }
     const uint16_t* xb = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
 #pragma unroll
-    for (int j = 0; j < kXv; ++j) xreg[j] = *reinterpret_cast<const u32x4_t*>(xb + x_off[j]);
+    for (int j = 0; j < kXv; ++j)
+      xreg[j] = *reinterpret_cast<const u32x4_t*>(xb + min(x_off0 + 64 * j * kKStep, x_offmax));
   };
   auto store = [&](int buf) {
     uint16_t* as = smem + buf * buf_elems;
@@ -1838,49 +1833,58 @@ void wgrad_rows_kernel(WgRowsArgs a) {
     store(0);
   }
   __syncthreads();
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int cur = (kt - kt0) & 1;
-    const bool more = kt + 1 < kt1;
-    if (more) load(kt + 1);
-    const uint16_t* ab = smem + cur * buf_elems + a_lane;
-    const uint16_t* xb0 = smem + cur * buf_elems + x_lane;
-    const uint16_t* xbr[3] = {xb0, xb0 + wrow, xb0 + 2 * wrow};
+  // the k-tile loop, instantiated with and without the bias sums (a wave-uniform choice
+  // outside the loop: a branch inside it made every k-step wait for all its LDS reads)
+  auto ktiles = [&](auto bias_tag) {
+    constexpr bool kBias = decltype(bias_tag)::value;
+    for (int kt = kt0; kt < kt1; ++kt) {
+      const int cur = (kt - kt0) & 1;
+      const bool more = kt + 1 < kt1;
+      if (more) load(kt + 1);
+      const uint16_t* ab = smem + cur * buf_elems + a_lane;
+      const uint16_t* xb0 = smem + cur * buf_elems + x_lane;
+      const uint16_t* xbr[3] = {xb0, xb0 + wrow, xb0 + 2 * wrow};
 #pragma unroll
-    for (int ks = 0; ks < KT / 16; ++ks) {
-      const int q = ks * 16;
-      const uint2 a0 = wr_tr(ab + q * kWrA), a1 = wr_tr(ab + (q + 4) * kWrA);
-      const u32x4_t av = {a0.x, a0.y, a1.x, a1.y};
-      if (do_bias) {
+      for (int ks = 0; ks < KT / 16; ++ks) {
+        const int q = ks * 16;
+        const uint2 a0 = wr_tr(ab + q * kWrA), a1 = wr_tr(ab + (q + 4) * kWrA);
+        const u32x4_t av = {a0.x, a0.y, a1.x, a1.y};
+        if (kBias) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          bsum += __uint_as_float(av[e] << 16) + __uint_as_float(av[e] & 0xFFFF0000u);
+          for (int e = 0; e < 4; ++e)
+            bsum += __uint_as_float(av[e] << 16) + __uint_as_float(av[e] & 0xFFFF0000u);
+        }
+        const bf16x8_t af = as_bf16x8(av);
+#pragma unroll
+        for (int dy = 0; dy < 3; ++dy) {
+          const uint16_t* xr = xbr[dy] + q * kWrX;
+          const uint2 r0 = wr_tr(xr), r1 = wr_tr(xr + 4 * kWrX);
+          const u32x4_t l = {r0.x, r0.y, r1.x, r1.y};
+          // dx = 1, 2: the same 12 rows shifted by one and two (reading the dx = 2 operand
+          // directly instead measured the same)
+          const uint2 r2 = wr_tr(xr + 8 * kWrX);
+          u32x4_t s1, s2;
+          s1[0] = __builtin_amdgcn_alignbit(r0.y, r0.x, 16);
+          s1[1] = __builtin_amdgcn_alignbit(r1.x, r0.y, 16);
+          s1[2] = __builtin_amdgcn_alignbit(r1.y, r1.x, 16);
+          s1[3] = __builtin_amdgcn_alignbit(r2.x, r1.y, 16);
+          s2[0] = r0.y;
+          s2[1] = r1.x;
+          s2[2] = r1.y;
+          s2[3] = r2.x;
+          acc[dy * 3 + 0] = mfma_32x32x16(af, as_bf16x8(l), acc[dy * 3 + 0]);
+          acc[dy * 3 + 1] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1]);
+          acc[dy * 3 + 2] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2]);
+        }
       }
-      const bf16x8_t af = as_bf16x8(av);
-#pragma unroll
-      for (int dy = 0; dy < 3; ++dy) {
-        const uint16_t* xr = xbr[dy] + q * kWrX;
-        const uint2 r0 = wr_tr(xr), r1 = wr_tr(xr + 4 * kWrX);
-        const u32x4_t l = {r0.x, r0.y, r1.x, r1.y};
-        // dx = 1, 2: the same 12 rows shifted by one and two (reading the dx = 2 operand
-        // directly instead measured the same)
-        const uint2 r2 = wr_tr(xr + 8 * kWrX);
-        u32x4_t s1, s2;
-        s1[0] = __builtin_amdgcn_alignbit(r0.y, r0.x, 16);
-        s1[1] = __builtin_amdgcn_alignbit(r1.x, r0.y, 16);
-        s1[2] = __builtin_amdgcn_alignbit(r1.y, r1.x, 16);
-        s1[3] = __builtin_amdgcn_alignbit(r2.x, r1.y, 16);
-        s2[0] = r0.y;
-        s2[1] = r1.x;
-        s2[2] = r1.y;
-        s2[3] = r2.x;
-        acc[dy * 3 + 0] = mfma_32x32x16(af, as_bf16x8(l), acc[dy * 3 + 0]);
-        acc[dy * 3 + 1] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1]);
-        acc[dy * 3 + 2] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2]);
-      }
+      if (more) store(cur ^ 1);
+      __syncthreads();
     }
-    if (more) store(cur ^ 1);
-    __syncthreads();
-  }
+  };
+  if (do_bias)
+    ktiles(std::true_type{});
+  else
+    ktiles(std::false_type{});
 
   // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci
   const int lr = lane & 31;
