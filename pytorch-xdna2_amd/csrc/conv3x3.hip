@@ -837,24 +837,28 @@ void conv_small_kernel(RowsArgs a) {
     store_chunk();
     __syncthreads();
     if (ch + 1 < ch1) load_chunk(ch + 1);
-    u32x4_t aq[2], bq[2][NT];
-    aq[0] = *reinterpret_cast<const u32x4_t*>(wa_base);
+    // k-step s = (tap, 16-channel slice): its fragments are read kPre k-steps ahead into
+    // a ring of registers (one wave per SIMD: an MFMA or two cannot cover an LDS read)
+    constexpr int kPre = 3;
+    u32x4_t aq[kPre + 1], bq[kPre + 1][NT];
+    const uint16_t* xrow[3] = {xb, xb + a.wp * kPitch, xb + 2 * a.wp * kPitch};
+    auto fetch = [&](int step) {
+      const int tap = step >> 2, ks = step & 3, slot = step % (kPre + 1);
+      aq[slot] = *reinterpret_cast<const u32x4_t*>(wa_base + tap * kKStep + ks * 16);
+      const uint16_t* xq = xrow[tap / 3] + (tap % 3) * kPitch + ks * 16;
 #pragma unroll
-    for (int n = 0; n < NT; ++n) bq[0][n] = *reinterpret_cast<const u32x4_t*>(xb + n * 32 * kPitch);
+      for (int n = 0; n < NT; ++n) bq[slot][n] = *reinterpret_cast<const u32x4_t*>(xq + n * 32 * kPitch);
+    };
+#pragma unroll
+    for (int step = 0; step < kPre; ++step) fetch(step);
 #pragma unroll
     for (int step = 0; step < 36; ++step) {
-      if (step + 1 < 36) {
-        const int ntap = (step + 1) >> 2, nks = (step + 1) & 3;
-        const int noff = ((ntap / 3) * a.wp + (ntap % 3)) * kPitch + nks * 16;
-        aq[(step + 1) & 1] = *reinterpret_cast<const u32x4_t*>(wa_base + ntap * kKStep + nks * 16);
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-          bq[(step + 1) & 1][n] = *reinterpret_cast<const u32x4_t*>(xb + noff + n * 32 * kPitch);
-      }
+      if (step + kPre < 36) fetch(step + kPre);
       __builtin_amdgcn_sched_barrier(0);
-      const bf16x8_t af = as_bf16x8(aq[step & 1]);
+      const int slot = step % (kPre + 1);
+      const bf16x8_t af = as_bf16x8(aq[slot]);
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] = mfma_32x32x16(af, as_bf16x8(bq[step & 1][n]), acc[n]);
+      for (int n = 0; n < NT; ++n) acc[n] = mfma_32x32x16(af, as_bf16x8(bq[slot][n]), acc[n]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
