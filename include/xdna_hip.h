@@ -235,6 +235,11 @@ int xdna_conv3x3_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw,
  * the same reference stages as xdna_conv3x3_wgrad_bf16 (XdnaConv3x3wDwRuntime::
  * pack_operands / compute, torch_xdna_device.cpp:2660-2751). */
 size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, int W, int layout);
+/* Output rows per k-tile of xdna_conv3x3_wgrad_rows_bf16: 0 the default (128), 64 or 128.
+ * The split-K partition, and with it the fp32 summation order, follows from it; both stay
+ * within the conv bar.  Workspace sizes depend on it: query them after setting it.  No
+ * reference counterpart (measurements and tests). */
+int xdna_conv3x3_set_wgrad_rows_kt(int kt_rows);
 int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_t* gw, uint16_t* gb, int B,
                                  int Cin, int Cout, int H, int W, int layout, void* workspace,
                                  size_t workspace_bytes, void* stream);

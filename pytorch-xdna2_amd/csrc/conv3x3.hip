@@ -1677,7 +1677,8 @@ WgradPlan wgrad_plan(int B, int Cin, int Cout, int H, int W) {
 
 constexpr size_t kMaxWgradLds = 160 * 1024;
 
-// Output rows per k-tile of the rows weight gradient (64 or 128; XDNA_WGRAD_KT).
+// Output rows per k-tile of the rows weight gradient (64 or 128; XDNA_WGRAD_KT at start-up,
+// xdna_conv3x3_set_wgrad_rows_kt).
 std::atomic<int> g_wgrad_rows_kt{[] {
   const char* e = std::getenv("XDNA_WGRAD_KT");
   return e && std::atoi(e) == 64 ? 64 : 128;
@@ -2252,6 +2253,15 @@ int xdna_conv3x3_layout_rows_bf16(const uint16_t* xp, const uint16_t* wt, const 
     return -1;
   }
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout);
+}
+
+int xdna_conv3x3_set_wgrad_rows_kt(int kt_rows) {
+  if (kt_rows != 0 && kt_rows != 64 && kt_rows != 128) {
+    set_error("xdna_conv3x3_set_wgrad_rows_kt: k-tile rows must be 0 (default), 64 or 128");
+    return -1;
+  }
+  g_wgrad_rows_kt.store(kt_rows == 64 ? 64 : 128);
+  return 0;
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {

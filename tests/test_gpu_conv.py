@@ -169,13 +169,21 @@ def test_forward_tight_layout(hip, shape, variant):
     check_bf16(host(y), oracle.conv3x3_fwd(x, w, b), what=f"fwd tight {shape}")
 
 
+@pytest.fixture(params=[128, 64], ids=lambda k: f"kt{k}")
+def wgrad_kt(hip, request):
+    assert hip.xdna_conv3x3_set_wgrad_rows_kt(request.param) == 0
+    yield request.param
+    assert hip.xdna_conv3x3_set_wgrad_rows_kt(0) == 0
+
+
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("shape", SHAPES + LAYOUT_SHAPES[4:6], ids=lambda s: "x".join(map(str, s)))
-def test_wgrad_rows(hip, shape, layout):
+def test_wgrad_rows(hip, shape, layout, wgrad_kt):
     """Weight gradient from the packed row layouts (x and dY packed as the forward and
-    input-gradient convs pack them) vs the oracle; run-to-run bit equality."""
+    input-gradient convs pack them), with 128- and 64-row k-tiles, vs the oracle; run-to-run
+    bit equality."""
     B, Cin, Cout, H, W = shape
-    print(f"conv wgrad rows {shape} layout {layout}", flush=True)
+    print(f"conv wgrad rows {shape} layout {layout} kt {wgrad_kt}", flush=True)
     x, _, _, dy = _data(*shape, seed=sum(shape) + 3)
     ref_w, ref_b = oracle.conv3x3_wgrad(x, dy)
     xp = _pack(hip, x, layout)
@@ -195,6 +203,11 @@ def test_wgrad_rows(hip, shape, layout):
     np.testing.assert_array_equal(host(gw2), got_w)
     assert hip.xdna_conv3x3_wgrad_rows_bf16(ptr(xp), ptr(dp), ptr(gw2), None, B, Cin, Cout, H, W, layout,
                                             ptr(ws), ws_bytes - 1, stream()) == -1
+
+
+def test_wgrad_rows_kt_setter_rejects(hip):
+    assert hip.xdna_conv3x3_set_wgrad_rows_kt(96) == -1
+    assert hip.xdna_conv3x3_set_wgrad_rows_kt(0) == 0
 
 
 def test_workspace_too_small_is_an_error(hip):
