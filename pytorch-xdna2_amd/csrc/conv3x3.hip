@@ -89,6 +89,7 @@ struct RowsArgs {
   int64_t img, m_total, m_pad;
   int B;                 // images
   int out_rs;            // 1: stores through a buffer resource (every tile's span < 2^30 bytes)
+  int bias_vec;          // 1: bias 8-byte aligned and cout % 4 == 0 (4-channel vector loads)
 };
 
 // Branch-free NCHW epilogue.  The resource starts at the first image a tile touches; a
@@ -554,7 +555,22 @@ void conv_rows4_kernel(RowsArgs a) {
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     f32x16_t init = zero_acc();
-    if (a.bias) {
+    if (a.bias && a.bias_vec) {
+      // a lane's 16 rows are 4 runs of 4 consecutive channels (mfma_row): one 8-byte load
+      // per run through a buffer resource (channels past cout read as zero); 2-byte loads
+      // per row measured 4.7 % slower over the sweep
+      const __amdgpu_buffer_rsrc_t brs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.bias), 0, a.cout * 2, 0x00020000);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int co = co0 + wm * MT * 32 + m * 32 + 8 * q + 4 * (lane >> 5);
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(brs, co * 2, 0, 0));
+        init[4 * q + 0] = __uint_as_float(v.x << 16);
+        init[4 * q + 1] = __uint_as_float(v.x & 0xFFFF0000u);
+        init[4 * q + 2] = __uint_as_float(v.y << 16);
+        init[4 * q + 3] = __uint_as_float(v.y & 0xFFFF0000u);
+      }
+    } else if (a.bias) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int co = co0 + wm * MT * 32 + m * 32 + mfma_row(i, lane);
@@ -787,7 +803,20 @@ void conv_small_kernel(RowsArgs a) {
   f32x16_t acc[NT];
   {
     f32x16_t init = zero_acc();
-    if (a.bias && !a.part) {
+    if (a.bias && !a.part && a.bias_vec) {
+      // 4 runs of 4 consecutive channels per lane: 8-byte buffer loads (as the main kernel)
+      const __amdgpu_buffer_rsrc_t brs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.bias), 0, a.cout * 2, 0x00020000);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int co = co0 + wm * 32 + 8 * q + 4 * (lane >> 5);
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(brs, co * 2, 0, 0));
+        init[4 * q + 0] = __uint_as_float(v.x << 16);
+        init[4 * q + 1] = __uint_as_float(v.x & 0xFFFF0000u);
+        init[4 * q + 2] = __uint_as_float(v.y << 16);
+        init[4 * q + 3] = __uint_as_float(v.y & 0xFFFF0000u);
+      }
+    } else if (a.bias && !a.part) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int co = co0 + wm * 32 + mfma_row(i, lane);
@@ -1495,6 +1524,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.m_total = geom.m_total;
   a.m_pad = int64_t(geom.groups) * kGroupOutRows;
   a.B = B;
+  a.bias_vec = bias && (reinterpret_cast<uintptr_t>(bias) & 7) == 0 && cout % 4 == 0 ? 1 : 0;
   {
     // images a tile of up to 512 grid rows can touch, and the bytes they span
     const int64_t span = (512 - 1) / geom.img + 2;
