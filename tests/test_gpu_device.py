@@ -152,6 +152,25 @@ def test_kept_packed_input_shared_and_stale(xdna):
     xdna.empty_cache()
 
 
+@pytest.mark.parametrize("offset", [0, 1, 4], ids=lambda o: f"bias_offset{o}")
+@pytest.mark.parametrize("cout", [64, 66])
+def test_conv_bias_views(xdna, offset, cout):
+    """Conv bias as a view into a larger tensor: 8-byte aligned (offset 0, 4: 4-channel
+    vector loads when cout % 4 == 0) and 2-byte aligned (offset 1: per-row loads), against
+    the oracle, on the main and the small-grid kernels."""
+    g = torch.Generator().manual_seed(31 + offset + cout)
+    for (B, H, W) in ((2, 12, 12), (16, 36, 36)):
+        x = torch.randn(B, 48, H, W, generator=g).bfloat16()
+        w = (torch.randn(cout, 48, 3, 3, generator=g) * 0.05).bfloat16()
+        big = torch.randn(cout + 8, generator=g).bfloat16()
+        bias = big[offset:offset + cout]
+        ref = oracle.conv3x3_fwd(bits(x), bits(w), bits(bias))
+        bd = big.to(X)[offset:offset + cout]
+        assert bd.data_ptr() % 8 == (2 * offset) % 8
+        y = F.conv2d(x.to(X), w.to(X), bd, padding=1)
+        check_bf16(bits(y), ref, what=f"conv with bias view (offset {offset}, cout {cout}, B {B})")
+
+
 def test_other_convs_run_on_general_kernels(xdna):
     """5x5, 1x1, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on the general
     HIP kernels (mode 2: always), the 3x3 / stride-2 / pad-1 one on the stride-1 3x3 path,
