@@ -91,15 +91,39 @@ int xdna_hip_cache_pool_release(int64_t pool);
  * path uses).  A diagnostic that lets tests pin the rounding; no reference counterpart. */
 int xdna_round_bf16(const float* in, uint16_t* out, int64_t n, void* stream);
 
+/* The calling thread's current private pool (0: the shared pool). */
+int64_t xdna_hip_cache_pool_current(void);
+
+/* 1 if `stream` is capturing a graph, 0 if not, -1 on error.  The backend asks this
+ * before using its host-side caches of device buffers, whose contents a captured graph
+ * must not depend on. */
+int xdna_hip_stream_capturing(void* stream);
+
 int xdna_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
                           void* stream); /* kind: 1 H2D, 2 D2H, 3 D2D, 4 default */
 int xdna_hip_memset_async(void* dst, int value, size_t bytes, void* stream);
+
+/* Host waits with a deadline (the dispatch deadline of xrt_shim.cpp:57-90, 174-233).
+ * Each returns 0 when the work is done, -1 on an error reported by the device or the
+ * runtime, and -2 when the deadline passed first: the work may still be running, so the
+ * process is poisoned (later launches are refused, frees leak).  The message from
+ * xdna_hip_last_error() starts with "deadline:" and names what was waited for.  The
+ * deadline is XDNA_WAIT_TIMEOUT_MS (default 30000; 0 = no limit). */
 int xdna_hip_stream_synchronize(void* stream);
 int xdna_hip_device_synchronize(void);
+int xdna_hip_set_wait_timeout_ms(int64_t ms);
+int64_t xdna_hip_wait_timeout_ms(void);
+/* Longest completed wait of this process, in ms (to size the deadline by measurement;
+ * replaces shim_dispatch_max_wait_ms, xrt_shim.h:81). */
+double xdna_hip_max_wait_ms(void);
+/* Test hook: the n-th host wait from now (n >= 1) reports a timeout at once, without
+ * touching the device, and poisons the process; n = 0 disables.  Host-only. */
+int xdna_hip_inject_wait_timeout(int64_t nth_wait);
 
 void* xdna_hip_event_create(int timing);
 int xdna_hip_event_destroy(void* event);
 int xdna_hip_event_record(void* event, void* stream);
+/* Bounded like the waits above: 0 done, -1 error, -2 deadline. */
 int xdna_hip_event_synchronize(void* event);
 /* 1 done, 0 pending, -1 error. */
 int xdna_hip_event_query(void* event);
@@ -403,6 +427,19 @@ int xdna_fused_adam(int n_tensors, void* const* params, void* const* grads,
                     double beta2, double weight_decay, double eps, int amsgrad,
                     int maximize, int mode, const float* grad_scale,
                     const float* found_inf, void* stream);
+
+/* The same step with lr a device scalar (lr_dtype 1 = fp32, 2 = fp64), read by the kernel
+ * at its value as a double, as torch's CPU kernel reads it (lr.item<double>()): the
+ * tensor-lr overloads _fused_adam_.tensor_lr / _fused_adamw_.tensor_lr, which capturable
+ * optimizers with a tensor lr call.  No host read of lr, so the step can be captured in
+ * a graph.  Same reference counterpart as xdna_fused_adam. */
+int xdna_fused_adam_tensor_lr(int n_tensors, void* const* params, void* const* grads,
+                              void* const* exp_avgs, void* const* exp_avg_sqs,
+                              void* const* max_exp_avg_sqs, const float* const* steps,
+                              const int64_t* numels, int dtype, const void* lr, int lr_dtype,
+                              double beta1, double beta2, double weight_decay, double eps,
+                              int amsgrad, int maximize, int mode, const float* grad_scale,
+                              const float* found_inf, void* stream);
 
 /* tensors[i][j] += value (fp32, computed as t + value in fp32) for every element of
  * n_tensors device tensors: torch._foreach_add_(state_steps, 1), which the optimizers

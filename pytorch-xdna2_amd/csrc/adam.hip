@@ -52,6 +52,10 @@ struct AdamArgs {
 struct AdamScalars {
   double lr, beta1, beta2, wd, eps;
   int amsgrad, maximize, adamw;
+  // lr as a device scalar (torch's tensor-lr overloads), read where the step constants
+  // are computed: 0 absent (lr above), 1 fp32, 2 fp64
+  const void* lr_dev;
+  int lr_dtype;
 };
 
 template <typename T> __device__ inline float ld(const T* p, int64_t i);
@@ -125,8 +129,13 @@ __device__ inline StepConsts step_consts(const AdamScalars& s, float step_f) {
   const double step = double(step_f);
   const double bc1 = 1.0 - pow(s.beta1, step);
   const double bc2 = 1.0 - pow(s.beta2, step);
+  // a tensor lr is used at its value as a double, as torch's CPU kernel reads it
+  // (lr.item<double>())
+  const double lr = s.lr_dtype == 1   ? double(*static_cast<const float*>(s.lr_dev))
+                    : s.lr_dtype == 2 ? *static_cast<const double*>(s.lr_dev)
+                                      : s.lr;
   StepConsts k;
-  k.step_size = float(s.lr / bc1);
+  k.step_size = float(lr / bc1);
   k.bc2_sqrt = float(sqrt(bc2));
   k.eps = float(s.eps);
   k.beta2 = float(s.beta2);
@@ -134,7 +143,7 @@ __device__ inline StepConsts step_consts(const AdamScalars& s, float step_f) {
   k.w = float(1.0 - s.beta1);
   k.one_minus_w = 1.0f - k.w;
   k.wd = float(s.wd);
-  k.decay = float(1.0 - s.lr * s.wd);
+  k.decay = float(1.0 - lr * s.wd);
   return k;
 }
 
@@ -281,22 +290,22 @@ __global__ __launch_bounds__(256) void foreach_add_f32_kernel(ForeachArgs a, flo
 
 using namespace xdna;
 
-extern "C" int xdna_fused_adam(int n_tensors, void* const* params, void* const* grads,
-                               void* const* exp_avgs, void* const* exp_avg_sqs,
-                               void* const* max_exp_avg_sqs, const float* const* steps,
-                               const int64_t* numels, int dtype, double lr, double beta1,
-                               double beta2, double weight_decay, double eps, int amsgrad,
-                               int maximize, int mode, const float* grad_scale,
-                               const float* found_inf, void* stream) {
-  if (n_tensors < 0 || (dtype != 0 && dtype != 1) || (mode != 0 && mode != 1)) {
+namespace xdna {
+namespace {
+
+int fused_adam_launch(int n_tensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                      void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, const float* const* steps,
+                      const int64_t* numels, int dtype, const AdamScalars& s, const float* grad_scale,
+                      const float* found_inf, void* stream) {
+  if (n_tensors < 0 || (dtype != 0 && dtype != 1) || (s.adamw != 0 && s.adamw != 1)) {
     set_error("xdna_fused_adam: invalid arguments");
     return -1;
   }
-  if (amsgrad && !max_exp_avg_sqs) {
+  if (s.amsgrad && !max_exp_avg_sqs) {
     set_error("xdna_fused_adam: amsgrad needs max_exp_avg_sqs");
     return -1;
   }
-  AdamScalars s{lr, beta1, beta2, weight_decay, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, mode};
+  const int amsgrad = s.amsgrad;
   int done = 0;
   while (done < n_tensors) {
     AdamArgs a{};
@@ -337,6 +346,37 @@ extern "C" int xdna_fused_adam(int n_tensors, void* const* params, void* const* 
     if (check_launch("xdna_fused_adam")) return -1;
   }
   return 0;
+}
+
+}  // namespace
+}  // namespace xdna
+
+extern "C" int xdna_fused_adam(int n_tensors, void* const* params, void* const* grads,
+                               void* const* exp_avgs, void* const* exp_avg_sqs,
+                               void* const* max_exp_avg_sqs, const float* const* steps,
+                               const int64_t* numels, int dtype, double lr, double beta1,
+                               double beta2, double weight_decay, double eps, int amsgrad,
+                               int maximize, int mode, const float* grad_scale,
+                               const float* found_inf, void* stream) {
+  const AdamScalars s{lr, beta1, beta2, weight_decay, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, mode, nullptr, 0};
+  return fused_adam_launch(n_tensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, steps, numels,
+                           dtype, s, grad_scale, found_inf, stream);
+}
+
+extern "C" int xdna_fused_adam_tensor_lr(int n_tensors, void* const* params, void* const* grads,
+                                         void* const* exp_avgs, void* const* exp_avg_sqs,
+                                         void* const* max_exp_avg_sqs, const float* const* steps,
+                                         const int64_t* numels, int dtype, const void* lr, int lr_dtype,
+                                         double beta1, double beta2, double weight_decay, double eps,
+                                         int amsgrad, int maximize, int mode, const float* grad_scale,
+                                         const float* found_inf, void* stream) {
+  if (!lr || (lr_dtype != 1 && lr_dtype != 2)) {
+    set_error("xdna_fused_adam_tensor_lr: lr must be a device fp32 (1) or fp64 (2) scalar");
+    return -1;
+  }
+  const AdamScalars s{0.0, beta1, beta2, weight_decay, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, mode, lr, lr_dtype};
+  return fused_adam_launch(n_tensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, steps, numels,
+                           dtype, s, grad_scale, found_inf, stream);
 }
 
 extern "C" int xdna_foreach_add_scalar_f32(int n_tensors, float* const* tensors, const int64_t* numels,

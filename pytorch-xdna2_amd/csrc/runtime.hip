@@ -10,10 +10,15 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
+#include <condition_variable>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
+#include <thread>
 #include <unordered_map>
 
 namespace xdna {
@@ -24,6 +29,32 @@ std::atomic<bool> g_poisoned{false};
 std::atomic<int64_t> g_launches{0};
 std::atomic<int64_t> g_inject_at{0};     // absolute launch number that fails (0: off)
 std::atomic<int> g_inject_poison{0};
+
+// Host waits (stream, event and device synchronization) are bounded: a wait that passes
+// the deadline returns a timeout status distinct from an error, names what it waited
+// for, and poisons the process, since the work it waited for may still be running and
+// still use its buffers.  The deadline bounds a hang, not latency: the default, 30 s, is
+// several hundred times the longest healthy wait of any workload here (a sweep step of
+// 18 ms).  XDNA_WAIT_TIMEOUT_MS sets it; 0 waits without a limit.  The reference bounds
+// its NPU dispatch waits the same way (xrt_shim.cpp:57-90, 174-233).
+std::atomic<int64_t> g_wait_limit_ms{[] {
+  const char* e = std::getenv("XDNA_WAIT_TIMEOUT_MS");
+  if (!e || !*e) return int64_t(30000);
+  char* end = nullptr;
+  const long long v = std::strtoll(e, &end, 10);
+  return end && *end == '\0' && v >= 0 ? int64_t(v) : int64_t(30000);
+}()};
+std::atomic<int64_t> g_waits{0};
+std::atomic<int64_t> g_inject_wait_at{0};  // absolute wait number that times out (0: off)
+std::atomic<int64_t> g_max_wait_us{0};
+
+using WaitClock = std::chrono::steady_clock;
+
+void note_wait(int64_t us) {
+  int64_t prev = g_max_wait_us.load(std::memory_order_relaxed);
+  while (us > prev && !g_max_wait_us.compare_exchange_weak(prev, us, std::memory_order_relaxed)) {
+  }
+}
 }  // namespace
 
 void set_error(const std::string& msg) { t_error = msg; }
@@ -60,6 +91,61 @@ int check_launch(const char* what) {
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return launch_failed(what, err);
   return 0;
+}
+
+// Polls `poll` (1 done, 0 pending, -1 failed with the error set) until it reports done
+// or the deadline passes.  0 done, -1 error, -2 timeout (process poisoned).  The first
+// 50 ms spin with yields (what a blocking HIP wait does too), later polls sleep 50 us.
+template <class Poll>
+int bounded_wait(const char* what, Poll poll) {
+  const int64_t n = g_waits.fetch_add(1, std::memory_order_relaxed) + 1;
+  const int64_t inj = g_inject_wait_at.load(std::memory_order_relaxed);
+  if (inj != 0 && n == inj) {
+    g_inject_wait_at.store(0, std::memory_order_relaxed);
+    g_poisoned.store(true);
+    set_error(std::string("deadline: wait for ") + what + " timed out (injected); the process is poisoned");
+    return -2;
+  }
+  const int64_t limit_ms = g_wait_limit_ms.load(std::memory_order_relaxed);
+  const auto t0 = WaitClock::now();
+  for (;;) {
+    const int r = poll();
+    const int64_t us =
+        std::chrono::duration_cast<std::chrono::microseconds>(WaitClock::now() - t0).count();
+    if (r != 0) {
+      note_wait(us);
+      return r > 0 ? 0 : -1;
+    }
+    if (limit_ms > 0 && us >= limit_ms * 1000) {
+      g_poisoned.store(true);
+      set_error(std::string("deadline: wait for ") + what + " still pending after " + std::to_string(us / 1000) +
+                " ms (XDNA_WAIT_TIMEOUT_MS = " + std::to_string(limit_ms) +
+                "); device work may still use its buffers, so the process is poisoned");
+      return -2;
+    }
+    if (us < 50000)
+      std::this_thread::yield();
+    else
+      std::this_thread::sleep_for(std::chrono::microseconds(50));
+  }
+}
+
+// One event per host thread for stream waits (recorded, then polled).
+hipEvent_t thread_wait_event() {
+  thread_local hipEvent_t ev = nullptr;
+  if (!ev && hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    ev = nullptr;
+  }
+  return ev;
+}
+
+int poll_event(hipEvent_t ev, const char* what) {
+  const hipError_t e = hipEventQuery(ev);
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  launch_failed(what, e);
+  return -1;
 }
 
 // ---- caching allocator ---------------------------------------------------------
@@ -142,6 +228,7 @@ int xdna_hip_reset_failure_state(void) {
   g_poisoned.store(false);
   g_inject_at.store(0);
   g_inject_poison.store(0);
+  g_inject_wait_at.store(0);
   return 0;
 }
 
@@ -358,14 +445,87 @@ int xdna_hip_memset_async(void* dst, int value, size_t bytes, void* stream) {
 }
 
 int xdna_hip_stream_synchronize(void* stream) {
-  const hipError_t e = hipStreamSynchronize(as_stream(stream));
-  if (e != hipSuccess) return launch_failed("hipStreamSynchronize", e);
-  return 0;
+  // the injected timeout comes first: it must not touch the device
+  hipEvent_t ev = nullptr;
+  bool recorded = false;
+  return bounded_wait("the stream", [&]() -> int {
+    if (!recorded) {
+      ev = thread_wait_event();
+      if (!ev) {
+        set_error("xdna_hip_stream_synchronize: cannot create the wait event");
+        return -1;
+      }
+      const hipError_t e = hipEventRecord(ev, as_stream(stream));
+      if (e != hipSuccess) {
+        launch_failed("hipEventRecord (stream wait)", e);
+        return -1;
+      }
+      recorded = true;
+    }
+    return poll_event(ev, "hipEventQuery (stream wait)");
+  });
 }
 
 int xdna_hip_device_synchronize(void) {
-  const hipError_t e = hipDeviceSynchronize();
-  if (e != hipSuccess) return launch_failed("hipDeviceSynchronize", e);
+  // hipDeviceSynchronize cannot be polled: it runs on a helper thread and the caller waits
+  // for it with the deadline.  A helper stuck past the deadline is left behind (detached).
+  struct Job {
+    std::mutex mu;
+    bool done = false;
+    hipError_t err = hipSuccess;
+  };
+  std::shared_ptr<Job> job;
+  int dev = 0;
+  return bounded_wait("the device", [&]() -> int {
+    if (!job) {
+      job = std::make_shared<Job>();
+      if (hipGetDevice(&dev) != hipSuccess) (void)hipGetLastError();
+      std::thread([job, dev] {
+        (void)hipSetDevice(dev);
+        const hipError_t e = hipDeviceSynchronize();
+        std::lock_guard<std::mutex> lock(job->mu);
+        job->err = e;
+        job->done = true;
+      }).detach();
+    }
+    std::lock_guard<std::mutex> lock(job->mu);
+    if (!job->done) return 0;
+    if (job->err != hipSuccess) {
+      launch_failed("hipDeviceSynchronize", job->err);
+      return -1;
+    }
+    return 1;
+  });
+}
+
+int xdna_hip_stream_capturing(void* stream) {
+  hipStreamCaptureStatus s = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(as_stream(stream), &s);
+  if (e != hipSuccess) return launch_failed("hipStreamIsCapturing", e);
+  return s == hipStreamCaptureStatusActive ? 1 : 0;
+}
+
+int64_t xdna_hip_cache_pool_current(void) { return t_pool; }
+
+int xdna_hip_set_wait_timeout_ms(int64_t ms) {
+  if (ms < 0) {
+    set_error("xdna_hip_set_wait_timeout_ms: negative deadline");
+    return -1;
+  }
+  g_wait_limit_ms.store(ms);
+  return 0;
+}
+
+int64_t xdna_hip_wait_timeout_ms(void) { return g_wait_limit_ms.load(); }
+
+double xdna_hip_max_wait_ms(void) { return double(g_max_wait_us.load()) / 1000.0; }
+
+int xdna_hip_inject_wait_timeout(int64_t nth_wait) {
+  if (nth_wait < 0) {
+    set_error("xdna_hip_inject_wait_timeout: negative wait index");
+    return -1;
+  }
+  g_inject_wait_at.store(nth_wait == 0 ? 0 : g_waits.load() + nth_wait);
   return 0;
 }
 
@@ -394,9 +554,8 @@ int xdna_hip_event_record(void* event, void* stream) {
 }
 
 int xdna_hip_event_synchronize(void* event) {
-  const hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(event));
-  if (e != hipSuccess) return launch_failed("hipEventSynchronize", e);
-  return 0;
+  hipEvent_t ev = reinterpret_cast<hipEvent_t>(event);
+  return bounded_wait("an event", [&]() -> int { return poll_event(ev, "hipEventQuery"); });
 }
 
 int xdna_hip_event_query(void* event) {

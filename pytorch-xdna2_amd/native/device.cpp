@@ -102,6 +102,63 @@ ScopedCount::~ScopedCount() { count_call(name, now_ns() - t0); }
 
 void* current_stream() { return c10::hip::getCurrentHIPStream(0).stream(); }
 
+int64_t capture_tag() {
+  const int r = xdna_hip_stream_capturing(current_stream());
+  TORCH_CHECK(r >= 0, "xdna: capture status query failed: ", xdna_hip_last_error());
+  if (r == 0) return 0;
+  const int64_t pool = xdna_hip_cache_pool_current();
+  return pool != 0 ? pool : -1;
+}
+
+// ------------------------------------------------------------------------------------
+// Write epochs, keyed by the base address of the allocation a storage uses (all views,
+// `.data` aliases and ROCm aliases of one allocation share it).  A fresh epoch comes
+// from one counter, so no two writes anywhere share a value; an allocation never written
+// since it was made reads 0, and the caches also key on the storage itself.
+// ------------------------------------------------------------------------------------
+namespace {
+
+struct EpochTable {
+  std::mutex mu;
+  std::unordered_map<const void*, uint64_t> epoch;
+  uint64_t next = 0;
+};
+
+EpochTable& epochs() {
+  static auto* t = new EpochTable();  // never destroyed: frees can run at exit
+  return *t;
+}
+
+const void* allocation_base(const at::Tensor& t) {
+  if (!t.defined() || !t.has_storage()) return nullptr;
+  return t.storage().data();
+}
+
+void forget_epoch(const void* base) {
+  EpochTable& e = epochs();
+  std::lock_guard<std::mutex> lock(e.mu);
+  e.epoch.erase(base);
+}
+
+}  // namespace
+
+uint64_t write_epoch(const at::Tensor& t) {
+  const void* base = allocation_base(t);
+  if (!base) return 0;
+  EpochTable& e = epochs();
+  std::lock_guard<std::mutex> lock(e.mu);
+  auto it = e.epoch.find(base);
+  return it == e.epoch.end() ? 0 : it->second;
+}
+
+void bump_write_epoch(const at::Tensor& t) {
+  const void* base = allocation_base(t);
+  if (!base) return;
+  EpochTable& e = epochs();
+  std::lock_guard<std::mutex> lock(e.mu);
+  e.epoch[base] = ++e.next;
+}
+
 void check_abi(int rc, const char* what) {
   TORCH_CHECK(rc == 0, "xdna: ", what, " failed: ", xdna_hip_last_error());
 }
@@ -112,7 +169,9 @@ void check_abi(int rc, const char* what) {
 namespace {
 
 void xdna_delete(void* p) {
-  if (p) xdna_hip_cache_free(p);
+  if (!p) return;
+  forget_epoch(p);
+  xdna_hip_cache_free(p);
 }
 
 struct XdnaAllocator final : c10::Allocator {
@@ -313,6 +372,7 @@ const at::Tensor& resize_xdna_(const at::Tensor& self, c10::SymIntArrayRef size,
   if (impl->sizes() != sizes) impl->set_sizes_contiguous(sizes);
   if (fmt && *fmt != at::MemoryFormat::Preserve) impl->empty_tensor_restride(*fmt);
   ensure_storage(self);
+  bump_write_epoch(self);
   return self;
 }
 
@@ -330,6 +390,7 @@ at::Tensor& set_storage_offset_(at::Tensor& self, c10::Storage source, c10::SymI
     impl->set_sizes_contiguous(sz);
   }
   ensure_storage(self);
+  bump_write_epoch(self);
   return self;
 }
 
@@ -364,6 +425,7 @@ at::Tensor copy_from_xdna(const at::Tensor& self, const at::Tensor& dst, bool no
   ScopedCount sc("xdna.copy");
   if (self.numel() == 0) return dst;
   const at::Tensor& src = self;
+  if (dst.device().type() == kXdna) bump_write_epoch(dst);
   if (is_devmem(src) && is_devmem(dst)) {
     at::Tensor d = as_rocm(dst);
     d.copy_(as_rocm(src), non_blocking);
@@ -491,7 +553,10 @@ void xdna_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
 
   op.redispatchBoxed(c10::DispatchKeySet(c10::DispatchKey::CUDA), stack);
 
-  for (const auto& [alias, orig] : written) sync_back(alias, orig);
+  for (const auto& [alias, orig] : written) {
+    sync_back(alias, orig);
+    bump_write_epoch(orig);
+  }
   const size_t r = schema.returns().size();
   for (size_t j = 0; j < r; ++j) {
     c10::IValue& iv = (*stack)[stack->size() - r + j];
@@ -653,6 +718,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     d["learned_k"] = 0;
     return d;
   });
+  mod.def("set_wait_timeout_ms", [](int64_t ms) {
+    check_abi(xdna_hip_set_wait_timeout_ms(ms), "set_wait_timeout_ms");
+  });
+  mod.def("wait_timeout_ms", [] { return xdna_hip_wait_timeout_ms(); });
+  mod.def("max_wait_ms", [] { return xdna_hip_max_wait_ms(); });
+  mod.def("write_epoch", [](const at::Tensor& t) { return write_epoch(t); });
   mod.def("poisoned", [] { return xdna_hip_poisoned() != 0; });
   mod.def("inject_failure", [](int64_t n, bool poison) {
     check_abi(xdna_hip_inject_failure(n, poison ? 1 : 0), "inject_failure");

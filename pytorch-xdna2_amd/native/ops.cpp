@@ -5,6 +5,7 @@
 // kernels (torch_xdna_device.cpp:4524-4606, 4608-4885, 4360-4417, 3740-3790).
 #include "xdna.h"
 
+#include <ATen/MemoryOverlap.h>
 #include <ATen/native/Resize.h>
 #include <ATen/ops/_fused_adam_native.h>
 #include <ATen/ops/instance_norm_native.h>
@@ -82,14 +83,20 @@ bool conv_s2_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArray
 }
 
 // Prepared weights of frozen tensors (requires_grad false: a loss network's weights),
-// keyed by storage, offset, shape, version and direction, the role of the reference's
-// weight slots (torch_xdna_device.cpp:2208-2271).  A weak reference to the storage tells
-// a live tensor from a new one at a recycled address; in-place writes bump the version.
+// keyed by storage, data address, offset, shape, version, write epoch and direction, the
+// role of the reference's weight slots (torch_xdna_device.cpp:2208-2271, keyed on the
+// data pointer, version and write epoch).  A weak reference to the storage tells a live
+// tensor from a new one at a recycled address; in-place writes through autograd bump the
+// version, and every xdna write path (`.data` writes included) bumps the write epoch.
 // Trainable weights are prepared on every call: the optimizer changes them in place
-// (also inside replayed graphs, where no version is bumped).
+// (also inside replayed graphs, where no host code runs).  Entries carry the capture tag
+// they were made under and serve only the same tag: during a capture the frozen form is
+// prepared inside the graph, which then owns it and sees writes made between replays.
 struct PreparedWeights {
   c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
-  int64_t offset = 0, version = 0;
+  const void* data = nullptr;
+  int64_t offset = 0, version = 0, tag = 0;
+  uint64_t epoch = 0;
   std::array<int64_t, 4> sizes{};
   bool dgrad = false;
   at::Tensor wt;
@@ -124,12 +131,18 @@ bool weight_cacheable(const at::Tensor& w) {
 
 std::array<int64_t, 4> sizes4(const at::Tensor& w) { return {w.size(0), w.size(1), w.size(2), w.size(3)}; }
 
-at::Tensor cached_weights(const at::Tensor& w, bool dgrad) {
+bool same_weight(const PreparedWeights& e, const at::Tensor& w, bool dgrad, int64_t tag) {
+  return e.dgrad == dgrad && e.tag == tag && e.offset == w.storage_offset() && e.data == w.storage().data() &&
+         e.sizes == sizes4(w);
+}
+
+at::Tensor cached_weights(const at::Tensor& w, bool dgrad, int64_t tag) {
+  const uint64_t epoch = write_epoch(w);
   WeightCache& c = weight_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   const int64_t ver = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
   for (auto& e : c.entries) {
-    if (e.dgrad != dgrad || e.offset != w.storage_offset() || e.version != ver || e.sizes != sizes4(w)) continue;
+    if (!same_weight(e, w, dgrad, tag) || e.version != ver || e.epoch != epoch) continue;
     auto live = e.storage.lock();
     if (!live || live.get() != w.storage().unsafeGetStorageImpl()) continue;
     e.last_use = ++c.tick;
@@ -138,7 +151,8 @@ at::Tensor cached_weights(const at::Tensor& w, bool dgrad) {
   return at::Tensor();
 }
 
-void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
+void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt, int64_t tag) {
+  const uint64_t epoch = write_epoch(w);
   WeightCache& c = weight_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   // drop entries of dead storages, then the least recently used one when full
@@ -150,17 +164,19 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
                                 [](const auto& a, const auto& b) { return a.last_use < b.last_use; });
     c.entries.erase(lru);
   }
-  // an entry for the same tensor and direction (an older version) is replaced
+  // an entry for the same tensor, direction and tag (an older version) is replaced
   const auto same = [&](const PreparedWeights& e) {
     auto live = e.storage.lock();
-    return e.dgrad == dgrad && e.offset == w.storage_offset() && e.sizes == sizes4(w) && live &&
-           live.get() == w.storage().unsafeGetStorageImpl();
+    return same_weight(e, w, dgrad, tag) && live && live.get() == w.storage().unsafeGetStorageImpl();
   };
   c.entries.erase(std::remove_if(c.entries.begin(), c.entries.end(), same), c.entries.end());
   PreparedWeights e;
   e.storage = c10::weak_intrusive_ptr<c10::StorageImpl>(w.storage().getWeakStorageImpl());
+  e.data = w.storage().data();
   e.offset = w.storage_offset();
   e.version = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
+  e.epoch = epoch;
+  e.tag = tag;
   e.sizes = sizes4(w);
   e.dgrad = dgrad;
   e.wt = wt;
@@ -197,13 +213,17 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor wc = w.contiguous();
   void* st = current_stream();
-  // Frozen weights: both forms cached by storage and version.  Trainable weights: the
-  // forward prepares the input gradient's form in the same launch and leaves it in the
-  // cache under the weight's current version, where the backward of the same step finds
-  // it (an optimizer step bumps the version; a stale entry is never read).
-  const bool cacheable = weight_cacheable(w);
+  // Frozen weights: both forms cached by storage, version and write epoch, outside
+  // captures.  Trainable weights: the forward prepares the input gradient's form in the
+  // same launch and leaves it in the cache under the weight's current version, epoch and
+  // capture tag, where the backward of the same step finds it (an optimizer step bumps
+  // the epoch; a stale entry is never read).
+  const int64_t tag = capture_tag();
+  const bool cacheable = weight_cacheable(w) && tag == 0;
   const bool trainable = w.requires_grad() && !w.is_inference();
-  at::Tensor wt = cacheable || (trainable && dgrad) ? cached_weights(w, dgrad) : at::Tensor();
+  at::Tensor wt = cacheable || (trainable && dgrad) ? cached_weights(w, dgrad, tag) : at::Tensor();
+  // prepare / hit counters (the reference's npu_conv3x3w.weights{,_hit})
+  count_call(wt.defined() ? "hip_conv3x3.weights_hit" : "hip_conv3x3.weights", 0);
   if (!wt.defined()) {
     wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
     if (trainable && !dgrad) {
@@ -213,13 +233,13 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
                                                        static_cast<uint16_t*>(wtd.data_ptr()), int(w.size(0)),
                                                        int(w.size(1)), st),
                 "conv weights");
-      remember_weights(w, true, wtd);
+      remember_weights(w, true, wtd, tag);
     } else {
       check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
                                                   static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
                                                   int(w.size(1)), dgrad ? 1 : 0, st),
                 "conv weights");
-      if (cacheable) remember_weights(w, dgrad, wt);
+      if (cacheable) remember_weights(w, dgrad, wt, tag);
     }
   }
   at::Tensor out = empty_xdna({B, cout, H, W}, at::kBFloat16);
@@ -242,13 +262,17 @@ at::Tensor hip_conv(const at::Tensor& src, const at::Tensor& w, const at::Tensor
 }
 
 // Packed inputs of forward convs kept for the rows weight gradient of the same layer, so
-// that the backward does not pack x again.  Keyed by the input's storage, offset, sizes,
-// strides and version (autograd keeps the input alive and unchanged until the backward);
-// the backward takes its entry out.  Entries whose input storage has died are dropped,
-// and the oldest go once the kept bytes pass a cap.
+// that the backward does not pack x again.  Keyed by the input's storage, data address,
+// offset, sizes, strides, version, write epoch and capture tag (autograd keeps the input
+// alive and unchanged until the backward; a pack kept outside a capture is never read
+// by a captured backward, nor the reverse); the backward takes its entry out.  Entries
+// whose input storage has died are dropped, and the oldest go once the kept bytes pass
+// a cap.
 struct PackedInput {
   c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
-  int64_t offset = 0, version = 0;
+  const void* data = nullptr;
+  int64_t offset = 0, version = 0, tag = 0;
+  uint64_t epoch = 0;
   std::vector<int64_t> sizes, strides;
   int layout = 0;
   at::Tensor packed;
@@ -266,8 +290,9 @@ PackedInputCache& packed_input_cache() {
   return *c;
 }
 
-bool same_input(const PackedInput& e, const at::Tensor& x, int layout) {
-  if (e.layout != layout || e.offset != x.storage_offset() || e.sizes != x.sizes().vec() || e.strides != x.strides().vec() ||
+bool same_input(const PackedInput& e, const at::Tensor& x, int layout, int64_t tag, uint64_t epoch) {
+  if (e.layout != layout || e.tag != tag || e.epoch != epoch || e.data != x.storage().data() ||
+      e.offset != x.storage_offset() || e.sizes != x.sizes().vec() || e.strides != x.strides().vec() ||
       e.version != int64_t(x.unsafeGetTensorImpl()->version_counter().current_version()))
     return false;
   auto live = e.storage.lock();
@@ -275,10 +300,12 @@ bool same_input(const PackedInput& e, const at::Tensor& x, int layout) {
 }
 
 void remember_packed_input(const at::Tensor& x, const at::Tensor& packed, int layout) {
+  const int64_t tag = capture_tag();
+  const uint64_t epoch = write_epoch(x);
   PackedInputCache& c = packed_input_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   for (auto it = c.entries.begin(); it != c.entries.end();) {
-    if (it->storage.expired() || same_input(*it, x, layout)) {
+    if (it->storage.expired() || same_input(*it, x, layout, tag, epoch)) {
       c.bytes -= size_t(it->packed.nbytes());
       it = c.entries.erase(it);
     } else {
@@ -287,8 +314,11 @@ void remember_packed_input(const at::Tensor& x, const at::Tensor& packed, int la
   }
   PackedInput e;
   e.storage = c10::weak_intrusive_ptr<c10::StorageImpl>(x.storage().getWeakStorageImpl());
+  e.data = x.storage().data();
   e.offset = x.storage_offset();
   e.version = int64_t(x.unsafeGetTensorImpl()->version_counter().current_version());
+  e.tag = tag;
+  e.epoch = epoch;
   e.sizes = x.sizes().vec();
   e.strides = x.strides().vec();
   e.layout = layout;
@@ -303,10 +333,12 @@ void remember_packed_input(const at::Tensor& x, const at::Tensor& packed, int la
 
 at::Tensor take_packed_input(const at::Tensor& x, int layout) {
   if (x.is_inference()) return at::Tensor();
+  const int64_t tag = capture_tag();
+  const uint64_t epoch = write_epoch(x);
   PackedInputCache& c = packed_input_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   for (auto it = c.entries.begin(); it != c.entries.end(); ++it) {
-    if (!same_input(*it, x, layout)) continue;
+    if (!same_input(*it, x, layout, tag, epoch)) continue;
     at::Tensor p = it->packed;
     c.bytes -= size_t(p.nbytes());
     c.entries.erase(it);
@@ -714,7 +746,39 @@ at::Tensor mm_xdna(const at::Tensor& a, const at::Tensor& b) {
   return back(at::_ops::mm::call(rocm(a), rocm(b)));
 }
 
+// Whether an out= argument can take the product directly: an xdna bf16 tensor (already
+// resized to the result's shape) with no internal overlap and no memory shared with any
+// operand.  Otherwise the product goes to a new tensor and is copied (the reference's
+// prepare_out_xdna / copy, torch_xdna_device.cpp:3500-3524).
+// Whether `out` and an operand use the same allocation (conservative: any overlap of
+// storages, whatever the strides).
+bool shares_memory(const at::Tensor& out, std::initializer_list<const at::Tensor*> operands) {
+  if (!out.has_storage() || out.storage().nbytes() == 0) return false;
+  for (const at::Tensor* t : operands)
+    if (t->defined() && t->has_storage() && t->storage().data() == out.storage().data()) return true;
+  return false;
+}
+
+bool out_direct_ok(const at::Tensor& out, std::initializer_list<const at::Tensor*> operands) {
+  if (out.device().type() != kXdna || out.scalar_type() != at::kBFloat16 || !fits_int(out)) return false;
+  if (at::has_internal_overlap(out) != at::MemOverlap::No) return false;
+  return !shares_memory(out, operands);
+}
+
 at::Tensor& mm_out_xdna(const at::Tensor& a, const at::Tensor& b, at::Tensor& out) {
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2, "mm: expected 2-D tensors");
+  TORCH_CHECK(a.size(1) == b.size(0), "mm: mat1 and mat2 shapes cannot be multiplied (",
+              a.size(0), "x", a.size(1), " and ", b.size(0), "x", b.size(1), ")");
+  // operands are checked for shared memory before the resize, which could move it
+  if (gemm_dtype_ok({&a, &b}) && fits_int(a) && fits_int(b) && !shares_memory(out, {&a, &b})) {
+    at::native::resize_output(out, {a.size(0), b.size(1)});
+    if (out_direct_ok(out, {&a, &b})) {
+      ScopedCount sc("hip_gemm.mm_out.run");
+      run_gemm(a, b, out, nullptr, 1.0f, 0.0f);
+      bump_write_epoch(out);
+      return out;
+    }
+  }
   at::Tensor r = mm_xdna(a, b);
   at::native::resize_output(out, r.sizes());
   out.copy_(r);
@@ -742,6 +806,23 @@ at::Tensor addmm_xdna(const at::Tensor& self, const at::Tensor& a, const at::Ten
 
 at::Tensor& addmm_out_xdna(const at::Tensor& self, const at::Tensor& a, const at::Tensor& b,
                            const at::Scalar& beta, const at::Scalar& alpha, at::Tensor& out) {
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2, "addmm: expected 2-D matrices");
+  TORCH_CHECK(a.size(1) == b.size(0), "addmm: mat1 and mat2 shapes cannot be multiplied (",
+              a.size(0), "x", a.size(1), " and ", b.size(0), "x", b.size(1), ")");
+  const int64_t M = a.size(0), N = b.size(1);
+  const bool self_ok = self.dim() <= 2 && self.scalar_type() == at::kBFloat16 &&
+                       self.device().type() == kXdna && at::is_expandable_to(self.sizes(), {M, N});
+  // out sharing memory with an operand (self included: out = self is common) takes the
+  // copy path; checked before the resize, which could move that memory
+  if (gemm_dtype_ok({&a, &b}) && self_ok && fits_int(a) && fits_int(b) && !shares_memory(out, {&a, &b, &self})) {
+    at::native::resize_output(out, {M, N});
+    if (out_direct_ok(out, {&a, &b, &self})) {
+      ScopedCount sc("hip_gemm.addmm_out.run");
+      run_gemm(a, b, out, &self, alpha.to<float>(), beta.to<float>());
+      bump_write_epoch(out);
+      return out;
+    }
+  }
   at::Tensor r = addmm_xdna(self, a, b, beta, alpha);
   at::native::resize_output(out, r.sizes());
   out.copy_(r);
@@ -763,6 +844,17 @@ at::Tensor bmm_xdna(const at::Tensor& a, const at::Tensor& b) {
 }
 
 at::Tensor& bmm_out_xdna(const at::Tensor& a, const at::Tensor& b, at::Tensor& out) {
+  TORCH_CHECK(a.dim() == 3 && b.dim() == 3, "batch1 and batch2 must be 3D tensors");
+  TORCH_CHECK(a.size(0) == b.size(0) && a.size(2) == b.size(1), "bmm: shape mismatch");
+  if (gemm_dtype_ok({&a, &b}) && fits_int(a) && fits_int(b) && a.size(0) <= 65535 && !shares_memory(out, {&a, &b})) {
+    at::native::resize_output(out, {a.size(0), a.size(1), b.size(2)});
+    if (out_direct_ok(out, {&a, &b})) {
+      ScopedCount sc("hip_gemm.bmm_out.run");
+      run_gemm(a, b, out, nullptr, 1.0f, 0.0f);
+      bump_write_epoch(out);
+      return out;
+    }
+  }
   at::Tensor r = bmm_xdna(a, b);
   at::native::resize_output(out, r.sizes());
   out.copy_(r);
@@ -803,16 +895,33 @@ std::vector<at::Tensor> rocm_list(at::TensorList l) {
   return out;
 }
 
+// The lists a fused step writes: parameters, moments (max_exp_avg_sqs with amsgrad) and,
+// with a grad scale, the unscaled gradients.
+void bump_adam_epochs(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
+                      at::TensorList mx, bool amsgrad, bool grads_written) {
+  for (const at::TensorList& l : {p, m, v})
+    for (const auto& t : l) bump_write_epoch(t);
+  if (amsgrad)
+    for (const auto& t : mx) bump_write_epoch(t);
+  if (grads_written)
+    for (const auto& t : g) bump_write_epoch(t);
+}
+
+// lr is a host double, or a device scalar (`lr_t`, the tensor-lr overloads) read by the
+// kernel, so no host synchronization happens and the step can be captured.
 void fused_adam_common(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
-                       at::TensorList mx, at::TensorList steps, double lr, double beta1,
-                       double beta2, double wd, double eps, bool amsgrad, bool maximize,
+                       at::TensorList mx, at::TensorList steps, double lr, const at::Tensor* lr_t,
+                       double beta1, double beta2, double wd, double eps, bool amsgrad, bool maximize,
                        const std::optional<at::Tensor>& grad_scale,
                        const std::optional<at::Tensor>& found_inf, bool adamw) {
   int dtype = 1;
   const bool scalars_ok =
       (!grad_scale || (grad_scale->device().type() == kXdna && grad_scale->scalar_type() == at::kFloat)) &&
       (!found_inf || (found_inf->device().type() == kXdna && found_inf->scalar_type() == at::kFloat));
-  if (scalars_ok && adam_eligible(p, g, m, v, mx, steps, amsgrad, dtype)) {
+  const bool lr_ok = !lr_t || (lr_t->device().type() == kXdna && lr_t->numel() == 1 &&
+                               (lr_t->scalar_type() == at::kFloat || lr_t->scalar_type() == at::kDouble));
+  bump_adam_epochs(p, g, m, v, mx, amsgrad, grad_scale.has_value());
+  if (scalars_ok && lr_ok && adam_eligible(p, g, m, v, mx, steps, amsgrad, dtype)) {
     ScopedCount sc(adamw ? "hip_adamw.run" : "hip_adam.run");
     const size_t n = p.size();
     std::vector<void*> pp(n), gp(n), mp(n), vp(n), xp(n);
@@ -831,20 +940,34 @@ void fused_adam_common(at::TensorList p, at::TensorList g, at::TensorList m, at:
     for (size_t i = 0; i < n; ++i)
       bytes += double(numel[i]) * double(p[i].element_size()) * (amsgrad ? 9.0 : 7.0);
     KernelTimer kt("fused_adam", bytes);
-    check_abi(xdna_fused_adam(int(n), pp.data(), gp.data(), mp.data(), vp.data(),
-                              amsgrad ? xp.data() : nullptr, sp.data(), numel.data(), dtype, lr, beta1,
-                              beta2, wd, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, adamw ? 1 : 0,
-                              grad_scale ? static_cast<const float*>(grad_scale->const_data_ptr()) : nullptr,
-                              found_inf ? static_cast<const float*>(found_inf->const_data_ptr()) : nullptr,
-                              current_stream()),
-              "fused adam");
+    const float* gsp = grad_scale ? static_cast<const float*>(grad_scale->const_data_ptr()) : nullptr;
+    const float* fip = found_inf ? static_cast<const float*>(found_inf->const_data_ptr()) : nullptr;
+    if (lr_t)
+      check_abi(xdna_fused_adam_tensor_lr(int(n), pp.data(), gp.data(), mp.data(), vp.data(),
+                                          amsgrad ? xp.data() : nullptr, sp.data(), numel.data(), dtype,
+                                          lr_t->const_data_ptr(), lr_t->scalar_type() == at::kFloat ? 1 : 2,
+                                          beta1, beta2, wd, eps, amsgrad ? 1 : 0, maximize ? 1 : 0,
+                                          adamw ? 1 : 0, gsp, fip, current_stream()),
+                "fused adam (tensor lr)");
+    else
+      check_abi(xdna_fused_adam(int(n), pp.data(), gp.data(), mp.data(), vp.data(),
+                                amsgrad ? xp.data() : nullptr, sp.data(), numel.data(), dtype, lr, beta1,
+                                beta2, wd, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, adamw ? 1 : 0, gsp, fip,
+                                current_stream()),
+                "fused adam");
     return;
   }
   ScopedCount sc("aten::_fused_adam_.rocm");
   BelowAutograd guard;
   auto rp = rocm_list(p), rg = rocm_list(g), rm = rocm_list(m), rv = rocm_list(v), rx = rocm_list(mx),
        rs = rocm_list(steps);
-  if (adamw)
+  if (lr_t && adamw)
+    at::_ops::_fused_adamw__tensor_lr::call(rp, rg, rm, rv, rx, rs, rocm(*lr_t), beta1, beta2, wd, eps, amsgrad,
+                                            maximize, rocm(grad_scale), rocm(found_inf));
+  else if (lr_t)
+    at::_ops::_fused_adam__tensor_lr::call(rp, rg, rm, rv, rx, rs, rocm(*lr_t), beta1, beta2, wd, eps, amsgrad,
+                                           maximize, rocm(grad_scale), rocm(found_inf));
+  else if (adamw)
     at::_ops::_fused_adamw_::call(rp, rg, rm, rv, rx, rs, lr, beta1, beta2, wd, eps, amsgrad, maximize,
                                   rocm(grad_scale), rocm(found_inf));
   else
@@ -857,7 +980,7 @@ void fused_adam_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::T
                      double wd, double eps, bool amsgrad, bool maximize,
                      const std::optional<at::Tensor>& grad_scale,
                      const std::optional<at::Tensor>& found_inf) {
-  fused_adam_common(p, g, m, v, mx, steps, lr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
+  fused_adam_common(p, g, m, v, mx, steps, lr, nullptr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
                     found_inf, false);
 }
 
@@ -866,13 +989,14 @@ void fused_adamw_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::
                       double wd, double eps, bool amsgrad, bool maximize,
                       const std::optional<at::Tensor>& grad_scale,
                       const std::optional<at::Tensor>& found_inf) {
-  fused_adam_common(p, g, m, v, mx, steps, lr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
+  fused_adam_common(p, g, m, v, mx, steps, lr, nullptr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
                     found_inf, true);
 }
 
 // torch._foreach_add_(state_steps, 1) before every fused Adam step: one HIP launch for
 // the whole list of fp32 xdna tensors; other forms go to PyTorch-ROCm on aliases.
 void foreach_add_scalar_xdna(at::TensorList self, const at::Scalar& scalar) {
+  for (const auto& t : self) bump_write_epoch(t);
   bool ok = g_mode.load() >= 1 && !scalar.isComplex();
   for (const auto& t : self)
     ok = ok && t.defined() && t.device().type() == kXdna && t.scalar_type() == at::kFloat && t.is_contiguous();
@@ -894,15 +1018,13 @@ void foreach_add_scalar_xdna(at::TensorList self, const at::Scalar& scalar) {
   at::_ops::_foreach_add__Scalar::call(rocm_list(self), scalar);
 }
 
-double lr_value(const at::Tensor& lr) { return lr.item<double>(); }
-
 void fused_adam_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
                          at::TensorList mx, at::TensorList steps, const at::Tensor& lr, double beta1,
                          double beta2, double wd, double eps, bool amsgrad, bool maximize,
                          const std::optional<at::Tensor>& grad_scale,
                          const std::optional<at::Tensor>& found_inf) {
-  fused_adam_common(p, g, m, v, mx, steps, lr_value(lr), beta1, beta2, wd, eps, amsgrad, maximize,
-                    grad_scale, found_inf, false);
+  fused_adam_common(p, g, m, v, mx, steps, 0.0, &lr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
+                    found_inf, false);
 }
 
 void fused_adamw_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorList v,
@@ -910,8 +1032,8 @@ void fused_adamw_tlr_xdna(at::TensorList p, at::TensorList g, at::TensorList m, 
                           double beta2, double wd, double eps, bool amsgrad, bool maximize,
                           const std::optional<at::Tensor>& grad_scale,
                           const std::optional<at::Tensor>& found_inf) {
-  fused_adam_common(p, g, m, v, mx, steps, lr_value(lr), beta1, beta2, wd, eps, amsgrad, maximize,
-                    grad_scale, found_inf, true);
+  fused_adam_common(p, g, m, v, mx, steps, 0.0, &lr, beta1, beta2, wd, eps, amsgrad, maximize, grad_scale,
+                    found_inf, true);
 }
 
 struct TimedLaunch {

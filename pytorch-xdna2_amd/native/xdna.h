@@ -51,6 +51,22 @@ extern std::atomic<int> g_wgrad_form;
 // Row layout of the 3x3 conv operands: 1 (default) tight strips, 0 the reference's layout.
 extern std::atomic<int> g_conv_layout;
 
+// Write epochs of device allocations (the reference's per-allocation write epoch,
+// torch_xdna_device.cpp:493, 576, 620-633, 2222).  Every xdna write path bumps the epoch
+// of the allocation it writes: hot-op out= arguments, the arguments the boxed fallback
+// writes, copies, resize_ and set_, the fused optimizer steps.  Unlike the version
+// counter, this also sees writes through `.data` aliases.  Caches of derived device
+// buffers (prepared weights, kept packs) key on it.  Writes made by replaying a captured
+// graph run no host code and bump nothing.
+uint64_t write_epoch(const at::Tensor& t);
+void bump_write_epoch(const at::Tensor& t);
+
+// Tag of the capture the calling thread is in: 0 when the current stream is not
+// capturing, else the private pool the captured allocations come from (-1 without one).
+// Host caches of device buffers serve only entries made under the same tag, so a graph
+// never reads a buffer it does not own.
+int64_t capture_tag();
+
 // Per-path counters (the reference's ScopedMappedCpu, torch_xdna_device.cpp:1470-1521).
 void count_call(const char* name, int64_t ns);
 

@@ -16,6 +16,7 @@ from .device import (
     is_available,
     is_xrt_backed,
     mapped_cpu_stats,
+    max_wait_ms,
     native_library_path,
     npu_mode,
     register_xdna_device,
@@ -24,6 +25,7 @@ from .device import (
     set_general_conv_mode,
     set_conv_layout,
     set_npu_mode,
+    set_wait_timeout_ms,
     set_wgrad_form,
     synchronize,
     try_register_xdna_device,
@@ -56,6 +58,8 @@ __all__ = [
     "conv_layout",
     "wgrad_form",
     "wait_for_builds",
+    "set_wait_timeout_ms",
+    "max_wait_ms",
     "reset_fallback_stats",
     "fallback_stats",
     "mapped_cpu_stats",

@@ -35,17 +35,16 @@ def _release(cuda_graph, pool: int) -> None:
     try:
         cuda_graph.reset()
     finally:
-        if _device._C is not None:
-            _device._C.pool_release(pool)
+        _device.native().pool_release(pool)
 
 
 class Graph:
     """A captured sequence of xdna (and PyTorch-ROCm) work, replayed with ``replay()``."""
 
     def __init__(self):
-        _device.register_xdna_device()
+        ext = _device.native()
         self._cuda = torch.cuda.CUDAGraph()
-        self._pool = int(_device._C.pool_create())
+        self._pool = int(ext.pool_create())
         self._release = weakref.finalize(self, _release, self._cuda, self._pool)
 
     @property
@@ -69,13 +68,13 @@ def graph(g: Graph, stream: torch.cuda.Stream | None = None, capture_error_mode:
         raise TypeError("torch.xdna.graph expects a torch.xdna.Graph")
     _device.synchronize()
     with torch.cuda.graph(g._cuda, stream=stream, capture_error_mode=capture_error_mode):
-        _device._C.pool_begin(g.pool)
+        _device.native().pool_begin(g.pool)
         try:
             yield g
         finally:
-            _device._C.pool_end()
+            _device.native().pool_end()
 
 
 # torch.xdna.Graph / torch.xdna.graph, next to torch.xdna.synchronize and the others
-_device._XdnaDeviceModule.Graph = Graph
-_device._XdnaDeviceModule.graph = staticmethod(graph)
+_device._device_module.Graph = Graph
+_device._device_module.graph = graph

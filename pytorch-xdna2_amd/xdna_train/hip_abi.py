@@ -59,6 +59,12 @@ SIGNATURES = {
     "xdna_hip_event_query": (I, [P]),
     "xdna_hip_event_elapsed_ms": (I, [P, P, ctypes.POINTER(F)]),
     "xdna_hip_stream_wait_event": (I, [P, P]),
+    "xdna_hip_cache_pool_current": (L, []),
+    "xdna_hip_stream_capturing": (I, [P]),
+    "xdna_hip_set_wait_timeout_ms": (I, [L]),
+    "xdna_hip_wait_timeout_ms": (L, []),
+    "xdna_hip_max_wait_ms": (D, []),
+    "xdna_hip_inject_wait_timeout": (I, [L]),
     "xdna_conv3x3w_pack_input_bf16": (I, [P, P, I, I, I, I, I, P]),
     "xdna_conv3x3w_pack_input_range_bf16": (I, [P, P, I, I, I, I, I, I, I, P]),
     "xdna_conv3x3w_pack_input_strips_range_bf16": (I, [P, P, I, I, I, I, I, I, I, I, I, I, P]),
@@ -108,6 +114,7 @@ SIGNATURES = {
     "xdna_batch_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
     "xdna_foreach_add_scalar_f32": (I, [I, PP, PL, ctypes.c_float, P]),
     "xdna_fused_adam": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, D, D, D, D, D, I, I, I, P, P, P]),
+    "xdna_fused_adam_tensor_lr": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, P, I, D, D, D, D, I, I, I, P, P, P]),
 }
 
 _lib = None

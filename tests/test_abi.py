@@ -75,6 +75,52 @@ def test_injected_failure_and_poisoning():
     assert lib.xdna_hip_poisoned() == 0
 
 
+def test_injected_wait_timeout_is_distinct_and_poisons():
+    """The dispatch deadline (xrt_shim.cpp:57-90, 174-233): a wait past it returns -2, not
+    the error status -1, names what it waited for, and poisons the process.  Forced from
+    the host by the injection hook: the injected wait never touches the device."""
+    lib = hip_abi.load()
+    lib.xdna_hip_reset_failure_state()
+    cases = [(lambda: lib.xdna_hip_stream_synchronize(None), "the stream"),
+             (lambda: lib.xdna_hip_device_synchronize(), "the device"),
+             (lambda: lib.xdna_hip_event_synchronize(None), "an event")]
+    try:
+        for wait, what in cases:
+            assert lib.xdna_hip_inject_wait_timeout(1) == 0
+            assert wait() == -2
+            msg = hip_abi.last_error()
+            assert msg.startswith("deadline:") and what in msg and "poisoned" in msg
+            assert lib.xdna_hip_poisoned() == 1
+            # poisoned: launches are refused, frees leak
+            assert lib.xdna_conv3x3w_pack_input_bf16(None, None, 1, 1, 1, 1, 1, None) == -1
+            assert "poisoned" in hip_abi.last_error()
+            lib.xdna_hip_reset_failure_state()
+        # the n-th wait from now, not the next one: a 0 disables it again
+        assert lib.xdna_hip_inject_wait_timeout(0) == 0
+        assert lib.xdna_hip_inject_wait_timeout(-1) == -1
+    finally:
+        lib.xdna_hip_reset_failure_state()
+    assert lib.xdna_hip_poisoned() == 0
+
+
+def test_wait_deadline_setting_and_real_waits_are_not_timeouts():
+    lib = hip_abi.load()
+    old = lib.xdna_hip_wait_timeout_ms()
+    try:
+        assert lib.xdna_hip_set_wait_timeout_ms(250) == 0
+        assert lib.xdna_hip_wait_timeout_ms() == 250
+        assert lib.xdna_hip_set_wait_timeout_ms(-5) == -1
+    finally:
+        lib.xdna_hip_set_wait_timeout_ms(old)
+    # without injection a wait either completes (GPU present) or fails as an error (no
+    # device here): never a timeout
+    lib.xdna_hip_reset_failure_state()
+    try:
+        assert lib.xdna_hip_stream_synchronize(None) in (0, -1)
+    finally:
+        lib.xdna_hip_reset_failure_state()
+
+
 def test_error_message_is_thread_local():
     import threading
 

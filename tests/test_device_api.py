@@ -1,6 +1,7 @@
 """Host-side API of the xdna device (no GPU needed): registration on import, the
 torch.xdna module and the reference's public functions (xdna_train/__init__.py:3-50),
-the fused-optimizer pre-hook's selection rule (device.py:408-436)."""
+the fused-optimizer pre-hook's selection rule (device.py:408-436), parameter identity
+across Module.to("xdna") (device.py:355-405)."""
 from types import SimpleNamespace
 
 import torch
@@ -37,12 +38,12 @@ def test_mode_switch():
 
 
 def test_device_index_rules():
-    assert dev._device_index(None) == 0
-    assert dev._device_index("xdna") == 0
-    assert dev._device_index("xdna:0") == 0
+    assert dev._xdna_index(None) == 0
+    assert dev._xdna_index("xdna") == 0
+    assert dev._xdna_index("xdna:0") == 0
     for bad in ("xdna:1", "cpu", 3):
         try:
-            dev._device_index(bad)
+            dev._xdna_index(bad)
         except ValueError:
             continue
         raise AssertionError(bad)
@@ -68,10 +69,39 @@ def test_prefer_fused_optimizer_rule():
               {"params": [_fake_param("xdna")], "fused": None, "foreach": False},
               {"params": [_fake_param("xdna", floating=False)], "fused": None, "foreach": None}]
     opt = SimpleNamespace(param_groups=groups, state={})
-    dev._prefer_fused_optimizer(opt, (), {})
+    dev._default_fused_step(opt, (), {})
     assert groups[0]["fused"] is True
     assert groups[1]["fused"] is None and groups[2]["fused"] is None and groups[3]["fused"] is None
     # decided once: later calls do nothing
     groups[1]["params"] = [_fake_param("xdna")]
-    dev._prefer_fused_optimizer(opt, (), {})
+    dev._default_fused_step(opt, (), {})
     assert groups[1]["fused"] is None
+
+
+def test_module_move_keeps_parameters_only_for_xdna():
+    """The move methods are wrapped once, and the swap switch is on only while a move
+    targets xdna (checked without device memory: the target parser alone)."""
+    for name in ("to", "to_empty", "xdna"):
+        assert hasattr(getattr(torch.nn.Module, name), "__xdna_original__"), name
+    assert dev._targets_xdna(dev._PARAM_MOVES["to"], ("xdna",), {})
+    assert dev._targets_xdna(dev._PARAM_MOVES["to"], (torch.device("xdna:0"),), {})
+    assert not dev._targets_xdna(dev._PARAM_MOVES["to"], (torch.bfloat16,), {})
+    assert not dev._targets_xdna(dev._PARAM_MOVES["to"], ("cpu",), {})
+    assert dev._targets_xdna(dev._PARAM_MOVES["to_empty"], (), {"device": "xdna"})
+    assert not dev._targets_xdna(dev._PARAM_MOVES["to"], ("no such device",), {})
+    # a CPU move leaves the switch as it was
+    before = torch.__future__.get_swap_module_params_on_conversion()
+    m = torch.nn.Linear(2, 2)
+    m.to(torch.float64)
+    assert torch.__future__.get_swap_module_params_on_conversion() == before
+    assert m.weight.dtype == torch.float64
+
+
+def test_wait_deadline_setting():
+    old = xdna_train.device.native().wait_timeout_ms()
+    try:
+        xdna_train.set_wait_timeout_ms(1234)
+        assert xdna_train.device.native().wait_timeout_ms() == 1234
+    finally:
+        xdna_train.set_wait_timeout_ms(old)
+    assert xdna_train.max_wait_ms() >= 0.0
