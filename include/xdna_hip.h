@@ -409,6 +409,23 @@ int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uin
  * knob).  XDNA_GEMM_VARIANT sets the initial value. */
 int xdna_gemm_set_variant(int variant);
 
+/* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, kernels and results, bit for bit; it calls no
+ * hipMalloc, hipFree or allocating routine.  The split-K fp32 partials, the only device
+ * memory the product needs beyond its operands, live in a library-owned device array of
+ * XDNA_GEMM_NOALLOC_SCRATCH_BYTES per GPU, held from the first call until the process
+ * ends.  A product whose partials need more returns -1 before anything is launched (use
+ * xdna_gemm_bf16 for it).  All calls on one GPU share that array, which keeps the last
+ * call's contents: calls that can overlap on one GPU (other streams, other threads)
+ * race; calls ordered on one stream do not. */
+#define XDNA_GEMM_NOALLOC_SCRATCH_BYTES (64u << 20)
+int xdna_gemm_bf16_noalloc(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uint16_t* bias,
+                           int batch, int M, int N, int K, int64_t lda_m, int64_t lda_k, int64_t stride_a,
+                           int64_t ldb_k, int64_t ldb_n, int64_t stride_b, int64_t ldc_m, int64_t ldc_n,
+                           int64_t stride_c, int bias_mode, int64_t bias_sm, int64_t bias_sn, float alpha,
+                           float beta, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused Adam / AdamW: replaces torch._fused_adam_ reached through the        */
 /* boxed CPU fallback (xdna_cpu_fallback, torch_xdna_device.cpp:5273-5295;    */

@@ -15,6 +15,8 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
+#include <string>
 #include "../../include/xdna_hip.h"
 
 namespace xdna {
@@ -730,25 +732,78 @@ void launch_b(int mb, dim3 grid, hipStream_t st, const GemmArgs& g) {
   else gemm_kernel<MA, kScalar><<<grid, 256, 0, st>>>(g);
 }
 
-}  // namespace
-}  // namespace xdna
+// Device scratch of xdna_gemm_bf16_noalloc: its split-K partials live here instead of in
+// blocks of the caching allocator.  Each GPU the library runs on holds its own copy until
+// the process ends; host code reaches it only through the per-device address that
+// hipGetSymbolAddress returns (the array's name is a host-side stand-in, not a device
+// address).  Every split writes all of its slab before the reduce reads it, so nothing
+// has to be cleared between calls.
+static __device__ __align__(256) float scratch[XDNA_GEMM_NOALLOC_SCRATCH_BYTES / sizeof(float)];
 
-using namespace xdna;
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxScratchDevices] = {};
 
-extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C,
-                              const uint16_t* bias, int batch, int M, int N, int K, int64_t lda_m,
-                              int64_t lda_k, int64_t stride_a, int64_t ldb_k, int64_t ldb_n,
-                              int64_t stride_b, int64_t ldc_m, int64_t ldc_n, int64_t stride_c,
-                              int bias_mode, int64_t bias_sm, int64_t bias_sn, float alpha,
-                              float beta, void* stream) {
+// The current device's copy of `scratch`, looked up once per device with that device
+// current.  NULL (error set) when the lookup fails.
+float* scratch_of_current_device() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    launch_failed("xdna_gemm_bf16_noalloc: hipGetDevice", e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("xdna_gemm_bf16_noalloc: device index beyond the scratch table");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      launch_failed("xdna_gemm_bf16_noalloc: hipGetSymbolAddress(scratch)", e != hipSuccess ? e : hipErrorUnknown);
+      return nullptr;
+    }
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  return g_scratch[dev];
+}
+
+// Where one call's split-K partials come from: the caching allocator (xdna_gemm_bf16) or
+// the fixed device scratch (xdna_gemm_bf16_noalloc, `scratch` non-null).
+struct PartialsSource {
+  const char* who;
+  float* scratch;
+  float* take(size_t bytes) const {
+    if (!scratch) return static_cast<float*>(xdna_hip_cache_alloc(bytes));
+    if (bytes > size_t(XDNA_GEMM_NOALLOC_SCRATCH_BYTES)) {
+      set_error(std::string(who) + ": the split-K partials of this product need " + std::to_string(bytes) +
+                " bytes, above the " + std::to_string(size_t(XDNA_GEMM_NOALLOC_SCRATCH_BYTES)) +
+                "-byte scratch (use xdna_gemm_bf16)");
+      return nullptr;
+    }
+    return scratch;
+  }
+  // stream-ordered reuse: the next user of a cache block runs after the reduce
+  void give_back(float* p) const {
+    if (!scratch && p) xdna_hip_cache_free(p);
+  }
+};
+
+int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, uint16_t* C,
+             const uint16_t* bias, int batch, int M, int N, int K, int64_t lda_m, int64_t lda_k,
+             int64_t stride_a, int64_t ldb_k, int64_t ldb_n, int64_t stride_b, int64_t ldc_m,
+             int64_t ldc_n, int64_t stride_c, int bias_mode, int64_t bias_sm, int64_t bias_sn,
+             float alpha, float beta, void* stream) {
   if (batch < 0 || M < 0 || N < 0 || K < 0 || bias_mode < 0 || bias_mode > 3 ||
       (bias_mode && !bias)) {
-    set_error("xdna_gemm_bf16: invalid arguments");
+    set_error(std::string(src.who) + ": invalid arguments");
     return -1;
   }
   if (batch == 0 || M == 0 || N == 0) return 0;
   if (batch > 65535) {
-    set_error("xdna_gemm_bf16: batch too large");
+    set_error(std::string(src.who) + ": batch too large");
     return -1;
   }
   GemmArgs g;
@@ -828,8 +883,7 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
       g.nsplit = int(ceil_div(kt2, g.kt_per));
     }
     if (g.nsplit > 1) {
-      g.part = static_cast<float*>(
-          xdna_hip_cache_alloc(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float)));
+      g.part = src.take(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float));
       if (!g.part) return -1;
     }
     const dim3 grid2(unsigned(ceil_div(N, kT2)), unsigned(ceil_div(M, kT2)), unsigned(batch * g.nsplit));
@@ -843,17 +897,16 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
       ok = mb == kAlongK ? launch2<kAlongRow, kAlongK>(grid2, st2, g) : launch2<kAlongRow, kAlongRow>(grid2, st2, g);
     }
     if (!ok) {
-      if (g.part) xdna_hip_cache_free(g.part);
-      set_error("xdna_gemm_bf16: cannot enable a large-tile kernel's LDS size");
+      src.give_back(g.part);
+      set_error(std::string(src.who) + ": cannot enable a large-tile kernel's LDS size");
       return -1;
     }
     if (g.nsplit > 1) {
       const int64_t n_all = int64_t(batch) * M * N;
       gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st2>>>(g);
-      // stream-ordered reuse: the next user of the block runs after the reduce
-      xdna_hip_cache_free(g.part);
+      src.give_back(g.part);
     }
-    return check_launch("xdna_gemm_bf16");
+    return check_launch(src.who);
   }
   // Few output tiles and a long K (Gram matrices: [C x HW] x [HW x C]): split K over
   // blockIdx.z so the grid covers the CUs; fp32 partials are summed in split order.
@@ -870,8 +923,7 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   }
   hipStream_t st = as_stream(stream);
   if (g.nsplit > 1) {
-    g.part = static_cast<float*>(
-        xdna_hip_cache_alloc(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float)));
+    g.part = src.take(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float));
     if (!g.part) return -1;
   }
   const dim3 grid(unsigned(ceil_div(N, kTN)), unsigned(ceil_div(M, kTM)), unsigned(batch * g.nsplit));
@@ -881,10 +933,38 @@ extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C
   if (g.nsplit > 1) {
     const int64_t n_all = int64_t(batch) * M * N;
     gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st>>>(g);
-    // stream-ordered reuse: the next user of the block runs after the reduce
-    xdna_hip_cache_free(g.part);
+    src.give_back(g.part);
   }
-  return check_launch("xdna_gemm_bf16");
+  return check_launch(src.who);
+}
+
+}  // namespace
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C,
+                              const uint16_t* bias, int batch, int M, int N, int K, int64_t lda_m,
+                              int64_t lda_k, int64_t stride_a, int64_t ldb_k, int64_t ldb_n,
+                              int64_t stride_b, int64_t ldc_m, int64_t ldc_n, int64_t stride_c,
+                              int bias_mode, int64_t bias_sm, int64_t bias_sn, float alpha,
+                              float beta, void* stream) {
+  const PartialsSource src{"xdna_gemm_bf16", nullptr};
+  return gemm_run(src, A, Bm, C, bias, batch, M, N, K, lda_m, lda_k, stride_a, ldb_k, ldb_n, stride_b, ldc_m,
+                  ldc_n, stride_c, bias_mode, bias_sm, bias_sn, alpha, beta, stream);
+}
+
+extern "C" int xdna_gemm_bf16_noalloc(const uint16_t* A, const uint16_t* Bm, uint16_t* C,
+                                      const uint16_t* bias, int batch, int M, int N, int K, int64_t lda_m,
+                                      int64_t lda_k, int64_t stride_a, int64_t ldb_k, int64_t ldb_n,
+                                      int64_t stride_b, int64_t ldc_m, int64_t ldc_n, int64_t stride_c,
+                                      int bias_mode, int64_t bias_sm, int64_t bias_sn, float alpha,
+                                      float beta, void* stream) {
+  float* sp = scratch_of_current_device();
+  if (!sp) return -1;
+  const PartialsSource src{"xdna_gemm_bf16_noalloc", sp};
+  return gemm_run(src, A, Bm, C, bias, batch, M, N, K, lda_m, lda_k, stride_a, ldb_k, ldb_n, stride_b, ldc_m,
+                  ldc_n, stride_c, bias_mode, bias_sm, bias_sn, alpha, beta, stream);
 }
 
 extern "C" int xdna_gemm_set_variant(int variant) {
