@@ -278,7 +278,7 @@ def main() -> int:
     assert xdna_train.is_available(), "xdna device not available"
     from xdna_train import device as xdev
 
-    C = xdev._C
+    C = xdev.native()
     X = torch.device("xdna")
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 

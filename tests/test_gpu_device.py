@@ -419,12 +419,12 @@ def test_launch_errors_raise(xdna):
 
     conv = nn.Conv2d(16, 16, 3, padding=1).bfloat16().to(X)
     x = torch.randn(1, 16, 8, 8).bfloat16().to(X)
-    dev._C.inject_failure(1, False)
+    dev.native().inject_failure(1, False)
     try:
         with pytest.raises(RuntimeError, match="injected failure"):
             conv(x)
     finally:
-        dev._C.reset_failure_state()
+        dev.native().reset_failure_state()
     assert conv(x).shape == (1, 16, 8, 8)
 
 
@@ -456,9 +456,9 @@ def test_frozen_weights_prepared_once_and_refreshed_on_write():
     cd = cd.to(X)
     xd = x.to(X)
     y1 = cd(xd)
-    n0 = xdna_train.device._C.launch_count()
+    n0 = xdna_train.device.native().launch_count()
     y2 = cd(xd)
-    n1 = xdna_train.device._C.launch_count()
+    n1 = xdna_train.device.native().launch_count()
     assert torch.equal(y1.cpu(), y2.cpu())
     # the second call reuses the prepared weights: pack + conv only (no preparation launch)
     assert n1 - n0 == 2, (n0, n1)
