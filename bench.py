@@ -119,7 +119,10 @@ def gram(f):
     return (x @ x.transpose(1, 2)).float() / float(c * h * w)
 
 
-def build_style(torch, device, batch=40, size=36):
+def build_style(torch, device, batch=40, size=36, fused=True):
+    """BASELINE config 4's training step on `device`; returns (step, generator).  fused:
+    Adam's fused kernel (what an xdna model runs, and the reference's pre-hook picks),
+    or None for the optimizer's default (single-tensor on the CPU)."""
     nn = torch.nn
     Generator, VGG = style_models(torch, nn)
     torch.manual_seed(0)
@@ -139,7 +142,7 @@ def build_style(torch, device, batch=40, size=36):
         sf = vgg(style, STYLE_TAPS)
         style_grams = {k: gram(v) for k, v in sf.items()}
     # capturable: the step may be captured in a graph (same fused Adam kernel either way)
-    opt = torch.optim.Adam(gen.parameters(), lr=1e-3, fused=True, capturable=device.type != "cpu")
+    opt = torch.optim.Adam(gen.parameters(), lr=1e-3, fused=fused, capturable=device.type != "cpu")
 
     def step():
         opt.zero_grad(set_to_none=True)
@@ -159,13 +162,59 @@ def build_style(torch, device, batch=40, size=36):
 
 
 # ---------------------------------------------------------------------------------------
+# MLP training step; config 1: one 3x3 conv
+# ---------------------------------------------------------------------------------------
+def build_mlp(torch, device, fused=True):
+    """Linear 1024->4096->4096->1024 with GELU, x [8192,1024] and target ~ N(0,1), MSE,
+    Adam 1e-3 (model seed 0, data seed 1); returns (step, model)."""
+    nn = torch.nn
+    torch.manual_seed(0)
+    mlp = nn.Sequential(nn.Linear(1024, 4096), nn.GELU(), nn.Linear(4096, 4096), nn.GELU(),
+                        nn.Linear(4096, 1024)).bfloat16().to(device)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(8192, 1024, generator=g).bfloat16().to(device)
+    t = torch.randn(8192, 1024, generator=g).bfloat16().to(device)
+    opt = torch.optim.Adam(mlp.parameters(), lr=1e-3, fused=fused)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = torch.nn.functional.mse_loss(mlp(x).float(), t.float())
+        loss.backward()
+        opt.step()
+        return loss
+
+    return step, mlp
+
+
+def build_c1(torch, device, fused=True):
+    """BASELINE config 1 (README.md:57-68): Conv2d 128->128 3x3 pad 1 with bias, default
+    init (seed 0), x ~ N(0,1) [16,128,36,36], MSE to zeros, Adam 1e-3; returns (step, conv)."""
+    torch.manual_seed(0)
+    conv = torch.nn.Conv2d(128, 128, 3, padding=1).bfloat16().to(device)
+    x = torch.randn(16, 128, 36, 36).bfloat16().to(device)
+    target = torch.zeros(16, 128, 36, 36, device=device)
+    opt = torch.optim.Adam(conv.parameters(), lr=1e-3, fused=fused)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = torch.nn.functional.mse_loss(conv(x).float(), target)
+        loss.backward()
+        opt.step()
+        return loss
+
+    return step, conv
+
+
+# ---------------------------------------------------------------------------------------
 def sync(torch):
     torch.xdna.synchronize()
 
 
-def conv_sweep_data(torch, device, shapes):
+def conv_sweep_data(torch, device, shapes, first_index=0):
+    """x, w, b, dy of each shape; shape i of the sweep is seeded 1000 + i (`first_index`
+    names the sweep index of shapes[0])."""
     data = []
-    for idx, (n, c, h) in enumerate(shapes):
+    for idx, (n, c, h) in enumerate(shapes, start=first_index):
         torch.manual_seed(1000 + idx)
         bound = math.sqrt(6.0 / (9 * c))
         x = torch.randn(n, c, h, h, device=device).bfloat16()
@@ -382,20 +431,7 @@ def main() -> int:
     # --- MLP training step (config 3): mm / addmm fwd + both backward GEMMs + Adam -------
     if not args.skip_mlp:
         log("mlp: building")
-        torch.manual_seed(0)
-        mlp = torch.nn.Sequential(torch.nn.Linear(1024, 4096), torch.nn.GELU(), torch.nn.Linear(4096, 4096),
-                                  torch.nn.GELU(), torch.nn.Linear(4096, 1024)).bfloat16().to(X)
-        gm = torch.Generator().manual_seed(1)
-        xm = torch.randn(8192, 1024, generator=gm).bfloat16().to(X)
-        tm = torch.randn(8192, 1024, generator=gm).bfloat16().to(X)
-        mopt = torch.optim.Adam(mlp.parameters(), lr=1e-3, fused=True)
-
-        def mlp_step():
-            mopt.zero_grad(set_to_none=True)
-            loss = torch.nn.functional.mse_loss(mlp(xm).float(), tm.float())
-            loss.backward()
-            mopt.step()
-            return loss
+        mlp_step, _ = build_mlp(torch, X)
 
         for _ in range(3):
             mlp_step()
@@ -421,7 +457,7 @@ def main() -> int:
                         "step_gemm_tflops = 1168.2 GFLOP of GEMM per step / wall time of the whole step",
         }
         log(f"mlp: {result['mlp']['ms_per_step']} ms/step, {result['mlp']['step_gemm_tflops']} TFLOP/s")
-        del mlp, mopt, xm, tm
+        del mlp_step
 
     # --- style step (config 4) ---------------------------------------------------------
     if not args.skip_style:
