@@ -649,6 +649,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     check_abi(xdna_hip_device_synchronize(), "synchronize");
     check_abi(xdna_hip_cache_empty(), "empty_cache");
   });
+  mod.def("note_graph_replay", [] { note_graph_replay(); });
   mod.def("pool_create", [] { return xdna_hip_cache_pool_create(); });
   mod.def("pool_begin", [](int64_t pool) { check_abi(xdna_hip_cache_pool_begin(pool), "pool_begin"); });
   mod.def("pool_end", [] { check_abi(xdna_hip_cache_pool_end(), "pool_end"); });

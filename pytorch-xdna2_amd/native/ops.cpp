@@ -82,21 +82,22 @@ bool conv_s2_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArray
   return x.device().type() == kXdna && w.device().type() == kXdna;
 }
 
-// Prepared weights of frozen tensors (requires_grad false: a loss network's weights),
-// keyed by storage, data address, offset, shape, version, write epoch and direction, the
-// role of the reference's weight slots (torch_xdna_device.cpp:2208-2271, keyed on the
-// data pointer, version and write epoch).  A weak reference to the storage tells a live
-// tensor from a new one at a recycled address; in-place writes through autograd bump the
-// version, and every xdna write path (`.data` writes included) bumps the write epoch.
-// Trainable weights are prepared on every call: the optimizer changes them in place
-// (also inside replayed graphs, where no host code runs).  Entries carry the capture tag
-// they were made under and serve only the same tag: during a capture the frozen form is
-// prepared inside the graph, which then owns it and sees writes made between replays.
+// Prepared weight forms (forward and input-gradient), keyed by storage, data address,
+// offset, shape, version, write epoch, graph-replay generation and direction: the role
+// of the reference's weight slots (torch_xdna_device.cpp:2208-2271, keyed on the data
+// pointer, version and write epoch).  A weak reference to the storage tells a live tensor
+// from a new one at a recycled address; in-place writes through autograd bump the
+// version, and every xdna write path (`.data` writes and the fused optimizer steps
+// included) bumps the write epoch.  The one writer no host code sees is the replay of a
+// captured graph (an optimizer step inside it), so every replay starts a new generation
+// and older entries are not served.  Entries carry the capture tag they were made under
+// and serve only the same tag: inside a capture the forms are prepared by the graph
+// itself, which owns them and sees writes made between replays.
 struct PreparedWeights {
   c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
   const void* data = nullptr;
   int64_t offset = 0, version = 0, tag = 0;
-  uint64_t epoch = 0;
+  uint64_t epoch = 0, generation = 0;
   std::array<int64_t, 4> sizes{};
   bool dgrad = false;
   at::Tensor wt;
@@ -107,8 +108,12 @@ struct WeightCache {
   std::mutex mu;
   std::vector<PreparedWeights> entries;
   uint64_t tick = 0;
-  static constexpr size_t kMaxEntries = 64;
+  size_t bytes = 0;
+  static constexpr size_t kMaxEntries = 1024;
+  static constexpr size_t kMaxBytes = size_t(4) << 30;
 };
+
+std::atomic<uint64_t> g_replay_generation{0};
 
 WeightCache& weight_cache() {
   static auto* c = new WeightCache();
@@ -121,13 +126,14 @@ void clear_weight_cache() {
   WeightCache& c = weight_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   c.entries.clear();
+  c.bytes = 0;
 }
+
+void note_graph_replay() { g_replay_generation.fetch_add(1); }
 
 namespace {
 
-bool weight_cacheable(const at::Tensor& w) {
-  return !w.requires_grad() && !w.is_inference() && w.dim() == 4;
-}
+bool weight_cacheable(const at::Tensor& w) { return !w.is_inference() && w.dim() == 4; }
 
 std::array<int64_t, 4> sizes4(const at::Tensor& w) { return {w.size(0), w.size(1), w.size(2), w.size(3)}; }
 
@@ -141,8 +147,9 @@ at::Tensor cached_weights(const at::Tensor& w, bool dgrad, int64_t tag) {
   WeightCache& c = weight_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   const int64_t ver = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
+  const uint64_t gen = g_replay_generation.load();
   for (auto& e : c.entries) {
-    if (!same_weight(e, w, dgrad, tag) || e.version != ver || e.epoch != epoch) continue;
+    if (!same_weight(e, w, dgrad, tag) || e.version != ver || e.epoch != epoch || e.generation != gen) continue;
     auto live = e.storage.lock();
     if (!live || live.get() != w.storage().unsafeGetStorageImpl()) continue;
     e.last_use = ++c.tick;
@@ -155,32 +162,43 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt, int
   const uint64_t epoch = write_epoch(w);
   WeightCache& c = weight_cache();
   std::lock_guard<std::mutex> lock(c.mu);
-  // drop entries of dead storages, then the least recently used one when full
-  c.entries.erase(std::remove_if(c.entries.begin(), c.entries.end(),
-                                 [](const PreparedWeights& e) { return e.storage.expired(); }),
-                  c.entries.end());
-  if (c.entries.size() >= WeightCache::kMaxEntries) {
-    auto lru = std::min_element(c.entries.begin(), c.entries.end(),
-                                [](const auto& a, const auto& b) { return a.last_use < b.last_use; });
-    c.entries.erase(lru);
-  }
-  // an entry for the same tensor, direction and tag (an older version) is replaced
-  const auto same = [&](const PreparedWeights& e) {
+  const uint64_t gen = g_replay_generation.load();
+  // drop entries of dead storages and older generations, and any entry for the same
+  // tensor, direction and tag (an older version or epoch)
+  const auto stale = [&](const PreparedWeights& e) {
+    if (e.storage.expired() || (e.tag == 0 && e.generation != gen)) return true;
     auto live = e.storage.lock();
     return same_weight(e, w, dgrad, tag) && live && live.get() == w.storage().unsafeGetStorageImpl();
   };
-  c.entries.erase(std::remove_if(c.entries.begin(), c.entries.end(), same), c.entries.end());
+  for (auto it = c.entries.begin(); it != c.entries.end();) {
+    if (stale(*it)) {
+      c.bytes -= size_t(it->wt.nbytes());
+      it = c.entries.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  // then the least recently used ones while over the caps
+  while (!c.entries.empty() && (c.entries.size() >= WeightCache::kMaxEntries ||
+                                c.bytes + size_t(wt.nbytes()) > WeightCache::kMaxBytes)) {
+    auto lru = std::min_element(c.entries.begin(), c.entries.end(),
+                                [](const auto& a, const auto& b) { return a.last_use < b.last_use; });
+    c.bytes -= size_t(lru->wt.nbytes());
+    c.entries.erase(lru);
+  }
   PreparedWeights e;
   e.storage = c10::weak_intrusive_ptr<c10::StorageImpl>(w.storage().getWeakStorageImpl());
   e.data = w.storage().data();
   e.offset = w.storage_offset();
   e.version = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
   e.epoch = epoch;
+  e.generation = gen;
   e.tag = tag;
   e.sizes = sizes4(w);
   e.dgrad = dgrad;
   e.wt = wt;
   e.last_use = ++c.tick;
+  c.bytes += size_t(wt.nbytes());
   c.entries.push_back(std::move(e));
 }
 
@@ -213,15 +231,13 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor wc = w.contiguous();
   void* st = current_stream();
-  // Frozen weights: both forms cached by storage, version and write epoch, outside
-  // captures.  Trainable weights: the forward prepares the input gradient's form in the
-  // same launch and leaves it in the cache under the weight's current version, epoch and
-  // capture tag, where the backward of the same step finds it (an optimizer step bumps
-  // the epoch; a stale entry is never read).
+  // Both forms are cached (see PreparedWeights).  A trainable weight's forward prepares
+  // the input gradient's form in the same launch, so the backward of the step finds it;
+  // the optimizer step then bumps the epoch and the next forward prepares both again.
   const int64_t tag = capture_tag();
-  const bool cacheable = weight_cacheable(w) && tag == 0;
+  const bool cacheable = weight_cacheable(w);
   const bool trainable = w.requires_grad() && !w.is_inference();
-  at::Tensor wt = cacheable || (trainable && dgrad) ? cached_weights(w, dgrad, tag) : at::Tensor();
+  at::Tensor wt = cacheable ? cached_weights(w, dgrad, tag) : at::Tensor();
   // prepare / hit counters (the reference's npu_conv3x3w.weights{,_hit})
   count_call(wt.defined() ? "hip_conv3x3.weights_hit" : "hip_conv3x3.weights", 0);
   if (!wt.defined()) {
@@ -234,6 +250,7 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
                                                        int(w.size(1)), st),
                 "conv weights");
       remember_weights(w, true, wtd, tag);
+      remember_weights(w, false, wt, tag);
     } else {
       check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
                                                   static_cast<uint16_t*>(wt.data_ptr()), int(w.size(0)),
@@ -272,7 +289,7 @@ struct PackedInput {
   c10::weak_intrusive_ptr<c10::StorageImpl> storage{c10::intrusive_ptr<c10::StorageImpl>()};
   const void* data = nullptr;
   int64_t offset = 0, version = 0, tag = 0;
-  uint64_t epoch = 0;
+  uint64_t epoch = 0, generation = 0;
   std::vector<int64_t> sizes, strides;
   int layout = 0;
   at::Tensor packed;
@@ -291,7 +308,8 @@ PackedInputCache& packed_input_cache() {
 }
 
 bool same_input(const PackedInput& e, const at::Tensor& x, int layout, int64_t tag, uint64_t epoch) {
-  if (e.layout != layout || e.tag != tag || e.epoch != epoch || e.data != x.storage().data() ||
+  if (e.layout != layout || e.tag != tag || e.epoch != epoch || e.generation != g_replay_generation.load() ||
+      e.data != x.storage().data() ||
       e.offset != x.storage_offset() || e.sizes != x.sizes().vec() || e.strides != x.strides().vec() ||
       e.version != int64_t(x.unsafeGetTensorImpl()->version_counter().current_version()))
     return false;
@@ -319,6 +337,7 @@ void remember_packed_input(const at::Tensor& x, const at::Tensor& packed, int la
   e.version = int64_t(x.unsafeGetTensorImpl()->version_counter().current_version());
   e.tag = tag;
   e.epoch = epoch;
+  e.generation = g_replay_generation.load();
   e.sizes = x.sizes().vec();
   e.strides = x.strides().vec();
   e.layout = layout;

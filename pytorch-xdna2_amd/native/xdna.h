@@ -82,8 +82,11 @@ void register_hot_ops(torch::Library& m);
 // Autograd-level overrides for the backend (ops.cpp): instance_norm.
 void register_autograd_ops(torch::Library& m);
 
-// Drops the prepared weights of frozen tensors (ops.cpp).
+// Drops the cached prepared weight forms (ops.cpp).
 void clear_weight_cache();
+// A captured graph was replayed: host caches of forms derived from tensors it may have
+// written (prepared weights, kept packs) stop serving their older entries (ops.cpp).
+void note_graph_replay();
 // Drops the packed conv inputs kept for weight gradients (ops.cpp).
 void clear_packed_inputs();
 

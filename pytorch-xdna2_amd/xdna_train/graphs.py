@@ -53,7 +53,10 @@ class Graph:
         return self._pool
 
     def replay(self) -> None:
-        """Launches the captured work on the current stream."""
+        """Launches the captured work on the current stream.  The backend's host caches of
+        forms derived from tensors (prepared conv weights, kept packs) stop serving entries
+        made before the replay, whose tensors the graph may have rewritten."""
+        _device.native().note_graph_replay()
         self._cuda.replay()
 
     def reset(self) -> None:

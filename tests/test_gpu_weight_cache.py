@@ -119,6 +119,54 @@ def test_frozen_weight_prepared_once_then_hit():
     assert (prep, hit) == (2, 8), (prep, hit)  # forward and input-gradient forms once each
 
 
+def test_trainable_weight_prepared_once_per_optimizer_step():
+    """Trainable weights are prepared once (both forms, one launch) until a write: steps
+    without an optimizer update hit the cache, the update's epoch bump forces a new form."""
+    torch.manual_seed(0)
+    x, dy = _data()
+    conv = nn.Conv2d(64, 64, 3, padding=1, bias=False).bfloat16().to(X)
+    opt = torch.optim.Adam(conv.parameters(), lr=0.05)
+    torch.xdna.empty_cache()
+    xdna_train.reset_mapped_cpu_stats()
+    for _ in range(3):
+        conv(x).backward(dy)
+    st = {k: v["calls"] for k, v in xdna_train.mapped_cpu_stats().items()}
+    # x needs no gradient: one forward lookup per step (one preparation, then hits)
+    assert _counts() == (1, 2), st
+    opt.step()
+    xdna_train.reset_mapped_cpu_stats()
+    got = _fwd_dx(conv, x, dy)
+    st = {k: v["calls"] for k, v in xdna_train.mapped_cpu_stats().items()}
+    assert _counts() == (1, 1), st
+    assert _same(got, _uncached(conv, x, dy))
+
+
+def test_eager_after_graph_replay_uses_the_replayed_weights():
+    """A replayed optimizer step writes the weights with no host code: the eager forms
+    cached before the capture must not be served after a replay."""
+    torch.manual_seed(0)
+    x, dy = _data()
+    conv = nn.Conv2d(64, 64, 3, padding=1, bias=False).bfloat16().to(X)
+    opt = torch.optim.Adam(conv.parameters(), lr=0.05, fused=True, capturable=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        conv(x).backward(dy)
+        opt.step()
+
+    step()
+    step()  # eager: the forms of the current weights are cached
+    graph = torch.xdna.Graph()
+    with torch.xdna.graph(graph):
+        step()
+    for _ in range(3):
+        graph.replay()
+    torch.xdna.synchronize()
+    got = _fwd_dx(conv, x, dy)
+    assert _same(got, _uncached(conv, x, dy))
+    graph.reset()
+
+
 @pytest.mark.parametrize("make", [
     lambda p: torch.optim.SGD(p, lr=0.5),
     lambda p: torch.optim.SGD(p, lr=0.5, momentum=0.9, weight_decay=0.1),
