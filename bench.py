@@ -205,6 +205,64 @@ def build_c1(torch, device, fused=True):
     return step, conv
 
 
+def build_resnet(torch, device, fused=True, batch=128, size=64):
+    """ResNet-18-style network (BasicBlock [2,2,2,2], widths 64/128/256/
+    512, 3x3 stride-1 stem, strided 3x3 + 1x1 downsample convs, BatchNorm + ReLU, global
+    average pool, FC to 1000), input [128,3,64,64] ~ N(0,1), labels uniform in [0,1000),
+    cross-entropy, Adam 1e-3 (model seed 0, data seed 1); returns (step, model)."""
+    nn = torch.nn
+
+    class Block(nn.Module):
+        def __init__(self, cin, cout, stride):
+            super().__init__()
+            self.c1 = nn.Conv2d(cin, cout, 3, stride, 1, bias=False)
+            self.b1 = nn.BatchNorm2d(cout)
+            self.c2 = nn.Conv2d(cout, cout, 3, 1, 1, bias=False)
+            self.b2 = nn.BatchNorm2d(cout)
+            self.down = None
+            if stride != 1 or cin != cout:
+                self.down = nn.Sequential(nn.Conv2d(cin, cout, 1, stride, bias=False), nn.BatchNorm2d(cout))
+
+        def forward(self, x):
+            y = torch.relu(self.b1(self.c1(x)))
+            y = self.b2(self.c2(y))
+            return torch.relu(y + (x if self.down is None else self.down(x)))
+
+    class ResNet18(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.stem = nn.Sequential(nn.Conv2d(3, 64, 3, 1, 1, bias=False), nn.BatchNorm2d(64), nn.ReLU())
+            blocks, cin = [], 64
+            for cout, stride in ((64, 1), (128, 2), (256, 2), (512, 2)):
+                blocks += [Block(cin, cout, stride), Block(cout, cout, 1)]
+                cin = cout
+            self.blocks = nn.Sequential(*blocks)
+            self.pool = nn.AdaptiveAvgPool2d(1)
+            self.fc = nn.Linear(512, 1000)
+
+        def forward(self, x):
+            return self.fc(torch.flatten(self.pool(self.blocks(self.stem(x))), 1))
+
+    torch.manual_seed(0)
+    model = ResNet18().bfloat16().to(device).train()
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(batch, 3, size, size, generator=g).bfloat16().to(device)
+    labels = torch.randint(0, 1000, (batch,), generator=g).to(device)
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3, fused=fused)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = torch.nn.functional.cross_entropy(model(x).float(), labels)
+        loss.backward()
+        opt.step()
+        return loss
+
+    return step, model
+
+
+RESNET_GFLOP = 3 * 2 * 284.4  # fwd + dgrad + wgrad of its 284.4 GMAC forward (dgrad of the stem included)
+
+
 # ---------------------------------------------------------------------------------------
 def sync(torch):
     torch.xdna.synchronize()

@@ -466,6 +466,24 @@ int xdna_fused_adam_tensor_lr(int n_tensors, void* const* params, void* const* g
 int xdna_foreach_add_scalar_f32(int n_tensors, float* const* tensors, const int64_t* numels,
                                 float value, void* stream);
 
+/* Batch norm of convolutional activations in training mode, any channel length N*L, with
+ * the running statistics updated when given: x[N][C][L] bf16, contiguous.  Replaces
+ * PyTorch's CPU native_batch_norm / native_batch_norm_backward that the reference reaches
+ * through its zero-copy fallback (torch_xdna_device.cpp:5124-5260) for ResNet-style
+ * layers.  weight / bias: param_dtype 0 (absent), 1 bf16, 2 fp32; running_mean /
+ * running_var: stat_dtype 1 bf16 or 2 fp32 (both NULL: not tracked; stat_dtype 0).  Batch
+ * statistics in fp32 from per-range partials combined in a fixed order (the same bits on
+ * every call): save_mean, save_invstd = 1 / sqrt(biased var + eps) (fp32 [C]); running
+ * stats updated as running = (1 - momentum) * running + momentum * batch, with the
+ * unbiased variance.  Backward: dx, dweight, dbias may each be NULL. */
+int xdna_batch_norm_train_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                   void* running_mean, void* running_var, int stat_dtype, double momentum,
+                                   double eps, uint16_t* y, float* save_mean, float* save_invstd, int64_t N,
+                                   int64_t C, int64_t L, void* stream);
+int xdna_batch_norm_train_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
+                                   const float* save_mean, const float* save_invstd, uint16_t* dx,
+                                   void* dweight, void* dbias, int64_t N, int64_t C, int64_t L, void* stream);
+
 /* Batch norm in training mode without running statistics over x[N][C][L] bf16 (the form
  * PyTorch's instance_norm takes: [B, C, H, W] as [1, B*C, H*W]).  Replaces PyTorch's CPU
  * native_batch_norm / native_batch_norm_backward, which the reference reaches through

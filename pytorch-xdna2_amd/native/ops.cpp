@@ -378,6 +378,7 @@ void clear_packed_inputs() {
 namespace {
 
 bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W);
+std::atomic<int64_t> g_dw_jobs{0};
 
 // Forward of a 3x3 / stride-1 conv; the packed input is kept when the weight is trainable
 // and its gradient takes the rows form (whether or not autograd records this call: a
@@ -469,6 +470,105 @@ at::Tensor hip_gconv_fwd(const at::Tensor& input, const at::Tensor& weight, cons
   return y;
 }
 
+// ---------------------------------------------------------------------------------------
+// 1x1 convolutions (stride 1 or 2, no padding: ResNet's downsampling shortcut) as MFMA
+// GEMMs: y[n] = W [Cout x Cin] . x[n] [Cin x HW] for every image (one batched launch with
+// the weight broadcast), dx[n] = W^T . dy[n], and dW = dY^T . X over all N*HW pixels as
+// one split-K product of channel-major copies.  Stride 2 takes every other pixel of x
+// (subsample2) and spreads dx back onto the full grid with zeros (dilate2).  The
+// reference runs these on its CPU (torch_xdna_device.cpp:4594-4604, 4862-4874).
+// ---------------------------------------------------------------------------------------
+bool conv1x1_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
+                      c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation, bool transposed,
+                      c10::SymIntArrayRef output_padding, const c10::SymInt& groups) {
+  if (g_mode.load() < 1) return false;
+  if (x.scalar_type() != at::kBFloat16 || w.scalar_type() != at::kBFloat16) return false;
+  if (x.dim() != 4 || w.dim() != 4 || w.size(2) != 1 || w.size(3) != 1 || x.size(1) != w.size(1)) return false;
+  if (!(is_one(stride, 1) || is_one(stride, 2)) || !is_one(padding, 0) || !is_one(dilation, 1) || transposed)
+    return false;
+  if (!is_one(output_padding, 0) || groups != 1) return false;
+  if (x.device().type() != kXdna || w.device().type() != kXdna) return false;
+  for (int64_t d = 0; d < 4; ++d)
+    if (x.size(d) < 1 || w.size(d) < 1) return false;
+  const int64_t lim = int64_t(1) << 30;
+  return x.numel() < lim && x.size(0) <= 65535 && x.size(0) * x.size(2) * x.size(3) < lim;
+}
+
+// x itself (stride 1) or its stride-2 sample, contiguous
+at::Tensor conv1x1_input(const at::Tensor& input, int64_t s) {
+  at::Tensor x = input.contiguous();
+  if (s == 1) return x;
+  const int64_t N = x.size(0), C = x.size(1), H = x.size(2), W = x.size(3);
+  at::Tensor xs = empty_xdna({N, C, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16);
+  check_abi(xdna_subsample2_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                 static_cast<uint16_t*>(xs.data_ptr()), N * C, int(H), int(W), current_stream()),
+            "conv1x1 subsample");
+  return xs;
+}
+
+at::Tensor hip_conv1x1_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias, int64_t s) {
+  const at::Tensor xs = conv1x1_input(input, s);
+  const at::Tensor w = weight.contiguous();
+  const int64_t N = xs.size(0), Ci = xs.size(1), Ho = xs.size(2), Wo = xs.size(3), Co = w.size(0), P = Ho * Wo;
+  at::Tensor y = empty_xdna({N, Co, Ho, Wo}, at::kBFloat16);
+  at::Tensor bc;
+  if (bias) bc = bias->contiguous();
+  KernelTimer kt("conv1x1.fwd", 2.0 * N * P * double(Co) * Ci);
+  check_abi(xdna_gemm_bf16(static_cast<const uint16_t*>(w.const_data_ptr()),
+                           static_cast<const uint16_t*>(xs.const_data_ptr()), static_cast<uint16_t*>(y.data_ptr()),
+                           bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr, int(N), int(Co), int(P),
+                           int(Ci), Ci, 1, 0, P, 1, Ci * P, P, 1, Co * P, bias ? 3 : 0, 1, 0, 1.0f, 1.0f,
+                           current_stream()),
+            "conv1x1 forward");
+  return y;
+}
+
+void hip_conv1x1_bwd(const at::Tensor& grad_output, const at::Tensor& input, const at::Tensor& weight, int64_t s,
+                     std::array<bool, 3> mask, at::Tensor& gi, at::Tensor& gw, at::Tensor& gb) {
+  const at::Tensor dy = grad_output.contiguous();
+  const at::Tensor w = weight.contiguous();
+  const int64_t N = input.size(0), Ci = input.size(1), H = input.size(2), W = input.size(3);
+  const int64_t Co = w.size(0), Ho = dy.size(2), Wo = dy.size(3), P = Ho * Wo;
+  void* st = current_stream();
+  if (mask[0]) {
+    at::Tensor dxs = empty_xdna({N, Ci, Ho, Wo}, at::kBFloat16);
+    KernelTimer kt("conv1x1.dgrad", 2.0 * N * P * double(Co) * Ci);
+    check_abi(xdna_gemm_bf16(static_cast<const uint16_t*>(w.const_data_ptr()),
+                             static_cast<const uint16_t*>(dy.const_data_ptr()), static_cast<uint16_t*>(dxs.data_ptr()),
+                             nullptr, int(N), int(Ci), int(P), int(Co), 1, Ci, 0, P, 1, Co * P, P, 1, Ci * P, 0, 0, 0,
+                             1.0f, 0.0f, st),
+              "conv1x1 input gradient");
+    if (s == 1) {
+      gi = dxs;
+    } else {
+      gi = empty_xdna({N, Ci, H, W}, at::kBFloat16);
+      check_abi(xdna_dilate2_bf16(static_cast<const uint16_t*>(dxs.const_data_ptr()),
+                                  static_cast<uint16_t*>(gi.data_ptr()), N * Ci, int(H), int(W), st),
+                "conv1x1 dilate");
+    }
+  }
+  if (mask[1]) {
+    // channel-major copies: dY^T [Co][N*P] and X^T [Ci][N*P], then one product over N*P
+    const at::Tensor dyt = dy.permute({1, 0, 2, 3}).contiguous();
+    const at::Tensor xst = conv1x1_input(input, s).permute({1, 0, 2, 3}).contiguous();
+    const int64_t K = N * P;
+    gw = empty_xdna({Co, Ci, 1, 1}, at::kBFloat16);
+    KernelTimer kt("conv1x1.wgrad", 2.0 * N * P * double(Co) * Ci);
+    check_abi(xdna_gemm_bf16(static_cast<const uint16_t*>(dyt.const_data_ptr()),
+                             static_cast<const uint16_t*>(xst.const_data_ptr()), static_cast<uint16_t*>(gw.data_ptr()),
+                             nullptr, 1, int(Co), int(Ci), int(K), K, 1, 0, 1, K, 0, Ci, 1, 0, 0, 0, 0, 1.0f, 0.0f, st),
+              "conv1x1 weight gradient");
+    g_dw_jobs.fetch_add(1);
+  }
+  if (mask[2]) {
+    gb = empty_xdna({Co}, at::kBFloat16);
+    check_abi(xdna_conv3x3_bias_grad_bf16(static_cast<const uint16_t*>(dy.const_data_ptr()),
+                                          static_cast<uint16_t*>(gb.data_ptr()), int(N), int(Co), int(Ho), int(Wo),
+                                          st),
+              "conv1x1 bias grad");
+  }
+}
+
 at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tensor& weight,
                                          const std::optional<at::Tensor>& bias,
                                          c10::SymIntArrayRef stride, c10::SymIntArrayRef padding,
@@ -493,6 +593,12 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
                                    static_cast<uint16_t*>(y.data_ptr()), B * C, int(H), int(W), current_stream()),
               "conv stride-2 subsample");
     return y;
+  }
+  if (conv1x1_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
+      (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
+                     bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
+    ScopedCount sc("hip_conv1x1.fwd.run");
+    return hip_conv1x1_fwd(input, weight, has_bias ? &*bias : nullptr, stride[0].expect_int());
   }
   const int gmode = g_gconv_mode.load();
   if (gmode > 0 &&
@@ -574,8 +680,6 @@ bool wgrad_rows_pick(int64_t Cin, int64_t Cout, int64_t W) {
   return W > 142 || g_wgrad_form.load() != 1;
 }
 
-std::atomic<int64_t> g_dw_jobs{0};
-
 std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable_xdna(
     const at::Tensor& grad_output, const at::Tensor& input, const at::Tensor& weight,
     c10::SymIntArrayRef stride, c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation,
@@ -634,6 +738,18 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
                                           current_stream()),
               "conv bias grad");
     mask[2] = false;
+  }
+  if (!hip && go_ok && (mask[0] || mask[1] || mask[2]) &&
+      conv1x1_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups)) {
+    const int64_t s = stride[0].expect_int();
+    TORCH_CHECK(grad_output.size(2) == (input.size(2) + s - 1) / s && grad_output.size(3) == (input.size(3) + s - 1) / s,
+                "convolution_backward: grad_output has the wrong spatial size");
+    ScopedCount sc("hip_conv1x1.bwd.run");
+    std::array<bool, 3> m1 = mask;
+    if (g_mode.load() < 2) m1[1] = false;  // mode 1: no HIP weight gradient
+    hip_conv1x1_bwd(grad_output, input, weight, s, m1, gi, gw, gb);
+    for (int i = 0; i < 3; ++i)
+      if (m1[i]) mask[i] = false;
   }
   const int gmode = g_gconv_mode.load();
   const bool ghip = !hip && gmode > 0 &&
@@ -1163,10 +1279,54 @@ bool norm_eligible(const at::Tensor& input, const std::optional<at::Tensor>& wei
   return norm_param_dtype(weight, bias) >= 0 && norm_param_ok(weight, C) && norm_param_ok(bias, C);
 }
 
+// Training-mode batch norm of conv activations with the spatial kernels (bnorm.hip): any
+// channel length, running statistics (bf16 or fp32, both or neither) updated in the same
+// launch pair.
+int running_stats_dtype(const std::optional<at::Tensor>& rm, const std::optional<at::Tensor>& rv, int64_t C) {
+  const bool hm = rm && rm->defined(), hv = rv && rv->defined();
+  if (!hm && !hv) return 0;
+  if (hm != hv || rm->scalar_type() != rv->scalar_type()) return -1;
+  for (const at::Tensor* t : {&*rm, &*rv})
+    if (t->dim() != 1 || t->size(0) != C || !t->is_contiguous() || t->device().type() != kXdna) return -1;
+  return rm->scalar_type() == at::kBFloat16 ? 1 : rm->scalar_type() == at::kFloat ? 2 : -1;
+}
+
+bool bn_train_eligible(const at::Tensor& input, const std::optional<at::Tensor>& weight,
+                       const std::optional<at::Tensor>& bias, bool training) {
+  if (g_mode.load() < 1 || !training) return false;
+  if (input.scalar_type() != at::kBFloat16 || input.dim() < 2 || input.device().type() != kXdna) return false;
+  const int64_t C = input.size(1);
+  if (C < 1 || input.numel() == 0 || input.size(0) < 1) return false;
+  return norm_param_dtype(weight, bias) >= 0 && norm_param_ok(weight, C) && norm_param_ok(bias, C);
+}
+
 std::tuple<at::Tensor, at::Tensor, at::Tensor> native_batch_norm_xdna(
     const at::Tensor& input, const std::optional<at::Tensor>& weight, const std::optional<at::Tensor>& bias,
     const std::optional<at::Tensor>& running_mean, const std::optional<at::Tensor>& running_var, bool training,
     double momentum, double eps) {
+  const int rsd = input.dim() >= 2 ? running_stats_dtype(running_mean, running_var, input.size(1)) : -1;
+  if (rsd >= 0 && bn_train_eligible(input, weight, bias, training) &&
+      (rsd > 0 || input.numel() / input.size(1) > kNormMaxPerChannel)) {
+    ScopedCount sc("hip_batch_norm_train.fwd.run");
+    const at::Tensor x = input.contiguous();
+    const int64_t N = x.size(0), C = x.size(1), L = x.numel() / (N * C);
+    const int wd = norm_param_dtype(weight, bias);
+    at::Tensor y = empty_xdna(x.sizes(), at::kBFloat16);
+    at::Tensor mean = empty_xdna({C}, at::kFloat), invstd = empty_xdna({C}, at::kFloat);
+    check_abi(xdna_batch_norm_train_fwd_bf16(
+                  static_cast<const uint16_t*>(x.const_data_ptr()),
+                  weight && weight->defined() ? weight->const_data_ptr() : nullptr,
+                  bias && bias->defined() ? bias->const_data_ptr() : nullptr, wd,
+                  rsd ? running_mean->data_ptr() : nullptr, rsd ? running_var->data_ptr() : nullptr, rsd, momentum,
+                  eps, static_cast<uint16_t*>(y.data_ptr()), mean.data_ptr<float>(), invstd.data_ptr<float>(), N, C,
+                  L, current_stream()),
+              "batch_norm fwd (training)");
+    if (rsd) {
+      bump_write_epoch(*running_mean);
+      bump_write_epoch(*running_var);
+    }
+    return {y, mean, invstd};
+  }
   if (norm_eligible(input, weight, bias, running_mean, running_var, training)) {
     ScopedCount sc("hip_batch_norm.fwd.run");
     const at::Tensor x = input.contiguous();
@@ -1200,6 +1360,30 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> native_batch_norm_backward_xdna(
                         save_mean->is_contiguous() && save_invstd->is_contiguous() &&
                         save_mean->device().type() == kXdna && save_invstd->device().type() == kXdna;
   const bool param_grads_ok = !(mask[1] || mask[2]) || (weight && weight->defined());
+  // long channels or running statistics (which the backward does not use): the spatial kernels
+  if (stats_ok && param_grads_ok && bn_train_eligible(input, weight, std::nullopt, train) &&
+      grad_out.scalar_type() == at::kBFloat16 && grad_out.sizes() == input.sizes() &&
+      grad_out.device().type() == kXdna && save_mean->numel() == input.size(1) &&
+      save_invstd->numel() == input.size(1) &&
+      (input.numel() / input.size(1) > kNormMaxPerChannel || (running_mean && running_mean->defined()))) {
+    ScopedCount sc("hip_batch_norm_train.bwd.run");
+    const at::Tensor x = input.contiguous(), dy = grad_out.contiguous();
+    const int64_t N = x.size(0), C = x.size(1), L = x.numel() / (N * C);
+    const int wd = norm_param_dtype(weight, std::nullopt);
+    at::Tensor dx, dw, db;
+    if (mask[0]) dx = empty_xdna(x.sizes(), at::kBFloat16);
+    const at::ScalarType pt = wd == 2 ? at::kFloat : at::kBFloat16;
+    if (mask[1]) dw = empty_xdna({C}, pt);
+    if (mask[2]) db = empty_xdna({C}, pt);
+    check_abi(xdna_batch_norm_train_bwd_bf16(
+                  static_cast<const uint16_t*>(dy.const_data_ptr()), static_cast<const uint16_t*>(x.const_data_ptr()),
+                  weight && weight->defined() ? weight->const_data_ptr() : nullptr, wd,
+                  save_mean->const_data_ptr<float>(), save_invstd->const_data_ptr<float>(),
+                  mask[0] ? static_cast<uint16_t*>(dx.data_ptr()) : nullptr, mask[1] ? dw.data_ptr() : nullptr,
+                  mask[2] ? db.data_ptr() : nullptr, N, C, L, current_stream()),
+              "batch_norm bwd (training)");
+    return {dx, dw, db};
+  }
   if (stats_ok && param_grads_ok && norm_eligible(input, weight, std::nullopt, running_mean, running_var, train) &&
       grad_out.scalar_type() == at::kBFloat16 && grad_out.sizes() == input.sizes() &&
       grad_out.device().type() == kXdna && save_mean->numel() == input.size(1) &&

@@ -112,6 +112,8 @@ SIGNATURES = {
     "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_gemm_bf16_noalloc": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_batch_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, P]),
+    "xdna_batch_norm_train_fwd_bf16": (I, [P, P, P, I, P, P, I, D, D, P, P, P, L, L, L, P]),
+    "xdna_batch_norm_train_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
     "xdna_batch_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
     "xdna_foreach_add_scalar_f32": (I, [I, PP, PL, ctypes.c_float, P]),
     "xdna_fused_adam": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, D, D, D, D, D, I, I, I, P, P, P]),

@@ -161,7 +161,9 @@ def test_batch_norm_training_without_running_stats(pdtype):
     check_param_grads(((wd.grad, wr.grad, "dweight"), (bd.grad, br.grad, "dbias")), pdtype)
 
 
-def test_batch_norm_with_running_stats_falls_back():
+def test_batch_norm_running_stats_training_on_hip_eval_on_rocm():
+    """Training mode with running statistics takes the spatial HIP kernels; eval mode
+    (normalising by the running statistics) is served by PyTorch-ROCm on aliases."""
     x = torch.randn(4, 8, 6, 6).bfloat16()
     bn = torch.nn.BatchNorm2d(8).bfloat16()
     ref = bn(x.clone())
@@ -170,5 +172,70 @@ def test_batch_norm_with_running_stats_falls_back():
     out = bnd(x.to(X))
     torch.xdna.synchronize()
     stats = xdna_train.mapped_cpu_stats()
-    assert stats.get("aten::native_batch_norm.rocm", {}).get("calls", 0) >= 1, stats
+    assert stats.get("hip_batch_norm_train.fwd.run", {}).get("calls", 0) == 1, stats
     assert torch.allclose(out.cpu().float(), ref.float(), atol=3e-2, rtol=3e-2)
+    assert torch.allclose(bnd.running_mean.cpu().float(), bn.running_mean.float(), atol=1e-2)
+    bn.eval()
+    bnd.eval()
+    xdna_train.reset_mapped_cpu_stats()
+    out = bnd(x.to(X))
+    stats = xdna_train.mapped_cpu_stats()
+    assert stats.get("aten::native_batch_norm.rocm", {}).get("calls", 0) >= 1, stats
+    assert torch.allclose(out.cpu().float(), bn(x.clone()).float(), atol=3e-2, rtol=3e-2)
+
+
+@pytest.mark.parametrize("shape,track", [
+    ((128, 64, 64, 64), True),   # config 5's first stage: 524288 elements per channel
+    ((128, 512, 8, 8), True),
+    ((16, 32, 9, 9), True),      # short channels, running statistics
+    ((3, 5, 7, 5), True),        # planes not a multiple of 8 (element path)
+    ((4, 48, 200, 100), False),  # long channels, no running statistics
+])
+def test_batch_norm_training_matches_fp64(shape, track):
+    """BatchNorm2d in training mode with running statistics (bf16 module): the spatial
+    batch-norm kernels against fp64 batch_norm of the same bf16 inputs; running mean and
+    variance (momentum 0.1, unbiased variance) within 1 bf16 ulp of the fp64 update."""
+    print("batch norm", shape, track, flush=True)
+    g = torch.Generator().manual_seed(11)
+    C = shape[1]
+    x = (torch.randn(shape, generator=g) * 2 + 0.7).bfloat16()
+    dy = torch.randn(shape, generator=g).bfloat16()
+    w = (torch.rand(C, generator=g) + 0.5).bfloat16()
+    b = (torch.randn(C, generator=g) * 0.1).bfloat16()
+    rm0 = (torch.randn(C, generator=g) * 0.1).bfloat16()
+    rv0 = (torch.rand(C, generator=g) + 0.5).bfloat16()
+    # reference in fp64
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    br = b.double().requires_grad_(True)
+    rmr, rvr = rm0.double().clone(), rv0.double().clone()
+    yr = torch.nn.functional.batch_norm(xr, rmr if track else None, rvr if track else None, wr, br,
+                                        training=True, momentum=0.1, eps=1e-5)
+    yr.backward(dy.double())
+    # device: a bf16 module
+    bn = torch.nn.BatchNorm2d(C, momentum=0.1, eps=1e-5, track_running_stats=track).bfloat16()
+    with torch.no_grad():
+        bn.weight.copy_(w)
+        bn.bias.copy_(b)
+        if track:
+            bn.running_mean.copy_(rm0)
+            bn.running_var.copy_(rv0)
+    bn = bn.to(X).train()
+    xd = x.to(X).requires_grad_(True)
+    xdna_train.reset_mapped_cpu_stats()
+    yd = bn(xd)
+    yd.backward(dy.to(X))
+    torch.xdna.synchronize()
+    stats = xdna_train.mapped_cpu_stats()
+    assert stats.get("hip_batch_norm_train.fwd.run", {}).get("calls", 0) == 1, stats
+    assert stats.get("hip_batch_norm_train.bwd.run", {}).get("calls", 0) == 1, stats
+    assert not any(k.startswith("aten::native_batch_norm") for k in stats), stats
+    check_bf16(bits(yd), yr.detach().numpy(), what="batch_norm out")
+    check_bf16(bits(xd.grad), xr.grad.numpy(), what="batch_norm dx")
+    check_param_grads(((bn.weight.grad, wr.grad, "dweight"), (bn.bias.grad, br.grad, "dbias")), torch.bfloat16)
+    if track:
+        for got, ref, name in ((bn.running_mean, rmr, "running_mean"), (bn.running_var, rvr, "running_var")):
+            gv = got.detach().cpu().double().numpy()
+            rv = ref.numpy()
+            tol = oracle.bf16_ulp(rv) + 1e-7
+            assert (np.abs(gv - rv) <= tol).all(), (name, np.abs(gv - rv).max())
