@@ -299,26 +299,124 @@ def sweep_flops(shapes):
     return sum(3 * 2.0 * n * h * h * c * c * 9 for n, c, h in shapes)
 
 
-def cpu_conv_baseline(torch, budget_s=12.0):
-    """PyTorch CPU bf16 conv fwd + dgrad + wgrad (+ bias grad) over N=16 sweep shapes,
-    repeated until ~budget_s of CPU work."""
-    shapes = [(16, c, h) for c in (64, 128, 256) for h in (18, 36)]
-    flops, t_total = 0.0, 0.0
-    cpu = torch.device("cpu")
-    data = conv_sweep_data(torch, cpu, shapes)
-    reps = 0
-    while t_total < budget_s and reps < 50:
-        for (x, w, b, dy), (n, c, h) in zip(data, shapes):
-            xr = x.clone().requires_grad_()
-            wr = w.detach().clone().requires_grad_()
-            br = b.clone().requires_grad_()
-            t0 = time.perf_counter()
-            y = torch.nn.functional.conv2d(xr, wr, br, padding=1)
-            y.backward(dy)
-            t_total += time.perf_counter() - t0
-            flops += 3 * 2.0 * n * h * h * c * c * 9
-        reps += 1
-    return flops / t_total / 1e12, reps, shapes
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the reference's CPU BF16 path (stock PyTorch CPU kernels) timed on this
+# box's host cores, in worker processes alternating with the GPU timing of the same
+# workload (ABBA over rounds), median of the per-round medians (BASELINE.md's method,
+# after benchmarks/end_to_end_speed.py:53-64, 98-107 and model_zoo.py:281-286).
+# ---------------------------------------------------------------------------------------
+# every C and H of the sweep at N16: the sample the CPU conv rate is measured on
+CPU_SWEEP_SAMPLE = [(16, c, h) for c in (64, 128, 256, 512) for h in (18, 36, 72)]
+
+
+def cpu_topology():
+    """(cpus in this process's affinity, physical cores among them, lscpu model name)."""
+    aff = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for cpu in aff:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{cpu}/topology/"
+            cores.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+        except OSError:
+            cores.add(("cpu", str(cpu)))
+    model = ""
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), "")
+    except (OSError, ValueError):
+        pass
+    return len(aff), len(cores), model
+
+
+def cpu_threads():
+    """Physical cores visible to the process, capped by the box's CPU share (OMP_NUM_THREADS)."""
+    _, phys, _ = cpu_topology()
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(phys, share) if share > 0 else phys)
+
+
+def timed_steps(step, warmup, steps, sync_fn):
+    """Per-step wall times (s) of `steps` steps after `warmup`; each step ends in a host read
+    of its result, as a logging script does (end_to_end_speed.py:53-64)."""
+    for _ in range(warmup):
+        step()
+    sync_fn()
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        out = step()
+        if out is not None:
+            float(out.detach())
+        sync_fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def sweep_sample_step(torch, device):
+    """One fwd + dgrad + wgrad (+ bias grad) pass over CPU_SWEEP_SAMPLE through
+    F.conv2d and autograd (the reference's CPU path; on xdna the same aten ops)."""
+    data = conv_sweep_data(torch, device, CPU_SWEEP_SAMPLE)
+
+    def step():
+        for x, w, b, dy in data:
+            xr = x.detach().requires_grad_()
+            wr = w.detach().requires_grad_()
+            br = b.detach().requires_grad_()
+            torch.nn.functional.conv2d(xr, wr, br, padding=1).backward(dy)
+        return None
+
+    return step
+
+
+CPU_WORKLOADS = {
+    # name -> (builder(torch, device) -> step, warmup, steps, unit, work per step)
+    "conv_sweep_sample": (lambda t, d: sweep_sample_step(t, d), 1, 3, "TFLOP/s", sweep_flops(CPU_SWEEP_SAMPLE)),
+    "style_default_adam": (lambda t, d: build_style(t, d, fused=None)[0], 3, 20, "it/s", 1.0),
+    "style_fused_adam": (lambda t, d: build_style(t, d, fused=True)[0], 3, 20, "it/s", 1.0),
+    "resnet18_default_adam": (lambda t, d: build_resnet(t, d, fused=None)[0], 2, 5, "it/s", 1.0),
+}
+
+
+def cpu_worker(name):
+    """Runs one CPU workload in this (fresh) process and prints RESULT={json}."""
+    import torch
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    build, warmup, steps, unit, work = CPU_WORKLOADS[name]
+    step = build(torch, torch.device("cpu"))
+    times = timed_steps(step, warmup, steps, lambda: None)
+    med = statistics.median(times)
+    rate = work / med / (1e12 if unit == "TFLOP/s" else 1.0)
+    print("RESULT=" + json.dumps({"name": name, "median_s": med, "rate": rate, "unit": unit, "steps": steps,
+                                  "threads": threads}), flush=True)
+
+
+def run_cpu_worker(name, timeout=600):
+    import subprocess
+    env = dict(os.environ, XDNA_CPU_WORKER="1")
+    p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-worker", name], capture_output=True,
+                       text=True, env=env, timeout=timeout)
+    for ln in p.stdout.splitlines():
+        if ln.startswith("RESULT="):
+            return json.loads(ln[7:])
+    raise RuntimeError(f"cpu worker {name} failed (rc {p.returncode}):\n{p.stderr[-2000:]}")
+
+
+def abba(cpu_name, gpu_rate, rounds=2, log=None):
+    """ABBA rounds of the CPU worker and the GPU timing (gpu_rate() -> rate in the worker's
+    unit); medians over the rounds."""
+    cpu, gpu = [], []
+    for r in range(rounds):
+        for side in (("cpu", "gpu") if r % 2 == 0 else ("gpu", "cpu")):
+            if side == "cpu":
+                cpu.append(run_cpu_worker(cpu_name)["rate"])
+            else:
+                gpu.append(gpu_rate())
+        if log:
+            log(f"cpu baseline {cpu_name}: round {r + 1}: cpu {cpu[-1]:.4g}, gpu {gpu[-1]:.4g}")
+    return statistics.median(cpu), statistics.median(gpu), cpu, gpu
 
 
 CALIB_BYTES = 256 << 20     # plain device copy whose PMC byte counts calibrate FETCH/WRITE_SIZE
@@ -372,7 +470,14 @@ def main() -> int:
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--mlp-steps", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="small subset (profiling runs)")
+    ap.add_argument("--skip-resnet", action="store_true")
+    ap.add_argument("--resnet-steps", type=int, default=10)
+    ap.add_argument("--cpu-rounds", type=int, default=2)
+    ap.add_argument("--cpu-worker", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_worker:
+        cpu_worker(args.cpu_worker)
+        return 0
     if args.gpus != 1:
         print("bench.py: this build runs on one MI355X only (one process, one GPU); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -551,31 +656,79 @@ def main() -> int:
                                "steps": args.style_steps, "loss": loss_g}
         log(f"style net (graph): {it_s:.1f} it/s, loss {loss_g:.4f}")
         graph.reset()
-        if not args.skip_cpu:
-            cpu_step, _ = build_style(torch, torch.device("cpu"))
-            cpu_step()
-            times = []
-            t_end = time.perf_counter() + 20.0
-            while time.perf_counter() < t_end and len(times) < 20:
-                t1 = time.perf_counter()
-                cpu_step().item()
-                times.append(time.perf_counter() - t1)
-            cpu_it_s = 1.0 / statistics.median(times)
-            result["style_net"].update({"cpu_it_s": round(cpu_it_s, 3), "cpu_steps": len(times),
-                                        "speedup_vs_cpu": round(it_s / cpu_it_s, 1)})
-            log(f"style net CPU: {cpu_it_s:.2f} it/s")
 
-    # --- CPU baseline of the headline ---------------------------------------------------
+        def style_gpu_it_s():
+            g2 = xdna_train.Graph()
+            with xdna_train.graph(g2):
+                l2 = step()
+            g2.replay()
+            sync(torch)
+            t1 = time.perf_counter()
+            for _ in range(args.style_steps):
+                g2.replay()
+            float(l2.detach())
+            rate = args.style_steps / (time.perf_counter() - t1)
+            g2.reset()
+            return rate
+
+    # --- ResNet-18 training step (config 5) --------------------------------------------
+    if not args.skip_resnet:
+        log("resnet18: building")
+        rstep, _ = build_resnet(torch, X)
+        rt = timed_steps(rstep, 3, args.resnet_steps, lambda: sync(torch))
+        r_it_s = 1.0 / statistics.median(rt)
+        result["resnet18"] = {"it_s": round(r_it_s, 2), "ms_per_step": round(1e3 * statistics.median(rt), 3),
+                              "mode": "eager", "steps": args.resnet_steps,
+                              "step_tflops": round(RESNET_GFLOP * r_it_s / 1e3, 1),
+                              "workload": "BASELINE config 5: ResNet-18 (BasicBlock [2,2,2,2]), B128 3x64x64, "
+                                          "CE, Adam; median step time, each step ending in loss.item()"}
+        log(f"resnet18: {r_it_s:.1f} it/s")
+
+        # --- CPU baselines (the reference's CPU BF16 path), ABBA against the GPU ------------
     if not args.skip_cpu:
-        log("cpu baseline: conv sweep sample")
-        cpu_tf, reps, cpu_shapes = cpu_conv_baseline(torch)
+        n_aff, n_phys, model = cpu_topology()
+        threads = cpu_threads()
+        log(f"cpu baseline: {threads} threads ({n_phys} physical cores of {n_aff} CPUs visible; {model})")
+        sample_step = sweep_sample_step(torch, X)
+        sample_flops = sweep_flops(CPU_SWEEP_SAMPLE)
+
+        def sweep_sample_gpu_tflops():
+            ts = timed_steps(sample_step, 1, 5, lambda: sync(torch))
+            return sample_flops / statistics.median(ts) / 1e12
+
+        c_tf, g_tf, c_runs, g_runs = abba("conv_sweep_sample", sweep_sample_gpu_tflops, args.cpu_rounds, log)
         result["cpu_baseline"] = {
-            "value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "reference",
-            "sample": f"PyTorch CPU bf16 conv2d fwd+dgrad+wgrad(+bias grad), the reference's CPU BF16 "
-                      f"path, on {len(cpu_shapes)} sweep shapes (N16, C 64-256, H 18/36) x {reps} reps",
+            "value": round(c_tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"PyTorch CPU bf16 conv2d fwd+dgrad+wgrad(+bias grad) (the reference's CPU BF16 path) over "
+                      f"{len(CPU_SWEEP_SAMPLE)} sweep shapes, N16 x every C {{64..512}} x every H {{18,36,72}} "
+                      f"({sample_flops / 1e9:.0f} GFLOP per pass), median of 3 passes per worker",
+            "method": f"separate worker processes, ABBA over {args.cpu_rounds} rounds against the GPU timing of the "
+                      f"same sample, median of per-round medians",
+            "cpu_rounds": [round(v, 4) for v in c_runs], "gpu_same_sample_tflops": round(g_tf, 1),
+            "gpu_rounds": [round(v, 1) for v in g_runs], "speedup_same_sample": round(g_tf / c_tf, 1),
+            "threads": threads, "physical_cores_visible": n_phys, "cpus_in_affinity": n_aff, "cpu_model": model,
         }
-        log(f"cpu baseline: {cpu_tf:.3f} TFLOP/s on {torch.get_num_threads()} threads")
+        log(f"cpu baseline: conv sample {c_tf:.3f} TFLOP/s on the CPU, {g_tf:.1f} on the GPU")
+        if "style_net" in result:
+            c_d, g_d, cd_runs, gd_runs = abba("style_default_adam", style_gpu_it_s, args.cpu_rounds, log)
+            c_f, _, cf_runs, _ = abba("style_fused_adam", style_gpu_it_s, 1, log)
+            result["style_net"].update({
+                "cpu_it_s": round(c_d, 3), "cpu_it_s_rounds": [round(v, 3) for v in cd_runs],
+                "cpu_adam": "CPU default (single-tensor) Adam, the reference's CPU path",
+                "cpu_fused_adam_it_s": round(c_f, 3), "gpu_it_s_abba": round(g_d, 2),
+                "gpu_it_s_abba_rounds": [round(v, 2) for v in gd_runs],
+                "speedup_vs_cpu": round(result["style_net"]["it_s"] / c_d, 1),
+                "speedup_vs_cpu_fused_adam": round(result["style_net"]["it_s"] / c_f, 1)})
+            log(f"style net CPU: {c_d:.2f} it/s (default Adam), {c_f:.2f} it/s (fused Adam)")
+        if "resnet18" in result:
+            c_r, g_r, cr_runs, gr_runs = abba(
+                "resnet18_default_adam",
+                lambda: 1.0 / statistics.median(timed_steps(rstep, 1, args.resnet_steps, lambda: sync(torch))),
+                args.cpu_rounds, log)
+            result["resnet18"].update({"cpu_it_s": round(c_r, 3), "cpu_it_s_rounds": [round(v, 3) for v in cr_runs],
+                                       "gpu_it_s_abba": round(g_r, 2),
+                                       "speedup_vs_cpu": round(result["resnet18"]["it_s"] / c_r, 1)})
+            log(f"resnet18 CPU: {c_r:.3f} it/s")
     print(json.dumps(result), flush=True)
     return 0
 
