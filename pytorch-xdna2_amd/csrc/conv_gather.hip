@@ -323,6 +323,261 @@ __global__ __launch_bounds__(256) void gather_reduce_kernel(const float* __restr
   }
 }
 
+// Weight gradient of stride-1 convs with at most 4 output channels (the style network's
+// last layer, 9x9 32->3): gw[co][ci][ky][kx] = sum over pixels of dy[n][co][oy][ox] *
+// x[n][ci][oy + ky - ph][ox + kx - pw].  As a GEMM its output dimension is the 3 output
+// channels, which MFMA tiles would pad 10x; here each workgroup takes a run of output rows
+// (n, oy), stages the row's Cin x KH input rows (zero-padded to Wo + KW - 1 columns) and
+// its dY row in LDS as fp32, and each thread accumulates Cout sums for each of its
+// (ci, ky, kx) taps with fp32 FMAs.  Partials per workgroup go through gather_reduce_kernel
+// (fixed order).
+constexpr int kFoMaxTaps = 16;  // taps per thread: Cin * KH * KW <= 4096
+
+struct FoArgs {
+  const uint16_t* x;
+  const uint16_t* dy;
+  float* part;  // [workgroups][Cout * Cin * KH * KW]
+  int B, Ci, Co, H, W, KH, KW, ph, pw, Ho, Wo, Wp;
+  int rows_per_wg;
+  int64_t rows;
+};
+
+template <int CO>
+__global__ __launch_bounds__(256) void wgrad_fewout_kernel(FoArgs a) {
+  extern __shared__ float fsm[];
+  const int nxr = a.Ci * a.KH;      // staged input rows
+  float* xs = fsm;                  // [Ci * KH][Wp]
+  float* ds = fsm + nxr * a.Wp;     // [CO][Wo]
+  const int T = a.Ci * a.KH * a.KW;
+  const int tid = threadIdx.x;
+  int toff[kFoMaxTaps];
+  float acc[kFoMaxTaps][CO];
+#pragma unroll
+  for (int j = 0; j < kFoMaxTaps; ++j) {
+    const int t = tid + 256 * j;
+    const int ci = t / (a.KH * a.KW), r = t - ci * (a.KH * a.KW);
+    const int ky = r / a.KW, kx = r - ky * a.KW;
+    toff[j] = t < T ? (ci * a.KH + ky) * a.Wp + kx : -1;
+#pragma unroll
+    for (int c = 0; c < CO; ++c) acc[j][c] = 0.f;
+  }
+  const int rows_per_pass = 256 / a.Wp;  // staged rows loaded per pass (Wp <= 256)
+  const int lrow = tid / a.Wp, lcol = tid - lrow * a.Wp;
+  const int64_t r0 = int64_t(blockIdx.x) * a.rows_per_wg;
+  const int64_t r1 = min(a.rows, r0 + a.rows_per_wg);
+  for (int64_t row = r0; row < r1; ++row) {
+    const int n = int(row / a.Ho), oy = int(row - int64_t(n) * a.Ho);
+    __syncthreads();  // the previous row's reads are done
+    if (lrow < rows_per_pass) {
+      const int ix = lcol - a.pw;
+      for (int q = lrow; q < nxr; q += rows_per_pass) {
+        const int ci = q / a.KH, ky = q - ci * a.KH;
+        const int iy = oy + ky - a.ph;
+        float v = 0.f;
+        if (iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
+          v = bf16_to_f32(a.x[((int64_t(n) * a.Ci + ci) * a.H + iy) * a.W + ix]);
+        xs[q * a.Wp + lcol] = v;
+      }
+    }
+    for (int i = tid; i < CO * a.Wo; i += 256) {
+      const int c = i / a.Wo, ox = i - c * a.Wo;
+      ds[i] = c < a.Co ? bf16_to_f32(a.dy[((int64_t(n) * a.Co + c) * a.Ho + oy) * a.Wo + ox]) : 0.f;
+    }
+    __syncthreads();
+    for (int ox = 0; ox < a.Wo; ++ox) {
+      float d[CO];
+#pragma unroll
+      for (int c = 0; c < CO; ++c) d[c] = ds[c * a.Wo + ox];
+#pragma unroll
+      for (int j = 0; j < kFoMaxTaps; ++j) {
+        if (toff[j] < 0) break;
+        const float xv = xs[toff[j] + ox];
+#pragma unroll
+        for (int c = 0; c < CO; ++c) acc[j][c] = fmaf(d[c], xv, acc[j][c]);
+      }
+    }
+  }
+  float* pb = a.part + int64_t(blockIdx.x) * a.Co * T;
+#pragma unroll
+  for (int j = 0; j < kFoMaxTaps; ++j) {
+    const int t = tid + 256 * j;
+    if (t >= T) break;
+#pragma unroll
+    for (int c = 0; c < CO; ++c)
+      if (c < a.Co) pb[int64_t(c) * T + t] = acc[j][c];
+  }
+}
+
+bool fewout_ok(int Cout, int Cin, int KH, int KW, int sh, int sw, int Wo) {
+  const int Wp = Wo + KW - 1;
+  return sh == 1 && sw == 1 && Cout <= 4 && int64_t(Cin) * KH * KW <= 256 * kFoMaxTaps && Wp <= 256 &&
+         size_t(int64_t(Cin) * KH * Wp + 4 * Wo) * 4 <= 64 * 1024;
+}
+
+// Sliding-window form of the few-output weight gradient for odd kernel widths up to 9.
+// A workgroup takes a run of rows_per_wg consecutive output rows (n, oy), in tiles of at
+// most R rows within one image.  Per tile it stages the tile's input rows, Cin x (R + KH
+// - 1) rows of Wo + KW - 1 columns (fp32, zero padding written out, odd row pitch so that
+// consecutive rows start in different banks), and dY's Cout x R rows.  Thread p owns the
+// row pair (ci, ky) = (p / KH, p % KH) and its KW x Cout sums; it walks each staged row
+// with a KW-wide register window (a ring indexed by the unrolled column phase), so every
+// output column costs one LDS read of x, Cout broadcast reads of dY and KW x Cout FMAs.
+// The staging issues eight global loads before waiting on any.  Each workgroup writes its
+// sums to its own partial slab; gather_reduce_kernel adds the slabs in a fixed order.
+struct FsArgs {
+  const uint16_t* x;
+  const uint16_t* dy;
+  float* part;      // [workgroups][Cout][Cin * KH * KW]
+  int Ci, Co, H, W, KH, ph, pw, Ho, Wo;
+  int pitch;        // staged row pitch in floats: odd, >= Wo + KW - 1
+  int R;            // output rows per tile
+  int rows_per_wg;
+  int64_t rows;     // B * Ho
+};
+
+constexpr int kFsStage = 8;  // global loads in flight per thread while staging
+
+template <int CO, int KW>
+__global__ __launch_bounds__(512) void wgrad_slide_kernel(FsArgs a) {
+  extern __shared__ float fsm[];
+  const int Rs = a.R + a.KH - 1;
+  float* xs = fsm;                        // [Ci][Rs][pitch]
+  float* ds = fsm + a.Ci * Rs * a.pitch;  // [CO][R][Wo]
+  const int P = a.Ci * a.KH, T = P * KW;
+  const int nt = blockDim.x, tid = threadIdx.x;
+  const int wp = a.Wo + KW - 1;
+  const int rpp = nt / wp;  // staged rows per pass (wp <= nt)
+  const int lrow = tid / wp, col = tid - lrow * wp;
+  const int ix = col - a.pw;
+  const bool colok = lrow < rpp && ix >= 0 && ix < a.W;
+  const int64_t r0 = int64_t(blockIdx.x) * a.rows_per_wg;
+  const int64_t r1 = min(a.rows, r0 + a.rows_per_wg);
+  float* pb = a.part + int64_t(blockIdx.x) * a.Co * T;
+  for (int p0 = 0; p0 < P; p0 += nt) {
+    const int p = p0 + tid;
+    const int ci = p / a.KH, ky = p - ci * a.KH;
+    float acc[KW][CO];
+#pragma unroll
+    for (int k = 0; k < KW; ++k)
+#pragma unroll
+      for (int c = 0; c < CO; ++c) acc[k][c] = 0.f;
+    for (int64_t row = r0; row < r1;) {
+      const int n = int(row / a.Ho), oy0 = int(row - int64_t(n) * a.Ho);
+      const int nr = int(min(min(r1 - row, int64_t(a.R)), int64_t(a.Ho - oy0)));
+      const int srows = nr + a.KH - 1, nq = a.Ci * srows;
+      __syncthreads();  // the previous tile's reads are done
+      if (lrow < rpp) {
+        int c = lrow / srows, rr = lrow - c * srows;
+        for (int q = lrow; q < nq; q += kFsStage * rpp) {
+          float v[kFsStage];
+          int dst[kFsStage];
+#pragma unroll
+          for (int j = 0; j < kFsStage; ++j) {
+            const bool in = q + j * rpp < nq;
+            const int iy = oy0 - a.ph + rr;
+            v[j] = in && colok && iy >= 0 && iy < a.H
+                       ? bf16_to_f32(a.x[((int64_t(n) * a.Ci + c) * a.H + iy) * a.W + ix])
+                       : 0.f;
+            dst[j] = in ? (c * Rs + rr) * a.pitch + col : -1;
+            rr += rpp;
+            while (rr >= srows) {
+              rr -= srows;
+              ++c;
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < kFsStage; ++j)
+            if (dst[j] >= 0) xs[dst[j]] = v[j];
+        }
+      }
+      for (int i = tid; i < CO * nr * a.Wo; i += nt) {
+        const int q = i / a.Wo, ox = i - q * a.Wo;
+        const int c = q / nr, r = q - c * nr;
+        ds[(c * a.R + r) * a.Wo + ox] =
+            c < a.Co ? bf16_to_f32(a.dy[((int64_t(n) * a.Co + c) * a.Ho + oy0 + r) * a.Wo + ox]) : 0.f;
+      }
+      __syncthreads();
+      if (p < P) {
+        for (int r = 0; r < nr; ++r) {
+          const float* xr = xs + (ci * Rs + r + ky) * a.pitch;
+          const float* dr = ds + r * a.Wo;
+          float w[KW];
+#pragma unroll
+          for (int k = 0; k < KW - 1; ++k) w[k] = xr[k];
+          for (int ox0 = 0; ox0 < a.Wo; ox0 += KW) {
+#pragma unroll
+            for (int u = 0; u < KW; ++u) {
+              const int ox = ox0 + u;
+              if (ox >= a.Wo) break;
+              w[(u + KW - 1) % KW] = xr[ox + KW - 1];
+              float d[CO];
+#pragma unroll
+              for (int c = 0; c < CO; ++c) d[c] = dr[c * a.R * a.Wo + ox];
+#pragma unroll
+              for (int k = 0; k < KW; ++k)
+#pragma unroll
+                for (int c = 0; c < CO; ++c) acc[k][c] = fmaf(d[c], w[(u + k) % KW], acc[k][c]);
+            }
+          }
+        }
+      }
+      row += nr;
+    }
+    if (p < P) {
+#pragma unroll
+      for (int c = 0; c < CO; ++c)
+#pragma unroll
+        for (int k = 0; k < KW; ++k) pb[int64_t(c) * T + p * KW + k] = acc[k][c];
+    }
+  }
+}
+
+constexpr size_t kFsLdsBudget = 80 * 1024;  // two workgroups per CU
+constexpr size_t kFsLdsMax = 160 * 1024;
+
+size_t slide_lds(int Ci, int KH, int pitch, int R, int Wo) {
+  return (size_t(Ci) * (R + KH - 1) * pitch + size_t(4) * R * Wo) * 4;
+}
+
+// The sliding form's geometry, or false when it does not apply (stride other than 1, more
+// than 4 outputs, an even or wider kernel, rows wider than the block, or one tile beyond
+// one CU's LDS).
+bool slide_args(FsArgs& f, int B, int Cin, int Cout, int H, int W, int KH, int KW, int sh, int sw, int ph,
+                int pw, int Ho, int Wo, int& nt) {
+  if (sh != 1 || sw != 1 || Cout > 4 || Cout < 1 || (KW != 3 && KW != 5 && KW != 7 && KW != 9)) return false;
+  const int64_t P = int64_t(Cin) * KH;
+  nt = int(std::min<int64_t>(512, ceil_div(P, 64) * 64));
+  const int wp = Wo + KW - 1;
+  if (wp > nt || P * KW > (int64_t(1) << 24)) return false;
+  f.pitch = wp | 1;
+  if (slide_lds(Cin, KH, f.pitch, 1, Wo) > kFsLdsMax) return false;
+  f.Ci = Cin; f.Co = Cout; f.H = H; f.W = W; f.KH = KH; f.ph = ph; f.pw = pw; f.Ho = Ho; f.Wo = Wo;
+  f.rows = int64_t(B) * Ho;
+  // about two workgroups per CU; tiles as tall as the LDS budget allows
+  f.rows_per_wg = int(ceil_div(f.rows, std::min<int64_t>(f.rows, 512)));
+  f.R = 1;
+  while (f.R < f.rows_per_wg && f.R < Ho && slide_lds(Cin, KH, f.pitch, f.R + 1, Wo) <= kFsLdsBudget) ++f.R;
+  return true;
+}
+
+template <int CO>
+int launch_slide(const FsArgs& f, int KW, unsigned grid, int nt, size_t lds, hipStream_t st) {
+  const void* fn = KW == 3   ? reinterpret_cast<const void*>(&wgrad_slide_kernel<CO, 3>)
+                   : KW == 5 ? reinterpret_cast<const void*>(&wgrad_slide_kernel<CO, 5>)
+                   : KW == 7 ? reinterpret_cast<const void*>(&wgrad_slide_kernel<CO, 7>)
+                             : reinterpret_cast<const void*>(&wgrad_slide_kernel<CO, 9>);
+  if (lds > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(kFsLdsMax)) !=
+                             hipSuccess) {
+    set_error("xdna_conv2d_wgrad_bf16: cannot raise the LDS limit of the few-output kernel");
+    return -1;
+  }
+  if (KW == 3) wgrad_slide_kernel<CO, 3><<<grid, nt, lds, st>>>(f);
+  else if (KW == 5) wgrad_slide_kernel<CO, 5><<<grid, nt, lds, st>>>(f);
+  else if (KW == 7) wgrad_slide_kernel<CO, 7><<<grid, nt, lds, st>>>(f);
+  else wgrad_slide_kernel<CO, 9><<<grid, nt, lds, st>>>(f);
+  return 0;
+}
+
 bool gconv_args(const char* what, GArgs& a, int B, int Cin, int Cout, int H, int W, int KH, int KW,
                 int sh, int sw, int ph, int pw) {
   if (B < 1 || Cin < 1 || Cout < 1 || H < 1 || W < 1 || KH < 1 || KW < 1 || sh < 1 || sw < 1 || ph < 0 ||
@@ -687,6 +942,57 @@ int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, 
   GArgs a{};
   if (!gconv_args("xdna_conv2d_wgrad_bf16", a, B, Cin, Cout, H, W, KH, KW, sh, sw, ph, pw)) return -1;
   a.x = x; a.dy = dy;
+  hipStream_t st = as_stream(stream);
+  FsArgs fs{};
+  int fs_nt = 0;
+  if (slide_args(fs, B, Cin, Cout, H, W, KH, KW, sh, sw, ph, pw, a.Ho, a.Wo, fs_nt)) {
+    fs.x = x;
+    fs.dy = dy;
+    const int64_t nwg = ceil_div(fs.rows, fs.rows_per_wg);
+    const int64_t mn = int64_t(Cout) * Cin * KH * KW;
+    if (!admit_launch("xdna_conv2d_wgrad_bf16")) return -1;
+    fs.part = static_cast<float*>(xdna_hip_cache_alloc(size_t(nwg) * size_t(mn) * sizeof(float)));
+    if (!fs.part) return -1;
+    const size_t lds = slide_lds(Cin, KH, fs.pitch, fs.R, fs.Wo);
+    const unsigned grid = unsigned(nwg);
+    const int rc = Cout == 1   ? launch_slide<1>(fs, KW, grid, fs_nt, lds, st)
+                   : Cout == 2 ? launch_slide<2>(fs, KW, grid, fs_nt, lds, st)
+                   : Cout == 3 ? launch_slide<3>(fs, KW, grid, fs_nt, lds, st)
+                               : launch_slide<4>(fs, KW, grid, fs_nt, lds, st);
+    if (rc) {
+      xdna_hip_cache_free(fs.part);
+      return -1;
+    }
+    gather_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(mn, 32), 8192)), 256, 0, st>>>(fs.part, gw, mn,
+                                                                                           int(nwg));
+    xdna_hip_cache_free(fs.part);  // stream-ordered reuse
+    if (check_launch("xdna_conv2d_wgrad_bf16")) return -1;
+    if (gb) return xdna_conv3x3_bias_grad_bf16(dy, gb, B, Cout, a.Ho, a.Wo, stream);
+    return 0;
+  }
+  if (fewout_ok(Cout, Cin, KH, KW, sh, sw, a.Wo)) {
+    FoArgs f{x, dy, nullptr, B, Cin, Cout, H, W, KH, KW, ph, pw, a.Ho, a.Wo, a.Wo + KW - 1, 1,
+             int64_t(B) * a.Ho};
+    // about two workgroups per CU, at least one output row each
+    const int64_t wgs = std::min<int64_t>(f.rows, 512);
+    f.rows_per_wg = int(ceil_div(f.rows, wgs));
+    const int64_t nwg = ceil_div(f.rows, f.rows_per_wg);
+    const int64_t mn = int64_t(Cout) * Cin * KH * KW;
+    if (!admit_launch("xdna_conv2d_wgrad_bf16")) return -1;
+    f.part = static_cast<float*>(xdna_hip_cache_alloc(size_t(nwg) * size_t(mn) * sizeof(float)));
+    if (!f.part) return -1;
+    const size_t lds = size_t(int64_t(Cin) * KH * f.Wp + 4 * f.Wo) * 4;
+    if (Cout == 1) wgrad_fewout_kernel<1><<<unsigned(nwg), 256, lds, st>>>(f);
+    else if (Cout == 2) wgrad_fewout_kernel<2><<<unsigned(nwg), 256, lds, st>>>(f);
+    else if (Cout == 3) wgrad_fewout_kernel<3><<<unsigned(nwg), 256, lds, st>>>(f);
+    else wgrad_fewout_kernel<4><<<unsigned(nwg), 256, lds, st>>>(f);
+    gather_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(mn, 32), 8192)), 256, 0, st>>>(f.part, gw, mn,
+                                                                                           int(nwg));
+    xdna_hip_cache_free(f.part);  // stream-ordered reuse
+    if (check_launch("xdna_conv2d_wgrad_bf16")) return -1;
+    if (gb) return xdna_conv3x3_bias_grad_bf16(dy, gb, B, Cout, a.Ho, a.Wo, stream);
+    return 0;
+  }
   a.M = Cout; a.N = Cin * KH * KW; a.K = B * a.Ho * a.Wo;
   // split the pixel reduction until the grid covers the CUs twice (fixed-order partial sums)
   const int64_t tiles = ceil_div(a.M, tile_m(a.M)) * ceil_div(a.N, kGTN);
@@ -699,7 +1005,6 @@ int xdna_conv2d_wgrad_bf16(const uint16_t* x, const uint16_t* dy, uint16_t* gw, 
   if (!admit_launch("xdna_conv2d_wgrad_bf16")) return -1;
   a.part = static_cast<float*>(xdna_hip_cache_alloc(size_t(a.nsplit) * size_t(mn) * sizeof(float)));
   if (!a.part) return -1;
-  hipStream_t st = as_stream(stream);
   if (launch_gather<kGWgrad>(a, st)) {
     xdna_hip_cache_free(a.part);
     return -1;

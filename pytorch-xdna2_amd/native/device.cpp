@@ -37,12 +37,14 @@
 namespace xdna_backend {
 
 std::atomic<int> g_mode{2};
-// Convolutions outside the 3x3 path: 0 PyTorch-ROCm, 1 (default) the general HIP kernels
-// where they measured faster than MIOpen, 2 the general HIP kernels always.
+// Convolutions outside the 3x3 path: 0 PyTorch-ROCm, 1 the general HIP kernels where they
+// measured faster than MIOpen, 2 (default) the general HIP kernels always: MIOpen misses
+// the conv bar (2 bf16 ulp) on some of these layers, the HIP kernels sum in fp32 and
+// round once.
 std::atomic<int> g_gconv_mode{[] {
   const char* e = std::getenv("XDNA_GENERAL_CONV");
-  const int v = e ? std::atoi(e) : 1;
-  return v < 0 || v > 2 ? 1 : v;
+  const int v = e ? std::atoi(e) : 2;
+  return v < 0 || v > 2 ? 2 : v;
 }()};
 std::atomic<int> g_conv_layout{[] {
   const char* e = std::getenv("XDNA_CONV_LAYOUT");

@@ -316,10 +316,11 @@ def npu_mode() -> int:
 
 @_api
 def set_general_conv_mode(mode: int) -> None:
-    """Convolutions outside the 3x3 path (strided, 1x1, 9x9, ...): 0 PyTorch-ROCm (MIOpen),
-    1 (default) the general HIP kernels where they measured faster and within the conv
-    bar, 2 the general HIP kernels always.  XDNA_GENERAL_CONV sets the initial value.  No
-    reference counterpart (the reference runs these on its CPU)."""
+    """Convolutions outside the 3x3 and 1x1 paths (strided, 5x5, 9x9, ...): 0 PyTorch-ROCm
+    (MIOpen), 1 the general HIP kernels where they measured faster than MIOpen, 2 (default)
+    the general HIP kernels always (MIOpen misses the conv bar on some layers).
+    XDNA_GENERAL_CONV sets the initial value.  No reference counterpart (the reference runs
+    these on its CPU)."""
     native().set_general_conv_mode(int(mode))
 
 

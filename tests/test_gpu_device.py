@@ -172,9 +172,9 @@ def test_conv_bias_views(xdna, offset, cout):
 
 
 def test_other_convs_run_on_general_kernels(xdna):
-    """5x5, 1x1, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on the general
-    HIP kernels (mode 2: always), the 3x3 / stride-2 / pad-1 one on the stride-1 3x3 path,
-    and all match the CPU bf16 path and the float64 oracle."""
+    """5x5, 9x9 and 7x7-stride-2 convolutions (forward and backward) run on the general HIP
+    kernels (mode 2: always), 1x1 ones on the 1x1 GEMM path, the 3x3 / stride-2 / pad-1 one
+    on the stride-1 3x3 path, and all match the CPU bf16 path and the float64 oracle."""
     xdna.reset_mapped_cpu_stats()
     xdna.set_general_conv_mode(2)
     specs = [(8, 16, 5, 1, 2), (8, 16, 3, 2, 1), (8, 16, 1, 1, 0), (3, 32, 9, 1, 4), (3, 16, 7, 2, 3),
@@ -202,54 +202,94 @@ def test_other_convs_run_on_general_kernels(xdna):
         for got, ref in ((yd, yc), (xd.grad, xc.grad), (cd.weight.grad, conv.weight.grad)):
             g, r = got.detach().cpu().float(), ref.detach().float()
             assert (g - r).norm() / r.norm() < 1e-2, what
-    xdna.set_general_conv_mode(1)
     st = xdna.mapped_cpu_stats()
-    n = len(specs) - 1  # all but the 3x3 / stride-2 / pad-1 conv
     for key in ("hip_conv2d.fwd.run", "hip_conv2d.dx.run", "hip_conv2d.dw.run"):
-        assert st.get(key, {}).get("calls", 0) == n, (key, st)
+        assert st.get(key, {}).get("calls", 0) == 3, (key, st)  # 5x5, 9x9, 7x7 / stride 2
+    for key in ("hip_conv1x1.fwd.run", "hip_conv1x1.bwd.run"):
+        assert st.get(key, {}).get("calls", 0) == 2, (key, st)
     for key in ("hip_conv3x3_s2.fwd.run", "hip_conv3x3_s2.bwd.run"):
         assert st.get(key, {}).get("calls", 0) == 1, (key, st)
     assert "aten::convolution.rocm" not in st and "aten::convolution_backward.rocm" not in st
 
 
+def _routed_conv(cin, cout, k, s, pd, B=2, H=12, W=10, seed=0):
+    """One conv forward + backward on xdna from CPU-made bf16 operands; returns the path
+    counters and the results checked against the float64 oracle."""
+    torch.manual_seed(seed + cin + cout + k)
+    conv = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16()
+    x = torch.randn(B, cin, H, W).bfloat16()
+    cd = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16().to(X)
+    cd.load_state_dict(conv.state_dict())
+    xdna_train.reset_mapped_cpu_stats()
+    xd = x.to(X).requires_grad_()
+    yd = cd(xd)
+    dy = torch.randn(yd.shape).bfloat16()
+    yd.backward(dy.to(X))
+    torch.xdna.synchronize()
+    st = xdna_train.mapped_cpu_stats()
+    xb, wb, bb, dyb = (bits(t) for t in (x, conv.weight, conv.bias, dy))
+    what = f"k{k} s{s} {cin}->{cout} B{B} {H}x{W}"
+    check_bf16(bits(yd), oracle.conv2d_fwd(xb, wb, bb, (s, s), (pd, pd)), what=f"fwd {what}")
+    check_bf16(bits(xd.grad), oracle.conv2d_dgrad(dyb, wb, (H, W), (s, s), (pd, pd)), what=f"dgrad {what}")
+    gw, gb = oracle.conv2d_wgrad(xb, dyb, (k, k), (s, s), (pd, pd))
+    check_bf16(bits(cd.weight.grad), gw, what=f"wgrad {what}")
+    return st, bits(cd.bias.grad), gb, what
+
+
 def test_default_routing_of_general_convs(xdna):
-    """Mode 1 (default) routes each conv direction where it was measured faster: the 9x9
-    32->3 forward and the 9x9 3->32 input gradient to the direct form, the 9x9 3->32
-    forward and weight gradient to the gather GEMM, 3x3 / stride-2 layers to the stride-1
-    3x3 path, the 9x9 32->3 gradients to MIOpen; every result matches the float64
+    """Mode 2 (default) runs every eligible conv direction on the HIP kernels, the style
+    network's 9x9 32->3 gradients included (the few-output weight-gradient kernel and the
+    gather input gradient); 3x3 / stride-2 layers take the stride-1 3x3 path.  Mode 1 keeps
+    the gradients of few-output layers on MIOpen.  Every result matches the float64
     oracle."""
-    assert xdna.general_conv_mode() == 1
-    specs = [  # cin, cout, k, s, p, expected counters
-        (32, 3, 9, 1, 4, {"hip_conv2d.fwd.run": 1, "aten::convolution_backward.rocm": 1}),
-        (3, 32, 9, 1, 4, {"hip_conv2d.fwd.run": 1, "hip_conv2d.dw.run": 1, "hip_conv2d.dx.run": 1,
-                          "aten::convolution_backward.rocm": 0}),
-        (32, 64, 3, 2, 1, {"hip_conv3x3_s2.fwd.run": 1, "hip_conv3x3_s2.bwd.run": 1,
-                           "aten::convolution.rocm": 0, "aten::convolution_backward.rocm": 0}),
+    assert xdna.general_conv_mode() == 2
+    hip_all = {"hip_conv2d.fwd.run": 1, "hip_conv2d.dw.run": 1, "hip_conv2d.dx.run": 1,
+               "aten::convolution.rocm": 0, "aten::convolution_backward.rocm": 0}
+    specs = [  # cin, cout, k, s, p, mode, expected counters
+        (32, 3, 9, 1, 4, 2, hip_all),
+        (3, 32, 9, 1, 4, 2, hip_all),
+        (32, 64, 3, 2, 1, 2, {"hip_conv3x3_s2.fwd.run": 1, "hip_conv3x3_s2.bwd.run": 1,
+                              "aten::convolution.rocm": 0, "aten::convolution_backward.rocm": 0}),
+        (32, 3, 9, 1, 4, 1, {"hip_conv2d.fwd.run": 1, "aten::convolution_backward.rocm": 1}),
     ]
-    for cin, cout, k, s, pd, expect in specs:
-        torch.manual_seed(cin + cout)
-        conv = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16()
-        x = torch.randn(2, cin, 12, 10).bfloat16()
-        cd = nn.Conv2d(cin, cout, k, stride=s, padding=pd).bfloat16().to(X)
-        cd.load_state_dict(conv.state_dict())
-        xdna.reset_mapped_cpu_stats()
-        xd = x.to(X).requires_grad_()
-        yd = cd(xd)
-        dy = torch.randn(yd.shape).bfloat16()
-        yd.backward(dy.to(X))
-        torch.xdna.synchronize()
-        st = xdna.mapped_cpu_stats()
-        for key, n in expect.items():
-            assert st.get(key, {}).get("calls", 0) == n, (cin, cout, key, st)
-        xb, wb, bb, dyb = (bits(t) for t in (x, conv.weight, conv.bias, dy))
-        what = f"k{k} s{s} {cin}->{cout}"
-        check_bf16(bits(yd), oracle.conv2d_fwd(xb, wb, bb, (s, s), (pd, pd)), what=f"fwd {what}")
-        check_bf16(bits(xd.grad), oracle.conv2d_dgrad(dyb, wb, (12, 10), (s, s), (pd, pd)), what=f"dgrad {what}")
-        gw, gb = oracle.conv2d_wgrad(xb, dyb, (k, k), (s, s), (pd, pd))
-        check_bf16(bits(cd.weight.grad), gw, what=f"wgrad {what}")
-        # bias gradients from MIOpen sum in another order: relative bar
-        g, r = oracle.bf16_value(bits(cd.bias.grad)), gb
-        assert np.abs(g - r).max() <= 2 * oracle.bf16_ulp(np.abs(r).max()) + 1e-6, what
+    try:
+        for cin, cout, k, s, pd, mode, expect in specs:
+            xdna.set_general_conv_mode(mode)
+            st, gbd, gb, what = _routed_conv(cin, cout, k, s, pd)
+            for key, n in expect.items():
+                assert st.get(key, {}).get("calls", 0) == n, (cin, cout, mode, key, st)
+            if mode == 2:
+                check_bf16(gbd, gb, what=f"bias grad {what}")
+            else:  # bias gradients from MIOpen sum in another order: relative bar
+                g = oracle.bf16_value(gbd)
+                assert np.abs(g - gb).max() <= 2 * oracle.bf16_ulp(np.abs(gb).max()) + 1e-6, what
+    finally:
+        xdna.set_general_conv_mode(2)
+
+
+@pytest.mark.parametrize("cin,cout,k,pd,B,H,W", [
+    (32, 3, 9, 4, 40, 36, 36),   # the style network's last layer at its training size
+    (32, 3, 9, 4, 1, 7, 5),      # output narrower than the kernel
+    (16, 1, 5, 2, 3, 17, 33),
+    (48, 2, 7, 0, 2, 20, 19),    # no padding
+    (4, 4, 3, 0, 5, 9, 130),     # wide rows: one staged input row per pass
+    (64, 4, 7, 3, 2, 11, 11),    # 3136 taps: 13 per thread
+    (3, 3, 9, 4, 2, 16, 16),
+    (640, 1, 3, 0, 2, 6, 6),     # 1920 row pairs: four passes of 512 threads
+    (8, 2, 11, 5, 2, 15, 14),    # wider than 9 and even widths: the per-tap form
+    (16, 3, 4, 2, 2, 10, 12),
+])
+def test_few_output_weight_gradient(xdna, cin, cout, k, pd, B, H, W):
+    """Stride-1 convs with at most 4 output channels take the few-output weight-gradient
+    kernels (fp32 FMA over staged rows, fixed-order partial reduce; a sliding register
+    window for odd widths up to 9, one sum per tap otherwise): weight and bias gradients
+    match the float64 oracle to the conv bar, across kernel sizes, paddings, row widths and
+    tap counts."""
+    st, gbd, gb, what = _routed_conv(cin, cout, k, 1, pd, B=B, H=H, W=W, seed=5)
+    check_bf16(gbd, gb, what=f"bias grad {what}")
+    for key in ("hip_conv2d.dw.run", "hip_conv2d.dx.run"):
+        assert st.get(key, {}).get("calls", 0) == 1, (key, st)
+    assert "aten::convolution_backward.rocm" not in st
 
 
 def test_trainable_weight_forms_follow_the_version(xdna):
