@@ -1323,11 +1323,14 @@ void wgrad_kernel(WgradArgs a) {
   }
 }
 
-// gw[co][ci][t] = bf16(sum over splits of part[split][co][t][ci]) and gb likewise from
-// bpart.  The 256 threads are ZG groups of 256 / ZG consecutive outputs: group z sums
-// splits z, z + ZG, ... and the groups are added in order through LDS, a fixed
-// association per output (deterministic), with ZG loads in flight per output when the
-// split count is large.
+// gw[co][ci][0..8] = bf16(sum over splits of part[split][co][t][ci]) and gb likewise from
+// bpart.  Thread (z, e) of a block owns the (co, ci) pair base + e with its nine taps and
+// sums splits z, z + ZG, ... (nine independent loads per split, each coalesced over e);
+// the ZG groups are added in order through LDS, a fixed association per output (the
+// result is deterministic).  The bf16 results are staged in LDS and the block writes its
+// pairs' outputs, one contiguous run of gw, consecutive threads on consecutive elements
+// (OIHW keeps the nine taps of a pair together, the partials keep each tap's ci run
+// together: the transposition happens in LDS).
 template <int ZG>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part,
                                                            const float* __restrict__ bpart,
@@ -1335,6 +1338,65 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
                                                            uint16_t* __restrict__ gb, int Cout,
                                                            int Cin, int co_pad, int ci_pad,
                                                            int splits) {
+  constexpr int EPB = 256 / ZG;
+  const int z = threadIdx.x / EPB, e = threadIdx.x % EPB;
+  const int64_t npair = int64_t(Cout) * Cin;
+  const int64_t stride = int64_t(co_pad) * 9 * ci_pad;
+  __shared__ float red[ZG > 1 ? 9 * 256 : 1];
+  __shared__ uint16_t ob[9 * EPB];
+  for (int64_t base = int64_t(blockIdx.x) * EPB; base < npair; base += int64_t(gridDim.x) * EPB) {
+    const int64_t i = base + e;
+    float s[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) s[t] = 0.0f;
+    if (i < npair) {
+      const int co = int(i / Cin), ci = int(i - int64_t(co) * Cin);
+      const float* src = part + int64_t(co) * 9 * ci_pad + ci;
+      for (int k = z; k < splits; k += ZG) {
+        const float* q = src + k * stride;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) s[t] += q[t * ci_pad];
+      }
+    }
+    if (ZG > 1) {
+#pragma unroll
+      for (int t = 0; t < 9; ++t) red[t * 256 + threadIdx.x] = s[t];
+      __syncthreads();
+      if (z == 0)
+        for (int g = 1; g < ZG; ++g)
+#pragma unroll
+          for (int t = 0; t < 9; ++t) s[t] += red[t * 256 + g * EPB + e];
+    }
+    if (z == 0)
+#pragma unroll
+      for (int t = 0; t < 9; ++t) ob[e * 9 + t] = f32_to_bf16(s[t]);
+    __syncthreads();
+    const int n_out = int(min(int64_t(EPB), npair - base)) * 9;
+    for (int j = threadIdx.x; j < n_out; j += 256) gw[base * 9 + j] = ob[j];
+    __syncthreads();  // red and ob are rewritten by the next pass
+  }
+  if (gb)
+    for (int co = blockIdx.x * 256 + threadIdx.x; co < Cout; co += gridDim.x * 256) {
+      float s = 0.0f;
+      for (int k = 0; k < splits; ++k) s += bpart[int64_t(k) * co_pad + co];
+      gb[co] = f32_to_bf16(s);
+    }
+}
+
+// One thread per output element, for layers with few outputs: gw[co][ci][t] = bf16(sum
+// over splits of part[split][co][t][ci]), gb likewise from bpart.  The 256 threads are ZG
+// groups of 256 / ZG consecutive elements in partial order (coalesced reads): group z sums
+// splits z, z + ZG, ... and the groups are added in order through LDS (a fixed
+// association per output), with ZG loads in flight per output when the split count is
+// large.  Nine times the threads of wgrad_reduce_kernel: small layers have few outputs and
+// many splits.
+template <int ZG>
+__global__ __launch_bounds__(256) void wgrad_reduce_elem_kernel(const float* __restrict__ part,
+                                                                const float* __restrict__ bpart,
+                                                                uint16_t* __restrict__ gw,
+                                                                uint16_t* __restrict__ gb, int Cout,
+                                                                int Cin, int co_pad, int ci_pad,
+                                                                int splits) {
   constexpr int EPB = 256 / ZG;
   const int z = threadIdx.x / EPB, e = threadIdx.x % EPB;
   const int64_t n = int64_t(Cout) * 9 * Cin;
@@ -1371,6 +1433,41 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
       }
     }
   }
+}
+
+// Launches the split-K reduce of the weight gradient: the pair form (coalesced writes)
+// from 65536 (co, ci) pairs on, with at most 16 splits per thread; the element form below
+// (its parallelism is what layers with few outputs and many splits need).
+void launch_wgrad_reduce(const float* part, const float* bpart, uint16_t* gw, uint16_t* gb, int Cout, int Cin,
+                         int co_pad, int ci_pad, int splits, hipStream_t st) {
+  const int64_t npair = int64_t(Cout) * Cin;
+  if (npair >= 65536) {
+    int zg = 1;
+    while (zg < 8 && zg * 2 <= splits && ceil_div(splits, zg) > 16) zg *= 2;
+    const unsigned grid = unsigned(std::max<int64_t>(std::min<int64_t>(ceil_div(npair, 256 / zg), 16384),
+                                                     gb ? ceil_div(Cout, 256) : 1));
+#define XDNA_WRED(zg_) wgrad_reduce_kernel<zg_><<<grid, 256, 0, st>>>(part, bpart, gw, gb, Cout, Cin, co_pad, ci_pad, splits)
+    switch (zg) {
+      case 1: XDNA_WRED(1); break;
+      case 2: XDNA_WRED(2); break;
+      case 4: XDNA_WRED(4); break;
+      default: XDNA_WRED(8); break;
+    }
+#undef XDNA_WRED
+    return;
+  }
+  const int64_t n = npair * 9 + Cout;
+  const int zg = splits >= 64 ? 8 : splits >= 16 ? 4 : splits >= 4 ? 2 : 1;
+  const unsigned grid = unsigned(std::min<int64_t>(ceil_div(n, 256 / zg), 8192));
+#define XDNA_WRED(zg_) \
+  wgrad_reduce_elem_kernel<zg_><<<grid, 256, 0, st>>>(part, bpart, gw, gb, Cout, Cin, co_pad, ci_pad, splits)
+  switch (zg) {
+    case 1: XDNA_WRED(1); break;
+    case 2: XDNA_WRED(2); break;
+    case 4: XDNA_WRED(4); break;
+    default: XDNA_WRED(8); break;
+  }
+#undef XDNA_WRED
 }
 
 // Bias gradient on its own: one workgroup per channel, fixed-order tree.
@@ -2131,17 +2228,7 @@ int xdna_conv3x3_wgrad_packed_bf16(uint16_t* gw, uint16_t* gb, int B, int Cin, i
     wgrad_kernel<4><<<grid, kWgThreads, p.lds_bytes, st>>>(a);
   else
     wgrad_kernel<6><<<grid, kWgThreads, p.lds_bytes, st>>>(a);
-  const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
-  const int zg = p.splits >= 64 ? 8 : p.splits >= 16 ? 4 : p.splits >= 4 ? 2 : 1;
-  const unsigned rgrid = unsigned(std::min<int64_t>(ceil_div(n, 256 / zg), 8192));
-  if (zg == 8)
-    wgrad_reduce_kernel<8><<<rgrid, 256, 0, st>>>(bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  else if (zg == 4)
-    wgrad_reduce_kernel<4><<<rgrid, 256, 0, st>>>(bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  else if (zg == 2)
-    wgrad_reduce_kernel<2><<<rgrid, 256, 0, st>>>(bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  else
-    wgrad_reduce_kernel<1><<<rgrid, 256, 0, st>>>(bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  launch_wgrad_reduce(bufs.part, bufs.bpart, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits, st);
   return check_launch("conv3x3 wgrad");
 }
 
@@ -2220,18 +2307,7 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
     wgrad_rows_kernel<128><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
   else
     wgrad_rows_kernel<64><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
-  const int64_t n = int64_t(Cout) * 9 * Cin + Cout;
-  const int zg = p.splits >= 64 ? 8 : p.splits >= 16 ? 4 : p.splits >= 4 ? 2 : 1;
-  const unsigned rgrid = unsigned(std::min<int64_t>(ceil_div(n, 256 / zg), 8192));
-  float* bp = gb ? a.bpart : nullptr;
-  if (zg == 8)
-    wgrad_reduce_kernel<8><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  else if (zg == 4)
-    wgrad_reduce_kernel<4><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  else if (zg == 2)
-    wgrad_reduce_kernel<2><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
-  else
-    wgrad_reduce_kernel<1><<<rgrid, 256, 0, st>>>(a.part, bp, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits);
+  launch_wgrad_reduce(a.part, gb ? a.bpart : nullptr, gw, gb, Cout, Cin, p.co_pad, p.ci_pad, p.splits, st);
   return check_launch("conv3x3 wgrad rows");
 }
 
