@@ -31,6 +31,12 @@ CASES = [
     ("f32_s9", torch.float32, 9, 1e-3, 0.9, 0.999, 1e-8, 0.0, False, False, False, None),
     ("f32_adamw_ams", torch.float32, 6, 1e-3, 0.9, 0.999, 1e-8, 0.02, True, False, True, None),
     ("f32_wd", torch.float32, 3, 1e-3, 0.9, 0.999, 1e-8, 0.01, False, False, False, None),
+    # beta1 <= 0.5: the first moment's lerp weight 1 - beta1 is >= 0.5, which takes the
+    # lerp's other form (computed from the end point)
+    ("bf16_b1_03", torch.bfloat16, 3, 1e-3, 0.3, 0.999, 1e-8, 0.0, False, False, False, None),
+    ("f32_b1_03", torch.float32, 4, 1e-3, 0.3, 0.99, 1e-8, 0.01, False, False, False, None),
+    ("bf16_b1_05", torch.bfloat16, 2, 1e-3, 0.5, 0.999, 1e-8, 0.0, False, False, False, None),
+    ("f32_b1_0_ams", torch.float32, 5, 1e-3, 0.0, 0.999, 1e-8, 0.02, True, False, True, None),
 ]
 
 

@@ -1,7 +1,7 @@
 """Training on xdna follows the reference's CPU bf16 path: loss curves of BASELINE configs
-1 (200 steps), 4 (200 steps) and 3 (40 steps, bounded by the CPU's time) against the same
-seeded run on torch.device("cpu") in bf16, plus config 4's first-step gradients against
-an fp32 computation.
+1 (200 steps), 4 (200 steps), 3 (40 steps) and 5 (20 steps; the last two bounded by the
+CPU's time) against the same seeded run on torch.device("cpu") in bf16, plus config 4's
+first-step gradients against an fp32 computation.
 
 Curves are compared as the reference compares them (benchmarks/loss_curve_compare.py:
 25-36): means over windows of max(10, steps/10) steps.  The CPU run uses Adam's fused
@@ -119,6 +119,17 @@ def test_c4_style_200_steps():
 def test_c3_mlp_40_steps():
     _check("C3", bench.build_mlp, 40, ("hip_gemm.addmm.run", "hip_gemm.mm.run", "hip_adam.run"),
            strict_windows=None)
+
+
+@pytest.mark.timeout(600)
+def test_c5_resnet18_20_steps():
+    """BASELINE config 5 (ResNet-18, B128 3x64x64, CE, Adam): 20 steps, two windows of 10,
+    bounded by the CPU's time (about 0.6 s a step, five CPU runs).  Every conv direction,
+    the training batch norms and the Adam step run on the HIP kernels."""
+    _check("C5", bench.build_resnet, 20,
+           ("hip_conv3x3.fwd.run", "hip_conv3x3.dx.run", "hip_conv3x3.dw_rows.run", "hip_conv3x3_s2.fwd.run",
+            "hip_conv1x1.fwd.run", "hip_batch_norm_train.fwd.run", "hip_batch_norm_train.bwd.run",
+            "hip_adam.run"), strict_windows=1)
 
 
 def _style_grads(device, dtype):
