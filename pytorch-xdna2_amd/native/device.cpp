@@ -102,7 +102,21 @@ void count_call(const char* name, int64_t ns) {
 ScopedCount::ScopedCount(const char* n) : name(n), t0(now_ns()) {}
 ScopedCount::~ScopedCount() { count_call(name, now_ns() - t0); }
 
-void* current_stream() { return c10::hip::getCurrentHIPStream(0).stream(); }
+// Backend work runs on PyTorch-ROCm's current stream of device 0.  The caching allocator
+// does not track streams: a freed block serves the next allocation at once, which is safe
+// because every user of a block is ordered on that one stream.  Work on another stream is
+// therefore refused, except on a stream that is capturing a graph (a capture allocates
+// from a private pool whose blocks no eager work receives).
+void* current_stream() {
+  const c10::hip::HIPStream s = c10::hip::getCurrentHIPStream(0);
+  if (s != c10::hip::getDefaultHIPStream(0)) {
+    const int r = xdna_hip_stream_capturing(s.stream());
+    TORCH_CHECK(r > 0, "xdna: work on a stream other than the default one is not supported (the device's "
+                "caching allocator orders every use of a block on one stream); run xdna tensors on the "
+                "default stream, or capture the work in a graph");
+  }
+  return s.stream();
+}
 
 int64_t capture_tag() {
   const int r = xdna_hip_stream_capturing(current_stream());

@@ -511,3 +511,24 @@ def test_frozen_weights_prepared_once_and_refreshed_on_write():
     y3 = cd(xd)
     assert torch.allclose(y3.cpu().float(), conv(x).float(), atol=5e-2, rtol=5e-2)
     assert not torch.allclose(y3.cpu().float(), y2.cpu().float(), atol=5e-2, rtol=5e-2)
+
+
+def test_non_default_stream_is_refused(xdna):
+    """The device's caching allocator orders every use of a block on one stream, so xdna
+    work on a side stream raises (instead of racing a recycled block); the default stream
+    keeps working afterwards, and a graph capture (on its own capturing stream) is allowed."""
+    a = torch.ones(1024, device=X)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with pytest.raises(RuntimeError, match="default one is not supported"):
+            (a + 1).cpu()
+    torch.cuda.synchronize()
+    assert float((a + 1).sum().cpu()) == 2048.0
+    g = xdna.Graph()
+    b = torch.zeros(1024, device=X)
+    with xdna.graph(g):
+        b.add_(a)
+    g.replay()
+    g.replay()
+    torch.xdna.synchronize()
+    assert float(b.sum().cpu()) == 2048.0
