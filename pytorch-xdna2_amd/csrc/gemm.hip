@@ -44,7 +44,31 @@ struct GemmArgs {
   float* part;  // split-K: fp32 partial products [nsplit][batch][M][N], else null
   int rs_ok;    // 1: the epilogue stores through buffer resources (extents host-checked)
   int c_bytes, bias_bytes, part_bytes;  // byte extents of one batch's C / bias / partials
+  int xcd_group;  // > 0: XCD-blocked tile order with groups of this many tile rows (gemm4)
 };
+
+// Workgroups go round-robin to the 8 XCDs (each with its own L2) in linear id order.  In
+// launch order (x = column tile fastest) XCD x would take the column tiles x, x + 8, ...
+// of every row, so each XCD would read all of A.  With xcd_group = G (the tile count a
+// multiple of 8), XCD x takes tiles [x T/8, (x+1) T/8) of a grouped order (G tile rows at
+// a time, rows fastest): a compact block of rows and columns per XCD, whose A and B tiles
+// its L2 holds for the workgroups in flight.
+constexpr int kGemmXcds = 8;
+
+__device__ inline void gemm_tile_xy(const GemmArgs& g, int& bx, int& by) {
+  bx = blockIdx.x;
+  by = blockIdx.y;
+  if (g.xcd_group <= 0) return;
+  const int nx = gridDim.x, my = gridDim.y;
+  const int T = nx * my;
+  const int L = by * nx + bx;
+  const int t = (L % kGemmXcds) * (T / kGemmXcds) + L / kGemmXcds;
+  const int gsz = g.xcd_group * nx;
+  const int grp = t / gsz, r = t - grp * gsz;
+  const int gm = min(g.xcd_group, my - grp * g.xcd_group);
+  by = grp * g.xcd_group + r % gm;
+  bx = r / gm;
+}
 
 // Branch-free epilogue of one wave's MI x NJ block of 32 x 32 MFMA tiles (rows mb + i*32 +
 // mfma_row(r, lane), columns nb + j*32 + lane % 32), through buffer resources: an element
@@ -568,7 +592,9 @@ void gemm4_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * kT4, n0 = blockIdx.x * kT4;
+  int tbx, tby;
+  gemm_tile_xy(g, tbx, tby);
+  const int m0 = tby * kT4, n0 = tbx * kT4;
   const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
   const int kbeg = split * g.kt_per * kK4, kend = min(g.K, kbeg + g.kt_per * kK4);
   const int ntiles = kend > kbeg ? (kend - kbeg + kK4 - 1) / kK4 : 0;
@@ -725,6 +751,13 @@ std::atomic<int> g_gemm_variant{[] {
   return e ? std::atoi(e) : 0;
 }()};
 
+// XCD-blocked tile order of the four-wave kernel: 1 (default) on, 0 launch order
+// (XDNA_GEMM_XCD at start-up).
+std::atomic<int> g_gemm_xcd{[] {
+  const char* e = std::getenv("XDNA_GEMM_XCD");
+  return e && std::atoi(e) == 0 ? 0 : 1;
+}()};
+
 template <int MA>
 void launch_b(int mb, dim3 grid, hipStream_t st, const GemmArgs& g) {
   if (mb == kAlongK) gemm_kernel<MA, kAlongK><<<grid, 256, 0, st>>>(g);
@@ -807,6 +840,7 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
     return -1;
   }
   GemmArgs g;
+  g.xcd_group = 0;
   g.a = A;
   g.b = Bm;
   g.c = C;
@@ -888,6 +922,8 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
     }
     const dim3 grid2(unsigned(ceil_div(N, kT2)), unsigned(ceil_div(M, kT2)), unsigned(batch * g.nsplit));
     bool ok;
+    if (use4 && g_gemm_xcd.load() && (int64_t(grid2.x) * grid2.y) % kGemmXcds == 0)
+      g.xcd_group = int(std::min<unsigned>(grid2.y, 8));
     if (use4) {
       if (ma == kAlongK) ok = mb == kAlongK ? launch4<kAlongK, kAlongK>(grid2, st2, g) : launch4<kAlongK, kAlongRow>(grid2, st2, g);
       else ok = mb == kAlongK ? launch4<kAlongRow, kAlongK>(grid2, st2, g) : launch4<kAlongRow, kAlongRow>(grid2, st2, g);
