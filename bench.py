@@ -85,8 +85,7 @@ def style_models(torch, nn):
     # VGG19 conv stack through relu4_1 (random init, frozen)
     cfg = [(3, 64), (64, 64), "M", (64, 128), (128, 128), "M", (128, 256), (256, 256),
            (256, 256), (256, 256), "M", (256, 512)]
-    names = ["relu1_1", "relu1_2", "pool1", "relu2_1", "relu2_2", "pool2", "relu3_1",
-             "relu3_2", "relu3_3", "relu3_4", "pool3", "relu4_1"]
+    names = STYLE_LAYER_NAMES
 
     class VGGFeatures(nn.Module):
         def __init__(self):
@@ -109,6 +108,8 @@ def style_models(torch, nn):
     return Generator, VGGFeatures
 
 
+STYLE_LAYER_NAMES = ("relu1_1", "relu1_2", "pool1", "relu2_1", "relu2_2", "pool2", "relu3_1", "relu3_2", "relu3_3",
+                     "relu3_4", "pool3", "relu4_1")
 STYLE_TAPS = ("relu1_1", "relu2_1", "relu3_1", "relu4_1")
 CONTENT_TAP = "relu2_2"
 
@@ -119,10 +120,12 @@ def gram(f):
     return (x @ x.transpose(1, 2)).float() / float(c * h * w)
 
 
-def build_style(torch, device, batch=40, size=36, fused=True):
+def build_style(torch, device, batch=40, size=36, fused=True, region=False):
     """BASELINE config 4's training step on `device`; returns (step, generator).  fused:
     Adam's fused kernel (what an xdna model runs, and the reference's pre-hook picks),
-    or None for the optimizer's default (single-tensor on the CPU)."""
+    or None for the optimizer's default (single-tensor on the CPU).  region: the loss
+    through xdna_train.regions.frozen_feature_loss (the frozen VGG, its content and Gram
+    style terms as one fused region; opt-in, like the reference's regions)."""
     nn = torch.nn
     Generator, VGG = style_models(torch, nn)
     torch.manual_seed(0)
@@ -143,6 +146,25 @@ def build_style(torch, device, batch=40, size=36, fused=True):
         style_grams = {k: gram(v) for k, v in sf.items()}
     # capturable: the step may be captured in a graph (same fused Adam kernel either way)
     opt = torch.optim.Adam(gen.parameters(), lr=1e-3, fused=fused, capturable=device.type != "cpu")
+
+    if region:
+        from xdna_train import regions
+        flat, tap_index = [], {}
+        for name, layer in zip(STYLE_LAYER_NAMES, vgg.layers):
+            flat += list(layer) if isinstance(layer, torch.nn.Sequential) else [layer]
+            tap_index[name] = len(flat) - 1
+        chain = regions.FrozenFeatureChain.from_sequential(flat, [tap_index[k] for k in STYLE_TAPS + (CONTENT_TAP,)])
+        style = {tap_index[k]: (style_grams[k], 1e5) for k in STYLE_TAPS}
+        content_tap = (tap_index[CONTENT_TAP],)
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            loss = regions.frozen_feature_loss(chain, gen(content), content, mse_taps=content_tap, style=style)
+            loss.backward()
+            opt.step()
+            return loss
+
+        return step, gen
 
     def step():
         opt.zero_grad(set_to_none=True)
@@ -657,6 +679,32 @@ def main() -> int:
         log(f"style net (graph): {it_s:.1f} it/s, loss {loss_g:.4f}")
         graph.reset()
 
+        # the same step with the loss as one fused frozen-feature region (opt-in, as the
+        # reference's "XDNA + fused loss region" figure)
+        rstep, _ = build_style(torch, X, region=True)
+        for _ in range(3):
+            rstep()
+        sync(torch)
+        rgraph = xdna_train.Graph()
+        with xdna_train.graph(rgraph):
+            rloss = rstep()
+        for _ in range(2):
+            rgraph.replay()
+        sync(torch)
+        t0 = time.perf_counter()
+        for _ in range(args.style_steps):
+            rgraph.replay()
+        r_loss = float(rloss.item())
+        r_it_s = args.style_steps / (time.perf_counter() - t0)
+        rgraph.reset()
+        result["style_net"]["region_it_s"] = round(r_it_s, 2)
+        result["style_net"]["region_ms_per_step"] = round(1e3 / r_it_s, 3)
+        result["style_net"]["region_loss"] = r_loss
+        result["style_net"]["region"] = ("loss via xdna_train.regions.frozen_feature_loss (frozen VGG conv+ReLU "
+                                         "epilogues, device-side tap terms, fused backward), HIP graph replay")
+        log(f"style net (region, graph): {r_it_s:.1f} it/s, loss {r_loss:.4f}")
+        del rstep
+
         def style_gpu_it_s():
             g2 = xdna_train.Graph()
             with xdna_train.graph(g2):
@@ -719,6 +767,8 @@ def main() -> int:
                 "gpu_it_s_abba_rounds": [round(v, 2) for v in gd_runs],
                 "speedup_vs_cpu": round(result["style_net"]["it_s"] / c_d, 1),
                 "speedup_vs_cpu_fused_adam": round(result["style_net"]["it_s"] / c_f, 1)})
+            if "region_it_s" in result["style_net"]:
+                result["style_net"]["region_speedup_vs_cpu"] = round(result["style_net"]["region_it_s"] / c_d, 1)
             log(f"style net CPU: {c_d:.2f} it/s (default Adam), {c_f:.2f} it/s (fused Adam)")
         if "resnet18" in result:
             c_r, g_r, cr_runs, gr_runs = abba(

@@ -532,6 +532,60 @@ int xdna_upsample_nearest2x_bwd_bf16(const uint16_t* dy, uint16_t* dx, int64_t p
 int xdna_subsample2_bf16(const uint16_t* full, uint16_t* y, int64_t planes, int H, int W, void* stream);
 int xdna_dilate2_bf16(const uint16_t* dy, uint16_t* full, int64_t planes, int H, int W, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Fused training regions: the frozen-feature (perceptual) loss of          */
+/* xdna_train/regions.py:1-425 with its host kernels                        */
+/* (_native/region_kernels.cpp:51-340) on device memory.  bf16 storage,     */
+/* fp32 arithmetic, one rounding per output.  `go` is the loss gradient     */
+/* autograd hands in, read on the device: go_dtype 0 none (1), 1 fp32 *,    */
+/* 2 bf16 *.                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* xdna_conv3x3_layout_rows_bf16 with an activation in the epilogue, applied to the fp32
+ * sum before its rounding: act 0 none, 1 ReLU (PyTorch's: NaN kept, -0 to +0; the result
+ * equals relu of the unfused conv output bit for bit).  Replaces the reference region's
+ * conv followed by region_relu (regions.py:203-236, region_kernels.cpp:74-92). */
+int xdna_conv3x3_layout_rows_act_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                      int B, int cin, int cout, int H, int W, int layout, int act, void* stream);
+
+/* 2x2 / stride-2 max-pool of `planes` H x W bf16 planes into floor(H/2) x floor(W/2):
+ * PyTorch's rule (the first maximum in row-major window order; a NaN replaces any value).
+ * Replaces the pooling half of xdna_region_relu_maxpool2_bf16 (region_kernels.cpp:
+ * 149-185), whose ReLU is in the conv epilogue here. */
+int xdna_region_maxpool2_bf16(const uint16_t* x, uint16_t* y, int64_t planes, int H, int W, void* stream);
+
+/* Backward of ReLU, max-pool and tap terms in one pass over `planes` H x W planes:
+ *   out = (r && r <= 0) ? 0 : bf16(base + extra + scale * go * (ta - tb))
+ * base = g, or gp (the gradient of the pooled floor(H/2) x floor(W/2) planes) routed to each
+ * window's maximum of px (the pool input; the forward's rule), 0 elsewhere; r, g, gp,
+ * extra and ta/tb may each be NULL (g and gp not both).  Replaces region_relu_bwd,
+ * region_addtap and region_maxpool2_bwd (region_kernels.cpp:187-340). */
+int xdna_region_backward_bf16(const uint16_t* r, const uint16_t* g, const uint16_t* gp, const uint16_t* px,
+                              const uint16_t* extra, const uint16_t* ta, const uint16_t* tb, float scale,
+                              const void* go, int go_dtype, uint16_t* out, int64_t planes, int H, int W,
+                              void* stream);
+
+/* Partial sums per loss term: each call writes xdna_region_loss_parts() floats,
+ * scale * (sums of the squared differences over a fixed partition of the elements);
+ * xdna_region_loss_finish adds n partials in a fixed order (fp64) into the loss, as an fp32
+ * and/or bf16 scalar.  sqdiff: d = a - b (bf16).  gram_sqdiff: d = G / chw - t for bf16
+ * Gram matrices G [batch][cc] and fp32 targets t (batch stride t_bstride, 0 to broadcast
+ * one).  Replace region_sqdiff_sum (region_kernels.cpp:51-72) without its host
+ * round trip. */
+int xdna_region_loss_parts(void);
+int xdna_region_sqdiff_bf16(const uint16_t* a, const uint16_t* b, int64_t n, float scale, float* part,
+                            void* stream);
+int xdna_region_gram_sqdiff_bf16(const uint16_t* G, const float* t, int64_t t_bstride, int64_t batch, int64_t cc,
+                                 float chw, float scale, float* part, void* stream);
+int xdna_region_loss_finish(const float* part, int n, float* out_f32, uint16_t* out_bf16, void* stream);
+
+/* S = bf16(coef * go * (d + d^T) / chw), d = G / chw - t, for batch C x C Gram matrices
+ * G = F F^T: the gradient of coef / 2 * sum d^2 with respect to the features F is S F
+ * (coef = 2 w / N for w times a mean over N elements).  No reference counterpart (the
+ * reference's region has feature taps only). */
+int xdna_region_gram_grad_bf16(const uint16_t* G, const float* t, int64_t t_bstride, int64_t batch, int C,
+                               float chw, float coef, const void* go, int go_dtype, uint16_t* S, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

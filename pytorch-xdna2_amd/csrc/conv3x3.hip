@@ -90,7 +90,13 @@ struct RowsArgs {
   int B;                 // images
   int out_rs;            // 1: stores through a buffer resource (every tile's span < 2^30 bytes)
   int bias_vec;          // 1: bias 8-byte aligned and cout % 4 == 0 (4-channel vector loads)
+  int act;               // epilogue activation: 0 none, 1 ReLU
 };
+
+// The epilogue's activation, applied to the fp32 sum before its one rounding.  ReLU keeps
+// NaN and maps -0 to +0 (PyTorch's relu); rounding is monotonic and keeps the sign, so
+// bf16(relu(v)) equals relu(bf16(v)) bit for bit: the fused result is the unfused one.
+__device__ inline float rows_act(const RowsArgs& a, float v) { return a.act && v <= 0.0f ? 0.0f : v; }
 
 // Branch-free NCHW epilogue.  The resource starts at the first image a tile touches; a
 // store whose pixel or channel lies outside the output gets an offset of kOutSkip or more,
@@ -329,7 +335,7 @@ void conv_rows_kernel(RowsArgs a) {
       if (co >= a.cout) continue;
 #pragma unroll
       for (int n = 0; n < NT; ++n)
-        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[m][n][i]));
     }
 }
 
@@ -494,7 +500,7 @@ void conv_rows2_kernel(RowsArgs a) {
       if (co >= a.cout) continue;
 #pragma unroll
       for (int n = 0; n < 4; ++n)
-        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[m][n][i]));
     }
 }
 
@@ -729,7 +735,7 @@ void conv_rows4_kernel(RowsArgs a) {
         const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
         for (int n = 0; n < NT; ++n)
-          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(acc[m][n][i]), om.rs, poff[n] + coff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act(a, acc[m][n][i])), om.rs, poff[n] + coff, 0, 0);
       }
     return;
   }
@@ -760,7 +766,7 @@ void conv_rows4_kernel(RowsArgs a) {
       if (co >= a.cout) continue;
 #pragma unroll
       for (int n = 0; n < NT; ++n)
-        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[m][n][i]);
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[m][n][i]));
     }
 }
 
@@ -919,7 +925,7 @@ void conv_small_kernel(RowsArgs a) {
       const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
       for (int n = 0; n < NT; ++n)
-        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(acc[n][i]), om.rs, poff[n] + coff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act(a, acc[n][i])), om.rs, poff[n] + coff, 0, 0);
     }
     return;
   }
@@ -948,7 +954,7 @@ void conv_small_kernel(RowsArgs a) {
     if (co >= a.cout) continue;
 #pragma unroll
     for (int n = 0; n < NT; ++n)
-      if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(acc[n][i]);
+      if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[n][i]));
   }
 }
 
@@ -968,7 +974,7 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(RowsArgs a, int nsplit
   const float* pp = a.part + int64_t(co) * a.m_pad + p;
   const int64_t zstride = int64_t(a.cout) * a.m_pad;
   for (int z = 0; z < nsplit; ++z) v += pp[z * zstride];
-  a.out[int64_t(plane) * a.H * a.W + pix] = f32_to_bf16(v);
+  a.out[int64_t(plane) * a.H * a.W + pix] = f32_to_bf16(rows_act(a, v));
 }
 
 // ---------------------------------------------------------------------------------
@@ -1600,9 +1606,10 @@ std::atomic<int> g_rows_variant{[] {
 }()};
 
 int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
-                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef) {
+                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef, int act = 0) {
   const ConvGeom geom = conv_geom(B, H, W, layout);
   RowsArgs a;
+  a.act = act;
   a.xp = xp;
   a.wt = wt;
   a.bias = bias;
@@ -2361,6 +2368,16 @@ int xdna_conv3x3_layout_rows_bf16(const uint16_t* xp, const uint16_t* wt, const 
     return -1;
   }
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout);
+}
+
+int xdna_conv3x3_layout_rows_act_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                      int B, int cin, int cout, int H, int W, int layout, int act, void* stream) {
+  if (!shape_ok("xdna_conv3x3_layout_rows_act_bf16", B, cin, cout, H, W)) return -1;
+  if ((layout != kLayoutRef && layout != kLayoutTight) || act < 0 || act > 1) {
+    set_error("xdna_conv3x3_layout_rows_act_bf16: unknown layout or activation");
+    return -1;
+  }
+  return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout, act);
 }
 
 int xdna_conv3x3_set_wgrad_rows_kt(int kt_rows) {

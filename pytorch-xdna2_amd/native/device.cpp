@@ -746,4 +746,24 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     check_abi(xdna_hip_inject_failure(n, poison ? 1 : 0), "inject_failure");
   });
   mod.def("reset_failure_state", [] { xdna_hip_reset_failure_state(); });
+  // fused training regions (xdna_train/regions.py)
+  mod.def("region_conv3x3", &region_conv3x3);
+  mod.def("region_bmm", &region_bmm);
+  mod.def("region_maxpool2", &region_maxpool2);
+  mod.def("region_backward", [](std::optional<at::Tensor> r, std::optional<at::Tensor> g,
+                                std::optional<at::Tensor> gp, std::optional<at::Tensor> px,
+                                std::optional<at::Tensor> extra, std::optional<at::Tensor> ta,
+                                std::optional<at::Tensor> tb, double scale, std::optional<at::Tensor> go,
+                                std::vector<int64_t> shape) {
+    return region_backward(r, g, gp, px, extra, ta, tb, scale, go, shape);
+  });
+  mod.def("region_loss_parts", &region_loss_parts);
+  mod.def("region_sqdiff", [](const at::Tensor& a, const at::Tensor& b, double scale, at::Tensor part,
+                              int64_t offset) { region_sqdiff(a, b, scale, part, offset); });
+  mod.def("region_gram_sqdiff", [](const at::Tensor& G, const at::Tensor& t, double chw, double scale,
+                                   at::Tensor part, int64_t offset) {
+    region_gram_sqdiff(G, t, chw, scale, part, offset);
+  });
+  mod.def("region_loss_finish", &region_loss_finish);
+  mod.def("region_gram_grad", &region_gram_grad);
 }

@@ -226,7 +226,7 @@ at::Tensor pack_rows(const at::Tensor& src, int layout) {
 // Runs the conv of a packed input (NCHW shape `src`, cin channels) with `w` (forward: w as
 // given; dgrad: flip+swap) into a new NCHW tensor of cout channels.
 at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef src, const at::Tensor& w,
-                           const at::Tensor* bias, bool dgrad) {
+                           const at::Tensor* bias, bool dgrad, int act = 0) {
   const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor wc = w.contiguous();
@@ -264,11 +264,11 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
   if (bias) bc = bias->contiguous();
   const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
   KernelTimer kt(dgrad ? "conv3x3_rows.dgrad" : "conv3x3_rows.fwd", flops);
-  check_abi(xdna_conv3x3_layout_rows_bf16(static_cast<const uint16_t*>(packed.const_data_ptr()),
-                                          static_cast<const uint16_t*>(wt.const_data_ptr()),
-                                          bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
-                                          static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout),
-                                          int(H), int(W), layout, st),
+  check_abi(xdna_conv3x3_layout_rows_act_bf16(static_cast<const uint16_t*>(packed.const_data_ptr()),
+                                              static_cast<const uint16_t*>(wt.const_data_ptr()),
+                                              bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                                              static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout),
+                                              int(H), int(W), layout, act, st),
             "conv rows");
   return out;
 }
@@ -1578,6 +1578,43 @@ void register_hot_ops(torch::Library& m) {
   m.impl("native_batch_norm_backward", TORCH_FN(native_batch_norm_backward_xdna));
   m.impl("upsample_nearest2d", TORCH_FN(upsample_nearest2d_xdna));
   m.impl("upsample_nearest2d_backward", TORCH_FN(upsample_nearest2d_backward_xdna));
+}
+
+// ---------------------------------------------------------------------------------------
+// Convolution and product pieces of the fused regions (regions.cpp, xdna_train/regions.py)
+// ---------------------------------------------------------------------------------------
+
+// y = act(conv3x3(x, w) + b) for a 3x3 / stride-1 / pad-1 bf16 conv on the rows kernels,
+// the activation applied in the epilogue before the one rounding (act 0 none, 1 ReLU).
+// The weight's prepared form is cached as for any conv.
+at::Tensor region_conv3x3(const at::Tensor& x, const at::Tensor& w, const std::optional<at::Tensor>& b, int act) {
+  TORCH_CHECK(x.dim() == 4 && w.dim() == 4 && w.size(2) == 3 && w.size(3) == 3 && x.size(1) == w.size(1),
+              "region conv: expected a 3x3 conv of matching channels");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16 && w.scalar_type() == at::kBFloat16 &&
+                  x.device().type() == kXdna && w.device().type() == kXdna,
+              "region conv: bf16 xdna tensors expected");
+  TORCH_CHECK(act == 0 || act == 1, "region conv: activation must be 0 (none) or 1 (ReLU)");
+  const bool has_b = b.has_value() && b->defined();
+  if (has_b)
+    TORCH_CHECK(b->scalar_type() == at::kBFloat16 && b->dim() == 1 && b->size(0) == w.size(0) &&
+                    b->device().type() == kXdna,
+                "region conv: bias must be a bf16 xdna vector of the output channels");
+  ScopedCount sc(act ? "hip_region.conv_relu.run" : "hip_region.conv.run");
+  const int layout = g_conv_layout.load();
+  return hip_conv_packed(pack_rows(x, layout), layout, x.sizes(), w, has_b ? &*b : nullptr, false, act);
+}
+
+// c[i] = alpha * a[i] . b[i] for batched bf16 operands of any strides (the region's Gram
+// products and their gradients).
+at::Tensor region_bmm(const at::Tensor& a, const at::Tensor& b, double alpha) {
+  TORCH_CHECK(a.dim() == 3 && b.dim() == 3 && a.size(0) == b.size(0) && a.size(2) == b.size(1),
+              "region bmm: shape mismatch");
+  TORCH_CHECK(gemm_dtype_ok({&a, &b}) && fits_int(a) && fits_int(b) && a.size(0) <= 65535,
+              "region bmm: bf16 xdna operands expected");
+  ScopedCount sc("hip_region.bmm.run");
+  at::Tensor c = empty_xdna({a.size(0), a.size(1), b.size(2)}, at::kBFloat16);
+  run_gemm(a, b, c, nullptr, float(alpha), 0.0f);
+  return c;
 }
 
 }  // namespace xdna_backend

@@ -11,6 +11,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <optional>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -92,6 +93,25 @@ void clear_packed_inputs();
 
 // Weight-gradient launches so far (ops.cpp).
 int64_t dw_jobs();
+
+// Pieces of the fused training regions (ops.cpp): a 3x3 conv with its activation in the
+// epilogue (act 0 none, 1 ReLU) and a batched product scaled by alpha.
+at::Tensor region_conv3x3(const at::Tensor& x, const at::Tensor& w, const std::optional<at::Tensor>& b, int act);
+at::Tensor region_bmm(const at::Tensor& a, const at::Tensor& b, double alpha);
+// Region kernels on tensors (regions.cpp).
+at::Tensor region_maxpool2(const at::Tensor& x);
+at::Tensor region_backward(const std::optional<at::Tensor>& r, const std::optional<at::Tensor>& g,
+                           const std::optional<at::Tensor>& gp, const std::optional<at::Tensor>& px,
+                           const std::optional<at::Tensor>& extra, const std::optional<at::Tensor>& ta,
+                           const std::optional<at::Tensor>& tb, double scale, const std::optional<at::Tensor>& go,
+                           at::IntArrayRef shape);
+int64_t region_loss_parts();
+void region_sqdiff(const at::Tensor& a, const at::Tensor& b, double scale, at::Tensor& part, int64_t offset);
+void region_gram_sqdiff(const at::Tensor& G, const at::Tensor& t, double chw, double scale, at::Tensor& part,
+                        int64_t offset);
+std::tuple<at::Tensor, at::Tensor> region_loss_finish(const at::Tensor& part);
+at::Tensor region_gram_grad(const at::Tensor& G, const at::Tensor& t, double chw, double coef,
+                            const std::optional<at::Tensor>& go);
 
 // Live kernel timing: HIP events around hot-kernel launches on the launch stream,
 // with the algorithmic work (FLOP or bytes) of each launch.

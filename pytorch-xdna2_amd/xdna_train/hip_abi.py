@@ -106,6 +106,14 @@ SIGNATURES = {
     "xdna_conv3x3_layout_packed_bytes": (Z, [I, I, I, I, I]),
     "xdna_conv3x3_layout_pack_bf16": (I, [P, P, I, I, I, I, I, P]),
     "xdna_conv3x3_layout_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, I, P]),
+    "xdna_conv3x3_layout_rows_act_bf16": (I, [P, P, P, P, I, I, I, I, I, I, I, P]),
+    "xdna_region_maxpool2_bf16": (I, [P, P, L, I, I, P]),
+    "xdna_region_backward_bf16": (I, [P, P, P, P, P, P, P, F, P, I, P, L, I, I, P]),
+    "xdna_region_loss_parts": (I, []),
+    "xdna_region_sqdiff_bf16": (I, [P, P, L, F, P, P]),
+    "xdna_region_gram_sqdiff_bf16": (I, [P, P, L, L, L, F, F, P, P]),
+    "xdna_region_loss_finish": (I, [P, I, P, P, P]),
+    "xdna_region_gram_grad_bf16": (I, [P, P, L, L, I, F, F, P, I, P, P]),
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_gemm_set_variant": (I, [I]),

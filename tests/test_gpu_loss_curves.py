@@ -115,6 +115,17 @@ def test_c4_style_200_steps():
             "hip_adam.run"), strict_windows=1)
 
 
+@pytest.mark.timeout(400)
+def test_c4_style_with_fused_loss_region_200_steps():
+    """Config 4 with its loss through xdna_train.regions.frozen_feature_loss on xdna; on the
+    CPU the region declines and the same loss runs as eager ops, so the reference curve is
+    the plain CPU bf16 run."""
+    build = lambda torch, device, fused: bench.build_style(torch, device, fused=fused, region=True)
+    _check("C4 region", build, 200,
+           ("hip_region.conv_relu.run", "hip_region.gram_sqdiff.run", "hip_region.gram_grad.run",
+            "hip_region.backward.run", "hip_conv3x3.dw_rows.run", "hip_adam.run"), strict_windows=1)
+
+
 @pytest.mark.timeout(900)
 def test_c3_mlp_40_steps():
     _check("C3", bench.build_mlp, 40, ("hip_gemm.addmm.run", "hip_gemm.mm.run", "hip_adam.run"),

@@ -1,0 +1,92 @@
+"""The region module's host logic without a GPU: which layer chains a frozen-feature
+region accepts (plain Conv2d / ReLU / MaxPool2d(2, 2), frozen weights, a conv first; the
+reference's rules, regions.py:137-195), which convs fuse their ReLU, and the switch."""
+import torch
+import torch.nn as nn
+
+from xdna_train import regions
+
+
+def vgg_block():
+    return [nn.Conv2d(3, 8, 3, padding=1), nn.ReLU(), nn.Conv2d(8, 8, 3, padding=1), nn.ReLU(),
+            nn.MaxPool2d(2), nn.Conv2d(8, 16, 3, padding=1), nn.ReLU()]
+
+
+def frozen(layers):
+    for m in layers:
+        for p in m.parameters():
+            p.requires_grad_(False)
+    return layers
+
+
+def test_chain_parses_and_fuses_relus():
+    layers = frozen(vgg_block())
+    chain = regions.FrozenFeatureChain.from_sequential(layers, [3, 6])
+    assert chain is not None and chain.taps == (3, 6)
+    kinds = [op.kind for op in chain.ops]
+    assert kinds == ["conv", "relu", "conv", "relu", "maxpool2", "conv", "relu"]
+    assert [op.fused_relu for op in chain.ops] == [True, False, True, False, False, True, False]
+    assert chain.current()
+
+
+def test_tapped_conv_output_is_not_fused():
+    chain = regions.FrozenFeatureChain.from_sequential(frozen(vgg_block()), [2, 3])
+    assert [op.fused_relu for op in chain.ops[:4]] == [True, False, False, False]
+
+
+def test_rejected_chains():
+    assert regions.FrozenFeatureChain.from_sequential(vgg_block(), [3]) is None  # trainable weights
+    layers = frozen(vgg_block())
+    layers[1] = nn.LeakyReLU()
+    assert regions.FrozenFeatureChain.from_sequential(layers, [3]) is None
+    layers = frozen(vgg_block())
+    layers[4] = nn.MaxPool2d(3)
+    assert regions.FrozenFeatureChain.from_sequential(layers, [6]) is None
+    layers = frozen(vgg_block())
+    assert regions.FrozenFeatureChain.from_sequential(layers[1:], [2]) is None  # first layer not a conv
+    assert regions.FrozenFeatureChain.from_sequential(frozen(vgg_block()), []) is None
+    assert regions.FrozenFeatureChain.from_sequential(frozen(vgg_block()), [7]) is None
+    layers = frozen(vgg_block())
+    layers[2].register_forward_hook(lambda *a: None)
+    assert regions.FrozenFeatureChain.from_sequential(layers, [3]) is None
+
+
+def test_model_surgery_makes_the_chain_stale():
+    layers = frozen(vgg_block())
+    chain = regions.FrozenFeatureChain.from_sequential(layers, [3])
+    layers[2].stride = (2, 2)
+    assert not chain.current()
+
+
+def test_cpu_tensors_are_not_eligible_and_switch(monkeypatch):
+    chain = regions.FrozenFeatureChain.from_sequential(frozen(vgg_block()), [3])
+    x = torch.rand(1, 3, 8, 8).bfloat16().requires_grad_()
+    assert not chain.eligible(x, torch.rand(1, 3, 8, 8).bfloat16())
+    monkeypatch.setenv("XDNA_REGIONS", "0")
+    assert not regions.enabled()
+
+
+def test_eager_paths_on_cpu_match_the_definition():
+    """Ineligible inputs (CPU tensors) take the eager ops: the MSE over concatenated taps
+    and the Gram style terms, as written out here."""
+    torch.manual_seed(0)
+    layers = frozen(vgg_block())
+    chain = regions.FrozenFeatureChain.from_sequential(layers, [3, 6])
+    x = torch.rand(2, 3, 8, 8, requires_grad=True)
+    t = torch.rand(2, 3, 8, 8)
+    loss = regions.frozen_feature_mse(chain, x, t)
+    f = [x]
+    for m in layers:
+        f.append(m(f[-1]))
+    g = [t]
+    for m in layers:
+        g.append(m(g[-1]))
+    a = torch.cat([f[4].reshape(-1), f[7].reshape(-1)])
+    b = torch.cat([g[4].reshape(-1), g[7].reshape(-1)])
+    assert torch.allclose(loss, ((a - b) ** 2).mean())
+    T = torch.rand(1, 16, 16)
+    loss2 = regions.frozen_feature_loss(chain, x, t, mse_taps=[3], style={6: (T, 3.0)})
+    F3 = f[7].reshape(2, 16, -1)
+    gram = F3 @ F3.transpose(1, 2) / (16 * 4 * 4)
+    ref = ((f[4] - g[4]) ** 2).mean() + 3.0 * ((gram - T) ** 2).mean()
+    assert torch.allclose(loss2, ref, rtol=1e-5)
