@@ -17,6 +17,7 @@
 #include <deque>
 #include <mutex>
 #include <optional>
+#include <unordered_map>
 #include <vector>
 
 namespace xdna_backend {
@@ -131,6 +132,77 @@ void clear_weight_cache() {
 
 void note_graph_replay() { g_replay_generation.fetch_add(1); }
 
+// Prepared forms of frozen weights that a captured graph reads.  A capture that meets a
+// frozen weight (no gradient) whose form the eager cache holds adopts that form instead of
+// recording a preparation: the graph keeps the form (and the weight) alive, and every
+// replay first prepares it again, eagerly and on the replay's stream, if the weight was
+// written since (version or write epoch), so a replay computes with the weight's current
+// value as an eager step would.  Writes the graph itself makes to a frozen weight are not
+// seen (no host code runs); trainable weights are prepared inside the graph.
+namespace {
+struct GraphWeight {
+  at::Tensor weight, wt;
+  bool dgrad = false;
+  int64_t version = 0;
+  uint64_t epoch = 0;
+};
+
+struct GraphWeights {
+  std::mutex mu;
+  std::unordered_map<int64_t, std::vector<GraphWeight>> by_pool;
+};
+
+GraphWeights& graph_weights() {
+  static auto* g = new GraphWeights();
+  return *g;
+}
+
+int64_t weight_version(const at::Tensor& w) {
+  return int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
+}
+
+void adopt_graph_weight(int64_t pool, const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
+  GraphWeight e;
+  e.weight = w;
+  e.wt = wt;
+  e.dgrad = dgrad;
+  e.version = weight_version(w);
+  e.epoch = write_epoch(w);
+  GraphWeights& g = graph_weights();
+  std::lock_guard<std::mutex> lock(g.mu);
+  g.by_pool[pool].push_back(std::move(e));
+}
+}  // namespace
+
+int64_t refresh_graph_weights(int64_t pool) {
+  GraphWeights& g = graph_weights();
+  std::lock_guard<std::mutex> lock(g.mu);
+  auto it = g.by_pool.find(pool);
+  if (it == g.by_pool.end()) return 0;
+  int64_t n = 0;
+  for (GraphWeight& e : it->second) {
+    const int64_t ver = weight_version(e.weight);
+    const uint64_t ep = write_epoch(e.weight);
+    if (ver == e.version && ep == e.epoch) continue;
+    at::Tensor wc = e.weight.contiguous();
+    check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
+                                                static_cast<uint16_t*>(e.wt.data_ptr()), int(wc.size(0)),
+                                                int(wc.size(1)), e.dgrad ? 1 : 0, current_stream()),
+              "graph weight refresh");
+    e.version = ver;
+    e.epoch = ep;
+    ++n;
+  }
+  if (n) count_call("hip_conv3x3.weights_graph_refresh", 0);
+  return n;
+}
+
+void release_graph_weights(int64_t pool) {
+  GraphWeights& g = graph_weights();
+  std::lock_guard<std::mutex> lock(g.mu);
+  g.by_pool.erase(pool);
+}
+
 namespace {
 
 bool weight_cacheable(const at::Tensor& w) { return !w.is_inference() && w.dim() == 4; }
@@ -238,6 +310,16 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
   const bool cacheable = weight_cacheable(w);
   const bool trainable = w.requires_grad() && !w.is_inference();
   at::Tensor wt = cacheable ? cached_weights(w, dgrad, tag) : at::Tensor();
+  if (!wt.defined() && tag > 0 && cacheable && !trainable) {
+    // a capture meeting a frozen weight whose eager form is cached: the graph adopts it
+    // (kept alive by the graph, prepared again by replay when the weight was written)
+    wt = cached_weights(w, dgrad, 0);
+    if (wt.defined()) {
+      adopt_graph_weight(tag, w, dgrad, wt);
+      remember_weights(w, dgrad, wt, tag);
+      count_call("hip_conv3x3.weights_graph", 0);
+    }
+  }
   // prepare / hit counters (the reference's npu_conv3x3w.weights{,_hit})
   count_call(wt.defined() ? "hip_conv3x3.weights_hit" : "hip_conv3x3.weights", 0);
   if (!wt.defined()) {

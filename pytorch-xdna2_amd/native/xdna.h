@@ -90,6 +90,11 @@ void clear_weight_cache();
 void note_graph_replay();
 // Drops the packed conv inputs kept for weight gradients (ops.cpp).
 void clear_packed_inputs();
+// Frozen weights' prepared forms adopted by the captured graph of allocator pool `pool`:
+// prepare again those whose weight was written since (before a replay; returns how many),
+// or forget them (when the graph is released) (ops.cpp).
+int64_t refresh_graph_weights(int64_t pool);
+void release_graph_weights(int64_t pool);
 
 // Weight-gradient launches so far (ops.cpp).
 int64_t dw_jobs();

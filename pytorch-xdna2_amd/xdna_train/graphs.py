@@ -35,6 +35,7 @@ def _release(cuda_graph, pool: int) -> None:
     try:
         cuda_graph.reset()
     finally:
+        _device.native().release_graph_weights(pool)
         _device.native().pool_release(pool)
 
 
@@ -53,10 +54,14 @@ class Graph:
         return self._pool
 
     def replay(self) -> None:
-        """Launches the captured work on the current stream.  The backend's host caches of
-        forms derived from tensors (prepared conv weights, kept packs) stop serving entries
-        made before the replay, whose tensors the graph may have rewritten."""
-        _device.native().note_graph_replay()
+        """Launches the captured work on the current stream.  First, the prepared forms of
+        frozen conv weights the graph adopted are prepared again where the weight was
+        written since.  The backend's host caches of forms derived from tensors (prepared
+        conv weights, kept packs) stop serving entries made before the replay, whose
+        tensors the graph may have rewritten."""
+        ext = _device.native()
+        ext.refresh_graph_weights(self._pool)
+        ext.note_graph_replay()
         self._cuda.replay()
 
     def reset(self) -> None:

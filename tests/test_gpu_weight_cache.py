@@ -203,9 +203,10 @@ def _graph_model(seed):
 
 
 def test_capture_with_frozen_conv_survives_empty_cache_and_sees_updates():
-    """Frozen weights are prepared inside the graph (the graph owns the prepared form):
-    empty_cache between replays cannot free it, and writes to the frozen weight between
-    replays are used by the next replay, exactly as in the eager run."""
+    """A capture adopts the eager prepared form of a frozen weight instead of recording a
+    preparation (the graph keeps it alive): empty_cache between replays cannot free it,
+    and a write to the frozen weight between replays makes the next replay prepare it again
+    first, so every replay matches the eager run exactly."""
     g = torch.Generator().manual_seed(3)
     x_cpu = torch.randn(8, 32, 12, 12, generator=g).bfloat16()
     t_cpu = torch.randn(8, 32, 12, 12, generator=g)
@@ -235,8 +236,11 @@ def test_capture_with_frozen_conv_survives_empty_cache_and_sees_updates():
         for _ in range(2):
             losses.append(float(step()))
         graph = torch.xdna.Graph()
+        xdna_train.reset_mapped_cpu_stats()
         with torch.xdna.graph(graph):
             loss = step()
+        st = xdna_train.mapped_cpu_stats()
+        assert st.get("hip_conv3x3.weights_graph", {}).get("calls", 0) >= 1, st
         for i in range(2, n_steps):
             torch.xdna.empty_cache()  # frees every cached block the eager warm-up left
             junk = [torch.randn(64, 64, 3, 3, device=X).bfloat16() for _ in range(8)]
@@ -247,6 +251,8 @@ def test_capture_with_frozen_conv_survives_empty_cache_and_sees_updates():
             if i == update_after:
                 m[2].weight.data.copy_(w_new.to(X))
         out = [p.detach().cpu() for p in m.parameters()]
+        st = xdna_train.mapped_cpu_stats()
+        assert st.get("hip_conv3x3.weights_graph_refresh", {}).get("calls", 0) == 1, st
         graph.reset()
         return losses, out
 
