@@ -125,7 +125,8 @@ def build_style(torch, device, batch=40, size=36, fused=True, region=False):
     Adam's fused kernel (what an xdna model runs, and the reference's pre-hook picks),
     or None for the optimizer's default (single-tensor on the CPU).  region: the loss
     through xdna_train.regions.frozen_feature_loss (the frozen VGG, its content and Gram
-    style terms as one fused region; opt-in, like the reference's regions)."""
+    style terms as one fused region) and the generator's norm + ReLU pairs fused
+    (regions.fuse_norm_activations); opt-in, like the reference's regions."""
     nn = torch.nn
     Generator, VGG = style_models(torch, nn)
     torch.manual_seed(0)
@@ -149,6 +150,7 @@ def build_style(torch, device, batch=40, size=36, fused=True, region=False):
 
     if region:
         from xdna_train import regions
+        regions.fuse_norm_activations(gen)  # each InstanceNorm2d + ReLU pair as one kernel pair
         flat, tap_index = [], {}
         for name, layer in zip(STYLE_LAYER_NAMES, vgg.layers):
             flat += list(layer) if isinstance(layer, torch.nn.Sequential) else [layer]

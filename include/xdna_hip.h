@@ -484,6 +484,23 @@ int xdna_batch_norm_train_bwd_bf16(const uint16_t* dy, const uint16_t* x, const 
                                    const float* save_mean, const float* save_invstd, uint16_t* dx,
                                    void* dweight, void* dbias, int64_t N, int64_t C, int64_t L, void* stream);
 
+/* The same batch norm with its activation fused: y = bf16(act(norm(x))) with act 1 ReLU
+ * (v <= 0 -> 0) or 2 LeakyReLU (v > 0 ? v : v * slope), applied in fp32 before the one
+ * rounding; act 0 is the plain norm.  The backward takes dy through the activation's
+ * gradient from its output y (y <= 0 -> 0 for ReLU, y > 0 ? dy : dy * slope for LeakyReLU)
+ * before the norm's sums, so no masked gradient is written.  Replaces the reference's
+ * fused BatchNorm2d + ReLU / LeakyReLU region (regions.py:426-461 _BatchNormAct, its CPU
+ * kernels region_kernels.cpp:346-457), with the same NaN rule in the backward (ReLU
+ * passes the gradient where y is NaN, LeakyReLU scales it). */
+int xdna_batch_norm_train_act_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                       void* running_mean, void* running_var, int stat_dtype, double momentum,
+                                       double eps, uint16_t* y, float* save_mean, float* save_invstd, int64_t N,
+                                       int64_t C, int64_t L, int act, float slope, void* stream);
+int xdna_batch_norm_train_act_bwd_bf16(const uint16_t* dy, const uint16_t* x, const uint16_t* y,
+                                       const void* weight, int param_dtype, const float* save_mean,
+                                       const float* save_invstd, uint16_t* dx, void* dweight, void* dbias,
+                                       int64_t N, int64_t C, int64_t L, int act, float slope, void* stream);
+
 /* Batch norm in training mode without running statistics over x[N][C][L] bf16 (the form
  * PyTorch's instance_norm takes: [B, C, H, W] as [1, B*C, H*W]).  Replaces PyTorch's CPU
  * native_batch_norm / native_batch_norm_backward, which the reference reaches through
@@ -512,6 +529,17 @@ int xdna_instance_norm_fwd_bf16(const uint16_t* x, const void* weight, const voi
 int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
                                 const float* save_mean, const float* save_invstd, uint16_t* dx, void* dweight,
                                 void* dbias, int64_t B, int64_t C, int64_t L, void* stream);
+
+/* Instance norm with its activation fused (act and slope as for the batch norm above):
+ * the reference's norm + activation region (regions.py:426-461) widened to InstanceNorm2d,
+ * the norm of its style generator's blocks. */
+int xdna_instance_norm_act_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                    uint16_t* y, float* save_mean, float* save_invstd, int64_t B, int64_t C,
+                                    int64_t L, double eps, int act, float slope, void* stream);
+int xdna_instance_norm_act_bwd_bf16(const uint16_t* dy, const uint16_t* x, const uint16_t* y, const void* weight,
+                                    int param_dtype, const float* save_mean, const float* save_invstd,
+                                    uint16_t* dx, void* dweight, void* dbias, int64_t B, int64_t C, int64_t L,
+                                    int act, float slope, void* stream);
 
 /* Nearest-neighbour upsampling by exactly 2 of `planes` NCHW bf16 planes of H x W (the
  * input size): y[p][oy][ox] = x[p][oy/2][ox/2] into 2H x 2W planes; the backward writes

@@ -135,6 +135,8 @@ struct BnFwdArgs {
   float* save_mean;
   float* save_invstd;
   const float* part;
+  int act;      // activation applied before rounding (act_forward)
+  float slope;
 };
 
 __global__ __launch_bounds__(kBnThreads) void bn_norm_kernel(BnFwdArgs a, BnGeom g) {
@@ -180,18 +182,21 @@ __global__ __launch_bounds__(kBnThreads) void bn_norm_kernel(BnFwdArgs a, BnGeom
         uint32_t w4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          w4[e] = uint32_t(f32_to_bf16(fmaf(f[2 * e], scale, shift))) |
-                  (uint32_t(f32_to_bf16(fmaf(f[2 * e + 1], scale, shift))) << 16);
+          w4[e] = uint32_t(f32_to_bf16(act_forward(a.act, a.slope, fmaf(f[2 * e], scale, shift)))) |
+                  (uint32_t(f32_to_bf16(act_forward(a.act, a.slope, fmaf(f[2 * e + 1], scale, shift)))) << 16);
         *reinterpret_cast<uint4*>(a.y + o) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       },
-      [&](int64_t o) { a.y[o] = f32_to_bf16(fmaf(bf16_to_f32(a.x[o]), scale, shift)); });
+      [&](int64_t o) { a.y[o] = f32_to_bf16(act_forward(a.act, a.slope, fmaf(bf16_to_f32(a.x[o]), scale, shift))); });
 }
 
 // part[(c * S + s) * 2 + {0, 1}] = sum of dy, sum of dy * (x - mean) over range s
+// (with act, dy is first taken through the activation's gradient from its output y)
 __global__ __launch_bounds__(kBnThreads) void bn_bwd_stats_kernel(const uint16_t* __restrict__ dy,
                                                                   const uint16_t* __restrict__ x,
                                                                   const float* __restrict__ mean_in, BnGeom g,
-                                                                  float* __restrict__ part) {
+                                                                  float* __restrict__ part,
+                                                                  const uint16_t* __restrict__ y, int act,
+                                                                  float slope) {
   __shared__ float red[4];
   const int64_t c = blockIdx.x;
   const float mean = mean_in[c];
@@ -202,6 +207,12 @@ __global__ __launch_bounds__(kBnThreads) void bn_bwd_stats_kernel(const uint16_t
         float fd[8], fx[8];
         unpack8(*reinterpret_cast<const uint4*>(dy + o), fd);
         unpack8(*reinterpret_cast<const uint4*>(x + o), fx);
+        if (act) {
+          float fy[8];
+          unpack8(*reinterpret_cast<const uint4*>(y + o), fy);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) fd[e] = act_backward(act, slope, fy[e], fd[e]);
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           s1 += fd[e];
@@ -209,7 +220,8 @@ __global__ __launch_bounds__(kBnThreads) void bn_bwd_stats_kernel(const uint16_t
         }
       },
       [&](int64_t o) {
-        const float d = bf16_to_f32(dy[o]);
+        float d = bf16_to_f32(dy[o]);
+        if (act) d = act_backward(act, slope, bf16_to_f32(y[o]), d);
         s1 += d;
         s2 = fmaf(d, bf16_to_f32(x[o]) - mean, s2);
       });
@@ -232,6 +244,9 @@ struct BnBwdArgs {
   void* dw;
   void* db;
   const float* part;
+  const uint16_t* y;  // the activation's output (act != 0)
+  int act;
+  float slope;
 };
 
 // dx = (dy - sum(dy)/n - (x - mean) * invstd^2 * sum(dy (x - mean))/n) * invstd * w,
@@ -266,6 +281,12 @@ __global__ __launch_bounds__(kBnThreads) void bn_bwd_kernel2(BnBwdArgs a, BnGeom
         float fd[8], fx[8];
         unpack8(*reinterpret_cast<const uint4*>(a.dy + o), fd);
         unpack8(*reinterpret_cast<const uint4*>(a.x + o), fx);
+        if (a.act) {
+          float fy[8];
+          unpack8(*reinterpret_cast<const uint4*>(a.y + o), fy);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) fd[e] = act_backward(a.act, a.slope, fy[e], fd[e]);
+        }
         uint32_t w4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -276,7 +297,9 @@ __global__ __launch_bounds__(kBnThreads) void bn_bwd_kernel2(BnBwdArgs a, BnGeom
         *reinterpret_cast<uint4*>(a.dx + o) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       },
       [&](int64_t o) {
-        const float v = (bf16_to_f32(a.dy[o]) - gmean - (bf16_to_f32(a.x[o]) - mean) * proj) * gscale;
+        float d = bf16_to_f32(a.dy[o]);
+        if (a.act) d = act_backward(a.act, a.slope, bf16_to_f32(a.y[o]), d);
+        const float v = (d - gmean - (bf16_to_f32(a.x[o]) - mean) * proj) * gscale;
         a.dx[o] = f32_to_bf16(v);
       });
 }
@@ -312,14 +335,14 @@ bool bn_args_ok(const char* what, int64_t N, int64_t C, int64_t L, int wd) {
 
 using namespace xdna;
 
-extern "C" int xdna_batch_norm_train_fwd_bf16(const uint16_t* x, const void* weight, const void* bias,
-                                              int param_dtype, void* running_mean, void* running_var,
-                                              int stat_dtype, double momentum, double eps, uint16_t* y,
-                                              float* save_mean, float* save_invstd, int64_t N, int64_t C,
-                                              int64_t L, void* stream) {
+extern "C" int xdna_batch_norm_train_act_fwd_bf16(const uint16_t* x, const void* weight, const void* bias,
+                                                  int param_dtype, void* running_mean, void* running_var,
+                                                  int stat_dtype, double momentum, double eps, uint16_t* y,
+                                                  float* save_mean, float* save_invstd, int64_t N, int64_t C,
+                                                  int64_t L, int act, float slope, void* stream) {
   if (!bn_args_ok("xdna_batch_norm_train_fwd_bf16", N, C, L, param_dtype)) return -1;
   if (!x || !y || !save_mean || !save_invstd || stat_dtype < 0 || stat_dtype > 2 ||
-      ((running_mean || running_var) && stat_dtype == 0)) {
+      ((running_mean || running_var) && stat_dtype == 0) || act < 0 || act > 2) {
     set_error("xdna_batch_norm_train_fwd_bf16: invalid arguments");
     return -1;
   }
@@ -333,23 +356,35 @@ extern "C" int xdna_batch_norm_train_fwd_bf16(const uint16_t* x, const void* wei
   hipStream_t st = as_stream(stream);
   const dim3 grid(unsigned(C), unsigned(g.S));
   bn_stats_kernel<<<grid, kBnThreads, 0, st>>>(x, g, part);
-  BnFwdArgs a{x, weight, bias, param_dtype, running_mean, running_var, stat_dtype,
-              float(momentum), float(eps), y, save_mean, save_invstd, part};
+  BnFwdArgs a{x,     weight,    bias,        param_dtype, running_mean, running_var, stat_dtype,
+              float(momentum), float(eps), y, save_mean, save_invstd, part, act, slope};
   bn_norm_kernel<<<grid, kBnThreads, 0, st>>>(a, g);
   xdna_hip_cache_free(part);  // stream-ordered reuse
   return check_launch("xdna_batch_norm_train_fwd_bf16");
 }
 
-extern "C" int xdna_batch_norm_train_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight,
-                                              int param_dtype, const float* save_mean, const float* save_invstd,
-                                              uint16_t* dx, void* dweight, void* dbias, int64_t N, int64_t C,
+extern "C" int xdna_batch_norm_train_fwd_bf16(const uint16_t* x, const void* weight, const void* bias,
+                                              int param_dtype, void* running_mean, void* running_var,
+                                              int stat_dtype, double momentum, double eps, uint16_t* y,
+                                              float* save_mean, float* save_invstd, int64_t N, int64_t C,
                                               int64_t L, void* stream) {
+  return xdna_batch_norm_train_act_fwd_bf16(x, weight, bias, param_dtype, running_mean, running_var, stat_dtype,
+                                            momentum, eps, y, save_mean, save_invstd, N, C, L, 0, 0.0f, stream);
+}
+
+extern "C" int xdna_batch_norm_train_act_bwd_bf16(const uint16_t* dy, const uint16_t* x, const uint16_t* y,
+                                                  const void* weight, int param_dtype, const float* save_mean,
+                                                  const float* save_invstd, uint16_t* dx, void* dweight,
+                                                  void* dbias, int64_t N, int64_t C, int64_t L, int act, float slope,
+                                                  void* stream) {
   if (!bn_args_ok("xdna_batch_norm_train_bwd_bf16", N, C, L, param_dtype)) return -1;
-  if (!dy || !x || !save_mean || !save_invstd || ((dweight || dbias) && param_dtype == 0)) {
+  if (!dy || !x || !save_mean || !save_invstd || ((dweight || dbias) && param_dtype == 0) || act < 0 || act > 2 ||
+      (act && !y)) {
     set_error("xdna_batch_norm_train_bwd_bf16: invalid arguments");
     return -1;
   }
-  const BnGeom g = bn_geom(N, C, L, aligned16(dy) && aligned16(x) && (!dx || aligned16(dx)));
+  const BnGeom g =
+      bn_geom(N, C, L, aligned16(dy) && aligned16(x) && (!dx || aligned16(dx)) && (!act || aligned16(y)));
   float* part = static_cast<float*>(xdna_hip_cache_alloc(size_t(C) * g.S * 2 * sizeof(float)));
   if (!part) return -1;
   if (!admit_launch("xdna_batch_norm_train_bwd_bf16")) {
@@ -358,9 +393,17 @@ extern "C" int xdna_batch_norm_train_bwd_bf16(const uint16_t* dy, const uint16_t
   }
   hipStream_t st = as_stream(stream);
   const dim3 grid(unsigned(C), unsigned(g.S));
-  bn_bwd_stats_kernel<<<grid, kBnThreads, 0, st>>>(dy, x, save_mean, g, part);
-  BnBwdArgs a{dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, part};
+  bn_bwd_stats_kernel<<<grid, kBnThreads, 0, st>>>(dy, x, save_mean, g, part, y, act, slope);
+  BnBwdArgs a{dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, part, y, act, slope};
   bn_bwd_kernel2<<<grid, kBnThreads, 0, st>>>(a, g);
   xdna_hip_cache_free(part);
   return check_launch("xdna_batch_norm_train_bwd_bf16");
+}
+
+extern "C" int xdna_batch_norm_train_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight,
+                                              int param_dtype, const float* save_mean, const float* save_invstd,
+                                              uint16_t* dx, void* dweight, void* dbias, int64_t N, int64_t C,
+                                              int64_t L, void* stream) {
+  return xdna_batch_norm_train_act_bwd_bf16(dy, x, nullptr, weight, param_dtype, save_mean, save_invstd, dx,
+                                            dweight, dbias, N, C, L, 0, 0.0f, stream);
 }

@@ -114,4 +114,22 @@ __device__ inline uint16_t f32_to_bf16(float f) {
   return f != f ? uint16_t(0x7FC0) : h;
 }
 
+// ---- activations fused into producers (norm outputs, region ops) -------------
+// act 0: none, 1: ReLU (PyTorch's: NaN kept, -0 to +0), 2: LeakyReLU with slope
+// (x > 0 ? x : x * slope).  Applied to the fp32 value before its one rounding.
+__device__ inline float act_forward(int act, float slope, float v) {
+  if (act == 1) return v <= 0.0f ? 0.0f : v;
+  if (act == 2) return v > 0.0f ? v : v * slope;
+  return v;
+}
+
+// The gradient through the activation, from its output y: ReLU masks where y <= 0
+// (threshold_backward on the result: a NaN result passes the gradient), LeakyReLU scales
+// by slope where y <= 0 (leaky_relu_backward on the result).
+__device__ inline float act_backward(int act, float slope, float y, float g) {
+  if (act == 1) return y <= 0.0f ? 0.0f : g;
+  if (act == 2) return y > 0.0f ? g : g * slope;
+  return g;
+}
+
 }  // namespace xdna

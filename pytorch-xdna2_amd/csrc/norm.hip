@@ -46,7 +46,7 @@ __device__ inline void param_put(void* p, int wd, int64_t c, float v) {
 __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const void* __restrict__ b, int wd,
     uint16_t* __restrict__ y, float* __restrict__ save_mean, float* __restrict__ save_invstd,
-    int64_t N, int64_t C, int64_t L, float eps, int64_t pC) {
+    int64_t N, int64_t C, int64_t L, float eps, int64_t pC, int act, float slope) {
   const int lane = threadIdx.x & 63;
   const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
   if (c >= C) return;
@@ -76,7 +76,8 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
   for (int64_t n = 0; n < N; ++n) {
     const uint16_t* xp = x + (n * C + c) * L;
     uint16_t* yp = y + (n * C + c) * L;
-    for (int64_t l = lane; l < L; l += 64) yp[l] = f32_to_bf16(fmaf(bf16_to_f32(xp[l]), scale, shift));
+    for (int64_t l = lane; l < L; l += 64)
+      yp[l] = f32_to_bf16(act_forward(act, slope, fmaf(bf16_to_f32(xp[l]), scale, shift)));
   }
 }
 
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const void* __restrict__ w, int wd,
     const float* __restrict__ mean_in, const float* __restrict__ invstd_in, uint16_t* __restrict__ dx,
     void* __restrict__ dw, void* __restrict__ db, int64_t N, int64_t C, int64_t L, int64_t pC,
-    float* __restrict__ pw, float* __restrict__ pb) {
+    float* __restrict__ pw, float* __restrict__ pb, const uint16_t* __restrict__ yact, int act, float slope) {
   const int lane = threadIdx.x & 63;
   const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
   if (c >= C) return;
@@ -97,7 +98,8 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
   for (int64_t n = 0; n < N; ++n) {
     const int64_t o = (n * C + c) * L;
     for (int64_t l = lane; l < L; l += 64) {
-      const float g = bf16_to_f32(dy[o + l]);
+      const float g = act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), bf16_to_f32(dy[o + l]))
+                          : bf16_to_f32(dy[o + l]);
       sdy += g;
       sdot += g * (bf16_to_f32(x[o + l]) - mean);
     }
@@ -122,7 +124,9 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
     const int64_t o = (n * C + c) * L;
     for (int64_t l = lane; l < L; l += 64) {
       const float xm = bf16_to_f32(x[o + l]) - mean;
-      dx[o + l] = f32_to_bf16((bf16_to_f32(dy[o + l]) - gmean - xm * proj) * gscale);
+      const float g = act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), bf16_to_f32(dy[o + l]))
+                          : bf16_to_f32(dy[o + l]);
+      dx[o + l] = f32_to_bf16((g - gmean - xm * proj) * gscale);
     }
   }
 }
@@ -176,7 +180,7 @@ int xdna_batch_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* 
   }
   if (!admit_launch("batch_norm fwd")) return -1;
   bn_fwd_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
-      x, weight, bias, param_dtype, y, save_mean, save_invstd, N, C, L, float(eps), C);
+      x, weight, bias, param_dtype, y, save_mean, save_invstd, N, C, L, float(eps), C, 0, 0.0f);
   return check_launch("batch_norm fwd");
 }
 
@@ -191,14 +195,19 @@ int xdna_batch_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* 
   }
   if (!admit_launch("batch_norm bwd")) return -1;
   bn_bwd_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
-      dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, N, C, L, C, nullptr, nullptr);
+      dy, x, weight, param_dtype, save_mean, save_invstd, dx, dweight, dbias, N, C, L, C, nullptr, nullptr, nullptr,
+      0, 0.0f);
   return check_launch("batch_norm bwd");
 }
 
-int xdna_instance_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
-                                uint16_t* y, float* save_mean, float* save_invstd, int64_t B, int64_t C,
-                                int64_t L, double eps, void* stream) {
+int xdna_instance_norm_act_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                    uint16_t* y, float* save_mean, float* save_invstd, int64_t B, int64_t C,
+                                    int64_t L, double eps, int act, float slope, void* stream) {
   if (!norm_shape_ok("xdna_instance_norm_fwd_bf16", B, C, L, param_dtype)) return -1;
+  if (act < 0 || act > 2) {
+    set_error("xdna_instance_norm_fwd_bf16: activation must be 0, 1 or 2");
+    return -1;
+  }
   if (B == 0 || C == 0) return 0;
   if (L == 0) {
     set_error("xdna_instance_norm_fwd_bf16: empty reduction");
@@ -211,14 +220,26 @@ int xdna_instance_norm_fwd_bf16(const uint16_t* x, const void* weight, const voi
   }
   if (!admit_launch("instance_norm fwd")) return -1;
   bn_fwd_kernel<<<dim3(unsigned(ceil_div(ch, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
-      x, weight, bias, param_dtype, y, save_mean, save_invstd, 1, ch, L, float(eps), C);
+      x, weight, bias, param_dtype, y, save_mean, save_invstd, 1, ch, L, float(eps), C, act, slope);
   return check_launch("instance_norm fwd");
 }
 
-int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
-                                const float* save_mean, const float* save_invstd, uint16_t* dx, void* dweight,
-                                void* dbias, int64_t B, int64_t C, int64_t L, void* stream) {
+int xdna_instance_norm_fwd_bf16(const uint16_t* x, const void* weight, const void* bias, int param_dtype,
+                                uint16_t* y, float* save_mean, float* save_invstd, int64_t B, int64_t C,
+                                int64_t L, double eps, void* stream) {
+  return xdna_instance_norm_act_fwd_bf16(x, weight, bias, param_dtype, y, save_mean, save_invstd, B, C, L, eps, 0,
+                                         0.0f, stream);
+}
+
+int xdna_instance_norm_act_bwd_bf16(const uint16_t* dy, const uint16_t* x, const uint16_t* y, const void* weight,
+                                    int param_dtype, const float* save_mean, const float* save_invstd,
+                                    uint16_t* dx, void* dweight, void* dbias, int64_t B, int64_t C, int64_t L,
+                                    int act, float slope, void* stream) {
   if (!norm_shape_ok("xdna_instance_norm_bwd_bf16", B, C, L, param_dtype)) return -1;
+  if (act < 0 || act > 2 || (act && !y)) {
+    set_error("xdna_instance_norm_bwd_bf16: activation must be 0, 1 or 2, with its output");
+    return -1;
+  }
   if (B == 0 || C == 0) return 0;
   const bool params = dweight || dbias;
   if (params && (param_dtype == 0 || !dweight || !dbias)) {
@@ -239,7 +260,7 @@ int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const voi
   hipStream_t st = as_stream(stream);
   bn_bwd_kernel<<<dim3(unsigned(ceil_div(ch, kNormWaves))), 64 * kNormWaves, 0, st>>>(
       dy, x, weight, param_dtype, save_mean, save_invstd, dx, nullptr, nullptr, 1, ch, L, C, part,
-      part ? part + ch : nullptr);
+      part ? part + ch : nullptr, y, act, slope);
   if (params) {
     norm_param_reduce_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, st>>>(
         part, part + ch, dweight, dbias, param_dtype, B, C);
@@ -247,6 +268,13 @@ int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const voi
     xdna_hip_cache_free(part);
   }
   return check_launch("instance_norm bwd");
+}
+
+int xdna_instance_norm_bwd_bf16(const uint16_t* dy, const uint16_t* x, const void* weight, int param_dtype,
+                                const float* save_mean, const float* save_invstd, uint16_t* dx, void* dweight,
+                                void* dbias, int64_t B, int64_t C, int64_t L, void* stream) {
+  return xdna_instance_norm_act_bwd_bf16(dy, x, nullptr, weight, param_dtype, save_mean, save_invstd, dx, dweight,
+                                         dbias, B, C, L, 0, 0.0f, stream);
 }
 
 }  // extern "C"

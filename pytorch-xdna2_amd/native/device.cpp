@@ -751,6 +751,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   // fused training regions (xdna_train/regions.py)
   mod.def("region_conv3x3", &region_conv3x3);
   mod.def("region_bmm", &region_bmm);
+  mod.def("region_norm_act_fwd", &region_norm_act_fwd);
+  mod.def("region_norm_act_bwd", &region_norm_act_bwd);
   mod.def("region_maxpool2", &region_maxpool2);
   mod.def("region_backward", [](std::optional<at::Tensor> r, std::optional<at::Tensor> g,
                                 std::optional<at::Tensor> gp, std::optional<at::Tensor> px,

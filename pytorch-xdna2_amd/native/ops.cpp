@@ -70,10 +70,17 @@ bool conv_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef
 // the hot path.  4x the MACs of the strided conv, on kernels several times faster than
 // MIOpen's on these shapes, and within the conv bar where MIOpen is not.  The reference
 // runs them on its CPU through the fallback (torch_xdna_device.cpp:4524-4606, 4608-4885).
+// XDNA_CONV_S2=0 sends 3x3 / stride-2 convs to the general kernels instead (their real
+// MACs on the gather GEMM), for measurements.
+const bool g_conv_s2 = [] {
+  const char* e = std::getenv("XDNA_CONV_S2");
+  return !(e && std::atoi(e) == 0);
+}();
+
 bool conv_s2_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArrayRef stride,
                       c10::SymIntArrayRef padding, c10::SymIntArrayRef dilation, bool transposed,
                       c10::SymIntArrayRef output_padding, const c10::SymInt& groups) {
-  if (g_mode.load() < 1) return false;
+  if (g_mode.load() < 1 || !g_conv_s2) return false;
   if (x.scalar_type() != at::kBFloat16 || w.scalar_type() != at::kBFloat16) return false;
   if (x.dim() != 4 || w.dim() != 4 || w.size(2) != 3 || w.size(3) != 3) return false;
   if (!is_one(stride, 2) || !is_one(padding, 1) || !is_one(dilation, 1) || transposed) return false;
@@ -1697,6 +1704,105 @@ at::Tensor region_bmm(const at::Tensor& a, const at::Tensor& b, double alpha) {
   at::Tensor c = empty_xdna({a.size(0), a.size(1), b.size(2)}, at::kBFloat16);
   run_gemm(a, b, c, nullptr, float(alpha), 0.0f);
   return c;
+}
+
+// Training norm with its activation (act 1 ReLU, 2 LeakyReLU(slope)) applied before the one
+// rounding of the output: batch norm over N*L per channel with the running statistics
+// updated when given (bnorm.hip), or instance norm per (image, channel) plane (norm.hip).
+// Returns y, save_mean, save_invstd.  The reference's fused BatchNorm + activation
+// (region_kernels.cpp:346-457, reached from regions.py:426-461 _BatchNormAct).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> region_norm_act_fwd(
+    const at::Tensor& x, const at::Tensor& weight, const at::Tensor& bias, const std::optional<at::Tensor>& rm,
+    const std::optional<at::Tensor>& rv, double momentum, double eps, int act, double slope, bool instance) {
+  TORCH_CHECK(act == 1 || act == 2, "region norm: activation must be 1 (ReLU) or 2 (LeakyReLU)");
+  TORCH_CHECK(x.dim() >= 3 && x.scalar_type() == at::kBFloat16 && x.device().type() == kXdna &&
+                  x.is_contiguous() && x.numel() > 0,
+              "region norm: a non-empty contiguous bf16 xdna input of at least 3 dims expected");
+  const int64_t N = x.size(0), C = x.size(1), L = x.numel() / (N * C);
+  const int wd = norm_param_dtype(weight, bias);
+  TORCH_CHECK(weight.defined() && bias.defined() && wd > 0 && norm_param_ok(weight, C) && norm_param_ok(bias, C),
+              "region norm: affine bf16 or fp32 xdna parameters of the channel count expected");
+  const int rsd = running_stats_dtype(rm, rv, C);
+  TORCH_CHECK(rsd >= 0 && !(instance && rsd > 0), "region norm: unsupported running statistics");
+  TORCH_CHECK(!instance || L <= kNormMaxPerChannel, "region norm: instance planes above ", kNormMaxPerChannel,
+              " elements are not supported");
+  at::Tensor y = empty_xdna(x.sizes(), at::kBFloat16);
+  const int64_t nstat = instance ? N * C : C;
+  at::Tensor mean = empty_xdna({nstat}, at::kFloat), invstd = empty_xdna({nstat}, at::kFloat);
+  const auto* xp = static_cast<const uint16_t*>(x.const_data_ptr());
+  if (instance) {
+    ScopedCount sc("hip_region.instance_norm_act.run");
+    check_abi(xdna_instance_norm_act_fwd_bf16(xp, weight.const_data_ptr(), bias.const_data_ptr(), wd,
+                                              static_cast<uint16_t*>(y.data_ptr()), mean.data_ptr<float>(),
+                                              invstd.data_ptr<float>(), N, C, L, eps, act, float(slope),
+                                              current_stream()),
+              "instance_norm fwd (activation)");
+  } else {
+    ScopedCount sc("hip_region.batch_norm_act.run");
+    check_abi(xdna_batch_norm_train_act_fwd_bf16(
+                  xp, weight.const_data_ptr(), bias.const_data_ptr(), wd, rsd ? rm->data_ptr() : nullptr,
+                  rsd ? rv->data_ptr() : nullptr, rsd, momentum, eps, static_cast<uint16_t*>(y.data_ptr()),
+                  mean.data_ptr<float>(), invstd.data_ptr<float>(), N, C, L, act, float(slope), current_stream()),
+              "batch_norm fwd (activation)");
+    if (rsd) {
+      bump_write_epoch(*rm);
+      bump_write_epoch(*rv);
+    }
+  }
+  return {y, mean, invstd};
+}
+
+// Backward of region_norm_act_fwd: dy is taken through the activation's gradient (from
+// its output y) inside the norm's two passes.  Returns dx (if need_x) and dweight, dbias
+// (if need_params) in the parameters' dtype.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> region_norm_act_bwd(
+    const at::Tensor& grad, const at::Tensor& x, const at::Tensor& y, const at::Tensor& weight,
+    const at::Tensor& mean, const at::Tensor& invstd, int act, double slope, bool instance, bool need_x,
+    bool need_params) {
+  TORCH_CHECK(act == 1 || act == 2, "region norm: activation must be 1 (ReLU) or 2 (LeakyReLU)");
+  for (const at::Tensor* t : {&x, &y})
+    TORCH_CHECK(t->scalar_type() == at::kBFloat16 && t->device().type() == kXdna && t->is_contiguous() &&
+                    t->dim() >= 3,
+                "region norm: contiguous bf16 xdna input and output expected");
+  TORCH_CHECK(y.sizes() == x.sizes() && grad.sizes() == x.sizes() && grad.device().type() == kXdna,
+              "region norm: gradient, input and output shapes differ");
+  const int64_t N = x.size(0), C = x.size(1), L = x.numel() / (N * C);
+  const int wd = norm_param_dtype(weight, std::nullopt);
+  TORCH_CHECK(wd > 0 && norm_param_ok(weight, C), "region norm: affine parameters expected");
+  const int64_t nstat = instance ? N * C : C;
+  for (const at::Tensor* t : {&mean, &invstd})
+    TORCH_CHECK(t->scalar_type() == at::kFloat && t->numel() == nstat && t->is_contiguous() &&
+                    t->device().type() == kXdna,
+                "region norm: saved statistics of the wrong form");
+  at::Tensor dx, dw, db;
+  if (!need_x && !need_params) return {dx, dw, db};
+  const at::Tensor dy = grad.to(at::kBFloat16).contiguous();
+  if (need_x) dx = empty_xdna(x.sizes(), at::kBFloat16);
+  if (need_params) {
+    const at::ScalarType pt = wd == 2 ? at::kFloat : at::kBFloat16;
+    dw = empty_xdna({C}, pt);
+    db = empty_xdna({C}, pt);
+  }
+  const auto* dyp = static_cast<const uint16_t*>(dy.const_data_ptr());
+  const auto* xp = static_cast<const uint16_t*>(x.const_data_ptr());
+  const auto* yp = static_cast<const uint16_t*>(y.const_data_ptr());
+  uint16_t* dxp = need_x ? static_cast<uint16_t*>(dx.data_ptr()) : nullptr;
+  void* dwp = need_params ? dw.data_ptr() : nullptr;
+  void* dbp = need_params ? db.data_ptr() : nullptr;
+  if (instance) {
+    ScopedCount sc("hip_region.instance_norm_act_bwd.run");
+    check_abi(xdna_instance_norm_act_bwd_bf16(dyp, xp, yp, weight.const_data_ptr(), wd, mean.const_data_ptr<float>(),
+                                              invstd.const_data_ptr<float>(), dxp, dwp, dbp, N, C, L, act,
+                                              float(slope), current_stream()),
+              "instance_norm bwd (activation)");
+  } else {
+    ScopedCount sc("hip_region.batch_norm_act_bwd.run");
+    check_abi(xdna_batch_norm_train_act_bwd_bf16(dyp, xp, yp, weight.const_data_ptr(), wd,
+                                                 mean.const_data_ptr<float>(), invstd.const_data_ptr<float>(), dxp,
+                                                 dwp, dbp, N, C, L, act, float(slope), current_stream()),
+              "batch_norm bwd (activation)");
+  }
+  return {dx, dw, db};
 }
 
 }  // namespace xdna_backend

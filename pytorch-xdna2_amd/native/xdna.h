@@ -103,6 +103,15 @@ int64_t dw_jobs();
 // epilogue (act 0 none, 1 ReLU) and a batched product scaled by alpha.
 at::Tensor region_conv3x3(const at::Tensor& x, const at::Tensor& w, const std::optional<at::Tensor>& b, int act);
 at::Tensor region_bmm(const at::Tensor& a, const at::Tensor& b, double alpha);
+// Training batch / instance norm with a ReLU or LeakyReLU applied before the output's
+// rounding, and its backward through the activation's mask (ops.cpp).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> region_norm_act_fwd(
+    const at::Tensor& x, const at::Tensor& weight, const at::Tensor& bias, const std::optional<at::Tensor>& rm,
+    const std::optional<at::Tensor>& rv, double momentum, double eps, int act, double slope, bool instance);
+std::tuple<at::Tensor, at::Tensor, at::Tensor> region_norm_act_bwd(
+    const at::Tensor& grad, const at::Tensor& x, const at::Tensor& y, const at::Tensor& weight,
+    const at::Tensor& mean, const at::Tensor& invstd, int act, double slope, bool instance, bool need_x,
+    bool need_params);
 // Region kernels on tensors (regions.cpp).
 at::Tensor region_maxpool2(const at::Tensor& x);
 at::Tensor region_backward(const std::optional<at::Tensor>& r, const std::optional<at::Tensor>& g,

@@ -76,6 +76,8 @@ SIGNATURES = {
     "xdna_conv2d_fwd_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),
     "xdna_instance_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, ctypes.c_double, P]),
     "xdna_instance_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
+    "xdna_instance_norm_act_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, I, F, P]),
+    "xdna_instance_norm_act_bwd_bf16": (I, [P, P, P, P, I, P, P, P, P, P, L, L, L, I, F, P]),
     "xdna_upsample_nearest2x_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_set_variant": (I, [I]),
     "xdna_subsample2_bf16": (I, [P, P, L, I, I, P]),
@@ -122,6 +124,8 @@ SIGNATURES = {
     "xdna_batch_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, P]),
     "xdna_batch_norm_train_fwd_bf16": (I, [P, P, P, I, P, P, I, D, D, P, P, P, L, L, L, P]),
     "xdna_batch_norm_train_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
+    "xdna_batch_norm_train_act_fwd_bf16": (I, [P, P, P, I, P, P, I, D, D, P, P, P, L, L, L, I, F, P]),
+    "xdna_batch_norm_train_act_bwd_bf16": (I, [P, P, P, P, I, P, P, P, P, P, L, L, L, I, F, P]),
     "xdna_batch_norm_bwd_bf16": (I, [P, P, P, I, P, P, P, P, P, L, L, L, P]),
     "xdna_foreach_add_scalar_f32": (I, [I, PP, PL, ctypes.c_float, P]),
     "xdna_fused_adam": (I, [I, PP, PP, PP, PP, PP, PP, PL, I, D, D, D, D, D, I, I, I, P, P, P]),

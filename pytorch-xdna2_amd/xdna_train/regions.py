@@ -28,12 +28,16 @@ Regions (``XDNA_REGIONS=0`` turns them off; anything ineligible runs the eager o
   loss, mean over the concatenated tap elements of (features(x) - features(target))^2;
 * :func:`frozen_feature_loss`: the same chain with Gram-matrix style terms as well
   (w * mean((F F^T / chw - T)^2) per style tap, the style-transfer loss of the BASELINE
-  style configuration), an fp32 loss like the eager ``.float()`` losses it replaces.
+  style configuration), an fp32 loss like the eager ``.float()`` losses it replaces;
+* :func:`fuse_norm_activation` / :func:`fuse_norm_activations`: a training BatchNorm2d or
+  InstanceNorm2d and the ReLU / LeakyReLU applied to its output as one kernel pair, the
+  activation in the norm's output store and its mask in the norm's backward sums.
 """
 from __future__ import annotations
 
 import os
 import types
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -433,3 +437,164 @@ def fuse_perceptual_loss(loss_module, features_attr: str = "perceptual_vgg") -> 
     loss_module.__dict__["_xdna_region_cfg"] = {"features_attr": features_attr}
     loss_module.compute_perceptual_loss = types.MethodType(_fused_perceptual, loss_module)
     return True
+
+
+# ---------------------------------------------------------------------------------------
+# A training norm and the activation applied to its output as one pass each way (the
+# reference's fuse_norm_activation, regions.py:426-546), for BatchNorm2d and, beyond the
+# reference, InstanceNorm2d
+# ---------------------------------------------------------------------------------------
+# Smallest input (bytes) that takes the fused op.  On the GPU the fused pair saves a full
+# elementwise pass and its launch each way at every size, so every size is fused unless
+# this is raised (the reference's knob; its CPU kernels only win above ~4 MB).
+_NORM_ACT_MIN_BYTES = int(os.environ.get("XDNA_REGION_NORM_ACT_MIN_BYTES", "0"))
+
+
+class _NormAct(torch.autograd.Function):
+    """y = act(norm(x)) with training statistics on contiguous NCHW bf16, act applied in
+    fp32 before the one rounding of y (ReLU: the same bits as the eager norm then relu;
+    LeakyReLU: within one rounding of them).  Saved for backward: x, y (the activation's
+    mask is read from y), the weight and the fp32 statistics.  Gradients: input, weight and
+    bias, each only if requested.  Not double differentiable."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, running_mean, running_var, momentum, eps, act, slope, instance):
+        y, mean, invstd = _dev.native().region_norm_act_fwd(x, weight, bias, running_mean, running_var,
+                                                            momentum, eps, act, slope, instance)
+        ctx.save_for_backward(x, y, weight, mean, invstd)
+        ctx.act, ctx.slope, ctx.instance = act, slope, instance
+        return y
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        x, y, weight, mean, invstd = ctx.saved_tensors
+        need_x, need_w, need_b = ctx.needs_input_grad[0:3]
+        dx, dw, db = _dev.native().region_norm_act_bwd(dy, x, y, weight, mean, invstd, ctx.act, ctx.slope,
+                                                       ctx.instance, need_x, need_w or need_b)
+        return (dx if need_x else None, dw if need_w else None, db if need_b else None,
+                None, None, None, None, None, None, None)
+
+
+def _act_code(act):
+    """(code, slope) for the kernels, or None: exact types only (a subclass may override
+    forward, which the fused op would skip); a negative slope makes y > 0 no longer the
+    input's sign, so it stays eager."""
+    if type(act) is nn.ReLU:
+        return 1, 0.0
+    if type(act) is nn.LeakyReLU and float(act.negative_slope) >= 0.0:
+        return 2, float(act.negative_slope)
+    return None
+
+
+def _param_ok(t, x, dtypes):
+    return (isinstance(t, torch.Tensor) and t.device == x.device and t.dtype in dtypes and t.is_contiguous()
+            and t.dim() == 1 and t.numel() == x.shape[1])
+
+
+def _norm_act_args(norm, x):
+    """(running_mean, running_var, momentum, instance) when the fused op applies, else None."""
+    if not enabled() or not norm.affine:
+        return None
+    # a forward hook may replace the output, which would then be activated twice
+    if norm._forward_hooks or _modmod._global_forward_hooks:
+        return None
+    if not isinstance(x, torch.Tensor) or x.dim() != 4 or x.device.type != "xdna":
+        return None
+    if x.dtype != torch.bfloat16 or not x.is_contiguous() or x.numel() * 2 < max(_NORM_ACT_MIN_BYTES, 1):
+        return None
+    floats = (torch.bfloat16, torch.float32)
+    w, b = norm.weight, norm.bias
+    if not (_param_ok(w, x, floats) and _param_ok(b, x, floats)) or w.dtype != b.dtype:
+        return None
+    plane = x.shape[2] * x.shape[3]
+    if type(norm) is nn.InstanceNorm2d:
+        # running statistics (used or updated) stay eager; planes of one element are the
+        # eager path's error
+        if norm.track_running_stats or plane <= 1 or plane > 65536:
+            return None
+        return None, None, 0.0, True
+    if not norm.training or x.shape[0] * plane <= 1:
+        return None
+    if not norm.track_running_stats:
+        return None, None, 0.0, False
+    rm, rv = norm.running_mean, norm.running_var
+    if norm.momentum is None or rm is None or rv is None:  # cumulative average: eager
+        return None
+    if not (_param_ok(rm, x, floats) and _param_ok(rv, x, floats)) or rm.dtype != rv.dtype:
+        return None
+    return rm, rv, float(norm.momentum), False
+
+
+def _fused_norm_forward(self, x):
+    """Bound to the norm module (a deepcopy rebinds it to the copy).  The paired activation
+    and its slope are read from ``self`` at call time."""
+    act = self.__dict__.get("_xdna_pair")
+    code = _act_code(act) if act is not None else None
+    args = _norm_act_args(self, x) if code is not None else None
+    if args is None:
+        return type(self).forward(self, x)
+    rm, rv, momentum, instance = args
+    if rm is not None and self.num_batches_tracked is not None:
+        self.num_batches_tracked.add_(1)
+    y = _NormAct.apply(x, self.weight, self.bias, rm, rv, momentum, float(self.eps), code[0], code[1], instance)
+    y._xdna_act_for = weakref.ref(act)
+    return y
+
+
+def _checked_act_forward(self, x):
+    """Passes through, once, a tensor that the paired fused norm already activated, and
+    activates everything else."""
+    ref = getattr(x, "_xdna_act_for", None)
+    if ref is not None and ref() is self:
+        x._xdna_act_for = None  # consumed: a later call on the same tensor activates it
+        return x
+    return type(self).forward(self, x)
+
+
+def fuse_norm_activation(norm: nn.Module, act: nn.Module) -> bool:
+    """Declares that ``act`` (nn.ReLU or nn.LeakyReLU) is applied directly to the output of
+    ``norm`` (nn.BatchNorm2d or nn.InstanceNorm2d) and runs the pair as one fused op each
+    way, like the reference's fuse_norm_activation (regions.py:521-546).
+
+    Both modules keep their parameters, buffers and state_dict keys; only their forwards
+    are replaced, by methods bound to the modules, so a deepcopy of a model with the pair
+    gives a working pair (copy the two together: the pairing is stored on the norm).  When
+    the fused op applies (affine; BatchNorm2d in training mode with tracked statistics and
+    a float momentum, or none tracked; InstanceNorm2d without running statistics; bf16
+    contiguous NCHW on xdna), ``norm(x)`` returns the activated tensor and the next call of
+    ``act`` on exactly that tensor passes it through once; anything else runs both modules
+    unchanged.  The activation's slope is read on every call.
+
+    The pairing is the caller's statement about the model's dataflow: if the activation is
+    not applied to the norm's output directly (an add or a branch in between), do not
+    declare the pair.  Returns True if installed (or already installed with ``act``)."""
+    if not enabled() or type(norm) not in (nn.BatchNorm2d, nn.InstanceNorm2d):
+        return False
+    if type(act) not in (nn.ReLU, nn.LeakyReLU):
+        return False
+    if norm.__dict__.get("_xdna_pair") is not None:
+        return norm.__dict__["_xdna_pair"] is act
+    object.__setattr__(norm, "_xdna_pair", act)  # a plain attribute, not a submodule
+    norm.forward = types.MethodType(_fused_norm_forward, norm)
+    if not isinstance(act.forward, types.MethodType) or act.forward.__func__ is not _checked_act_forward:
+        act.forward = types.MethodType(_checked_act_forward, act)
+    return True
+
+
+def fuse_norm_activations(model: nn.Module) -> int:
+    """Pairs, in every nn.Sequential of ``model`` (or subclass that keeps its forward), each
+    BatchNorm2d / InstanceNorm2d that is immediately followed by a ReLU / LeakyReLU (such a
+    container feeds each module's output straight to the next, so the dataflow statement
+    holds).  Returns the pairs installed."""
+    n = 0
+    for m in model.modules():
+        if not isinstance(m, nn.Sequential) or type(m).forward is not nn.Sequential.forward:
+            continue
+        if "forward" in m.__dict__ or m._forward_hooks:
+            continue
+        mods = list(m)
+        for a, b in zip(mods, mods[1:]):
+            if type(a) in (nn.BatchNorm2d, nn.InstanceNorm2d) and type(b) in (nn.ReLU, nn.LeakyReLU):
+                n += bool(fuse_norm_activation(a, b))
+    return n

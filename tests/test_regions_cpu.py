@@ -90,3 +90,35 @@ def test_eager_paths_on_cpu_match_the_definition():
     gram = F3 @ F3.transpose(1, 2) / (16 * 4 * 4)
     ref = ((f[4] - g[4]) ** 2).mean() + 3.0 * ((gram - T) ** 2).mean()
     assert torch.allclose(loss2, ref, rtol=1e-5)
+
+
+def test_norm_activation_pairing_on_the_cpu():
+    """fuse_norm_activation's pairing rules (the reference's, regions.py:521-546, widened to
+    InstanceNorm2d); on CPU tensors the pair runs both modules unchanged."""
+    import copy
+
+    import bench
+    bn, act = nn.BatchNorm2d(4), nn.LeakyReLU(0.2)
+    assert regions.fuse_norm_activation(bn, act)
+    assert regions.fuse_norm_activation(bn, act)
+    assert not regions.fuse_norm_activation(bn, nn.ReLU())
+    assert not regions.fuse_norm_activation(nn.BatchNorm2d(4), nn.Sigmoid())
+    assert not regions.fuse_norm_activation(nn.BatchNorm1d(4), nn.ReLU())
+    assert not regions.fuse_norm_activation(nn.InstanceNorm2d(4), nn.GELU())
+    assert "_xdna_pair" not in bn._modules and set(bn.state_dict()) == set(nn.BatchNorm2d(4).state_dict())
+    torch.manual_seed(0)
+    x = torch.randn(2, 4, 5, 5)
+    ref_bn = nn.BatchNorm2d(4)
+    y = act(bn(x))
+    ref = nn.functional.leaky_relu(ref_bn(x), 0.2)
+    assert torch.equal(y, ref) and getattr(y, "_xdna_act_for", None) is None
+    assert torch.equal(bn.running_mean, ref_bn.running_mean) and int(bn.num_batches_tracked) == 1
+    clone = copy.deepcopy(nn.Sequential(bn, act))
+    assert clone[0]._xdna_pair is clone[1] and clone[0].forward.__self__ is clone[0]
+    Generator, _ = bench.style_models(torch, nn)
+    assert regions.fuse_norm_activations(Generator()) == 10
+
+
+def test_norm_activation_switch(monkeypatch):
+    monkeypatch.setenv("XDNA_REGIONS", "0")
+    assert not regions.fuse_norm_activation(nn.BatchNorm2d(4), nn.ReLU())
