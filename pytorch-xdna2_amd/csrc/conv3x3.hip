@@ -1835,7 +1835,10 @@ std::atomic<int> g_wgrad_rows_kt{[] {
 // (images wider than 36 are packed as strips with one real column on each side) are
 // zeroed in the dY tile: those pixels belong to the neighbouring strip.  Either row layout
 // (the reference's, or the tight one without zero columns).
-constexpr int kWrA = 128 + 16;   // LDS pitch (elements) of the dY tile: rows 8 banks apart
+// LDS pitch of the dY tile: 160 elements (80 dwords, 16 mod 64) puts the 4 rows x 2
+// column halves of a half-wave transposing read on 8 distinct groups of 8 banks (144 put
+// two of them on the same banks)
+constexpr int kWrA = 128 + 32;
 // LDS pitch of the x window: 96 elements (192 bytes, 64 mod 128) keeps the 32 lanes of a
 // half-wave transposing read on distinct banks of gfx950's 64 (5.5x fewer conflicts than
 // 80 on the largest sweep shape)

@@ -494,10 +494,11 @@ void gemm2_kernel(GemmArgs g) {
 // row-contiguous ones (checked by the launcher).
 // ---------------------------------------------------------------------------------------
 constexpr int kT4 = 256, kK4 = 64, kP4 = 72;
-// A row-contiguous operand's k-tile stays in its own layout, [k][row] with pitch kPR4
-// (consecutive k rows start 8 banks apart), and its MFMA fragments are read with the
-// transposing LDS read; it fits the region of a k-contiguous tile.
-constexpr int kPR4 = kT4 + 16;
+// A row-contiguous operand's k-tile stays in its own layout, [k][row] with pitch kPR4,
+// and its MFMA fragments are read with the transposing LDS read; it fits the region of a
+// k-contiguous tile.  The pitch (144 dwords, 16 mod 64) puts the 4 k rows x 32 row
+// elements of a half-wave read on distinct banks (272 elements overlapped two of them).
+constexpr int kPR4 = kT4 + 32;
 static_assert(kK4 * kPR4 <= kT4 * kP4, "a [k][row] tile fits the operand region");
 typedef short g4i16x4 __attribute__((ext_vector_type(4)));
 constexpr size_t kGemm4Lds = size_t(2) * 2 * kT4 * kP4 * 2;  // 2 buffers x (A, B)

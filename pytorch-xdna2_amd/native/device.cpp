@@ -622,6 +622,11 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("set_", TORCH_FN(set_empty_));
   m.impl("_copy_from", TORCH_FN(copy_from_xdna));
   m.impl("_copy_from_and_resize", TORCH_FN(copy_from_and_resize_xdna));
+  // mse_loss is structured: without a kernel of its own the non-functional composite
+  // allocates a 0-dim output and calls mse_loss.out, whose ROCm kernel builds its
+  // elementwise iterator into that output (a deprecated resize) before reducing into it.
+  // The functional ROCm kernel on aliases allocates the output itself.
+  m.impl("mse_loss", torch::CppFunction::makeFromBoxedFunction<&xdna_fallback>());
   register_hot_ops(m);
 }
 

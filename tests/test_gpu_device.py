@@ -532,3 +532,25 @@ def test_non_default_stream_is_refused(xdna):
     g.replay()
     torch.xdna.synchronize()
     assert float(b.sum().cpu()) == 2048.0
+
+
+def test_mse_loss_without_resized_outputs():
+    """mse_loss runs PyTorch-ROCm's functional kernel (not the out= form through the
+    composite, which resized a 0-dim output), for every reduction, forward and backward."""
+    import warnings
+    g = torch.Generator().manual_seed(11)
+    a = torch.randn(4, 8, 6, 6, generator=g)
+    b = torch.randn(4, 8, 6, 6, generator=g)
+    for red in ("mean", "sum", "none"):
+        ad = a.to(X).requires_grad_()
+        with warnings.catch_warnings(record=True) as w:
+            warnings.simplefilter("always")
+            out = torch.nn.functional.mse_loss(ad, b.to(X), reduction=red)
+            out.sum().backward() if red == "none" else out.backward()
+        assert not [x for x in w if "resized" in str(x.message)], [str(x.message) for x in w]
+        ac = a.clone().requires_grad_()
+        ref = torch.nn.functional.mse_loss(ac, b, reduction=red)
+        ref.sum().backward() if red == "none" else ref.backward()
+        assert out.shape == ref.shape and out.device.type == "xdna"
+        torch.testing.assert_close(out.detach().cpu(), ref.detach(), rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(ad.grad.cpu(), ac.grad, rtol=1e-5, atol=1e-6)
