@@ -737,6 +737,206 @@ bool launch2(dim3 grid, hipStream_t st, const GemmArgs& g) {
   return true;
 }
 
+// ---------------------------------------------------------------------------------------
+// Direct-to-LDS variant of the four-wave kernel: the same 256 x 256 tile and wave layout,
+// with k-tiles of 32 loaded by gfx950's 16-byte LDS DMA (buffer_load ... lds): a wave's
+// load instruction writes 64 x 16 bytes contiguously at an LDS base (measured on the
+// MI355X: lane L at base + 16 L; a lane past the buffer's range writes zeros), so the
+// data never passes through registers and no LDS store is issued.  Four k-tile buffers
+// (128 KB) let a k-tile's loads issue three k-tiles before its first read; a wave waits
+// on its own loads with a counted s_waitcnt and the barrier publishes everyone's.
+// Layouts, both unpadded with 16-byte pieces permuted so that MFMA fragment reads hit
+// distinct banks (each lane loads the piece its LDS position holds):
+//   k-contiguous operand, [256 rows][4 pieces of 8 k]: piece c of row r at r * 4 + (c ^ ((r >> 2) & 3));
+//   row-contiguous operand, [32 k][32 pieces of 8 rows]: piece q of k row kr at kr * 32 + (q ^ 4 (kr & 3)).
+// ---------------------------------------------------------------------------------------
+constexpr int kK5 = 32, kNB5 = 4;
+constexpr int kTile5 = kT4 * kK5;                          // elements of one operand's k-tile
+constexpr size_t kGemm5Lds = size_t(kNB5) * 2 * kTile5 * 2;  // 4 buffers x (A, B): 128 KB
+typedef __attribute__((address_space(3))) void g5_lds;
+
+// One operand's DMA plan: per thread 4 loads of 16 bytes per k-tile (blocks 4 w + i of
+// 1 KB, w the wave).  roff: the row part of the element offset (-1: rows past the
+// operand), kq: the k offset within the k-tile.
+struct G5Operand {
+  __amdgpu_buffer_rsrc_t rs;
+  int roff[4];
+  int kq[4];
+  int s_k;
+};
+
+template <int kMode>
+__device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t s_k, int r0, int rows, int K,
+                                       int tid) {
+  G5Operand o;
+  const int64_t extent = ((int64_t(rows) - 1) * s_r + (int64_t(K) - 1) * s_k + 1) * 2;
+  o.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), 0, int(extent), 0x00020000);
+  o.s_k = int(s_k);
+  const int lane = tid & 63, w = tid >> 6;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = 4 * w + i;
+    if (kMode == kAlongK) {
+      // block j: rows 16 j .. 16 j + 15, lane L at row 16 j + L / 4, position L % 4
+      const int r = 16 * j + (lane >> 2);
+      const int c = (lane & 3) ^ ((r >> 2) & 3);
+      o.roff[i] = r0 + r < rows ? int(int64_t(r0 + r) * s_r) : -1;
+      o.kq[i] = c * 8;
+    } else {
+      // block j: k rows 2 j, 2 j + 1, lane L at k row 2 j + L / 32, position L % 32
+      const int kr = 2 * j + (lane >> 5);
+      const int q = (lane & 31) ^ (4 * (kr & 3));
+      o.roff[i] = r0 + 8 * q < rows ? (r0 + 8 * q) : -1;  // s_r == 1
+      o.kq[i] = kr;
+    }
+  }
+  return o;
+}
+
+// The 4 DMA loads of k-tile k0 .. k0 + 31 (clamped, masked past K) into `tile`.
+__device__ inline void g5_load(uint16_t* tile, const G5Operand& o, int k0, int K, int w) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = k0 + o.kq[i];
+    const bool ok = o.roff[i] >= 0 && k < K;
+    const int off = ok ? (o.roff[i] + k * o.s_k) * 2 : 0x7FFFFFF0;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rs, (g5_lds*)(tile + (4 * w + i) * 512), 16, off, 0, 0, 0);
+  }
+}
+
+// MFMA fragment (rows rb + lane % 32, k = 16 ks + 8 (lane / 32) .. +8) from a k-tile.
+template <int kMode>
+__device__ inline u32x4_t g5_frag(const uint16_t* tile, int rb, int ks, int lane) {
+  if (kMode == kAlongK) {
+    const int r = rb + (lane & 31);
+    const int c = (2 * ks + (lane >> 5)) ^ ((r >> 2) & 3);
+    return *reinterpret_cast<const u32x4_t*>(tile + (r * 4 + c) * 8);
+  }
+  // transposing reads: in 16-lane group g = lane / 16 (rows +16 (g % 2), k +8 (g / 2)),
+  // lane j supplies (k + j / 4, row + 4 (j % 4)); every lane receives 4 consecutive k of
+  // its own row.  The high half (k + 4) keeps k % 4, so the same piece permutation.
+  const int g = lane >> 4, j = lane & 15;
+  const int kr = 16 * ks + 8 * (g >> 1) + (j >> 2);
+  const int rr = rb + 16 * (g & 1) + 4 * (j & 3);
+  const uint16_t* p = tile + (kr * 32 + ((rr >> 3) ^ (4 * (kr & 3)))) * 8 + (rr & 7);
+  const g4i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) g4i16x4*)(p));
+  const g4i16x4 hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) g4i16x4*)(p + 4 * 32 * 8));
+  const g2u2 a = __builtin_bit_cast(g2u2, lo), b = __builtin_bit_cast(g2u2, hi);
+  return u32x4_t{a[0], a[1], b[0], b[1]};
+}
+
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
+template <int n>
+__device__ inline void g5_wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int kModeA, int kModeB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm5_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  int tbx, tby;
+  gemm_tile_xy(g, tbx, tby);
+  const int m0 = tby * kT4, n0 = tbx * kT4;
+  const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
+  // split-K ranges are whole k-tiles of 64 (kt_per counts those)
+  const int kbeg = split * g.kt_per * kK4, kend = min(g.K, kbeg + g.kt_per * kK4);
+  const int ntiles = kend > kbeg ? (kend - kbeg + kK5 - 1) / kK5 : 0;
+  const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
+  const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = zero_acc();
+
+  if (ntiles > 0) {
+    u32x4_t fa[2][4], fb[2][4];
+    const G5Operand oa = g5_operand<kModeA>(A, g.a_r, g.a_k, m0, g.M, g.K, tid);
+    const G5Operand ob = g5_operand<kModeB>(B, g.b_r, g.b_k, n0, g.N, g.K, tid);
+    // k-tile t in buffer t % 4: A then B
+    auto tbuf = [&](int t) { return smem + (t & (kNB5 - 1)) * 2 * kTile5; };
+#define XDNA_G5_LOAD(t_)                                                                      \
+  do {                                                                                        \
+    const int k_ = kbeg + min((t_), ntiles - 1) * kK5;                                        \
+    g5_load(tbuf(t_), oa, k_, kend, wave);                                                    \
+    g5_load(tbuf(t_) + kTile5, ob, k_, kend, wave);                                           \
+  } while (0)
+#define XDNA_G5_FRAGS(buf_, t_, ks_)                                                          \
+  do {                                                                                        \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                             \
+      fa[buf_][i] = g5_frag<kModeA>(tbuf(t_), wm * 128 + i * 32, (ks_), lane);                \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j)                                             \
+      fb[buf_][j] = g5_frag<kModeB>(tbuf(t_) + kTile5, wn * 128 + j * 32, (ks_), lane);       \
+  } while (0)
+#define XDNA_G5_MFMA(buf_)                                                                    \
+  do {                                                                                        \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                             \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j)                                           \
+        acc[i][j] = mfma_32x32x16(as_bf16x8(fa[buf_][i]), as_bf16x8(fb[buf_][j]), acc[i][j]); \
+  } while (0)
+
+    // prologue: k-tiles 0..3 in flight (8 loads each, always issued: the counts stay
+    // static); wait for k-tile 0's
+#pragma unroll
+    for (int t = 0; t < kNB5; ++t) XDNA_G5_LOAD(t);
+    g5_wait_vm<8 * (kNB5 - 1)>();
+    __builtin_amdgcn_s_barrier();
+    XDNA_G5_FRAGS(0, 0, 0);
+    constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100;
+    constexpr int kRd = (kModeA == kAlongK ? 4 : 8) + (kModeB == kAlongK ? 4 : 8);
+    for (int t = 0; t < ntiles; ++t) {
+      // k-step 0 of k-tile t: k-step 1's fragments are read meanwhile
+      XDNA_G5_FRAGS(1, t, 1);
+      XDNA_G5_MFMA(0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        if (i < kRd) __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // this wave's reads of buffer t are complete, and its loads of k-tile t+1 (two
+      // k-tiles, 16 loads, may stay in flight); the barrier makes k-tile t+1 visible and
+      // buffer t free
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8) | 15 | (3 << 14));  // lgkmcnt(0) only
+      g5_wait_vm<8 * (kNB5 - 2)>();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      XDNA_G5_LOAD(t + kNB5);              // into buffer t % kNB5
+      XDNA_G5_FRAGS(0, t + 1, 0);          // k-tile t+1 (past the end: never used)
+      XDNA_G5_MFMA(1);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        if (i < 8) __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
+        if (i < kRd) __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // drain the clamped loads issued past the end before the workgroup can exit
+    g5_wait_vm<0>();
+#undef XDNA_G5_LOAD
+#undef XDNA_G5_FRAGS
+#undef XDNA_G5_MFMA
+  }
+  store_block<4, 4>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
+}
+
+template <int MA, int MB>
+bool launch5(dim3 grid, hipStream_t st, const GemmArgs& g) {
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm5_kernel<MA, MB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(kGemm5Lds)) == hipSuccess;
+  if (!ok) return false;
+  gemm5_kernel<MA, MB><<<grid, 256, kGemm5Lds, st>>>(g);
+  return true;
+}
+
 template <int MA, int MB>
 bool launch4(dim3 grid, hipStream_t st, const GemmArgs& g) {
   static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm4_kernel<MA, MB>),
@@ -888,7 +1088,8 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   hipStream_t st2 = as_stream(stream);
   // Large tiles (256 x 256) when neither operand needs scalar staging and the grid still
   // has enough tiles: the four-wave kernel where its whole-vector loads fit the shape, else
-  // the eight-wave one; xdna_gemm_set_variant overrides (1 small, 2 eight-wave, 3 four-wave).
+  // the eight-wave one; xdna_gemm_set_variant overrides (1 small, 2 eight-wave, 3 four-wave,
+  // 4 four-wave with direct-to-LDS loads).
   const int variant = g_gemm_variant.load();
   const int64_t tiles2 = ceil_div(N, kT2) * ceil_div(M, kT2) * int64_t(batch);
   const bool vec_ok = ma != kScalar && mb != kScalar;
@@ -904,7 +1105,11 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   // four-wave kernel's longer prologue (one wave per SIMD) pays off from K = 1024 on
   // config 3's GEMMs (even there, ahead of the eight-wave kernel from K = 4096).
   const bool big = tiles2 >= 64 || K >= 16384;
-  const bool use4 = fits4 && g.rs_ok && (variant == 3 || (variant == 0 && big && K >= 1024));
+  const bool use4 = fits4 && g.rs_ok && (variant == 3 || variant == 4 || (variant == 0 && big && K >= 1024));
+  // the direct-to-LDS form where both operands are k-contiguous (measured 3-10 % ahead of
+  // the register-staged one on config 3's forward products; behind it when a transposing
+  // read is involved)
+  const bool use5 = use4 && (variant == 4 || (variant == 0 && ma == kAlongK && mb == kAlongK));
   if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && big))) {
     // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
     const int kt2 = int(ceil_div(K, kK2));
@@ -925,7 +1130,10 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
     bool ok;
     if (use4 && g_gemm_xcd.load() && (int64_t(grid2.x) * grid2.y) % kGemmXcds == 0)
       g.xcd_group = int(std::min<unsigned>(grid2.y, 8));
-    if (use4) {
+    if (use5) {
+      if (ma == kAlongK) ok = mb == kAlongK ? launch5<kAlongK, kAlongK>(grid2, st2, g) : launch5<kAlongK, kAlongRow>(grid2, st2, g);
+      else ok = mb == kAlongK ? launch5<kAlongRow, kAlongK>(grid2, st2, g) : launch5<kAlongRow, kAlongRow>(grid2, st2, g);
+    } else if (use4) {
       if (ma == kAlongK) ok = mb == kAlongK ? launch4<kAlongK, kAlongK>(grid2, st2, g) : launch4<kAlongK, kAlongRow>(grid2, st2, g);
       else ok = mb == kAlongK ? launch4<kAlongRow, kAlongK>(grid2, st2, g) : launch4<kAlongRow, kAlongRow>(grid2, st2, g);
     } else if (ma == kAlongK) {
@@ -1005,8 +1213,8 @@ extern "C" int xdna_gemm_bf16_noalloc(const uint16_t* A, const uint16_t* Bm, uin
 }
 
 extern "C" int xdna_gemm_set_variant(int variant) {
-  if (variant < 0 || variant > 3) {
-    set_error("xdna_gemm_set_variant: variant must be 0..3");
+  if (variant < 0 || variant > 4) {
+    set_error("xdna_gemm_set_variant: variant must be 0..4");
     return -1;
   }
   g_gemm_variant.store(variant);
