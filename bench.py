@@ -483,6 +483,29 @@ def kernel_summary(report):
     return out
 
 
+def gemm_product(layout, variant, M=8192, N=4096, K=4096, launches=30):
+    """Launches one config-3 product through the C ABI with a forced kernel variant: the
+    workload of the GEMM counter passes (rocprofv3 --pmc)."""
+    import torch
+
+    from xdna_train import hip_abi
+    lib = hip_abi.load()
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(0)
+    a = (torch.randn(K, M, generator=g) if layout[0] == "t" else torch.randn(M, K, generator=g)).cuda().bfloat16()
+    b = (torch.randn(N, K, generator=g) if layout[1] == "t" else torch.randn(K, N, generator=g)).cuda().bfloat16()
+    a_s = (1, M) if layout[0] == "t" else (K, 1)
+    b_s = (1, K) if layout[1] == "t" else (N, 1)
+    c = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    assert lib.xdna_gemm_set_variant(int(variant)) == 0
+    for _ in range(launches):
+        assert lib.xdna_gemm_bf16(a.data_ptr(), b.data_ptr(), c.data_ptr(), None, 1, M, N, K, a_s[0], a_s[1], 0,
+                                  b_s[0], b_s[1], 0, N, 1, M * N, 0, 0, 1, 1.0, 0.0, st) == 0
+    torch.cuda.synchronize()
+    print(f"gemm product {layout} variant {variant}: {launches} launches", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -498,10 +521,15 @@ def main() -> int:
     ap.add_argument("--resnet-steps", type=int, default=10)
     ap.add_argument("--cpu-rounds", type=int, default=2)
     ap.add_argument("--cpu-worker", help=argparse.SUPPRESS)
+    ap.add_argument("--gemm-product", metavar="LAYOUT,VARIANT",
+                    help="only 30 launches of config 3's largest product (M 8192, N 4096, K 4096) with "
+                         "operand layout nt / nn / tn and xdna_gemm_set_variant VARIANT (counter passes)")
     args = ap.parse_args()
     if args.cpu_worker:
         cpu_worker(args.cpu_worker)
         return 0
+    if args.gemm_product:
+        return gemm_product(*args.gemm_product.split(","))
     if args.gpus != 1:
         print("bench.py: this build runs on one MI355X only (one process, one GPU); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
