@@ -2046,8 +2046,269 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Weight gradient on the packed row layouts fed by gfx950's 16-byte LDS DMA (buffer_load
+// ... lds: a wave's load writes 64 x 16 bytes contiguously at an LDS base, lane L at base +
+// 16 L; a lane whose offset is past the buffer range writes zeros).  The workgroup tile,
+// waves, split plan and partial layout are wgrad_rows_kernel's (128 output x 64 input
+// channels x 9 taps over the k-tiles of one split; eight waves, wave (wm, wn) owning 32 x 32
+// channels); the staging differs: k-tiles of 64 output rows go into four LDS buffers three
+// k-tiles ahead of their first read, with no register staging, no LDS stores and one
+// barrier per k-tile, and fragment reads run one k-step ahead of the MFMAs.  Both tiles
+// are unpadded, their 16-byte pieces permuted so that the 4 rows x 64 bytes of a half-wave
+// transposing read fall on 64 distinct banks (each lane loads the piece its LDS position
+// holds):
+//   dY tile [64 rows][16 pieces of 8 channels]: piece c of row r at r * 16 + (c ^ 4 (r & 3));
+//   x window [160 rows][8 pieces]: piece c of row r at r * 8 + (c ^ 4 ((r >> 1) & 1)).
+// dY pieces past the last channel chunk, rows past the end and a strip's halo columns are
+// zeroed (an offset past the range); x rows past the group's 2126 read as zero.
+// ---------------------------------------------------------------------------------------
+constexpr int kW5Kt = 64;                               // output rows per k-tile
+constexpr int kW5Nb = 4;                                // k-tile buffers
+constexpr int kW5XRows = 160;                           // window rows per buffer (>= 64 + 78 + 4)
+constexpr int kW5Buf = kW5Kt * 128 + kW5XRows * 64;     // elements of one k-tile buffer
+constexpr size_t kW5Lds = size_t(kW5Nb) * kW5Buf * 2;   // 144 KiB
+// DMA blocks (1 KiB) per k-tile: 16 of dY (4 rows each), 20 of x (8 rows each).  Wave w
+// loads dY blocks 2w, 2w + 1 and x blocks 3w .. 3w + 2 (w < 4) or 2w + 4, 2w + 5 (w >= 4):
+// 5 or 4 loads per k-tile.
+constexpr int kW5LoadsHi = 5, kW5LoadsLo = 4;
+typedef int w5_i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource of `bytes` bytes at `base` (stride 0: offsets in bytes; the dword-3 flags
+// of __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000)).
+__device__ inline w5_i32x4 w5_rsrc(const void* base, int bytes) {
+  const uint64_t b = uint64_t(base);
+  return w5_i32x4{int(uint32_t(b)), int(uint32_t(b >> 32) & 0xFFFF), bytes, 0x00020000};
+}
+
+// One 16-byte LDS DMA (buffer_load_dwordx4 ... lds): lane L's 16 bytes at byte offset voff
+// of the resource land at lds + 16 L (zeros for an offset past the range).  Issued from
+// inline assembly: for the compiler's builtin, the compiler's wait insertion makes every
+// later LDS read wait for all outstanding DMA (vmcnt(0)), which would serialize the k-tile
+// pipeline; here completion is tracked by the kernel's own counted vmcnt waits before the
+// barriers that publish a k-tile.  M0 (the LDS base) is set inside the statement; nothing
+// else in the kernel uses M0.
+__device__ inline void w5_dma16(const w5_i32x4& rsrc, const uint16_t* lds, int voff) {
+  const uint32_t m0 = uint32_t(uintptr_t((__attribute__((address_space(3))) const uint16_t*)lds));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
+template <int n>
+__device__ inline void w5_wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+struct W5Frags {
+  u32x4_t a;      // dY fragment of the wave's 32 output channels
+  uint2 x[3][3];  // per kernel row: 12 consecutive rows of the wave's 32 input channels
+};
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void wgrad_rows5_kernel(WgRowsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  constexpr int kTilesPerGroup = kGroupOutRows / kW5Kt;
+  const int L = blockIdx.x;
+  const int xcd = L % kXcds, kq = L / kXcds;
+  const int tile = kq % a.ntiles;
+  const int split = (kq / a.ntiles) * kXcds + xcd;
+  if (split >= a.splits) return;
+  const int co_t = tile % a.nco_t, ci_t = tile / a.nco_t;
+  const int co0 = co_t * kTCo, ci0 = ci_t * 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 3, wn = wave >> 2;
+  const int kt0 = split * a.kt_per_split;
+  const int ntl = min(a.ktiles, kt0 + a.kt_per_split) - kt0;
+
+  f32x16_t acc[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) acc[t] = zero_acc();
+  float bsum = 0.0f;
+  const bool do_bias = a.bpart && ci_t == 0 && wn == 0;
+
+  if (ntl > 0) {
+    // DMA plan.  dY block 2 wave + i: k-tile rows 8 wave + 4 i + lane / 16, LDS position
+    // lane % 16 holding global piece dq (channel chunk co0 / 64 + dq / 8).
+    const bool strips = a.S > 1;
+    const int dq = (lane & 15) ^ (4 * (lane >> 4));
+    const bool dchunk_ok = co0 / 64 + (dq >> 3) < a.co_chunks;
+    const int doff0 = (dq >> 3) * kGroupRows * 128 + (dq & 7) * 16;  // bytes, + 128 per row
+    int drow[2], drmod[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      drow[i] = 8 * wave + 4 * i + (lane >> 4);
+      drmod[i] = drow[i] % a.wp;
+    }
+    const int nrel = min(2, a.co_chunks - co0 / 64);
+    const int dext = (nrel - 1) * kGroupRows * 128 + kW5Kt * 128;
+    // x block xb0 + i: window rows 8 (xb0 + i) + lane / 8, LDS position lane % 8 holding
+    // global piece xq (bit 1 of the row is bit 1 of lane / 8)
+    const int xb0 = wave < 4 ? 3 * wave : 2 * wave + 4;
+    const int xq = (lane & 7) ^ (4 * ((lane >> 4) & 1));
+    const int xoff0 = (8 * xb0 + (lane >> 3)) * 128 + xq * 16;  // bytes, + 1 KiB per block
+
+    // k-tile tl of the split (clamped to the last: the load count stays static) into
+    // buffer tl % kW5Nb
+    auto load = [&](int tl) {
+      const int kt = kt0 + min(tl, ntl - 1);
+      uint16_t* buf = smem + (tl & (kW5Nb - 1)) * kW5Buf;
+      const int g = kt / kTilesPerGroup, r0 = (kt % kTilesPerGroup) * kW5Kt;
+      const uint16_t* dbase =
+          a.dp + ((int64_t(g) * a.co_chunks + co0 / 64) * kGroupRows + r0 + a.wp + 1) * kKStep;
+      const w5_i32x4 drs = w5_rsrc(dbase, dext);
+      const int64_t rem = a.m_total - int64_t(kt) * kW5Kt;  // rows of this k-tile before the end
+      const int base = int((uint32_t(kt) * uint32_t(kW5Kt)) % uint32_t(a.wp));
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        // data column of the centre row p + wp + 1 (row position jc + 1, wrapping to the
+        // next row's position 0); a strip's halo columns are masked
+        int jc = base + drmod[i];
+        jc -= jc >= a.wp ? a.wp : 0;
+        int dj = jc + 1 - a.lead;
+        dj = dj == a.wp ? 0 : dj;
+        const bool halo = strips && (dj == 0 || dj == a.Wg - 1);
+        const bool ok = dchunk_ok && drow[i] < rem && !halo;
+        const int off = ok ? doff0 + drow[i] * 128 : 0x7FFFFFF0;
+        w5_dma16(drs, buf + (2 * wave + i) * 512, off);
+      }
+      const uint16_t* xbase = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
+      const w5_i32x4 xrs = w5_rsrc(xbase, (kGroupRows - r0) * 128);
+      const uint16_t* xl = buf + kW5Kt * 128 + xb0 * 512;
+      w5_dma16(xrs, xl, xoff0);
+      w5_dma16(xrs, xl + 512, xoff0 + 1024);
+      if (wave < 4) w5_dma16(xrs, xl + 1024, xoff0 + 2048);
+    };
+    // this wave's loads of the oldest k-tile in flight have landed, n k-tiles' may stay
+    // in flight
+    auto wait_tiles = [&](auto n_tag) {
+      constexpr int n = decltype(n_tag)::value;
+      if (wave < 4)
+        w5_wait_vm<kW5LoadsHi * n>();
+      else
+        w5_wait_vm<kW5LoadsLo * n>();
+    };
+
+    // Lane parts of the transposing reads (wr_lane_off's assignment: in 16-lane group
+    // gq = lane / 16, lane j supplies row + 8 (gq / 2) + j / 4, column + 16 (gq % 2) + 4 (j % 4)).
+    const int gq = lane >> 4, jq = lane & 15;
+    const int rq = 8 * (gq >> 1) + (jq >> 2);
+    int x_off[3];
+    const int ca = wm * 32 + 16 * (gq & 1) + 4 * (jq & 3);
+    const int a_off = rq * 128 + (((ca >> 3) ^ (4 * (rq & 3))) << 3) + (ca & 7);
+#pragma unroll
+    for (int dy = 0; dy < 3; ++dy) {
+      const int c = wn * 32 + 16 * (gq & 1) + 4 * (jq & 3);
+      const int r = dy * a.wp + rq;
+      x_off[dy] = kW5Kt * 128 + r * 64 + (((c >> 3) ^ (4 * ((r >> 1) & 1))) << 3) + (c & 7);
+    }
+    // k-step ks of a buffer: rows 16 ks .. +15 (the row bits the permutations use are
+    // those of the lane part: 16 ks and 4 q leave bits 0 and 1 of a row alone)
+    auto frags = [&](W5Frags& f, const uint16_t* buf, int ks) {
+      const uint2 lo = wr_tr(buf + a_off + ks * 16 * 128);
+      const uint2 hi = wr_tr(buf + a_off + (ks * 16 + 4) * 128);
+      f.a = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+        for (int q = 0; q < 3; ++q) f.x[dy][q] = wr_tr(buf + x_off[dy] + (ks * 16 + 4 * q) * 64);
+    };
+    auto mfmas = [&](const W5Frags& f, auto bias_tag) {
+      constexpr bool kBias = decltype(bias_tag)::value;
+      if (kBias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          bsum += __uint_as_float(f.a[e] << 16) + __uint_as_float(f.a[e] & 0xFFFF0000u);
+      }
+      const bf16x8_t af = as_bf16x8(f.a);
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy) {
+        const uint2 r0 = f.x[dy][0], r1 = f.x[dy][1], r2 = f.x[dy][2];
+        const u32x4_t l = {r0.x, r0.y, r1.x, r1.y};
+        u32x4_t s1, s2;
+        s1[0] = __builtin_amdgcn_alignbit(r0.y, r0.x, 16);
+        s1[1] = __builtin_amdgcn_alignbit(r1.x, r0.y, 16);
+        s1[2] = __builtin_amdgcn_alignbit(r1.y, r1.x, 16);
+        s1[3] = __builtin_amdgcn_alignbit(r2.x, r1.y, 16);
+        s2[0] = r0.y;
+        s2[1] = r1.x;
+        s2[2] = r1.y;
+        s2[3] = r2.x;
+        acc[dy * 3 + 0] = mfma_32x32x16(af, as_bf16x8(l), acc[dy * 3 + 0]);
+        acc[dy * 3 + 1] = mfma_32x32x16(af, as_bf16x8(s1), acc[dy * 3 + 1]);
+        acc[dy * 3 + 2] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2]);
+      }
+    };
+
+    // the k-tile loop, instantiated with and without the bias sums (a wave-uniform choice
+    // outside the loop)
+    auto run = [&](auto bias_tag) {
+      W5Frags f0, f1;
+#pragma unroll
+      for (int t = 0; t < kW5Nb; ++t) load(t);
+      wait_tiles(std::integral_constant<int, kW5Nb - 1>{});
+      __builtin_amdgcn_s_barrier();
+      frags(f0, smem, 0);
+      for (int tl = 0; tl < ntl; ++tl) {
+        const uint16_t* buf = smem + (tl & (kW5Nb - 1)) * kW5Buf;
+        frags(f1, buf, 1);
+        mfmas(f0, bias_tag);
+        frags(f0, buf, 2);
+        mfmas(f1, bias_tag);
+        frags(f1, buf, 3);
+        mfmas(f0, bias_tag);
+        // this wave's reads of the buffer are complete and its loads of k-tile tl + 1 have
+        // landed (two k-tiles of loads may stay in flight); the barrier publishes every
+        // wave's and frees the buffer for k-tile tl + kW5Nb
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8) | 15 | (3 << 14));  // lgkmcnt(0) only
+        wait_tiles(std::integral_constant<int, kW5Nb - 2>{});
+        __builtin_amdgcn_s_barrier();
+        load(tl + kW5Nb);
+        frags(f0, smem + ((tl + 1) & (kW5Nb - 1)) * kW5Buf, 0);  // past the end: never used
+        mfmas(f1, bias_tag);
+      }
+      // drain the clamped loads issued past the end before the workgroup can exit
+      w5_wait_vm<0>();
+    };
+    if (do_bias)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
+  }
+
+  // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci
+  const int lr = lane & 31;
+  float* pbase = a.part + int64_t(split) * a.co_pad * 9 * a.ci_pad;
+  const int ci = ci0 + wn * 32 + lr;
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 32 + mfma_row(i, lane);
+      pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][i];
+    }
+  if (do_bias) {
+    // lanes l and l+32 hold the two 8-row halves of channel row l % 32
+    const float other = __shfl_down(bsum, 32, 64);
+    if (lane < 32) a.bpart[int64_t(split) * a.co_pad + co0 + wm * 32 + lane] = bsum + other;
+  }
+}
+
+// Kernel of the rows weight gradient: 1 register-staged k-tiles (wgrad_rows_kernel), 2
+// k-tiles loaded straight into LDS (wgrad_rows5_kernel);
+// XDNA_WGRAD_KERNEL at start-up, xdna_conv3x3_set_wgrad_rows_kernel.
+std::atomic<int> g_wgrad_rows_form{[] {
+  const char* e = std::getenv("XDNA_WGRAD_KERNEL");
+  return e && std::atoi(e) == 2 ? 2 : 1;
+}()};
+
 struct WgRowsPlan {
   ConvGeom geom;
+  int form = 1;      // 1: wgrad_rows_kernel, 2: wgrad_rows5_kernel
   int kt_rows = 64;  // output rows per k-tile
   int ci_chunks = 0, co_chunks = 0, ci_pad = 0, co_pad = 0;
   int ktiles = 0, splits = 0, kt_per = 0;
@@ -2061,7 +2322,8 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   p.co_chunks = int(ceil_div(Cout, kKStep));
   p.ci_pad = p.ci_chunks * kKStep;
   p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
-  p.kt_rows = g_wgrad_rows_kt.load() == 128 ? 128 : 64;
+  p.form = g_wgrad_rows_form.load() == 2 ? 2 : 1;
+  p.kt_rows = p.form == 2 ? kW5Kt : g_wgrad_rows_kt.load() == 128 ? 128 : 64;
   p.ktiles = int(ceil_div(p.geom.m_total, p.kt_rows));
   const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
   const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
@@ -2086,7 +2348,8 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   p.splits = int(ceil_div(p.ktiles, p.kt_per));
   p.part_bytes = align256(size_t(p.splits) * out_elems * 4);
   p.bpart_bytes = align256(size_t(p.splits) * p.co_pad * 4);
-  p.lds_bytes = 2 * (size_t(p.kt_rows) * kWrA + size_t(p.kt_rows + 2 * p.geom.st.wp + 2 + 4) * kWrX) * 2;
+  p.lds_bytes = p.form == 2 ? kW5Lds
+                            : 2 * (size_t(p.kt_rows) * kWrA + size_t(p.kt_rows + 2 * p.geom.st.wp + 2 + 4) * kWrX) * 2;
   return p;
 }
 
@@ -2281,6 +2544,8 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
       hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel<64>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel<128>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows5_kernel),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess;
   if (!lds_attr || p.lds_bytes > kMaxWgradLds) {
     (void)hipGetLastError();
@@ -2313,7 +2578,9 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
     return -1;
   }
   hipStream_t st = as_stream(stream);
-  if (p.kt_rows == 128)
+  if (p.form == 2)
+    wgrad_rows5_kernel<<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
+  else if (p.kt_rows == 128)
     wgrad_rows_kernel<128><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
   else
     wgrad_rows_kernel<64><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
@@ -2389,6 +2656,15 @@ int xdna_conv3x3_set_wgrad_rows_kt(int kt_rows) {
     return -1;
   }
   g_wgrad_rows_kt.store(kt_rows == 64 ? 64 : 128);
+  return 0;
+}
+
+int xdna_conv3x3_set_wgrad_rows_kernel(int form) {
+  if (form < 0 || form > 2) {
+    set_error("xdna_conv3x3_set_wgrad_rows_kernel: form must be 0 (default), 1 or 2");
+    return -1;
+  }
+  g_wgrad_rows_form.store(form == 2 ? 2 : 1);
   return 0;
 }
 

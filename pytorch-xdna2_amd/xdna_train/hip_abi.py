@@ -85,6 +85,7 @@ SIGNATURES = {
     "xdna_conv3x3_wgrad_rows_workspace_bytes": (Z, [I, I, I, I, I, I]),
     "xdna_conv3x3_wgrad_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_set_wgrad_rows_kt": (I, [I]),
+    "xdna_conv3x3_set_wgrad_rows_kernel": (I, [I]),
     "xdna_dilate2_bf16": (I, [P, P, L, I, I, P]),
     "xdna_upsample_nearest2x_bwd_bf16": (I, [P, P, L, I, I, P]),
     "xdna_conv2d_dgrad_bf16": (I, [P, P, P] + [I] * 11 + [P]),

@@ -169,11 +169,16 @@ def test_forward_tight_layout(hip, shape, variant):
     check_bf16(host(y), oracle.conv3x3_fwd(x, w, b), what=f"fwd tight {shape}")
 
 
-@pytest.fixture(params=[128, 64], ids=lambda k: f"kt{k}")
+@pytest.fixture(params=[(1, 128), (1, 64), (2, 64)], ids=lambda p: f"form{p[0]}-kt{p[1]}")
 def wgrad_kt(hip, request):
-    assert hip.xdna_conv3x3_set_wgrad_rows_kt(request.param) == 0
-    yield request.param
+    """Kernel form of the rows weight gradient (1: register-staged k-tiles of 128 or 64
+    rows, 2: 64-row k-tiles loaded straight into LDS) and its k-tile rows."""
+    form, kt = request.param
+    assert hip.xdna_conv3x3_set_wgrad_rows_kernel(form) == 0
+    assert hip.xdna_conv3x3_set_wgrad_rows_kt(kt) == 0
+    yield kt
     assert hip.xdna_conv3x3_set_wgrad_rows_kt(0) == 0
+    assert hip.xdna_conv3x3_set_wgrad_rows_kernel(0) == 0
 
 
 @pytest.mark.parametrize("layout", [0, 1])
@@ -208,6 +213,8 @@ def test_wgrad_rows(hip, shape, layout, wgrad_kt):
 def test_wgrad_rows_kt_setter_rejects(hip):
     assert hip.xdna_conv3x3_set_wgrad_rows_kt(96) == -1
     assert hip.xdna_conv3x3_set_wgrad_rows_kt(0) == 0
+    assert hip.xdna_conv3x3_set_wgrad_rows_kernel(3) == -1
+    assert hip.xdna_conv3x3_set_wgrad_rows_kernel(0) == 0
 
 
 def test_workspace_too_small_is_an_error(hip):
