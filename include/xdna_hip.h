@@ -264,7 +264,7 @@ size_t xdna_conv3x3_wgrad_rows_workspace_bytes(int B, int Cin, int Cout, int H, 
  * within the conv bar.  Workspace sizes depend on it: query them after setting it.  No
  * reference counterpart (measurements and tests). */
 int xdna_conv3x3_set_wgrad_rows_kt(int kt_rows);
-/* Kernel of xdna_conv3x3_wgrad_rows_bf16: 0 the default, 1 k-tiles staged through
+/* Kernel of xdna_conv3x3_wgrad_rows_bf16: 0 the default (form 2), 1 k-tiles staged through
  * registers (their rows as set by xdna_conv3x3_set_wgrad_rows_kt), 2 64-row k-tiles loaded
  * straight into LDS four k-tiles deep.  Like the k-tile setter it changes the split-K
  * partition (and the workspace size) within the conv bar.  No reference counterpart

@@ -2072,37 +2072,6 @@ constexpr size_t kW5Lds = size_t(kW5Nb) * kW5Buf * 2;   // 144 KiB
 // loads dY blocks 2w, 2w + 1 and x blocks 3w .. 3w + 2 (w < 4) or 2w + 4, 2w + 5 (w >= 4):
 // 5 or 4 loads per k-tile.
 constexpr int kW5LoadsHi = 5, kW5LoadsLo = 4;
-typedef int w5_i32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer resource of `bytes` bytes at `base` (stride 0: offsets in bytes; the dword-3 flags
-// of __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000)).
-__device__ inline w5_i32x4 w5_rsrc(const void* base, int bytes) {
-  const uint64_t b = uint64_t(base);
-  return w5_i32x4{int(uint32_t(b)), int(uint32_t(b >> 32) & 0xFFFF), bytes, 0x00020000};
-}
-
-// One 16-byte LDS DMA (buffer_load_dwordx4 ... lds): lane L's 16 bytes at byte offset voff
-// of the resource land at lds + 16 L (zeros for an offset past the range).  Issued from
-// inline assembly: for the compiler's builtin, the compiler's wait insertion makes every
-// later LDS read wait for all outstanding DMA (vmcnt(0)), which would serialize the k-tile
-// pipeline; here completion is tracked by the kernel's own counted vmcnt waits before the
-// barriers that publish a k-tile.  M0 (the LDS base) is set inside the statement; nothing
-// else in the kernel uses M0.
-__device__ inline void w5_dma16(const w5_i32x4& rsrc, const uint16_t* lds, int voff) {
-  const uint32_t m0 = uint32_t(uintptr_t((__attribute__((address_space(3))) const uint16_t*)lds));
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(m0), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
-template <int n>
-__device__ inline void w5_wait_vm() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 struct W5Frags {
   u32x4_t a;      // dY fragment of the wave's 32 output channels
   uint2 x[3][3];  // per kernel row: 12 consecutive rows of the wave's 32 input channels
@@ -2160,7 +2129,7 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
       const int g = kt / kTilesPerGroup, r0 = (kt % kTilesPerGroup) * kW5Kt;
       const uint16_t* dbase =
           a.dp + ((int64_t(g) * a.co_chunks + co0 / 64) * kGroupRows + r0 + a.wp + 1) * kKStep;
-      const w5_i32x4 drs = w5_rsrc(dbase, dext);
+      const i32x4_t drs = lds_dma_rsrc(dbase, dext);
       const int64_t rem = a.m_total - int64_t(kt) * kW5Kt;  // rows of this k-tile before the end
       const int base = int((uint32_t(kt) * uint32_t(kW5Kt)) % uint32_t(a.wp));
 #pragma unroll
@@ -2174,23 +2143,23 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
         const bool halo = strips && (dj == 0 || dj == a.Wg - 1);
         const bool ok = dchunk_ok && drow[i] < rem && !halo;
         const int off = ok ? doff0 + drow[i] * 128 : 0x7FFFFFF0;
-        w5_dma16(drs, buf + (2 * wave + i) * 512, off);
+        lds_dma16(drs, buf + (2 * wave + i) * 512, off);
       }
       const uint16_t* xbase = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
-      const w5_i32x4 xrs = w5_rsrc(xbase, (kGroupRows - r0) * 128);
+      const i32x4_t xrs = lds_dma_rsrc(xbase, (kGroupRows - r0) * 128);
       const uint16_t* xl = buf + kW5Kt * 128 + xb0 * 512;
-      w5_dma16(xrs, xl, xoff0);
-      w5_dma16(xrs, xl + 512, xoff0 + 1024);
-      if (wave < 4) w5_dma16(xrs, xl + 1024, xoff0 + 2048);
+      lds_dma16(xrs, xl, xoff0);
+      lds_dma16(xrs, xl + 512, xoff0 + 1024);
+      if (wave < 4) lds_dma16(xrs, xl + 1024, xoff0 + 2048);
     };
     // this wave's loads of the oldest k-tile in flight have landed, n k-tiles' may stay
     // in flight
     auto wait_tiles = [&](auto n_tag) {
       constexpr int n = decltype(n_tag)::value;
       if (wave < 4)
-        w5_wait_vm<kW5LoadsHi * n>();
+        lds_dma_wait<kW5LoadsHi * n>();
       else
-        w5_wait_vm<kW5LoadsLo * n>();
+        lds_dma_wait<kW5LoadsLo * n>();
     };
 
     // Lane parts of the transposing reads (wr_lane_off's assignment: in 16-lane group
@@ -2264,7 +2233,7 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
         // this wave's reads of the buffer are complete and its loads of k-tile tl + 1 have
         // landed (two k-tiles of loads may stay in flight); the barrier publishes every
         // wave's and frees the buffer for k-tile tl + kW5Nb
-        __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8) | 15 | (3 << 14));  // lgkmcnt(0) only
+        lds_reads_wait();
         wait_tiles(std::integral_constant<int, kW5Nb - 2>{});
         __builtin_amdgcn_s_barrier();
         load(tl + kW5Nb);
@@ -2272,7 +2241,7 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
         mfmas(f1, bias_tag);
       }
       // drain the clamped loads issued past the end before the workgroup can exit
-      w5_wait_vm<0>();
+      lds_dma_wait<0>();
     };
     if (do_bias)
       run(std::true_type{});
@@ -2299,11 +2268,16 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
 }
 
 // Kernel of the rows weight gradient: 1 register-staged k-tiles (wgrad_rows_kernel), 2
-// k-tiles loaded straight into LDS (wgrad_rows5_kernel);
-// XDNA_WGRAD_KERNEL at start-up, xdna_conv3x3_set_wgrad_rows_kernel.
+// k-tiles loaded straight into LDS (wgrad_rows5_kernel); XDNA_WGRAD_KERNEL at start-up,
+// xdna_conv3x3_set_wgrad_rows_kernel.
+// The default, form 2: level with form 1 over the sweep's 36 shapes (GPU time per shape's
+// fwd + dgrad + wgrad step, two A/B runs: -0.7 % and +0.2 %), with fewer registers and no
+// LDS stores issued by the waves.
+constexpr int kWgradRowsDefaultForm = 2;
 std::atomic<int> g_wgrad_rows_form{[] {
   const char* e = std::getenv("XDNA_WGRAD_KERNEL");
-  return e && std::atoi(e) == 2 ? 2 : 1;
+  const int f = e ? std::atoi(e) : 0;
+  return f == 1 || f == 2 ? f : kWgradRowsDefaultForm;
 }()};
 
 struct WgRowsPlan {
@@ -2322,7 +2296,7 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   p.co_chunks = int(ceil_div(Cout, kKStep));
   p.ci_pad = p.ci_chunks * kKStep;
   p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
-  p.form = g_wgrad_rows_form.load() == 2 ? 2 : 1;
+  p.form = g_wgrad_rows_form.load();
   p.kt_rows = p.form == 2 ? kW5Kt : g_wgrad_rows_kt.load() == 128 ? 128 : 64;
   p.ktiles = int(ceil_div(p.geom.m_total, p.kt_rows));
   const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
@@ -2664,13 +2638,13 @@ int xdna_conv3x3_set_wgrad_rows_kernel(int form) {
     set_error("xdna_conv3x3_set_wgrad_rows_kernel: form must be 0 (default), 1 or 2");
     return -1;
   }
-  g_wgrad_rows_form.store(form == 2 ? 2 : 1);
+  g_wgrad_rows_form.store(form == 0 ? kWgradRowsDefaultForm : form);
   return 0;
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {
   if (variant < 0 || variant > 9) {
-    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..8");
+    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..9");
     return -1;
   }
   g_rows_variant.store(variant);

@@ -753,13 +753,12 @@ bool launch2(dim3 grid, hipStream_t st, const GemmArgs& g) {
 constexpr int kK5 = 32, kNB5 = 4;
 constexpr int kTile5 = kT4 * kK5;                          // elements of one operand's k-tile
 constexpr size_t kGemm5Lds = size_t(kNB5) * 2 * kTile5 * 2;  // 4 buffers x (A, B): 128 KB
-typedef __attribute__((address_space(3))) void g5_lds;
 
 // One operand's DMA plan: per thread 4 loads of 16 bytes per k-tile (blocks 4 w + i of
 // 1 KB, w the wave).  roff: the row part of the element offset (-1: rows past the
 // operand), kq: the k offset within the k-tile.
 struct G5Operand {
-  __amdgpu_buffer_rsrc_t rs;
+  i32x4_t rs;
   int roff[4];
   int kq[4];
   int s_k;
@@ -770,7 +769,7 @@ __device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t
                                        int tid) {
   G5Operand o;
   const int64_t extent = ((int64_t(rows) - 1) * s_r + (int64_t(K) - 1) * s_k + 1) * 2;
-  o.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), 0, int(extent), 0x00020000);
+  o.rs = lds_dma_rsrc(src, int(extent));
   o.s_k = int(s_k);
   const int lane = tid & 63, w = tid >> 6;
 #pragma unroll
@@ -800,7 +799,7 @@ __device__ inline void g5_load(uint16_t* tile, const G5Operand& o, int k0, int K
     const int k = k0 + o.kq[i];
     const bool ok = o.roff[i] >= 0 && k < K;
     const int off = ok ? (o.roff[i] + k * o.s_k) * 2 : 0x7FFFFFF0;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rs, (g5_lds*)(tile + (4 * w + i) * 512), 16, off, 0, 0, 0);
+    lds_dma16(o.rs, tile + (4 * w + i) * 512, off);
   }
 }
 
@@ -826,12 +825,6 @@ __device__ inline u32x4_t g5_frag(const uint16_t* tile, int rb, int ks, int lane
   return u32x4_t{a[0], a[1], b[0], b[1]};
 }
 
-// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
-template <int n>
-__device__ inline void g5_wait_vm() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 template <int kModeA, int kModeB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -885,7 +878,7 @@ void gemm5_kernel(GemmArgs g) {
     // static); wait for k-tile 0's
 #pragma unroll
     for (int t = 0; t < kNB5; ++t) XDNA_G5_LOAD(t);
-    g5_wait_vm<8 * (kNB5 - 1)>();
+    lds_dma_wait<8 * (kNB5 - 1)>();
     __builtin_amdgcn_s_barrier();
     XDNA_G5_FRAGS(0, 0, 0);
     constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100;
@@ -903,8 +896,8 @@ void gemm5_kernel(GemmArgs g) {
       // this wave's reads of buffer t are complete, and its loads of k-tile t+1 (two
       // k-tiles, 16 loads, may stay in flight); the barrier makes k-tile t+1 visible and
       // buffer t free
-      __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8) | 15 | (3 << 14));  // lgkmcnt(0) only
-      g5_wait_vm<8 * (kNB5 - 2)>();
+      lds_reads_wait();
+      lds_dma_wait<8 * (kNB5 - 2)>();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       XDNA_G5_LOAD(t + kNB5);              // into buffer t % kNB5
@@ -919,7 +912,7 @@ void gemm5_kernel(GemmArgs g) {
       __builtin_amdgcn_sched_barrier(0);
     }
     // drain the clamped loads issued past the end before the workgroup can exit
-    g5_wait_vm<0>();
+    lds_dma_wait<0>();
 #undef XDNA_G5_LOAD
 #undef XDNA_G5_FRAGS
 #undef XDNA_G5_MFMA
@@ -1106,10 +1099,10 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   // config 3's GEMMs (even there, ahead of the eight-wave kernel from K = 4096).
   const bool big = tiles2 >= 64 || K >= 16384;
   const bool use4 = fits4 && g.rs_ok && (variant == 3 || variant == 4 || (variant == 0 && big && K >= 1024));
-  // the direct-to-LDS form where both operands are k-contiguous (measured 3-10 % ahead of
-  // the register-staged one on config 3's forward products; behind it when a transposing
-  // read is involved)
-  const bool use5 = use4 && (variant == 4 || (variant == 0 && ma == kAlongK && mb == kAlongK));
+  // the direct-to-LDS form for every operand layout (config 3's nine products: 1441 against
+  // 1502 us for the register-staged form, 1-7 % ahead on each, same bits); variant 3 keeps
+  // the register-staged one
+  const bool use5 = use4 && (variant == 4 || variant == 0);
   if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && big))) {
     // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
     const int kt2 = int(ceil_div(K, kK2));

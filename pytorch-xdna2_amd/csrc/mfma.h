@@ -30,6 +30,48 @@ __device__ inline bf16x8_t as_bf16x8(const u32x4_t& u) { return __builtin_bit_ca
 // Row (within a 32x32 tile) of accumulator register i for lane l.
 __device__ inline int mfma_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
+// ---------------------------------------------------------------------------------------
+// gfx950's 16-byte LDS DMA (buffer_load_dwordx4 ... lds): one instruction per wave writes
+// 64 x 16 bytes contiguously at an LDS base (lane L at base + 16 L; a lane whose offset is
+// past the buffer's range writes zeros), with no register staging and no LDS store.
+// ---------------------------------------------------------------------------------------
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource of `bytes` bytes at `base`: stride 0 (offsets in bytes), the dword-3
+// flags of __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000).
+__device__ inline i32x4_t lds_dma_rsrc(const void* base, int bytes) {
+  const uint64_t b = uint64_t(base);
+  return i32x4_t{int(uint32_t(b)), int(uint32_t(b >> 32) & 0xFFFF), bytes, 0x00020000};
+}
+
+// One 16-byte LDS DMA of byte offset voff of the resource into lds + 16 L (the LDS base
+// and the resource are wave-uniform: lane 0's are used).  Issued from
+// inline assembly on purpose: for the compiler's builtin, its wait insertion makes every
+// later LDS read wait for all outstanding DMA (vmcnt(0)) whatever the read's address, which
+// serializes a multi-buffered pipeline.  The caller tracks completion with counted
+// s_waitcnt vmcnt (lds_dma_wait) before the barrier that publishes a buffer.  M0 (the LDS
+// base) is set inside the statement; kernels that use this helper use M0 for nothing else.
+__device__ inline void lds_dma16(const i32x4_t& rsrc, const uint16_t* lds, int voff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      uint32_t(uintptr_t((__attribute__((address_space(3))) const uint16_t*)lds)));
+  const i32x4_t rs = {__builtin_amdgcn_readfirstlane(rsrc[0]), __builtin_amdgcn_readfirstlane(rsrc[1]),
+                      __builtin_amdgcn_readfirstlane(rsrc[2]), __builtin_amdgcn_readfirstlane(rsrc[3])};
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rs)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
+template <int n>
+__device__ inline void lds_dma_wait() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// s_waitcnt lgkmcnt(0) alone: this wave's LDS reads have returned
+__device__ inline void lds_reads_wait() { __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8) | 15 | (3 << 14)); }
+
 __device__ inline f32x16_t zero_acc() {
   f32x16_t z;
 #pragma unroll

@@ -88,10 +88,22 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
 // for every strip of those rows.  Phase 1: each item is (source pixel, 8-channel piece);
 // consecutive threads take consecutive pixels, so each of the 8 channel loads of a wave
 // reads a contiguous run of NCHW, and the 8 values land in LDS as one 16-byte write
-// ([pixel][64 channels], pitch kLdsPitch).  Phase 2: consecutive threads take consecutive
+// ([pixel][64 channels], see tile_piece).  Phase 2: consecutive threads take consecutive
 // 16-byte pieces of packed rows, so a wave store covers 8 whole rows (1 KB contiguous).
-constexpr int kLdsPitch = 72;      // elements per staged pixel (64 + 8: 16-byte aligned rows)
-constexpr int kMaxTilePix = 256;   // pixels per workgroup (LDS 36 KiB: four workgroups per CU)
+constexpr int kLdsPitch = 64;      // elements per staged pixel (unpadded: pieces permuted)
+
+// Element offset of 16-byte piece q (channels 8q .. 8q + 7) of staged pixel pix: pieces sit
+// at position q ^ ((pix >> S) & 7) of the pixel's 128 bytes, S = log2 of the pixels per
+// phase-1 item.  A 16-lane pass of 16-byte LDS accesses covers 64 banks as 16 slots of 4:
+// pixel pix's position lands in slot 8 (pix % 2) + position.  Phase-1 writes (lane t at
+// pixel VP t + i, one piece) then use 8 slots (2-way; 16 with VP = 1), where the padded
+// 72-element pitch put 16 lanes on 4 slots; phase-2 reads (8 lanes per pixel, pixels
+// x and x + 1) use all 16.
+template <int S>
+__device__ inline int tile_piece(int pix, int q) {
+  return pix * kLdsPitch + ((q ^ ((pix >> S) & 7)) << 3);
+}
+constexpr int kMaxTilePix = 256;   // pixels per workgroup (LDS 32 KiB: four workgroups per CU)
 
 // Writes the 16-byte piece q of packed row p (main copy and, for the first 78 rows of a
 // group, the halo copy at the end of the previous group), when p is in [plo, phi).
@@ -119,6 +131,7 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
     int So, int Wg, int wp, int lead, int halo_zero, int chunks, int g0, int ng, int b0, int64_t plo,
     int64_t phi, int R, int ybl, int nimg, int64_t tail0) {
   extern __shared__ __attribute__((aligned(16))) uint16_t tile[];
+  constexpr int kVpShift = VP == 4 ? 2 : VP == 2 ? 1 : 0;
   int bid = blockIdx.x;
   if (kDense && bid >= nimg) {
     // rows [tail0, phi) hold no image: zeros for every chunk
@@ -181,9 +194,8 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
                          : ((i & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
                                     : __builtin_amdgcn_perm(b, a, 0x05040100u));
         }
-        uint4* tp = reinterpret_cast<uint4*>(tile + (pix0 + i) * kLdsPitch + seg * 16);
-        tp[0] = make_uint4(o[0], o[1], o[2], o[3]);
-        tp[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        *reinterpret_cast<uint4*>(tile + tile_piece<kVpShift>(pix0 + i, 2 * seg)) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(tile + tile_piece<kVpShift>(pix0 + i, 2 * seg + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
       }
     }
   }
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
       const bool zero_col = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
       uint4 v = make_uint4(0, 0, 0, 0);
       if (gy >= 1 && gy <= H && j >= 0 && j < Wg && x >= 0 && x < W && !zero_col && q * 8 < cc)
-        v = *reinterpret_cast<const uint4*>(tile + ((gy - 1 - y0) * W + x) * kLdsPitch + q * 8);
+        v = *reinterpret_cast<const uint4*>(tile + tile_piece<kVpShift>((gy - 1 - y0) * W + x, q));
       const int64_t p = ((int64_t(b) * S + s) * (H + 2) + gy) * wp + gx;
       put_row_piece(dst, p, q, v, chunks, chunk, g0, ng, plo, phi);
     }
@@ -233,7 +245,7 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
     const bool main_w = g >= g0 && g < int64_t(g0) + ng;
     const bool halo_w = g > g0 && g <= int64_t(g0) + ng && r + kGroupOutRows < kGroupRows;
     const bool zero = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
-    const uint16_t* tp = tile + (yy * W + x) * kLdsPitch + q * 8;
+    const uint16_t* tp = tile + tile_piece<kVpShift>(yy * W + x, q);
     const bool full = (q + 1) * 8 <= cc;
     uint4 v = make_uint4(0, 0, 0, 0);
     if (!zero) v = *reinterpret_cast<const uint4*>(tp);
