@@ -792,15 +792,16 @@ __device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t
   return o;
 }
 
+// Byte offset of DMA load i of k-tile k0 .. k0 + 31 (masked past K: out of range).
+__device__ inline int g5_off(const G5Operand& o, int i, int k0, int K) {
+  const int k = k0 + o.kq[i];
+  return o.roff[i] >= 0 && k < K ? (o.roff[i] + k * o.s_k) * 2 : 0x7FFFFFF0;
+}
+
 // The 4 DMA loads of k-tile k0 .. k0 + 31 (clamped, masked past K) into `tile`.
 __device__ inline void g5_load(uint16_t* tile, const G5Operand& o, int k0, int K, int w) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int k = k0 + o.kq[i];
-    const bool ok = o.roff[i] >= 0 && k < K;
-    const int off = ok ? (o.roff[i] + k * o.s_k) * 2 : 0x7FFFFFF0;
-    lds_dma16(o.rs, tile + (4 * w + i) * 512, off);
-  }
+  for (int i = 0; i < 4; ++i) lds_dma16(o.rs, tile + (4 * w + i) * 512, g5_off(o, i, k0, K));
 }
 
 // MFMA fragment (rows rb + lane % 32, k = 16 ks + 8 (lane / 32) .. +8) from a k-tile.
@@ -884,6 +885,15 @@ void gemm5_kernel(GemmArgs g) {
     constexpr int kMfma = 0x008, kVmemRd = 0x020, kDsRd = 0x100;
     constexpr int kRd = (kModeA == kAlongK ? 4 : 8) + (kModeB == kAlongK ? 4 : 8);
     for (int t = 0; t < ntiles; ++t) {
+      // offsets of the DMA of k-tile t + kNB5 (computed among the first k-step's MFMAs,
+      // issued after the barrier)
+      const int kn = kbeg + min(t + kNB5, ntiles - 1) * kK5;
+      int dofs[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dofs[i] = g5_off(oa, i, kn, kend);
+        dofs[4 + i] = g5_off(ob, i, kn, kend);
+      }
       // k-step 0 of k-tile t: k-step 1's fragments are read meanwhile
       XDNA_G5_FRAGS(1, t, 1);
       XDNA_G5_MFMA(0);
@@ -900,16 +910,25 @@ void gemm5_kernel(GemmArgs g) {
       lds_dma_wait<8 * (kNB5 - 2)>();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      XDNA_G5_LOAD(t + kNB5);              // into buffer t % kNB5
-      XDNA_G5_FRAGS(0, t + 1, 0);          // k-tile t+1 (past the end: never used)
-      XDNA_G5_MFMA(1);
+      // k-step 1 of k-tile t in 8 slices of two MFMAs, each slice also issuing one DMA of
+      // k-tile t + kNB5 (into buffer t % kNB5) and one fragment of k-tile t + 1, k-step 0
+      // (past the end: never used); the slices are fenced so that the DMA, which the
+      // scheduler cannot group, spreads over the MFMAs instead of delaying the first one
+      uint16_t* const nbuf = tbuf(t + kNB5);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        if (i < 8) __builtin_amdgcn_sched_group_barrier(kVmemRd, 1, 0);
-        if (i < kRd) __builtin_amdgcn_sched_group_barrier(kDsRd, 1, 0);
+      for (int sl = 0; sl < 8; ++sl) {
+        const int i = sl >> 1, j0 = 2 * (sl & 1);
+        acc[i][j0] = mfma_32x32x16(as_bf16x8(fa[1][i]), as_bf16x8(fb[1][j0]), acc[i][j0]);
+        acc[i][j0 + 1] = mfma_32x32x16(as_bf16x8(fa[1][i]), as_bf16x8(fb[1][j0 + 1]), acc[i][j0 + 1]);
+        if (sl < 4) {
+          lds_dma16(oa.rs, nbuf + (4 * wave + sl) * 512, dofs[sl]);
+          fa[0][sl] = g5_frag<kModeA>(tbuf(t + 1), wm * 128 + sl * 32, 0, lane);
+        } else {
+          lds_dma16(ob.rs, nbuf + kTile5 + (4 * wave + sl - 4) * 512, dofs[sl]);
+          fb[0][sl - 4] = g5_frag<kModeB>(tbuf(t + 1) + kTile5, wn * 128 + (sl - 4) * 32, 0, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     // drain the clamped loads issued past the end before the workgroup can exit
     lds_dma_wait<0>();

@@ -59,7 +59,7 @@ __device__ inline void lds_dma16(const i32x4_t& rsrc, const uint16_t* lds, int v
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(m0), "v"(voff), "s"(rs)
-               : "memory", "m0");
+               : "m0");
 }
 
 // s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
