@@ -2121,15 +2121,23 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
     const int xq = (lane & 7) ^ (4 * ((lane >> 4) & 1));
     const int xoff0 = (8 * xb0 + (lane >> 3)) * 128 + xq * 16;  // bytes, + 1 KiB per block
 
-    // k-tile tl of the split (clamped to the last: the load count stays static) into
-    // buffer tl % kW5Nb
-    auto load = [&](int tl) {
+    // DMA of k-tile tl of the split (clamped to the last: the load count stays static) into
+    // buffer tl % kW5Nb: its resources and offsets (plan), then its loads (issue_dy,
+    // issue_x), so that the address arithmetic can run before the barrier that frees the
+    // buffer and the loads after it
+    struct DmaPlan {
+      i32x4_t drs, xrs;
+      int doff[2];
+      const uint16_t* buf;
+    };
+    auto plan = [&](int tl) {
+      DmaPlan p;
       const int kt = kt0 + min(tl, ntl - 1);
-      uint16_t* buf = smem + (tl & (kW5Nb - 1)) * kW5Buf;
+      p.buf = smem + (tl & (kW5Nb - 1)) * kW5Buf;
       const int g = kt / kTilesPerGroup, r0 = (kt % kTilesPerGroup) * kW5Kt;
       const uint16_t* dbase =
           a.dp + ((int64_t(g) * a.co_chunks + co0 / 64) * kGroupRows + r0 + a.wp + 1) * kKStep;
-      const i32x4_t drs = lds_dma_rsrc(dbase, dext);
+      p.drs = lds_dma_rsrc(dbase, dext);
       const int64_t rem = a.m_total - int64_t(kt) * kW5Kt;  // rows of this k-tile before the end
       const int base = int((uint32_t(kt) * uint32_t(kW5Kt)) % uint32_t(a.wp));
 #pragma unroll
@@ -2142,15 +2150,26 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
         dj = dj == a.wp ? 0 : dj;
         const bool halo = strips && (dj == 0 || dj == a.Wg - 1);
         const bool ok = dchunk_ok && drow[i] < rem && !halo;
-        const int off = ok ? doff0 + drow[i] * 128 : 0x7FFFFFF0;
-        lds_dma16(drs, buf + (2 * wave + i) * 512, off);
+        p.doff[i] = ok ? doff0 + drow[i] * 128 : 0x7FFFFFF0;
       }
       const uint16_t* xbase = a.xp + ((int64_t(g) * a.ci_chunks + ci0 / 64) * kGroupRows + r0) * kKStep;
-      const i32x4_t xrs = lds_dma_rsrc(xbase, (kGroupRows - r0) * 128);
-      const uint16_t* xl = buf + kW5Kt * 128 + xb0 * 512;
-      lds_dma16(xrs, xl, xoff0);
-      lds_dma16(xrs, xl + 512, xoff0 + 1024);
-      if (wave < 4) lds_dma16(xrs, xl + 1024, xoff0 + 2048);
+      p.xrs = lds_dma_rsrc(xbase, (kGroupRows - r0) * 128);
+      return p;
+    };
+    auto issue_dy = [&](const DmaPlan& p) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) lds_dma16(p.drs, p.buf + (2 * wave + i) * 512, p.doff[i]);
+    };
+    auto issue_x = [&](const DmaPlan& p) {
+      const uint16_t* xl = p.buf + kW5Kt * 128 + xb0 * 512;
+      lds_dma16(p.xrs, xl, xoff0);
+      lds_dma16(p.xrs, xl + 512, xoff0 + 1024);
+      if (wave < 4) lds_dma16(p.xrs, xl + 1024, xoff0 + 2048);
+    };
+    auto load = [&](int tl) {
+      const DmaPlan p = plan(tl);
+      issue_dy(p);
+      issue_x(p);
     };
     // this wave's loads of the oldest k-tile in flight have landed, n k-tiles' may stay
     // in flight
@@ -2177,25 +2196,30 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
     }
     // k-step ks of a buffer: rows 16 ks .. +15 (the row bits the permutations use are
     // those of the lane part: 16 ks and 4 q leave bits 0 and 1 of a row alone)
-    auto frags = [&](W5Frags& f, const uint16_t* buf, int ks) {
+    auto frag_a = [&](W5Frags& f, const uint16_t* buf, int ks) {
       const uint2 lo = wr_tr(buf + a_off + ks * 16 * 128);
       const uint2 hi = wr_tr(buf + a_off + (ks * 16 + 4) * 128);
       f.a = u32x4_t{lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-      for (int dy = 0; dy < 3; ++dy)
-#pragma unroll
-        for (int q = 0; q < 3; ++q) f.x[dy][q] = wr_tr(buf + x_off[dy] + (ks * 16 + 4 * q) * 64);
     };
-    auto mfmas = [&](const W5Frags& f, auto bias_tag) {
+    auto frag_x = [&](W5Frags& f, const uint16_t* buf, int ks, int dy) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) f.x[dy][q] = wr_tr(buf + x_off[dy] + (ks * 16 + 4 * q) * 64);
+    };
+    auto frags = [&](W5Frags& f, const uint16_t* buf, int ks) {
+      frag_a(f, buf, ks);
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy) frag_x(f, buf, ks, dy);
+    };
+    // the three MFMAs of kernel row dy (dx = 0, 1, 2); the bias sums go with dy = 0
+    auto mfma_dy = [&](const W5Frags& f, int dy, auto bias_tag) {
       constexpr bool kBias = decltype(bias_tag)::value;
-      if (kBias) {
+      if (kBias && dy == 0) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           bsum += __uint_as_float(f.a[e] << 16) + __uint_as_float(f.a[e] & 0xFFFF0000u);
       }
       const bf16x8_t af = as_bf16x8(f.a);
-#pragma unroll
-      for (int dy = 0; dy < 3; ++dy) {
+      {
         const uint2 r0 = f.x[dy][0], r1 = f.x[dy][1], r2 = f.x[dy][2];
         const u32x4_t l = {r0.x, r0.y, r1.x, r1.y};
         u32x4_t s1, s2;
@@ -2212,6 +2236,20 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
         acc[dy * 3 + 2] = mfma_32x32x16(af, as_bf16x8(s2), acc[dy * 3 + 2]);
       }
     };
+    // one k-step (fragments fc) while the next k-step's fragments (fn: buffer nb, k-step
+    // nks) are read, in three fenced slices: kernel row dy's reads among its MFMAs
+    auto step = [&](W5Frags& fn, const uint16_t* nb, int nks, const W5Frags& fc, auto bias_tag) {
+      frag_a(fn, nb, nks);
+      frag_x(fn, nb, nks, 0);
+      mfma_dy(fc, 0, bias_tag);
+      __builtin_amdgcn_sched_barrier(0);
+      frag_x(fn, nb, nks, 1);
+      mfma_dy(fc, 1, bias_tag);
+      __builtin_amdgcn_sched_barrier(0);
+      frag_x(fn, nb, nks, 2);
+      mfma_dy(fc, 2, bias_tag);
+      __builtin_amdgcn_sched_barrier(0);
+    };
 
     // the k-tile loop, instantiated with and without the bias sums (a wave-uniform choice
     // outside the loop)
@@ -2224,21 +2262,35 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
       frags(f0, smem, 0);
       for (int tl = 0; tl < ntl; ++tl) {
         const uint16_t* buf = smem + (tl & (kW5Nb - 1)) * kW5Buf;
-        frags(f1, buf, 1);
-        mfmas(f0, bias_tag);
-        frags(f0, buf, 2);
-        mfmas(f1, bias_tag);
-        frags(f1, buf, 3);
-        mfmas(f0, bias_tag);
+        step(f1, buf, 1, f0, bias_tag);
+        step(f0, buf, 2, f1, bias_tag);
+        step(f1, buf, 3, f0, bias_tag);
+        // the address arithmetic of k-tile tl + kW5Nb's DMA, before the barrier
+        const DmaPlan p = plan(tl + kW5Nb);
+        __builtin_amdgcn_sched_barrier(0);
         // this wave's reads of the buffer are complete and its loads of k-tile tl + 1 have
         // landed (two k-tiles of loads may stay in flight); the barrier publishes every
         // wave's and frees the buffer for k-tile tl + kW5Nb
         lds_reads_wait();
         wait_tiles(std::integral_constant<int, kW5Nb - 2>{});
         __builtin_amdgcn_s_barrier();
-        load(tl + kW5Nb);
-        frags(f0, smem + ((tl + 1) & (kW5Nb - 1)) * kW5Buf, 0);  // past the end: never used
-        mfmas(f1, bias_tag);
+        __builtin_amdgcn_sched_barrier(0);
+        // k-step 3 in three fenced slices (one kernel row each), each also issuing part of
+        // k-tile tl + 1's first fragments (past the end: never used) and of the DMA into
+        // the freed buffer, so that the MFMAs start right after the barrier
+        const uint16_t* nbuf = smem + ((tl + 1) & (kW5Nb - 1)) * kW5Buf;
+        frag_a(f0, nbuf, 0);
+        frag_x(f0, nbuf, 0, 0);
+        mfma_dy(f1, 0, bias_tag);
+        issue_dy(p);
+        __builtin_amdgcn_sched_barrier(0);
+        frag_x(f0, nbuf, 0, 1);
+        mfma_dy(f1, 1, bias_tag);
+        issue_x(p);
+        __builtin_amdgcn_sched_barrier(0);
+        frag_x(f0, nbuf, 0, 2);
+        mfma_dy(f1, 2, bias_tag);
+        __builtin_amdgcn_sched_barrier(0);
       }
       // drain the clamped loads issued past the end before the workgroup can exit
       lds_dma_wait<0>();
@@ -2270,9 +2322,8 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
 // Kernel of the rows weight gradient: 1 register-staged k-tiles (wgrad_rows_kernel), 2
 // k-tiles loaded straight into LDS (wgrad_rows5_kernel); XDNA_WGRAD_KERNEL at start-up,
 // xdna_conv3x3_set_wgrad_rows_kernel.
-// The default, form 2: level with form 1 over the sweep's 36 shapes (GPU time per shape's
-// fwd + dgrad + wgrad step, two A/B runs: -0.7 % and +0.2 %), with fewer registers and no
-// LDS stores issued by the waves.
+// The default, form 2: 2.2 % ahead of form 1 over the sweep's 36 shapes (GPU time per
+// shape's fwd + dgrad + wgrad step), 3 % on the largest ones.
 constexpr int kWgradRowsDefaultForm = 2;
 std::atomic<int> g_wgrad_rows_form{[] {
   const char* e = std::getenv("XDNA_WGRAD_KERNEL");
