@@ -410,9 +410,12 @@ int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uin
  * 1 the 128 x 128 kernel (any strides, split-K for few long-K tiles), 2 the 256 x 256
  * kernel (8 waves; operands with a unit stride along k or along rows only, else 1 is
  * used), 3 its four-wave form (one wave per SIMD with 128 x 128 wave tiles, software-
- * pipelined; also needs K % 8 == 0 and rows % 8 == 0 for row-contiguous operands, else 2
- * or 1; the automatic choice where it applies).  No reference counterpart (a tuning
- * knob).  XDNA_GEMM_VARIANT sets the initial value. */
+ * pipelined, operands staged through registers; also needs K % 8 == 0 and rows % 8 == 0
+ * for row-contiguous operands, else 2 or 1), 4 the four-wave kernel with operands loaded
+ * straight into LDS (32x32x16 MFMAs; same conditions), 5 that kernel with 16x16x32 MFMAs
+ * for k-contiguous operand pairs (4 for other layouts).  Automatic: 5 where it applies,
+ * else 4, on large grids or long K.  No reference counterpart (a tuning knob).
+ * XDNA_GEMM_VARIANT sets the initial value. */
 int xdna_gemm_set_variant(int variant);
 
 /* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot

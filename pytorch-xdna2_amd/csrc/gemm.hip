@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include "../../include/xdna_hip.h"
 
 namespace xdna {
@@ -939,6 +940,234 @@ void gemm5_kernel(GemmArgs g) {
   store_block<4, 4>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
 }
 
+// ---------------------------------------------------------------------------------------
+// gemm5's tile, DMA plan and LDS layout with v_mfma_f32_16x16x32_bf16 (k-contiguous operands).
+// The MFMA-bound kernels run at the board's power limit, and the 16x16x32 form costs less
+// energy per flop: one wave per SIMD issuing independent MFMAs on random bf16 operands
+// sustains 2156 TFLOP/s against 1772 for 32x32x16, and this kernel runs at 2.08 GHz where
+// gemm5_kernel runs at 1.79 (counters on config 3's M 8192, N 4096, K 4096 product).  Its
+// MFMAs last 16 cycles instead of 32, so every LDS read and DMA is issued after a single
+// MFMA: behind a group of MFMAs the same instructions left the pipe idle (44.6 % busy,
+// 283.9 us; interleaved one by one, 234.9 us against gemm5's 264.6).
+// A fragment (16 rows x 32 k): lane l holds row l % 16, k 8 (l / 16) .. +7, one 16-byte LDS
+// read (rows r and pieces l / 16 of the permuted [256][4 pieces] tile: the 16 lanes of a
+// pass cover 16 distinct bank slots).  D (16 x 16, 4 fp32 per lane): register i of lane l
+// holds D[4 (l / 16) + i][l % 16].  A wave's 128 x 128 is 8 x 8 tiles (64 MFMAs per 32-k
+// k-tile, 64 x 4 accumulator registers).  Per k-tile: the first half of its MFMAs, then the
+// wait and barrier that publish the next k-tile and free this one's buffer, then the second
+// half with the next k-tile's DMA and fragment reads in fenced slices.
+// ---------------------------------------------------------------------------------------
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// The MFMA as an inline-assembly statement on an AGPR quad updated in place: with 64
+// accumulators filling the 256 AGPRs, the compiler's allocation of the builtin's results
+// renames them through v_accvgpr copies every k-tile.  The compiler then does not see an
+// MFMA, so the hazards it would pad are padded by the kernel (mfma16_fence): wait states
+// between the last MFMA writing an accumulator and any other read of it (VALU, stores), and
+// between VALU writes of an accumulator (its zero init) and the first MFMA reading it.
+// Operands A and B come from LDS reads, whose completion the compiler's s_waitcnt covers
+// for inline-assembly operands as for any instruction; each accumulator is updated once
+// per 64 MFMAs, so no MFMA reads a result of the MFMA just before it.
+// kInit: the first k-tile's MFMA, accumulating onto the inline constant 0 (no zero-filled
+// accumulators to set up)
+template <bool kInit>
+__device__ inline void mfma16_acc(f32x4_t& c, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (kInit)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// 24 wait states (the longest MFMA dependency in the gfx9 family needs 19), then every
+// accumulator of an 8 x 8 set passed through volatile statements, so that no read or
+// MFMA of them can be scheduled before the wait states
+__device__ inline void mfma16_fence(f32x4_t (&acc)[8][8]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    asm volatile("; mfma16 fence"
+                 : "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3]), "+a"(acc[i][4]),
+                   "+a"(acc[i][5]), "+a"(acc[i][6]), "+a"(acc[i][7]));
+}
+
+// epilogue of 16 x 16 tiles: rows mb + i*16 + 4 (lane / 16) + r, columns nb + j*16 + lane % 16
+template <int MI, int NJ>
+__device__ inline void store_block16(const GemmArgs& g, int batch, int split, const f32x4_t (&acc)[MI][NJ],
+                                     int mb, int nb, int lane) {
+  const int lc = lane & 15, lq = lane >> 4;
+  if (g.part) {
+    float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
+    const auto prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, g.part_bytes, 0x00020000);
+    int noff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = nb + j * 16 + lc;
+      noff[j] = n < g.N ? n * 4 : kSkip;
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = mb + i * 16 + 4 * lq + r;
+        const int moff = m < g.M ? m * g.N * 4 : kSkip;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), prs, moff + noff[j], 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    return;
+  }
+  const auto crs = __builtin_amdgcn_make_buffer_rsrc(g.c + int64_t(batch) * g.c_batch, 0, g.c_bytes, 0x00020000);
+  const bool bias = g.bias_mode != 0 && g.beta != 0.0f;
+  const auto brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.bias), 0, bias ? g.bias_bytes : 0,
+                                                     0x00020000);
+  int noff[NJ], nbo[NJ];
+  float bn[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = nb + j * 16 + lc;
+    noff[j] = n < g.N ? int(n * g.c_n * 2) : kSkip;
+    nbo[j] = n < g.N ? int(n * g.bias_sn * 2) : kSkip;
+    bn[j] = bias && g.bias_mode == 1 ? bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, nbo[j], 0, 0)) : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mb + i * 16 + 4 * lq + r;
+      const bool mok = m < g.M;
+      const int moff = mok ? int(m * g.c_m * 2) : kSkip;
+      const int mbo = mok ? int(m * g.bias_sm * 2) : kSkip;
+      float bm = 0.0f;
+      if (bias && g.bias_mode == 3) bm = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, mbo, 0, 0));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        float v = g.alpha * acc[i][j][r];
+        if (bias) {
+          float bv = g.bias_mode == 1 ? bn[j] : bm;
+          if (g.bias_mode == 2) bv = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, mbo + nbo[j], 0, 0));
+          v += g.beta * bv;
+        }
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), crs, moff + noff[j], 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// 16 x 32 fragment of a k-contiguous [256][4 pieces] k-tile: rows rb + lane % 16, piece lane / 16
+__device__ inline u32x4_t g6_frag(const uint16_t* tile, int rb, int lane) {
+  const int r = rb + (lane & 15);
+  const int c = (lane >> 4) ^ ((r >> 2) & 3);
+  return *reinterpret_cast<const u32x4_t*>(tile + (r * 4 + c) * 8);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm6_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  int tbx, tby;
+  gemm_tile_xy(g, tbx, tby);
+  const int m0 = tby * kT4, n0 = tbx * kT4;
+  const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
+  const int kbeg = split * g.kt_per * kK4, kend = min(g.K, kbeg + g.kt_per * kK4);
+  // an empty split still runs one k-tile: every load past kend is masked to zeros
+  const int ntiles = kend > kbeg ? (kend - kbeg + kK5 - 1) / kK5 : 1;
+  const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
+  const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
+
+  f32x4_t acc[8][8];
+  {
+    // one fragment set, each fragment read again for the next k-tile after its last MFMA
+    // of this one: rows 0..3 of A and the B columns during the second half, rows 4..7 of A
+    // during the next first half.  Both halves run column by column, so a fragment is read
+    // at least 16 MFMAs before its first use.
+    u32x4_t fa[8], fb[8];
+    const G5Operand oa = g5_operand<kAlongK>(A, g.a_r, g.a_k, m0, g.M, g.K, tid);
+    const G5Operand ob = g5_operand<kAlongK>(B, g.b_r, g.b_k, n0, g.N, g.K, tid);
+    auto tbuf = [&](int t) { return smem + (t & (kNB5 - 1)) * 2 * kTile5; };
+    auto load = [&](int t) {
+      const int k_ = kbeg + min(t, ntiles - 1) * kK5;
+      g5_load(tbuf(t), oa, k_, kend, wave);
+      g5_load(tbuf(t) + kTile5, ob, k_, kend, wave);
+    };
+#pragma unroll
+    for (int t = 0; t < kNB5; ++t) load(t);
+    lds_dma_wait<8 * (kNB5 - 1)>();
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = g6_frag(tbuf(0), wm * 128 + i * 16, lane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fb[j] = g6_frag(tbuf(0) + kTile5, wn * 128 + j * 16, lane);
+    // wave-uniform DMA state: resources and the LDS byte address of this wave's first
+    // destination block (the loop adds buffer and block offsets as scalar arithmetic)
+    const i32x4_t rsa = uniform_rsrc(oa.rs), rsb = uniform_rsrc(ob.rs);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds_w = lds_addr(smem) + uint32_t(4 * wave_u * 512 * 2);
+    // k-tile t (kFirst: t == 0, whose MFMAs start the accumulators).  A 16x16x32 MFMA
+    // occupies the matrix pipe for 16 cycles, so every LDS read and DMA is issued right
+    // after one MFMA (never several after a group): the wave issues them while that MFMA
+    // runs and the next MFMA is not held back.
+    auto ktile = [&](int t, auto first) {
+      constexpr bool kFirst = decltype(first)::value;
+      // k of the DMA loads (k-tile t + kNB5): their offsets are formed in the second half
+      const int kn = kbeg + min(t + kNB5, ntiles - 1) * kK5;
+      const uint32_t m0n = lds_w + uint32_t(((t + kNB5) & (kNB5 - 1)) * 2 * kTile5 * 2);
+      // first half (A rows 0..3) column by column; A rows 4..7 of this k-tile are read
+      // after the second MFMA of columns 0..3
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          mfma16_acc<kFirst>(acc[i][j], fa[i], fb[j]);
+          if (i == 1 && j < 4) fa[4 + j] = g6_frag(tbuf(t), wm * 128 + (4 + j) * 16, lane);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      // this wave's reads of buffer t are complete and its loads of k-tile t+1 have landed
+      // (two k-tiles of loads may stay in flight): the barrier publishes k-tile t+1 and
+      // frees buffer t
+      lds_reads_wait();
+      lds_dma_wait<8 * (kNB5 - 2)>();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // second half (A rows 4..7) column by column: DMA j of k-tile t+kNB5 after the
+      // column's first MFMA, k-tile t+1's A row j (j < 4) after its second, its B column j
+      // after the last (the last use of this k-tile's B column j)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mfma16_acc<kFirst>(acc[4][j], fa[4], fb[j]);
+        if (j < 4)
+          lds_dma16_m0(rsa, m0n + uint32_t(j * 512 * 2), g5_off(oa, j, kn, kend));
+        else
+          lds_dma16_m0(rsb, m0n + uint32_t((kTile5 + (j - 4) * 512) * 2), g5_off(ob, j - 4, kn, kend));
+        __builtin_amdgcn_sched_barrier(0);
+        mfma16_acc<kFirst>(acc[5][j], fa[5], fb[j]);
+        if (j < 4) fa[j] = g6_frag(tbuf(t + 1), wm * 128 + j * 16, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma16_acc<kFirst>(acc[6][j], fa[6], fb[j]);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma16_acc<kFirst>(acc[7][j], fa[7], fb[j]);
+        fb[j] = g6_frag(tbuf(t + 1) + kTile5, wn * 128 + j * 16, lane);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    ktile(0, std::true_type{});
+    for (int t = 1; t < ntiles; ++t) ktile(t, std::false_type{});
+    lds_dma_wait<0>();
+  }
+  mfma16_fence(acc);
+  store_block16<8, 8>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
+}
+
+bool launch6(dim3 grid, hipStream_t st, const GemmArgs& g) {
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm6_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(kGemm5Lds)) == hipSuccess;
+  if (!ok) return false;
+  gemm6_kernel<<<grid, 256, kGemm5Lds, st>>>(g);
+  return true;
+}
+
 template <int MA, int MB>
 bool launch5(dim3 grid, hipStream_t st, const GemmArgs& g) {
   static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm5_kernel<MA, MB>),
@@ -1117,11 +1346,15 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   // four-wave kernel's longer prologue (one wave per SIMD) pays off from K = 1024 on
   // config 3's GEMMs (even there, ahead of the eight-wave kernel from K = 4096).
   const bool big = tiles2 >= 64 || K >= 16384;
-  const bool use4 = fits4 && g.rs_ok && (variant == 3 || variant == 4 || (variant == 0 && big && K >= 1024));
+  const bool use4 = fits4 && g.rs_ok && (variant == 3 || variant == 4 || variant == 5 || (variant == 0 && big && K >= 1024));
   // the direct-to-LDS form for every operand layout (config 3's nine products: 1441 against
   // 1502 us for the register-staged form, 1-7 % ahead on each, same bits); variant 3 keeps
   // the register-staged one
-  const bool use5 = use4 && (variant == 4 || variant == 0);
+  const bool use5 = use4 && (variant == 4 || variant == 5 || variant == 0);
+  // 16x16x32 MFMAs (k-contiguous operand pairs)
+  // 16x16x32 MFMAs for k-contiguous operand pairs (config 3's forward products: 234.9
+  // against 264.6 us at M 8192, N 4096, K 4096, 84 against 91 us at K 1024; same bits)
+  const bool use6 = use5 && variant != 4 && ma == kAlongK && mb == kAlongK;
   if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && big))) {
     // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
     const int kt2 = int(ceil_div(K, kK2));
@@ -1142,7 +1375,9 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
     bool ok;
     if (use4 && g_gemm_xcd.load() && (int64_t(grid2.x) * grid2.y) % kGemmXcds == 0)
       g.xcd_group = int(std::min<unsigned>(grid2.y, 8));
-    if (use5) {
+    if (use6) {
+      ok = launch6(grid2, st2, g);
+    } else if (use5) {
       if (ma == kAlongK) ok = mb == kAlongK ? launch5<kAlongK, kAlongK>(grid2, st2, g) : launch5<kAlongK, kAlongRow>(grid2, st2, g);
       else ok = mb == kAlongK ? launch5<kAlongRow, kAlongK>(grid2, st2, g) : launch5<kAlongRow, kAlongRow>(grid2, st2, g);
     } else if (use4) {
@@ -1225,8 +1460,8 @@ extern "C" int xdna_gemm_bf16_noalloc(const uint16_t* A, const uint16_t* Bm, uin
 }
 
 extern "C" int xdna_gemm_set_variant(int variant) {
-  if (variant < 0 || variant > 4) {
-    set_error("xdna_gemm_set_variant: variant must be 0..4");
+  if (variant < 0 || variant > 5) {
+    set_error("xdna_gemm_set_variant: variant must be 0..5");
     return -1;
   }
   g_gemm_variant.store(variant);

@@ -62,6 +62,26 @@ __device__ inline void lds_dma16(const i32x4_t& rsrc, const uint16_t* lds, int v
                : "m0");
 }
 
+// LDS byte address of a shared-memory pointer, made wave-uniform (an SGPR value)
+__device__ inline uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(uint32_t(uintptr_t((__attribute__((address_space(3))) const void*)p)));
+}
+
+// lds_dma16 with the destination's LDS byte address and the resource already wave-uniform
+// (computed once outside a loop: no per-load readfirstlane or address-space conversion)
+__device__ inline void lds_dma16_m0(const i32x4_t& rs, uint32_t m0, int voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rs)
+               : "m0");
+}
+
+// a resource descriptor made wave-uniform
+__device__ inline i32x4_t uniform_rsrc(const i32x4_t& r) {
+  return i32x4_t{__builtin_amdgcn_readfirstlane(r[0]), __builtin_amdgcn_readfirstlane(r[1]),
+                 __builtin_amdgcn_readfirstlane(r[2]), __builtin_amdgcn_readfirstlane(r[3])};
+}
+
 // s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt at their maxima), gfx9 encoding
 template <int n>
 __device__ inline void lds_dma_wait() {

@@ -37,8 +37,8 @@ def variant(hip, request):
 
 
 # kernel variants (xdna_gemm_set_variant): 128 x 128 tiles, 256 x 256 tiles (eight- and four-wave,
-# and four-wave with direct-to-LDS loads)
-@pytest.mark.parametrize("variant", [1, 2, 3, 4], indirect=True, ids=lambda v: f"v{v}")
+# four-wave with direct-to-LDS loads, and that with 16x16x32 MFMAs for k-contiguous pairs)
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5], indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("M,N,K", [(256, 384, 512), (130, 70, 33), (1, 1, 1), (64, 257, 8),
                                    (300, 128, 1000), (520, 264, 136)])
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn", "tt"])
@@ -88,7 +88,7 @@ def test_k_zero_gives_beta_bias(hip):
     np.testing.assert_array_equal(oracle.bf16_value(host(c)), np.broadcast_to(2 * oracle.bf16_value(bias), (M, N)))
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4], indirect=True, ids=lambda v: f"v{v}")
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5], indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("mode", [1, 2, 3])
 def test_bias_modes_alpha_beta(hip, mode, variant):
     rng = np.random.default_rng(3 + mode)
@@ -107,7 +107,7 @@ def test_bias_modes_alpha_beta(hip, mode, variant):
     check_bf16(got, ref, what=f"bias mode {mode}")
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4], indirect=True, ids=lambda v: f"v{v}")
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5], indirect=True, ids=lambda v: f"v{v}")
 def test_batched(hip, variant):
     rng = np.random.default_rng(5)
     Bt, M, N, K = 6, 40, 72, 96
@@ -123,7 +123,7 @@ def test_batched(hip, variant):
     check_bf16(got_g, ref_g, what="gram")
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4], indirect=True, ids=lambda v: f"v{v}")
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5], indirect=True, ids=lambda v: f"v{v}")
 def test_mlp_shape(hip, variant):
     """One of config 3's GEMMs (x [8192,1024] . W^T [1024,4096]) on a row subset."""
     rng = np.random.default_rng(6)
