@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <utility>
 #include <type_traits>
 #include <cstdlib>
 
@@ -767,6 +768,271 @@ void conv_rows4_kernel(RowsArgs a) {
 #pragma unroll
       for (int n = 0; n < NT; ++n)
         if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[m][n][i]));
+    }
+}
+
+// Four-wave rows kernels on v_mfma_f32_16x16x32_bf16: the tiles, LDS layout, weight-slab
+// ring and window staging of conv_rows4_kernel, with 16 x 16 output tiles.  The MFMA-bound
+// kernels run at the board's power limit and the 16x16x32 form costs less energy per flop
+// (independent chains: 2156 against 1772 TFLOP/s for 32x32x16 on random bf16 operands), so
+// the clock runs higher; its MFMAs last 16 cycles instead of 32, so every LDS access and
+// global load is issued after a single MFMA, never after a group of them.
+// Wave (wm, wn) owns MI 16-channel x NJ 16-row tiles; a k-step is 32 channels (two per
+// tap).  One fragment set: A rows MI/2 .. MI-1 of a k-step are read during the first half
+// of its MFMAs (rows 0 .. MI/2-1, column by column), the next k-step's B columns and A
+// rows 0 .. MI/2-1 during the second half, each right after its last use.  The one
+// barrier per tap sits between the halves of its second k-step: every wave has then
+// read the tap's weight slot for the last time, so slab T+3 is stored into it during
+// the second half (and, at a chunk's last tap, the next chunk's window, followed by a
+// second barrier before its first fragment reads).
+// f(std::integral_constant<int, t>) for t = 0, 1, ...: call sites with compile-time indexes
+// (what a long unrolled loop does not guarantee)
+template <typename F, int... t>
+__device__ inline void for_each_index(std::integer_sequence<int, t...>, F&& f) {
+  (f(std::integral_constant<int, t>{}), ...);
+}
+
+template <int MI, int NJ, int WM>
+struct Q6 {
+  static constexpr int WN = 4 / WM;
+  static constexpr int CO = WM * MI * 16;                    // channels per workgroup
+  static constexpr int TP = WN * NJ * 16;                    // grid rows per workgroup
+  static constexpr int XRows = TP + kMaxHalo;                // window rows
+  static constexpr int Slot = CO * kPitch;                   // elements of one weight slot
+  static constexpr size_t Lds = size_t(XRows * kPitch + 3 * Slot) * 2;
+};
+
+template <int MI, int NJ, int WM, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
+void conv_rows6_kernel(RowsArgs a) {
+  using Q = Q6<MI, NJ, WM>;
+  constexpr int kXv = (Q::XRows * 8 + 255) / 256;      // window vectors per thread
+  constexpr int kWv = Q::CO * 8 / 256;                 // weight vectors per thread per slab
+  constexpr int kH = MI / 2;                           // A rows per half
+  constexpr int kQ = kH * NJ;                          // MFMAs per half
+  static_assert(MI % 2 == 0 && NJ >= kH && kH >= 2 && kWv >= 1, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs = smem;                                 // [XRows][kPitch]
+  uint16_t* wsl = smem + Q::XRows * kPitch;            // [3][CO][kPitch]
+
+  constexpr int tiles_per_group = kGroupOutRows / Q::TP;
+  int rt, ct;
+  if (!rows_tile(a, rt, ct)) return;
+  const int g = rt / tiles_per_group;
+  const int r0 = (rt % tiles_per_group) * Q::TP;
+  if (int64_t(g) * kGroupOutRows + r0 >= a.m_total) return;
+  const int co0 = ct * Q::CO;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int K = a.chunks * 9 * kKStep;
+  const int T1 = a.chunks * 9;
+  const int nrows = Q::TP + 2 * a.wp + 2;              // window rows (<= XRows)
+  const int l16 = lane & 15, lq = lane >> 4;
+
+  // accumulators start at the bias of their channel rows 4 lq .. 4 lq + 3
+  f32x4_t acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    f32x4_t init = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int cb = co0 + wm * MI * 16 + i * 16 + 4 * lq;
+    if (a.bias && a.bias_vec) {
+      const __amdgpu_buffer_rsrc_t brs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.bias), 0, a.cout * 2, 0x00020000);
+      const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(brs, cb * 2, 0, 0));
+      init[0] = __uint_as_float(v.x << 16);
+      init[1] = __uint_as_float(v.x & 0xFFFF0000u);
+      init[2] = __uint_as_float(v.y << 16);
+      init[3] = __uint_as_float(v.y & 0xFFFF0000u);
+    } else if (a.bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) init[r] = cb + r < a.cout ? bf16_to_f32(a.bias[cb + r]) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = init;
+  }
+  mfma16_fence(acc);
+
+  // weight vector j of a slab: row (tid >> 3) + 32 j, 8-element piece tid & 7
+  const uint16_t* wsrc = a.wt + (int64_t(co0) + (tid >> 3)) * K + (tid & 7) * 8;
+  const int wdst = (tid >> 3) * kPitch + (tid & 7) * 8;
+  // window vector j: row min((tid + 256 j) >> 3, nrows - 1), piece tid & 7
+  auto xoff = [&](int j) { return min((tid + j * 256) >> 3, nrows - 1) * 8 + (tid & 7); };
+  const uint16_t* xsrc0 = a.xp + (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
+  // fragment bases: A row wm*MI*16 + l16 of a slot, B row wn*NJ*16 + l16 of the window,
+  // k 8 lq of a k-step
+  const uint16_t* wfr = wsl + (wm * MI * 16 + l16) * kPitch + 8 * lq;
+  const uint16_t* xfr = xs + (wn * NJ * 16 + l16) * kPitch + 8 * lq;
+  const int wrow = a.wp * kPitch;
+
+  u32x4_t wreg[3][kWv];
+  u32x4_t xr[kXv];
+  u32x4_t fa[MI], fb[NJ];
+
+  auto w_load = [&](int set, int S) {
+    const uint16_t* s_ = wsrc + int64_t(min(S, T1 - 1)) * kKStep;
+#pragma unroll
+    for (int v = 0; v < kWv; ++v) wreg[set][v] = *reinterpret_cast<const u32x4_t*>(s_ + int64_t(v * 32) * K);
+  };
+  auto w_load1 = [&](int set, int S, int v) {
+    const uint16_t* s_ = wsrc + int64_t(min(S, T1 - 1)) * kKStep;
+    wreg[set][v] = *reinterpret_cast<const u32x4_t*>(s_ + int64_t(v * 32) * K);
+  };
+  auto w_store1 = [&](int set, int slot, int v) {
+    *reinterpret_cast<u32x4_t*>(wsl + slot * Q::Slot + wdst + v * 32 * kPitch) = wreg[set][v];
+  };
+  auto x_load1 = [&](int ch, int v) {
+    xr[v] = *reinterpret_cast<const u32x4_t*>(xsrc0 + int64_t(ch) * kGroupRows * kKStep + xoff(v) * 8);
+  };
+  auto x_store1 = [&](int v) {
+    *reinterpret_cast<u32x4_t*>(&xs[(xoff(v) >> 3) * kPitch + (xoff(v) & 7) * 8]) = xr[v];
+  };
+  auto frag_a = [&](int slot, int i, int ks) {
+    return *reinterpret_cast<const u32x4_t*>(wfr + slot * Q::Slot + i * 16 * kPitch + ks * 32);
+  };
+  auto frag_b = [&](int tap, int j, int ks) {
+    return *reinterpret_cast<const u32x4_t*>(xfr + (tap / 3) * wrow + ((tap % 3) + j * 16) * kPitch + ks * 32);
+  };
+
+  // prologue: slabs 0..2 and the window of chunk 0 in LDS; slabs 3, 4 in registers
+  w_load(0, 0);
+  w_load(1, 1);
+  w_load(2, 2);
+#pragma unroll
+  for (int v = 0; v < kXv; ++v) x_load1(0, v);
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int v = 0; v < kWv; ++v) w_store1(s, s, v);
+#pragma unroll
+  for (int v = 0; v < kXv; ++v) x_store1(v);
+  w_load(0, 3);
+  w_load(1, 4);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kH; ++i) fa[i] = frag_a(0, i, 0);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) fb[j] = frag_b(0, j, 0);
+
+  int ch = 0, chn = 0;
+  // one k-step (tap, ks) of chunk ch; tap and ks are compile-time constants, so every
+  // register-set index and every slot of the extra memory work below is static
+  auto kstep = [&](auto tap_c, auto ks_c) {
+        constexpr int tap = decltype(tap_c)::value, ks = decltype(ks_c)::value;
+        const int T = ch * 9 + tap;
+        // first half: A rows 0 .. kH-1 column by column; A rows kH + j read after the
+        // second MFMA of column j
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int i = 0; i < kH; ++i) {
+            mfma16_acc<false>(acc[i][j], fa[i], fb[j]);
+            if (i == 1 && j < kH) fa[kH + j] = frag_a(tap % 3, kH + j, ks);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        if (ks == 1) {
+          // every wave has read slot tap % 3 (and, at tap 8, this chunk's window) for the
+          // last time
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // second half: A rows kH .. MI-1 column by column.  After column j's last MFMA its
+        // B fragment is read for the next k-step (at a chunk's end, after the window
+        // store and barrier below); after its second MFMA, A row j (j < kH) of the next
+        // k-step.  Extra memory work, one instruction per MFMA slot: k-step 0 the next
+        // chunk's window loads (taps 0..6 share them), k-step 1 slab T+3 into slot
+        // tap % 3, slab T+5 into register set (tap + 2) % 3 and, at tap 8, the window store.
+        constexpr int ntap = ks == 0 ? tap : (tap + 1) % 9;
+        constexpr int nks = ks ^ 1;
+        constexpr bool chunk_end = ks == 1 && tap == 8;
+        // window loads of the next chunk, spread over taps 0..6
+        constexpr int nx_lo = tap < 7 ? tap * kXv / 7 : kXv, nx_hi = tap < 7 ? (tap + 1) * kXv / 7 : kXv;
+        constexpr int n_extra = ks == 0 ? nx_hi - nx_lo : 2 * kWv + (tap == 8 ? kXv : 0);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int r = 0; r < kH; ++r) {
+            const int q = j * kH + r;
+            mfma16_acc<false>(acc[kH + r][j], fa[kH + r], fb[j]);
+            if (r == kH - 1 && !chunk_end) fb[j] = frag_b(ntap, j, nks);
+            if (r == 1 && j < kH) fa[j] = frag_a(ntap % 3, j, nks);
+#pragma unroll
+            for (int e = 0; e < 2 * kWv + kXv; ++e) {
+              if (e >= n_extra || e * kQ / (n_extra > 0 ? n_extra : 1) != q) continue;
+              if (ks == 0) {
+                x_load1(chn, nx_lo + e);
+              } else if (e < kWv) {
+                w_store1(tap % 3, tap % 3, e);
+              } else if (e < 2 * kWv) {
+                w_load1((tap + 2) % 3, T + 5, e - kWv);
+              } else {
+                x_store1(e - 2 * kWv);
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        if (chunk_end) {
+          __syncthreads();  // the next chunk's window is in place
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) fb[j] = frag_b(0, j, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+  };
+  for (; ch < a.chunks; ++ch) {
+    chn = min(ch + 1, a.chunks - 1);
+    for_each_index(std::make_integer_sequence<int, 9>{}, [&](auto tap_c) {
+      kstep(tap_c, std::integral_constant<int, 0>{});
+      kstep(tap_c, std::integral_constant<int, 1>{});
+    });
+  }
+
+  mfma16_fence(acc);
+  if (a.out_rs) {
+    const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
+    const int plane2 = a.H * a.W * 2;
+    int poff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      poff[j] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int co = co0 + wm * MI * 16 + i * 16 + 4 * lq + r;
+        const int coff = co < a.cout ? co * plane2 : kOutSkip;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act(a, acc[i][j][r])), om.rs, poff[j] + coff, 0, 0);
+      }
+    return;
+  }
+  const int first = a.first;
+  const int64_t plane = int64_t(a.H) * a.W;
+  uint16_t* obase[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    obase[j] = nullptr;
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16;
+    if (p >= a.m_total) continue;
+    const int64_t vb = p / a.img;
+    const int64_t rem = p - vb * a.img;
+    const int y = int(rem / a.wp);
+    const int col = int(rem - int64_t(y) * a.wp) - first;
+    if (y >= a.H || col < 0) continue;
+    const int b = int(vb / a.S), s = int(vb % a.S);
+    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+    if (col >= cols) continue;
+    const int x = (a.S == 1 ? 0 : s * a.So) + col;
+    obase[j] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int co = co0 + wm * MI * 16 + i * 16 + 4 * lq + r;
+      if (co >= a.cout) continue;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (obase[j]) obase[j][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[i][j][r]));
     }
 }
 
@@ -1599,6 +1865,23 @@ int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   return check_launch("conv3x3 rows");
 }
 
+template <int MI, int NJ, int WM, int OCC = 1>
+int launch_rows6(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
+  using Q = Q6<MI, NJ, WM>;
+  static const bool lds_ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows6_kernel<MI, NJ, WM, OCC>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess;
+  if (!lds_ok) {
+    set_error("conv3x3 rows: cannot enable the 16x16x32 kernel's LDS size");
+    return -1;
+  }
+  a.nrt = int(ceil_div(geom.m_total, Q::TP));
+  a.ncot = int(ceil_div(cout, Q::CO));
+  const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
+  conv_rows6_kernel<MI, NJ, WM, OCC><<<grid, 256, Q::Lds, st>>>(a);
+  return check_launch("conv3x3 rows");
+}
+
 // conv of packed input xp (cin channels) with prepared weights -> NCHW out (cout channels).
 std::atomic<int> g_rows_variant{[] {
   const char* e = std::getenv("XDNA_ROWS_VARIANT");
@@ -1661,7 +1944,9 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     } else {
       // slots: workgroups one round holds (256 CUs x workgroups per CU)
       struct Cand { int v, co, tp, slots; double cost; };
-      const Cand all[] = {{7, 128, 512, 256, 1.0}, {5, 256, 256, 256, 1.0}, {6, 128, 256, 256, 1.1},
+      // (the 128 x 512 tile in its 16x16x32 form, variant 10: 2.8 % less time per conv
+      // step than variant 7 on N64 C512 H72, 1-5 % on the sweep's other 512-channel shapes)
+      const Cand all[] = {{10, 128, 512, 256, 1.0}, {5, 256, 256, 256, 1.0}, {6, 128, 256, 256, 1.1},
                           {9, 64, 256, 512, 1.05}};
       double best = 1e300;
       for (const Cand& c : all) {
@@ -1682,6 +1967,9 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   if (variant == 8) return launch_rows4<2, 4, 1>(a, geom, cout, st);
   // 64 x 256 tiles, two workgroups per CU (76 KB of LDS each)
   if (variant == 9) return launch_rows4<2, 2, 1, 2>(a, geom, cout, st);
+  // the 16x16x32 forms of variants 7 and 9
+  if (variant == 10) return launch_rows6<8, 8, 1>(a, geom, cout, st);
+  if (variant == 11) return launch_rows6<4, 4, 1, 2>(a, geom, cout, st);
   // the wide kernels: 256-channel tiles (cout > 128 only: the weights are padded to 256
   // rows from there on); the four-wave form unless the eight-wave one is asked for
   const bool wide = cout > kTCo && (variant == 4 || variant == 5);
@@ -2694,8 +2982,8 @@ int xdna_conv3x3_set_wgrad_rows_kernel(int form) {
 }
 
 int xdna_conv3x3_set_rows_variant(int variant) {
-  if (variant < 0 || variant > 9) {
-    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..9");
+  if (variant < 0 || variant > 11) {
+    set_error("xdna_conv3x3_set_rows_variant: variant must be 0..11");
     return -1;
   }
   g_rows_variant.store(variant);

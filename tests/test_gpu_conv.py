@@ -52,9 +52,9 @@ def _ws(nbytes):
 # rows-kernel variants (xdna_conv3x3_set_rows_variant): main kernel, small-grid kernel
 # with 64- and 128-row tiles (split-K over chunks where the grid is small), wide kernel
 # with eight and with four waves (256-channel tiles, for cout > 128; the main kernel
-# otherwise), four-wave kernels with 128 x 256, 128 x 512 and 64 x 512 tiles, and 64 x 256
-# tiles two per CU
-VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8, 9]
+# otherwise), four-wave kernels with 128 x 256, 128 x 512 and 64 x 512 tiles, 64 x 256
+# tiles two per CU, and the 16x16x32 MFMA forms of the 128 x 512 and 64 x 256 tiles
+VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11]
 
 
 @pytest.fixture
