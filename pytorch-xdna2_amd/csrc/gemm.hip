@@ -957,39 +957,6 @@ void gemm5_kernel(GemmArgs g) {
 // wait and barrier that publish the next k-tile and free this one's buffer, then the second
 // half with the next k-tile's DMA and fragment reads in fenced slices.
 // ---------------------------------------------------------------------------------------
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-// The MFMA as an inline-assembly statement on an AGPR quad updated in place: with 64
-// accumulators filling the 256 AGPRs, the compiler's allocation of the builtin's results
-// renames them through v_accvgpr copies every k-tile.  The compiler then does not see an
-// MFMA, so the hazards it would pad are padded by the kernel (mfma16_fence): wait states
-// between the last MFMA writing an accumulator and any other read of it (VALU, stores), and
-// between VALU writes of an accumulator (its zero init) and the first MFMA reading it.
-// Operands A and B come from LDS reads, whose completion the compiler's s_waitcnt covers
-// for inline-assembly operands as for any instruction; each accumulator is updated once
-// per 64 MFMAs, so no MFMA reads a result of the MFMA just before it.
-// kInit: the first k-tile's MFMA, accumulating onto the inline constant 0 (no zero-filled
-// accumulators to set up)
-template <bool kInit>
-__device__ inline void mfma16_acc(f32x4_t& c, const u32x4_t& a, const u32x4_t& b) {
-  if constexpr (kInit)
-    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
-  else
-    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-}
-
-// 24 wait states (the longest MFMA dependency in the gfx9 family needs 19), then every
-// accumulator of an 8 x 8 set passed through volatile statements, so that no read or
-// MFMA of them can be scheduled before the wait states
-__device__ inline void mfma16_fence(f32x4_t (&acc)[8][8]) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    asm volatile("; mfma16 fence"
-                 : "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3]), "+a"(acc[i][4]),
-                   "+a"(acc[i][5]), "+a"(acc[i][6]), "+a"(acc[i][7]));
-}
-
 // epilogue of 16 x 16 tiles: rows mb + i*16 + 4 (lane / 16) + r, columns nb + j*16 + lane % 16
 template <int MI, int NJ>
 __device__ inline void store_block16(const GemmArgs& g, int batch, int split, const f32x4_t (&acc)[MI][NJ],

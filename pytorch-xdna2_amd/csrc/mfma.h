@@ -31,6 +31,47 @@ __device__ inline bf16x8_t as_bf16x8(const u32x4_t& u) { return __builtin_bit_ca
 __device__ inline int mfma_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
 // ---------------------------------------------------------------------------------------
+// v_mfma_f32_16x16x32_bf16, per 64-lane wave:
+//   A fragment (16 x 32): lane l holds A[l % 16][8*(l/16) .. 8*(l/16)+7]
+//   B fragment (32 x 16): lane l holds B[8*(l/16) .. +7][l % 16]
+//   D (16 x 16, 4 fp32 per lane): register r of lane l holds D[4*(l/16) + r][l % 16]
+// ---------------------------------------------------------------------------------------
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// The MFMA as an inline-assembly statement on an AGPR quad updated in place: with 64
+// accumulators filling the 256 AGPRs, the compiler's allocation of the builtin's results
+// renames them through v_accvgpr copies every k-step.  The compiler then does not see an
+// MFMA, so the hazards it would pad are padded by the kernel (mfma16_fence): wait states
+// between the last MFMA writing an accumulator and any other read of it (VALU, stores), and
+// between VALU writes of an accumulator (its initial value) and the first MFMA reading it.
+// Operands A and B must come straight from LDS reads, whose completion the compiler's
+// s_waitcnt covers for inline-assembly operands as for any instruction (an operand written
+// by a VALU instruction would need 2 wait states before the MFMA, which nothing pads
+// here); a kernel updates each accumulator once per k-step of many MFMAs, so no MFMA reads
+// a result of the MFMA just before it.
+// kInit: the first k-step's MFMA, accumulating onto the inline constant 0 (no zero-filled
+// accumulators to set up)
+template <bool kInit>
+__device__ inline void mfma16_acc(f32x4_t& c, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (kInit)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// 24 wait states (the longest MFMA dependency in the gfx9 family needs 19), then every
+// accumulator of the set passed through volatile statements, so that no read or MFMA of
+// them can be scheduled before the wait states
+template <int MI, int NJ>
+__device__ inline void mfma16_fence(f32x4_t (&acc)[MI][NJ]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) asm volatile("; mfma16 fence" : "+a"(acc[i][j]));
+}
+
+// ---------------------------------------------------------------------------------------
 // gfx950's 16-byte LDS DMA (buffer_load_dwordx4 ... lds): one instruction per wave writes
 // 64 x 16 bytes contiguously at an LDS base (lane L at base + 16 L; a lane whose offset is
 // past the buffer's range writes zeros), with no register staging and no LDS store.
