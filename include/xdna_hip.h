@@ -414,8 +414,8 @@ int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uin
  * pipelined, operands staged through registers; also needs K % 8 == 0 and rows % 8 == 0
  * for row-contiguous operands, else 2 or 1), 4 the four-wave kernel with operands loaded
  * straight into LDS (32x32x16 MFMAs; same conditions), 5 that kernel with 16x16x32 MFMAs
- * for k-contiguous operand pairs (4 for other layouts).  Automatic: 5 where it applies,
- * else 4, on large grids or long K.  No reference counterpart (a tuning knob).
+ * (the automatic choice on large grids or long K where 3 applies).  No reference
+ * counterpart (a tuning knob).
  * XDNA_GEMM_VARIANT sets the initial value. */
 int xdna_gemm_set_variant(int variant);
 

@@ -765,7 +765,9 @@ struct G5Operand {
   int s_k;
 };
 
-template <int kMode>
+// kPerm16: the [k][row] tile permutation of the 16x16x32 kernel (gemm6_kernel), whose
+// transposing reads cover k rows R .. R+3 and R+8 .. R+11 in one half-wave
+template <int kMode, bool kPerm16 = false>
 __device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t s_k, int r0, int rows, int K,
                                        int tid) {
   G5Operand o;
@@ -785,7 +787,7 @@ __device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t
     } else {
       // block j: k rows 2 j, 2 j + 1, lane L at k row 2 j + L / 32, position L % 32
       const int kr = 2 * j + (lane >> 5);
-      const int q = (lane & 31) ^ (4 * (kr & 3));
+      const int q = (lane & 31) ^ (4 * (kr & 3) + (kPerm16 ? 2 * ((kr >> 3) & 1) : 0));
       o.roff[i] = r0 + 8 * q < rows ? (r0 + 8 * q) : -1;  // s_r == 1
       o.kq[i] = kr;
     }
@@ -941,7 +943,7 @@ void gemm5_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
-// gemm5's tile, DMA plan and LDS layout with v_mfma_f32_16x16x32_bf16 (k-contiguous operands).
+// gemm5's tile, DMA plan and LDS layout with v_mfma_f32_16x16x32_bf16.
 // The MFMA-bound kernels run at the board's power limit, and the 16x16x32 form costs less
 // energy per flop: one wave per SIMD issuing independent MFMAs on random bf16 operands
 // sustains 2156 TFLOP/s against 1772 for 32x32x16, and this kernel runs at 2.08 GHz where
@@ -949,9 +951,10 @@ void gemm5_kernel(GemmArgs g) {
 // MFMAs last 16 cycles instead of 32, so every LDS read and DMA is issued after a single
 // MFMA: behind a group of MFMAs the same instructions left the pipe idle (44.6 % busy,
 // 283.9 us; interleaved one by one, 234.9 us against gemm5's 264.6).
-// A fragment (16 rows x 32 k): lane l holds row l % 16, k 8 (l / 16) .. +7, one 16-byte LDS
-// read (rows r and pieces l / 16 of the permuted [256][4 pieces] tile: the 16 lanes of a
-// pass cover 16 distinct bank slots).  D (16 x 16, 4 fp32 per lane): register i of lane l
+// A fragment (16 rows x 32 k): lane l holds row l % 16, k 8 (l / 16) .. +7: one 16-byte LDS
+// read from a k-contiguous tile (rows r and pieces l / 16 of the permuted [256][4 pieces]
+// tile: the 16 lanes of a pass cover 16 distinct bank slots), two transposing reads from a
+// [k][row] tile (g6_frag).  D (16 x 16, 4 fp32 per lane): register i of lane l
 // holds D[4 (l / 16) + i][l % 16].  A wave's 128 x 128 is 8 x 8 tiles (64 MFMAs per 32-k
 // k-tile, 64 x 4 accumulator registers).  Per k-tile: the first half of its MFMAs, then the
 // wait and barrier that publish the next k-tile and free this one's buffer, then the second
@@ -1022,12 +1025,30 @@ __device__ inline void store_block16(const GemmArgs& g, int batch, int split, co
 }
 
 // 16 x 32 fragment of a k-contiguous [256][4 pieces] k-tile: rows rb + lane % 16, piece lane / 16
+// 16 x 32 fragment of a [k][row] k-tile (row-contiguous operand): two transposing reads.
+// In 16-lane group g = lane / 16, lane j supplies (k row 8 g + 4 h + j / 4, rows rb + 4 (j % 4)
+// .. +3) and receives row rb + j at k rows 8 g + 4 h .. +3 (h = 0, 1).  Piece q (8 rows) of
+// k row kr sits at q ^ (4 (kr & 3) + 2 ((kr >> 3) & 1)): a half-wave's k rows R .. R+3 and
+// R+8 .. R+11 fall on 16 distinct 16-byte positions of a 64-bank window.
+template <int kMode>
 __device__ inline u32x4_t g6_frag(const uint16_t* tile, int rb, int lane) {
-  const int r = rb + (lane & 15);
-  const int c = (lane >> 4) ^ ((r >> 2) & 3);
-  return *reinterpret_cast<const u32x4_t*>(tile + (r * 4 + c) * 8);
+  if (kMode == kAlongK) {
+    const int r = rb + (lane & 15);
+    const int c = (lane >> 4) ^ ((r >> 2) & 3);
+    return *reinterpret_cast<const u32x4_t*>(tile + (r * 4 + c) * 8);
+  }
+  const int g = lane >> 4, j = lane & 15;
+  const int kr = 8 * g + (j >> 2);
+  const int rr = rb + 4 * (j & 3);
+  const uint16_t* p = tile + (kr * 32 + ((rr >> 3) ^ (4 * (kr & 3) + 2 * ((kr >> 3) & 1)))) * 8 + (rr & 7);
+  const g4i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) g4i16x4*)(p));
+  const g4i16x4 hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) g4i16x4*)(p + 4 * 32 * 8));
+  const g2u2 a = __builtin_bit_cast(g2u2, lo), b = __builtin_bit_cast(g2u2, hi);
+  return u32x4_t{a[0], a[1], b[0], b[1]};
 }
 
+template <int kModeA, int kModeB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm6_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -1050,8 +1071,8 @@ void gemm6_kernel(GemmArgs g) {
     // during the next first half.  Both halves run column by column, so a fragment is read
     // at least 16 MFMAs before its first use.
     u32x4_t fa[8], fb[8];
-    const G5Operand oa = g5_operand<kAlongK>(A, g.a_r, g.a_k, m0, g.M, g.K, tid);
-    const G5Operand ob = g5_operand<kAlongK>(B, g.b_r, g.b_k, n0, g.N, g.K, tid);
+    const G5Operand oa = g5_operand<kModeA, true>(A, g.a_r, g.a_k, m0, g.M, g.K, tid);
+    const G5Operand ob = g5_operand<kModeB, true>(B, g.b_r, g.b_k, n0, g.N, g.K, tid);
     auto tbuf = [&](int t) { return smem + (t & (kNB5 - 1)) * 2 * kTile5; };
     auto load = [&](int t) {
       const int k_ = kbeg + min(t, ntiles - 1) * kK5;
@@ -1063,9 +1084,9 @@ void gemm6_kernel(GemmArgs g) {
     lds_dma_wait<8 * (kNB5 - 1)>();
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = g6_frag(tbuf(0), wm * 128 + i * 16, lane);
+    for (int i = 0; i < 4; ++i) fa[i] = g6_frag<kModeA>(tbuf(0), wm * 128 + i * 16, lane);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) fb[j] = g6_frag(tbuf(0) + kTile5, wn * 128 + j * 16, lane);
+    for (int j = 0; j < 8; ++j) fb[j] = g6_frag<kModeB>(tbuf(0) + kTile5, wn * 128 + j * 16, lane);
     // wave-uniform DMA state: resources and the LDS byte address of this wave's first
     // destination block (the loop adds buffer and block offsets as scalar arithmetic)
     const i32x4_t rsa = uniform_rsrc(oa.rs), rsb = uniform_rsrc(ob.rs);
@@ -1087,7 +1108,7 @@ void gemm6_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           mfma16_acc<kFirst>(acc[i][j], fa[i], fb[j]);
-          if (i == 1 && j < 4) fa[4 + j] = g6_frag(tbuf(t), wm * 128 + (4 + j) * 16, lane);
+          if (i == 1 && j < 4) fa[4 + j] = g6_frag<kModeA>(tbuf(t), wm * 128 + (4 + j) * 16, lane);
           __builtin_amdgcn_sched_barrier(0);
         }
       // this wave's reads of buffer t are complete and its loads of k-tile t+1 have landed
@@ -1109,12 +1130,12 @@ void gemm6_kernel(GemmArgs g) {
           lds_dma16_m0(rsb, m0n + uint32_t((kTile5 + (j - 4) * 512) * 2), g5_off(ob, j - 4, kn, kend));
         __builtin_amdgcn_sched_barrier(0);
         mfma16_acc<kFirst>(acc[5][j], fa[5], fb[j]);
-        if (j < 4) fa[j] = g6_frag(tbuf(t + 1), wm * 128 + j * 16, lane);
+        if (j < 4) fa[j] = g6_frag<kModeA>(tbuf(t + 1), wm * 128 + j * 16, lane);
         __builtin_amdgcn_sched_barrier(0);
         mfma16_acc<kFirst>(acc[6][j], fa[6], fb[j]);
         __builtin_amdgcn_sched_barrier(0);
         mfma16_acc<kFirst>(acc[7][j], fa[7], fb[j]);
-        fb[j] = g6_frag(tbuf(t + 1) + kTile5, wn * 128 + j * 16, lane);
+        fb[j] = g6_frag<kModeB>(tbuf(t + 1) + kTile5, wn * 128 + j * 16, lane);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -1126,12 +1147,13 @@ void gemm6_kernel(GemmArgs g) {
   store_block16<8, 8>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
 }
 
+template <int MA, int MB>
 bool launch6(dim3 grid, hipStream_t st, const GemmArgs& g) {
-  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm6_kernel),
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm6_kernel<MA, MB>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              int(kGemm5Lds)) == hipSuccess;
   if (!ok) return false;
-  gemm6_kernel<<<grid, 256, kGemm5Lds, st>>>(g);
+  gemm6_kernel<MA, MB><<<grid, 256, kGemm5Lds, st>>>(g);
   return true;
 }
 
@@ -1318,10 +1340,10 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   // 1502 us for the register-staged form, 1-7 % ahead on each, same bits); variant 3 keeps
   // the register-staged one
   const bool use5 = use4 && (variant == 4 || variant == 5 || variant == 0);
-  // 16x16x32 MFMAs (k-contiguous operand pairs)
-  // 16x16x32 MFMAs for k-contiguous operand pairs (config 3's forward products: 234.9
-  // against 264.6 us at M 8192, N 4096, K 4096, 84 against 91 us at K 1024; same bits)
-  const bool use6 = use5 && variant != 4 && ma == kAlongK && mb == kAlongK;
+  // 16x16x32 MFMAs for every operand layout (config 3's nine products: 1284.6 against
+  // 1352.2 us for the 32x32x16 form on one box, 0-8 % ahead on each but one level; same
+  // bits); variant 4 keeps the 32x32x16 form
+  const bool use6 = use5 && (variant == 5 || variant == 0);
   if (vec_ok && K > 0 && (use4 || variant == 2 || (variant == 0 && big))) {
     // split K while the grid is below the CU count (fp32 partials, fixed-order reduce)
     const int kt2 = int(ceil_div(K, kK2));
@@ -1343,7 +1365,8 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
     if (use4 && g_gemm_xcd.load() && (int64_t(grid2.x) * grid2.y) % kGemmXcds == 0)
       g.xcd_group = int(std::min<unsigned>(grid2.y, 8));
     if (use6) {
-      ok = launch6(grid2, st2, g);
+      if (ma == kAlongK) ok = mb == kAlongK ? launch6<kAlongK, kAlongK>(grid2, st2, g) : launch6<kAlongK, kAlongRow>(grid2, st2, g);
+      else ok = mb == kAlongK ? launch6<kAlongRow, kAlongK>(grid2, st2, g) : launch6<kAlongRow, kAlongRow>(grid2, st2, g);
     } else if (use5) {
       if (ma == kAlongK) ok = mb == kAlongK ? launch5<kAlongK, kAlongK>(grid2, st2, g) : launch5<kAlongK, kAlongRow>(grid2, st2, g);
       else ok = mb == kAlongK ? launch5<kAlongRow, kAlongK>(grid2, st2, g) : launch5<kAlongRow, kAlongRow>(grid2, st2, g);

@@ -37,7 +37,7 @@ def variant(hip, request):
 
 
 # kernel variants (xdna_gemm_set_variant): 128 x 128 tiles, 256 x 256 tiles (eight- and four-wave,
-# four-wave with direct-to-LDS loads, and that with 16x16x32 MFMAs for k-contiguous pairs)
+# four-wave with direct-to-LDS loads, and that with 16x16x32 MFMAs)
 @pytest.mark.parametrize("variant", [1, 2, 3, 4, 5], indirect=True, ids=lambda v: f"v{v}")
 @pytest.mark.parametrize("M,N,K", [(256, 384, 512), (130, 70, 33), (1, 1, 1), (64, 257, 8),
                                    (300, 128, 1000), (520, 264, 136)])
