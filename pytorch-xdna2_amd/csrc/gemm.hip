@@ -765,8 +765,11 @@ struct G5Operand {
   int s_k;
 };
 
-// kPerm16: the [k][row] tile permutation of the 16x16x32 kernel (gemm6_kernel), whose
-// transposing reads cover k rows R .. R+3 and R+8 .. R+11 in one half-wave
+// kPerm16: the tile permutations of the 16x16x32 kernel (gemm6_kernel): k-contiguous,
+// piece c of row r at c ^ 2 ((r >> 3) & 1), which the LDS serves without bank conflicts for
+// reads of 16 rows x 4 pieces (the k-contiguous permutation above measured 2 conflict cycles
+// per LDS-active cycle there); [k][row], for transposing reads that cover k rows R .. R+3
+// and R+8 .. R+11 in one half-wave
 template <int kMode, bool kPerm16 = false>
 __device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t s_k, int r0, int rows, int K,
                                        int tid) {
@@ -781,7 +784,7 @@ __device__ inline G5Operand g5_operand(const uint16_t* src, int64_t s_r, int64_t
     if (kMode == kAlongK) {
       // block j: rows 16 j .. 16 j + 15, lane L at row 16 j + L / 4, position L % 4
       const int r = 16 * j + (lane >> 2);
-      const int c = (lane & 3) ^ ((r >> 2) & 3);
+      const int c = (lane & 3) ^ (kPerm16 ? 2 * ((r >> 3) & 1) : (r >> 2) & 3);
       o.roff[i] = r0 + r < rows ? int(int64_t(r0 + r) * s_r) : -1;
       o.kq[i] = c * 8;
     } else {
@@ -952,9 +955,8 @@ void gemm5_kernel(GemmArgs g) {
 // MFMA: behind a group of MFMAs the same instructions left the pipe idle (44.6 % busy,
 // 283.9 us; interleaved one by one, 234.9 us against gemm5's 264.6).
 // A fragment (16 rows x 32 k): lane l holds row l % 16, k 8 (l / 16) .. +7: one 16-byte LDS
-// read from a k-contiguous tile (rows r and pieces l / 16 of the permuted [256][4 pieces]
-// tile: the 16 lanes of a pass cover 16 distinct bank slots), two transposing reads from a
-// [k][row] tile (g6_frag).  D (16 x 16, 4 fp32 per lane): register i of lane l
+// read from a k-contiguous tile (row r, piece (l / 16) ^ 2 ((r >> 3) & 1) of the [256][4
+// pieces] tile), two transposing reads from a [k][row] tile (g6_frag).  D (16 x 16, 4 fp32 per lane): register i of lane l
 // holds D[4 (l / 16) + i][l % 16].  A wave's 128 x 128 is 8 x 8 tiles (64 MFMAs per 32-k
 // k-tile, 64 x 4 accumulator registers).  Per k-tile: the first half of its MFMAs, then the
 // wait and barrier that publish the next k-tile and free this one's buffer, then the second
@@ -1034,7 +1036,7 @@ template <int kMode>
 __device__ inline u32x4_t g6_frag(const uint16_t* tile, int rb, int lane) {
   if (kMode == kAlongK) {
     const int r = rb + (lane & 15);
-    const int c = (lane >> 4) ^ ((r >> 2) & 3);
+    const int c = (lane >> 4) ^ (2 * ((r >> 3) & 1));
     return *reinterpret_cast<const u32x4_t*>(tile + (r * 4 + c) * 8);
   }
   const int g = lane >> 4, j = lane & 15;
