@@ -792,28 +792,44 @@ __device__ inline void for_each_index(std::integer_sequence<int, t...>, F&& f) {
   (f(std::integral_constant<int, t>{}), ...);
 }
 
-template <int MI, int NJ, int WM>
+// LDS rows of 80 elements (160 bytes) where one workgroup per CU leaves room, with the
+// 16 rows of a fragment read in the lane order that swaps bits 2 and 3 of the lane's row
+// index: rocprofv3's bank-conflict counter and a probe of ds_read_b128 lane groupings on
+// the MI355X show 16-row x 4-piece reads at a 144-byte pitch conflicting (about 2 conflict
+// cycles per LDS-active cycle) and this form free of conflicts at any starting row (the tap
+// offsets).  The MFMA then sees rows and channels in that order, which the accumulator
+// mapping follows.  Two workgroups per CU keep the 144-byte pitch and the plain order.
+template <int MI, int NJ, int WM, int OCC = 1>
 struct Q6 {
   static constexpr int WN = 4 / WM;
   static constexpr int CO = WM * MI * 16;                    // channels per workgroup
   static constexpr int TP = WN * NJ * 16;                    // grid rows per workgroup
   static constexpr int XRows = TP + kMaxHalo;                // window rows
-  static constexpr int Slot = CO * kPitch;                   // elements of one weight slot
-  static constexpr size_t Lds = size_t(XRows * kPitch + 3 * Slot) * 2;
+  static constexpr bool Swz = size_t(XRows + 3 * CO) * 160 * OCC <= 160 * 1024;
+  static constexpr int Pitch = Swz ? 80 : kPitch;            // LDS row pitch (elements)
+  static constexpr int Slot = CO * Pitch;                    // elements of one weight slot
+  static constexpr size_t Lds = size_t(XRows * Pitch + 3 * Slot) * 2;
 };
+
+// the lane order of a fragment's 16 rows: bits 2 and 3 swapped (kSwz), else as is
+template <bool kSwz>
+__device__ inline int q6_row(int r) {
+  return kSwz ? (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1) : r;
+}
 
 template <int MI, int NJ, int WM, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 void conv_rows6_kernel(RowsArgs a) {
-  using Q = Q6<MI, NJ, WM>;
+  using Q = Q6<MI, NJ, WM, OCC>;
+  constexpr int kP = Q::Pitch;
   constexpr int kXv = (Q::XRows * 8 + 255) / 256;      // window vectors per thread
   constexpr int kWv = Q::CO * 8 / 256;                 // weight vectors per thread per slab
   constexpr int kH = MI / 2;                           // A rows per half
   constexpr int kQ = kH * NJ;                          // MFMAs per half
   static_assert(MI % 2 == 0 && NJ >= kH && kH >= 2 && kWv >= 1, "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* xs = smem;                                 // [XRows][kPitch]
-  uint16_t* wsl = smem + Q::XRows * kPitch;            // [3][CO][kPitch]
+  uint16_t* xs = smem;                                 // [XRows][kP]
+  uint16_t* wsl = smem + Q::XRows * kP;                // [3][CO][kP]
 
   constexpr int tiles_per_group = kGroupOutRows / Q::TP;
   int rt, ct;
@@ -828,13 +844,16 @@ void conv_rows6_kernel(RowsArgs a) {
   const int T1 = a.chunks * 9;
   const int nrows = Q::TP + 2 * a.wp + 2;              // window rows (<= XRows)
   const int l16 = lane & 15, lq = lane >> 4;
+  // the fragment row this lane reads, and the first of the 4 channel rows (4 lq .. 4 lq + 3
+  // of a 16-row tile in MFMA order) its accumulators hold
+  const int l16s = q6_row<Q::Swz>(l16), lqs = q6_row<Q::Swz>(4 * lq) >> 2;
 
   // accumulators start at the bias of their channel rows 4 lq .. 4 lq + 3
   f32x4_t acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     f32x4_t init = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int cb = co0 + wm * MI * 16 + i * 16 + 4 * lq;
+    const int cb = co0 + wm * MI * 16 + i * 16 + 4 * lqs;
     if (a.bias && a.bias_vec) {
       const __amdgpu_buffer_rsrc_t brs =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.bias), 0, a.cout * 2, 0x00020000);
@@ -854,15 +873,15 @@ void conv_rows6_kernel(RowsArgs a) {
 
   // weight vector j of a slab: row (tid >> 3) + 32 j, 8-element piece tid & 7
   const uint16_t* wsrc = a.wt + (int64_t(co0) + (tid >> 3)) * K + (tid & 7) * 8;
-  const int wdst = (tid >> 3) * kPitch + (tid & 7) * 8;
+  const int wdst = (tid >> 3) * kP + (tid & 7) * 8;
   // window vector j: row min((tid + 256 j) >> 3, nrows - 1), piece tid & 7
   auto xoff = [&](int j) { return min((tid + j * 256) >> 3, nrows - 1) * 8 + (tid & 7); };
   const uint16_t* xsrc0 = a.xp + (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
   // fragment bases: A row wm*MI*16 + l16 of a slot, B row wn*NJ*16 + l16 of the window,
   // k 8 lq of a k-step
-  const uint16_t* wfr = wsl + (wm * MI * 16 + l16) * kPitch + 8 * lq;
-  const uint16_t* xfr = xs + (wn * NJ * 16 + l16) * kPitch + 8 * lq;
-  const int wrow = a.wp * kPitch;
+  const uint16_t* wfr = wsl + (wm * MI * 16 + l16s) * kP + 8 * lq;
+  const uint16_t* xfr = xs + (wn * NJ * 16 + l16s) * kP + 8 * lq;
+  const int wrow = a.wp * kP;
 
   u32x4_t wreg[3][kWv];
   u32x4_t xr[kXv];
@@ -878,19 +897,19 @@ void conv_rows6_kernel(RowsArgs a) {
     wreg[set][v] = *reinterpret_cast<const u32x4_t*>(s_ + int64_t(v * 32) * K);
   };
   auto w_store1 = [&](int set, int slot, int v) {
-    *reinterpret_cast<u32x4_t*>(wsl + slot * Q::Slot + wdst + v * 32 * kPitch) = wreg[set][v];
+    *reinterpret_cast<u32x4_t*>(wsl + slot * Q::Slot + wdst + v * 32 * kP) = wreg[set][v];
   };
   auto x_load1 = [&](int ch, int v) {
     xr[v] = *reinterpret_cast<const u32x4_t*>(xsrc0 + int64_t(ch) * kGroupRows * kKStep + xoff(v) * 8);
   };
   auto x_store1 = [&](int v) {
-    *reinterpret_cast<u32x4_t*>(&xs[(xoff(v) >> 3) * kPitch + (xoff(v) & 7) * 8]) = xr[v];
+    *reinterpret_cast<u32x4_t*>(&xs[(xoff(v) >> 3) * kP + (xoff(v) & 7) * 8]) = xr[v];
   };
   auto frag_a = [&](int slot, int i, int ks) {
-    return *reinterpret_cast<const u32x4_t*>(wfr + slot * Q::Slot + i * 16 * kPitch + ks * 32);
+    return *reinterpret_cast<const u32x4_t*>(wfr + slot * Q::Slot + i * 16 * kP + ks * 32);
   };
   auto frag_b = [&](int tap, int j, int ks) {
-    return *reinterpret_cast<const u32x4_t*>(xfr + (tap / 3) * wrow + ((tap % 3) + j * 16) * kPitch + ks * 32);
+    return *reinterpret_cast<const u32x4_t*>(xfr + (tap / 3) * wrow + ((tap % 3) + j * 16) * kP + ks * 32);
   };
 
   // prologue: slabs 0..2 and the window of chunk 0 in LDS; slabs 3, 4 in registers
@@ -992,12 +1011,12 @@ void conv_rows6_kernel(RowsArgs a) {
     int poff[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
-      poff[j] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16);
+      poff[j] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16s);
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int co = co0 + wm * MI * 16 + i * 16 + 4 * lq + r;
+        const int co = co0 + wm * MI * 16 + i * 16 + 4 * lqs + r;
         const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
@@ -1011,7 +1030,7 @@ void conv_rows6_kernel(RowsArgs a) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     obase[j] = nullptr;
-    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16;
+    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16s;
     if (p >= a.m_total) continue;
     const int64_t vb = p / a.img;
     const int64_t rem = p - vb * a.img;
@@ -1028,7 +1047,7 @@ void conv_rows6_kernel(RowsArgs a) {
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int co = co0 + wm * MI * 16 + i * 16 + 4 * lq + r;
+      const int co = co0 + wm * MI * 16 + i * 16 + 4 * lqs + r;
       if (co >= a.cout) continue;
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
@@ -1867,7 +1886,7 @@ int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
 
 template <int MI, int NJ, int WM, int OCC = 1>
 int launch_rows6(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
-  using Q = Q6<MI, NJ, WM>;
+  using Q = Q6<MI, NJ, WM, OCC>;
   static const bool lds_ok =
       hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows6_kernel<MI, NJ, WM, OCC>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess;
