@@ -506,6 +506,27 @@ def gemm_product(layout, variant, M=8192, N=4096, K=4096, launches=30):
     return 0
 
 
+def conv_rows_shape(variant, n, c, h, launches=20):
+    """20 forward 3x3 convs of one sweep-shaped problem (N, C, H = W; seeded sweep data) through
+    the aten op with xdna_conv3x3_set_rows_variant VARIANT: the workload of the rows-kernel
+    counter passes (rocprofv3 --pmc)."""
+    import torch
+
+    import xdna_train  # noqa: F401  (registers the xdna device)
+    from xdna_train import hip_abi
+    lib = hip_abi.load()
+    X = torch.device("xdna")
+    (x, w, b, _), = conv_sweep_data(torch, X, [(int(n), int(c), int(h))])
+    assert lib.xdna_conv3x3_set_rows_variant(int(variant)) == 0
+    with torch.no_grad():
+        for _ in range(launches):
+            torch.ops.aten.convolution_overrideable(x, w, b, [1, 1], [1, 1], [1, 1], False, [0, 0], 1)
+    sync(torch)
+    assert lib.xdna_conv3x3_set_rows_variant(0) == 0
+    print(f"conv rows variant {variant} N{n} C{c} H{h}: {launches} forward convs", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -524,12 +545,17 @@ def main() -> int:
     ap.add_argument("--gemm-product", metavar="LAYOUT,VARIANT",
                     help="only 30 launches of config 3's largest product (M 8192, N 4096, K 4096) with "
                          "operand layout nt / nn / tn and xdna_gemm_set_variant VARIANT (counter passes)")
+    ap.add_argument("--conv-rows", metavar="VARIANT,N,C,H",
+                    help="only 20 forward convs of one sweep shape with xdna_conv3x3_set_rows_variant "
+                         "VARIANT (counter passes)")
     args = ap.parse_args()
     if args.cpu_worker:
         cpu_worker(args.cpu_worker)
         return 0
     if args.gemm_product:
         return gemm_product(*args.gemm_product.split(","))
+    if args.conv_rows:
+        return conv_rows_shape(*args.conv_rows.split(","))
     if args.gpus != 1:
         print("bench.py: this build runs on one MI355X only (one process, one GPU); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
