@@ -370,7 +370,8 @@ int xdna_conv2d_set_variant(int variant);
  * rows and 64 channels x 512 rows per workgroup (any cout), 9 the four-wave kernel with
  * 64 channels x 256 rows and two workgroups per CU (the automatic choice up to 256
  * output channels on all but the smallest grids), 10 / 11 the 128 x 512 and 64 x 256
- * kernels with 16x16x32 MFMAs (10 is the automatic choice where 7 was).
+ * kernels with 16x16x32 MFMAs (10 is the automatic choice where 7 was, 11 where 9 was for
+ * 256 output channels on large grids).
  * Results agree to the same tolerance; only the
  * summation grouping differs.  No reference counterpart (a tuning knob, like the
  * reference's XDNA_* performance environment variables).  XDNA_ROWS_VARIANT sets the

@@ -806,15 +806,22 @@ struct Q6 {
   static constexpr int TP = WN * NJ * 16;                    // grid rows per workgroup
   static constexpr int XRows = TP + kMaxHalo;                // window rows
   static constexpr bool Swz = size_t(XRows + 3 * CO) * 160 * OCC <= 160 * 1024;
+  static constexpr int Mode = Swz ? 1 : 2;                   // q6_row's lane order
   static constexpr int Pitch = Swz ? 80 : kPitch;            // LDS row pitch (elements)
   static constexpr int Slot = CO * Pitch;                    // elements of one weight slot
   static constexpr size_t Lds = size_t(XRows * Pitch + 3 * Slot) * 2;
 };
 
-// the lane order of a fragment's 16 rows: bits 2 and 3 swapped (kSwz), else as is
-template <bool kSwz>
+// The lane order of a fragment's 16 rows: mode 1 (160-byte rows) bits 2 and 3 swapped;
+// mode 2 (144-byte rows, two workgroups per CU) the two 2-bit halves swapped, with the
+// k-step's 8-channel pieces taken in the order (0, 4, 1, 5), (2, 6, 3, 7) by lane groups 0..3
+// (both operands alike, so the sum is unchanged): a probe of that layout on the MI355X reads
+// without bank conflicts at any starting row.
+template <int kMode>
 __device__ inline int q6_row(int r) {
-  return kSwz ? (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1) : r;
+  if (kMode == 1) return (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1);
+  if (kMode == 2) return ((r >> 2) & 3) | ((r & 3) << 2);
+  return r;
 }
 
 template <int MI, int NJ, int WM, int OCC>
@@ -846,25 +853,32 @@ void conv_rows6_kernel(RowsArgs a) {
   const int l16 = lane & 15, lq = lane >> 4;
   // the fragment row this lane reads, and the first of the 4 channel rows (4 lq .. 4 lq + 3
   // of a 16-row tile in MFMA order) its accumulators hold
-  const int l16s = q6_row<Q::Swz>(l16), lqs = q6_row<Q::Swz>(4 * lq) >> 2;
+  const int l16s = q6_row<Q::Mode>(l16);
+  int chr[4];  // channel row (within a 16-channel tile) of accumulator register r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) chr[r] = q6_row<Q::Mode>(4 * lq + r);
+  // this lane group's 8 channels of k-step ks: + kqs * ks
+  constexpr int kqs = Q::Mode == 2 ? 16 : 32;
+  const int kq0 = Q::Mode == 2 ? 8 * (lq >> 1) + 32 * (lq & 1) : 8 * lq;
 
   // accumulators start at the bias of their channel rows 4 lq .. 4 lq + 3
   f32x4_t acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     f32x4_t init = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int cb = co0 + wm * MI * 16 + i * 16 + 4 * lqs;
-    if (a.bias && a.bias_vec) {
+    const int cb = co0 + wm * MI * 16 + i * 16;
+    if (a.bias && a.bias_vec && Q::Mode != 2) {
+      // 4 consecutive channels from chr[0] on
       const __amdgpu_buffer_rsrc_t brs =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.bias), 0, a.cout * 2, 0x00020000);
-      const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(brs, cb * 2, 0, 0));
+      const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(brs, (cb + chr[0]) * 2, 0, 0));
       init[0] = __uint_as_float(v.x << 16);
       init[1] = __uint_as_float(v.x & 0xFFFF0000u);
       init[2] = __uint_as_float(v.y << 16);
       init[3] = __uint_as_float(v.y & 0xFFFF0000u);
     } else if (a.bias) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) init[r] = cb + r < a.cout ? bf16_to_f32(a.bias[cb + r]) : 0.0f;
+      for (int r = 0; r < 4; ++r) init[r] = cb + chr[r] < a.cout ? bf16_to_f32(a.bias[cb + chr[r]]) : 0.0f;
     }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = init;
@@ -877,10 +891,10 @@ void conv_rows6_kernel(RowsArgs a) {
   // window vector j: row min((tid + 256 j) >> 3, nrows - 1), piece tid & 7
   auto xoff = [&](int j) { return min((tid + j * 256) >> 3, nrows - 1) * 8 + (tid & 7); };
   const uint16_t* xsrc0 = a.xp + (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
-  // fragment bases: A row wm*MI*16 + l16 of a slot, B row wn*NJ*16 + l16 of the window,
-  // k 8 lq of a k-step
-  const uint16_t* wfr = wsl + (wm * MI * 16 + l16s) * kP + 8 * lq;
-  const uint16_t* xfr = xs + (wn * NJ * 16 + l16s) * kP + 8 * lq;
+  // fragment bases: A row wm*MI*16 + l16s of a slot, B row wn*NJ*16 + l16s of the window,
+  // this lane group's 8 channels of a k-step (kq0)
+  const uint16_t* wfr = wsl + (wm * MI * 16 + l16s) * kP + kq0;
+  const uint16_t* xfr = xs + (wn * NJ * 16 + l16s) * kP + kq0;
   const int wrow = a.wp * kP;
 
   u32x4_t wreg[3][kWv];
@@ -906,10 +920,10 @@ void conv_rows6_kernel(RowsArgs a) {
     *reinterpret_cast<u32x4_t*>(&xs[(xoff(v) >> 3) * kP + (xoff(v) & 7) * 8]) = xr[v];
   };
   auto frag_a = [&](int slot, int i, int ks) {
-    return *reinterpret_cast<const u32x4_t*>(wfr + slot * Q::Slot + i * 16 * kP + ks * 32);
+    return *reinterpret_cast<const u32x4_t*>(wfr + slot * Q::Slot + i * 16 * kP + ks * kqs);
   };
   auto frag_b = [&](int tap, int j, int ks) {
-    return *reinterpret_cast<const u32x4_t*>(xfr + (tap / 3) * wrow + ((tap % 3) + j * 16) * kP + ks * 32);
+    return *reinterpret_cast<const u32x4_t*>(xfr + (tap / 3) * wrow + ((tap % 3) + j * 16) * kP + ks * kqs);
   };
 
   // prologue: slabs 0..2 and the window of chunk 0 in LDS; slabs 3, 4 in registers
@@ -1016,7 +1030,7 @@ void conv_rows6_kernel(RowsArgs a) {
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int co = co0 + wm * MI * 16 + i * 16 + 4 * lqs + r;
+        const int co = co0 + wm * MI * 16 + i * 16 + chr[r];
         const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
@@ -1047,7 +1061,7 @@ void conv_rows6_kernel(RowsArgs a) {
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int co = co0 + wm * MI * 16 + i * 16 + 4 * lqs + r;
+      const int co = co0 + wm * MI * 16 + i * 16 + chr[r];
       if (co >= a.cout) continue;
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
@@ -1959,7 +1973,10 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     if (wgs9 < 150) {
       variant = -1;
     } else if (cout <= 2 * kTCo) {
-      variant = 9;
+      // its 16x16x32 form (variant 11) from 256 output channels on grids of 300 such
+      // workgroups or more: 0.5-3.4 % less step time on the sweep's C256 shapes with H >= 36,
+      // 2-4 us more on the small ones
+      variant = cout > kTCo && wgs9 >= 300 ? 11 : 9;
     } else {
       // slots: workgroups one round holds (256 CUs x workgroups per CU)
       struct Cand { int v, co, tp, slots; double cost; };
