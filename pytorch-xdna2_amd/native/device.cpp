@@ -673,6 +673,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   mod.def("note_graph_replay", [] { note_graph_replay(); });
   mod.def("refresh_graph_weights", [](int64_t pool) { return refresh_graph_weights(pool); });
   mod.def("release_graph_weights", [](int64_t pool) { release_graph_weights(pool); });
+  mod.def("cache_stats", [](int64_t tag) { return cache_stats(tag); }, py::arg("tag") = -1);
   mod.def("pool_create", [] { return xdna_hip_cache_pool_create(); });
   mod.def("pool_begin", [](int64_t pool) { check_abi(xdna_hip_cache_pool_begin(pool), "pool_begin"); });
   mod.def("pool_end", [] { check_abi(xdna_hip_cache_pool_end(), "pool_end"); });

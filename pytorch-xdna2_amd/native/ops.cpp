@@ -91,7 +91,9 @@ bool conv_s2_eligible(const at::Tensor& x, const at::Tensor& w, c10::SymIntArray
 }
 
 // Prepared weight forms (forward and input-gradient), keyed by storage, data address,
-// offset, shape, version, write epoch, graph-replay generation and direction: the role
+// offset, shape, strides, version, write epoch, graph-replay generation and direction
+// (strides: two views of one storage with the same offset and shape, such as w and
+// w.transpose(2, 3), are different weights with one version counter and epoch): the role
 // of the reference's weight slots (torch_xdna_device.cpp:2208-2271, keyed on the data
 // pointer, version and write epoch).  A weak reference to the storage tells a live tensor
 // from a new one at a recycled address; in-place writes through autograd bump the
@@ -106,7 +108,7 @@ struct PreparedWeights {
   const void* data = nullptr;
   int64_t offset = 0, version = 0, tag = 0;
   uint64_t epoch = 0, generation = 0;
-  std::array<int64_t, 4> sizes{};
+  std::array<int64_t, 4> sizes{}, strides{};
   bool dgrad = false;
   at::Tensor wt;
   uint64_t last_use = 0;
@@ -204,10 +206,18 @@ int64_t refresh_graph_weights(int64_t pool) {
   return n;
 }
 
+void purge_capture_entries(int64_t tag);
+
+// Drops everything kept for a captured graph's pool: its adopted frozen weights and the
+// prepared weights and kept packs made under its capture tag (never served again, since
+// tags are unique pool ids, but holding their device memory until evicted).
 void release_graph_weights(int64_t pool) {
-  GraphWeights& g = graph_weights();
-  std::lock_guard<std::mutex> lock(g.mu);
-  g.by_pool.erase(pool);
+  {
+    GraphWeights& g = graph_weights();
+    std::lock_guard<std::mutex> lock(g.mu);
+    g.by_pool.erase(pool);
+  }
+  if (pool != 0) purge_capture_entries(pool);
 }
 
 namespace {
@@ -215,10 +225,13 @@ namespace {
 bool weight_cacheable(const at::Tensor& w) { return !w.is_inference() && w.dim() == 4; }
 
 std::array<int64_t, 4> sizes4(const at::Tensor& w) { return {w.size(0), w.size(1), w.size(2), w.size(3)}; }
+std::array<int64_t, 4> strides4(const at::Tensor& w) {
+  return {w.stride(0), w.stride(1), w.stride(2), w.stride(3)};
+}
 
 bool same_weight(const PreparedWeights& e, const at::Tensor& w, bool dgrad, int64_t tag) {
   return e.dgrad == dgrad && e.tag == tag && e.offset == w.storage_offset() && e.data == w.storage().data() &&
-         e.sizes == sizes4(w);
+         e.sizes == sizes4(w) && e.strides == strides4(w);
 }
 
 at::Tensor cached_weights(const at::Tensor& w, bool dgrad, int64_t tag) {
@@ -274,6 +287,7 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt, int
   e.generation = gen;
   e.tag = tag;
   e.sizes = sizes4(w);
+  e.strides = strides4(w);
   e.dgrad = dgrad;
   e.wt = wt;
   e.last_use = ++c.tick;
@@ -462,6 +476,52 @@ void clear_packed_inputs() {
   std::lock_guard<std::mutex> lock(c.mu);
   c.entries.clear();
   c.bytes = 0;
+}
+
+std::vector<int64_t> cache_stats(int64_t tag) {
+  std::vector<int64_t> out(4, 0);
+  {
+    WeightCache& c = weight_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    for (const auto& e : c.entries) {
+      if (tag >= 0 && e.tag != tag) continue;
+      out[0] += 1;
+      out[1] += int64_t(e.wt.nbytes());
+    }
+  }
+  PackedInputCache& c = packed_input_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (const auto& e : c.entries) {
+    if (tag >= 0 && e.tag != tag) continue;
+    out[2] += 1;
+    out[3] += int64_t(e.packed.nbytes());
+  }
+  return out;
+}
+
+void purge_capture_entries(int64_t tag) {
+  {
+    WeightCache& c = weight_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    for (auto it = c.entries.begin(); it != c.entries.end();) {
+      if (it->tag == tag) {
+        c.bytes -= size_t(it->wt.nbytes());
+        it = c.entries.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+  PackedInputCache& c = packed_input_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (auto it = c.entries.begin(); it != c.entries.end();) {
+    if (it->tag == tag) {
+      c.bytes -= size_t(it->packed.nbytes());
+      it = c.entries.erase(it);
+    } else {
+      ++it;
+    }
+  }
 }
 
 namespace {

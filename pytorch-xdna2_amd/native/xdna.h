@@ -95,6 +95,9 @@ void clear_packed_inputs();
 // or forget them (when the graph is released) (ops.cpp).
 int64_t refresh_graph_weights(int64_t pool);
 void release_graph_weights(int64_t pool);
+// Entries of the prepared-weight and kept-pack caches made under capture tag `tag` (all
+// entries for tag < 0): {weights, weight bytes, packs, pack bytes} (ops.cpp).
+std::vector<int64_t> cache_stats(int64_t tag);
 
 // Weight-gradient launches so far (ops.cpp).
 int64_t dw_jobs();

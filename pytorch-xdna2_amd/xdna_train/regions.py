@@ -27,8 +27,8 @@ Regions (``XDNA_REGIONS=0`` turns them off; anything ineligible runs the eager o
 * :func:`frozen_feature_mse` / :func:`fuse_perceptual_loss`: the reference's perceptual
   loss, mean over the concatenated tap elements of (features(x) - features(target))^2;
 * :func:`frozen_feature_loss`: the same chain with Gram-matrix style terms as well
-  (w * mean((F F^T / chw - T)^2) per style tap, the style-transfer loss of the BASELINE
-  style configuration), an fp32 loss like the eager ``.float()`` losses it replaces;
+  (w * mean((F F^T / chw - T)^2) per style tap, the loss of a style-transfer training
+  step), an fp32 loss like the eager ``.float()`` losses it replaces;
 * :func:`fuse_norm_activation` / :func:`fuse_norm_activations`: a training BatchNorm2d or
   InstanceNorm2d and the ReLU / LeakyReLU applied to its output as one kernel pair, the
   activation in the norm's output store and its mask in the norm's backward sums.
@@ -36,9 +36,7 @@ Regions (``XDNA_REGIONS=0`` turns them off; anything ineligible runs the eager o
 from __future__ import annotations
 
 import os
-import types
 import weakref
-from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
@@ -54,40 +52,66 @@ def enabled() -> bool:
     return os.environ.get("XDNA_REGIONS", "1") != "0"
 
 
-def _exactly(m: nn.Module, cls) -> bool:
-    """m is ``cls`` itself and runs nothing around its forward that a region would skip:
-    no instance-level forward, no module or global hooks, no parametrization."""
-    if type(m) is not cls or "forward" in m.__dict__:
+def _call_extras(m: nn.Module) -> tuple:
+    """What calling ``m`` runs besides ``type(m).forward``, whose arithmetic is all a
+    region reproduces: an instance-level forward, module or global hooks, a
+    parametrization.  Empty for a module that is called plainly."""
+    found = []
+    if "forward" in vars(m):
+        found.append("instance forward")
+    for attr in ("_forward_pre_hooks", "_forward_hooks", "_backward_pre_hooks", "_backward_hooks"):
+        if len(getattr(m, attr)):
+            found.append(attr.lstrip("_"))
+    if len(_modmod._global_forward_pre_hooks) or len(_modmod._global_forward_hooks):
+        found.append("global forward hooks")
+    if parametrize.is_parametrized(m):
+        found.append("parametrization")
+    return tuple(found)
+
+
+def _conv_state(m: nn.Conv2d):
+    if m.padding_mode != "zeros" or isinstance(m.padding, str):
+        return None
+    return (m.weight, m.bias, tuple(m.stride), tuple(m.padding), tuple(m.dilation), m.groups)
+
+
+def _pool2_state(m: nn.MaxPool2d):
+    def pair(v, want):
+        return v == want or v == (want, want)
+    shape_ok = pair(m.kernel_size, 2) and pair(m.stride, 2) and pair(m.padding, 0) and pair(m.dilation, 1)
+    return () if shape_ok and not m.ceil_mode and not m.return_indices else None
+
+
+# exact module type -> (kind, state function); a state is what the region's result depends
+# on beyond the kind, or None when the module's configuration is not supported
+_LAYER_KINDS = {
+    nn.Conv2d: ("conv", _conv_state),
+    nn.ReLU: ("relu", lambda m: ()),
+    nn.MaxPool2d: ("maxpool2", _pool2_state),
+}
+
+
+def _describe(m: nn.Module):
+    """(kind, state) of a layer the region can run, else None.  Exact types only: a
+    subclass may compute something else in its forward."""
+    entry = _LAYER_KINDS.get(type(m))
+    if entry is None or _call_extras(m):
+        return None
+    state = entry[1](m)
+    return None if state is None else (entry[0], state)
+
+
+def _same_description(a, b) -> bool:
+    """Descriptions compared with tensors by identity (a replaced weight is a new layer)."""
+    if a is None or b is None or a[0] != b[0] or len(a[1]) != len(b[1]):
         return False
-    if m._forward_hooks or m._forward_pre_hooks or m._backward_hooks or m._backward_pre_hooks:
-        return False
-    if _modmod._global_forward_hooks or _modmod._global_forward_pre_hooks:
-        return False
-    return not parametrize.is_parametrized(m)
-
-
-def _signature(m: nn.Module):
-    """What the chain depends on for one layer (re-checked on every call), or None."""
-    if _exactly(m, nn.Conv2d):
-        if m.padding_mode != "zeros" or isinstance(m.padding, str):
-            return None
-        return ("conv", id(m), id(m.weight), id(m.bias), tuple(m.stride), tuple(m.padding), tuple(m.dilation),
-                m.groups)
-    if _exactly(m, nn.ReLU):
-        return ("relu", id(m))
-    if _exactly(m, nn.MaxPool2d):
-        two = lambda v: v in (2, (2, 2))
-        if (two(m.kernel_size) and two(m.stride) and m.padding in (0, (0, 0)) and m.dilation in (1, (1, 1))
-                and not m.ceil_mode and not m.return_indices):
-            return ("maxpool2", id(m))
-    return None
-
-
-@dataclass
-class _Op:
-    kind: str                 # "conv" | "relu" | "maxpool2"
-    module: nn.Module
-    fused_relu: bool = False  # conv whose following ReLU runs in its epilogue
+    for u, v in zip(a[1], b[1]):
+        if isinstance(u, torch.Tensor) or isinstance(v, torch.Tensor):
+            if u is not v:
+                return False
+        elif u != v:
+            return False
+    return True
 
 
 def _conv3x3_s1(m: nn.Conv2d) -> bool:
@@ -97,48 +121,45 @@ def _conv3x3_s1(m: nn.Conv2d) -> bool:
 
 class FrozenFeatureChain:
     """A parsed ``layers[0 .. max(taps)]`` of conv / ReLU / 2x2 max-pool modules with
-    frozen weights; ``taps`` are the layer indices whose outputs the loss reads."""
+    frozen weights; ``taps`` are the layer indices whose outputs the loss reads.
 
-    def __init__(self, layers, taps, sig):
+    ``kinds[i]`` is layer i's kind ("conv", "relu" or "maxpool2"); ``fused_relu[i]`` is
+    True for a 3x3 stride-1 conv that applies the following ReLU in its epilogue (not
+    done when the loss reads the conv's own output)."""
+
+    def __init__(self, layers, taps, descriptions):
         self.layers = layers
         self.taps = taps
-        self.sig = sig
-        tapset = set(taps)
-        self.ops: list[_Op] = []
-        for i, m in enumerate(layers):
-            kind = sig[i][0]
-            op = _Op(kind, m)
-            # conv + ReLU in one launch unless the loss reads the pre-activation
-            if (kind == "conv" and i + 1 < len(layers) and sig[i + 1][0] == "relu" and i not in tapset
-                    and _conv3x3_s1(m)):
-                op.fused_relu = True
-            self.ops.append(op)
+        self._descriptions = descriptions
+        self.kinds = tuple(d[0] for d in descriptions)
+        read = set(taps)
+        self.fused_relu = tuple(
+            k == "conv" and i + 1 < len(layers) and self.kinds[i + 1] == "relu" and i not in read
+            and _conv3x3_s1(layers[i])
+            for i, k in enumerate(self.kinds))
 
     @classmethod
     def from_sequential(cls, layers, taps) -> "FrozenFeatureChain | None":
-        """The chain of ``layers[0 .. max(taps)]``, or None if a layer is not a plain
-        Conv2d / ReLU / MaxPool2d(2, 2), a weight is trainable, or the first layer is not
-        a conv (it reads the image)."""
-        layers = list(layers)
+        """The chain of ``layers[0 .. max(taps)]``, or None when some layer is not a plain
+        Conv2d / ReLU / MaxPool2d(2, 2), a conv parameter is trainable, or the first layer
+        is not a conv (the region's first pass reads the image through a conv)."""
         taps = tuple(sorted({int(t) for t in taps}))
+        layers = list(layers)
         if not taps or taps[0] < 0 or taps[-1] >= len(layers):
             return None
         layers = layers[: taps[-1] + 1]
-        sig = []
-        for m in layers:
-            s = _signature(m)
-            if s is None:
-                return None
-            if s[0] == "conv" and (m.weight.requires_grad or (m.bias is not None and m.bias.requires_grad)):
-                return None
-            sig.append(s)
-        if sig[0][0] != "conv":
+        descriptions = tuple(_describe(m) for m in layers)
+        if any(d is None for d in descriptions) or descriptions[0][0] != "conv":
             return None
-        return cls(layers, taps, tuple(sig))
+        for m, d in zip(layers, descriptions):
+            if d[0] == "conv" and any(p.requires_grad for p in m.parameters(recurse=False)):
+                return None
+        return cls(layers, taps, descriptions)
 
     def current(self) -> bool:
-        """The layers still are what the chain was parsed from (strides, hooks, weights)."""
-        return tuple(_signature(m) for m in self.layers) == self.sig
+        """The layers are still what the chain was parsed from (types, strides, hooks, the
+        weight and bias objects)."""
+        return all(_same_description(_describe(m), d) for m, d in zip(self.layers, self._descriptions))
 
     def eligible(self, x: torch.Tensor, target: torch.Tensor | None = None) -> bool:
         if not enabled() or not isinstance(x, torch.Tensor) or x.device.type != "xdna":
@@ -152,10 +173,10 @@ class FrozenFeatureChain:
             return False  # the region's backward produces dX only
         if not self.current():
             return False
-        for op in self.ops:
-            if op.kind != "conv":
+        for m, kind in zip(self.layers, self.kinds):
+            if kind != "conv":
                 continue
-            w, b = op.module.weight, op.module.bias
+            w, b = m.weight, m.bias
             if w.device.type != "xdna" or w.dtype != torch.bfloat16 or w.requires_grad:
                 return False
             if b is not None and (b.device.type != "xdna" or b.dtype != torch.bfloat16 or b.requires_grad):
@@ -166,14 +187,13 @@ class FrozenFeatureChain:
 def _run(chain: FrozenFeatureChain, x: torch.Tensor, upto: int):
     """outs[i] = output of layer i for i <= upto (None for a conv whose ReLU is fused)."""
     C = _dev.native()
-    outs: list[torch.Tensor | None] = [None] * len(chain.ops)
+    outs: list[torch.Tensor | None] = [None] * len(chain.layers)
     cur = x
     i = 0
     while i <= upto:
-        op = chain.ops[i]
-        m = op.module
-        if op.kind == "conv":
-            if op.fused_relu and i + 1 <= upto:
+        m, kind = chain.layers[i], chain.kinds[i]
+        if kind == "conv":
+            if chain.fused_relu[i] and i + 1 <= upto:
                 cur = C.region_conv3x3(cur.contiguous(), m.weight, m.bias, 1)
                 outs[i + 1] = cur
                 i += 2
@@ -182,7 +202,7 @@ def _run(chain: FrozenFeatureChain, x: torch.Tensor, upto: int):
                 cur = C.region_conv3x3(cur.contiguous(), m.weight, m.bias, 0)
             else:
                 cur = torch.nn.functional.conv2d(cur, m.weight, m.bias, m.stride, m.padding, m.dilation, m.groups)
-        elif op.kind == "relu":
+        elif kind == "relu":
             cur = torch.relu(cur)
         else:
             cur = C.region_maxpool2(cur.contiguous())
@@ -204,7 +224,7 @@ class _FrozenFeatureLoss(torch.autograd.Function):
         last = max(list(mse_taps) + list(style.keys()))
         with torch.no_grad():
             outs = _run(chain, x, last)
-            t_outs = _run(chain, target, max(mse_taps)) if mse_taps else [None] * len(chain.ops)
+            t_outs = _run(chain, target, max(mse_taps)) if mse_taps else [None] * len(chain.layers)
             nterms = len(mse_taps) + len(style)
             part = torch.empty(nterms * parts, dtype=torch.float32, device=x.device)
             total = sum(outs[k].numel() for k in mse_taps)
@@ -241,7 +261,7 @@ class _FrozenFeatureLoss(torch.autograd.Function):
         saved = ctx.saved_tensors  # raises if a saved tensor was written in place
         x = saved[0]
         n = 1
-        outs = [None] * len(chain.ops)
+        outs = [None] * len(chain.layers)
         for i in keep:
             outs[i] = saved[n]
             n += 1
@@ -275,10 +295,10 @@ class _FrozenFeatureLoss(torch.autograd.Function):
         G = None   # gradient with respect to the output of layer k
         Gp = None  # gradient with respect to a max-pool's output, not yet routed
         for k in range(last, -1, -1):
-            op = chain.ops[k]
-            if op.kind == "conv" and op.fused_relu:
+            kind = chain.kinds[k]
+            if kind == "conv" and chain.fused_relu[k]:
                 pass  # the ReLU above produced the gradient of the pre-activation
-            elif op.kind == "maxpool2":
+            elif kind == "maxpool2":
                 # gradient of this pool's output: routed from a pool above (whose input
                 # this output is) and the tap terms; it is routed to the window maxima of
                 # this pool's input by the layer below
@@ -291,14 +311,14 @@ class _FrozenFeatureLoss(torch.autograd.Function):
             else:
                 ta, tb, extra = tap_terms(k)
                 src = outs[k]
-                if op.kind == "relu" or Gp is not None or ta is not None or extra is not None:
-                    G = C.region_backward(src if op.kind == "relu" else None, G, Gp, src if Gp is not None else None,
+                if kind == "relu" or Gp is not None or ta is not None or extra is not None:
+                    G = C.region_backward(src if kind == "relu" else None, G, Gp, src if Gp is not None else None,
                                           extra, ta, tb, mse_scale, go, list(src.shape))
                     Gp = None
-                if op.kind == "relu":
+                if kind == "relu":
                     continue
             # conv: the input gradient through the backend's conv path (frozen weight: dX only)
-            m = op.module
+            m = chain.layers[k]
             inp = outs[k - 1] if k > 0 else x
             G = torch.ops.aten.convolution_backward(G, inp, m.weight, None, list(m.stride), list(m.padding),
                                                     list(m.dilation), False, [0, 0], m.groups,
@@ -374,81 +394,109 @@ def _eager_loss(chain, x, target, mse_taps, style, mse_weight):
 
 
 # ---------------------------------------------------------------------------------------
-# Routing a loss module's perceptual loss through the region (the reference's
-# fuse_perceptual_loss, regions.py:351-425)
+# A loss module's perceptual loss through the region (the interface of the reference's
+# fuse_perceptual_loss, regions.py:392-425)
 # ---------------------------------------------------------------------------------------
-def _module_chain(loss_module):
-    cfg = loss_module.__dict__["_xdna_region_cfg"]
-    net = getattr(loss_module, cfg["features_attr"], None)
+def _perceptual_layers(net):
+    """(layers, taps) of a feature network in the loss-module pattern: ``net.model.features``
+    (a Sequential) and ``net.feature_layers`` (tap indices); None otherwise."""
     feats = getattr(getattr(net, "model", None), "features", None)
     taps = getattr(net, "feature_layers", None)
-    if feats is None or taps is None or not len(taps):
+    if feats is None or taps is None or len(taps) == 0:
         return None
-    layers = list(feats)[: max(taps) + 1]
-    chain = loss_module.__dict__.get("_xdna_chain")
-    if chain is not None and (chain.taps != tuple(sorted({int(t) for t in taps})) or chain.layers != layers
-                              or not chain.current()):
-        chain = None
-    if chain is None:
-        chain = FrozenFeatureChain.from_sequential(layers, taps)
-        loss_module.__dict__["_xdna_chain"] = chain
-    return chain
+    taps = tuple(sorted({int(t) for t in taps}))
+    return list(feats)[: taps[-1] + 1], taps
 
 
-def _fused_perceptual(self, input, target):
-    """Bound to the loss module: everything is read from ``self`` at call time."""
-    chain = _module_chain(self)
-    if chain is None or not chain.eligible(input, target):
-        return type(self).compute_perceptual_loss(self, input, target)
-    net = getattr(self, self.__dict__["_xdna_region_cfg"]["features_attr"])
-    x, t = input, target
-    if getattr(net, "use_norm", False):
-        norm = getattr(net, "norm", None)
-        mean, std = getattr(norm, "mean", None), getattr(norm, "std", None)
-        if mean is None or std is None:
-            return type(self).compute_perceptual_loss(self, input, target)
-        m = torch.as_tensor(mean, dtype=x.dtype, device=x.device).view(1, -1, 1, 1)
-        s = torch.as_tensor(std, dtype=x.dtype, device=x.device).view(1, -1, 1, 1)
-        x, t = (x - m) / s, (t - m) / s
-    return _FrozenFeatureLoss.apply(chain, x, t, chain.taps, {}, 1.0, True)
+def _input_normalizer(net):
+    """``(mean, std)`` the network applies to its inputs first (``use_norm`` with a ``norm``
+    holding both), ``()`` when it applies none, None when it names a norm the region
+    cannot reproduce."""
+    if not getattr(net, "use_norm", False):
+        return ()
+    norm = getattr(net, "norm", None)
+    mean, std = getattr(norm, "mean", None), getattr(norm, "std", None)
+    return None if mean is None or std is None else (mean, std)
+
+
+class _PerceptualRoute:
+    """What ``loss_module.compute_perceptual_loss`` becomes once routed: a callable that
+    holds its module (``owner``) and the name of the feature network's attribute, and
+    decides on every call between the region and the class's own method.
+
+    It is an instance attribute of the module, so ``copy.deepcopy`` of the module copies it
+    with ``owner`` pointing at the copy (deepcopy's memo), and the copy runs on its own
+    weights.  The parsed chain is kept with the layer identities it was parsed from and
+    rebuilt when the module's feature layers, taps or their state change."""
+
+    def __init__(self, owner, features_attr: str):
+        self.owner = owner
+        self.features_attr = features_attr
+        self._parsed = None  # (layer ids, taps, chain or None)
+
+    def chain(self):
+        found = _perceptual_layers(getattr(self.owner, self.features_attr, None))
+        if found is None:
+            return None
+        layers, taps = found
+        ids = tuple(id(m) for m in layers)
+        parsed = self._parsed
+        fresh = parsed is not None and parsed[:2] == (ids, taps) and parsed[2] is not None and parsed[2].current()
+        if not fresh:  # a layer that did not parse may have become eligible since
+            parsed = self._parsed = (ids, taps, FrozenFeatureChain.from_sequential(layers, taps))
+        return parsed[2]
+
+    def __call__(self, input, target):
+        chain = self.chain()
+        scale = _input_normalizer(getattr(self.owner, self.features_attr, None))
+        if chain is None or scale is None or not chain.eligible(input, target):
+            return type(self.owner).compute_perceptual_loss(self.owner, input, target)
+        if scale:
+            shape = (1, -1, 1, 1)
+            mean = torch.as_tensor(scale[0], dtype=input.dtype, device=input.device).view(shape)
+            std = torch.as_tensor(scale[1], dtype=input.dtype, device=input.device).view(shape)
+            input, target = (input - mean) / std, (target - mean) / std
+        return _FrozenFeatureLoss.apply(chain, input, target, chain.taps, {}, 1.0, True)
 
 
 def fuse_perceptual_loss(loss_module, features_attr: str = "perceptual_vgg") -> bool:
-    """Routes ``loss_module.compute_perceptual_loss`` through the region when the module
-    follows the reference's pattern (regions.py:392-425): ``getattr(loss_module,
-    features_attr)`` has ``model.features`` (a Sequential), ``feature_layers`` (tap
-    indices), optional ``use_norm`` / ``norm`` (mean / std), and the loss is the mean
-    squared tap difference.  Every call re-checks eligibility; anything else takes the
-    module's own method.  The wrapper is bound to the module, so a deepcopy uses its own
-    weights.  Returns True if the region was installed."""
-    if not enabled():
+    """Routes ``loss_module.compute_perceptual_loss(input, target)`` through the region.
+
+    The module must follow the loss-module pattern: ``getattr(loss_module, features_attr)``
+    has ``model.features`` (a Sequential), ``feature_layers`` (tap indices) and optionally
+    ``use_norm`` with a ``norm`` holding ``mean`` / ``std``; its loss is the mean squared
+    difference of the concatenated taps.  Returns False, installing nothing, when the
+    pattern or the chain does not fit now.  Once installed, every call checks again and
+    falls back to the class's own ``compute_perceptual_loss`` for anything the region does
+    not take (trainable or replaced feature layers, other dtypes or devices)."""
+    if not enabled() or not hasattr(loss_module, "compute_perceptual_loss"):
         return False
     net = getattr(loss_module, features_attr, None)
-    feats = getattr(getattr(net, "model", None), "features", None)
-    taps = getattr(net, "feature_layers", None)
-    if feats is None or taps is None or not len(taps) or not hasattr(loss_module, "compute_perceptual_loss"):
+    found = _perceptual_layers(net)
+    if found is None or _input_normalizer(net) is None:
         return False
-    if FrozenFeatureChain.from_sequential(list(feats)[: max(taps) + 1], taps) is None:
+    if FrozenFeatureChain.from_sequential(*found) is None:
         return False
-    if getattr(net, "use_norm", False):
-        norm = getattr(net, "norm", None)
-        if getattr(norm, "mean", None) is None or getattr(norm, "std", None) is None:
-            return False
-    loss_module.__dict__["_xdna_region_cfg"] = {"features_attr": features_attr}
-    loss_module.compute_perceptual_loss = types.MethodType(_fused_perceptual, loss_module)
+    vars(loss_module)["compute_perceptual_loss"] = _PerceptualRoute(loss_module, features_attr)
     return True
 
 
+def perceptual_route(loss_module):
+    """The installed route of ``fuse_perceptual_loss`` (its ``chain()`` is the parsed
+    region), or None."""
+    route = vars(loss_module).get("compute_perceptual_loss")
+    return route if isinstance(route, _PerceptualRoute) else None
+
+
 # ---------------------------------------------------------------------------------------
-# A training norm and the activation applied to its output as one pass each way (the
-# reference's fuse_norm_activation, regions.py:426-546), for BatchNorm2d and, beyond the
-# reference, InstanceNorm2d
+# A training norm and the activation applied to its output, one kernel each way (the
+# interface of the reference's fuse_norm_activation, regions.py:521-546, for BatchNorm2d
+# and, beyond the reference, InstanceNorm2d)
 # ---------------------------------------------------------------------------------------
 # Smallest input (bytes) that takes the fused op.  On the GPU the fused pair saves a full
 # elementwise pass and its launch each way at every size, so every size is fused unless
 # this is raised (the reference's knob; its CPU kernels only win above ~4 MB).
 _NORM_ACT_MIN_BYTES = int(os.environ.get("XDNA_REGION_NORM_ACT_MIN_BYTES", "0"))
-
 
 class _NormAct(torch.autograd.Function):
     """y = act(norm(x)) with training statistics on contiguous NCHW bf16, act applied in
@@ -476,125 +524,171 @@ class _NormAct(torch.autograd.Function):
                 None, None, None, None, None, None, None)
 
 
-def _act_code(act):
-    """(code, slope) for the kernels, or None: exact types only (a subclass may override
-    forward, which the fused op would skip); a negative slope makes y > 0 no longer the
-    input's sign, so it stays eager."""
-    if type(act) is nn.ReLU:
-        return 1, 0.0
-    if type(act) is nn.LeakyReLU and float(act.negative_slope) >= 0.0:
-        return 2, float(act.negative_slope)
-    return None
+# Activations the fused kernels apply: exact type -> kernel code.  A subclass may override
+# forward, which the fused op would skip.
+_ACT_KERNEL_CODES = {nn.ReLU: 1, nn.LeakyReLU: 2}
+_NORM_TYPES = (nn.BatchNorm2d, nn.InstanceNorm2d)
 
 
-def _param_ok(t, x, dtypes):
+def _act_kernel_args(act):
+    """(code, slope) for the kernels, or None.  A negative LeakyReLU slope stays eager: the
+    backward reads the activation's mask from the output's sign, which then flips."""
+    code = _ACT_KERNEL_CODES.get(type(act))
+    slope = float(getattr(act, "negative_slope", 0.0)) if code == 2 else 0.0
+    return None if code is None or slope < 0.0 else (code, slope)
+
+
+def _vector_like(t, x, dtypes) -> bool:
+    """t is a contiguous 1-D per-channel tensor of x on x's device."""
     return (isinstance(t, torch.Tensor) and t.device == x.device and t.dtype in dtypes and t.is_contiguous()
             and t.dim() == 1 and t.numel() == x.shape[1])
 
 
-def _norm_act_args(norm, x):
-    """(running_mean, running_var, momentum, instance) when the fused op applies, else None."""
-    if not enabled() or not norm.affine:
+def _norm_plan(norm, x):
+    """How the fused kernels run ``norm`` on ``x``: (running_mean, running_var, momentum,
+    per_image), or None when the module's own forward must run (eval mode, running
+    statistics the kernels do not keep, unsupported tensors)."""
+    if not enabled() or not norm.affine or len(norm._forward_hooks) or len(_modmod._global_forward_hooks):
+        return None  # a forward hook may replace the output, which would then be activated twice
+    if not isinstance(x, torch.Tensor) or x.device.type != "xdna" or x.dtype != torch.bfloat16:
         return None
-    # a forward hook may replace the output, which would then be activated twice
-    if norm._forward_hooks or _modmod._global_forward_hooks:
+    if x.dim() != 4 or not x.is_contiguous() or 2 * x.numel() < max(_NORM_ACT_MIN_BYTES, 1):
         return None
-    if not isinstance(x, torch.Tensor) or x.dim() != 4 or x.device.type != "xdna":
-        return None
-    if x.dtype != torch.bfloat16 or not x.is_contiguous() or x.numel() * 2 < max(_NORM_ACT_MIN_BYTES, 1):
-        return None
-    floats = (torch.bfloat16, torch.float32)
-    w, b = norm.weight, norm.bias
-    if not (_param_ok(w, x, floats) and _param_ok(b, x, floats)) or w.dtype != b.dtype:
+    params = (torch.bfloat16, torch.float32)
+    if not (_vector_like(norm.weight, x, params) and _vector_like(norm.bias, x, params)
+            and norm.weight.dtype == norm.bias.dtype):
         return None
     plane = x.shape[2] * x.shape[3]
     if type(norm) is nn.InstanceNorm2d:
-        # running statistics (used or updated) stay eager; planes of one element are the
-        # eager path's error
-        if norm.track_running_stats or plane <= 1 or plane > 65536:
-            return None
-        return None, None, 0.0, True
+        # statistics per (image, channel) plane; running statistics stay eager, and so do
+        # one-element planes (the eager path's error)
+        ok = not norm.track_running_stats and 1 < plane <= 65536
+        return (None, None, 0.0, True) if ok else None
     if not norm.training or x.shape[0] * plane <= 1:
         return None
     if not norm.track_running_stats:
         return None, None, 0.0, False
     rm, rv = norm.running_mean, norm.running_var
-    if norm.momentum is None or rm is None or rv is None:  # cumulative average: eager
-        return None
-    if not (_param_ok(rm, x, floats) and _param_ok(rv, x, floats)) or rm.dtype != rv.dtype:
-        return None
-    return rm, rv, float(norm.momentum), False
+    if norm.momentum is None or not (_vector_like(rm, x, params) and _vector_like(rv, x, params)):
+        return None  # a cumulative average (momentum None) stays eager
+    return (rm, rv, float(norm.momentum), False) if rm.dtype == rv.dtype else None
 
 
-def _fused_norm_forward(self, x):
-    """Bound to the norm module (a deepcopy rebinds it to the copy).  The paired activation
-    and its slope are read from ``self`` at call time."""
-    act = self.__dict__.get("_xdna_pair")
-    code = _act_code(act) if act is not None else None
-    args = _norm_act_args(self, x) if code is not None else None
-    if args is None:
-        return type(self).forward(self, x)
-    rm, rv, momentum, instance = args
-    if rm is not None and self.num_batches_tracked is not None:
-        self.num_batches_tracked.add_(1)
-    y = _NormAct.apply(x, self.weight, self.bias, rm, rv, momentum, float(self.eps), code[0], code[1], instance)
-    y._xdna_act_for = weakref.ref(act)
-    return y
+class _ActivationGuard:
+    """``act.forward`` of a paired activation.  It keeps weak references to the tensors that
+    fused norms returned already activated for it; a call on one of them returns it
+    unchanged and forgets it (one pass-through per fused output), and any other call runs
+    the activation's class forward.  One activation may serve several norms."""
+
+    def __init__(self, act):
+        self.act = act
+        self._ready = []
+
+    def expect(self, y):
+        self._ready = [r for r in self._ready if r() is not None]
+        self._ready.append(weakref.ref(y))
+
+    def awaits(self, y) -> bool:
+        return any(r() is y for r in self._ready)
+
+    def __call__(self, x):
+        for i, r in enumerate(self._ready):
+            if r() is x:
+                del self._ready[i]
+                return x
+        return type(self.act).forward(self.act, x)
+
+    def __getstate__(self):  # a copy starts with nothing pending
+        return {"act": self.act, "_ready": []}
 
 
-def _checked_act_forward(self, x):
-    """Passes through, once, a tensor that the paired fused norm already activated, and
-    activates everything else."""
-    ref = getattr(x, "_xdna_act_for", None)
-    if ref is not None and ref() is self:
-        x._xdna_act_for = None  # consumed: a later call on the same tensor activates it
-        return x
-    return type(self).forward(self, x)
+class _FusedNorm:
+    """``norm.forward`` of a paired norm: one fused kernel pair when ``_norm_plan`` accepts the
+    call and the paired activation is still guarded, else the norm's class forward (the
+    activation then runs its own).  Holds both modules, so a deepcopy of a model holding
+    both gets a pair of the copies."""
+
+    def __init__(self, norm, act):
+        self.norm = norm
+        self.act = act
+
+    def __call__(self, x):
+        norm, act = self.norm, self.act
+        guard = vars(act).get("forward")
+        kernel = _act_kernel_args(act) if isinstance(guard, _ActivationGuard) else None
+        plan = _norm_plan(norm, x) if kernel is not None else None
+        if plan is None:
+            return type(norm).forward(norm, x)
+        running_mean, running_var, momentum, per_image = plan
+        if running_mean is not None and norm.num_batches_tracked is not None:
+            norm.num_batches_tracked.add_(1)
+        y = _NormAct.apply(x, norm.weight, norm.bias, running_mean, running_var, momentum, float(norm.eps),
+                           kernel[0], kernel[1], per_image)
+        guard.expect(y)
+        return y
+
+
+def paired_activation(norm: nn.Module):
+    """The activation ``norm`` is paired with by ``fuse_norm_activation``, or None."""
+    fused = vars(norm).get("forward")
+    return fused.act if isinstance(fused, _FusedNorm) else None
+
+
+def awaits_activation(y: torch.Tensor, act: nn.Module) -> bool:
+    """True if ``y`` is a fused norm's output that ``act`` will pass through unchanged."""
+    guard = vars(act).get("forward")
+    return isinstance(guard, _ActivationGuard) and guard.awaits(y)
 
 
 def fuse_norm_activation(norm: nn.Module, act: nn.Module) -> bool:
     """Declares that ``act`` (nn.ReLU or nn.LeakyReLU) is applied directly to the output of
-    ``norm`` (nn.BatchNorm2d or nn.InstanceNorm2d) and runs the pair as one fused op each
-    way, like the reference's fuse_norm_activation (regions.py:521-546).
+    ``norm`` (nn.BatchNorm2d or nn.InstanceNorm2d), so the pair runs as one fused kernel
+    each way.
 
-    Both modules keep their parameters, buffers and state_dict keys; only their forwards
-    are replaced, by methods bound to the modules, so a deepcopy of a model with the pair
-    gives a working pair (copy the two together: the pairing is stored on the norm).  When
-    the fused op applies (affine; BatchNorm2d in training mode with tracked statistics and
-    a float momentum, or none tracked; InstanceNorm2d without running statistics; bf16
-    contiguous NCHW on xdna), ``norm(x)`` returns the activated tensor and the next call of
-    ``act`` on exactly that tensor passes it through once; anything else runs both modules
-    unchanged.  The activation's slope is read on every call.
+    Both modules keep their parameters, buffers and state_dict keys: the pairing lives in
+    callable instance attributes that replace the two forwards (``norm.forward`` holds the
+    pair, ``act.forward`` guards the activation), and a deepcopy of a model holding both
+    modules gives a working pair of the copies.  When the fused op applies (affine;
+    BatchNorm2d in training mode with tracked statistics and a float momentum, or none
+    tracked; InstanceNorm2d without running statistics; bf16 contiguous NCHW on xdna),
+    ``norm(x)`` returns the activated tensor and the next call of ``act`` on exactly that
+    tensor returns it unchanged; anything else runs both modules unchanged.  The
+    activation's slope is read on every call.
 
-    The pairing is the caller's statement about the model's dataflow: if the activation is
-    not applied to the norm's output directly (an add or a branch in between), do not
-    declare the pair.  Returns True if installed (or already installed with ``act``)."""
-    if not enabled() or type(norm) not in (nn.BatchNorm2d, nn.InstanceNorm2d):
+    The caller states the dataflow: an activation that is not applied to the norm's output
+    directly (an add or a branch in between) must not be declared.  Returns True if the
+    pair is installed now or was already installed with ``act``."""
+    if not enabled() or type(norm) not in _NORM_TYPES or type(act) not in _ACT_KERNEL_CODES:
         return False
-    if type(act) not in (nn.ReLU, nn.LeakyReLU):
-        return False
-    if norm.__dict__.get("_xdna_pair") is not None:
-        return norm.__dict__["_xdna_pair"] is act
-    object.__setattr__(norm, "_xdna_pair", act)  # a plain attribute, not a submodule
-    norm.forward = types.MethodType(_fused_norm_forward, norm)
-    if not isinstance(act.forward, types.MethodType) or act.forward.__func__ is not _checked_act_forward:
-        act.forward = types.MethodType(_checked_act_forward, act)
+    current = paired_activation(norm)
+    if current is not None:
+        return current is act
+    if not isinstance(vars(act).get("forward"), _ActivationGuard):
+        vars(act)["forward"] = _ActivationGuard(act)
+    vars(norm)["forward"] = _FusedNorm(norm, act)
     return True
 
 
+def unfuse_norm_activation(norm: nn.Module) -> None:
+    """Removes the pairing of ``norm`` (its activation keeps its guard, which passes through
+    nothing once no norm expects it)."""
+    if isinstance(vars(norm).get("forward"), _FusedNorm):
+        del vars(norm)["forward"]
+
+
 def fuse_norm_activations(model: nn.Module) -> int:
-    """Pairs, in every nn.Sequential of ``model`` (or subclass that keeps its forward), each
-    BatchNorm2d / InstanceNorm2d that is immediately followed by a ReLU / LeakyReLU (such a
-    container feeds each module's output straight to the next, so the dataflow statement
-    holds).  Returns the pairs installed."""
+    """Pairs, in every nn.Sequential of ``model`` whose forward is Sequential's own, each
+    BatchNorm2d / InstanceNorm2d directly followed by a ReLU / LeakyReLU: such a container
+    feeds each module's output straight to the next, so the pairing's dataflow statement
+    holds.  Returns the number of pairs installed."""
     n = 0
-    for m in model.modules():
-        if not isinstance(m, nn.Sequential) or type(m).forward is not nn.Sequential.forward:
+    for seq in model.modules():
+        if not isinstance(seq, nn.Sequential) or type(seq).forward is not nn.Sequential.forward:
             continue
-        if "forward" in m.__dict__ or m._forward_hooks:
+        if "forward" in vars(seq) or len(seq._forward_hooks):
             continue
-        mods = list(m)
-        for a, b in zip(mods, mods[1:]):
-            if type(a) in (nn.BatchNorm2d, nn.InstanceNorm2d) and type(b) in (nn.ReLU, nn.LeakyReLU):
-                n += bool(fuse_norm_activation(a, b))
+        children = list(seq)
+        for first, second in zip(children, children[1:]):
+            if type(first) in _NORM_TYPES and type(second) in _ACT_KERNEL_CODES:
+                n += bool(fuse_norm_activation(first, second))
     return n

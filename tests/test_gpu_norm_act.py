@@ -175,7 +175,7 @@ def test_pairing_contract():
     assert not regions.fuse_norm_activation(nn.BatchNorm2d(4), nn.Sigmoid())
     assert not regions.fuse_norm_activation(nn.LayerNorm(4), nn.ReLU())
     y = norm(x)
-    assert y._xdna_act_for() is act
+    assert regions.awaits_activation(y, act)
     z = act(y)
     assert z is y  # passed through once
     w = act(y)  # a second call activates
@@ -188,16 +188,16 @@ def test_pairing_contract():
     # a negative slope runs both modules unchanged (the output's sign no longer masks)
     act.negative_slope = -0.5
     y3 = norm(x)
-    assert getattr(y3, "_xdna_act_for", None) is None
+    assert not regions.awaits_activation(y3, act)
     # eval mode and CPU tensors: eager
     norm.eval()
-    assert getattr(norm(x), "_xdna_act_for", None) is None
+    assert not regions.awaits_activation(norm(x), act)
     norm.train()
     cpu_norm = make_norm("bn", 8, 1)
     cpu_act = nn.ReLU()
     assert regions.fuse_norm_activation(cpu_norm, cpu_act)
     yc = cpu_act(cpu_norm(x.cpu()))
-    assert getattr(yc, "_xdna_act_for", None) is None and bool((yc >= 0).all())
+    assert not regions.awaits_activation(yc, cpu_act) and bool((yc >= 0).all())
 
 
 def test_deepcopy_keeps_a_working_pair():
@@ -205,8 +205,8 @@ def test_deepcopy_keeps_a_working_pair():
                           nn.Conv2d(8, 8, 3, padding=1), nn.BatchNorm2d(8), nn.LeakyReLU(0.2)).bfloat16().to(X)
     assert regions.fuse_norm_activations(model) == 2
     clone = copy.deepcopy(model)
-    assert clone[1]._xdna_pair is clone[2] and clone[4]._xdna_pair is clone[5]
-    assert clone[1].forward.__self__ is clone[1]
+    assert regions.paired_activation(clone[1]) is clone[2] and regions.paired_activation(clone[4]) is clone[5]
+    assert clone[1].forward.norm is clone[1]
     gen = torch.Generator().manual_seed(4)
     x = torch.randn(2, 4, 16, 16, generator=gen).bfloat16().to(X)
     xdna_train.reset_mapped_cpu_stats()
@@ -216,8 +216,8 @@ def test_deepcopy_keeps_a_working_pair():
     assert st.get("hip_region.batch_norm_act.run", {}).get("calls", 0) == 1
     plain = copy.deepcopy(model)
     for m in plain.modules():
-        m.__dict__.pop("forward", None)
-        m.__dict__.pop("_xdna_pair", None)
+        regions.unfuse_norm_activation(m)
+        m.__dict__.pop("forward", None)  # the activations' guards
     ref = plain(x)
     assert rel_l2(y, ref) <= 2.0 ** -7
 

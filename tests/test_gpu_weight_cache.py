@@ -167,6 +167,56 @@ def test_eager_after_graph_replay_uses_the_replayed_weights():
     graph.reset()
 
 
+@pytest.mark.parametrize("frozen", [True, False], ids=["frozen", "trainable"])
+def test_views_of_one_storage_are_different_weights(frozen):
+    """w and w.transpose(2, 3) share storage, offset, shape, version counter and write
+    epoch; only their strides differ.  Each conv must compute with its own view's values
+    (forward and input gradient against the float64 oracle), in either call order."""
+    import oracle
+    from gpu_util import check_bf16
+    g = torch.Generator().manual_seed(5)
+    w_cpu = (torch.randn(64, 64, 3, 3, generator=g) * 0.05).bfloat16()
+    w = w_cpu.to(X).requires_grad_(not frozen)
+    x, dy = _data()
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    dyb = dy.cpu().view(torch.int16).numpy().view(np.uint16)
+    for label, view in (("w", w), ("w.T", w.transpose(2, 3)), ("w again", w), ("w.T again", w.transpose(2, 3))):
+        xx = x.clone().requires_grad_()
+        y = F.conv2d(xx, view, None, 1, 1)
+        y.backward(dy)
+        vb = view.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+        check_bf16(_bits(y).numpy().view(np.uint16), oracle.conv3x3_fwd(xb, vb), what=f"{label} forward")
+        check_bf16(_bits(xx.grad).numpy().view(np.uint16), oracle.conv3x3_dgrad(dyb, vb), what=f"{label} dgrad")
+
+
+def test_released_graph_drops_its_cache_entries():
+    """Releasing a captured graph drops the prepared weights and kept packs made under its
+    capture tag; the eager entries stay."""
+    torch.manual_seed(0)
+    x, dy = _data()
+    frozen = nn.Conv2d(64, 64, 3, padding=1).bfloat16().to(X).requires_grad_(False)
+    conv = nn.Conv2d(64, 64, 3, padding=1).bfloat16().to(X)
+    C = xdna_train.device.native()
+
+    def step():
+        xx = x.clone().requires_grad_()
+        conv(frozen(xx)).backward(dy)
+
+    step()
+    eager = C.cache_stats(0)
+    graph = torch.xdna.Graph()
+    with torch.xdna.graph(graph):
+        step()
+    graph.replay()
+    torch.xdna.synchronize()
+    assert C.cache_stats(graph.pool)[0] > 0  # trainable forms prepared inside the capture
+    pool = graph.pool
+    graph.reset()
+    torch.xdna.synchronize()
+    assert C.cache_stats(pool) == [0, 0, 0, 0]
+    assert C.cache_stats(0)[0] >= 1 and eager[0] >= 1
+
+
 @pytest.mark.parametrize("make", [
     lambda p: torch.optim.SGD(p, lr=0.5),
     lambda p: torch.optim.SGD(p, lr=0.5, momentum=0.9, weight_decay=0.1),

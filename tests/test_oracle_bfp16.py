@@ -43,10 +43,11 @@ def test_matches_reference_digests(case):
         assert _sha(oracle.pack_weights_dx_bfp16(w, -(-cout // 64), nb)) == digest, f"dx block {nb}"
 
 
-@pytest.mark.skipif(oracle.ref_pack() is None, reason="reference build (oracle/_ref) absent")
 @pytest.mark.parametrize("cin,cout,kind", [(130, 200, "recipe"), (64, 72, "special"), (9, 300, "recipe")])
 def test_matches_reference_build(cin, cout, kind):
-    ref = oracle.ref_pack()
+    ref = oracle.ref_pack()  # looked up here, not at collection: the GPU box has no build
+    if ref is None:
+        pytest.skip("reference build (oracle/_ref) absent: the committed digests pin the BFP16 bytes")
     w = np.ascontiguousarray(bfp16_weights(cin, cout, kind, 77))
     chunks = -(-cin // 64)
     for nb in range(-(-cout // 128)):

@@ -81,12 +81,13 @@ def test_unpack_matches_reference_digest(case):
     assert _sha(out2) == case["unpack"]
 
 
-@pytest.mark.skipif(oracle.ref_pack() is None, reason="reference tree absent (GPU box): digests pin instead")
 @pytest.mark.parametrize("shape", [(1, 1, 1, 1), (2, 65, 3, 40, ), (5, 130, 7, 9), (2, 64, 11, 75),
                                    (3, 17, 2, 100)])
 def test_pack_against_reference_build(shape):
     B, C, H, W = shape
-    ref = oracle.ref_pack()
+    ref = oracle.ref_pack()  # looked up here, not at collection: the GPU box has no build
+    if ref is None:
+        pytest.skip("reference build (oracle/_ref) absent: the committed digests pin the layouts")
     rng = np.random.default_rng(7 + B + C)
     x = oracle.rng_bf16(rng, (B, C, H, W))
     for strips in (False, True):

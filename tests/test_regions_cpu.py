@@ -23,15 +23,14 @@ def test_chain_parses_and_fuses_relus():
     layers = frozen(vgg_block())
     chain = regions.FrozenFeatureChain.from_sequential(layers, [3, 6])
     assert chain is not None and chain.taps == (3, 6)
-    kinds = [op.kind for op in chain.ops]
-    assert kinds == ["conv", "relu", "conv", "relu", "maxpool2", "conv", "relu"]
-    assert [op.fused_relu for op in chain.ops] == [True, False, True, False, False, True, False]
+    assert chain.kinds == ("conv", "relu", "conv", "relu", "maxpool2", "conv", "relu")
+    assert chain.fused_relu == (True, False, True, False, False, True, False)
     assert chain.current()
 
 
 def test_tapped_conv_output_is_not_fused():
     chain = regions.FrozenFeatureChain.from_sequential(frozen(vgg_block()), [2, 3])
-    assert [op.fused_relu for op in chain.ops[:4]] == [True, False, False, False]
+    assert chain.fused_relu[:4] == (True, False, False, False)
 
 
 def test_rejected_chains():
@@ -105,16 +104,19 @@ def test_norm_activation_pairing_on_the_cpu():
     assert not regions.fuse_norm_activation(nn.BatchNorm2d(4), nn.Sigmoid())
     assert not regions.fuse_norm_activation(nn.BatchNorm1d(4), nn.ReLU())
     assert not regions.fuse_norm_activation(nn.InstanceNorm2d(4), nn.GELU())
-    assert "_xdna_pair" not in bn._modules and set(bn.state_dict()) == set(nn.BatchNorm2d(4).state_dict())
+    assert regions.paired_activation(bn) is act and not list(bn.children())
+    assert set(bn.state_dict()) == set(nn.BatchNorm2d(4).state_dict())
     torch.manual_seed(0)
     x = torch.randn(2, 4, 5, 5)
     ref_bn = nn.BatchNorm2d(4)
     y = act(bn(x))
     ref = nn.functional.leaky_relu(ref_bn(x), 0.2)
-    assert torch.equal(y, ref) and getattr(y, "_xdna_act_for", None) is None
+    assert torch.equal(y, ref) and not regions.awaits_activation(y, act)
     assert torch.equal(bn.running_mean, ref_bn.running_mean) and int(bn.num_batches_tracked) == 1
     clone = copy.deepcopy(nn.Sequential(bn, act))
-    assert clone[0]._xdna_pair is clone[1] and clone[0].forward.__self__ is clone[0]
+    assert regions.paired_activation(clone[0]) is clone[1] and clone[0].forward.norm is clone[0]
+    regions.unfuse_norm_activation(clone[0])
+    assert regions.paired_activation(clone[0]) is None and regions.paired_activation(bn) is act
     Generator, _ = bench.style_models(torch, nn)
     assert regions.fuse_norm_activations(Generator()) == 10
 
@@ -122,3 +124,65 @@ def test_norm_activation_pairing_on_the_cpu():
 def test_norm_activation_switch(monkeypatch):
     monkeypatch.setenv("XDNA_REGIONS", "0")
     assert not regions.fuse_norm_activation(nn.BatchNorm2d(4), nn.ReLU())
+
+
+def test_perceptual_route_on_the_cpu():
+    """fuse_perceptual_loss on the loss-module pattern: the route re-parses after model
+    surgery, follows a deepcopy to the copy's own layers, and runs the module's own method
+    for inputs the region does not take (CPU tensors here)."""
+    import copy
+
+    class Norm(nn.Module):
+        mean = [0.5, 0.4, 0.3]
+        std = [0.2, 0.25, 0.3]
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.model = nn.Module()
+            self.model.features = nn.Sequential(*frozen(vgg_block()))
+            self.feature_layers = [3, 6]
+            self.use_norm = True
+            self.norm = Norm()
+
+    class Loss(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.perceptual_vgg = Net()
+            self.own_calls = 0
+
+        def compute_perceptual_loss(self, input, target):
+            self.own_calls += 1
+            f = self.perceptual_vgg.model.features
+            return ((f(input) - f(target)) ** 2).mean()
+
+    lm = Loss()
+    assert regions.perceptual_route(lm) is None
+    assert regions.fuse_perceptual_loss(lm)
+    route = regions.perceptual_route(lm)
+    assert route is not None and route.owner is lm
+    chain = route.chain()
+    assert chain.taps == (3, 6) and chain.layers == list(lm.perceptual_vgg.model.features)
+    assert route.chain() is chain  # cached while nothing changes
+    x, t = torch.rand(1, 3, 8, 8), torch.rand(1, 3, 8, 8)
+    got = lm.compute_perceptual_loss(x, t)
+    assert lm.own_calls == 1 and torch.equal(got, Loss.compute_perceptual_loss(lm, x, t))
+    clone = copy.deepcopy(lm)
+    croute = regions.perceptual_route(clone)
+    assert croute.owner is clone and croute.chain().layers == list(clone.perceptual_vgg.model.features)
+    lm.perceptual_vgg.model.features[2].stride = (2, 2)  # surgery: parsed again
+    strided = route.chain()
+    assert strided is not chain and strided.fused_relu[2] is False and strided.current()
+    handle = lm.perceptual_vgg.model.features[5].register_forward_hook(lambda *a: None)
+    assert route.chain() is None  # a hooked layer: the module's own method runs
+    handle.remove()
+    assert route.chain() is not None
+    lm.perceptual_vgg.feature_layers = [1]
+    assert route.chain().taps == (1,)
+    # patterns the region cannot take are not installed
+    bad = Loss()
+    bad.perceptual_vgg.model.features[0].weight.requires_grad_(True)
+    assert not regions.fuse_perceptual_loss(bad) and regions.perceptual_route(bad) is None
+    nonorm = Loss()
+    nonorm.perceptual_vgg.norm = nn.Module()
+    assert not regions.fuse_perceptual_loss(nonorm)
