@@ -217,7 +217,8 @@ def build_c1(torch, device, fused=True):
     conv = torch.nn.Conv2d(128, 128, 3, padding=1).bfloat16().to(device)
     x = torch.randn(16, 128, 36, 36).bfloat16().to(device)
     target = torch.zeros(16, 128, 36, 36, device=device)
-    opt = torch.optim.Adam(conv.parameters(), lr=1e-3, fused=fused)
+    # capturable: the step may be captured in a graph (same fused Adam kernel either way)
+    opt = torch.optim.Adam(conv.parameters(), lr=1e-3, fused=fused, capturable=device.type != "cpu")
 
     def step():
         opt.zero_grad(set_to_none=True)
@@ -307,14 +308,18 @@ def conv_sweep_data(torch, device, shapes, first_index=0):
     return data
 
 
-def conv_step(torch, data):
-    # The weights are trainable tensors (requires_grad): their layout is prepared on every
-    # call, as in training, where the optimizer rewrites them each step.  no_grad: the
-    # aten calls are the whole step, nothing is recorded for autograd.
+def conv_step(torch, data, note_write=None):
+    """fwd + dgrad + wgrad (+ bias grad) of every shape through the aten ops.  note_write:
+    called on each weight first, recording a write as the optimizer step of a training
+    step makes, so the weight's prepared forms are made again (as in training); None leaves
+    the weights unwritten, so the forms cached by the previous step serve.  no_grad: the
+    aten calls are the whole step, nothing is recorded for autograd."""
     aten = torch.ops.aten
     s, p, d, op = [1, 1], [1, 1], [1, 1], [0, 0]
     with torch.no_grad():
         for x, w, b, dy in data:
+            if note_write is not None:
+                note_write(w)
             aten.convolution_overrideable(x, w, b, s, p, d, False, op, 1)
             aten.convolution_backward_overrideable(dy, x, w, s, p, d, False, op, 1, [True, True, True])
 
@@ -396,6 +401,7 @@ def sweep_sample_step(torch, device):
 CPU_WORKLOADS = {
     # name -> (builder(torch, device) -> step, warmup, steps, unit, work per step)
     "conv_sweep_sample": (lambda t, d: sweep_sample_step(t, d), 1, 3, "TFLOP/s", sweep_flops(CPU_SWEEP_SAMPLE)),
+    "c1_default_adam": (lambda t, d: build_c1(t, d, fused=None)[0], 3, 20, "it/s", 1.0),
     "style_default_adam": (lambda t, d: build_style(t, d, fused=None)[0], 3, 20, "it/s", 1.0),
     "style_fused_adam": (lambda t, d: build_style(t, d, fused=True)[0], 3, 20, "it/s", 1.0),
     "resnet18_default_adam": (lambda t, d: build_resnet(t, d, fused=None)[0], 2, 5, "it/s", 1.0),
@@ -476,11 +482,78 @@ def kernel_summary(report):
     for name, e in report.items():
         ms = e["total_ms"]
         rate = e["work"] / (ms * 1e-3) if ms > 0 else 0.0
-        is_bytes = name in ("conv3x3w_pack", "fused_adam")
+        is_bytes = name in ("conv3x3w_pack", "fused_adam", "conv3x3_prep")
         out[name] = {"launches": e["launches"], "total_ms": round(ms, 4),
                      "avg_us": round(1e3 * ms / max(1, e["launches"]), 3),
                      ("GB/s" if is_bytes else "TFLOP/s"): round(rate / (1e9 if is_bytes else 1e12), 2)}
     return out
+
+
+def shape_table(torch, C, X, reps=5, cpu=True, log=None):
+    """Per-shape figures of the sweep (BASELINE.md's C2 report, after
+    benchmarks/conv_shape_sweep.py:60-126): each shape's fwd + dgrad + wgrad step with its
+    weight written first (wall time over `reps` steps), the kernel time of every direction
+    (HIP events on the launch stream) as TFLOP/s and a fraction of the dense bf16 peak, the
+    packs' and weight preparations' GB/s, and the CPU bf16 path per direction (torch CPU,
+    the same operands, one warm-up and the median of three runs each)."""
+    import torch.nn.functional as F
+    rows = []
+    threads = cpu_threads()
+    for idx, (n, c, h) in enumerate(SWEEP):
+        data = conv_sweep_data(torch, X, [(n, c, h)], first_index=idx)
+        for _ in range(2):
+            conv_step(torch, data, C.note_write)
+        sync(torch)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            conv_step(torch, data, C.note_write)
+        sync(torch)
+        wall = (time.perf_counter() - t0) / reps
+        C.kernel_timing(True)
+        for _ in range(reps):
+            conv_step(torch, data, C.note_write)
+        rep = dict(C.kernel_timing_report())
+        C.kernel_timing(False)
+        flop = 2.0 * n * h * h * c * c * 9
+        e = {"N": n, "C": c, "H": h, "gflop_per_direction": round(flop / 1e9, 3), "step_us": round(1e6 * wall, 1),
+             "step_tflops": round(3 * flop / wall / 1e12, 1)}
+        for key, name in (("fwd", "conv3x3_rows.fwd"), ("dgrad", "conv3x3_rows.dgrad"), ("wgrad", "conv3x3_wgrad")):
+            k = rep.get(name)
+            if k:
+                us = 1e3 * k["total_ms"] / k["launches"]
+                e[key + "_us"] = round(us, 1)
+                e[key + "_tflops"] = round(flop / (us * 1e-6) / 1e12, 1)
+                e[key + "_frac_peak"] = round(flop / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4)
+        for key, name in (("pack", "conv3x3w_pack"), ("prep", "conv3x3_prep")):
+            k = rep.get(name)
+            if k:
+                e[key + "_us"] = round(1e3 * k["total_ms"] / k["launches"], 2)
+                e[key + "_gbs"] = round(k["work"] / (k["total_ms"] * 1e-3) / 1e9, 1)
+        if cpu:
+            torch.set_num_threads(threads)
+            x, w, b, dy = (t.detach().cpu() for t in data[0])
+            aten = torch.ops.aten
+
+            def cpu_ms(fn):
+                fn()
+                ts = []
+                for _ in range(3):
+                    t1 = time.perf_counter()
+                    fn()
+                    ts.append(time.perf_counter() - t1)
+                return 1e3 * statistics.median(ts)
+
+            e["cpu_fwd_ms"] = round(cpu_ms(lambda: F.conv2d(x, w, b, padding=1)), 2)
+            e["cpu_dgrad_ms"] = round(cpu_ms(lambda: aten.convolution_backward(
+                dy, x, w, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1, [True, False, False])), 2)
+            e["cpu_wgrad_ms"] = round(cpu_ms(lambda: aten.convolution_backward(
+                dy, x, w, [c], [1, 1], [1, 1], [1, 1], False, [0, 0], 1, [False, True, True])), 2)
+        rows.append(e)
+        del data
+        if log:
+            log(f"shape {n} {c} {h}: {e['step_tflops']} TFLOP/s")
+    return {"shapes": rows, "reps": reps, "cpu_threads": threads if cpu else None,
+            "cpu_model": cpu_topology()[2] if cpu else None}
 
 
 def gemm_product(layout, variant, M=8192, N=4096, K=4096, launches=30):
@@ -539,6 +612,11 @@ def main() -> int:
     ap.add_argument("--mlp-steps", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="small subset (profiling runs)")
     ap.add_argument("--skip-resnet", action="store_true")
+    ap.add_argument("--skip-c1", action="store_true")
+    ap.add_argument("--c1-steps", type=int, default=50)
+    ap.add_argument("--shape-table", action="store_true",
+                    help="per-shape fwd / dgrad / wgrad / pack figures of the sweep (GPU kernel times and "
+                         "the CPU bf16 path per direction), one JSON object")
     ap.add_argument("--resnet-steps", type=int, default=10)
     ap.add_argument("--cpu-rounds", type=int, default=2)
     ap.add_argument("--cpu-worker", help=argparse.SUPPRESS)
@@ -571,6 +649,9 @@ def main() -> int:
     C = xdev.native()
     X = torch.device("xdna")
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+    if args.shape_table:
+        print(json.dumps(shape_table(torch, C, X, cpu=not args.skip_cpu, log=log)), flush=True)
+        return 0
 
     calibration_copy(torch, C)
 
@@ -578,20 +659,30 @@ def main() -> int:
     shapes = SWEEP if not args.quick else [(16, 128, 36), (64, 256, 36)]
     log(f"conv sweep: {len(shapes)} shapes, building data")
     data = conv_sweep_data(torch, X, shapes)
+    # every step writes the weights first (as an optimizer step does), so each step prepares
+    # every weight's forms again, as in training
+    note = C.note_write
     for _ in range(args.warmup):
-        conv_step(torch, data)
+        conv_step(torch, data, note)
     sync(torch)
     log("conv sweep: warm")
     # value: K steps with nothing but the step on the stream
     sync(torch)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        conv_step(torch, data)
+        conv_step(torch, data, note)
     sync(torch)
     dt = time.perf_counter() - t0
     flops_step = sweep_flops(shapes)
     value = flops_step * args.steps / dt / 1e12
     log(f"conv sweep: {value:.1f} TFLOP/s, {1e3 * dt / args.steps:.2f} ms/step")
+    # beside it: the same steps with the weights unwritten (their prepared forms cached)
+    sync(torch)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        conv_step(torch, data)
+    sync(torch)
+    dt_cached = time.perf_counter() - t0
     # per-kernel figures (and the roofline): K more steps with a HIP event pair around every
     # hot-kernel launch.  The event records cost GPU time between launches, so this pass
     # is not the one `value` is timed on.
@@ -599,7 +690,7 @@ def main() -> int:
     sync(torch)
     t1 = time.perf_counter()
     for _ in range(args.steps):
-        conv_step(torch, data)
+        conv_step(torch, data, note)
     sync(torch)
     dt_ev = time.perf_counter() - t1
     kreport = dict(C.kernel_timing_report())
@@ -640,10 +731,15 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) activations and dY, Kaiming-uniform weights)",
         "config": {"workload": "BASELINE config 2: 3x3 conv sweep, stride 1, pad 1, bias, bf16, "
                                "N{16,40,64} x C{64,128,256,512} x H=W{18,36,72}; step = fwd + dgrad + "
-                               "wgrad(+bias grad) of every shape via aten convolution(_backward)_overrideable",
+                               "wgrad(+bias grad) of every shape via aten convolution(_backward)_overrideable, "
+                               "each weight written first (its forms prepared every step, as in training)",
                    "shapes": len(shapes), "gflop_per_step": round(flops_step / 1e9, 1),
                    "parallelism": "single GPU"},
         "roofline": roofline,
+        "weights_unwritten": {"TFLOP/s": round(flops_step * args.steps / dt_cached / 1e12, 2),
+                              "ms_per_step": round(1e3 * dt_cached / args.steps, 3),
+                              "note": "the same steps without the per-step weight write: every weight's "
+                                      "prepared forms come from the cache"},
         "kernel_timing_pass_ms_per_step": round(1e3 * dt_ev / args.steps, 3),
         "kernel_tflops_by_direction": per_dir,
         "kernels": kernels,
@@ -668,6 +764,55 @@ def main() -> int:
                           "avg_launch_us": round(1e3 * ar["total_ms"] / ar["launches"], 2)}
         log(f"adam: {gbs:.0f} GB/s")
     del params, opt
+
+    # --- config 1: one Conv2d(128->128) training step --------------------------------------
+    if not args.skip_c1:
+        log("c1: building")
+        c1_step, _ = build_c1(torch, X)
+        c1_eager = 1.0 / statistics.median(timed_steps(c1_step, 3, args.c1_steps, lambda: sync(torch)))
+        c1_graph = xdna_train.Graph()
+        with xdna_train.graph(c1_graph):
+            c1_loss = c1_step()
+        for _ in range(2):
+            c1_graph.replay()
+        sync(torch)
+        t0 = time.perf_counter()
+        for _ in range(args.c1_steps):
+            c1_graph.replay()
+        float(c1_loss.detach())
+        c1_it_s = args.c1_steps / (time.perf_counter() - t0)
+        c1_graph.reset()
+        C.kernel_timing(True)
+        for _ in range(args.c1_steps):
+            c1_step()
+        c1rep = dict(C.kernel_timing_report())
+        C.kernel_timing(False)
+        # forward and weight gradient (x is data: no input gradient is computed)
+        c1_flop = 2.0 * 16 * 36 * 36 * 128 * 128 * 9
+        c1_dirs = {}
+        for key, name in (("fwd", "conv3x3_rows.fwd"), ("dgrad", "conv3x3_rows.dgrad"), ("wgrad", "conv3x3_wgrad")):
+            e = c1rep.get(name)
+            if e:
+                tf = e["work"] / (e["total_ms"] * 1e-3) / 1e12
+                c1_dirs[key] = {"TFLOP/s": round(tf, 1), "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                                "avg_us": round(1e3 * e["total_ms"] / e["launches"], 2)}
+        ea = c1rep.get("fused_adam")
+        c1_adam = None
+        if ea:
+            gb = ea["work"] / (ea["total_ms"] * 1e-3) / 1e9
+            c1_adam = {"params": 147584, "GB/s": round(gb, 1), "frac_hbm": round(gb / PEAK_HBM_GBS, 4),
+                       "avg_us": round(1e3 * ea["total_ms"] / ea["launches"], 2)}
+        result["c1"] = {"it_s": round(c1_it_s, 1), "mode": "HIP graph replay of the whole training step",
+                        "eager_it_s": round(c1_eager, 1), "gflop_per_step": round(2 * c1_flop / 1e9, 2),
+                        "step_tflops": round(2 * c1_flop * c1_it_s / 1e12, 1), "by_direction": c1_dirs,
+                        "adam": c1_adam,
+                        "workload": "BASELINE config 1: Conv2d 128->128 3x3 pad 1 + bias, x [16,128,36,36], "
+                                    "MSE to zeros, Adam 1e-3 (README.md:57-68); fwd + wgrad (+ bias grad) per "
+                                    "step, x needs no gradient"}
+        log(f"c1: {c1_it_s:.1f} it/s (graph), {c1_eager:.1f} it/s (eager)")
+
+        def c1_gpu_it_s():
+            return 1.0 / statistics.median(timed_steps(c1_step, 3, args.c1_steps, lambda: sync(torch)))
 
     # --- MLP training step (config 3): mm / addmm fwd + both backward GEMMs + Adam -------
     if not args.skip_mlp:
@@ -813,6 +958,13 @@ def main() -> int:
             "threads": threads, "physical_cores_visible": n_phys, "cpus_in_affinity": n_aff, "cpu_model": model,
         }
         log(f"cpu baseline: conv sample {c_tf:.3f} TFLOP/s on the CPU, {g_tf:.1f} on the GPU")
+        if "c1" in result:
+            c_c1, g_c1, cc1_runs, gc1_runs = abba("c1_default_adam", c1_gpu_it_s, args.cpu_rounds, log)
+            result["c1"].update({"cpu_it_s": round(c_c1, 2), "cpu_it_s_rounds": [round(v, 2) for v in cc1_runs],
+                                 "gpu_eager_it_s_abba": round(g_c1, 1),
+                                 "speedup_vs_cpu": round(result["c1"]["it_s"] / c_c1, 1),
+                                 "eager_speedup_vs_cpu": round(g_c1 / c_c1, 1)})
+            log(f"c1 CPU: {c_c1:.2f} it/s")
         if "style_net" in result:
             c_d, g_d, cd_runs, gd_runs = abba("style_default_adam", style_gpu_it_s, args.cpu_rounds, log)
             c_f, _, cf_runs, _ = abba("style_fused_adam", style_gpu_it_s, 1, log)
@@ -822,6 +974,7 @@ def main() -> int:
                 "cpu_fused_adam_it_s": round(c_f, 3), "gpu_it_s_abba": round(g_d, 2),
                 "gpu_it_s_abba_rounds": [round(v, 2) for v in gd_runs],
                 "speedup_vs_cpu": round(result["style_net"]["it_s"] / c_d, 1),
+                "eager_speedup_vs_cpu": round(result["style_net"]["eager_it_s"] / c_d, 1),
                 "speedup_vs_cpu_fused_adam": round(result["style_net"]["it_s"] / c_f, 1)})
             if "region_it_s" in result["style_net"]:
                 result["style_net"]["region_speedup_vs_cpu"] = round(result["style_net"]["region_it_s"] / c_d, 1)

@@ -420,6 +420,13 @@ int xdna_gemm_bf16(const uint16_t* A, const uint16_t* Bm, uint16_t* C, const uin
  * XDNA_GEMM_VARIANT sets the initial value. */
 int xdna_gemm_set_variant(int variant);
 
+/* 1 (default): under the automatic choice, products with a side or a k of at most 128
+ * (and k at most 8192) take the batched small-matrix kernel (64 x 64 tiles, k-tiles of 64
+ * with the next one's loads in flight, split-K finished by the fixed-order reduce): the
+ * style loss's Gram matrices and their gradients.  0: the other kernels only.  No
+ * reference counterpart (a tuning knob).  XDNA_GEMM_SMALL sets the initial value. */
+int xdna_gemm_set_small(int on);
+
 /* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments, kernels and results, bit for bit; it calls no
@@ -624,6 +631,30 @@ int xdna_region_loss_finish(const float* part, int n, float* out_f32, uint16_t* 
  * reference's region has feature taps only). */
 int xdna_region_gram_grad_bf16(const uint16_t* G, const float* t, int64_t t_bstride, int64_t batch, int C,
                                float chw, float coef, const void* go, int go_dtype, uint16_t* S, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Losses of plain training scripts.  The reference runs them on its CPU    */
+/* through the zero-copy fallback (torch_xdna_device.cpp:5124-5260).        */
+/* dtype / go_dtype: 1 fp32, 2 bf16.  b's element for a's element i is      */
+/* b[i % period] (period == n: same shape; a divisor of n: b broadcast over */
+/* leading dimensions, as target.expand_as(input)).  reduction: 1 mean,     */
+/* 2 sum (PyTorch's enum; 0 none is not served).                            */
+/* ------------------------------------------------------------------------ */
+
+/* mse_loss(a, b): the mean (or sum) of (a - b)^2 over n elements into the 0-dim `out` of
+ * the operands' dtype.  fp32 partial sums over a fixed partition of the elements, then one
+ * workgroup adds them in index order in fp64, so equal inputs give equal bits.  The
+ * workspace holds the partials (xdna_mse_loss_workspace_bytes(n)).  Replaces PyTorch's mse_loss
+ * (aten::mse_loss, reduced) reached through the fallback. */
+size_t xdna_mse_loss_workspace_bytes(int64_t n);
+int xdna_mse_loss(const void* a, const void* b, int dtype, int64_t n, int64_t period, int reduction, void* out,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* mse_loss_backward: grad[i] = norm * (a[i] - b[i % period]) * go, norm = 2 / n (mean) or
+ * 2 (sum), go the incoming gradient (a device scalar of go_dtype), every element of grad
+ * written (no fill).  Replaces aten::mse_loss_backward reached through the fallback. */
+int xdna_mse_loss_bwd(const void* go, int go_dtype, const void* a, const void* b, int dtype, int64_t n,
+                      int64_t period, int reduction, void* grad, void* stream);
 
 #ifdef __cplusplus
 }

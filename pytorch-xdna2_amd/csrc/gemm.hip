@@ -1198,6 +1198,178 @@ void launch_b(int mb, dim3 grid, hipStream_t st, const GemmArgs& g) {
   else gemm_kernel<MA, kScalar><<<grid, 256, 0, st>>>(g);
 }
 
+// ---------------------------------------------------------------------------------------
+// Batched products of small matrices (the style loss's Gram matrices G = F F^T and their
+// gradients: C x C outputs over an HW-long k, C x HW and HW x C outputs over a C-long k,
+// HW as small as 16 and odd): 64 x 64 output tiles, four waves of 32 x 32 (one 32x32x16
+// accumulator each), k-tiles of 64 in LDS ([row][k], pitch 72) with the next k-tile's
+// loads in registers during the current one's MFMAs and one barrier per k-tile.  The large
+// tiles leave most of such an output empty and the 128 x 128 kernel stages its k-tiles
+// without overlap, a memory latency each.  K is split over blockIdx.z while the grid is
+// small, into fp32 partials that gemm_reduce_kernel adds in split order.  (A tile's last
+// split adding them itself would need a device-scope fence per workgroup, whose L2
+// write-back cost more than the separate launch on this multi-XCD part.)
+// ---------------------------------------------------------------------------------------
+constexpr int kSmT = 64, kSmK = 64, kSmP = 72;
+// One operand's 64 x 64 k-tile in registers: 16 elements per thread.  kAlongK: two 16-byte
+// vectors (8 k of one row); kAlongRow: two vectors of 8 rows at one k; kScalar: 16 single
+// elements, consecutive lanes along the operand's unit-stride direction where it has one.
+// Out-of-range elements are zero (no load).
+struct SmRegs {
+  uint32_t u[8];
+};
+
+template <int kMode>
+__device__ inline void sm_load(SmRegs& r, const uint16_t* src, int64_t s_r, int64_t s_k, int r0, int rows, int k0,
+                               int K, int tid) {
+  if (kMode == kAlongK) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + j * 256;
+      const int row = r0 + (i >> 3), k = k0 + (i & 7) * 8;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      if (row < rows && k < K) {
+        const uint16_t* p = src + int64_t(row) * s_r + k;
+        if (k + 8 <= K) {
+          const uint4 v = *reinterpret_cast<const uint4*>(p);
+          w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k + e < K) w[e >> 1] |= uint32_t(p[e]) << ((e & 1) * 16);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r.u[4 * j + q] = w[q];
+    }
+  } else if (kMode == kAlongRow) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + j * 256;
+      const int k = k0 + (i >> 3), row = r0 + (i & 7) * 8;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      if (k < K && row < rows) {
+        const uint16_t* p = src + int64_t(k) * s_k + row;
+        if (row + 8 <= rows) {
+          const uint4 v = *reinterpret_cast<const uint4*>(p);
+          w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (row + e < rows) w[e >> 1] |= uint32_t(p[e]) << ((e & 1) * 16);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r.u[4 * j + q] = w[q];
+    }
+  } else {
+    const bool rows_fast = s_r == 1 && s_k != 1;
+    uint32_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = tid + j * 256;
+      const int rr = rows_fast ? (i & 63) : (i >> 6), kk = rows_fast ? (i >> 6) : (i & 63);
+      const int row = r0 + rr, k = k0 + kk;
+      const bool ok = row < rows && k < K;
+      const uint32_t e = src[ok ? int64_t(row) * s_r + int64_t(k) * s_k : 0];
+      v[j] = ok ? e : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r.u[q] = v[2 * q] | (v[2 * q + 1] << 16);
+  }
+}
+
+template <int kMode>
+__device__ inline void sm_store(uint16_t* lds, const SmRegs& r, int64_t s_r, int64_t s_k, int tid) {
+  if (kMode == kAlongK) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + j * 256;
+      *reinterpret_cast<uint4*>(lds + (i >> 3) * kSmP + (i & 7) * 8) =
+          make_uint4(r.u[4 * j], r.u[4 * j + 1], r.u[4 * j + 2], r.u[4 * j + 3]);
+    }
+  } else if (kMode == kAlongRow) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + j * 256;
+      const int kk = i >> 3, rv = (i & 7) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        lds[(rv + e) * kSmP + kk] = uint16_t((e & 1) ? (r.u[4 * j + (e >> 1)] >> 16) : (r.u[4 * j + (e >> 1)] & 0xFFFF));
+    }
+  } else {
+    const bool rows_fast = s_r == 1 && s_k != 1;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = tid + j * 256;
+      const int rr = rows_fast ? (i & 63) : (i >> 6), kk = rows_fast ? (i >> 6) : (i & 63);
+      lds[rr * kSmP + kk] = uint16_t((j & 1) ? (r.u[j >> 1] >> 16) : (r.u[j >> 1] & 0xFFFF));
+    }
+  }
+}
+
+template <int kModeA, int kModeB>
+__global__ __launch_bounds__(256) void gemm_small_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t as[2][kSmT * kSmP];
+  __shared__ __attribute__((aligned(16))) uint16_t bs[2][kSmT * kSmP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kSmT, n0 = blockIdx.x * kSmT;
+  const int batch = blockIdx.z / g.nsplit, split = blockIdx.z - batch * g.nsplit;
+  const int kbeg = split * g.kt_per * kSmK, kend = min(g.K, kbeg + g.kt_per * kSmK);
+  const uint16_t* A = g.a + int64_t(batch) * g.a_batch;
+  const uint16_t* B = g.b + int64_t(batch) * g.b_batch;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc = zero_acc();
+  SmRegs ra, rb;
+  if (kbeg < kend) {
+    sm_load<kModeA>(ra, A, g.a_r, g.a_k, m0, g.M, kbeg, kend, tid);
+    sm_load<kModeB>(rb, B, g.b_r, g.b_k, n0, g.N, kbeg, kend, tid);
+    sm_store<kModeA>(as[0], ra, g.a_r, g.a_k, tid);
+    sm_store<kModeB>(bs[0], rb, g.b_r, g.b_k, tid);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = kbeg; k0 < kend; k0 += kSmK) {
+    const bool more = k0 + kSmK < kend;
+    if (more) {  // the next k-tile's loads fly during this one's MFMAs
+      sm_load<kModeA>(ra, A, g.a_r, g.a_k, m0, g.M, k0 + kSmK, kend, tid);
+      sm_load<kModeB>(rb, B, g.b_r, g.b_k, n0, g.N, k0 + kSmK, kend, tid);
+    }
+    const uint16_t* ab = as[buf] + (wm * 32 + lr) * kSmP + lk;
+    const uint16_t* bb = bs[buf] + (wn * 32 + lr) * kSmP + lk;
+#pragma unroll
+    for (int ks = 0; ks < kSmK / 16; ++ks)
+      acc = mfma_32x32x16(as_bf16x8(*reinterpret_cast<const uint4*>(ab + ks * 16)),
+                          as_bf16x8(*reinterpret_cast<const uint4*>(bb + ks * 16)), acc);
+    if (more) {  // the other buffer's last reads ended before the previous barrier
+      sm_store<kModeA>(as[buf ^ 1], ra, g.a_r, g.a_k, tid);
+      sm_store<kModeB>(bs[buf ^ 1], rb, g.b_r, g.b_k, tid);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // the tile, or (split-K) this split's fp32 partial tile
+  const f32x16_t out[1][1] = {{acc}};
+  store_block<1, 1>(g, batch, split, out, m0 + wm * 32, n0 + wn * 32, lane);
+}
+
+template <int MA>
+void launch_small_b(int mb, dim3 grid, hipStream_t st, const GemmArgs& g) {
+  if (mb == kAlongK) gemm_small_kernel<MA, kAlongK><<<grid, 256, 0, st>>>(g);
+  else if (mb == kAlongRow) gemm_small_kernel<MA, kAlongRow><<<grid, 256, 0, st>>>(g);
+  else gemm_small_kernel<MA, kScalar><<<grid, 256, 0, st>>>(g);
+}
+
+// Small products take gemm_small_kernel: a side of at most 128 or a k of at most 128, and
+// a k up to 8192 (XDNA_GEMM_SMALL=0 at start-up, or xdna_gemm_set_small(0), turns it off).
+std::atomic<int> g_gemm_small{[] {
+  const char* e = std::getenv("XDNA_GEMM_SMALL");
+  return e && std::atoi(e) == 0 ? 0 : 1;
+}()};
+
 // Device scratch of xdna_gemm_bf16_noalloc: its split-K partials live here instead of in
 // blocks of the caching allocator.  Each GPU the library runs on holds its own copy until
 // the process ends; host code reaches it only through the per-device address that
@@ -1317,6 +1489,37 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   const int mb = stage_mode(Bm, ldb_n, ldb_k, stride_b, batch);
   if (!admit_launch("xdna_gemm_bf16")) return -1;
   g.batch = batch;
+  // (two element-staged operands with a short k stay on the 128 x 128 tiles, which read each
+  // element fewer times: 15 against 22 us for the style loss's 256-channel Gram product)
+  if (g_gemm_small.load() && g_gemm_variant.load() == 0 && g.rs_ok && K > 0 && K <= 8192 &&
+      (M <= 128 || N <= 128 || K <= 128) && !(ma == kScalar && mb == kScalar && K <= 128)) {
+    // small products (gemm_small_kernel): K split while the grid is below two workgroups
+    // per CU, each split keeping at least two k-tiles
+    const int64_t tiles = ceil_div(M, kSmT) * ceil_div(N, kSmT) * int64_t(batch);
+    const int ktiles = int(ceil_div(K, kSmK));
+    int nsplit = 1;
+    if (tiles < 256 && ktiles >= 4)
+      nsplit = int(std::max<int64_t>(1, std::min<int64_t>({ceil_div(512, tiles), int64_t(ktiles / 2),
+                                                           int64_t(65535 / std::max(batch, 1))})));
+    g.kt_per = int(ceil_div(ktiles, nsplit));
+    g.nsplit = int(ceil_div(ktiles, g.kt_per));
+    g.part = nullptr;
+    if (g.nsplit > 1) {
+      g.part = src.take(size_t(g.nsplit) * size_t(batch) * size_t(M) * size_t(N) * sizeof(float));
+      if (!g.part) return -1;
+    }
+    const dim3 grid(unsigned(ceil_div(N, kSmT)), unsigned(ceil_div(M, kSmT)), unsigned(batch * g.nsplit));
+    hipStream_t sts = as_stream(stream);
+    if (ma == kAlongK) launch_small_b<kAlongK>(mb, grid, sts, g);
+    else if (ma == kAlongRow) launch_small_b<kAlongRow>(mb, grid, sts, g);
+    else launch_small_b<kScalar>(mb, grid, sts, g);
+    if (g.nsplit > 1) {
+      const int64_t n_all = int64_t(batch) * M * N;
+      gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, sts>>>(g);
+      src.give_back(g.part);  // stream-ordered reuse: the next user of the block runs after the reduce
+    }
+    return check_launch(src.who);
+  }
   hipStream_t st2 = as_stream(stream);
   // Large tiles (256 x 256) when neither operand needs scalar staging and the grid still
   // has enough tiles: the four-wave kernel where its whole-vector loads fit the shape, else
@@ -1449,6 +1652,15 @@ extern "C" int xdna_gemm_bf16_noalloc(const uint16_t* A, const uint16_t* Bm, uin
   const PartialsSource src{"xdna_gemm_bf16_noalloc", sp};
   return gemm_run(src, A, Bm, C, bias, batch, M, N, K, lda_m, lda_k, stride_a, ldb_k, ldb_n, stride_b, ldc_m,
                   ldc_n, stride_c, bias_mode, bias_sm, bias_sn, alpha, beta, stream);
+}
+
+extern "C" int xdna_gemm_set_small(int on) {
+  if (on != 0 && on != 1) {
+    set_error("xdna_gemm_set_small: 0 or 1");
+    return -1;
+  }
+  g_gemm_small.store(on);
+  return 0;
 }
 
 extern "C" int xdna_gemm_set_variant(int variant) {

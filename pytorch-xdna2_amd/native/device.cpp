@@ -622,11 +622,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("set_", TORCH_FN(set_empty_));
   m.impl("_copy_from", TORCH_FN(copy_from_xdna));
   m.impl("_copy_from_and_resize", TORCH_FN(copy_from_and_resize_xdna));
-  // mse_loss is structured: without a kernel of its own the non-functional composite
-  // allocates a 0-dim output and calls mse_loss.out, whose ROCm kernel builds its
-  // elementwise iterator into that output (a deprecated resize) before reducing into it.
-  // The functional ROCm kernel on aliases allocates the output itself.
-  m.impl("mse_loss", torch::CppFunction::makeFromBoxedFunction<&xdna_fallback>());
+  // mse_loss (ops.cpp) has a kernel of its own: without one the non-functional composite
+  // would allocate a 0-dim output and call mse_loss.out, whose ROCm kernel resizes it.
   register_hot_ops(m);
 }
 
@@ -749,6 +746,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
   mod.def("wait_timeout_ms", [] { return xdna_hip_wait_timeout_ms(); });
   mod.def("max_wait_ms", [] { return xdna_hip_max_wait_ms(); });
   mod.def("write_epoch", [](const at::Tensor& t) { return write_epoch(t); });
+  // records a write of t's allocation made outside the xdna ops (as an optimizer step's),
+  // so cached forms derived from it stop serving
+  mod.def("note_write", [](const at::Tensor& t) { bump_write_epoch(t); });
   mod.def("poisoned", [] { return xdna_hip_poisoned() != 0; });
   mod.def("inject_failure", [](int64_t n, bool poison) {
     check_abi(xdna_hip_inject_failure(n, poison ? 1 : 0), "inject_failure");

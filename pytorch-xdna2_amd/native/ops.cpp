@@ -9,6 +9,7 @@
 #include <ATen/native/Resize.h>
 #include <ATen/ops/_fused_adam_native.h>
 #include <ATen/ops/instance_norm_native.h>
+#include <ATen/ops/max_pool2d_native.h>
 #include <torch/csrc/autograd/custom_function.h>
 #include <c10/core/impl/LocalDispatchKeySet.h>
 
@@ -345,6 +346,8 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
   count_call(wt.defined() ? "hip_conv3x3.weights_hit" : "hip_conv3x3.weights", 0);
   if (!wt.defined()) {
     wt = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cin), int(cout)));
+    // bytes: the OIHW weight read once, each prepared form written
+    KernelTimer kt("conv3x3_prep", double(w.numel()) * 2.0 * (trainable && !dgrad ? 3.0 : 2.0));
     if (trainable && !dgrad) {
       at::Tensor wtd = alloc_bytes(xdna_conv3x3_prepared_weight_bytes(int(cout), int(cin)));
       check_abi(xdna_conv3x3_prepare_weights_both_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
@@ -1705,8 +1708,137 @@ at::Tensor upsample_nearest2d_backward_xdna(const at::Tensor& grad_output, c10::
                                                           scales_w));
 }
 
+// ---------------------------------------------------------------------------------------
+// Losses and pooling of plain training scripts (the style step's content and Gram style
+// terms, VGG's 2x2 pools): one HIP launch each way where PyTorch-ROCm takes two to four
+// (fills, indices, separate reductions).  The reference runs all of them on its CPU
+// through the fallback (torch_xdna_device.cpp:5124-5260).
+// ---------------------------------------------------------------------------------------
+
+// `t`'s row-major element i is the element i % period of the contiguous block at t's data
+// pointer when its trailing dimensions are contiguous and its leading ones have stride 0
+// (t = block.expand(...)); returns that period, or -1.
+int64_t broadcast_period(const at::Tensor& t) {
+  int64_t period = 1, k = t.dim();
+  while (k > 0 && (t.size(k - 1) == 1 || t.stride(k - 1) == period)) {
+    period *= t.size(k - 1);
+    --k;
+  }
+  for (int64_t q = 0; q < k; ++q)
+    if (t.size(q) != 1 && t.stride(q) != 0) return -1;
+  return period;
+}
+
+int loss_dtype(at::ScalarType t) { return t == at::kFloat ? 1 : t == at::kBFloat16 ? 2 : 0; }
+
+bool mse_eligible(const at::Tensor& self, const at::Tensor& target, int64_t reduction) {
+  return g_mode.load() >= 1 && (reduction == 1 || reduction == 2) && self.device().type() == kXdna &&
+         target.device().type() == kXdna && self.scalar_type() == target.scalar_type() &&
+         loss_dtype(self.scalar_type()) != 0 && self.sizes() == target.sizes() && self.numel() > 0;
+}
+
+// b operand and its period: target itself when it is a batch-broadcast block, else a copy
+std::pair<at::Tensor, int64_t> period_operand(const at::Tensor& target) {
+  const int64_t p = broadcast_period(target);
+  if (p > 0) return {target, p};
+  at::Tensor b = target.contiguous();
+  return {b, b.numel()};
+}
+
+at::Tensor mse_loss_xdna(const at::Tensor& self, const at::Tensor& target, int64_t reduction) {
+  if (mse_eligible(self, target, reduction)) {
+    ScopedCount sc("hip_mse_loss.fwd.run");
+    const at::Tensor a = self.contiguous();
+    const auto [b, period] = period_operand(target);
+    const int64_t n = a.numel();
+    at::Tensor out = empty_xdna({}, a.scalar_type());
+    const size_t wb = xdna_mse_loss_workspace_bytes(n);
+    at::Tensor ws = alloc_bytes(wb);
+    check_abi(xdna_mse_loss(a.const_data_ptr(), b.const_data_ptr(), loss_dtype(a.scalar_type()), n, period,
+                            int(reduction), out.data_ptr(), ws.data_ptr(), wb, current_stream()),
+              "mse_loss");
+    return out;
+  }
+  ScopedCount sc("aten::mse_loss.rocm");
+  BelowAutograd g;
+  return back(at::_ops::mse_loss::call(rocm(self), rocm(target), reduction));
+}
+
+at::Tensor mse_loss_backward_xdna(const at::Tensor& grad_output, const at::Tensor& self, const at::Tensor& target,
+                                  int64_t reduction) {
+  if (mse_eligible(self, target, reduction) && grad_output.numel() == 1 &&
+      grad_output.device().type() == kXdna && loss_dtype(grad_output.scalar_type()) != 0) {
+    ScopedCount sc("hip_mse_loss.bwd.run");
+    const at::Tensor a = self.contiguous();
+    const auto [b, period] = period_operand(target);
+    const at::Tensor go = grad_output.contiguous();
+    at::Tensor grad = empty_xdna(a.sizes(), a.scalar_type());
+    check_abi(xdna_mse_loss_bwd(go.const_data_ptr(), loss_dtype(go.scalar_type()), a.const_data_ptr(),
+                                b.const_data_ptr(), loss_dtype(a.scalar_type()), a.numel(), period, int(reduction),
+                                grad.data_ptr(), current_stream()),
+              "mse_loss_backward");
+    return grad;
+  }
+  ScopedCount sc("aten::mse_loss_backward.rocm");
+  BelowAutograd g;
+  return back(at::_ops::mse_loss_backward::call(rocm(grad_output), rocm(self), rocm(target), reduction));
+}
+
+// 2x2 / stride-2 max-pool (floor mode) of bf16 NCHW tensors as its own autograd node: the
+// forward writes the pooled values only (no int64 indices), the backward routes each
+// window's gradient to the window's maximum recomputed from the saved input (PyTorch's
+// rule: the first maximum in row-major order, a NaN wins) and writes every input element,
+// so no fill runs first.  Other pools keep PyTorch's composite.
+bool pair_of(at::IntArrayRef v, int64_t x) {
+  return (v.size() == 1 && v[0] == x) || (v.size() == 2 && v[0] == x && v[1] == x);
+}
+
+bool maxpool2_eligible(const at::Tensor& x, at::IntArrayRef kernel, at::IntArrayRef stride,
+                       at::IntArrayRef padding, at::IntArrayRef dilation, bool ceil_mode) {
+  if (g_mode.load() < 1 || ceil_mode || x.scalar_type() != at::kBFloat16 || x.dim() != 4) return false;
+  if (x.device().type() != kXdna || x.size(2) < 2 || x.size(3) < 2 || x.numel() == 0) return false;
+  return pair_of(kernel, 2) && (stride.empty() || pair_of(stride, 2)) && pair_of(padding, 0) &&
+         pair_of(dilation, 1);
+}
+
+struct MaxPool2Fn : public torch::autograd::Function<MaxPool2Fn> {
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& input) {
+    ScopedCount sc("hip_maxpool2.fwd.run");
+    const at::Tensor x = input.contiguous();
+    at::Tensor y = empty_xdna({x.size(0), x.size(1), x.size(2) / 2, x.size(3) / 2}, at::kBFloat16);
+    check_abi(xdna_region_maxpool2_bf16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                        static_cast<uint16_t*>(y.data_ptr()), x.size(0) * x.size(1),
+                                        int(x.size(2)), int(x.size(3)), current_stream()),
+              "max_pool2d");
+    ctx->save_for_backward({x});
+    return y;
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const at::Tensor x = ctx->get_saved_variables()[0];
+    if (!grads[0].defined()) return {at::Tensor()};
+    ScopedCount sc("hip_maxpool2.bwd.run");
+    const at::Tensor dy = grads[0].to(at::kBFloat16).contiguous();
+    at::Tensor dx = empty_xdna(x.sizes(), at::kBFloat16);
+    check_abi(xdna_region_backward_bf16(nullptr, nullptr, static_cast<const uint16_t*>(dy.const_data_ptr()),
+                                        static_cast<const uint16_t*>(x.const_data_ptr()), nullptr, nullptr, nullptr,
+                                        0.0f, nullptr, 0, static_cast<uint16_t*>(dx.data_ptr()),
+                                        x.size(0) * x.size(1), int(x.size(2)), int(x.size(3)), current_stream()),
+              "max_pool2d backward");
+    return {dx};
+  }
+};
+
+at::Tensor max_pool2d_autograd_xdna(const at::Tensor& self, at::IntArrayRef kernel_size, at::IntArrayRef stride,
+                                    at::IntArrayRef padding, at::IntArrayRef dilation, bool ceil_mode) {
+  if (maxpool2_eligible(self, kernel_size, stride, padding, dilation, ceil_mode)) return MaxPool2Fn::apply(self);
+  return at::native::max_pool2d(self, kernel_size, stride, padding, dilation, ceil_mode);
+}
+
 void register_autograd_ops(torch::Library& m) {
   m.impl("instance_norm", TORCH_FN(instance_norm_autograd_xdna));
+  m.impl("max_pool2d", TORCH_FN(max_pool2d_autograd_xdna));
 }
 
 void register_hot_ops(torch::Library& m) {
@@ -1727,6 +1859,8 @@ void register_hot_ops(torch::Library& m) {
   m.impl("native_batch_norm_backward", TORCH_FN(native_batch_norm_backward_xdna));
   m.impl("upsample_nearest2d", TORCH_FN(upsample_nearest2d_xdna));
   m.impl("upsample_nearest2d_backward", TORCH_FN(upsample_nearest2d_backward_xdna));
+  m.impl("mse_loss", TORCH_FN(mse_loss_xdna));
+  m.impl("mse_loss_backward", TORCH_FN(mse_loss_backward_xdna));
 }
 
 // ---------------------------------------------------------------------------------------

@@ -117,9 +117,13 @@ SIGNATURES = {
     "xdna_region_gram_sqdiff_bf16": (I, [P, P, L, L, L, F, F, P, P]),
     "xdna_region_loss_finish": (I, [P, I, P, P, P]),
     "xdna_region_gram_grad_bf16": (I, [P, P, L, L, I, F, F, P, I, P, P]),
+    "xdna_mse_loss_workspace_bytes": (Z, [L]),
+    "xdna_mse_loss": (I, [P, P, I, L, L, I, P, P, Z, P]),
+    "xdna_mse_loss_bwd": (I, [P, I, P, P, I, L, L, I, P, P]),
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_gemm_set_variant": (I, [I]),
+    "xdna_gemm_set_small": (I, [I]),
     "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_gemm_bf16_noalloc": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_batch_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, P]),
