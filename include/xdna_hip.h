@@ -427,6 +427,11 @@ int xdna_gemm_set_variant(int variant);
  * reference counterpart (a tuning knob).  XDNA_GEMM_SMALL sets the initial value. */
 int xdna_gemm_set_small(int on);
 
+/* Image rows per workgroup of the packs that stage rows in LDS: 0 (default) the automatic
+ * choice, else this many (clamped to the image and to 256 pixels).  For measurements; no
+ * reference counterpart. */
+int xdna_conv3x3_set_pack_rows(int rows);
+
 /* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments, kernels and results, bit for bit; it calls no

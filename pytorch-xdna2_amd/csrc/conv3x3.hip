@@ -49,28 +49,77 @@ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 // Weight preparation: OIHW bf16 -> Wt[co_pad][chunks*9*64] (k order chunk, tap, c).
 // dgrad: the conv of dY (cin' = Cout channels) with w'[ci][co][t] = w[co][ci][8-t].
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prep_weights_kernel(const uint16_t* __restrict__ w,
-                                                           uint16_t* __restrict__ wt, int Cout,
-                                                           int Cin, int co_pad, int chunks,
-                                                           int dgrad) {
-  const int64_t K = int64_t(chunks) * 9 * kKStep;
-  const int64_t n = int64_t(co_pad) * K;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += int64_t(gridDim.x) * blockDim.x) {
-    const int row = int(i / K);          // output channel of this conv
-    const int k = int(i - int64_t(row) * K);
-    const int c = k % kKStep;
-    const int tap = (k / kKStep) % 9;
-    const int chunk = k / (kKStep * 9);
-    const int col = chunk * kKStep + c;  // input channel of this conv
-    uint16_t v = 0;
-    if (!dgrad) {
-      if (row < Cout && col < Cin) v = w[(int64_t(row) * Cin + col) * 9 + tap];
-    } else {
-      // this conv: out channel = forward ci (row), in channel = forward co (col)
-      if (row < Cin && col < Cout) v = w[(int64_t(col) * Cin + row) * 9 + (8 - tap)];
+// Both prepared forms from one read of the weight: a workgroup takes a block of 32 output
+// x 64 input channels of the OIHW weight (32 rows of 64 x 9 contiguous elements, read with
+// 16-byte loads where the rows allow) into LDS, then writes the forward form's 32 rows
+// [tap][64 ci] of chunk ci0 / 64 and the input-gradient form's 64 rows [tap][32 co] (taps
+// flipped) of chunk co0 / 64, each in 16-byte stores.  Blocks cover the padded extents of
+// both forms; elements outside Cout x Cin are zeros.  wt or wtd may be null (that form is
+// not written).  (The element-per-thread form spent most of its time in 64-bit index
+// divisions and 18-byte-strided gathers: up to 17 us for a 512-channel weight.)
+constexpr int kPrepCo = 32, kPrepCi = 64, kPrepRow = kPrepCi * 9;  // 576 elements per block row
+
+__global__ __launch_bounds__(256) void prep_tiled_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                         uint16_t* __restrict__ wtd, int Cout, int Cin, int co_pad_f,
+                                                         int chunks_f, int co_pad_d, int chunks_d, int vec) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kPrepCo * kPrepRow];  // [co_l][ci_l * 9 + tap]
+  const int ci0 = blockIdx.x * kPrepCi, co0 = blockIdx.y * kPrepCo;
+  const int tid = threadIdx.x;
+  const bool full = vec && ci0 + kPrepCi <= Cin && co0 + kPrepCo <= Cout;
+  if (full) {
+    // 32 rows x 72 pieces of 16 bytes, each row starting at a 16-byte boundary (Cin % 8 == 0)
+    for (int e = tid; e < kPrepCo * (kPrepRow / 8); e += 256) {
+      const int r = e / (kPrepRow / 8), q = e - r * (kPrepRow / 8);
+      const uint4 v = *reinterpret_cast<const uint4*>(w + (int64_t(co0 + r) * Cin + ci0) * 9 + q * 8);
+      *reinterpret_cast<uint4*>(tile + r * kPrepRow + q * 8) = v;
     }
-    wt[i] = v;
+  } else if (co0 < Cout && ci0 < Cin) {
+    // a block at the weight's edge: element loads, 8 per thread in flight per round
+    for (int e0 = tid * 8; e0 < kPrepCo * kPrepRow; e0 += 256 * 8) {
+      uint16_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + j, r = e / kPrepRow, q = e - r * kPrepRow;
+        const int co = co0 + r, ci = ci0 + q / 9;
+        v[j] = co < Cout && ci < Cin ? w[(int64_t(co) * Cin + ci) * 9 + q % 9] : uint16_t(0);
+      }
+      *reinterpret_cast<uint4*>(tile + e0) = make_uint4(v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16),
+                                                         v[4] | (uint32_t(v[5]) << 16), v[6] | (uint32_t(v[7]) << 16));
+    }
+  } else {
+    // only padding: zeros, no loads
+    for (int e0 = tid * 8; e0 < kPrepCo * kPrepRow; e0 += 256 * 8)
+      *reinterpret_cast<uint4*>(tile + e0) = make_uint4(0u, 0u, 0u, 0u);
+  }
+  __syncthreads();
+  // forward form: row co, k = (chunk ci0 / 64, tap, c); 8 consecutive c per store
+  if (wt && co0 < co_pad_f && ci0 < chunks_f * kKStep) {
+    for (int e = tid; e < kPrepCo * 72; e += 256) {
+      const int r = e / 72, q = e - r * 72;
+      const int tap = q >> 3, c0 = (q & 7) * 8;
+      uint32_t u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        u[j] = uint32_t(tile[r * kPrepRow + (c0 + 2 * j) * 9 + tap]) |
+               (uint32_t(tile[r * kPrepRow + (c0 + 2 * j + 1) * 9 + tap]) << 16);
+      uint16_t* dst = wt + (int64_t(co0 + r) * chunks_f + ci0 / kKStep) * kPrepRow + tap * kKStep + c0;
+      *reinterpret_cast<uint4*>(dst) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+  }
+  // input-gradient form: row ci, k = (chunk co0 / 64, tap, co), w'[ci][co][t] = w[co][ci][8 - t]
+  if (wtd && ci0 < co_pad_d && co0 < chunks_d * kKStep) {
+    const int cb = co0 % kKStep;  // 0 or 32: this block's half of the chunk
+    for (int e = tid; e < kPrepCi * 9 * (kPrepCo / 8); e += 256) {
+      const int r = e / (9 * (kPrepCo / 8)), q = e - r * (9 * (kPrepCo / 8));
+      const int tap = q / (kPrepCo / 8), c0 = (q % (kPrepCo / 8)) * 8;
+      uint32_t u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        u[j] = uint32_t(tile[(c0 + 2 * j) * kPrepRow + r * 9 + (8 - tap)]) |
+               (uint32_t(tile[(c0 + 2 * j + 1) * kPrepRow + r * 9 + (8 - tap)]) << 16);
+      uint16_t* dst = wtd + (int64_t(ci0 + r) * chunks_d + co0 / kKStep) * kPrepRow + tap * kKStep + cb + c0;
+      *reinterpret_cast<uint4*>(dst) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
   }
 }
 
@@ -1841,44 +1890,28 @@ bool shape_ok(const char* what, int B, int Cin, int Cout, int H, int W) {
   return true;
 }
 
-// Both forms of a trainable weight in one launch: the forward one into wt and the
-// flip+swap one of the input gradient into wtd (workgroups past the first form's take the
-// second), so the backward need not launch its own preparation.
-__global__ __launch_bounds__(256) void prep_weights_both_kernel(const uint16_t* __restrict__ w,
-                                                                uint16_t* __restrict__ wt,
-                                                                uint16_t* __restrict__ wtd, int Cout, int Cin,
-                                                                int co_pad_f, int chunks_f, int co_pad_d,
-                                                                int chunks_d, int blocks_f) {
-  const bool d = int(blockIdx.x) >= blocks_f;
-  const int co_pad = d ? co_pad_d : co_pad_f, chunks = d ? chunks_d : chunks_f;
-  const int b0 = d ? int(blockIdx.x) - blocks_f : int(blockIdx.x);
-  const int nb = d ? int(gridDim.x) - blocks_f : blocks_f;
-  uint16_t* out = d ? wtd : wt;
-  const int64_t K = int64_t(chunks) * 9 * kKStep;
-  const int64_t n = int64_t(co_pad) * K;
-  for (int64_t i = int64_t(b0) * 256 + threadIdx.x; i < n; i += int64_t(nb) * 256) {
-    const int row = int(i / K);
-    const int k = int(i - int64_t(row) * K);
-    const int c = k % kKStep;
-    const int tap = (k / kKStep) % 9;
-    const int col = (k / (kKStep * 9)) * kKStep + c;
-    uint16_t v = 0;
-    if (!d) {
-      if (row < Cout && col < Cin) v = w[(int64_t(row) * Cin + col) * 9 + tap];
-    } else {
-      if (row < Cin && col < Cout) v = w[(int64_t(col) * Cin + row) * 9 + (8 - tap)];
-    }
-    out[i] = v;
-  }
+// The forward form (wt) and / or the input-gradient form (wtd) of an OIHW weight in one
+// launch of prep_tiled_kernel.
+int launch_prep_tiled(const uint16_t* w, uint16_t* wt, uint16_t* wtd, int Cout, int Cin, void* stream) {
+  if (!admit_launch("conv3x3 weight preparation")) return -1;
+  const FwdPlan pf = fwd_plan(1, Cin, Cout, 1, 1), pd = fwd_plan(1, Cout, Cin, 1, 1);
+  // extents: forward rows co_pad_f x chunks_f * 64 columns; gradient rows co_pad_d (over
+  // ci) x chunks_d * 64 (over co)
+  const int ci_ext = std::max(wt ? pf.chunks * kKStep : 0, wtd ? pd.co_pad : 0);
+  const int co_ext = std::max(wt ? pf.co_pad : 0, wtd ? pd.chunks * kKStep : 0);
+  const int vec = (Cin % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) ? 1 : 0;
+  const dim3 grid(unsigned(ceil_div(ci_ext, kPrepCi)), unsigned(ceil_div(co_ext, kPrepCo)));
+  prep_tiled_kernel<<<grid, 256, 0, as_stream(stream)>>>(w, wt, wtd, Cout, Cin, pf.co_pad, pf.chunks, pd.co_pad,
+                                                          pd.chunks, vec);
+  return check_launch("conv3x3 weight preparation");
 }
 
 int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, int chunks,
                 int dgrad, void* stream) {
-  if (!admit_launch("conv3x3 weight preparation")) return -1;
-  const int64_t n = int64_t(co_pad) * chunks * 9 * kKStep;
-  const int blocks = int(std::min<int64_t>(ceil_div(n, 256), 4096));
-  prep_weights_kernel<<<blocks, 256, 0, as_stream(stream)>>>(w, wt, Cout, Cin, co_pad, chunks, dgrad);
-  return check_launch("conv3x3 weight preparation");
+  (void)co_pad;
+  (void)chunks;
+  return dgrad ? launch_prep_tiled(w, nullptr, wt, Cout, Cin, stream)
+               : launch_prep_tiled(w, wt, nullptr, Cout, Cin, stream);
 }
 
 template <int MT, int NT, int WM, int OCC = 1>
@@ -2964,13 +2997,7 @@ int xdna_conv3x3_prepare_weights_both_bf16(const uint16_t* w, uint16_t* wt, uint
     set_error("xdna_conv3x3_prepare_weights_both_bf16: invalid arguments");
     return -1;
   }
-  const FwdPlan pf = fwd_plan(1, Cin, Cout, 1, 1), pd = fwd_plan(1, Cout, Cin, 1, 1);
-  const int64_t nf = int64_t(pf.co_pad) * pf.chunks * 9 * kKStep, nd = int64_t(pd.co_pad) * pd.chunks * 9 * kKStep;
-  const int bf = int(std::min<int64_t>(ceil_div(nf, 256), 2048)), bd = int(std::min<int64_t>(ceil_div(nd, 256), 2048));
-  if (!admit_launch("conv3x3 weight preparation")) return -1;
-  prep_weights_both_kernel<<<bf + bd, 256, 0, as_stream(stream)>>>(w, wt, wt_dgrad, Cout, Cin, pf.co_pad, pf.chunks,
-                                                                   pd.co_pad, pd.chunks, bf);
-  return check_launch("conv3x3 weight preparation");
+  return launch_prep_tiled(w, wt, wt_dgrad, Cout, Cin, stream);
 }
 
 int xdna_conv3x3_rows_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,

@@ -226,3 +226,40 @@ def test_workspace_too_small_is_an_error(hip):
     w = dev_zeros((C, C, 3, 3))
     rc = hip.xdna_conv3x3_fwd_bf16(ptr(x), ptr(w), None, ptr(y), B, C, C, H, W, ptr(ws), 64, stream())
     assert rc == -1
+
+
+def _prepared_expected(w, dgrad):
+    """The prepared form on the host: rows = the conv's output channels padded to 128 (or a
+    multiple of 256 beyond 128), k = (64-channel chunk, tap, channel); the input-gradient
+    form is that of w'[ci][co][t] = w[co][ci][8 - t]."""
+    Cout, Cin = w.shape[:2]
+    wf = w.reshape(Cout, Cin, 9)
+    if dgrad:
+        wf = wf[:, :, ::-1].transpose(1, 0, 2)
+    rows, cols = wf.shape[:2]
+    co_pad = 128 if rows <= 128 else -(-rows // 256) * 256
+    chunks = -(-cols // 64)
+    tmp = np.zeros((co_pad, chunks * 64, 9), np.uint16)
+    tmp[:rows, :cols] = wf
+    return tmp.reshape(co_pad, chunks, 64, 9).transpose(0, 1, 3, 2).reshape(-1)
+
+
+@pytest.mark.parametrize("cin,cout", [(3, 64), (64, 64), (128, 128), (256, 512), (512, 256), (100, 36), (36, 300),
+                                      (8, 3), (520, 130)])
+def test_prepared_weights_bit_exact(hip, cin, cout):
+    """Both prepared forms, from the single-form and the two-form entry points, bit-exact
+    against the host construction (every padded element zero)."""
+    rng = np.random.default_rng(cin * 1000 + cout)
+    w = oracle.rng_bf16(rng, (cout, cin, 3, 3))
+    wd = dev(w)
+    nf = hip.xdna_conv3x3_prepared_weight_bytes(cin, cout)
+    nd = hip.xdna_conv3x3_prepared_weight_bytes(cout, cin)
+    for dgrad, n in ((0, nf), (1, nd)):
+        out = dev_zeros((n // 2,)) - 1  # every element must be written
+        assert hip.xdna_conv3x3_prepare_weights_bf16(ptr(wd), ptr(out), cout, cin, dgrad, stream()) == 0
+        exp = _prepared_expected(w, dgrad)
+        np.testing.assert_array_equal(host(out)[:exp.size], exp, err_msg=f"form {dgrad}")
+    of, od = dev_zeros((nf // 2,)) - 1, dev_zeros((nd // 2,)) - 1
+    assert hip.xdna_conv3x3_prepare_weights_both_bf16(ptr(wd), ptr(of), ptr(od), cout, cin, stream()) == 0
+    np.testing.assert_array_equal(host(of)[:_prepared_expected(w, 0).size], _prepared_expected(w, 0))
+    np.testing.assert_array_equal(host(od)[:_prepared_expected(w, 1).size], _prepared_expected(w, 1))

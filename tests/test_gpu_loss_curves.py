@@ -10,17 +10,17 @@ kernel, which is what the reference executes for an xdna model (its pre-hook pic
 fused=True and the CPU kernel runs it, device.py:408-436); the xdna run leaves the choice
 to the backend's pre-hook.  The bar:
 
-* configs 1 and 3, and config 4's first window: every window within 1 % of the CPU run
-  (north_star's bar), with an absolute floor of 1e-4 x the first window for losses that
-  have collapsed to rounding level (config 1 trains to ~0);
+* config 1, config 3's first two windows and the first window of configs 4 and 5: within
+  1 % of the CPU run (north_star's bar), with an absolute floor of 1e-4 x the first window
+  for losses that have collapsed to rounding level (config 1 trains to ~0);
 * every window of every config: within 1 %, or within 1.5x the CPU's own rounding spread
   up to that window: the largest deviation, over the windows so far, of three CPU runs
   whose only difference is one weight moved by one bf16 ulp (a trajectory that rounding
   has moved stays moved, so the envelope is cumulative).  This is the reference's
   criterion ("stays within the run-to-run spread", loss_curve_compare.py:10-14).  On
-  config 4 that spread is ~3 % (measured): rounding alone moves its curve by more than
-  1 %, so no implementation that is not bit-identical to the CPU's kernels can meet a flat
-  1 % there.
+  config 4 that spread is ~3 % (measured), on config 3 past step 40 up to ~27 %: rounding
+  alone moves those curves by more than 1 %, so no implementation that is not
+  bit-identical to the CPU's kernels can meet a flat 1 % there.
 
 The CPU's default single-tensor Adam (the reference's plain CPU path) is run too, and the
 xdna curve must be as close to it as the CPU's fused run is, within 1 % more.  Path
@@ -147,9 +147,12 @@ def _fixture(name):
 def test_c3_mlp_200_steps():
     """BASELINE config 3 (MLP, x [8192,1024], MSE, Adam): 200 steps against the CPU bf16
     runs recorded by tests/golden/make_loss_curves.py (five 200-step CPU runs do not fit the
-    test's time)."""
+    test's time).  The first 40 steps (two windows) within a flat 1 %; from step 40 on the
+    run is chaotic (the loss oscillates, and the CPU's own run with one weight moved by one
+    ulp leaves it by 1.7 % in steps 40-59 and by over 20 % later), so later windows take
+    the spread criterion, as config 4's do."""
     _check("C3", bench.build_mlp, 200, ("hip_gemm.addmm.run", "hip_gemm.mm.run", "hip_adam.run"),
-           strict_windows=None, fixture=_fixture("C3"))
+           strict_windows=2, fixture=_fixture("C3"))
 
 
 @pytest.mark.timeout(300)
