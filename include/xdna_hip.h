@@ -432,6 +432,10 @@ int xdna_gemm_set_small(int on);
  * reference counterpart. */
 int xdna_conv3x3_set_pack_rows(int rows);
 
+/* Output channels per workgroup of the weight preparation: 0 (default) by the weight's
+ * size, else 8 or 32.  For measurements; no reference counterpart. */
+int xdna_conv3x3_set_prep_tile(int co);
+
 /* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments, kernels and results, bit for bit; it calls no

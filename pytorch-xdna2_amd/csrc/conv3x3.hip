@@ -49,33 +49,38 @@ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 // Weight preparation: OIHW bf16 -> Wt[co_pad][chunks*9*64] (k order chunk, tap, c).
 // dgrad: the conv of dY (cin' = Cout channels) with w'[ci][co][t] = w[co][ci][8-t].
 // ---------------------------------------------------------------------------------
-// Both prepared forms from one read of the weight: a workgroup takes a block of 32 output
-// x 64 input channels of the OIHW weight (32 rows of 64 x 9 contiguous elements, read with
-// 16-byte loads where the rows allow) into LDS, then writes the forward form's 32 rows
-// [tap][64 ci] of chunk ci0 / 64 and the input-gradient form's 64 rows [tap][32 co] (taps
+// Both prepared forms from one read of the weight: a workgroup takes a block of CO output
+// x 64 input channels of the OIHW weight (CO rows of 64 x 9 contiguous elements, read with
+// 16-byte loads where the rows allow) into LDS, then writes the forward form's CO rows
+// [tap][64 ci] of chunk ci0 / 64 and the input-gradient form's 64 rows [tap][CO co] (taps
 // flipped) of chunk co0 / 64, each in 16-byte stores.  Blocks cover the padded extents of
 // both forms; elements outside Cout x Cin are zeros.  wt or wtd may be null (that form is
-// not written).  (The element-per-thread form spent most of its time in 64-bit index
-// divisions and 18-byte-strided gathers: up to 17 us for a 512-channel weight.)
-constexpr int kPrepCo = 32, kPrepCi = 64, kPrepRow = kPrepCi * 9;  // 576 elements per block row
+// not written).  CO is 32 for weights that give a full grid of such blocks and 8 (a quarter
+// of the work per workgroup, four times the workgroups) for smaller ones, whose time is the
+// latency of one block.  (The element-per-thread form spent most of its time in 64-bit
+// index divisions and 18-byte-strided gathers: up to 17 us for a 512-channel weight.)
+constexpr int kPrepCi = 64, kPrepRow = kPrepCi * 9;  // 576 elements per block row
 
-__global__ __launch_bounds__(256) void prep_tiled_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
-                                                         uint16_t* __restrict__ wtd, int Cout, int Cin, int co_pad_f,
-                                                         int chunks_f, int co_pad_d, int chunks_d, int vec) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[kPrepCo * kPrepRow];  // [co_l][ci_l * 9 + tap]
-  const int ci0 = blockIdx.x * kPrepCi, co0 = blockIdx.y * kPrepCo;
+template <int CO>
+__global__ __launch_bounds__(CO * 8) void prep_tiled_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                            uint16_t* __restrict__ wtd, int Cout, int Cin, int co_pad_f,
+                                                            int chunks_f, int co_pad_d, int chunks_d, int vec) {
+  constexpr int NT = CO * 8;  // threads
+  __shared__ __attribute__((aligned(16))) uint16_t tile[CO * kPrepRow];  // [co_l][ci_l * 9 + tap]
+  const int ci0 = blockIdx.x * kPrepCi, co0 = blockIdx.y * CO;
   const int tid = threadIdx.x;
-  const bool full = vec && ci0 + kPrepCi <= Cin && co0 + kPrepCo <= Cout;
+  const bool full = vec && ci0 + kPrepCi <= Cin && co0 + CO <= Cout;
   if (full) {
-    // 32 rows x 72 pieces of 16 bytes, each row starting at a 16-byte boundary (Cin % 8 == 0)
-    for (int e = tid; e < kPrepCo * (kPrepRow / 8); e += 256) {
+    // CO rows x 72 pieces of 16 bytes, each row starting at a 16-byte boundary (Cin % 8 == 0)
+#pragma unroll
+    for (int e = tid; e < CO * (kPrepRow / 8); e += NT) {
       const int r = e / (kPrepRow / 8), q = e - r * (kPrepRow / 8);
       const uint4 v = *reinterpret_cast<const uint4*>(w + (int64_t(co0 + r) * Cin + ci0) * 9 + q * 8);
       *reinterpret_cast<uint4*>(tile + r * kPrepRow + q * 8) = v;
     }
   } else if (co0 < Cout && ci0 < Cin) {
     // a block at the weight's edge: element loads, 8 per thread in flight per round
-    for (int e0 = tid * 8; e0 < kPrepCo * kPrepRow; e0 += 256 * 8) {
+    for (int e0 = tid * 8; e0 < CO * kPrepRow; e0 += NT * 8) {
       uint16_t v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -88,13 +93,13 @@ __global__ __launch_bounds__(256) void prep_tiled_kernel(const uint16_t* __restr
     }
   } else {
     // only padding: zeros, no loads
-    for (int e0 = tid * 8; e0 < kPrepCo * kPrepRow; e0 += 256 * 8)
+    for (int e0 = tid * 8; e0 < CO * kPrepRow; e0 += NT * 8)
       *reinterpret_cast<uint4*>(tile + e0) = make_uint4(0u, 0u, 0u, 0u);
   }
   __syncthreads();
   // forward form: row co, k = (chunk ci0 / 64, tap, c); 8 consecutive c per store
   if (wt && co0 < co_pad_f && ci0 < chunks_f * kKStep) {
-    for (int e = tid; e < kPrepCo * 72; e += 256) {
+    for (int e = tid; e < CO * 72; e += NT) {
       const int r = e / 72, q = e - r * 72;
       const int tap = q >> 3, c0 = (q & 7) * 8;
       uint32_t u[4];
@@ -108,10 +113,10 @@ __global__ __launch_bounds__(256) void prep_tiled_kernel(const uint16_t* __restr
   }
   // input-gradient form: row ci, k = (chunk co0 / 64, tap, co), w'[ci][co][t] = w[co][ci][8 - t]
   if (wtd && ci0 < co_pad_d && co0 < chunks_d * kKStep) {
-    const int cb = co0 % kKStep;  // 0 or 32: this block's half of the chunk
-    for (int e = tid; e < kPrepCi * 9 * (kPrepCo / 8); e += 256) {
-      const int r = e / (9 * (kPrepCo / 8)), q = e - r * (9 * (kPrepCo / 8));
-      const int tap = q / (kPrepCo / 8), c0 = (q % (kPrepCo / 8)) * 8;
+    const int cb = co0 % kKStep;  // this block's CO-channel part of the chunk
+    for (int e = tid; e < kPrepCi * 9 * (CO / 8); e += NT) {
+      const int r = e / (9 * (CO / 8)), q = e - r * (9 * (CO / 8));
+      const int tap = q / (CO / 8), c0 = (q % (CO / 8)) * 8;
       uint32_t u[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -1892,6 +1897,9 @@ bool shape_ok(const char* what, int B, int Cin, int Cout, int H, int W) {
 
 // The forward form (wt) and / or the input-gradient form (wtd) of an OIHW weight in one
 // launch of prep_tiled_kernel.
+// output-channel tile of the weight preparation: 0 by size, else 8 or 32
+std::atomic<int> g_prep_co{0};
+
 int launch_prep_tiled(const uint16_t* w, uint16_t* wt, uint16_t* wtd, int Cout, int Cin, void* stream) {
   if (!admit_launch("conv3x3 weight preparation")) return -1;
   const FwdPlan pf = fwd_plan(1, Cin, Cout, 1, 1), pd = fwd_plan(1, Cout, Cin, 1, 1);
@@ -1900,9 +1908,15 @@ int launch_prep_tiled(const uint16_t* w, uint16_t* wt, uint16_t* wtd, int Cout, 
   const int ci_ext = std::max(wt ? pf.chunks * kKStep : 0, wtd ? pd.co_pad : 0);
   const int co_ext = std::max(wt ? pf.co_pad : 0, wtd ? pd.chunks * kKStep : 0);
   const int vec = (Cin % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) ? 1 : 0;
-  const dim3 grid(unsigned(ceil_div(ci_ext, kPrepCi)), unsigned(ceil_div(co_ext, kPrepCo)));
-  prep_tiled_kernel<<<grid, 256, 0, as_stream(stream)>>>(w, wt, wtd, Cout, Cin, pf.co_pad, pf.chunks, pd.co_pad,
-                                                          pd.chunks, vec);
+  const int64_t blocks32 = ceil_div(ci_ext, kPrepCi) * ceil_div(co_ext, 32);
+  const int co_tile = g_prep_co.load() ? g_prep_co.load() : (blocks32 < 256 ? 8 : 32);
+  const dim3 grid(unsigned(ceil_div(ci_ext, kPrepCi)), unsigned(ceil_div(co_ext, co_tile)));
+  if (co_tile == 8)
+    prep_tiled_kernel<8><<<grid, 64, 0, as_stream(stream)>>>(w, wt, wtd, Cout, Cin, pf.co_pad, pf.chunks, pd.co_pad,
+                                                             pd.chunks, vec);
+  else
+    prep_tiled_kernel<32><<<grid, 256, 0, as_stream(stream)>>>(w, wt, wtd, Cout, Cin, pf.co_pad, pf.chunks, pd.co_pad,
+                                                               pd.chunks, vec);
   return check_launch("conv3x3 weight preparation");
 }
 
@@ -3050,6 +3064,15 @@ int xdna_conv3x3_set_rows_variant(int variant) {
     return -1;
   }
   g_rows_variant.store(variant);
+  return 0;
+}
+
+int xdna_conv3x3_set_prep_tile(int co) {
+  if (co != 0 && co != 8 && co != 32) {
+    set_error("xdna_conv3x3_set_prep_tile: the tile must be 0 (by size), 8 or 32");
+    return -1;
+  }
+  g_prep_co.store(co);
   return 0;
 }
 

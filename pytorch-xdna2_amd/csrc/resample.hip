@@ -56,6 +56,45 @@ __global__ __launch_bounds__(256) void upsample2x_bwd_kernel(const uint16_t* __r
 // and the spread of a gradient onto the stride-1 grid, full[p][y][x] = dy[p][y/2][x/2] at
 // even (y, x) and 0 elsewhere (the input / weight gradients then run at stride 1; the
 // zeros add nothing to their sums).  Full planes H x W, sampled ceil(H/2) x ceil(W/2).
+//
+// Widths that are multiples of 4 (every ResNet and style-network plane) take the vector
+// forms: one thread per 8 bytes of the full grid (4 pixels) and 4 bytes of the sampled one
+// (2 pixels), 32-bit index arithmetic; other widths take one thread per element.
+
+// y[r][2q .. 2q+1] = full[row(r)][4q], full[row(r)][4q + 2]; r = plane * Ho + oy, Wq = W / 4
+__global__ __launch_bounds__(256) void subsample2_vec_kernel(const uint2* __restrict__ full,
+                                                             uint32_t* __restrict__ y, uint32_t n, uint32_t Wq,
+                                                             uint32_t H, uint32_t Ho) {
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
+    const uint32_t r = i / Wq, q = i - r * Wq;
+    const uint32_t p = r / Ho, oy = r - p * Ho;
+    const uint2 v = full[(p * H + 2u * oy) * Wq + q];
+    y[i] = (v.x & 0xFFFFu) | (v.y << 16);
+  }
+}
+
+// full[row][4q .. 4q+3] = (dy[p][y/2][2q], 0, dy[p][y/2][2q+1], 0) on even rows y, zeros on
+// odd ones; row = plane * H + y, Wq = W / 4 = Wo / 2
+__global__ __launch_bounds__(256) void dilate2_vec_kernel(const uint32_t* __restrict__ dy,
+                                                          uint2* __restrict__ full, uint32_t n, uint32_t Wq,
+                                                          uint32_t H, uint32_t Ho) {
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
+    const uint32_t row = i / Wq, q = i - row * Wq;
+    const uint32_t p = row / H, yy = row - p * H;
+    uint2 o = make_uint2(0u, 0u);
+    if ((yy & 1u) == 0) {
+      const uint32_t v = dy[(p * Ho + yy / 2u) * Wq + q];
+      o = make_uint2(v & 0xFFFFu, v >> 16);
+    }
+    full[i] = o;
+  }
+}
+
+// vector forms apply: W % 4 == 0, both buffers 8-byte aligned, index range in 32 bits
+bool resample_vec(const void* a, const void* b, int64_t planes, int H, int W) {
+  return W % 4 == 0 && ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 7) == 0 &&
+         planes * H * int64_t(W) < (int64_t(1) << 31);
+}
 __global__ __launch_bounds__(256) void subsample2_kernel(const uint16_t* __restrict__ full,
                                                          uint16_t* __restrict__ y, int64_t n, int H, int W) {
   const int Ho = (H + 1) / 2, Wo = (W + 1) / 2;
@@ -130,8 +169,15 @@ int xdna_subsample2_bf16(const uint16_t* full, uint16_t* y, int64_t planes, int 
   const int64_t n = planes * ((H + 1) / 2) * ((W + 1) / 2);
   if (n == 0) return 0;
   if (!admit_launch("xdna_subsample2_bf16")) return -1;
-  subsample2_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(full, y, n,
-                                                                                                          H, W);
+  if (resample_vec(full, y, planes, H, W)) {
+    const uint32_t nv = uint32_t(n / 2);  // 2 output pixels per thread (Wo = W / 2 is even)
+    subsample2_vec_kernel<<<unsigned(std::min<int64_t>(ceil_div(nv, 256), 65536)), 256, 0, as_stream(stream)>>>(
+        reinterpret_cast<const uint2*>(full), reinterpret_cast<uint32_t*>(y), nv, uint32_t(W / 4), uint32_t(H),
+        uint32_t((H + 1) / 2));
+  } else {
+    subsample2_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(full, y,
+                                                                                                            n, H, W);
+  }
   return check_launch("xdna_subsample2_bf16");
 }
 
@@ -143,8 +189,15 @@ int xdna_dilate2_bf16(const uint16_t* dy, uint16_t* full, int64_t planes, int H,
   const int64_t n = planes * H * W;
   if (n == 0) return 0;
   if (!admit_launch("xdna_dilate2_bf16")) return -1;
-  dilate2_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(dy, full, n, H,
-                                                                                                       W);
+  if (resample_vec(dy, full, planes, H, W)) {
+    const uint32_t nv = uint32_t(n / 4);  // 4 full-grid pixels per thread
+    dilate2_vec_kernel<<<unsigned(std::min<int64_t>(ceil_div(nv, 256), 65536)), 256, 0, as_stream(stream)>>>(
+        reinterpret_cast<const uint32_t*>(dy), reinterpret_cast<uint2*>(full), nv, uint32_t(W / 4), uint32_t(H),
+        uint32_t((H + 1) / 2));
+  } else {
+    dilate2_kernel<<<unsigned(std::min<int64_t>(ceil_div(n, 256), 65536)), 256, 0, as_stream(stream)>>>(dy, full, n,
+                                                                                                         H, W);
+  }
   return check_launch("xdna_dilate2_bf16");
 }
 

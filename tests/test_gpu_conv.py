@@ -244,11 +244,21 @@ def _prepared_expected(w, dgrad):
     return tmp.reshape(co_pad, chunks, 64, 9).transpose(0, 1, 3, 2).reshape(-1)
 
 
+@pytest.mark.parametrize("tile", [0, 8, 32])
 @pytest.mark.parametrize("cin,cout", [(3, 64), (64, 64), (128, 128), (256, 512), (512, 256), (100, 36), (36, 300),
                                       (8, 3), (520, 130)])
-def test_prepared_weights_bit_exact(hip, cin, cout):
+def test_prepared_weights_bit_exact(hip, cin, cout, tile):
     """Both prepared forms, from the single-form and the two-form entry points, bit-exact
-    against the host construction (every padded element zero)."""
+    against the host construction (every padded element zero), with the preparation's
+    output-channel tile chosen by size (0) or forced to 8 or 32."""
+    assert hip.xdna_conv3x3_set_prep_tile(tile) == 0
+    try:
+        _check_prepared(hip, cin, cout)
+    finally:
+        hip.xdna_conv3x3_set_prep_tile(0)
+
+
+def _check_prepared(hip, cin, cout):
     rng = np.random.default_rng(cin * 1000 + cout)
     w = oracle.rng_bf16(rng, (cout, cin, 3, 3))
     wd = dev(w)

@@ -51,17 +51,21 @@ def test_stride2_conv_matches_oracle(shape):
     check_bf16(bits(cd.bias.grad), gb, what=f"bias grad {shape}")
 
 
-def test_stride2_sampling_c_abi():
+@pytest.mark.parametrize("H,W", [(7, 10), (16, 16), (9, 12), (36, 36), (64, 64), (5, 4)])
+def test_stride2_sampling_c_abi(H, W):
+    """Both samplings bit for bit against slicing, in the element form (W % 4 != 0) and the
+    vector form (W % 4 == 0, odd H included)."""
     lib = hip_abi.load()
     st = torch.cuda.current_stream().cuda_stream
-    full = torch.randn(3, 4, 7, 10, device="cuda").bfloat16()
-    y = torch.full((3, 4, 4, 5), 7.0, device="cuda").bfloat16()
-    assert lib.xdna_subsample2_bf16(full.data_ptr(), y.data_ptr(), 12, 7, 10, st) == 0
-    back = torch.full((3, 4, 7, 10), 7.0, device="cuda").bfloat16()
-    assert lib.xdna_dilate2_bf16(y.data_ptr(), back.data_ptr(), 12, 7, 10, st) == 0
+    Ho, Wo = (H + 1) // 2, (W + 1) // 2
+    full = torch.randn(3, 4, H, W, device="cuda").bfloat16()
+    y = torch.full((3, 4, Ho, Wo), 7.0, device="cuda").bfloat16()
+    assert lib.xdna_subsample2_bf16(full.data_ptr(), y.data_ptr(), 12, H, W, st) == 0
+    back = torch.full((3, 4, H, W), 7.0, device="cuda").bfloat16()
+    assert lib.xdna_dilate2_bf16(y.data_ptr(), back.data_ptr(), 12, H, W, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(y, full[:, :, ::2, ::2])
     ref = torch.zeros_like(full)
     ref[:, :, ::2, ::2] = full[:, :, ::2, ::2]
     assert torch.equal(back, ref)
-    assert lib.xdna_subsample2_bf16(full.data_ptr(), None, 12, 7, 10, st) == -1
+    assert lib.xdna_subsample2_bf16(full.data_ptr(), None, 12, H, W, st) == -1
