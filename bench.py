@@ -120,7 +120,7 @@ def gram(f):
     return (x @ x.transpose(1, 2)).float() / float(c * h * w)
 
 
-def build_style(torch, device, batch=40, size=36, fused=True, region=False):
+def build_style(torch, device, batch=40, size=36, fused=True, region=False, lr=1e-3, weight_decay=0.0):
     """BASELINE config 4's training step on `device`; returns (step, generator).  fused:
     Adam's fused kernel (what an xdna model runs, and the reference's pre-hook picks),
     or None for the optimizer's default (single-tensor on the CPU).  region: the loss
@@ -146,7 +146,8 @@ def build_style(torch, device, batch=40, size=36, fused=True, region=False):
         sf = vgg(style, STYLE_TAPS)
         style_grams = {k: gram(v) for k, v in sf.items()}
     # capturable: the step may be captured in a graph (same fused Adam kernel either way)
-    opt = torch.optim.Adam(gen.parameters(), lr=1e-3, fused=fused, capturable=device.type != "cpu")
+    opt = torch.optim.Adam(gen.parameters(), lr=lr, weight_decay=weight_decay, fused=fused,
+                           capturable=device.type != "cpu")
 
     if region:
         from xdna_train import regions

@@ -193,6 +193,30 @@ size_t xdna_conv3x3w_weights_bfp16_bytes(int chunks);
  * reproducing the NPU's weight rounding. */
 int xdna_bfp16_decode_f32(const uint8_t* src, float* dst, int64_t nblocks, void* stream);
 
+/* BFP16 emulation of the reference NPU's conv arithmetic (the optional mode its
+ * benchmarks/bfp16_training_gate.py:1-20 restates on the CPU; kernel
+ * _designs/conv3x3w_kernel.cc:40-51, 105-108, 129-138).
+ *
+ * xdna_bfp16_quantize8_bf16: every aligned run of 8 bf16 values (nblocks runs, 16 bytes
+ * each, 16-byte aligned; src == dst allowed) becomes the values of its bfp16ebs8 block,
+ * q * 2^(e_max - 133) with q the codec's mantissa (conv_pack.cpp:398-443: e_max the
+ * largest biased exponent, q = clamp(round_half_even(v * 2^(133 - e_max)), -128, 127)),
+ * as bf16 bits (exact; -2^128 overflows to -inf).  NaN stays NaN; +-inf saturate to +-inf
+ * as the codec's bytes decode.  On the packed rows this is the NPU core's 8-channel
+ * conversion of the activations; on the prepared weights, the codec's blocks.
+ *
+ * xdna_conv3x3_layout_rows_bfp16_emul_bf16: xdna_conv3x3_layout_rows_act_bf16 with that
+ * arithmetic: the packed input and the prepared weights quantized (into transient
+ * copies), the running sum stored as bf16 after every (chunk, tap), chunks outer and the
+ * 9 taps inner as the NPU loops (conv3x3w.py:172-177), the bias added after the last
+ * rounding in one more bf16 rounding (torch_xdna_device.cpp:2477-2480).  The forward and
+ * input-gradient convs use it (the reference's NPU runs both); weight gradients stay
+ * exact. */
+int xdna_bfp16_quantize8_bf16(const uint16_t* src, uint16_t* dst, int64_t nblocks, void* stream);
+int xdna_conv3x3_layout_rows_bfp16_emul_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
+                                             uint16_t* y, int B, int cin, int cout, int H, int W, int layout, int act,
+                                             void* stream);
+
 /* Replaces xdna_conv3x3w_unpack_output_bf16 (conv_pack.cpp:447-466):
  * [groups*2048][128] bf16 rows -> channel slice [c_start, c_start+cout_valid)
  * of NCHW [B][C_total][H][W] (valid pixels only). */

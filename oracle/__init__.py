@@ -8,7 +8,8 @@ Contents:
 
 * ``liboracle.so`` (``oracle.c``): plain-C restatements of the conv3x3w layouts
   (pack / unpack, with strips, halo_zero and group ranges), the BFP16 weight codec
-  (forward and dX forms), the direct 3x3 convolution forward / input-gradient /
+  (forward and dX forms), the BFP16 emulation of the NPU's conv arithmetic (block
+  quantization, bf16 running sum per chunk and tap), the direct 3x3 convolution forward / input-gradient /
   weight-gradient / bias-gradient in double precision, and the fused Adam step.
 * numpy helpers: bf16 rounding, the GEMM reference (float64 products of bf16 values),
   and the layout geometry.
@@ -63,6 +64,8 @@ def lib():
         _lib.oracle_adam.argtypes = [P, P, P, P, P, L, I, D, D, D, D, D, D, I, I, I, D, I]
         _lib.oracle_strip_geometry.argtypes = [I, ctypes.POINTER(I), ctypes.POINTER(I)]
         _lib.oracle_pack_weights_bfp16.argtypes = [P, P, I, I, I, I, I, I]
+        _lib.oracle_bfp16_quantize8.argtypes = [P, P, L]
+        _lib.oracle_conv3x3_bfp16_emul.argtypes = [P, P, P, P, I, I, I, I, I]
     return _lib
 
 
@@ -253,6 +256,40 @@ def bfp16_decode(blocks: np.ndarray) -> np.ndarray:
     e = b[:, :1].astype(np.int64)
     m = b[:, 1:].view(np.int8).astype(np.float64)
     return np.ldexp(m, e - 133).reshape(-1)
+
+
+# ---------------------------------------------------------------------------
+# BFP16 emulation of the reference NPU's conv arithmetic (oracle.c: quantization as the
+# codec's blocks decode; chunk-major, tap-inner bf16 running sum; bias after)
+# ---------------------------------------------------------------------------
+
+def bfp16_quantize8(bits: np.ndarray) -> np.ndarray:
+    """bf16 bits (size a multiple of 8) -> the BFP16 values of each aligned run of 8, as bf16 bits."""
+    src = np.ascontiguousarray(bits, dtype=np.uint16)
+    assert src.size % 8 == 0
+    out = np.empty_like(src)
+    lib().oracle_bfp16_quantize8(src.ctypes.data, out.ctypes.data, src.size // 8)
+    return out
+
+
+def conv3x3_bfp16_emul(x_bits, w_bits, bias_bits=None) -> np.ndarray:
+    """The NPU-arithmetic forward conv (3x3, stride 1, pad 1) -> bf16 bits [B, Cout, H, W]."""
+    B, Cin, H, W = x_bits.shape
+    Cout = w_bits.shape[0]
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    w = np.ascontiguousarray(w_bits, np.uint16)
+    b = None if bias_bits is None else np.ascontiguousarray(bias_bits, np.uint16)
+    y = np.empty((B, Cout, H, W), np.uint16)
+    lib().oracle_conv3x3_bfp16_emul(x.ctypes.data, w.ctypes.data, None if b is None else b.ctypes.data,
+                                    y.ctypes.data, B, Cin, Cout, H, W)
+    return y
+
+
+def conv3x3_dgrad_bfp16_emul(dy_bits, w_bits) -> np.ndarray:
+    """The NPU-arithmetic input gradient: the emulated forward conv of dY with the flipped,
+    swapped weights w'[ci][co][t] = w[co][ci][8 - t] (conv_pack.cpp:470-473)."""
+    wd = np.ascontiguousarray(np.asarray(w_bits, np.uint16)[:, :, ::-1, ::-1].transpose(1, 0, 2, 3))
+    return conv3x3_bfp16_emul(dy_bits, wd)
 
 
 # ---------------------------------------------------------------------------

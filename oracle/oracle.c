@@ -12,6 +12,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define GROUP_OUT_ROWS 2048
@@ -325,4 +326,109 @@ void oracle_pack_weights_bfp16(const uint16_t* w, uint8_t* dst, int Cout, int Ci
             }
           }
   }
+}
+
+/*
+ * BFP16 emulation of the reference NPU's conv arithmetic (the optional mode restated by
+ * the reference's benchmarks/bfp16_training_gate.py:33-57; the NPU kernel
+ * _designs/conv3x3w_kernel.cc:40-51, 105-108 and its loop order conv3x3w.py:172-177).
+ *
+ * Quantization: an aligned run of 8 values becomes the values of its bfp16ebs8 block, as
+ * the codec above encodes it and the block decodes: q = clip(rint(v * 2^(133 - e_max)),
+ * -128, 127), value q * 2^(e_max - 133), with e_max the largest biased exponent field of
+ * the 8 (NaN stays NaN).  The value is formed in double and converted to float (exact, or
+ * +-inf past the float range) and then to bf16 (exact: at most 8 significant bits).
+ */
+static void bfp16_quant8(const uint16_t* in, uint16_t* out) {
+  int emax = 0;
+  for (int i = 0; i < 8; ++i) {
+    const int e = (in[i] >> 7) & 0xFF;
+    if (e > emax) emax = e;
+  }
+  for (int i = 0; i < 8; ++i) {
+    const float v = bf16f(in[i]);
+    if (isnan(v)) {
+      out[i] = 0x7FC0;
+      continue;
+    }
+    double q = nearbyint(ldexp((double)v, 133 - emax));
+    if (q < -128.0) q = -128.0;
+    if (q > 127.0) q = 127.0;
+    if (q == 0.0) q = 0.0; /* an int8 mantissa of 0 is +0 (nearbyint keeps the sign of -0.3) */
+    out[i] = f2bf16((float)ldexp(q, emax - 133));
+  }
+}
+
+void oracle_bfp16_quantize8(const uint16_t* src, uint16_t* dst, int64_t nblocks) {
+  for (int64_t b = 0; b < nblocks; ++b) bfp16_quant8(src + 8 * b, dst + 8 * b);
+}
+
+/* Round-to-nearest-even of a double to bf16 bits in one step (no float in between):
+ * 8 significant bits in the normal range, multiples of 2^-133 below 2^-126. */
+static uint16_t d2bf16(double x) {
+  if (isnan(x)) return 0x7FC0;
+  if (x == 0.0) return signbit(x) ? 0x8000 : 0;
+  int e;
+  (void)frexp(x, &e);                       /* |x| in [2^(e-1), 2^e) */
+  const int lsb = e - 8 > -133 ? e - 8 : -133;
+  const double r = ldexp(nearbyint(ldexp(x, -lsb)), lsb);
+  return f2bf16((float)r);                  /* exact, or +-inf past the range */
+}
+
+/*
+ * The emulated forward conv (3x3, stride 1, pad 1): x [B][Cin][H][W] quantized in runs of
+ * 8 channels at each pixel (channels past Cin are zeros), w [Cout][Cin][3][3] in runs of 8
+ * input channels at each (output channel, tap); per output, C = 0 and, for each 64-channel
+ * chunk and within it each tap (dy, dx) in order, C = bf16(C + the chunk's 64-term sum in
+ * double); then y = bf16(float(C) + float(bias)) (the reference's host bias add,
+ * torch_xdna_device.cpp:2477-2480).  y holds bf16 bits.
+ */
+void oracle_conv3x3_bfp16_emul(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* y, int B,
+                               int Cin, int Cout, int H, int W) {
+  const int chunks = (Cin + KSTEP - 1) / KSTEP, cpad = chunks * KSTEP;
+  const size_t plane = (size_t)H * W;
+  /* quantized operands: xq [B][H][W][cpad] (channel runs contiguous), wq [Cout][9][cpad] */
+  uint16_t* xq = (uint16_t*)malloc((size_t)B * plane * cpad * 2);
+  uint16_t* wq = (uint16_t*)malloc((size_t)Cout * 9 * cpad * 2);
+  if (!xq || !wq) {
+    free(xq);
+    free(wq);
+    return;
+  }
+  uint16_t run[8];
+  for (int b = 0; b < B; ++b)
+    for (size_t p = 0; p < plane; ++p)
+      for (int c0 = 0; c0 < cpad; c0 += 8) {
+        for (int i = 0; i < 8; ++i)
+          run[i] = c0 + i < Cin ? x[((size_t)b * Cin + c0 + i) * plane + p] : 0;
+        bfp16_quant8(run, xq + ((size_t)b * plane + p) * cpad + c0);
+      }
+  for (int co = 0; co < Cout; ++co)
+    for (int t = 0; t < 9; ++t)
+      for (int c0 = 0; c0 < cpad; c0 += 8) {
+        for (int i = 0; i < 8; ++i) run[i] = c0 + i < Cin ? w[((size_t)co * Cin + c0 + i) * 9 + t] : 0;
+        bfp16_quant8(run, wq + ((size_t)co * 9 + t) * cpad + c0);
+      }
+  for (int b = 0; b < B; ++b)
+    for (int co = 0; co < Cout; ++co)
+      for (int yy = 0; yy < H; ++yy)
+        for (int xx = 0; xx < W; ++xx) {
+          double C = 0.0;
+          for (int ch = 0; ch < chunks; ++ch)
+            for (int t = 0; t < 9; ++t) {
+              const int sy = yy + t / 3 - 1, sx = xx + t % 3 - 1;
+              double s = 0.0;
+              if (sy >= 0 && sy < H && sx >= 0 && sx < W) {
+                const uint16_t* xr = xq + ((size_t)b * plane + (size_t)sy * W + sx) * cpad + ch * KSTEP;
+                const uint16_t* wr = wq + ((size_t)co * 9 + t) * cpad + ch * KSTEP;
+                for (int c = 0; c < KSTEP; ++c) s += (double)bf16f(xr[c]) * (double)bf16f(wr[c]);
+              }
+              C = (double)bf16f(d2bf16(C + s));
+            }
+          float out = (float)C;
+          if (bias) out += bf16f(bias[co]);
+          y[(((size_t)b * Cout + co) * H + yy) * W + xx] = f2bf16(out);
+        }
+  free(xq);
+  free(wq);
 }

@@ -103,6 +103,57 @@ __global__ __launch_bounds__(256) void bfp16_decode_kernel(const uint8_t* __rest
   for (int i = 0; i < 8; ++i) dst[b * 8 + i] = ldexpf(float(int8_t(s[1 + i])), e - 133);
 }
 
+// ---------------------------------------------------------------------------------
+// Quantization in place of the format: every aligned run of 8 bf16 values becomes the
+// values its bfp16ebs8 block decodes to, q * 2^(e_max - 133), as bf16 bits.  This is what
+// the reference's NPU conv computes with (weights through the codec above, activations
+// through the core's round-to-nearest-even conversion of 8-channel blocks; the emulation
+// is restated in benchmarks/bfp16_training_gate.py:33-44).  The result is exact: |q| <= 128
+// has at most 8 significant bits and e_max >= 1 puts its last bit at or above 2^-132, so
+// it is a bf16 value (subnormal below 2^-126); a block whose largest exponent is 254 can
+// round -1.99 * 2^127 to -128 * 2^121 = -2^128, which overflows to -inf, as the decode does
+// in fp32.  Non-finite inputs: NaN stays NaN (0x7FC0; the reference's conv gives NaN
+// outputs for NaN operands), +-inf saturate to +-127 / -128 at e_max = 255 and decode to
+// +-inf; the other values of such a block are quantized against e_max = 255, as the codec
+// does.
+// ---------------------------------------------------------------------------------
+__device__ inline uint32_t bfp16_value_bits(int q, int emax) {
+  if (q == 0) return 0u;
+  const uint32_t s = q < 0 ? 0x8000u : 0u;
+  const int mag = q < 0 ? -q : q;                 // 1 .. 128
+  const int k = 31 - __builtin_clz(uint32_t(mag));  // floor(log2 mag): 0 .. 7
+  const int E = emax - 6 + k;                     // biased bf16 exponent of the value
+  if (E >= 255) return s | 0x7F80u;               // overflow: inf
+  if (E >= 1) return s | (uint32_t(E) << 7) | (uint32_t(mag << (7 - k)) & 0x7Fu);
+  return s | uint32_t(mag << emax);               // subnormal: (mag << emax) * 2^-133, < 2^7
+}
+
+__device__ inline uint32_t bfp16_quant_bits(uint16_t h, int emax) {
+  if ((h & 0x7F80u) == 0x7F80u && (h & 0x7Fu)) return 0x7FC0u;  // NaN
+  return bfp16_value_bits(int(int8_t(uint8_t(bfp16_mantissa(h, emax)))), emax);
+}
+
+// one thread per 8-value block (16 bytes)
+__global__ __launch_bounds__(256) void bfp16_quant8_kernel(const u32x4_t* __restrict__ src, u32x4_t* __restrict__ dst,
+                                                           int64_t nblocks) {
+  for (int64_t b = int64_t(blockIdx.x) * 256 + threadIdx.x; b < nblocks; b += int64_t(gridDim.x) * 256) {
+    const u32x4_t v = src[b];
+    uint16_t h[8];
+    int emax = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[2 * i] = uint16_t(v[i] & 0xFFFFu);
+      h[2 * i + 1] = uint16_t(v[i] >> 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) emax = max(emax, (h[i] >> 7) & 0xFF);
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = bfp16_quant_bits(h[2 * i], emax) | (bfp16_quant_bits(h[2 * i + 1], emax) << 16);
+    dst[b] = o;
+  }
+}
+
 bool bfp16_args_ok(const char* what, const void* w, const void* dst, int Cout, int Cin, int chunks,
                    int n_block) {
   if (!w || !dst || Cout < 1 || Cin < 1 || chunks < 1 || n_block < 0 || chunks > (1 << 20)) {
@@ -147,6 +198,22 @@ int xdna_conv3x3w_pack_weights_dx_bfp16(const uint16_t* w, uint8_t* dst, int Cou
   bfp16_weights_kernel<true><<<unsigned(ceil_div(threads, 256)), 256, 0, as_stream(stream)>>>(
       w, dst, Cin_fwd, Cout_fwd, Cin_fwd, chunks, n_block);
   return check_launch("xdna_conv3x3w_pack_weights_dx_bfp16");
+}
+
+int xdna_bfp16_quantize8_bf16(const uint16_t* src, uint16_t* dst, int64_t nblocks, void* stream) {
+  if (nblocks < 0 || (nblocks > 0 && (!src || !dst))) {
+    set_error("xdna_bfp16_quantize8_bf16: invalid arguments");
+    return -1;
+  }
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) {
+    set_error("xdna_bfp16_quantize8_bf16: buffers must be 16-byte aligned");
+    return -1;
+  }
+  if (nblocks == 0) return 0;
+  if (!admit_launch("xdna_bfp16_quantize8_bf16")) return -1;
+  bfp16_quant8_kernel<<<unsigned(std::min<int64_t>(ceil_div(nblocks, 256), 16384)), 256, 0, as_stream(stream)>>>(
+      reinterpret_cast<const u32x4_t*>(src), reinterpret_cast<u32x4_t*>(dst), nblocks);
+  return check_launch("xdna_bfp16_quantize8_bf16");
 }
 
 int xdna_bfp16_decode_f32(const uint8_t* src, float* dst, int64_t nblocks, void* stream) {

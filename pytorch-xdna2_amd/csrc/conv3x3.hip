@@ -1130,10 +1130,18 @@ void conv_rows6_kernel(RowsArgs a) {
 // registers before the current chunk is multiplied.  Wave (wm, wn) owns channels
 // [wm*32, +32) x rows [wn*TP/2, +TP/2).  For convs whose grid is a few hundred
 // workgroups or less, where the main kernel waits on its per-tap weight loads.
+//
+// EMUL: the reference NPU's arithmetic (conv3x3w_kernel.cc:40-51, 105-108; loop order
+// conv3x3w.py:172-177): the running sum is kept as bf16 and rounded after every (chunk,
+// tap), chunks outer and taps inner, and the bias is added after the last rounding (the
+// reference's host bias add, torch_xdna_device.cpp:2477-2480).  Operands come in already
+// quantized to BFP16 values; no split-K (it would change the rounding order).
 constexpr int kSCo = 64;                  // output channels per workgroup
 constexpr int kSWPitch = 9 * kKStep + 8;  // LDS pitch of a staged weight row (584)
 
-template <int TP>
+__device__ inline float round_bf16(float v) { return __uint_as_float(uint32_t(f32_to_bf16(v)) << 16); }
+
+template <int TP, bool EMUL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void conv_small_kernel(RowsArgs a) {
   constexpr int kXRows = TP + kMaxHalo;
@@ -1160,9 +1168,19 @@ void conv_small_kernel(RowsArgs a) {
   const int lr = lane & 31, lk = (lane >> 5) * 8;
 
   f32x16_t acc[NT];
+  float bco[EMUL ? 16 : 1];  // EMUL: the bias of each accumulator row, added at the end
+  if constexpr (EMUL) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 32 + mfma_row(i, lane);
+      bco[i] = a.bias && co < a.cout ? bf16_to_f32(a.bias[co]) : 0.0f;
+    }
+  }
   {
     f32x16_t init = zero_acc();
-    if (a.bias && !a.part && a.bias_vec) {
+    if (EMUL) {
+      // the running sum starts at zero
+    } else if (a.bias && !a.part && a.bias_vec) {
       // 4 runs of 4 consecutive channels per lane: 8-byte buffer loads (as the main kernel)
       const __amdgpu_buffer_rsrc_t brs =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.bias), 0, a.cout * 2, 0x00020000);
@@ -1247,8 +1265,22 @@ void conv_small_kernel(RowsArgs a) {
       const bf16x8_t af = as_bf16x8(aq[slot]);
 #pragma unroll
       for (int n = 0; n < NT; ++n) acc[n] = mfma_32x32x16(af, as_bf16x8(bq[slot][n]), acc[n]);
+      if constexpr (EMUL) {
+        if ((step & 3) == 3) {  // the tap's 64 channels are in: C stored as bf16
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[n][i] = round_bf16(acc[n][i]);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
+  if constexpr (EMUL) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[n][i] += bco[i];
   }
 
   if (a.part) {
@@ -1968,9 +2000,8 @@ std::atomic<int> g_rows_variant{[] {
   return e ? std::atoi(e) : 0;
 }()};
 
-int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
-                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef, int act = 0) {
-  const ConvGeom geom = conv_geom(B, H, W, layout);
+RowsArgs rows_args(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out, int B, int cin,
+                   int cout, int H, int W, const ConvGeom& geom, int act) {
   RowsArgs a;
   a.act = act;
   a.xp = xp;
@@ -1997,6 +2028,26 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     const int64_t span = (512 - 1) / geom.img + 2;
     a.out_rs = span * cout * int64_t(H) * W * 2 < kOutSkip ? 1 : 0;
   }
+  return a;
+}
+
+// LDS of the small-grid kernel with TP-row tiles
+constexpr size_t small_lds(int TP) { return size_t(TP + kMaxHalo) * kPitch * 2 + size_t(kSCo) * kSWPitch * 2; }
+
+template <bool EMUL>
+bool small_lds_ok() {
+  static const bool ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<64, EMUL>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(64))) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128, EMUL>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(128))) == hipSuccess;
+  return ok;
+}
+
+int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
+                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef, int act = 0) {
+  const ConvGeom geom = conv_geom(B, H, W, layout);
+  RowsArgs a = rows_args(xp, wt, bias, out, B, cin, cout, H, W, geom, act);
   if (!admit_launch("conv3x3 rows")) return -1;
   hipStream_t st = as_stream(stream);
   // Kernel choice (xdna_conv3x3_set_rows_variant, or XDNA_ROWS_VARIANT at start-up,
@@ -2088,15 +2139,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
       conv_rows_kernel<64><<<grid, 256, 0, st>>>(a);
     return check_launch("conv3x3 rows");
   }
-  static const bool lds_ok = [] {
-    const int b64 = (64 + kMaxHalo) * kPitch * 2 + kSCo * kSWPitch * 2;
-    const int b128 = (128 + kMaxHalo) * kPitch * 2 + kSCo * kSWPitch * 2;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<64>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, b64) == hipSuccess &&
-           hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, b128) == hipSuccess;
-  }();
-  if (!lds_ok) {
+  if (!small_lds_ok<false>()) {
     set_error("conv3x3 rows: cannot enable the small-grid kernel's LDS size");
     return -1;
   }
@@ -2120,11 +2163,10 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.nrt = int(ceil_div(geom.m_total, TP));
   a.ncot = int(stiles);
   const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, unsigned(nsplit));
-  const size_t lds = size_t(TP + kMaxHalo) * kPitch * 2 + size_t(kSCo) * kSWPitch * 2;
   if (TP == 128)
-    conv_small_kernel<128><<<grid, 256, lds, st>>>(a);
+    conv_small_kernel<128><<<grid, 256, small_lds(128), st>>>(a);
   else
-    conv_small_kernel<64><<<grid, 256, lds, st>>>(a);
+    conv_small_kernel<64><<<grid, 256, small_lds(64), st>>>(a);
   if (nsplit > 1) {
     const unsigned pix_blocks = unsigned(ceil_div(int64_t(H) * W, 256));
     const int planes = B * cout;
@@ -2134,6 +2176,50 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
     xdna_hip_cache_free(a.part);
   }
   return check_launch("conv3x3 rows");
+}
+
+// The BFP16 emulation of the reference NPU's conv: the packed rows and the prepared
+// weights quantized to BFP16 values (8-element blocks: 8 channels of a pixel, 8 channels
+// of a (row, tap) of the weights, which are the codec's blocks), then the small-grid kernel
+// in its EMUL form over every tile, without split-K.  The quantized copies are transient.
+int launch_rows_emul(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out, int B, int cin,
+                     int cout, int H, int W, void* stream, int layout, int act) {
+  const ConvGeom geom = conv_geom(B, H, W, layout);
+  const int chunks = int(ceil_div(cin, kKStep));
+  const size_t xbytes = size_t(geom.groups) * chunks * kGroupRows * kKStep * 2;
+  const size_t wbytes = xdna_conv3x3_prepared_weight_bytes(cin, cout);
+  if (!small_lds_ok<true>()) {
+    set_error("conv3x3 BFP16 emulation: cannot enable the small-grid kernel's LDS size");
+    return -1;
+  }
+  uint16_t* xq = static_cast<uint16_t*>(xdna_hip_cache_alloc(xbytes));
+  if (!xq) return -1;
+  uint16_t* wq = static_cast<uint16_t*>(xdna_hip_cache_alloc(wbytes));
+  if (!wq) {
+    xdna_hip_cache_free(xq);
+    return -1;
+  }
+  int rc = xdna_bfp16_quantize8_bf16(xp, xq, int64_t(xbytes / 16), stream);
+  if (rc == 0) rc = xdna_bfp16_quantize8_bf16(wt, wq, int64_t(wbytes / 16), stream);
+  if (rc == 0 && admit_launch("conv3x3 BFP16 emulation")) {
+    RowsArgs a = rows_args(xq, wq, bias, out, B, cin, cout, H, W, geom, act);
+    const unsigned stiles = unsigned(ceil_div(cout, kSCo));
+    const int TP = ceil_div(geom.m_total, 128) * stiles >= 128 ? 128 : 64;
+    a.nrt = int(ceil_div(geom.m_total, TP));
+    a.ncot = int(stiles);
+    const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
+    if (TP == 128)
+      conv_small_kernel<128, true><<<grid, 256, small_lds(128), as_stream(stream)>>>(a);
+    else
+      conv_small_kernel<64, true><<<grid, 256, small_lds(64), as_stream(stream)>>>(a);
+    rc = check_launch("conv3x3 BFP16 emulation");
+  } else if (rc == 0) {
+    rc = -1;
+  }
+  // stream-ordered reuse: the next user of either block runs after the conv
+  xdna_hip_cache_free(wq);
+  xdna_hip_cache_free(xq);
+  return rc;
 }
 
 struct WgradPlan {
@@ -3038,6 +3124,21 @@ int xdna_conv3x3_layout_rows_act_bf16(const uint16_t* xp, const uint16_t* wt, co
     return -1;
   }
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout, act);
+}
+
+int xdna_conv3x3_layout_rows_bfp16_emul_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
+                                             uint16_t* y, int B, int cin, int cout, int H, int W, int layout, int act,
+                                             void* stream) {
+  if (!shape_ok("xdna_conv3x3_layout_rows_bfp16_emul_bf16", B, cin, cout, H, W)) return -1;
+  if ((layout != kLayoutRef && layout != kLayoutTight) || act < 0 || act > 1) {
+    set_error("xdna_conv3x3_layout_rows_bfp16_emul_bf16: unknown layout or activation");
+    return -1;
+  }
+  if ((reinterpret_cast<uintptr_t>(xp) | reinterpret_cast<uintptr_t>(wt)) & 15) {
+    set_error("xdna_conv3x3_layout_rows_bfp16_emul_bf16: packed rows and weights must be 16-byte aligned");
+    return -1;
+  }
+  return launch_rows_emul(xp, wt, bias, y, B, cin, cout, H, W, stream, layout, act);
 }
 
 int xdna_conv3x3_set_wgrad_rows_kt(int kt_rows) {

@@ -51,6 +51,10 @@ std::atomic<int> g_conv_layout{[] {
   const int v = e ? std::atoi(e) : 1;
   return v < 0 || v > 1 ? 1 : v;
 }()};
+std::atomic<int> g_bfp16_emul{[] {
+  const char* e = std::getenv("XDNA_BFP16_EMULATION");
+  return e && std::atoi(e) == 1 ? 1 : 0;
+}()};
 std::atomic<int> g_wgrad_form{[] {
   const char* e = std::getenv("XDNA_WGRAD_FORM");
   const int v = e ? std::atoi(e) : 0;
@@ -707,6 +711,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     g_conv_layout.store(m);
   });
   mod.def("conv_layout", [] { return g_conv_layout.load(); });
+  mod.def("set_bfp16_emulation", [](bool on) { g_bfp16_emul.store(on ? 1 : 0); });
+  mod.def("bfp16_emulation", [] { return g_bfp16_emul.load() != 0; });
   mod.def("mapped_cpu_stats", [] { return stats_dict(path_stats()); });
   mod.def("reset_mapped_cpu_stats", [] {
     std::lock_guard<std::mutex> lock(stats_mu());

@@ -319,8 +319,10 @@ at::Tensor pack_rows(const at::Tensor& src, int layout) {
 
 // Runs the conv of a packed input (NCHW shape `src`, cin channels) with `w` (forward: w as
 // given; dgrad: flip+swap) into a new NCHW tensor of cout channels.
+// s1: a stride-1 conv of the model (not the stride-1 form of a stride-2 conv), which the
+// BFP16 emulation covers: the reference's NPU takes only stride-1 convs.
 at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef src, const at::Tensor& w,
-                           const at::Tensor* bias, bool dgrad, int act = 0) {
+                           const at::Tensor* bias, bool dgrad, int act = 0, bool s1 = true) {
   const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor wc = w.contiguous();
@@ -369,6 +371,15 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
   at::Tensor bc;
   if (bias) bc = bias->contiguous();
   const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
+  if (s1 && g_bfp16_emul.load()) {
+    ScopedCount sc(dgrad ? "hip_conv3x3.bfp16_emul.dx.run" : "hip_conv3x3.bfp16_emul.fwd.run");
+    check_abi(xdna_conv3x3_layout_rows_bfp16_emul_bf16(
+                  static_cast<const uint16_t*>(packed.const_data_ptr()), static_cast<const uint16_t*>(wt.const_data_ptr()),
+                  bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                  static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout), int(H), int(W), layout, act, st),
+              "conv rows (BFP16 emulation)");
+    return out;
+  }
   KernelTimer kt(dgrad ? "conv3x3_rows.dgrad" : "conv3x3_rows.fwd", flops);
   check_abi(xdna_conv3x3_layout_rows_act_bf16(static_cast<const uint16_t*>(packed.const_data_ptr()),
                                               static_cast<const uint16_t*>(wt.const_data_ptr()),
@@ -536,13 +547,13 @@ std::atomic<int64_t> g_dw_jobs{0};
 // and its gradient takes the rows form (whether or not autograd records this call: a
 // caller may run the aten backward itself).  A kept pack whose backward never comes goes
 // when its input dies.  Inference tensors keep nothing (they have no version counter).
-at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias) {
+at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias, bool s1 = true) {
   const int layout = g_conv_layout.load();
   at::Tensor packed = pack_rows(input, layout);
   if (g_mode.load() >= 2 && weight.requires_grad() && !weight.is_inference() && !input.is_inference() &&
       wgrad_rows_pick(input.size(1), weight.size(0), input.size(3)))
     remember_packed_input(input, packed, layout);
-  return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false);
+  return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false, 0, s1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -738,7 +749,7 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv3x3_s2.fwd.run");
-    const at::Tensor full = hip_conv_fwd(input, weight, has_bias ? &*bias : nullptr);
+    const at::Tensor full = hip_conv_fwd(input, weight, has_bias ? &*bias : nullptr, /*s1=*/false);
     const int64_t B = full.size(0), C = full.size(1), H = full.size(2), W = full.size(3);
     at::Tensor y = empty_xdna({B, C, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16);
     check_abi(xdna_subsample2_bf16(static_cast<const uint16_t*>(full.const_data_ptr()),
@@ -845,6 +856,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
              go_ok && grad_output.size(2) == input.size(2) && grad_output.size(3) == input.size(3);
   // stride 2: the stride-1 gradients of the gradient spread onto the stride-1 grid
   at::Tensor go = grad_output;
+  bool strided = false;
   if (!hip && go_ok && conv_s2_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
       grad_output.size(2) == (input.size(2) + 1) / 2 && grad_output.size(3) == (input.size(3) + 1) / 2) {
     ScopedCount sc("hip_conv3x3_s2.bwd.run");
@@ -855,6 +867,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
                                 static_cast<uint16_t*>(go.data_ptr()), B * C, int(H), int(W), current_stream()),
               "conv stride-2 dilate");
     hip = true;
+    strided = true;
   }
   auto mask = output_mask;
   const bool dw = hip && mask[1] && g_mode.load() >= 2;
@@ -865,7 +878,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   if (hip && (mask[0] || dw_rows)) gop = pack_rows(go, layout);
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
-    gi = hip_conv_packed(gop, layout, go.sizes(), weight, nullptr, true);
+    gi = hip_conv_packed(gop, layout, go.sizes(), weight, nullptr, true, 0, !strided);
     mask[0] = false;
   }
   if (dw) {

@@ -51,6 +51,10 @@ extern std::atomic<int> g_gconv_mode;
 extern std::atomic<int> g_wgrad_form;
 // Row layout of the 3x3 conv operands: 1 (default) tight strips, 0 the reference's layout.
 extern std::atomic<int> g_conv_layout;
+// 1: the 3x3 / stride-1 forward and input-gradient convs emulate the reference NPU's BFP16
+// arithmetic (XDNA_BFP16_EMULATION=1 or set_bfp16_emulation); 0 (default) bf16 x bf16 with
+// fp32 sums, the reference's CPU path.
+extern std::atomic<int> g_bfp16_emul;
 
 // Write epochs of device allocations (the reference's per-allocation write epoch,
 // torch_xdna_device.cpp:493, 576, 620-633, 2222).  Every xdna write path bumps the epoch

@@ -7,6 +7,7 @@ from .device import (
     allocator_stats,
     async_dw_stats,
     autotune_result,
+    bfp16_emulation,
     bo_handle,
     conv_layout,
     coherency_state,
@@ -22,6 +23,7 @@ from .device import (
     register_xdna_device,
     reset_fallback_stats,
     reset_mapped_cpu_stats,
+    set_bfp16_emulation,
     set_general_conv_mode,
     set_conv_layout,
     set_npu_mode,
@@ -56,6 +58,8 @@ __all__ = [
     "set_wgrad_form",
     "set_conv_layout",
     "conv_layout",
+    "set_bfp16_emulation",
+    "bfp16_emulation",
     "wgrad_form",
     "wait_for_builds",
     "set_wait_timeout_ms",

@@ -357,6 +357,23 @@ def conv_layout() -> int:
 
 
 @_api
+def set_bfp16_emulation(on: bool) -> None:
+    """Emulate the reference NPU's conv arithmetic on the 3x3 / stride-1 forward and
+    input-gradient convs: activations and weights quantized to BFP16 (bfp16ebs8 blocks of
+    8 channels), the running sum stored as bf16 after every 64-channel chunk and tap, the
+    bias added after (benchmarks/bfp16_training_gate.py:1-20 restates it; kernel
+    _designs/conv3x3w_kernel.cc).  Weight gradients stay exact.  Off by default: the
+    default arithmetic is the reference's CPU bf16 path.  XDNA_BFP16_EMULATION=1 sets it
+    at start-up."""
+    native().set_bfp16_emulation(bool(on))
+
+
+@_api
+def bfp16_emulation() -> bool:
+    return bool(native().bfp16_emulation())
+
+
+@_api
 def set_wait_timeout_ms(ms: int) -> None:
     """Deadline of every host wait on the device (default 30000, XDNA_WAIT_TIMEOUT_MS;
     0 = none).  A wait past it raises and poisons the process (xrt_shim.cpp:57-90)."""
