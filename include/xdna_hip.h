@@ -611,6 +611,21 @@ int xdna_upsample_nearest2x_bwd_bf16(const uint16_t* dy, uint16_t* dx, int64_t p
 int xdna_subsample2_bf16(const uint16_t* full, uint16_t* y, int64_t planes, int H, int W, void* stream);
 int xdna_dilate2_bf16(const uint16_t* dy, uint16_t* full, int64_t planes, int H, int W, void* stream);
 
+/* The same conv without the sampling passes (the backend's path for 3x3 / stride-2 /
+ * pad-1 convs; the reference runs them on its CPU, torch_xdna_device.cpp:4524-4606,
+ * 4608-4885):
+ * xdna_conv3x3_layout_rows_stride2_bf16: xdna_conv3x3_layout_rows_bf16 of the input
+ * packed at its full H x W, storing only the outputs at even (y, x), at (y/2, x/2) of a
+ * [B][cout][ceil(H/2)][ceil(W/2)] tensor.
+ * xdna_conv3x3_layout_pack_dilate2_bf16: xdna_conv3x3_layout_pack_bf16 of the H x W
+ * spread of src ([B][C][ceil(H/2)][ceil(W/2)]: src at even (y, x), 0 elsewhere), without
+ * materializing the spread; the input- and weight-gradient convs of the stride-2 conv read
+ * this packed gradient.  W <= 256. */
+int xdna_conv3x3_layout_rows_stride2_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                          int B, int cin, int cout, int H, int W, int layout, void* stream);
+int xdna_conv3x3_layout_pack_dilate2_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
+                                          int layout, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused training regions: the frozen-feature (perceptual) loss of          */
 /* xdna_train/regions.py:1-425 with its host kernels                        */

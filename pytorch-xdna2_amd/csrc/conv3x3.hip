@@ -146,6 +146,10 @@ struct RowsArgs {
   int out_rs;            // 1: stores through a buffer resource (every tile's span < 2^30 bytes)
   int bias_vec;          // 1: bias 8-byte aligned and cout % 4 == 0 (4-channel vector loads)
   int act;               // epilogue activation: 0 none, 1 ReLU
+  // Output image: oH x oW.  osh = 0: the conv's own H x W.  osh = 1: the forward of a
+  // 3x3 / stride-2 / pad-1 conv, ceil(H/2) x ceil(W/2): only grid pixels at even (y, x)
+  // are stored, at (y/2, x/2) (the buffer-store epilogues and the split-K reduce).
+  int osh, oH, oW;
 };
 
 // The epilogue's activation, applied to the fp32 sum before its one rounding.  ReLU keeps
@@ -169,7 +173,7 @@ struct OutMap {
 __device__ inline OutMap out_map(const RowsArgs& a, int64_t p_first) {
   OutMap o;
   o.b0 = int(p_first / a.img / a.S);
-  o.cp = int64_t(a.cout) * a.H * a.W;
+  o.cp = int64_t(a.cout) * a.oH * a.oW;
   const int64_t left = (int64_t(a.B) - o.b0) * o.cp * 2;
   o.rs = __builtin_amdgcn_make_buffer_rsrc(a.out + o.b0 * o.cp, 0, int(left < kOutSkip ? left : kOutSkip - 1),
                                            0x00020000);
@@ -189,7 +193,8 @@ __device__ inline int out_pixel_off(const RowsArgs& a, const OutMap& o, int64_t 
   const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
   if (y >= a.H || col < 0 || col >= cols) return kOutSkip;
   const int x = (a.S == 1 ? 0 : s * a.So) + col;
-  return int(((int64_t(b - o.b0)) * o.cp + int64_t(y) * a.W + x) * 2);
+  if ((y | x) & a.osh) return kOutSkip;  // stride-2 output: odd rows and columns are not outputs
+  return int(((int64_t(b - o.b0)) * o.cp + int64_t(y >> a.osh) * a.oW + (x >> a.osh)) * 2);
 }
 
 constexpr int kXcds = 8;  // MI355X: workgroups go round-robin to 8 XCDs, each with its own L2
@@ -777,7 +782,7 @@ void conv_rows4_kernel(RowsArgs a) {
 
   if (a.out_rs) {
     const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
-    const int plane2 = a.H * a.W * 2;
+    const int plane2 = a.oH * a.oW * 2;
     int poff[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
@@ -1075,7 +1080,7 @@ void conv_rows6_kernel(RowsArgs a) {
   mfma16_fence(acc);
   if (a.out_rs) {
     const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
-    const int plane2 = a.H * a.W * 2;
+    const int plane2 = a.oH * a.oW * 2;
     int poff[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
@@ -1299,7 +1304,7 @@ void conv_small_kernel(RowsArgs a) {
   }
   if (a.out_rs) {
     const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
-    const int plane2 = a.H * a.W * 2;
+    const int plane2 = a.oH * a.oW * 2;
     int poff[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
@@ -1350,8 +1355,10 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(RowsArgs a, int nsplit
   const int plane = plane0 + int(blockIdx.y);
   const int b = plane / a.cout, co = plane - b * a.cout;
   const int pix = int(blockIdx.x) * 256 + int(threadIdx.x);
-  if (pix >= a.H * a.W) return;
-  const int y = pix / a.W, x = pix - y * a.W;
+  if (pix >= a.oH * a.oW) return;
+  // output pixel pix of the oH x oW image; its grid pixel (y, x) (stride-2 output: 2x)
+  const int yo = pix / a.oW, xo = pix - yo * a.oW;
+  const int y = yo << a.osh, x = xo << a.osh;
   const int s = a.S == 1 ? 0 : x / a.So;
   const int col = x - s * a.So + a.first;
   const int64_t p = (int64_t(b) * a.S + s) * a.img + int64_t(y) * a.wp + col;
@@ -1359,7 +1366,7 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(RowsArgs a, int nsplit
   const float* pp = a.part + int64_t(co) * a.m_pad + p;
   const int64_t zstride = int64_t(a.cout) * a.m_pad;
   for (int z = 0; z < nsplit; ++z) v += pp[z * zstride];
-  a.out[int64_t(plane) * a.H * a.W + pix] = f32_to_bf16(rows_act(a, v));
+  a.out[int64_t(plane) * a.oH * a.oW + pix] = f32_to_bf16(rows_act(a, v));
 }
 
 // ---------------------------------------------------------------------------------
@@ -2004,6 +2011,9 @@ RowsArgs rows_args(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
                    int cout, int H, int W, const ConvGeom& geom, int act) {
   RowsArgs a;
   a.act = act;
+  a.osh = 0;
+  a.oH = H;
+  a.oW = W;
   a.xp = xp;
   a.wt = wt;
   a.bias = bias;
@@ -2045,9 +2055,19 @@ bool small_lds_ok() {
 }
 
 int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
-                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef, int act = 0) {
+                int B, int cin, int cout, int H, int W, void* stream, int layout = kLayoutRef, int act = 0,
+                bool s2out = false) {
   const ConvGeom geom = conv_geom(B, H, W, layout);
   RowsArgs a = rows_args(xp, wt, bias, out, B, cin, cout, H, W, geom, act);
+  if (s2out) {
+    a.osh = 1;
+    a.oH = (H + 1) / 2;
+    a.oW = (W + 1) / 2;
+    if (!a.out_rs) {
+      set_error("conv3x3 rows: the stride-2 output needs the buffer-store epilogue (output too large)");
+      return -1;
+    }
+  }
   if (!admit_launch("conv3x3 rows")) return -1;
   hipStream_t st = as_stream(stream);
   // Kernel choice (xdna_conv3x3_set_rows_variant, or XDNA_ROWS_VARIANT at start-up,
@@ -2055,6 +2075,9 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   // main kernel needs a grid of several workgroups per CU to hide its per-tap weight
   // loads; below that the small-grid kernel, which stages whole chunks, is faster.
   int variant = g_rows_variant.load();
+  // the stride-2 output is stored by the buffer-store epilogues only: the main and the
+  // eight-wave kernels (variants 1, 4; 5 up to 128 channels) have none
+  if (s2out && (variant == 1 || variant == 4 || (variant == 5 && cout <= kTCo))) variant = 0;
   const unsigned ytiles = unsigned(ceil_div(cout, kTCo));
   if (variant == 0) {
     // Automatic choice (fitted to the sweep shapes on an MI355X).  Grids of a few hundred
@@ -2168,7 +2191,7 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   else
     conv_small_kernel<64><<<grid, 256, small_lds(64), st>>>(a);
   if (nsplit > 1) {
-    const unsigned pix_blocks = unsigned(ceil_div(int64_t(H) * W, 256));
+    const unsigned pix_blocks = unsigned(ceil_div(int64_t(a.oH) * a.oW, 256));
     const int planes = B * cout;
     for (int p0 = 0; p0 < planes; p0 += 65535)
       rows_reduce_kernel<<<dim3(pix_blocks, unsigned(std::min(65535, planes - p0))), 256, 0, st>>>(a, nsplit, p0);
@@ -3124,6 +3147,16 @@ int xdna_conv3x3_layout_rows_act_bf16(const uint16_t* xp, const uint16_t* wt, co
     return -1;
   }
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout, act);
+}
+
+int xdna_conv3x3_layout_rows_stride2_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                          int B, int cin, int cout, int H, int W, int layout, void* stream) {
+  if (!shape_ok("xdna_conv3x3_layout_rows_stride2_bf16", B, cin, cout, H, W)) return -1;
+  if (layout != kLayoutRef && layout != kLayoutTight) {
+    set_error("xdna_conv3x3_layout_rows_stride2_bf16: unknown layout");
+    return -1;
+  }
+  return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout, 0, /*s2out=*/true);
 }
 
 int xdna_conv3x3_layout_rows_bfp16_emul_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,

@@ -127,7 +127,11 @@ __device__ inline void put_row_piece(uint16_t* __restrict__ dst, int64_t p, int 
 // element of groups [g0, g0 + ng) is written, zeros included (border rows and columns,
 // padded channels, the rows past the last image), so a buffer needs no fill; workgroups
 // from nimg on write the rows past the last image.
-template <int VP, bool kDense>
+// kDil (dense only): the packed image is the H x W spread of src, whose planes are
+// ceil(H/2) x ceil(W/2): pixel (y, x) = src[y/2][x/2] at even y and x, 0 elsewhere (the
+// gradient of a stride-2 conv on the stride-1 grid).  R is even, so a workgroup's full
+// rows [y0, y0 + R) read the source rows [y0/2, y0/2 + R/2) and the LDS tile holds those.
+template <int VP, bool kDense, bool kDil = false>
 __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
     const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int C, int H, int W, int S,
     int So, int Wg, int wp, int lead, int halo_zero, int chunks, int g0, int ng, int b0, int64_t plo,
@@ -155,9 +159,12 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
   if (cc <= 0) return;
   const int y0 = yb * R;
   const int rows = min(R, H - y0);
-  const int npix = rows * W;
-  const int64_t plane = int64_t(H) * W;
-  const uint16_t* sbase = src + (int64_t(b) * C + chunk * kKStep) * plane + int64_t(y0) * W;
+  // source planes: H x W, or ceil(H/2) x ceil(W/2) spread over H x W (kDil)
+  const int Hs = kDil ? (H + 1) >> 1 : H, Ws = kDil ? (W + 1) >> 1 : W;
+  const int ys0 = kDil ? y0 >> 1 : y0;
+  const int npix = (kDil ? min((rows + 1) >> 1, Hs - ys0) : rows) * Ws;
+  const int64_t plane = int64_t(Hs) * Ws;
+  const uint16_t* sbase = src + (int64_t(b) * C + chunk * kKStep) * plane + int64_t(ys0) * Ws;
   // phase 1: NCHW rows [y0, y0 + rows) -> tile[pix][c], pix = yy * W + x.  An item is
   // VP consecutive pixels x 16 channels: 16 loads of VP pixels each (one per channel, all
   // issued before the first LDS write), then VP x two 16-byte LDS writes.
@@ -222,8 +229,14 @@ __global__ __launch_bounds__(256) void pack_rows_lds_kernel(
       const int x = (S == 1 ? 0 : s * So - 1) + j;
       const bool zero_col = halo_zero && S > 1 && (j == 0 || j == Wg - 1);
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (gy >= 1 && gy <= H && j >= 0 && j < Wg && x >= 0 && x < W && !zero_col && q * 8 < cc)
+      const bool real = gy >= 1 && gy <= H && j >= 0 && j < Wg && x >= 0 && x < W && !zero_col && q * 8 < cc;
+      if (kDil) {
+        // image row gy - 1 and column x even: source pixel ((gy - 1) / 2, x / 2)
+        if (real && ((gy - 1) & 1) == 0 && (x & 1) == 0)
+          v = *reinterpret_cast<const uint4*>(tile + tile_piece<kVpShift>((((gy - 1) >> 1) - ys0) * Ws + (x >> 1), q));
+      } else if (real) {
         v = *reinterpret_cast<const uint4*>(tile + tile_piece<kVpShift>((gy - 1 - y0) * W + x, q));
+      }
       const int64_t p = ((int64_t(b) * S + s) * (H + 2) + gy) * wp + gx;
       put_row_piece(dst, p, q, v, chunks, chunk, g0, ng, plo, phi);
     }
@@ -321,7 +334,7 @@ std::atomic<int> g_pack_rows{0};
 
 int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
                 int S, int So, int halo_zero, int chunks, int g0, int ng, void* stream,
-                bool dense = false, int layout = kLayoutRef) {
+                bool dense = false, int layout = kLayoutRef, bool dil = false) {
   if (B < 0 || C < 0 || H < 0 || W < 0 || chunks < 0 || S < 1 || g0 < 0 || ng < 0 ||
       (S > 1 && So < 1)) {
     set_error(std::string(what) + ": invalid geometry");
@@ -338,8 +351,12 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
   const int64_t phi = int64_t(g0 + ng) * kGroupOutRows + (kGroupRows - kGroupOutRows);
   const int64_t v0 = plo / img;
   const int64_t v1 = std::min<int64_t>((phi - 1) / img + 1, Bv);
-  if (dense && (!aligned16(dst) || W > kMaxTilePix)) {
+  if ((dense || dil) && (!aligned16(dst) || W > kMaxTilePix)) {
     set_error(std::string(what) + ": dense packing needs a 16-byte aligned destination and W <= 256");
+    return -1;
+  }
+  if (dil && !dense) {
+    set_error(std::string(what) + ": the spread pack is dense only");
     return -1;
   }
   if (v1 <= v0 && !dense) return 0;
@@ -355,7 +372,8 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
     const int64_t row_tasks = (b1 - b0) * chunks * H;
     const int forced = g_pack_rows.load();
     const int by_width = W >= 64 ? 2 : W >= 32 ? (row_tasks >= 4096 ? 4 : 3) : W >= 16 ? 3 : 2;
-    const int R = std::max(1, std::min({forced > 0 ? forced : by_width, H, kMaxTilePix / W}));
+    int R = std::max(1, std::min({forced > 0 ? forced : by_width, H, kMaxTilePix / W}));
+    if (dil) R = std::max(2, R + (R & 1));  // even: a tile's source rows start at y0 / 2
     const int ybl = int(ceil_div(H, R));
     const int64_t nimg = (b1 - b0) * chunks * ybl;
     // dense: rows [tail0, phi) past the last image get workgroups of their own
@@ -363,22 +381,30 @@ int pack_launch(const char* what, const uint16_t* src, uint16_t* dst, int B, int
     const int64_t ntail = dense && phi > tail0 ? std::min<int64_t>(ceil_div((phi - tail0) * chunks * 8, 256), 1024) : 0;
     const int64_t blocks = nimg + ntail;
     if (blocks == 0) return 0;
-    const size_t lds = size_t(R) * W * kLdsPitch * 2;
+    // the tile: R rows of W pixels, or R / 2 source rows of ceil(W/2) (kDil)
+    const size_t lds = (dil ? size_t(R / 2) * size_t((W + 1) / 2) : size_t(R) * W) * kLdsPitch * 2;
     // pixels per lane load: every channel run (plane offset + y0 * W) must keep the
     // alignment of the load for every tile row start; the last group of a run is cut
     // short by the tile's pixel count only, and runs are padded in LDS to the group size
-    const int64_t plane = int64_t(H) * W;
-    const int64_t step = std::gcd<int64_t>(plane, int64_t(R) * W);  // all run offsets are multiples
+    // (kDil: source planes ceil(H/2) x ceil(W/2), R / 2 source rows per tile)
+    const int64_t Ws = dil ? (W + 1) / 2 : W;
+    const int64_t plane = dil ? int64_t((H + 1) / 2) * Ws : int64_t(H) * W;
+    const int64_t tile_src = dil ? int64_t(R / 2) * Ws : int64_t(R) * W;
+    const int64_t step = std::gcd<int64_t>(plane, tile_src);  // all run offsets are multiples
     const uintptr_t sa = reinterpret_cast<uintptr_t>(src);
-    const int VP = (sa % 8 == 0 && step % 4 == 0 && (R * W) % 4 == 0) ? 4
-                   : (sa % 4 == 0 && step % 2 == 0 && (R * W) % 2 == 0) ? 2 : 1;
+    const int VP = (sa % 8 == 0 && step % 4 == 0 && tile_src % 4 == 0) ? 4
+                   : (sa % 4 == 0 && step % 2 == 0 && tile_src % 2 == 0) ? 2 : 1;
     const dim3 grid{unsigned(blocks)};
     hipStream_t st = as_stream(stream);
-#define XDNA_PACK_LAUNCH(vp, dn)                                                                  \
-  pack_rows_lds_kernel<vp, dn><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, lead, halo_zero, \
-                                                      chunks, g0, ng, int(b0), plo, phi, R, ybl,   \
+#define XDNA_PACK_LAUNCH(vp, dn, ...)                                                             \
+  pack_rows_lds_kernel<vp, dn, ##__VA_ARGS__><<<grid, 256, lds, st>>>(src, dst, C, H, W, S, So, Wg, wp, lead,  \
+                                                      halo_zero, chunks, g0, ng, int(b0), plo, phi, R, ybl,   \
                                                       int(nimg), tail0)
-    if (dense) {
+    if (dil) {
+      if (VP == 4) XDNA_PACK_LAUNCH(4, true, true);
+      else if (VP == 2) XDNA_PACK_LAUNCH(2, true, true);
+      else XDNA_PACK_LAUNCH(1, true, true);
+    } else if (dense) {
       if (VP == 4) XDNA_PACK_LAUNCH(4, true);
       else if (VP == 2) XDNA_PACK_LAUNCH(2, true);
       else XDNA_PACK_LAUNCH(1, true);
@@ -475,6 +501,21 @@ size_t xdna_conv3x3_layout_packed_bytes(int B, int C, int H, int W, int layout) 
   if (B < 1 || C < 1 || H < 1 || W < 1 || (layout != kLayoutRef && layout != kLayoutTight)) return 0;
   const ConvGeom cg = conv_geom(B, H, W, layout);
   return size_t(cg.groups) * size_t(ceil_div(C, kKStep)) * kGroupRows * kKStep * 2;
+}
+
+int xdna_conv3x3_layout_pack_dilate2_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
+                                          int layout, void* stream) {
+  if (B < 1 || C < 1 || H < 1 || W < 1 || (layout != kLayoutRef && layout != kLayoutTight) || !src || !dst) {
+    set_error("xdna_conv3x3_layout_pack_dilate2_bf16: invalid arguments");
+    return -1;
+  }
+  if (!aligned16(dst) || W > kMaxTilePix) {
+    set_error("xdna_conv3x3_layout_pack_dilate2_bf16: needs a 16-byte aligned destination and W <= 256");
+    return -1;
+  }
+  const ConvGeom cg = conv_geom(B, H, W, layout);
+  return pack_launch("xdna_conv3x3_layout_pack_dilate2_bf16", src, dst, B, C, H, W, cg.st.S, cg.st.So, 0,
+                     int(ceil_div(C, kKStep)), 0, cg.groups, stream, /*dense=*/true, layout, /*dil=*/true);
 }
 
 int xdna_conv3x3_layout_pack_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W, int layout,

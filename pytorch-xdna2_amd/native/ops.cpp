@@ -321,8 +321,10 @@ at::Tensor pack_rows(const at::Tensor& src, int layout) {
 // given; dgrad: flip+swap) into a new NCHW tensor of cout channels.
 // s1: a stride-1 conv of the model (not the stride-1 form of a stride-2 conv), which the
 // BFP16 emulation covers: the reference's NPU takes only stride-1 convs.
+// s2out: the forward of a 3x3 / stride-2 / pad-1 conv, storing only the even outputs of
+// the stride-1 conv into a ceil(H/2) x ceil(W/2) tensor.
 at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef src, const at::Tensor& w,
-                           const at::Tensor* bias, bool dgrad, int act = 0, bool s1 = true) {
+                           const at::Tensor* bias, bool dgrad, int act = 0, bool s1 = true, bool s2out = false) {
   const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor wc = w.contiguous();
@@ -367,10 +369,20 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
       if (cacheable) remember_weights(w, dgrad, wt, tag);
     }
   }
-  at::Tensor out = empty_xdna({B, cout, H, W}, at::kBFloat16);
+  at::Tensor out = s2out ? empty_xdna({B, cout, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16)
+                         : empty_xdna({B, cout, H, W}, at::kBFloat16);
   at::Tensor bc;
   if (bias) bc = bias->contiguous();
   const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
+  if (s2out) {
+    KernelTimer kt("conv3x3_rows.s2", flops);
+    check_abi(xdna_conv3x3_layout_rows_stride2_bf16(
+                  static_cast<const uint16_t*>(packed.const_data_ptr()), static_cast<const uint16_t*>(wt.const_data_ptr()),
+                  bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                  static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout), int(H), int(W), layout, st),
+              "conv rows (stride-2 output)");
+    return out;
+  }
   if (s1 && g_bfp16_emul.load()) {
     ScopedCount sc(dgrad ? "hip_conv3x3.bfp16_emul.dx.run" : "hip_conv3x3.bfp16_emul.fwd.run");
     check_abi(xdna_conv3x3_layout_rows_bfp16_emul_bf16(
@@ -547,13 +559,38 @@ std::atomic<int64_t> g_dw_jobs{0};
 // and its gradient takes the rows form (whether or not autograd records this call: a
 // caller may run the aten backward itself).  A kept pack whose backward never comes goes
 // when its input dies.  Inference tensors keep nothing (they have no version counter).
-at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias, bool s1 = true) {
+at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias, bool s1 = true,
+                        bool s2out = false) {
   const int layout = g_conv_layout.load();
   at::Tensor packed = pack_rows(input, layout);
   if (g_mode.load() >= 2 && weight.requires_grad() && !weight.is_inference() && !input.is_inference() &&
       wgrad_rows_pick(input.size(1), weight.size(0), input.size(3)))
     remember_packed_input(input, packed, layout);
-  return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false, 0, s1);
+  return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false, 0, s1, s2out);
+}
+
+// The spread-and-pack of a stride-2 conv's output gradient: the packed rows of its H x W
+// spread (gradient at even (y, x), zeros elsewhere), in one pass.
+at::Tensor pack_rows_spread(const at::Tensor& grad_output, int64_t H, int64_t W, int layout) {
+  const at::Tensor d = grad_output.contiguous();
+  const int64_t B = d.size(0), C = d.size(1);
+  if (W > 256) {
+    // rows wider than the pack's LDS tile: the spread tensor, then the ordinary pack
+    at::Tensor full = empty_xdna({B, C, H, W}, at::kBFloat16);
+    check_abi(xdna_dilate2_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                static_cast<uint16_t*>(full.data_ptr()), B * C, int(H), int(W), current_stream()),
+              "conv stride-2 dilate");
+    return pack_rows(full, layout);
+  }
+  const size_t pbytes = xdna_conv3x3_layout_packed_bytes(int(B), int(C), int(H), int(W), layout);
+  TORCH_CHECK(pbytes > 0, "xdna conv: invalid packed layout");
+  at::Tensor packed = alloc_bytes(pbytes);
+  KernelTimer kt("conv3x3w_pack", 2.0 * double(d.numel()) + double(pbytes));
+  check_abi(xdna_conv3x3_layout_pack_dilate2_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                                  static_cast<uint16_t*>(packed.data_ptr()), int(B), int(C), int(H),
+                                                  int(W), layout, current_stream()),
+            "conv spread pack");
+  return packed;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -749,13 +786,7 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv3x3_s2.fwd.run");
-    const at::Tensor full = hip_conv_fwd(input, weight, has_bias ? &*bias : nullptr, /*s1=*/false);
-    const int64_t B = full.size(0), C = full.size(1), H = full.size(2), W = full.size(3);
-    at::Tensor y = empty_xdna({B, C, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16);
-    check_abi(xdna_subsample2_bf16(static_cast<const uint16_t*>(full.const_data_ptr()),
-                                   static_cast<uint16_t*>(y.data_ptr()), B * C, int(H), int(W), current_stream()),
-              "conv stride-2 subsample");
-    return y;
+    return hip_conv_fwd(input, weight, has_bias ? &*bias : nullptr, /*s1=*/false, /*s2out=*/true);
   }
   if (conv1x1_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
@@ -855,17 +886,16 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   bool hip = conv_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
              go_ok && grad_output.size(2) == input.size(2) && grad_output.size(3) == input.size(3);
   // stride 2: the stride-1 gradients of the gradient spread onto the stride-1 grid
+  // stride 2: the stride-1 gradients of the gradient spread onto the stride-1 grid (its
+  // packed rows made in one pass; the spread tensor itself only for the channel-major
+  // weight gradient)
   at::Tensor go = grad_output;
   bool strided = false;
+  std::vector<int64_t> go_sizes = grad_output.sizes().vec();
   if (!hip && go_ok && conv_s2_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
       grad_output.size(2) == (input.size(2) + 1) / 2 && grad_output.size(3) == (input.size(3) + 1) / 2) {
     ScopedCount sc("hip_conv3x3_s2.bwd.run");
-    const at::Tensor d = grad_output.contiguous();
-    const int64_t B = input.size(0), C = weight.size(0), H = input.size(2), W = input.size(3);
-    go = empty_xdna({B, C, H, W}, at::kBFloat16);
-    check_abi(xdna_dilate2_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
-                                static_cast<uint16_t*>(go.data_ptr()), B * C, int(H), int(W), current_stream()),
-              "conv stride-2 dilate");
+    go_sizes = {input.size(0), weight.size(0), input.size(2), input.size(3)};
     hip = true;
     strided = true;
   }
@@ -875,11 +905,21 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   // dY packed once: the input gradient's conv and the rows weight gradient read it
   const int layout = g_conv_layout.load();
   at::Tensor gop;
-  if (hip && (mask[0] || dw_rows)) gop = pack_rows(go, layout);
+  if (hip && (mask[0] || dw_rows))
+    gop = strided ? pack_rows_spread(grad_output, go_sizes[2], go_sizes[3], layout) : pack_rows(go, layout);
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
-    gi = hip_conv_packed(gop, layout, go.sizes(), weight, nullptr, true, 0, !strided);
+    gi = hip_conv_packed(gop, layout, go_sizes, weight, nullptr, true, 0, !strided);
     mask[0] = false;
+  }
+  if (strided && dw && !dw_rows) {
+    // the channel-major weight gradient reads the spread gradient as a tensor
+    const at::Tensor d = grad_output.contiguous();
+    go = empty_xdna(go_sizes, at::kBFloat16);
+    check_abi(xdna_dilate2_bf16(static_cast<const uint16_t*>(d.const_data_ptr()),
+                                static_cast<uint16_t*>(go.data_ptr()), go_sizes[0] * go_sizes[1], int(go_sizes[2]),
+                                int(go_sizes[3]), current_stream()),
+              "conv stride-2 dilate");
   }
   if (dw) {
     ScopedCount sc("hip_conv3x3.dw.run");

@@ -74,6 +74,8 @@ SIGNATURES = {
     "xdna_conv3x3w_weights_bfp16_bytes": (Z, [I]),
     "xdna_bfp16_decode_f32": (I, [P, P, L, P]),
     "xdna_bfp16_quantize8_bf16": (I, [P, P, L, P]),
+    "xdna_conv3x3_layout_rows_stride2_bf16": (I, [P, P, P, P, I, I, I, I, I, I, P]),
+    "xdna_conv3x3_layout_pack_dilate2_bf16": (I, [P, P, I, I, I, I, I, P]),
     "xdna_conv3x3_layout_rows_bfp16_emul_bf16": (I, [P, P, P, P, I, I, I, I, I, I, I, P]),
     "xdna_conv2d_fwd_bf16": (I, [P, P, P, P] + [I] * 11 + [P]),
     "xdna_instance_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, ctypes.c_double, P]),
