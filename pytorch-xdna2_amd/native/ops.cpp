@@ -631,6 +631,16 @@ struct GeomArgs {
 // Strided layers, other input gradients, and the weight gradient of few-output layers
 // stay on MIOpen unless mode 2 asks otherwise.
 bool gconv_auto(int cout, int sh, int sw) { return cout >= 32 && sh == 1 && sw == 1; }
+// 3x3 / stride-1 convs with at most 4 input channels (RGB input layers): the rows path
+// pads the input to a 64-channel chunk (16-21x the MACs), so their forward and weight
+// gradient take the general kernels (measured on MI355X: ResNet-18's stem B128 3->64 at
+// 64x64 forward 80.6 -> 31.0 us, weight gradient 209 -> 133 us; VGG's first layer B40 at
+// 36x36 forward 19.2 -> 8.5 us); their input gradient (64 input channels of the gradient
+// conv) stays on the rows path, which is faster there.
+bool few_input_3x3(const at::Tensor& x, const at::Tensor& w) {
+  const int m = g_gconv_mode.load();
+  return x.size(1) <= 4 && (m == 2 || (m == 1 && gconv_auto(int(w.size(0)), 1, 1)));
+}
 bool gconv_auto_fwd(int cin, int cout, int sh, int sw) {
   return gconv_auto(cout, sh, sw) || (cout <= 32 && cin >= 16 && sh == 1 && sw == 1);
 }
@@ -776,7 +786,7 @@ at::Tensor convolution_overrideable_xdna(const at::Tensor& input, const at::Tens
                                          c10::SymIntArrayRef output_padding, c10::SymInt groups) {
   const bool has_bias = bias && bias->defined();
   if (conv_eligible(input, weight, stride, padding, dilation, transposed, output_padding, groups) &&
-      input.size(1) == weight.size(1) &&
+      input.size(1) == weight.size(1) && !few_input_3x3(input, weight) &&
       (!has_bias || (bias->scalar_type() == at::kBFloat16 && bias->dim() == 1 &&
                      bias->size(0) == weight.size(0) && bias->device().type() == kXdna))) {
     ScopedCount sc("hip_conv3x3.fwd.run");
@@ -900,7 +910,9 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     strided = true;
   }
   auto mask = output_mask;
-  const bool dw = hip && mask[1] && g_mode.load() >= 2;
+  // few input channels: the input gradient here, the weight gradient on the general kernels
+  const bool few_in = hip && !strided && few_input_3x3(input, weight);
+  const bool dw = hip && mask[1] && g_mode.load() >= 2 && !few_in;
   const bool dw_rows = dw && wgrad_rows_pick(input.size(1), weight.size(0), input.size(3));
   // dY packed once: the input gradient's conv and the rows weight gradient read it
   const int layout = g_conv_layout.load();
@@ -957,7 +969,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
       if (m1[i]) mask[i] = false;
   }
   const int gmode = g_gconv_mode.load();
-  const bool ghip = !hip && gmode > 0 &&
+  const bool ghip = (!hip || few_in) && gmode > 0 &&
                     gconv_eligible(input, weight, stride, padding, dilation, transposed,
                                    output_padding, groups) &&
                     grad_output.scalar_type() == at::kBFloat16 && grad_output.dim() == 4 &&

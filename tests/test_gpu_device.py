@@ -239,9 +239,10 @@ def _routed_conv(cin, cout, k, s, pd, B=2, H=12, W=10, seed=0):
 def test_default_routing_of_general_convs(xdna):
     """Mode 2 (default) runs every eligible conv direction on the HIP kernels, the style
     network's 9x9 32->3 gradients included (the few-output weight-gradient kernel and the
-    gather input gradient); 3x3 / stride-2 layers take the stride-1 3x3 path.  Mode 1 keeps
-    the gradients of few-output layers on MIOpen.  Every result matches the float64
-    oracle."""
+    gather input gradient); 3x3 / stride-2 layers take the stride-1 3x3 path; 3x3 layers
+    with at most 4 input channels take the general forward and weight gradient and the
+    3x3 input gradient, with 8 inputs the 3x3 path throughout.  Mode 1 keeps the gradients
+    of few-output layers on MIOpen.  Every result matches the float64 oracle."""
     assert xdna.general_conv_mode() == 2
     hip_all = {"hip_conv2d.fwd.run": 1, "hip_conv2d.dw.run": 1, "hip_conv2d.dx.run": 1,
                "aten::convolution.rocm": 0, "aten::convolution_backward.rocm": 0}
@@ -250,6 +251,13 @@ def test_default_routing_of_general_convs(xdna):
         (3, 32, 9, 1, 4, 2, hip_all),
         (32, 64, 3, 2, 1, 2, {"hip_conv3x3_s2.fwd.run": 1, "hip_conv3x3_s2.bwd.run": 1,
                               "aten::convolution.rocm": 0, "aten::convolution_backward.rocm": 0}),
+        (3, 64, 3, 1, 1, 2, {"hip_conv2d.fwd.run": 1, "hip_conv3x3.dx.run": 1, "hip_conv2d.dw.run": 1,
+                             "hip_conv3x3.fwd.run": 0, "hip_conv3x3.dw.run": 0, "aten::convolution.rocm": 0,
+                             "aten::convolution_backward.rocm": 0}),
+        (4, 32, 3, 1, 1, 1, {"hip_conv2d.fwd.run": 1, "hip_conv3x3.dx.run": 1, "hip_conv2d.dw.run": 1,
+                             "aten::convolution_backward.rocm": 0}),
+        (8, 64, 3, 1, 1, 2, {"hip_conv3x3.fwd.run": 1, "hip_conv3x3.dx.run": 1, "hip_conv3x3.dw.run": 1,
+                             "hip_conv2d.fwd.run": 0, "hip_conv2d.dw.run": 0}),
         (32, 3, 9, 1, 4, 1, {"hip_conv2d.fwd.run": 1, "aten::convolution_backward.rocm": 1}),
     ]
     try:
