@@ -460,6 +460,10 @@ int xdna_conv3x3_set_pack_rows(int rows);
  * size, else 8 or 32.  For measurements; no reference counterpart. */
 int xdna_conv3x3_set_prep_tile(int co);
 
+/* Split-K count of the rows weight gradient: 0 (default) its cost model, else this many
+ * (at most one per 64-row k-tile).  For measurements; no reference counterpart. */
+int xdna_conv3x3_set_wgrad_splits(int splits);
+
 /* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments, kernels and results, bit for bit; it calls no

@@ -2820,6 +2820,10 @@ struct WgRowsPlan {
   size_t part_bytes = 0, bpart_bytes = 0, lds_bytes = 0;
 };
 
+// split count of the rows weight gradient: 0 (default) the model below, else forced
+// (xdna_conv3x3_set_wgrad_splits, for measurements)
+std::atomic<int> g_wgrad_splits{0};
+
 WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   WgRowsPlan p;
   p.geom = conv_geom(B, H, W, layout);
@@ -2849,6 +2853,7 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
       best = s;
     }
   }
+  if (g_wgrad_splits.load() > 0) best = std::min<int64_t>(g_wgrad_splits.load(), p.ktiles);
   p.kt_per = int(ceil_div(p.ktiles, best));
   p.splits = int(ceil_div(p.ktiles, p.kt_per));
   p.part_bytes = align256(size_t(p.splits) * out_elems * 4);
@@ -3198,6 +3203,15 @@ int xdna_conv3x3_set_rows_variant(int variant) {
     return -1;
   }
   g_rows_variant.store(variant);
+  return 0;
+}
+
+int xdna_conv3x3_set_wgrad_splits(int splits) {
+  if (splits < 0) {
+    set_error("xdna_conv3x3_set_wgrad_splits: 0 (the model) or a positive split count");
+    return -1;
+  }
+  g_wgrad_splits.store(splits);
   return 0;
 }
 
