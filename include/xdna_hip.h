@@ -460,6 +460,15 @@ int xdna_conv3x3_set_pack_rows(int rows);
  * size, else 8 or 32.  For measurements; no reference counterpart. */
 int xdna_conv3x3_set_prep_tile(int co);
 
+/* Both prepared forms of n weights in one launch (w[i] OIHW bf16 [cout[i]][cin[i]][3][3];
+ * wt[i] / wtd[i] the forward / input-gradient forms as xdna_conv3x3_prepare_weights_both_bf16
+ * writes them, either may be NULL).  The backend's fused optimizer step calls it for the
+ * conv weights it has just written, so the next forward finds their forms prepared.  No
+ * reference counterpart (the reference re-encodes each weight at its next forward,
+ * torch_xdna_device.cpp:2208-2271). */
+int xdna_conv3x3_prepare_weights_multi_bf16(int n, const uint16_t* const* w, uint16_t* const* wt,
+                                            uint16_t* const* wtd, const int* cout, const int* cin, void* stream);
+
 /* Split-K count of the rows weight gradient: 0 (default) its cost model, else this many
  * (at most one per 64-row k-tile).  For measurements; no reference counterpart. */
 int xdna_conv3x3_set_wgrad_splits(int splits);

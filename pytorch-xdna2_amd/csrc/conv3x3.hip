@@ -61,13 +61,12 @@ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 // index divisions and 18-byte-strided gathers: up to 17 us for a 512-channel weight.)
 constexpr int kPrepCi = 64, kPrepRow = kPrepCi * 9;  // 576 elements per block row
 
+// one block (input channels [ci0, ci0 + 64), output channels [co0, co0 + CO)) of both forms
 template <int CO>
-__global__ __launch_bounds__(CO * 8) void prep_tiled_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
-                                                            uint16_t* __restrict__ wtd, int Cout, int Cin, int co_pad_f,
-                                                            int chunks_f, int co_pad_d, int chunks_d, int vec) {
+__device__ inline void prep_block(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                  uint16_t* __restrict__ wtd, int Cout, int Cin, int co_pad_f, int chunks_f,
+                                  int co_pad_d, int chunks_d, int vec, int ci0, int co0, uint16_t* tile) {
   constexpr int NT = CO * 8;  // threads
-  __shared__ __attribute__((aligned(16))) uint16_t tile[CO * kPrepRow];  // [co_l][ci_l * 9 + tap]
-  const int ci0 = blockIdx.x * kPrepCi, co0 = blockIdx.y * CO;
   const int tid = threadIdx.x;
   const bool full = vec && ci0 + kPrepCi <= Cin && co0 + CO <= Cout;
   if (full) {
@@ -126,6 +125,42 @@ __global__ __launch_bounds__(CO * 8) void prep_tiled_kernel(const uint16_t* __re
       *reinterpret_cast<uint4*>(dst) = make_uint4(u[0], u[1], u[2], u[3]);
     }
   }
+}
+
+template <int CO>
+__global__ __launch_bounds__(CO * 8) void prep_tiled_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                            uint16_t* __restrict__ wtd, int Cout, int Cin, int co_pad_f,
+                                                            int chunks_f, int co_pad_d, int chunks_d, int vec) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[CO * kPrepRow];  // [co_l][ci_l * 9 + tap]
+  prep_block<CO>(w, wt, wtd, Cout, Cin, co_pad_f, chunks_f, co_pad_d, chunks_d, vec, blockIdx.x * kPrepCi,
+                 blockIdx.y * CO, tile);
+}
+
+// Several weights' forms in one launch (the optimizer step's refresh of every conv weight
+// it wrote): job e owns blocks [block0, next job's block0), gx input-channel blocks per
+// row of 8-output-channel blocks, as prep_tiled_kernel<8>'s grid.
+constexpr int kPrepJobs = 32;
+struct PrepJob {
+  const uint16_t* w;
+  uint16_t* wt;
+  uint16_t* wtd;
+  int Cout, Cin, co_pad_f, chunks_f, co_pad_d, chunks_d, gx, vec, block0;
+};
+struct PrepJobs {
+  PrepJob j[kPrepJobs];
+  int n;
+};
+
+__global__ __launch_bounds__(64) void prep_multi_kernel(PrepJobs jobs) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[8 * kPrepRow];
+  const int bid = blockIdx.x;
+  int e = 0;
+  while (e + 1 < jobs.n && bid >= jobs.j[e + 1].block0) ++e;
+  const PrepJob& J = jobs.j[e];
+  const int lb = bid - J.block0;
+  const int cy = lb / J.gx, cx = lb - cy * J.gx;
+  prep_block<8>(J.w, J.wt, J.wtd, J.Cout, J.Cin, J.co_pad_f, J.chunks_f, J.co_pad_d, J.chunks_d, J.vec, cx * kPrepCi,
+                cy * 8, tile);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1959,6 +1994,32 @@ int launch_prep_tiled(const uint16_t* w, uint16_t* wt, uint16_t* wtd, int Cout, 
   return check_launch("conv3x3 weight preparation");
 }
 
+// prep_multi_kernel over n weights, in launches of up to kPrepJobs
+int launch_prep_multi(int n, const uint16_t* const* w, uint16_t* const* wt, uint16_t* const* wtd, const int* cout,
+                      const int* cin, void* stream) {
+  for (int first = 0; first < n; first += kPrepJobs) {
+    PrepJobs jobs{};
+    jobs.n = std::min(kPrepJobs, n - first);
+    int blocks = 0;
+    for (int e = 0; e < jobs.n; ++e) {
+      const int i = first + e;
+      const FwdPlan pf = fwd_plan(1, cin[i], cout[i], 1, 1), pd = fwd_plan(1, cout[i], cin[i], 1, 1);
+      const int ci_ext = std::max(wt[i] ? pf.chunks * kKStep : 0, wtd[i] ? pd.co_pad : 0);
+      const int co_ext = std::max(wt[i] ? pf.co_pad : 0, wtd[i] ? pd.chunks * kKStep : 0);
+      PrepJob& J = jobs.j[e];
+      J = PrepJob{w[i], wt[i], wtd[i], cout[i], cin[i], pf.co_pad, pf.chunks, pd.co_pad, pd.chunks,
+                  int(ceil_div(ci_ext, kPrepCi)),
+                  (cin[i] % 8 == 0 && (reinterpret_cast<uintptr_t>(w[i]) & 15) == 0) ? 1 : 0, blocks};
+      blocks += J.gx * int(ceil_div(co_ext, 8));
+    }
+    if (blocks == 0) continue;
+    if (!admit_launch("conv3x3 weight preparation (several weights)")) return -1;
+    prep_multi_kernel<<<unsigned(blocks), 64, 0, as_stream(stream)>>>(jobs);
+    if (check_launch("conv3x3 weight preparation (several weights)")) return -1;
+  }
+  return 0;
+}
+
 int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, int chunks,
                 int dgrad, void* stream) {
   (void)co_pad;
@@ -3204,6 +3265,20 @@ int xdna_conv3x3_set_rows_variant(int variant) {
   }
   g_rows_variant.store(variant);
   return 0;
+}
+
+int xdna_conv3x3_prepare_weights_multi_bf16(int n, const uint16_t* const* w, uint16_t* const* wt,
+                                            uint16_t* const* wtd, const int* cout, const int* cin, void* stream) {
+  if (n < 0 || (n > 0 && (!w || !wt || !wtd || !cout || !cin))) {
+    set_error("xdna_conv3x3_prepare_weights_multi_bf16: invalid arguments");
+    return -1;
+  }
+  for (int i = 0; i < n; ++i)
+    if (!w[i] || cout[i] < 1 || cin[i] < 1 || cout[i] > (1 << 20) || cin[i] > (1 << 20)) {
+      set_error("xdna_conv3x3_prepare_weights_multi_bf16: invalid weight " + std::to_string(i));
+      return -1;
+    }
+  return launch_prep_multi(n, w, wt, wtd, cout, cin, stream);
 }
 
 int xdna_conv3x3_set_wgrad_splits(int splits) {

@@ -235,6 +235,11 @@ bool same_weight(const PreparedWeights& e, const at::Tensor& w, bool dgrad, int6
          e.sizes == sizes4(w) && e.strides == strides4(w);
 }
 
+// The version of an entry that the optimizer step refreshed (refresh_conv_forms): its
+// epoch, which every xdna write advances, and its generation decide; the version counter
+// moves after the step returns.
+constexpr int64_t kAnyVersion = -1;
+
 at::Tensor cached_weights(const at::Tensor& w, bool dgrad, int64_t tag) {
   const uint64_t epoch = write_epoch(w);
   WeightCache& c = weight_cache();
@@ -242,7 +247,9 @@ at::Tensor cached_weights(const at::Tensor& w, bool dgrad, int64_t tag) {
   const int64_t ver = int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
   const uint64_t gen = g_replay_generation.load();
   for (auto& e : c.entries) {
-    if (!same_weight(e, w, dgrad, tag) || e.version != ver || e.epoch != epoch || e.generation != gen) continue;
+    if (!same_weight(e, w, dgrad, tag) || (e.version != ver && e.version != kAnyVersion) || e.epoch != epoch ||
+        e.generation != gen)
+      continue;
     auto live = e.storage.lock();
     if (!live || live.get() != w.storage().unsafeGetStorageImpl()) continue;
     e.last_use = ++c.tick;
@@ -294,6 +301,69 @@ void remember_weights(const at::Tensor& w, bool dgrad, const at::Tensor& wt, int
   e.last_use = ++c.tick;
   c.bytes += size_t(wt.nbytes());
   c.entries.push_back(std::move(e));
+}
+
+// After a fused optimizer step outside graph capture: the conv weights it has just written
+// that have eager prepared forms get them made again, all in one launch, into the same
+// buffers (stream-ordered after every earlier read of them), and their entries take the
+// new epoch; the next forward and input gradient find them instead of preparing each
+// weight in a launch of its own.  XDNA_ADAM_PREP=0 turns it off.  Captured steps keep
+// preparing in the graph (a replay writes the weights with no host code).
+std::atomic<int> g_adam_prep{[] {
+  const char* e = std::getenv("XDNA_ADAM_PREP");
+  return e && std::atoi(e) == 0 ? 0 : 1;
+}()};
+
+void refresh_conv_forms(at::TensorList params) {
+  if (!g_adam_prep.load() || capture_tag() != 0) return;
+  WeightCache& c = weight_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  const uint64_t gen = g_replay_generation.load();
+  std::vector<const uint16_t*> w;
+  std::vector<uint16_t*> wt, wtd;
+  std::vector<int> co, ci;
+  std::vector<std::array<PreparedWeights*, 2>> ent;
+  std::vector<uint64_t> epochs;
+  for (const auto& p : params) {
+    if (!p.defined() || p.scalar_type() != at::kBFloat16 || p.dim() != 4 || p.size(2) != 3 || p.size(3) != 3 ||
+        !p.is_contiguous())
+      continue;
+    std::array<PreparedWeights*, 2> fd{nullptr, nullptr};
+    for (auto& e : c.entries) {
+      if (!same_weight(e, p, e.dgrad, 0)) continue;  // eager entries of this tensor, either direction
+      auto live = e.storage.lock();
+      if (!live || live.get() != p.storage().unsafeGetStorageImpl()) continue;
+      fd[e.dgrad ? 1 : 0] = &e;
+    }
+    if (!fd[0] && !fd[1]) continue;
+    w.push_back(static_cast<const uint16_t*>(p.const_data_ptr()));
+    wt.push_back(fd[0] ? static_cast<uint16_t*>(fd[0]->wt.data_ptr()) : nullptr);
+    wtd.push_back(fd[1] ? static_cast<uint16_t*>(fd[1]->wt.data_ptr()) : nullptr);
+    co.push_back(int(p.size(0)));
+    ci.push_back(int(p.size(1)));
+    ent.push_back(fd);
+    epochs.push_back(write_epoch(p));
+  }
+  if (w.empty()) return;
+  double bytes = 0.0;
+  for (size_t i = 0; i < w.size(); ++i)
+    bytes += double(co[i]) * ci[i] * 9.0 * 2.0 * (1.0 + (wt[i] ? 1.0 : 0.0) + (wtd[i] ? 1.0 : 0.0));
+  {
+    KernelTimer kt("conv3x3_prep", bytes);
+    check_abi(xdna_conv3x3_prepare_weights_multi_bf16(int(w.size()), w.data(), wt.data(), wtd.data(), co.data(),
+                                                      ci.data(), current_stream()),
+              "conv weights (optimizer step)");
+  }
+  for (size_t i = 0; i < ent.size(); ++i) {
+    for (PreparedWeights* e : ent[i]) {
+      if (!e) continue;
+      e->version = kAnyVersion;
+      e->epoch = epochs[i];
+      e->generation = gen;
+      e->last_use = ++c.tick;
+    }
+    count_call("hip_conv3x3.weights_refresh", 0);
+  }
 }
 
 // The packed row layout of an NCHW bf16 tensor ([groups][chunks][2126 rows][64 channels],
@@ -1307,6 +1377,7 @@ void fused_adam_common(at::TensorList p, at::TensorList g, at::TensorList m, at:
                                 beta2, wd, eps, amsgrad ? 1 : 0, maximize ? 1 : 0, adamw ? 1 : 0, gsp, fip,
                                 current_stream()),
                 "fused adam");
+    refresh_conv_forms(p);
     return;
   }
   ScopedCount sc("aten::_fused_adam_.rocm");

@@ -121,7 +121,10 @@ def test_frozen_weight_prepared_once_then_hit():
 
 def test_trainable_weight_prepared_once_per_optimizer_step():
     """Trainable weights are prepared once (both forms, one launch) until a write: steps
-    without an optimizer update hit the cache, the update's epoch bump forces a new form."""
+    without an optimizer update hit the cache.  A fused optimizer step makes both forms
+    again itself (one launch for all the conv weights it wrote) and the next forward and
+    input gradient find them; with that refresh off (XDNA_ADAM_PREP=0) the update's epoch
+    bump makes the next forward prepare them."""
     torch.manual_seed(0)
     x, dy = _data()
     conv = nn.Conv2d(64, 64, 3, padding=1, bias=False).bfloat16().to(X)
@@ -133,11 +136,24 @@ def test_trainable_weight_prepared_once_per_optimizer_step():
     st = {k: v["calls"] for k, v in xdna_train.mapped_cpu_stats().items()}
     # x needs no gradient: one forward lookup per step (one preparation, then hits)
     assert _counts() == (1, 2), st
+    xdna_train.reset_mapped_cpu_stats()
+    opt.step()
+    st = {k: v["calls"] for k, v in xdna_train.mapped_cpu_stats().items()}
+    assert st.get("hip_conv3x3.weights_refresh", 0) == 1, st
+    # a write outside the optimizer after the refresh: the next forward prepares again
+    with torch.no_grad():
+        conv.weight.data.mul_(0.5)
+    xdna_train.reset_mapped_cpu_stats()
+    got = _fwd_dx(conv, x, dy)
+    assert _counts() == (1, 1), xdna_train.mapped_cpu_stats()
+    assert _same(got, _uncached(conv, x, dy))
+    # the refreshed forms serve the next forward and input gradient
+    conv(x).backward(dy)
     opt.step()
     xdna_train.reset_mapped_cpu_stats()
     got = _fwd_dx(conv, x, dy)
     st = {k: v["calls"] for k, v in xdna_train.mapped_cpu_stats().items()}
-    assert _counts() == (1, 1), st
+    assert _counts() == (0, 2), st
     assert _same(got, _uncached(conv, x, dy))
 
 
