@@ -639,6 +639,20 @@ int xdna_conv3x3_layout_rows_stride2_bf16(const uint16_t* xp, const uint16_t* wt
 int xdna_conv3x3_layout_pack_dilate2_bf16(const uint16_t* src, uint16_t* dst, int B, int C, int H, int W,
                                           int layout, void* stream);
 
+/* The pack and the conv in one launch for small grids (the reference's pack_input,
+ * conv_pack.cpp:632-700, followed by its conv run, torch_xdna_device.cpp:2317-2483, which
+ * this pair replaces where no packed copy of the input is needed afterwards):
+ * xdna_conv3x3_nchw_act_bf16 is xdna_conv3x3_layout_rows_act_bf16 (s2out = 0) or
+ * xdna_conv3x3_layout_rows_stride2_bf16 (s2out = 1, act 0) of the input packed, with the
+ * window gathered from the NCHW input x [B][cin][H][W] by the small-grid kernel itself:
+ * the same bits as the packed path.  Only where xdna_conv3x3_nchw_small_eligible is 1
+ * (W <= 36, cin % 8 == 0, input under 2 GiB, and a grid the small-grid kernel takes);
+ * otherwise -1 with an error.  wt is the prepared form of either direction (input gradient:
+ * x is dY and cin its channels). */
+int xdna_conv3x3_nchw_small_eligible(int B, int cin, int cout, int H, int W);
+int xdna_conv3x3_nchw_act_bf16(const uint16_t* x, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int B,
+                               int cin, int cout, int H, int W, int act, int s2out, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused training regions: the frozen-feature (perceptual) loss of          */
 /* xdna_train/regions.py:1-425 with its host kernels                        */

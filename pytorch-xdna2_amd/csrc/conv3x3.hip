@@ -168,6 +168,8 @@ __global__ __launch_bounds__(64) void prep_multi_kernel(PrepJobs jobs) {
 // ---------------------------------------------------------------------------------
 struct RowsArgs {
   const uint16_t* xp;    // [groups][chunks][2126][64]
+  const uint16_t* xsrc;  // NCHW [B][cin][H][W] (the small-grid kernel's NCHW form), else null
+  int cin;               // input channels (NCHW form)
   const uint16_t* wt;    // [co_pad][K]
   const uint16_t* bias;  // [cout] or null
   uint16_t* out;         // NCHW [B][cout][H][W]
@@ -1176,12 +1178,21 @@ void conv_rows6_kernel(RowsArgs a) {
 // tap), chunks outer and taps inner, and the bias is added after the last rounding (the
 // reference's host bias add, torch_xdna_device.cpp:2477-2480).  Operands come in already
 // quantized to BFP16 values; no split-K (it would change the rounding order).
+//
+// NCHW: the halo window is gathered from the NCHW input itself instead of packed rows
+// (images up to 36 columns, input channels a multiple of 8): window row i is padded-grid
+// row q = rt * TP + i of the packed layout (q = (b (H+2) + y + 1) wp + x + 1 for pixel
+// (y, x) of image b, wp = W + 2), so the LDS window, and with it every product and sum, is
+// the one the packed input gives, and no pack pass runs.  Item (row, 8-channel piece):
+// consecutive threads take consecutive rows, so each of the piece's eight 2-byte channel
+// loads of a wave reads one contiguous run of a channel plane; border, padding and
+// past-the-end rows read zeros (an offset past the buffer's range).
 constexpr int kSCo = 64;                  // output channels per workgroup
 constexpr int kSWPitch = 9 * kKStep + 8;  // LDS pitch of a staged weight row (584)
 
 __device__ inline float round_bf16(float v) { return __uint_as_float(uint32_t(f32_to_bf16(v)) << 16); }
 
-template <int TP, bool EMUL = false>
+template <int TP, bool EMUL = false, bool NCHW = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void conv_small_kernel(RowsArgs a) {
   constexpr int kXRows = TP + kMaxHalo;
@@ -1245,13 +1256,54 @@ void conv_small_kernel(RowsArgs a) {
   }
 
   u32x4_t xr[kXv], wr[kWv];
-  // weight vector v of the workgroup's chunk slab: row v / 72, piece v % 72 (8 elements)
-  auto load_chunk = [&](int ch) {
-    const uint16_t* xsrc = a.xp + ((int64_t(g) * a.chunks + ch) * kGroupRows + r0) * kKStep;
+  // NCHW: per window item j of this thread (row xrow[j], piece xpc[j]) the element offset of
+  // its pixel in channel plane 0 of its image, or a negative value for a zero row
+  const int nrows = TP + 2 * a.wp + 2;
+  int xoff[NCHW ? kXv : 1], xpc[NCHW ? kXv : 1], xrow[NCHW ? kXv : 1];
+  __amdgpu_buffer_rsrc_t xrs;
+  int plane_bytes = 0;
+  if constexpr (NCHW) {
+    const int hw = a.H * a.W;
+    plane_bytes = hw * 2;
+    xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xsrc), 0,
+                                            int(int64_t(a.B) * a.cin * hw * 2), 0x00020000);
+    const int64_t q0 = int64_t(g) * kGroupOutRows + r0;
 #pragma unroll
     for (int j = 0; j < kXv; ++j) {
       const int i = tid + j * 256;
-      if (i < nvec) xr[j] = *reinterpret_cast<const u32x4_t*>(xsrc + (i >> 3) * kKStep + (i & 7) * 8);
+      const int pc = i / nrows, row = i - pc * nrows;
+      xpc[j] = pc;
+      xrow[j] = row;
+      const int64_t q = q0 + row;
+      const int b = int(q / a.img);
+      const int rem = int(q - int64_t(b) * a.img);
+      const int yy = rem / a.wp, xx = rem - yy * a.wp;
+      const bool ok = i < nvec && q < a.m_total && yy >= 1 && yy <= a.H && xx >= 1 && xx <= a.W;
+      xoff[j] = ok ? (b * a.cin) * hw + (yy - 1) * a.W + (xx - 1) : -1;
+    }
+  }
+  // weight vector v of the workgroup's chunk slab: row v / 72, piece v % 72 (8 elements)
+  auto load_chunk = [&](int ch) {
+    if constexpr (NCHW) {
+#pragma unroll
+      for (int j = 0; j < kXv; ++j) {
+        const int c0 = ch * kKStep + 8 * xpc[j];
+        // element offset of (pixel, channel c0), or past the range (reads zeros)
+        const int off = xoff[j] >= 0 && c0 < a.cin ? 2 * (xoff[j] + c0 * (plane_bytes >> 1)) : 0x7FFFFFF0;
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          h[e] = uint32_t(__builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(
+                                                           xrs, off, e * plane_bytes, 0)));
+        xr[j] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      }
+    } else {
+      const uint16_t* xsrc = a.xp + ((int64_t(g) * a.chunks + ch) * kGroupRows + r0) * kKStep;
+#pragma unroll
+      for (int j = 0; j < kXv; ++j) {
+        const int i = tid + j * 256;
+        if (i < nvec) xr[j] = *reinterpret_cast<const u32x4_t*>(xsrc + (i >> 3) * kKStep + (i & 7) * 8);
+      }
     }
     const uint16_t* wsrc = a.wt + int64_t(co0) * K + int64_t(ch) * 9 * kKStep;
 #pragma unroll
@@ -1265,7 +1317,11 @@ void conv_small_kernel(RowsArgs a) {
 #pragma unroll
     for (int j = 0; j < kXv; ++j) {
       const int i = tid + j * 256;
-      if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[(i >> 3) * kPitch + (i & 7) * 8]) = xr[j];
+      if constexpr (NCHW) {
+        if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[xrow[j] * kPitch + xpc[j] * 8]) = xr[j];
+      } else {
+        if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[(i >> 3) * kPitch + (i & 7) * 8]) = xr[j];
+      }
     }
 #pragma unroll
     for (int j = 0; j < kWv; ++j) {
@@ -2076,6 +2132,8 @@ RowsArgs rows_args(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
   a.oH = H;
   a.oW = W;
   a.xp = xp;
+  a.xsrc = nullptr;
+  a.cin = cin;
   a.wt = wt;
   a.bias = bias;
   a.out = out;
@@ -2105,6 +2163,15 @@ RowsArgs rows_args(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
 // LDS of the small-grid kernel with TP-row tiles
 constexpr size_t small_lds(int TP) { return size_t(TP + kMaxHalo) * kPitch * 2 + size_t(kSCo) * kSWPitch * 2; }
 
+bool small_nchw_lds_ok() {
+  static const bool ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<64, false, true>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(64))) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128, false, true>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(128))) == hipSuccess;
+  return ok;
+}
+
 template <bool EMUL>
 bool small_lds_ok() {
   static const bool ok =
@@ -2113,6 +2180,40 @@ bool small_lds_ok() {
       hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128, EMUL>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(128))) == hipSuccess;
   return ok;
+}
+
+int launch_small(RowsArgs a, const ConvGeom& geom, int B, int cout, int variant, hipStream_t st);
+
+// Whether launch_rows would run this conv on the small-grid kernel and the kernel's NCHW
+// form can read the input in place: images up to 36 columns (one strip), input channels a
+// multiple of 8 (whole 8-channel pieces), an input under 2 GiB (32-bit buffer offsets).
+bool nchw_small_ok(int B, int cin, int cout, int H, int W) {
+  if (B < 1 || cin < 1 || cout < 1 || H < 1 || W < 1 || W > kMaxWidth || cin % 8 != 0) return false;
+  if (int64_t(B) * cin * H * W * 2 >= (int64_t(1) << 31)) return false;
+  const int variant = g_rows_variant.load();
+  if (variant == 2 || variant == 3) return true;
+  if (variant != 0) return false;
+  const ConvGeom geom = conv_geom(B, H, W, kLayoutTight);
+  return ceil_div(geom.m_total, 256) * ceil_div(cout, kSCo) < 150;
+}
+
+int launch_rows_nchw(const uint16_t* x, const uint16_t* wt, const uint16_t* bias, uint16_t* out, int B, int cin,
+                     int cout, int H, int W, int act, bool s2out, void* stream) {
+  const ConvGeom geom = conv_geom(B, H, W, kLayoutTight);
+  RowsArgs a = rows_args(nullptr, wt, bias, out, B, cin, cout, H, W, geom, act);
+  a.xsrc = x;
+  if (s2out) {
+    a.osh = 1;
+    a.oH = (H + 1) / 2;
+    a.oW = (W + 1) / 2;
+    if (!a.out_rs) {
+      set_error("conv3x3 nchw: the stride-2 output needs the buffer-store epilogue (output too large)");
+      return -1;
+    }
+  }
+  if (!admit_launch("conv3x3 nchw")) return -1;
+  const int v = g_rows_variant.load();
+  return launch_small(a, geom, B, cout, v == 2 || v == 3 ? v : -1, as_stream(stream));
 }
 
 int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* out,
@@ -2223,7 +2324,14 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
       conv_rows_kernel<64><<<grid, 256, 0, st>>>(a);
     return check_launch("conv3x3 rows");
   }
-  if (!small_lds_ok<false>()) {
+  return launch_small(a, geom, B, cout, variant, st);
+}
+
+// The small-grid kernel (variant 2 / 3 force its 64 / 128-row tiles; otherwise by grid
+// size), with split-K below 64 workgroups; a.xsrc set: its NCHW form.
+int launch_small(RowsArgs a, const ConvGeom& geom, int B, int cout, int variant, hipStream_t st) {
+  const bool nchw = a.xsrc != nullptr;
+  if (nchw ? !small_nchw_lds_ok() : !small_lds_ok<false>()) {
     set_error("conv3x3 rows: cannot enable the small-grid kernel's LDS size");
     return -1;
   }
@@ -2247,7 +2355,11 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
   a.nrt = int(ceil_div(geom.m_total, TP));
   a.ncot = int(stiles);
   const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, unsigned(nsplit));
-  if (TP == 128)
+  if (nchw && TP == 128)
+    conv_small_kernel<128, false, true><<<grid, 256, small_lds(128), st>>>(a);
+  else if (nchw)
+    conv_small_kernel<64, false, true><<<grid, 256, small_lds(64), st>>>(a);
+  else if (TP == 128)
     conv_small_kernel<128><<<grid, 256, small_lds(128), st>>>(a);
   else
     conv_small_kernel<64><<<grid, 256, small_lds(64), st>>>(a);
@@ -3213,6 +3325,25 @@ int xdna_conv3x3_layout_rows_act_bf16(const uint16_t* xp, const uint16_t* wt, co
     return -1;
   }
   return launch_rows(xp, wt, bias, y, B, cin, cout, H, W, stream, layout, act);
+}
+
+int xdna_conv3x3_nchw_small_eligible(int B, int cin, int cout, int H, int W) {
+  return nchw_small_ok(B, cin, cout, H, W) ? 1 : 0;
+}
+
+int xdna_conv3x3_nchw_act_bf16(const uint16_t* x, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int B,
+                               int cin, int cout, int H, int W, int act, int s2out, void* stream) {
+  if (!shape_ok("xdna_conv3x3_nchw_act_bf16", B, cin, cout, H, W)) return -1;
+  if (act < 0 || act > 1 || s2out < 0 || s2out > 1 || !x || !wt || !y) {
+    set_error("xdna_conv3x3_nchw_act_bf16: invalid activation, output form or null buffer");
+    return -1;
+  }
+  if (!nchw_small_ok(B, cin, cout, H, W)) {
+    set_error("xdna_conv3x3_nchw_act_bf16: not a small-grid conv with W <= 36, cin % 8 == 0 and an input under "
+              "2 GiB (xdna_conv3x3_nchw_small_eligible)");
+    return -1;
+  }
+  return launch_rows_nchw(x, wt, bias, y, B, cin, cout, H, W, act, s2out != 0, stream);
 }
 
 int xdna_conv3x3_layout_rows_stride2_bf16(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, uint16_t* y,

@@ -142,17 +142,27 @@ void clear_weight_cache() {
 
 void note_graph_replay() { g_replay_generation.fetch_add(1); }
 
-// Prepared forms of frozen weights that a captured graph reads.  A capture that meets a
-// frozen weight (no gradient) whose form the eager cache holds adopts that form instead of
+// Prepared forms that a captured graph reads without preparing them itself.  A capture
+// that meets a weight whose form the eager cache holds adopts that form instead of
 // recording a preparation: the graph keeps the form (and the weight) alive, and every
 // replay first prepares it again, eagerly and on the replay's stream, if the weight was
 // written since (version or write epoch), so a replay computes with the weight's current
-// value as an eager step would.  Writes the graph itself makes to a frozen weight are not
-// seen (no host code runs); trainable weights are prepared inside the graph.
+// value as an eager step would.  Writes the graph itself makes are not seen by host code:
+//  * a frozen weight is not written by its graph;
+//  * a trainable weight is written by the optimizer step, and where that step is part of
+//    the same capture (the fused optimizer's refresh_conv_forms under the capture's tag),
+//    the graph records one preparation of every adopted form it wrote right after the
+//    step, so each replay leaves the forms of the weights it produced for the next one;
+//  * a trainable weight whose adopted forms no captured step refreshes is prepared again
+//    before every replay (one launch for all of them).
+// The eager cache serves a trainable weight's forms only after the fused optimizer step
+// refreshed them (refresh_conv_forms), which an eager warm-up step before the capture does.
 namespace {
 struct GraphWeight {
   at::Tensor weight, wt;
   bool dgrad = false;
+  bool trainable = false;
+  bool graph_refreshed = false;  // a captured optimizer step prepares it again after writing
   int64_t version = 0;
   uint64_t epoch = 0;
 };
@@ -171,11 +181,12 @@ int64_t weight_version(const at::Tensor& w) {
   return int64_t(w.unsafeGetTensorImpl()->version_counter().current_version());
 }
 
-void adopt_graph_weight(int64_t pool, const at::Tensor& w, bool dgrad, const at::Tensor& wt) {
+void adopt_graph_weight(int64_t pool, const at::Tensor& w, bool dgrad, const at::Tensor& wt, bool trainable) {
   GraphWeight e;
   e.weight = w;
   e.wt = wt;
   e.dgrad = dgrad;
+  e.trainable = trainable;
   e.version = weight_version(w);
   e.epoch = write_epoch(w);
   GraphWeights& g = graph_weights();
@@ -189,23 +200,77 @@ int64_t refresh_graph_weights(int64_t pool) {
   std::lock_guard<std::mutex> lock(g.mu);
   auto it = g.by_pool.find(pool);
   if (it == g.by_pool.end()) return 0;
+  // every stale form, both forms of one contiguous weight as one job of a single launch
+  std::vector<at::Tensor> keep;
+  std::vector<const uint16_t*> w;
+  std::vector<uint16_t*> wt, wtd;
+  std::vector<int> co, ci;
   int64_t n = 0;
   for (GraphWeight& e : it->second) {
     const int64_t ver = weight_version(e.weight);
     const uint64_t ep = write_epoch(e.weight);
-    if (ver == e.version && ep == e.epoch) continue;
-    at::Tensor wc = e.weight.contiguous();
-    check_abi(xdna_conv3x3_prepare_weights_bf16(static_cast<const uint16_t*>(wc.const_data_ptr()),
-                                                static_cast<uint16_t*>(e.wt.data_ptr()), int(wc.size(0)),
-                                                int(wc.size(1)), e.dgrad ? 1 : 0, current_stream()),
-              "graph weight refresh");
+    if (ver == e.version && ep == e.epoch && !(e.trainable && !e.graph_refreshed)) continue;
     e.version = ver;
     e.epoch = ep;
     ++n;
+    at::Tensor wc = e.weight.contiguous();
+    const uint16_t* src = static_cast<const uint16_t*>(wc.const_data_ptr());
+    size_t j = 0;
+    while (j < w.size() && w[j] != src) ++j;
+    if (j == w.size()) {
+      keep.push_back(wc);
+      w.push_back(src);
+      wt.push_back(nullptr);
+      wtd.push_back(nullptr);
+      co.push_back(int(wc.size(0)));
+      ci.push_back(int(wc.size(1)));
+    }
+    (e.dgrad ? wtd : wt)[j] = static_cast<uint16_t*>(e.wt.data_ptr());
   }
+  if (!w.empty())
+    check_abi(xdna_conv3x3_prepare_weights_multi_bf16(int(w.size()), w.data(), wt.data(), wtd.data(), co.data(),
+                                                      ci.data(), current_stream()),
+              "graph weight refresh");
   if (n) count_call("hip_conv3x3.weights_graph_refresh", 0);
   return n;
 }
+
+namespace {
+// Inside a capture: the adopted forms of the weights a captured optimizer step has just
+// written, prepared again by one launch recorded right after the step.
+void refresh_captured_forms(int64_t pool, at::TensorList params) {
+  GraphWeights& g = graph_weights();
+  std::lock_guard<std::mutex> lock(g.mu);
+  auto it = g.by_pool.find(pool);
+  if (it == g.by_pool.end()) return;
+  std::vector<const uint16_t*> w;
+  std::vector<uint16_t*> wt, wtd;
+  std::vector<int> co, ci;
+  std::vector<GraphWeight*> hit;
+  for (const auto& p : params) {
+    if (!p.defined() || p.dim() != 4 || !p.is_contiguous()) continue;
+    std::array<GraphWeight*, 2> fd{nullptr, nullptr};
+    for (GraphWeight& e : it->second)
+      if (e.trainable && e.weight.const_data_ptr() == p.const_data_ptr() && e.weight.sizes() == p.sizes() &&
+          e.weight.strides() == p.strides())
+        fd[e.dgrad ? 1 : 0] = &e;
+    if (!fd[0] && !fd[1]) continue;
+    w.push_back(static_cast<const uint16_t*>(p.const_data_ptr()));
+    wt.push_back(fd[0] ? static_cast<uint16_t*>(fd[0]->wt.data_ptr()) : nullptr);
+    wtd.push_back(fd[1] ? static_cast<uint16_t*>(fd[1]->wt.data_ptr()) : nullptr);
+    co.push_back(int(p.size(0)));
+    ci.push_back(int(p.size(1)));
+    for (GraphWeight* e : fd)
+      if (e) hit.push_back(e);
+  }
+  if (w.empty()) return;
+  check_abi(xdna_conv3x3_prepare_weights_multi_bf16(int(w.size()), w.data(), wt.data(), wtd.data(), co.data(),
+                                                    ci.data(), current_stream()),
+            "conv weights (captured optimizer step)");
+  for (GraphWeight* e : hit) e->graph_refreshed = true;
+  count_call("hip_conv3x3.weights_graph_step_refresh", 0);
+}
+}  // namespace
 
 void purge_capture_entries(int64_t tag);
 
@@ -315,7 +380,11 @@ std::atomic<int> g_adam_prep{[] {
 }()};
 
 void refresh_conv_forms(at::TensorList params) {
-  if (!g_adam_prep.load() || capture_tag() != 0) return;
+  if (!g_adam_prep.load()) return;
+  if (const int64_t tag = capture_tag(); tag != 0) {
+    refresh_captured_forms(tag, params);
+    return;
+  }
   WeightCache& c = weight_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   const uint64_t gen = g_replay_generation.load();
@@ -393,25 +462,27 @@ at::Tensor pack_rows(const at::Tensor& src, int layout) {
 // BFP16 emulation covers: the reference's NPU takes only stride-1 convs.
 // s2out: the forward of a 3x3 / stride-2 / pad-1 conv, storing only the even outputs of
 // the stride-1 conv into a ceil(H/2) x ceil(W/2) tensor.
-at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef src, const at::Tensor& w,
-                           const at::Tensor* bias, bool dgrad, int act = 0, bool s1 = true, bool s2out = false) {
-  const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
+// The prepared form (forward, or input gradient: flip+swap) of conv weight w, from the
+// cache or made here.  Both forms are cached (see PreparedWeights).  A trainable weight's
+// forward prepares the input gradient's form in the same launch, so the backward of the
+// step finds it; the optimizer step then bumps the epoch and the next forward prepares
+// both again (or the fused optimizer step prepares them, refresh_conv_forms).
+at::Tensor conv_weight_form(const at::Tensor& w, bool dgrad) {
+  const int64_t cin = dgrad ? w.size(0) : w.size(1);
   const int64_t cout = dgrad ? w.size(1) : w.size(0);
   at::Tensor wc = w.contiguous();
   void* st = current_stream();
-  // Both forms are cached (see PreparedWeights).  A trainable weight's forward prepares
-  // the input gradient's form in the same launch, so the backward of the step finds it;
-  // the optimizer step then bumps the epoch and the next forward prepares both again.
   const int64_t tag = capture_tag();
   const bool cacheable = weight_cacheable(w);
   const bool trainable = w.requires_grad() && !w.is_inference();
   at::Tensor wt = cacheable ? cached_weights(w, dgrad, tag) : at::Tensor();
-  if (!wt.defined() && tag > 0 && cacheable && !trainable) {
-    // a capture meeting a frozen weight whose eager form is cached: the graph adopts it
-    // (kept alive by the graph, prepared again by replay when the weight was written)
+  if (!wt.defined() && tag > 0 && cacheable && (!trainable || g_adam_prep.load())) {
+    // a capture meeting a weight whose eager form is cached: the graph adopts it (kept
+    // alive by the graph, prepared again by the captured optimizer step or by replay when
+    // the weight was written; see GraphWeight)
     wt = cached_weights(w, dgrad, 0);
     if (wt.defined()) {
-      adopt_graph_weight(tag, w, dgrad, wt);
+      adopt_graph_weight(tag, w, dgrad, wt, trainable);
       remember_weights(w, dgrad, wt, tag);
       count_call("hip_conv3x3.weights_graph", 0);
     }
@@ -439,6 +510,52 @@ at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef
       if (cacheable) remember_weights(w, dgrad, wt, tag);
     }
   }
+  return wt;
+}
+
+// Small-grid convs read their NCHW input in place (xdna_conv3x3_nchw_act_bf16: the same
+// bits as the pack followed by the packed conv) unless XDNA_CONV_NCHW=0; the BFP16
+// emulation keeps its packed path.
+std::atomic<int> g_conv_nchw{[] {
+  const char* e = std::getenv("XDNA_CONV_NCHW");
+  return e && std::atoi(e) == 0 ? 0 : 1;
+}()};
+
+bool nchw_route(const at::Tensor& src, int64_t cout, bool s1) {
+  if (!g_conv_nchw.load() || (s1 && g_bfp16_emul.load())) return false;
+  return xdna_conv3x3_nchw_small_eligible(int(src.size(0)), int(src.size(1)), int(cout), int(src.size(2)),
+                                          int(src.size(3))) == 1;
+}
+
+// The conv of NCHW src (cin channels) with `w` as hip_conv_packed, for an nchw_route conv.
+at::Tensor hip_conv_nchw(const at::Tensor& src_in, const at::Tensor& w, const at::Tensor* bias, bool dgrad,
+                         int act = 0, bool s2out = false) {
+  const at::Tensor src = src_in.contiguous();
+  const int64_t B = src.size(0), cin = src.size(1), H = src.size(2), W = src.size(3);
+  const int64_t cout = dgrad ? w.size(1) : w.size(0);
+  at::Tensor wt = conv_weight_form(w, dgrad);
+  at::Tensor out = s2out ? empty_xdna({B, cout, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16)
+                         : empty_xdna({B, cout, H, W}, at::kBFloat16);
+  at::Tensor bc;
+  if (bias) bc = bias->contiguous();
+  const double flops = 2.0 * double(B) * double(H) * double(W) * double(cin) * double(cout) * 9.0;
+  KernelTimer kt(s2out ? "conv3x3_rows.s2" : dgrad ? "conv3x3_rows.dgrad" : "conv3x3_rows.fwd", flops);
+  count_call("hip_conv3x3.nchw", 0);
+  check_abi(xdna_conv3x3_nchw_act_bf16(static_cast<const uint16_t*>(src.const_data_ptr()),
+                                       static_cast<const uint16_t*>(wt.const_data_ptr()),
+                                       bias ? static_cast<const uint16_t*>(bc.const_data_ptr()) : nullptr,
+                                       static_cast<uint16_t*>(out.data_ptr()), int(B), int(cin), int(cout), int(H),
+                                       int(W), act, s2out ? 1 : 0, current_stream()),
+            "conv nchw");
+  return out;
+}
+
+at::Tensor hip_conv_packed(const at::Tensor& packed, int layout, at::IntArrayRef src, const at::Tensor& w,
+                           const at::Tensor* bias, bool dgrad, int act = 0, bool s1 = true, bool s2out = false) {
+  const int64_t B = src[0], cin = src[1], H = src[2], W = src[3];
+  const int64_t cout = dgrad ? w.size(1) : w.size(0);
+  void* st = current_stream();
+  at::Tensor wt = conv_weight_form(w, dgrad);
   at::Tensor out = s2out ? empty_xdna({B, cout, (H + 1) / 2, (W + 1) / 2}, at::kBFloat16)
                          : empty_xdna({B, cout, H, W}, at::kBFloat16);
   at::Tensor bc;
@@ -632,10 +749,12 @@ std::atomic<int64_t> g_dw_jobs{0};
 at::Tensor hip_conv_fwd(const at::Tensor& input, const at::Tensor& weight, const at::Tensor* bias, bool s1 = true,
                         bool s2out = false) {
   const int layout = g_conv_layout.load();
+  const bool keep = g_mode.load() >= 2 && weight.requires_grad() && !weight.is_inference() &&
+                    !input.is_inference() && wgrad_rows_pick(input.size(1), weight.size(0), input.size(3));
+  // no packed copy wanted afterwards: a small grid reads the input in place
+  if (!keep && nchw_route(input, weight.size(0), s1)) return hip_conv_nchw(input, weight, bias, false, 0, s2out);
   at::Tensor packed = pack_rows(input, layout);
-  if (g_mode.load() >= 2 && weight.requires_grad() && !weight.is_inference() && !input.is_inference() &&
-      wgrad_rows_pick(input.size(1), weight.size(0), input.size(3)))
-    remember_packed_input(input, packed, layout);
+  if (keep) remember_packed_input(input, packed, layout);
   return hip_conv_packed(packed, layout, input.sizes(), weight, bias, false, 0, s1, s2out);
 }
 
@@ -987,11 +1106,14 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   // dY packed once: the input gradient's conv and the rows weight gradient read it
   const int layout = g_conv_layout.load();
   at::Tensor gop;
-  if (hip && (mask[0] || dw_rows))
+  // the input gradient alone reads dY: a small grid reads it in place
+  const bool dx_nchw = hip && mask[0] && !dw_rows && !strided && nchw_route(go, weight.size(1), true);
+  if (hip && ((mask[0] && !dx_nchw) || dw_rows))
     gop = strided ? pack_rows_spread(grad_output, go_sizes[2], go_sizes[3], layout) : pack_rows(go, layout);
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
-    gi = hip_conv_packed(gop, layout, go_sizes, weight, nullptr, true, 0, !strided);
+    gi = dx_nchw ? hip_conv_nchw(go, weight, nullptr, true)
+                 : hip_conv_packed(gop, layout, go_sizes, weight, nullptr, true, 0, !strided);
     mask[0] = false;
   }
   if (strided && dw && !dw_rows) {
@@ -2019,6 +2141,7 @@ at::Tensor region_conv3x3(const at::Tensor& x, const at::Tensor& w, const std::o
                     b->device().type() == kXdna,
                 "region conv: bias must be a bf16 xdna vector of the output channels");
   ScopedCount sc(act ? "hip_region.conv_relu.run" : "hip_region.conv.run");
+  if (nchw_route(x, w.size(0), true)) return hip_conv_nchw(x, w, has_b ? &*b : nullptr, false, act);
   const int layout = g_conv_layout.load();
   return hip_conv_packed(pack_rows(x, layout), layout, x.sizes(), w, has_b ? &*b : nullptr, false, act);
 }

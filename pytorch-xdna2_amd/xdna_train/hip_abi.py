@@ -114,6 +114,8 @@ SIGNATURES = {
     "xdna_conv3x3_layout_pack_bf16": (I, [P, P, I, I, I, I, I, P]),
     "xdna_conv3x3_layout_rows_bf16": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "xdna_conv3x3_layout_rows_act_bf16": (I, [P, P, P, P, I, I, I, I, I, I, I, P]),
+    "xdna_conv3x3_nchw_small_eligible": (I, [I, I, I, I, I]),
+    "xdna_conv3x3_nchw_act_bf16": (I, [P, P, P, P, I, I, I, I, I, I, I, P]),
     "xdna_region_maxpool2_bf16": (I, [P, P, L, I, I, P]),
     "xdna_region_backward_bf16": (I, [P, P, P, P, P, P, P, F, P, I, P, L, I, I, P]),
     "xdna_region_loss_parts": (I, []),

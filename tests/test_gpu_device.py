@@ -508,8 +508,9 @@ def test_frozen_weights_prepared_once_and_refreshed_on_write():
     y2 = cd(xd)
     n1 = xdna_train.device.native().launch_count()
     assert torch.equal(y1.cpu(), y2.cpu())
-    # the second call reuses the prepared weights: pack + conv only (no preparation launch)
-    assert n1 - n0 == 2, (n0, n1)
+    # the second call reuses the prepared weights: the conv only (no preparation launch; a
+    # frozen conv on a grid this small reads its NCHW input in place, with no pack launch)
+    assert n1 - n0 == 1, (n0, n1)
     ref = conv(x).float()
     assert torch.allclose(y2.cpu().float(), ref, atol=5e-2, rtol=5e-2)
     # an in-place write bumps the version: the new weights are used

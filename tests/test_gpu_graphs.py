@@ -61,3 +61,97 @@ def test_captured_training_step_matches_eager():
         assert torch.equal(pe, pg.detach().cpu())
     graph.reset()
     torch.xdna.synchronize()
+
+
+def _stat_calls(name):
+    return xdna_train.mapped_cpu_stats().get(name, {}).get("calls", 0)
+
+
+def test_captured_step_adopts_trainable_forms():
+    """The trainable conv weights' prepared forms made by the eager optimizer step are
+    adopted by the capture (no preparation recorded per weight); the captured optimizer
+    step prepares them again in one launch; replays match the eager run bit for bit (the
+    test above) and the capture records no per-weight preparation."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(8, 64, 12, 12, generator=g).bfloat16().to(X)
+    t = torch.randn(8, 64, generator=g).to(X)
+    m = _model(0).to(X)
+    opt = torch.optim.Adam(m.parameters(), lr=1e-3, fused=True, capturable=True)
+    step = _step_fn(m, opt, x, t)
+    for _ in range(2):
+        step()
+    torch.xdna.synchronize()
+    prep0 = _stat_calls("hip_conv3x3.weights")
+    adopt0 = _stat_calls("hip_conv3x3.weights_graph")
+    refresh0 = _stat_calls("hip_conv3x3.weights_graph_step_refresh")
+    graph = torch.xdna.Graph()
+    with torch.xdna.graph(graph):
+        step()
+    assert _stat_calls("hip_conv3x3.weights") == prep0, "the capture prepared a weight itself"
+    # both forward forms and the second conv's input-gradient form (the first conv's input
+    # needs no gradient)
+    assert _stat_calls("hip_conv3x3.weights_graph") - adopt0 == 3
+    assert _stat_calls("hip_conv3x3.weights_graph_step_refresh") - refresh0 == 1
+    graph.reset()
+    torch.xdna.synchronize()
+
+
+@pytest.mark.parametrize("between", ["eager_optimizer", "weight_write"])
+def test_replays_see_eager_writes_of_adopted_trainable_weights(between):
+    """A graph of forward + backward only (the optimizer steps eagerly between replays),
+    or of the whole step with the weights rescaled eagerly between replays: the adopted
+    forms are prepared again before each replay that needs it, so every replay computes
+    with the weights' current values, bit for bit as the same sequence run eagerly."""
+    g = torch.Generator().manual_seed(4)
+    x_cpu = torch.randn(8, 64, 12, 12, generator=g).bfloat16()
+    t_cpu = torch.randn(8, 64, generator=g)
+
+    def run(graphed):
+        m = _model(1).to(X)
+        opt = torch.optim.Adam(m.parameters(), lr=1e-3, fused=True, capturable=True)
+        x, t = x_cpu.to(X), t_cpu.to(X)
+
+        def fwd_bwd():
+            opt.zero_grad(set_to_none=False)
+            loss = torch.nn.functional.mse_loss(m(x).float(), t)
+            loss.backward()
+            return loss
+
+        def full():
+            loss = fwd_bwd()
+            opt.step()
+            return loss
+
+        body = fwd_bwd if between == "eager_optimizer" else full
+        losses = []
+        for _ in range(2):
+            losses.append(float(full()))
+        if graphed:
+            graph = torch.xdna.Graph()
+            with torch.xdna.graph(graph):
+                loss = body()
+        for _ in range(4):
+            if graphed:
+                graph.replay()
+            else:
+                loss = body()
+            if between == "eager_optimizer":
+                opt.step()
+            else:
+                with torch.no_grad():
+                    m[0].weight.mul_(0.75)
+                    m[2].weight.mul_(1.25)
+            torch.xdna.synchronize()
+            losses.append(float(loss))
+        params = [p.detach().cpu() for p in m.parameters()]
+        if graphed:
+            graph.reset()
+            torch.xdna.synchronize()
+        return losses, params
+
+    le, pe = run(False)
+    lg, pg = run(True)
+    print(between, "eager", le, "graph", lg, flush=True)
+    assert lg == le
+    for a, b in zip(pe, pg):
+        assert torch.equal(a, b)
