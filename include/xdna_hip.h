@@ -472,6 +472,11 @@ int xdna_conv3x3_prepare_weights_multi_bf16(int n, const uint16_t* const* w, uin
 /* Split-K count of the rows weight gradient: 0 (default) its cost model, else this many
  * (at most one per 64-row k-tile).  For measurements; no reference counterpart. */
 int xdna_conv3x3_set_wgrad_splits(int splits);
+/* Output-channel tile of the rows weight gradient's direct-to-LDS form: 0 (default) by
+ * layer (64 channels, four waves, for up to 64 output channels and for layers of up to 256
+ * channels each side and 40 GFLOP; else 128, eight waves), or forced to 64 or 128.  For
+ * measurements; no reference counterpart. */
+int xdna_conv3x3_set_wgrad_tile(int co_tile);
 
 /* No counterpart in the reference: a form of xdna_gemm_bf16 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses

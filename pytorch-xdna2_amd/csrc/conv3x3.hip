@@ -234,6 +234,23 @@ __device__ inline int out_pixel_off(const RowsArgs& a, const OutMap& o, int64_t 
   return int(((int64_t(b - o.b0)) * o.cp + int64_t(y >> a.osh) * a.oW + (x >> a.osh)) * 2);
 }
 
+// out_pixel_off in 32-bit arithmetic, for grids of fewer than 2^31 rows (the small-grid
+// kernel's, checked on the host)
+__device__ inline int out_pixel_off32(const RowsArgs& a, const OutMap& o, int p) {
+  if (p >= int(a.m_total)) return kOutSkip;
+  const int img = int(a.img);
+  const int vb = p / img;
+  const int rem = p - vb * img;
+  const int y = rem / a.wp;
+  const int col = rem - y * a.wp - a.first;
+  const int b = a.S == 1 ? vb : vb / a.S, s = vb - b * a.S;
+  const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+  if (y >= a.H || col < 0 || col >= cols) return kOutSkip;
+  const int x = (a.S == 1 ? 0 : s * a.So) + col;
+  if ((y | x) & a.osh) return kOutSkip;
+  return ((b - o.b0) * int(o.cp) + (y >> a.osh) * a.oW + (x >> a.osh)) * 2;
+}
+
 constexpr int kXcds = 8;  // MI355X: workgroups go round-robin to 8 XCDs, each with its own L2
 
 // blockIdx.x -> (row tile, channel tile).  Workgroup L runs on XCD L % 8; on each XCD the
@@ -1282,7 +1299,26 @@ void conv_small_kernel(RowsArgs a) {
       xoff[j] = ok ? (b * a.cin) * hw + (yy - 1) * a.W + (xx - 1) : -1;
     }
   }
-  // weight vector v of the workgroup's chunk slab: row v / 72, piece v % 72 (8 elements)
+  // Chunk staging with addresses fixed per thread (no per-chunk index math):
+  //  * weights: thread t copies row t / 4 of the workgroup's 64-row slab, its 16-byte
+  //    pieces t % 4 + 4 j (j < 18) of 72: one buffer offset per thread, 64 j bytes as an
+  //    immediate, chunk ch's slab ch * 1152 bytes into the rows (scalar offset);
+  //  * packed window: item (row t / 8 + 32 j, piece t % 8): one buffer offset per thread,
+  //    the chunk's block and 4096 j bytes in the scalar offset; rows past the window are
+  //    read (inside the group's 2126 rows, or past the buffer: zeros) and not stored.
+  const int wrow = tid >> 2, wq = tid & 3;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.wt + int64_t(co0) * K), 0, kSCo * K * 2, 0x00020000);
+  const int wvo = wrow * K * 2 + wq * 16;
+  uint16_t* const wlds = ws + wrow * kSWPitch + wq * 8;
+  __amdgpu_buffer_rsrc_t prs;
+  if constexpr (!NCHW) {
+    const int64_t pbase = (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
+    const int64_t ptotal = (a.m_total + kGroupOutRows - 1) / kGroupOutRows * a.chunks * kGroupRows * kKStep;
+    prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xp + pbase), 0,
+                                            int(min<int64_t>((ptotal - pbase) * 2, 0x7FFFFFFF)), 0x00020000);
+  }
+  const int pvo = (tid >> 3) * 128 + (tid & 7) * 16;
   auto load_chunk = [&](int ch) {
     if constexpr (NCHW) {
 #pragma unroll
@@ -1298,37 +1334,30 @@ void conv_small_kernel(RowsArgs a) {
         xr[j] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
       }
     } else {
-      const uint16_t* xsrc = a.xp + ((int64_t(g) * a.chunks + ch) * kGroupRows + r0) * kKStep;
+      const int so = ch * (kGroupRows * kKStep * 2);
 #pragma unroll
-      for (int j = 0; j < kXv; ++j) {
-        const int i = tid + j * 256;
-        if (i < nvec) xr[j] = *reinterpret_cast<const u32x4_t*>(xsrc + (i >> 3) * kKStep + (i & 7) * 8);
-      }
+      for (int j = 0; j < kXv; ++j)
+        xr[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(prs, pvo, so + j * 4096, 0));
     }
-    const uint16_t* wsrc = a.wt + int64_t(co0) * K + int64_t(ch) * 9 * kKStep;
+    const int wso = ch * (9 * kKStep * 2);
+    static_assert(kWv == 18 && kSCo * 4 == 256, "weight staging: 4 threads per row, 18 pieces each");
 #pragma unroll
-    for (int j = 0; j < kWv; ++j) {
-      const int v = tid + j * 256;
-      const int row = v / 72, piece = v - row * 72;
-      wr[j] = *reinterpret_cast<const u32x4_t*>(wsrc + int64_t(row) * K + piece * 8);
-    }
+    for (int j = 0; j < kWv; ++j)
+      wr[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo + j * 64, wso, 0));
   };
   auto store_chunk = [&]() {
 #pragma unroll
     for (int j = 0; j < kXv; ++j) {
-      const int i = tid + j * 256;
       if constexpr (NCHW) {
+        const int i = tid + j * 256;
         if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[xrow[j] * kPitch + xpc[j] * 8]) = xr[j];
       } else {
-        if (i < nvec) *reinterpret_cast<u32x4_t*>(&xs[(i >> 3) * kPitch + (i & 7) * 8]) = xr[j];
+        const int row = (tid >> 3) + 32 * j;
+        if (row < nrows) *reinterpret_cast<u32x4_t*>(&xs[row * kPitch + (tid & 7) * 8]) = xr[j];
       }
     }
 #pragma unroll
-    for (int j = 0; j < kWv; ++j) {
-      const int v = tid + j * 256;
-      const int row = v / 72, piece = v - row * 72;
-      *reinterpret_cast<u32x4_t*>(&ws[row * kSWPitch + piece * 8]) = wr[j];
-    }
+    for (int j = 0; j < kWv; ++j) *reinterpret_cast<u32x4_t*>(wlds + j * 32) = wr[j];
   };
 
   load_chunk(ch0);
@@ -1399,7 +1428,7 @@ void conv_small_kernel(RowsArgs a) {
     int poff[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
-      poff[n] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr);
+      poff[n] = out_pixel_off32(a, om, g * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int co = co0 + wm * 32 + mfma_row(i, lane);
@@ -2331,6 +2360,11 @@ int launch_rows(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias, ui
 // size), with split-K below 64 workgroups; a.xsrc set: its NCHW form.
 int launch_small(RowsArgs a, const ConvGeom& geom, int B, int cout, int variant, hipStream_t st) {
   const bool nchw = a.xsrc != nullptr;
+  // 32-bit row indexes and weight-slab offsets in the kernel
+  if (geom.m_total >= (int64_t(1) << 30) || int64_t(kSCo) * a.chunks * 9 * kKStep * 2 >= (int64_t(1) << 31)) {
+    set_error("conv3x3 rows: grid or weights too large for the small-grid kernel");
+    return -1;
+  }
   if (nchw ? !small_nchw_lds_ok() : !small_lds_ok<false>()) {
     set_error("conv3x3 rows: cannot enable the small-grid kernel's LDS size");
     return -1;
@@ -2386,6 +2420,10 @@ int launch_rows_emul(const uint16_t* xp, const uint16_t* wt, const uint16_t* bia
   const size_t wbytes = xdna_conv3x3_prepared_weight_bytes(cin, cout);
   if (!small_lds_ok<true>()) {
     set_error("conv3x3 BFP16 emulation: cannot enable the small-grid kernel's LDS size");
+    return -1;
+  }
+  if (geom.m_total >= (int64_t(1) << 30) || int64_t(kSCo) * chunks * 9 * kKStep * 2 >= (int64_t(1) << 31)) {
+    set_error("conv3x3 BFP16 emulation: grid or weights too large for the small-grid kernel");
     return -1;
   }
   uint16_t* xq = static_cast<uint16_t*>(xdna_hip_cache_alloc(xbytes));
@@ -2730,8 +2768,18 @@ struct W5Frags {
   uint2 x[3][3];  // per kernel row: 12 consecutive rows of the wave's 32 input channels
 };
 
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NW = 4: the same k-tile pipeline with four waves on a 64-output-channel tile (waves
+// (wm, wn) in 2 x 2, 32 x 32 channels each): twice the workgroups for a split count and
+// half the fp32 partials per workgroup, for layers of up to 64 output channels (no
+// half-empty tile) and layers whose grid is small; only the dY tile's first 8 pieces (one
+// 64-channel chunk) are loaded, the rest of its LDS rows read as zeros and are never used.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void wgrad_rows5_kernel(WgRowsArgs a) {
+  static_assert(NW == 8 || NW == 4, "eight or four waves");
+  constexpr int kCT = NW == 8 ? kTCo : 64;           // output channels per tile
+  constexpr int kDyPer = 16 / NW;                    // dY DMA blocks per wave
+  constexpr int kXPer = NW == 8 ? 0 : 5;             // x DMA blocks per wave (four waves)
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   constexpr int kTilesPerGroup = kGroupOutRows / kW5Kt;
   const int L = blockIdx.x;
@@ -2740,10 +2788,10 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
   const int split = (kq / a.ntiles) * kXcds + xcd;
   if (split >= a.splits) return;
   const int co_t = tile % a.nco_t, ci_t = tile / a.nco_t;
-  const int co0 = co_t * kTCo, ci0 = ci_t * 64;
+  const int co0 = co_t * kCT, ci0 = ci_t * 64;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 3, wn = wave >> 2;
+  const int wm = NW == 8 ? wave & 3 : wave & 1, wn = NW == 8 ? wave >> 2 : wave >> 1;
   const int kt0 = split * a.kt_per_split;
   const int ntl = min(a.ktiles, kt0 + a.kt_per_split) - kt0;
 
@@ -2758,19 +2806,19 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
     // lane % 16 holding global piece dq (channel chunk co0 / 64 + dq / 8).
     const bool strips = a.S > 1;
     const int dq = (lane & 15) ^ (4 * (lane >> 4));
-    const bool dchunk_ok = co0 / 64 + (dq >> 3) < a.co_chunks;
+    const bool dchunk_ok = (dq >> 3) < kCT / 64 && co0 / 64 + (dq >> 3) < a.co_chunks;
     const int doff0 = (dq >> 3) * kGroupRows * 128 + (dq & 7) * 16;  // bytes, + 128 per row
-    int drow[2], drmod[2];
+    int drow[kDyPer], drmod[kDyPer];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      drow[i] = 8 * wave + 4 * i + (lane >> 4);
+    for (int i = 0; i < kDyPer; ++i) {
+      drow[i] = 4 * kDyPer * wave + 4 * i + (lane >> 4);
       drmod[i] = drow[i] % a.wp;
     }
-    const int nrel = min(2, a.co_chunks - co0 / 64);
+    const int nrel = min(kCT / 64, a.co_chunks - co0 / 64);
     const int dext = (nrel - 1) * kGroupRows * 128 + kW5Kt * 128;
     // x block xb0 + i: window rows 8 (xb0 + i) + lane / 8, LDS position lane % 8 holding
     // global piece xq (bit 1 of the row is bit 1 of lane / 8)
-    const int xb0 = wave < 4 ? 3 * wave : 2 * wave + 4;
+    const int xb0 = NW == 4 ? kXPer * wave : wave < 4 ? 3 * wave : 2 * wave + 4;
     const int xq = (lane & 7) ^ (4 * ((lane >> 4) & 1));
     const int xoff0 = (8 * xb0 + (lane >> 3)) * 128 + xq * 16;  // bytes, + 1 KiB per block
 
@@ -2780,7 +2828,7 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
     // buffer and the loads after it
     struct DmaPlan {
       i32x4_t drs, xrs;
-      int doff[2];
+      int doff[kDyPer];
       const uint16_t* buf;
     };
     auto plan = [&](int tl) {
@@ -2794,7 +2842,7 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
       const int64_t rem = a.m_total - int64_t(kt) * kW5Kt;  // rows of this k-tile before the end
       const int base = int((uint32_t(kt) * uint32_t(kW5Kt)) % uint32_t(a.wp));
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < kDyPer; ++i) {
         // data column of the centre row p + wp + 1 (row position jc + 1, wrapping to the
         // next row's position 0); a strip's halo columns are masked
         int jc = base + drmod[i];
@@ -2811,13 +2859,18 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
     };
     auto issue_dy = [&](const DmaPlan& p) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) lds_dma16(p.drs, p.buf + (2 * wave + i) * 512, p.doff[i]);
+      for (int i = 0; i < kDyPer; ++i) lds_dma16(p.drs, p.buf + (kDyPer * wave + i) * 512, p.doff[i]);
     };
     auto issue_x = [&](const DmaPlan& p) {
       const uint16_t* xl = p.buf + kW5Kt * 128 + xb0 * 512;
-      lds_dma16(p.xrs, xl, xoff0);
-      lds_dma16(p.xrs, xl + 512, xoff0 + 1024);
-      if (wave < 4) lds_dma16(p.xrs, xl + 1024, xoff0 + 2048);
+      if constexpr (NW == 4) {
+#pragma unroll
+        for (int i = 0; i < kXPer; ++i) lds_dma16(p.xrs, xl + i * 512, xoff0 + i * 1024);
+      } else {
+        lds_dma16(p.xrs, xl, xoff0);
+        lds_dma16(p.xrs, xl + 512, xoff0 + 1024);
+        if (wave < 4) lds_dma16(p.xrs, xl + 1024, xoff0 + 2048);
+      }
     };
     auto load = [&](int tl) {
       const DmaPlan p = plan(tl);
@@ -2828,7 +2881,9 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
     // in flight
     auto wait_tiles = [&](auto n_tag) {
       constexpr int n = decltype(n_tag)::value;
-      if (wave < 4)
+      if constexpr (NW == 4)
+        lds_dma_wait<(kDyPer + kXPer) * n>();
+      else if (wave < 4)
         lds_dma_wait<kW5LoadsHi * n>();
       else
         lds_dma_wait<kW5LoadsLo * n>();
@@ -2987,6 +3042,7 @@ std::atomic<int> g_wgrad_rows_form{[] {
 struct WgRowsPlan {
   ConvGeom geom;
   int form = 1;      // 1: wgrad_rows_kernel, 2: wgrad_rows5_kernel
+  int co_tile = 128; // output channels per workgroup tile (form 2: 128 eight waves, 64 four)
   int kt_rows = 64;  // output rows per k-tile
   int ci_chunks = 0, co_chunks = 0, ci_pad = 0, co_pad = 0;
   int ktiles = 0, splits = 0, kt_per = 0;
@@ -2996,6 +3052,9 @@ struct WgRowsPlan {
 // split count of the rows weight gradient: 0 (default) the model below, else forced
 // (xdna_conv3x3_set_wgrad_splits, for measurements)
 std::atomic<int> g_wgrad_splits{0};
+// output-channel tile of the rows weight gradient's form 2: 0 (by layer), 64 or 128
+// (xdna_conv3x3_set_wgrad_tile)
+std::atomic<int> g_wgrad_tile{0};
 
 WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   WgRowsPlan p;
@@ -3003,11 +3062,23 @@ WgRowsPlan wgrad_rows_plan(int B, int Cin, int Cout, int H, int W, int layout) {
   p.ci_chunks = int(ceil_div(Cin, kKStep));
   p.co_chunks = int(ceil_div(Cout, kKStep));
   p.ci_pad = p.ci_chunks * kKStep;
-  p.co_pad = int(ceil_div(Cout, kTCo) * kTCo);
   p.form = g_wgrad_rows_form.load();
+  {
+    // form 2's tile (xdna_conv3x3_set_wgrad_tile forces one): four waves on 64 output
+    // channels for layers of up to 64 output channels and for layers of up to 256 channels
+    // each side and 40 GFLOP (measured on the 36 sweep shapes, each tile at its modelled
+    // split count: 3-19 % less time there, 1.05-2.5x more on the larger and the
+    // 512-channel layers, where one wave per SIMD leaves the latency uncovered); else
+    // eight waves on 128
+    const int t = g_wgrad_tile.load();
+    const double gflop = 2.0 * 9.0 * double(B) * H * W * double(Cin) * double(Cout) * 1e-9;
+    const bool small = Cout <= 64 || (Cout <= 256 && Cin <= 256 && gflop <= 40.0);
+    p.co_tile = p.form == 2 && (t == 64 || (t == 0 && small)) ? 64 : kTCo;
+  }
+  p.co_pad = int(ceil_div(Cout, p.co_tile) * p.co_tile);
   p.kt_rows = p.form == 2 ? kW5Kt : g_wgrad_rows_kt.load() == 128 ? 128 : 64;
   p.ktiles = int(ceil_div(p.geom.m_total, p.kt_rows));
-  const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / kTCo);
+  const int64_t tiles = int64_t(p.ci_pad / 64) * (p.co_pad / p.co_tile);
   const int64_t out_elems = int64_t(p.co_pad) * 9 * p.ci_pad;
   // split count: the channel-major path's model (rounds of 256 workgroups x per-CU rate,
   // plus the write and read of the fp32 partials)
@@ -3228,7 +3299,9 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows_kernel<128>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows5_kernel),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows5_kernel<8>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_rows5_kernel<4>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxWgradLds)) == hipSuccess;
   if (!lds_attr || p.lds_bytes > kMaxWgradLds) {
     (void)hipGetLastError();
@@ -3253,7 +3326,7 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
   a.ktiles = p.ktiles;
   a.kt_per_split = p.kt_per;
   a.splits = p.splits;
-  a.nco_t = p.co_pad / kTCo;
+  a.nco_t = p.co_pad / p.co_tile;
   a.ntiles = a.nco_t * (p.ci_pad / 64);
   const int64_t nblocks = ceil_div(p.splits, kXcds) * kXcds * int64_t(a.ntiles);
   if (nblocks > int64_t(0x7fffffff)) {
@@ -3261,8 +3334,10 @@ int xdna_conv3x3_wgrad_rows_bf16(const uint16_t* xp, const uint16_t* dp, uint16_
     return -1;
   }
   hipStream_t st = as_stream(stream);
-  if (p.form == 2)
-    wgrad_rows5_kernel<<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
+  if (p.form == 2 && p.co_tile == 64)
+    wgrad_rows5_kernel<4><<<unsigned(nblocks), 256, p.lds_bytes, st>>>(a);
+  else if (p.form == 2)
+    wgrad_rows5_kernel<8><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
   else if (p.kt_rows == 128)
     wgrad_rows_kernel<128><<<unsigned(nblocks), 512, p.lds_bytes, st>>>(a);
   else
@@ -3410,6 +3485,15 @@ int xdna_conv3x3_prepare_weights_multi_bf16(int n, const uint16_t* const* w, uin
       return -1;
     }
   return launch_prep_multi(n, w, wt, wtd, cout, cin, stream);
+}
+
+int xdna_conv3x3_set_wgrad_tile(int co_tile) {
+  if (co_tile != 0 && co_tile != 64 && co_tile != 128) {
+    set_error("xdna_conv3x3_set_wgrad_tile: 0 (by layer), 64 or 128 output channels");
+    return -1;
+  }
+  g_wgrad_tile.store(co_tile);
+  return 0;
 }
 
 int xdna_conv3x3_set_wgrad_splits(int splits) {

@@ -134,6 +134,7 @@ SIGNATURES = {
     "xdna_conv3x3_set_prep_tile": (I, [I]),
     "xdna_conv3x3_prepare_weights_multi_bf16": (I, [I, P, P, P, P, P, P]),
     "xdna_conv3x3_set_wgrad_splits": (I, [I]),
+    "xdna_conv3x3_set_wgrad_tile": (I, [I]),
     "xdna_gemm_bf16": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_gemm_bf16_noalloc": (I, [P, P, P, P, I, I, I, I, L, L, L, L, L, L, L, L, L, I, L, L, F, F, P]),
     "xdna_batch_norm_fwd_bf16": (I, [P, P, P, I, P, P, P, L, L, L, D, P]),

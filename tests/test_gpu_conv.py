@@ -170,14 +170,18 @@ def test_forward_tight_layout(hip, shape, variant):
     check_bf16(host(y), oracle.conv3x3_fwd(x, w, b), what=f"fwd tight {shape}")
 
 
-@pytest.fixture(params=[(1, 128), (1, 64), (2, 64)], ids=lambda p: f"form{p[0]}-kt{p[1]}")
+@pytest.fixture(params=[(1, 128, 0), (1, 64, 0), (2, 64, 0), (2, 64, 64), (2, 64, 128)],
+                ids=lambda p: f"form{p[0]}-kt{p[1]}-tile{p[2]}")
 def wgrad_kt(hip, request):
     """Kernel form of the rows weight gradient (1: register-staged k-tiles of 128 or 64
-    rows, 2: 64-row k-tiles loaded straight into LDS) and its k-tile rows."""
-    form, kt = request.param
+    rows, 2: 64-row k-tiles loaded straight into LDS, its output-channel tile by layer (0),
+    or forced to 64 (four waves) or 128 (eight waves)) and its k-tile rows."""
+    form, kt, tile = request.param
     assert hip.xdna_conv3x3_set_wgrad_rows_kernel(form) == 0
     assert hip.xdna_conv3x3_set_wgrad_rows_kt(kt) == 0
+    assert hip.xdna_conv3x3_set_wgrad_tile(tile) == 0
     yield kt
+    assert hip.xdna_conv3x3_set_wgrad_tile(0) == 0
     assert hip.xdna_conv3x3_set_wgrad_rows_kt(0) == 0
     assert hip.xdna_conv3x3_set_wgrad_rows_kernel(0) == 0
 
@@ -216,6 +220,8 @@ def test_wgrad_rows_kt_setter_rejects(hip):
     assert hip.xdna_conv3x3_set_wgrad_rows_kt(0) == 0
     assert hip.xdna_conv3x3_set_wgrad_rows_kernel(3) == -1
     assert hip.xdna_conv3x3_set_wgrad_rows_kernel(0) == 0
+    assert hip.xdna_conv3x3_set_wgrad_tile(96) == -1
+    assert hip.xdna_conv3x3_set_wgrad_tile(0) == 0
 
 
 def test_workspace_too_small_is_an_error(hip):
