@@ -41,6 +41,11 @@ __device__ inline void param_put(void* p, int wd, int64_t c, float v) {
   else static_cast<float*>(p)[c] = v;
 }
 
+// The element loops below take each lane's elements l, l + 64, l + 128, ... of a plane in
+// that order, as a plain strided loop would, four loads ahead (kU): the same fp32 sums, bit
+// for bit, with the loads of four elements in flight instead of one.
+constexpr int kU = 4;
+
 // Parameters are indexed by channel % pC: pC = C for batch norm, the per-image channel
 // count for instance norm (whose B*C "channels" share C weights; no repeated copies).
 __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
@@ -54,15 +59,29 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
   float s = 0.f;
   for (int64_t n = 0; n < N; ++n) {
     const uint16_t* xp = x + (n * C + c) * L;
-    for (int64_t l = lane; l < L; l += 64) s += bf16_to_f32(xp[l]);
+    for (int64_t l0 = lane; l0 < L; l0 += 64 * kU) {
+      float v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = l0 + 64 * u < L ? bf16_to_f32(xp[l0 + 64 * u]) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (l0 + 64 * u < L) s += v[u];
+    }
   }
   const float mean = wave_sum(s) / float(cnt);
   float q = 0.f;
   for (int64_t n = 0; n < N; ++n) {
     const uint16_t* xp = x + (n * C + c) * L;
-    for (int64_t l = lane; l < L; l += 64) {
-      const float d = bf16_to_f32(xp[l]) - mean;
-      q += d * d;
+    for (int64_t l0 = lane; l0 < L; l0 += 64 * kU) {
+      float v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = l0 + 64 * u < L ? bf16_to_f32(xp[l0 + 64 * u]) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (l0 + 64 * u < L) {
+          const float d = v[u] - mean;
+          q += d * d;
+        }
     }
   }
   const float var = wave_sum(q) / float(cnt);
@@ -76,8 +95,58 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_fwd_kernel(
   for (int64_t n = 0; n < N; ++n) {
     const uint16_t* xp = x + (n * C + c) * L;
     uint16_t* yp = y + (n * C + c) * L;
-    for (int64_t l = lane; l < L; l += 64)
-      yp[l] = f32_to_bf16(act_forward(act, slope, fmaf(bf16_to_f32(xp[l]), scale, shift)));
+    for (int64_t l0 = lane; l0 < L; l0 += 64 * kU) {
+      float v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = l0 + 64 * u < L ? bf16_to_f32(xp[l0 + 64 * u]) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (l0 + 64 * u < L) yp[l0 + 64 * u] = f32_to_bf16(act_forward(act, slope, fmaf(v[u], scale, shift)));
+    }
+  }
+}
+
+// One plane's backward (elements [o, o + L)): its sums of g and g * (x - mean), where g is
+// dy through the activation (from its output yact), then, with dx set, dx from them.
+__device__ inline void plane_bwd_sums(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x,
+                                      const uint16_t* __restrict__ yact, int act, float slope, int64_t o,
+                                      int64_t L, float mean, int lane, float& sdy, float& sdot) {
+  for (int64_t l0 = lane; l0 < L; l0 += 64 * kU) {
+    float g[kU], xv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t l = l0 + 64 * u;
+      const bool ok = l < L;
+      const float d = ok ? bf16_to_f32(dy[o + l]) : 0.f;
+      g[u] = ok && act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), d) : d;
+      xv[u] = ok ? bf16_to_f32(x[o + l]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (l0 + 64 * u < L) {
+        sdy += g[u];
+        sdot += g[u] * (xv[u] - mean);
+      }
+  }
+}
+
+__device__ inline void plane_bwd_dx(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x,
+                                    const uint16_t* __restrict__ yact, int act, float slope, int64_t o, int64_t L,
+                                    float mean, float gmean, float proj, float gscale, int lane,
+                                    uint16_t* __restrict__ dx) {
+  for (int64_t l0 = lane; l0 < L; l0 += 64 * kU) {
+    float g[kU], xm[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t l = l0 + 64 * u;
+      const bool ok = l < L;
+      const float d = ok ? bf16_to_f32(dy[o + l]) : 0.f;
+      g[u] = ok && act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), d) : d;
+      xm[u] = (ok ? bf16_to_f32(x[o + l]) : 0.f) - mean;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (l0 + 64 * u < L) dx[o + l0 + 64 * u] = f32_to_bf16((g[u] - gmean - xm[u] * proj) * gscale);
   }
 }
 
@@ -95,15 +164,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
   if (c >= C) return;
   const float mean = mean_in[c], invstd = invstd_in[c];
   float sdy = 0.f, sdot = 0.f;
-  for (int64_t n = 0; n < N; ++n) {
-    const int64_t o = (n * C + c) * L;
-    for (int64_t l = lane; l < L; l += 64) {
-      const float g = act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), bf16_to_f32(dy[o + l]))
-                          : bf16_to_f32(dy[o + l]);
-      sdy += g;
-      sdot += g * (bf16_to_f32(x[o + l]) - mean);
-    }
-  }
+  for (int64_t n = 0; n < N; ++n) plane_bwd_sums(dy, x, yact, act, slope, (n * C + c) * L, L, mean, lane, sdy, sdot);
   sdy = wave_sum(sdy);
   sdot = wave_sum(sdot);
   if (lane == 0) {
@@ -120,15 +181,106 @@ __global__ __launch_bounds__(64 * kNormWaves) void bn_bwd_kernel(
   const float gmean = sdy * inv_cnt;
   const float proj = sdot * inv_cnt * invstd * invstd;
   const float gscale = invstd * param_at(w, wd, c % pC, 1.f);
-  for (int64_t n = 0; n < N; ++n) {
-    const int64_t o = (n * C + c) * L;
-    for (int64_t l = lane; l < L; l += 64) {
-      const float xm = bf16_to_f32(x[o + l]) - mean;
-      const float g = act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), bf16_to_f32(dy[o + l]))
-                          : bf16_to_f32(dy[o + l]);
-      dx[o + l] = f32_to_bf16((g - gmean - xm * proj) * gscale);
+  for (int64_t n = 0; n < N; ++n)
+    plane_bwd_dx(dy, x, yact, act, slope, (n * C + c) * L, L, mean, gmean, proj, gscale, lane, dx);
+}
+
+// Instance norm on planes of up to 64 NV elements held in registers (lane l: elements
+// l + 64 i, i < NV), so each plane is read once, all its loads issued together.  The sums
+// run over each lane's elements in the loops' order above and then the same lane sum, so
+// the results are those kernels', bit for bit.
+//
+// Forward: a wave per plane, four planes per workgroup (bn_fwd_kernel with N = 1).
+template <int NV>
+__global__ __launch_bounds__(64 * kNormWaves) void in_fwd_regs_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const void* __restrict__ b, int wd,
+    uint16_t* __restrict__ y, float* __restrict__ save_mean, float* __restrict__ save_invstd, int64_t P,
+    int L, float eps, int64_t pC, int act, float slope) {
+  const int lane = threadIdx.x & 63;
+  const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+  if (c >= P) return;
+  const uint16_t* xp = x + c * L;
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = lane + 64 * i < L ? bf16_to_f32(xp[lane + 64 * i]) : 0.f;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < L) s += v[i];
+  const float mean = wave_sum(s) / float(L);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < L) {
+      const float d = v[i] - mean;
+      q += d * d;
     }
+  const float var = wave_sum(q) / float(L);
+  const float invstd = 1.0f / sqrtf(var + eps);
+  if (lane == 0) {
+    save_mean[c] = mean;
+    save_invstd[c] = invstd;
   }
+  const float scale = param_at(w, wd, c % pC, 1.f) * invstd;
+  const float shift = param_at(b, wd, c % pC, 0.f) - mean * scale;
+  uint16_t* yp = y + c * L;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < L) yp[lane + 64 * i] = f32_to_bf16(act_forward(act, slope, fmaf(v[i], scale, shift)));
+}
+
+// Backward: a wave per plane, four planes per workgroup (bn_bwd_kernel with N = 1), the
+// plane's dy, x (and the activation's output) in registers; each plane's dw / db terms go
+// to pw / pb for norm_param_reduce_kernel's fixed-order sum over the images (pw null: not
+// written).
+template <int NV>
+__global__ __launch_bounds__(64 * kNormWaves) void in_bwd_regs_kernel(
+    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const void* __restrict__ w, int wd,
+    const float* __restrict__ mean_in, const float* __restrict__ invstd_in, uint16_t* __restrict__ dx, int64_t P,
+    int L, int64_t pC, float* __restrict__ pw, float* __restrict__ pb, const uint16_t* __restrict__ yact, int act,
+    float slope) {
+  const int lane = threadIdx.x & 63;
+  const int64_t c = int64_t(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
+  if (c >= P) return;
+  const int64_t o = c * L;
+  float g[NV], xv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int l = lane + 64 * i;
+    const bool ok = l < L;
+    const float d = ok ? bf16_to_f32(dy[o + l]) : 0.f;
+    g[i] = ok && act ? act_backward(act, slope, bf16_to_f32(yact[o + l]), d) : d;
+    xv[i] = ok ? bf16_to_f32(x[o + l]) : 0.f;
+  }
+  const float mean = mean_in[c], invstd = invstd_in[c];
+  float sdy = 0.f, sdot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < L) {
+      sdy += g[i];
+      sdot += g[i] * (xv[i] - mean);
+    }
+  sdy = wave_sum(sdy);
+  sdot = wave_sum(sdot);
+  if (pw && lane == 0) {
+    pw[c] = sdot * invstd;
+    pb[c] = sdy;
+  }
+  if (!dx) return;
+  const float inv_cnt = 1.0f / float(L);
+  const float gmean = sdy * inv_cnt;
+  const float proj = sdot * inv_cnt * invstd * invstd;
+  const float gscale = invstd * param_at(w, wd, c % pC, 1.f);
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < L) dx[o + lane + 64 * i] = f32_to_bf16((g[i] - gmean - (xv[i] - mean) * proj) * gscale);
+}
+
+// per-lane register count of a plane of L elements (power of two), 0 past 2048 elements
+inline int in_regs_nv(int64_t L) {
+  for (int nv = 1; nv <= 32; nv *= 2)
+    if (L <= 64 * nv) return nv;
+  return 0;
 }
 
 // dw[c] = sum_b pw[b*C + c], db likewise, stored in dtype wd: one wave per parameter,
@@ -219,8 +371,20 @@ int xdna_instance_norm_act_fwd_bf16(const uint16_t* x, const void* weight, const
     return -1;
   }
   if (!admit_launch("instance_norm fwd")) return -1;
-  bn_fwd_kernel<<<dim3(unsigned(ceil_div(ch, kNormWaves))), 64 * kNormWaves, 0, as_stream(stream)>>>(
-      x, weight, bias, param_dtype, y, save_mean, save_invstd, 1, ch, L, float(eps), C, act, slope);
+  const dim3 grid(unsigned(ceil_div(ch, kNormWaves)));
+  hipStream_t st = as_stream(stream);
+  switch (in_regs_nv(L)) {
+#define XDNA_INF(nv_)                                                                                  \
+  case nv_:                                                                                          \
+    in_fwd_regs_kernel<nv_><<<grid, 64 * kNormWaves, 0, st>>>(x, weight, bias, param_dtype, y, save_mean, \
+                                                               save_invstd, ch, int(L), float(eps), C, act, slope); \
+    break;
+    XDNA_INF(1) XDNA_INF(2) XDNA_INF(4) XDNA_INF(8) XDNA_INF(16) XDNA_INF(32)
+#undef XDNA_INF
+    default:
+      bn_fwd_kernel<<<grid, 64 * kNormWaves, 0, st>>>(x, weight, bias, param_dtype, y, save_mean, save_invstd, 1,
+                                                      ch, L, float(eps), C, act, slope);
+  }
   return check_launch("instance_norm fwd");
 }
 
@@ -252,15 +416,26 @@ int xdna_instance_norm_act_bwd_bf16(const uint16_t* dy, const uint16_t* x, const
     return -1;
   }
   if (!admit_launch("instance_norm bwd")) return -1;
+  hipStream_t st = as_stream(stream);
   float* part = nullptr;
   if (params) {
     part = static_cast<float*>(xdna_hip_cache_alloc(size_t(2 * ch) * sizeof(float)));
     if (!part) return -1;
   }
-  hipStream_t st = as_stream(stream);
-  bn_bwd_kernel<<<dim3(unsigned(ceil_div(ch, kNormWaves))), 64 * kNormWaves, 0, st>>>(
-      dy, x, weight, param_dtype, save_mean, save_invstd, dx, nullptr, nullptr, 1, ch, L, C, part,
-      part ? part + ch : nullptr, y, act, slope);
+  const dim3 grid(unsigned(ceil_div(ch, kNormWaves)));
+  float* const pw = part, *const pb = part ? part + ch : nullptr;
+  switch (in_regs_nv(L)) {
+#define XDNA_INB(nv_)                                                                                            \
+  case nv_:                                                                                                    \
+    in_bwd_regs_kernel<nv_><<<grid, 64 * kNormWaves, 0, st>>>(dy, x, weight, param_dtype, save_mean, save_invstd, \
+                                                               dx, ch, int(L), C, pw, pb, y, act, slope);         \
+    break;
+    XDNA_INB(1) XDNA_INB(2) XDNA_INB(4) XDNA_INB(8) XDNA_INB(16) XDNA_INB(32)
+#undef XDNA_INB
+    default:
+      bn_bwd_kernel<<<grid, 64 * kNormWaves, 0, st>>>(dy, x, weight, param_dtype, save_mean, save_invstd, dx,
+                                                      nullptr, nullptr, 1, ch, L, C, pw, pb, y, act, slope);
+  }
   if (params) {
     norm_param_reduce_kernel<<<dim3(unsigned(ceil_div(C, kNormWaves))), 64 * kNormWaves, 0, st>>>(
         part, part + ch, dweight, dbias, param_dtype, B, C);

@@ -239,3 +239,69 @@ def test_batch_norm_training_matches_fp64(shape, track):
             rv = ref.numpy()
             tol = oracle.bf16_ulp(rv) + 1e-7
             assert (np.abs(gv - rv) <= tol).all(), (name, np.abs(gv - rv).max())
+
+
+def _lane_sum_f32(terms):
+    """A 64-lane wave's sum of per-image terms as the kernels form it: lane l adds images
+    l, l + 64, ... in order, then the lanes' butterfly (xor 32, 16, ..., 1), in float32."""
+    t = np.zeros(64, np.float32)
+    for b, v in enumerate(np.asarray(terms, np.float32)):
+        t[b % 64] = np.float32(t[b % 64] + v)
+    for o in (32, 16, 8, 4, 2, 1):
+        t = (t + t[np.arange(64) ^ o]).astype(np.float32)
+    return t[0]
+
+
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("B,C,L", [(40, 16, 81), (3, 8, 1296), (70, 4, 5), (2, 3, 2048)])
+def test_instance_norm_register_planes_match_loop_kernels(hip, act, B, C, L):
+    """The instance-norm kernels that hold a plane in registers (planes up to 2048 elements)
+    against the batch-norm kernels' loop form on the same planes (batch norm over
+    [1, B*C, L], the weight repeated per plane, fp32 parameters): y, the saved statistics
+    and dx bit for bit, with the activation's mask applied to dy for the batch-norm side;
+    dweight / dbias equal to the batch-norm per-plane terms summed in the kernels' order."""
+    from gpu_util import stream
+    g = torch.Generator().manual_seed(B * L + act)
+    x = (torch.randn(B, C, L, generator=g) * 2 + 0.3).bfloat16().cuda()
+    dy = torch.randn(B, C, L, generator=g).bfloat16().cuda()
+    w = (torch.rand(C, generator=g) + 0.5).bfloat16().cuda()
+    b = (torch.randn(C, generator=g) * 0.1).bfloat16().cuda()
+    P = B * C
+    y = torch.empty_like(x)
+    mean, inv = torch.empty(P, device="cuda"), torch.empty(P, device="cuda")
+    assert hip.xdna_instance_norm_act_fwd_bf16(x.data_ptr(), w.data_ptr(), b.data_ptr(), 1, y.data_ptr(),
+                                               mean.data_ptr(), inv.data_ptr(), B, C, L, 1e-5, act, 0.0,
+                                               stream()) == 0
+    dx = torch.empty_like(x)
+    dw = torch.empty(C, dtype=torch.bfloat16, device="cuda")
+    db = torch.empty(C, dtype=torch.bfloat16, device="cuda")
+    assert hip.xdna_instance_norm_act_bwd_bf16(dy.data_ptr(), x.data_ptr(), y.data_ptr(), w.data_ptr(), 1,
+                                               mean.data_ptr(), inv.data_ptr(), dx.data_ptr(), dw.data_ptr(),
+                                               db.data_ptr(), B, C, L, act, 0.0, stream()) == 0
+    # the loop kernels: batch norm over the planes
+    wp = w.float().repeat(B).contiguous()
+    bp = b.float().repeat(B).contiguous()
+    y2 = torch.empty_like(x)
+    mean2, inv2 = torch.empty(P, device="cuda"), torch.empty(P, device="cuda")
+    assert hip.xdna_batch_norm_fwd_bf16(x.data_ptr(), wp.data_ptr(), bp.data_ptr(), 2, y2.data_ptr(),
+                                        mean2.data_ptr(), inv2.data_ptr(), 1, P, L, 1e-5, stream()) == 0
+    torch.cuda.synchronize()
+    if act:
+        y2 = torch.where(y2.float() <= 0, torch.zeros_like(y2), y2)
+    dy2 = torch.where(y.float() <= 0, torch.zeros_like(dy), dy) if act else dy
+    dx2 = torch.empty_like(x)
+    dw2 = torch.empty(P, device="cuda")
+    db2 = torch.empty(P, device="cuda")
+    assert hip.xdna_batch_norm_bwd_bf16(dy2.data_ptr(), x.data_ptr(), wp.data_ptr(), 2, mean2.data_ptr(),
+                                        inv2.data_ptr(), dx2.data_ptr(), dw2.data_ptr(), db2.data_ptr(), 1, P, L,
+                                        stream()) == 0
+    torch.cuda.synchronize()
+    for got, want, name in ((y, y2, "y"), (dx, dx2, "dx")):
+        assert torch.equal(got.view(torch.int16), want.contiguous().view(torch.int16)), name
+    assert torch.equal(mean, mean2) and torch.equal(inv, inv2), "statistics"
+    tw = dw2.view(B, C).cpu().numpy()
+    tb = db2.view(B, C).cpu().numpy()
+    want_w = torch.tensor([_lane_sum_f32(tw[:, c]) for c in range(C)]).bfloat16()
+    want_b = torch.tensor([_lane_sum_f32(tb[:, c]) for c in range(C)]).bfloat16()
+    assert torch.equal(dw.cpu().view(torch.int16), want_w.view(torch.int16)), "dweight"
+    assert torch.equal(db.cpu().view(torch.int16), want_b.view(torch.int16)), "dbias"
