@@ -736,6 +736,16 @@ int xdna_mse_loss(const void* a, const void* b, int dtype, int64_t n, int64_t pe
 int xdna_mse_loss_bwd(const void* go, int go_dtype, const void* a, const void* b, int dtype, int64_t n,
                       int64_t period, int reduction, void* grad, void* stream);
 
+/* Column sums of a row-major [R][N] bf16 matrix, out[n] = bf16(fp32 sum over rows), in a
+ * fixed order (row slices summed in order, then the slices in order: equal inputs give equal
+ * bits).  The bias gradient of a Linear layer (aten::sum over dim 0 of addmm's output
+ * gradient), which the reference reaches through its zero-copy CPU fallback
+ * (torch_xdna_device.cpp:5124-5260).  The workspace (16-byte aligned) holds the fp32 row
+ * slices' partial sums; 0 bytes when one slice suffices. */
+size_t xdna_colsum_workspace_bytes(const uint16_t* x, int64_t R, int64_t N);
+int xdna_colsum_bf16(const uint16_t* x, uint16_t* out, int64_t R, int64_t N, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

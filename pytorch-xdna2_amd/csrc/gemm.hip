@@ -714,6 +714,60 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs g) {
   }
 }
 
+// The same epilogue four outputs at a time, for C rows of unit column stride and N % 4 == 0
+// (8-byte-aligned C rows, 16-byte-aligned partials) and fewer than 2^31 groups of four: one
+// 16-byte partial load per split and one 8-byte store per thread, 32-bit index math.  Each
+// output is the scalar form's sum in the same split order, with the same alpha, bias and
+// rounding, so the bits are the same.
+__global__ __launch_bounds__(256) void gemm_reduce4_kernel(GemmArgs g) {
+  const int n4 = g.N >> 2;
+  const int rows = g.M * g.batch;  // (b, m) pairs, b-major
+  const int64_t n_all = int64_t(g.M) * g.N * g.batch;
+  const int total = rows * n4;
+  const float4* part = reinterpret_cast<const float4*>(g.part);
+  const int64_t zs = n_all >> 2;  // float4 stride of one split
+  for (int i = int(blockIdx.x) * 256 + int(threadIdx.x); i < total; i += int(gridDim.x) * 256) {
+    const int row = i / n4, q = i - row * n4;
+    const int b = row / g.M, m = row - b * g.M;
+    const int n = q << 2;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < g.nsplit; ++z) {
+      const float4 v = part[int64_t(z) * zs + i];
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    float o[4] = {g.alpha * acc.x, g.alpha * acc.y, g.alpha * acc.z, g.alpha * acc.w};
+    if (g.bias_mode && g.beta != 0.0f) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float bv;
+        if (g.bias_mode == 1) bv = bf16_to_f32(g.bias[int64_t(n + e) * g.bias_sn]);
+        else if (g.bias_mode == 2) bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm + int64_t(n + e) * g.bias_sn]);
+        else bv = bf16_to_f32(g.bias[int64_t(m) * g.bias_sm]);
+        o[e] += g.beta * bv;
+      }
+    }
+    const uint2 packed = make_uint2(uint32_t(f32_to_bf16(o[0])) | (uint32_t(f32_to_bf16(o[1])) << 16),
+                                    uint32_t(f32_to_bf16(o[2])) | (uint32_t(f32_to_bf16(o[3])) << 16));
+    *reinterpret_cast<uint2*>(g.c + int64_t(b) * g.c_batch + int64_t(m) * g.c_m + n) = packed;
+  }
+}
+
+// The split-K epilogue launch: the four-wide form where its conditions hold.
+void launch_gemm_reduce(const GemmArgs& g, hipStream_t st) {
+  const int64_t n_all = int64_t(g.batch) * g.M * g.N;
+  const bool vec = g.c_n == 1 && (g.N % 4) == 0 && (reinterpret_cast<uintptr_t>(g.c) & 7) == 0 &&
+                   (g.c_m % 4) == 0 && (g.batch <= 1 || (g.c_batch % 4) == 0) && n_all / 4 < (int64_t(1) << 31) &&
+                   int64_t(g.M) * g.batch < (int64_t(1) << 31);
+  if (vec) {
+    gemm_reduce4_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all / 4, 256), 8192)), 256, 0, st>>>(g);
+    return;
+  }
+  gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st>>>(g);
+}
+
 // Operand described as [rows][k] with element strides (s_r, s_k).
 int stage_mode(const void* base, int64_t s_r, int64_t s_k, int64_t s_batch, int batch) {
   const bool a16 = (reinterpret_cast<uintptr_t>(base) & 15) == 0;
@@ -1514,8 +1568,7 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
     else if (ma == kAlongRow) launch_small_b<kAlongRow>(mb, grid, sts, g);
     else launch_small_b<kScalar>(mb, grid, sts, g);
     if (g.nsplit > 1) {
-      const int64_t n_all = int64_t(batch) * M * N;
-      gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, sts>>>(g);
+      launch_gemm_reduce(g, sts);
       src.give_back(g.part);  // stream-ordered reuse: the next user of the block runs after the reduce
     }
     return check_launch(src.who);
@@ -1589,8 +1642,7 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
       return -1;
     }
     if (g.nsplit > 1) {
-      const int64_t n_all = int64_t(batch) * M * N;
-      gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st2>>>(g);
+      launch_gemm_reduce(g, st2);
       src.give_back(g.part);
     }
     return check_launch(src.who);
@@ -1618,8 +1670,7 @@ int gemm_run(const PartialsSource& src, const uint16_t* A, const uint16_t* Bm, u
   else if (ma == kAlongRow) launch_b<kAlongRow>(mb, grid, st, g);
   else launch_b<kScalar>(mb, grid, st, g);
   if (g.nsplit > 1) {
-    const int64_t n_all = int64_t(batch) * M * N;
-    gemm_reduce_kernel<<<unsigned(std::min<int64_t>(ceil_div(n_all, 256), 4096)), 256, 0, st>>>(g);
+    launch_gemm_reduce(g, st);
     src.give_back(g.part);
   }
   return check_launch(src.who);

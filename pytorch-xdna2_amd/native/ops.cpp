@@ -2042,6 +2042,32 @@ at::Tensor mse_loss_backward_xdna(const at::Tensor& grad_output, const at::Tenso
   return back(at::_ops::mse_loss_backward::call(rocm(grad_output), rocm(self), rocm(target), reduction));
 }
 
+// Sum over the rows of a 2-D bf16 tensor (dim 0, the form autograd's sum_to takes for a
+// Linear bias gradient): the fixed-order column sums of xdna_colsum_bf16.  Every other sum
+// keeps PyTorch-ROCm's kernel through the aliases.
+at::Tensor sum_dim_xdna(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
+                        std::optional<at::ScalarType> dtype) {
+  const bool rows = dim.has_value() && dim->size() == 1 && ((*dim)[0] == 0 || (*dim)[0] == -2);
+  if (g_mode.load() >= 1 && rows && self.dim() == 2 && self.scalar_type() == at::kBFloat16 &&
+      (!dtype || *dtype == at::kBFloat16) && self.device().type() == kXdna && self.size(0) >= 1 &&
+      self.size(1) >= 1) {
+    ScopedCount sc("hip_colsum.run");
+    const at::Tensor x = self.contiguous();
+    const int64_t R = x.size(0), N = x.size(1);
+    at::Tensor out = keepdim ? empty_xdna({1, N}, at::kBFloat16) : empty_xdna({N}, at::kBFloat16);
+    const uint16_t* xp = static_cast<const uint16_t*>(x.const_data_ptr());
+    const size_t wb = xdna_colsum_workspace_bytes(xp, R, N);
+    at::Tensor ws = wb ? alloc_bytes(wb) : at::Tensor();
+    check_abi(xdna_colsum_bf16(xp, static_cast<uint16_t*>(out.data_ptr()), R, N, wb ? ws.data_ptr() : nullptr, wb,
+                               current_stream()),
+              "sum over rows");
+    return out;
+  }
+  ScopedCount sc("aten::sum.rocm");
+  BelowAutograd g;
+  return back(at::_ops::sum_dim_IntList::call(rocm(self), dim, keepdim, dtype));
+}
+
 // 2x2 / stride-2 max-pool (floor mode) of bf16 NCHW tensors as its own autograd node: the
 // forward writes the pooled values only (no int64 indices), the backward routes each
 // window's gradient to the window's maximum recomputed from the saved input (PyTorch's
@@ -2119,6 +2145,7 @@ void register_hot_ops(torch::Library& m) {
   m.impl("upsample_nearest2d_backward", TORCH_FN(upsample_nearest2d_backward_xdna));
   m.impl("mse_loss", TORCH_FN(mse_loss_xdna));
   m.impl("mse_loss_backward", TORCH_FN(mse_loss_backward_xdna));
+  m.impl("sum.dim_IntList", TORCH_FN(sum_dim_xdna));
 }
 
 // ---------------------------------------------------------------------------------------

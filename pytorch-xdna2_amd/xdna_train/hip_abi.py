@@ -126,6 +126,8 @@ SIGNATURES = {
     "xdna_mse_loss_workspace_bytes": (Z, [L]),
     "xdna_mse_loss": (I, [P, P, I, L, L, I, P, P, Z, P]),
     "xdna_mse_loss_bwd": (I, [P, I, P, P, I, L, L, I, P, P]),
+    "xdna_colsum_workspace_bytes": (Z, [P, L, L]),
+    "xdna_colsum_bf16": (I, [P, P, L, L, P, Z, P]),
     "xdna_conv3x3_wgrad_pack_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_conv3x3_wgrad_packed_bf16": (I, [P, P, I, I, I, I, I, P, Z, P]),
     "xdna_gemm_set_variant": (I, [I]),
