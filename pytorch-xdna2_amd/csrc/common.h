@@ -114,6 +114,25 @@ __device__ inline uint16_t f32_to_bf16(float f) {
   return f != f ? uint16_t(0x7FC0) : h;
 }
 
+// Split-K partial sums: init + src[z * stride] + src[(z + step) * stride] + ... over
+// indices below n, added left to right in that order (the fixed association every
+// deterministic reduce here keeps), with eight loads issued before their sums: a loop of
+// single loads waits one memory latency per term.
+__device__ inline float sum_strided8(float init, const float* __restrict__ src, int64_t stride, int z, int step,
+                                     int n) {
+  float s = init;
+  int k = z;
+  for (; k + 7 * step < n; k += 8 * step) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[int64_t(k + u * step) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; k < n; k += step) s += src[int64_t(k) * stride];
+  return s;
+}
+
 // ---- activations fused into producers (norm outputs, region ops) -------------
 // act 0: none, 1: ReLU (PyTorch's: NaN kept, -0 to +0), 2: LeakyReLU with slope
 // (x > 0 ? x : x * slope).  Applied to the fp32 value before its one rounding.

@@ -1485,7 +1485,7 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(RowsArgs a, int nsplit
   float v = a.bias ? bf16_to_f32(a.bias[co]) : 0.0f;
   const float* pp = a.part + int64_t(co) * a.m_pad + p;
   const int64_t zstride = int64_t(a.cout) * a.m_pad;
-  for (int z = 0; z < nsplit; ++z) v += pp[z * zstride];
+  v = sum_strided8(v, pp, zstride, 0, 1, nsplit);
   a.out[int64_t(plane) * a.oH * a.oW + pix] = f32_to_bf16(rows_act(a, v));
 }
 
@@ -1870,7 +1870,20 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
     if (i < npair) {
       const int co = int(i / Cin), ci = int(i - int64_t(co) * Cin);
       const float* src = part + int64_t(co) * 9 * ci_pad + ci;
-      for (int k = z; k < splits; k += ZG) {
+      // four splits' 36 loads issued before their sums, which stay in split order
+      int k = z;
+      for (; k + 3 * ZG < splits; k += 4 * ZG) {
+        float v[4][9];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int t = 0; t < 9; ++t) v[u][t] = src[(k + u * ZG) * stride + t * ci_pad];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int t = 0; t < 9; ++t) s[t] += v[u][t];
+      }
+      for (; k < splits; k += ZG) {
         const float* q = src + k * stride;
 #pragma unroll
         for (int t = 0; t < 9; ++t) s[t] += q[t * ci_pad];
@@ -1896,7 +1909,7 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
   if (gb)
     for (int co = blockIdx.x * 256 + threadIdx.x; co < Cout; co += gridDim.x * 256) {
       float s = 0.0f;
-      for (int k = 0; k < splits; ++k) s += bpart[int64_t(k) * co_pad + co];
+      s = sum_strided8(0.0f, bpart + co, co_pad, 0, 1, splits);
       gb[co] = f32_to_bf16(s);
     }
 }
@@ -1928,10 +1941,10 @@ __global__ __launch_bounds__(256) void wgrad_reduce_elem_kernel(const float* __r
       const int t = int((i / Cin) % 9);
       const int co = int(i / (int64_t(Cin) * 9));
       const float* src = part + (int64_t(co) * 9 + t) * ci_pad + ci;
-      for (int k = z; k < splits; k += ZG) s += src[k * stride];
+      s = sum_strided8(0.0f, src, stride, z, ZG, splits);
     } else if (i < n + Cout && gb) {
       const int co = int(i - n);
-      for (int k = z; k < splits; k += ZG) s += bpart[int64_t(k) * co_pad + co];
+      s = sum_strided8(0.0f, bpart + co, co_pad, z, ZG, splits);
     }
     if (ZG > 1) {
       red[threadIdx.x] = s;

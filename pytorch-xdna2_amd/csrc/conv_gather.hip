@@ -311,8 +311,7 @@ __global__ __launch_bounds__(256) void gather_reduce_kernel(const float* __restr
   for (int64_t base = int64_t(blockIdx.x) * EPB; base < mn; base += int64_t(gridDim.x) * EPB) {
     const int64_t i = base + e;
     float s = 0.0f;
-    if (i < mn)
-      for (int k = z; k < nsplit; k += ZG) s += part[int64_t(k) * mn + i];
+    if (i < mn) s = sum_strided8(0.0f, part + i, mn, z, ZG, nsplit);
     red[threadIdx.x] = s;
     __syncthreads();
     if (z == 0) {

@@ -701,7 +701,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs g) {
     const int64_t r = i - int64_t(b) * mn;
     const int m = int(r / g.N), n = int(r - int64_t(m) * g.N);
     float acc = 0.0f;
-    for (int z = 0; z < g.nsplit; ++z) acc += g.part[int64_t(z) * n_all + i];
+    acc = sum_strided8(acc, g.part + i, n_all, 0, 1, g.nsplit);
     float v = g.alpha * acc;
     if (g.bias_mode && g.beta != 0.0f) {
       float bv;
@@ -731,7 +731,21 @@ __global__ __launch_bounds__(256) void gemm_reduce4_kernel(GemmArgs g) {
     const int b = row / g.M, m = row - b * g.M;
     const int n = q << 2;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int z = 0; z < g.nsplit; ++z) {
+    // four splits' loads issued before their sums, which stay in split order
+    int z = 0;
+    for (; z + 3 < g.nsplit; z += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = part[int64_t(z + u) * zs + i];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc.x += v[u].x;
+        acc.y += v[u].y;
+        acc.z += v[u].z;
+        acc.w += v[u].w;
+      }
+    }
+    for (; z < g.nsplit; ++z) {
       const float4 v = part[int64_t(z) * zs + i];
       acc.x += v.x;
       acc.y += v.y;
@@ -1016,12 +1030,24 @@ void gemm5_kernel(GemmArgs g) {
 // wait and barrier that publish the next k-tile and free this one's buffer, then the second
 // half with the next k-tile's DMA and fragment reads in fenced slices.
 // ---------------------------------------------------------------------------------------
-// epilogue of 16 x 16 tiles: rows mb + i*16 + 4 (lane / 16) + r, columns nb + j*16 + lane % 16
-template <int MI, int NJ>
+// epilogue of 16 x 16 tiles: rows mb + i*16 + 4 (lane / 16) + r, columns nb + j*16 + lane % 16.
+// EK, the form fixed at compile time (gemm_epilogue_kind): C with no bias (0: alpha * acc), a
+// bias per column (1: Linear's) or any bias form read at run time (2), or the split-K fp32
+// partials (3).  Each value is computed as the run-time form would (same products, sums and
+// rounding).  One form per kernel: the epilogue is straight-line code run once per tile, and
+// the kernel carrying every form was twice the size (a single 256 x 256 tile at K = 32 took
+// 15.5 against 8.9 us).
+int gemm_epilogue_kind(const GemmArgs& g) {
+  if (g.part) return 3;
+  if (g.bias_mode == 0 || g.beta == 0.0f) return 0;
+  return g.bias_mode == 1 ? 1 : 2;
+}
+
+template <int MI, int NJ, int EK>
 __device__ inline void store_block16(const GemmArgs& g, int batch, int split, const f32x4_t (&acc)[MI][NJ],
                                      int mb, int nb, int lane) {
   const int lc = lane & 15, lq = lane >> 4;
-  if (g.part) {
+  if constexpr (EK == 3) {
     float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
     const auto prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, g.part_bytes, 0x00020000);
     int noff[NJ];
@@ -1042,8 +1068,36 @@ __device__ inline void store_block16(const GemmArgs& g, int batch, int split, co
         __builtin_amdgcn_sched_barrier(0);
       }
     return;
-  }
+  } else {
   const auto crs = __builtin_amdgcn_make_buffer_rsrc(g.c + int64_t(batch) * g.c_batch, 0, g.c_bytes, 0x00020000);
+  if constexpr (EK < 2) {
+    int noff[NJ];
+    float bn[NJ];
+    const auto brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.bias), 0, EK ? g.bias_bytes : 0,
+                                                       0x00020000);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = nb + j * 16 + lc;
+      noff[j] = n < g.N ? int(n * g.c_n * 2) : kSkip;
+      bn[j] = EK ? bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, n < g.N ? int(n * g.bias_sn * 2) : kSkip, 0, 0))
+                 : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = mb + i * 16 + 4 * lq + r;
+        const int moff = m < g.M ? int(m * g.c_m * 2) : kSkip;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          float v = g.alpha * acc[i][j][r];
+          if (EK) v += g.beta * bn[j];
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), crs, moff + noff[j], 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    return;
+  }
   const bool bias = g.bias_mode != 0 && g.beta != 0.0f;
   const auto brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.bias), 0, bias ? g.bias_bytes : 0,
                                                      0x00020000);
@@ -1078,6 +1132,7 @@ __device__ inline void store_block16(const GemmArgs& g, int batch, int split, co
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
 }
 
 // 16 x 32 fragment of a k-contiguous [256][4 pieces] k-tile: rows rb + lane % 16, piece lane / 16
@@ -1104,7 +1159,7 @@ __device__ inline u32x4_t g6_frag(const uint16_t* tile, int rb, int lane) {
   return u32x4_t{a[0], a[1], b[0], b[1]};
 }
 
-template <int kModeA, int kModeB>
+template <int kModeA, int kModeB, int EK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm6_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -1200,16 +1255,25 @@ void gemm6_kernel(GemmArgs g) {
     lds_dma_wait<0>();
   }
   mfma16_fence(acc);
-  store_block16<8, 8>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
+  store_block16<8, 8, EK>(g, batch, split, acc, m0 + wm * 128, n0 + wn * 128, lane);
 }
 
 template <int MA, int MB>
 bool launch6(dim3 grid, hipStream_t st, const GemmArgs& g) {
-  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm6_kernel<MA, MB>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             int(kGemm5Lds)) == hipSuccess;
+  const auto lds = [](const void* f) {
+    return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemm5Lds)) == hipSuccess;
+  };
+  static const bool ok = lds(reinterpret_cast<const void*>(&gemm6_kernel<MA, MB, 0>)) &&
+                         lds(reinterpret_cast<const void*>(&gemm6_kernel<MA, MB, 1>)) &&
+                         lds(reinterpret_cast<const void*>(&gemm6_kernel<MA, MB, 2>)) &&
+                         lds(reinterpret_cast<const void*>(&gemm6_kernel<MA, MB, 3>));
   if (!ok) return false;
-  gemm6_kernel<MA, MB><<<grid, 256, kGemm5Lds, st>>>(g);
+  switch (gemm_epilogue_kind(g)) {
+    case 0: gemm6_kernel<MA, MB, 0><<<grid, 256, kGemm5Lds, st>>>(g); break;
+    case 1: gemm6_kernel<MA, MB, 1><<<grid, 256, kGemm5Lds, st>>>(g); break;
+    case 2: gemm6_kernel<MA, MB, 2><<<grid, 256, kGemm5Lds, st>>>(g); break;
+    default: gemm6_kernel<MA, MB, 3><<<grid, 256, kGemm5Lds, st>>>(g); break;
+  }
   return true;
 }
 

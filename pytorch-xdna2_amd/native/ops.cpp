@@ -1261,9 +1261,11 @@ void run_gemm(const at::Tensor& a, const at::Tensor& m, at::Tensor& c, const at:
   if (bias && beta != 0.0f) {
     be = bias->expand({M, N});
     bp = static_cast<const uint16_t*>(be.const_data_ptr());
-    mode = 2;
     bsm = be.stride(0);
     bsn = be.stride(1);
+    // a bias broadcast over rows (Linear's [N] vector) or over columns is read once per
+    // column / row in the epilogue rather than once per element
+    mode = bsm == 0 ? 1 : (bsn == 0 ? 3 : 2);
   }
   KernelTimer kt("gemm", 2.0 * double(batch) * double(M) * double(N) * double(K));
   check_abi(xdna_gemm_bf16(static_cast<const uint16_t*>(a.const_data_ptr()),
