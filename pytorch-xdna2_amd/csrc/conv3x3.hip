@@ -193,6 +193,9 @@ struct RowsArgs {
 // NaN and maps -0 to +0 (PyTorch's relu); rounding is monotonic and keeps the sign, so
 // bf16(relu(v)) equals relu(bf16(v)) bit for bit: the fused result is the unfused one.
 __device__ inline float rows_act(const RowsArgs& a, float v) { return a.act && v <= 0.0f ? 0.0f : v; }
+// rows_act with the activation fixed at compile time (ReLU when kRelu)
+template <bool kRelu>
+__device__ inline float rows_act_c(float v) { return kRelu && v <= 0.0f ? 0.0f : v; }
 
 // Branch-free NCHW epilogue.  The resource starts at the first image a tile touches; a
 // store whose pixel or channel lies outside the output gets an offset of kOutSkip or more,
@@ -218,24 +221,8 @@ __device__ inline OutMap out_map(const RowsArgs& a, int64_t p_first) {
 }
 
 // byte offset of padded-grid row p's output pixel (channel 0) from the map's base, or
-// kOutSkip for a border / padding row
-__device__ inline int out_pixel_off(const RowsArgs& a, const OutMap& o, int64_t p) {
-  if (p >= a.m_total) return kOutSkip;
-  const int first = a.first;
-  const int64_t vb = p / a.img;
-  const int64_t rem = p - vb * a.img;
-  const int y = int(rem / a.wp);
-  const int col = int(rem - int64_t(y) * a.wp) - first;
-  const int b = int(vb / a.S), s = int(vb % a.S);
-  const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
-  if (y >= a.H || col < 0 || col >= cols) return kOutSkip;
-  const int x = (a.S == 1 ? 0 : s * a.So) + col;
-  if ((y | x) & a.osh) return kOutSkip;  // stride-2 output: odd rows and columns are not outputs
-  return int(((int64_t(b - o.b0)) * o.cp + int64_t(y >> a.osh) * a.oW + (x >> a.osh)) * 2);
-}
-
-// out_pixel_off in 32-bit arithmetic, for grids of fewer than 2^31 rows (the small-grid
-// kernel's, checked on the host)
+// kOutSkip for a border / padding row; 32-bit arithmetic (grids of fewer than 2^31 rows,
+// checked on the host with the map's 1 GiB span)
 __device__ inline int out_pixel_off32(const RowsArgs& a, const OutMap& o, int p) {
   if (p >= int(a.m_total)) return kOutSkip;
   const int img = int(a.img);
@@ -645,7 +632,7 @@ struct Q4 {
   static constexpr size_t Lds = size_t(XRows * kPitch + 3 * Slot) * 2;
 };
 
-template <int MT, int NT, int WM, int OCC>
+template <int MT, int NT, int WM, int OCC, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 void conv_rows4_kernel(RowsArgs a) {
   using Q = Q4<MT, NT, WM>;
@@ -834,13 +821,13 @@ void conv_rows4_kernel(RowsArgs a) {
 #undef XDNA_F4_LOAD
 #undef XDNA_M4
 
-  if (a.out_rs) {
+  if constexpr (EPI < 2) {
     const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
     const int plane2 = a.oH * a.oW * 2;
     int poff[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
-      poff[n] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * NT * 32 + n * 32 + lr);
+      poff[n] = out_pixel_off32(a, om, g * kGroupOutRows + r0 + wn * NT * 32 + n * 32 + lr);
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -849,39 +836,40 @@ void conv_rows4_kernel(RowsArgs a) {
         const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
         for (int n = 0; n < NT; ++n)
-          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act(a, acc[m][n][i])), om.rs, poff[n] + coff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act_c<EPI == 1>(acc[m][n][i])), om.rs, poff[n] + coff, 0, 0);
       }
     return;
-  }
-  const int first = a.first;
-  const int64_t plane = int64_t(a.H) * a.W;
-  uint16_t* obase[NT];
+  } else {
+    const int first = a.first;
+    const int64_t plane = int64_t(a.H) * a.W;
+    uint16_t* obase[NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    obase[n] = nullptr;
-    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NT * 32 + n * 32 + lr;
-    if (p >= a.m_total) continue;
-    const int64_t vb = p / a.img;
-    const int64_t rem = p - vb * a.img;
-    const int y = int(rem / a.wp);
-    const int col = int(rem - int64_t(y) * a.wp) - first;
-    if (y >= a.H || col < 0) continue;
-    const int b = int(vb / a.S), s = int(vb % a.S);
-    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
-    if (col >= cols) continue;
-    const int x = (a.S == 1 ? 0 : s * a.So) + col;
-    obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
-  }
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int co = co0 + wm * MT * 32 + m * 32 + mfma_row(i, lane);
-      if (co >= a.cout) continue;
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[m][n][i]));
+    for (int n = 0; n < NT; ++n) {
+      obase[n] = nullptr;
+      const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NT * 32 + n * 32 + lr;
+      if (p >= a.m_total) continue;
+      const int64_t vb = p / a.img;
+      const int64_t rem = p - vb * a.img;
+      const int y = int(rem / a.wp);
+      const int col = int(rem - int64_t(y) * a.wp) - first;
+      if (y >= a.H || col < 0) continue;
+      const int b = int(vb / a.S), s = int(vb % a.S);
+      const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+      if (col >= cols) continue;
+      const int x = (a.S == 1 ? 0 : s * a.So) + col;
+      obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
     }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int co = co0 + wm * MT * 32 + m * 32 + mfma_row(i, lane);
+        if (co >= a.cout) continue;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[m][n][i]));
+      }
+  }
 }
 
 // Four-wave rows kernels on v_mfma_f32_16x16x32_bf16: the tiles, LDS layout, weight-slab
@@ -937,7 +925,7 @@ __device__ inline int q6_row(int r) {
   return r;
 }
 
-template <int MI, int NJ, int WM, int OCC>
+template <int MI, int NJ, int WM, int OCC, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 void conv_rows6_kernel(RowsArgs a) {
   using Q = Q6<MI, NJ, WM, OCC>;
@@ -1132,13 +1120,13 @@ void conv_rows6_kernel(RowsArgs a) {
   }
 
   mfma16_fence(acc);
-  if (a.out_rs) {
+  if constexpr (EPI < 2) {
     const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
     const int plane2 = a.oH * a.oW * 2;
     int poff[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
-      poff[j] = out_pixel_off(a, om, int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16s);
+      poff[j] = out_pixel_off32(a, om, g * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16s);
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -1147,39 +1135,40 @@ void conv_rows6_kernel(RowsArgs a) {
         const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act(a, acc[i][j][r])), om.rs, poff[j] + coff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act_c<EPI == 1>(acc[i][j][r])), om.rs, poff[j] + coff, 0, 0);
       }
     return;
-  }
-  const int first = a.first;
-  const int64_t plane = int64_t(a.H) * a.W;
-  uint16_t* obase[NJ];
+  } else {
+    const int first = a.first;
+    const int64_t plane = int64_t(a.H) * a.W;
+    uint16_t* obase[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    obase[j] = nullptr;
-    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16s;
-    if (p >= a.m_total) continue;
-    const int64_t vb = p / a.img;
-    const int64_t rem = p - vb * a.img;
-    const int y = int(rem / a.wp);
-    const int col = int(rem - int64_t(y) * a.wp) - first;
-    if (y >= a.H || col < 0) continue;
-    const int b = int(vb / a.S), s = int(vb % a.S);
-    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
-    if (col >= cols) continue;
-    const int x = (a.S == 1 ? 0 : s * a.So) + col;
-    obase[j] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
-  }
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int co = co0 + wm * MI * 16 + i * 16 + chr[r];
-      if (co >= a.cout) continue;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        if (obase[j]) obase[j][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[i][j][r]));
+    for (int j = 0; j < NJ; ++j) {
+      obase[j] = nullptr;
+      const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * NJ * 16 + j * 16 + l16s;
+      if (p >= a.m_total) continue;
+      const int64_t vb = p / a.img;
+      const int64_t rem = p - vb * a.img;
+      const int y = int(rem / a.wp);
+      const int col = int(rem - int64_t(y) * a.wp) - first;
+      if (y >= a.H || col < 0) continue;
+      const int b = int(vb / a.S), s = int(vb % a.S);
+      const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+      if (col >= cols) continue;
+      const int x = (a.S == 1 ? 0 : s * a.So) + col;
+      obase[j] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
     }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int co = co0 + wm * MI * 16 + i * 16 + chr[r];
+        if (co >= a.cout) continue;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          if (obase[j]) obase[j][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[i][j][r]));
+      }
+  }
 }
 
 // Small-grid variant: 64 output channels x TP grid rows per workgroup.  Per input chunk
@@ -1209,7 +1198,7 @@ constexpr int kSWPitch = 9 * kKStep + 8;  // LDS pitch of a staged weight row (5
 
 __device__ inline float round_bf16(float v) { return __uint_as_float(uint32_t(f32_to_bf16(v)) << 16); }
 
-template <int TP, bool EMUL = false, bool NCHW = false>
+template <int TP, bool EMUL = false, bool NCHW = false, int EP = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void conv_small_kernel(RowsArgs a) {
   constexpr int kXRows = TP + kMaxHalo;
@@ -1408,7 +1397,7 @@ void conv_small_kernel(RowsArgs a) {
       for (int i = 0; i < 16; ++i) acc[n][i] += bco[i];
   }
 
-  if (a.part) {
+  if constexpr (EP == 1) {
     float* pz = a.part + int64_t(blockIdx.z) * a.cout * a.m_pad;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -1421,8 +1410,7 @@ void conv_small_kernel(RowsArgs a) {
       }
     }
     return;
-  }
-  if (a.out_rs) {
+  } else if constexpr (EP == 0 || EP == 3) {
     const OutMap om = out_map(a, int64_t(g) * kGroupOutRows + r0);
     const int plane2 = a.oH * a.oW * 2;
     int poff[NT];
@@ -1435,36 +1423,37 @@ void conv_small_kernel(RowsArgs a) {
       const int coff = co < a.cout ? co * plane2 : kOutSkip;
 #pragma unroll
       for (int n = 0; n < NT; ++n)
-        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act(a, acc[n][i])), om.rs, poff[n] + coff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(rows_act_c<EP == 3>(acc[n][i])), om.rs, poff[n] + coff, 0, 0);
     }
     return;
-  }
-  const int first = a.first;
-  const int64_t plane = int64_t(a.H) * a.W;
-  uint16_t* obase[NT];
+  } else {
+    const int first = a.first;
+    const int64_t plane = int64_t(a.H) * a.W;
+    uint16_t* obase[NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    obase[n] = nullptr;
-    const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
-    if (p >= a.m_total) continue;
-    const int64_t vb = p / a.img;
-    const int64_t rem = p - vb * a.img;
-    const int y = int(rem / a.wp);
-    const int col = int(rem - int64_t(y) * a.wp) - first;
-    if (y >= a.H || col < 0) continue;
-    const int b = int(vb / a.S), s = int(vb % a.S);
-    const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
-    if (col >= cols) continue;
-    const int x = (a.S == 1 ? 0 : s * a.So) + col;
-    obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
-  }
+    for (int n = 0; n < NT; ++n) {
+      obase[n] = nullptr;
+      const int64_t p = int64_t(g) * kGroupOutRows + r0 + wn * (TP / 2) + n * 32 + lr;
+      if (p >= a.m_total) continue;
+      const int64_t vb = p / a.img;
+      const int64_t rem = p - vb * a.img;
+      const int y = int(rem / a.wp);
+      const int col = int(rem - int64_t(y) * a.wp) - first;
+      if (y >= a.H || col < 0) continue;
+      const int b = int(vb / a.S), s = int(vb % a.S);
+      const int cols = a.S == 1 ? a.W : min(a.So, a.W - s * a.So);
+      if (col >= cols) continue;
+      const int x = (a.S == 1 ? 0 : s * a.So) + col;
+      obase[n] = a.out + int64_t(b) * a.cout * plane + int64_t(y) * a.W + x;
+    }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int co = co0 + wm * 32 + mfma_row(i, lane);
-    if (co >= a.cout) continue;
+    for (int i = 0; i < 16; ++i) {
+      const int co = co0 + wm * 32 + mfma_row(i, lane);
+      if (co >= a.cout) continue;
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
-      if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[n][i]));
+      for (int n = 0; n < NT; ++n)
+        if (obase[n]) obase[n][int64_t(co) * plane] = f32_to_bf16(rows_act(a, acc[n][i]));
+    }
   }
 }
 
@@ -2126,11 +2115,21 @@ int launch_prep(const uint16_t* w, uint16_t* wt, int Cout, int Cin, int co_pad, 
                : launch_prep_tiled(w, wt, nullptr, Cout, Cin, stream);
 }
 
+// The rows kernels' epilogue form, a compile-time choice (the epilogue is straight-line code
+// run once per tile, and a kernel carrying every form was twice the size): 0 buffer stores,
+// 1 buffer stores with the fused ReLU, 2 per-element pointers (outputs past the buffer
+// stores' 1 GiB range, or grids of 2^31 rows or more), activation read at run time.
+int rows_epilogue(const RowsArgs& a) { return !a.out_rs ? 2 : a.act ? 1 : 0; }
+
 template <int MT, int NT, int WM, int OCC = 1>
 int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   using Q = Q4<MT, NT, WM>;
   static const bool lds_ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM, OCC>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM, OCC, 0>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM, OCC, 1>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows4_kernel<MT, NT, WM, OCC, 2>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess;
   if (!lds_ok) {
     set_error("conv3x3 rows: cannot enable the four-wave kernel's LDS size");
@@ -2139,7 +2138,11 @@ int launch_rows4(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   a.nrt = int(ceil_div(geom.m_total, Q::TP));
   a.ncot = int(ceil_div(cout, Q::CO));
   const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
-  conv_rows4_kernel<MT, NT, WM, OCC><<<grid, 256, Q::Lds, st>>>(a);
+  switch (rows_epilogue(a)) {
+    case 0: conv_rows4_kernel<MT, NT, WM, OCC, 0><<<grid, 256, Q::Lds, st>>>(a); break;
+    case 1: conv_rows4_kernel<MT, NT, WM, OCC, 1><<<grid, 256, Q::Lds, st>>>(a); break;
+    default: conv_rows4_kernel<MT, NT, WM, OCC, 2><<<grid, 256, Q::Lds, st>>>(a); break;
+  }
   return check_launch("conv3x3 rows");
 }
 
@@ -2147,7 +2150,11 @@ template <int MI, int NJ, int WM, int OCC = 1>
 int launch_rows6(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   using Q = Q6<MI, NJ, WM, OCC>;
   static const bool lds_ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows6_kernel<MI, NJ, WM, OCC>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows6_kernel<MI, NJ, WM, OCC, 0>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows6_kernel<MI, NJ, WM, OCC, 1>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_rows6_kernel<MI, NJ, WM, OCC, 2>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(Q::Lds)) == hipSuccess;
   if (!lds_ok) {
     set_error("conv3x3 rows: cannot enable the 16x16x32 kernel's LDS size");
@@ -2156,7 +2163,11 @@ int launch_rows6(RowsArgs a, const ConvGeom& geom, int cout, hipStream_t st) {
   a.nrt = int(ceil_div(geom.m_total, Q::TP));
   a.ncot = int(ceil_div(cout, Q::CO));
   const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
-  conv_rows6_kernel<MI, NJ, WM, OCC><<<grid, 256, Q::Lds, st>>>(a);
+  switch (rows_epilogue(a)) {
+    case 0: conv_rows6_kernel<MI, NJ, WM, OCC, 0><<<grid, 256, Q::Lds, st>>>(a); break;
+    case 1: conv_rows6_kernel<MI, NJ, WM, OCC, 1><<<grid, 256, Q::Lds, st>>>(a); break;
+    default: conv_rows6_kernel<MI, NJ, WM, OCC, 2><<<grid, 256, Q::Lds, st>>>(a); break;
+  }
   return check_launch("conv3x3 rows");
 }
 
@@ -2197,7 +2208,7 @@ RowsArgs rows_args(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
   {
     // images a tile of up to 512 grid rows can touch, and the bytes they span
     const int64_t span = (512 - 1) / geom.img + 2;
-    a.out_rs = span * cout * int64_t(H) * W * 2 < kOutSkip ? 1 : 0;
+    a.out_rs = span * cout * int64_t(H) * W * 2 < kOutSkip && geom.m_total < (int64_t(1) << 31) ? 1 : 0;
   }
   return a;
 }
@@ -2205,23 +2216,41 @@ RowsArgs rows_args(const uint16_t* xp, const uint16_t* wt, const uint16_t* bias,
 // LDS of the small-grid kernel with TP-row tiles
 constexpr size_t small_lds(int TP) { return size_t(TP + kMaxHalo) * kPitch * 2 + size_t(kSCo) * kSWPitch * 2; }
 
+// The small-grid kernel's epilogue form, a compile-time choice: 0 buffer stores, 1 split-K
+// partials, 2 per-element pointers (outputs past the buffer stores' 1 GiB range), 3 buffer
+// stores with the fused ReLU.
+int small_epilogue(const RowsArgs& a) { return a.part ? 1 : !a.out_rs ? 2 : a.act ? 3 : 0; }
+
+template <int TP, bool EMUL, bool NCHW>
+bool small_lds_set() {
+  const auto set = [](const void* f) {
+    return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(TP))) == hipSuccess;
+  };
+  return set(reinterpret_cast<const void*>(&conv_small_kernel<TP, EMUL, NCHW, 0>)) &&
+         set(reinterpret_cast<const void*>(&conv_small_kernel<TP, EMUL, NCHW, 1>)) &&
+         set(reinterpret_cast<const void*>(&conv_small_kernel<TP, EMUL, NCHW, 2>)) &&
+         set(reinterpret_cast<const void*>(&conv_small_kernel<TP, EMUL, NCHW, 3>));
+}
+
 bool small_nchw_lds_ok() {
-  static const bool ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<64, false, true>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(64))) == hipSuccess &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128, false, true>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(128))) == hipSuccess;
+  static const bool ok = small_lds_set<64, false, true>() && small_lds_set<128, false, true>();
   return ok;
 }
 
 template <bool EMUL>
 bool small_lds_ok() {
-  static const bool ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<64, EMUL>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(64))) == hipSuccess &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_small_kernel<128, EMUL>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, int(small_lds(128))) == hipSuccess;
+  static const bool ok = small_lds_set<64, EMUL, false>() && small_lds_set<128, EMUL, false>();
   return ok;
+}
+
+template <int TP, bool EMUL, bool NCHW>
+void launch_small_kernel(const RowsArgs& a, dim3 grid, hipStream_t st) {
+  switch (small_epilogue(a)) {
+    case 0: conv_small_kernel<TP, EMUL, NCHW, 0><<<grid, 256, small_lds(TP), st>>>(a); break;
+    case 1: conv_small_kernel<TP, EMUL, NCHW, 1><<<grid, 256, small_lds(TP), st>>>(a); break;
+    case 2: conv_small_kernel<TP, EMUL, NCHW, 2><<<grid, 256, small_lds(TP), st>>>(a); break;
+    default: conv_small_kernel<TP, EMUL, NCHW, 3><<<grid, 256, small_lds(TP), st>>>(a); break;
+  }
 }
 
 int launch_small(RowsArgs a, const ConvGeom& geom, int B, int cout, int variant, hipStream_t st);
@@ -2403,13 +2432,13 @@ int launch_small(RowsArgs a, const ConvGeom& geom, int B, int cout, int variant,
   a.ncot = int(stiles);
   const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, unsigned(nsplit));
   if (nchw && TP == 128)
-    conv_small_kernel<128, false, true><<<grid, 256, small_lds(128), st>>>(a);
+    launch_small_kernel<128, false, true>(a, grid, st);
   else if (nchw)
-    conv_small_kernel<64, false, true><<<grid, 256, small_lds(64), st>>>(a);
+    launch_small_kernel<64, false, true>(a, grid, st);
   else if (TP == 128)
-    conv_small_kernel<128><<<grid, 256, small_lds(128), st>>>(a);
+    launch_small_kernel<128, false, false>(a, grid, st);
   else
-    conv_small_kernel<64><<<grid, 256, small_lds(64), st>>>(a);
+    launch_small_kernel<64, false, false>(a, grid, st);
   if (nsplit > 1) {
     const unsigned pix_blocks = unsigned(ceil_div(int64_t(a.oH) * a.oW, 256));
     const int planes = B * cout;
@@ -2456,9 +2485,9 @@ int launch_rows_emul(const uint16_t* xp, const uint16_t* wt, const uint16_t* bia
     a.ncot = int(stiles);
     const dim3 grid(unsigned(ceil_div(a.nrt, kXcds) * kXcds * a.ncot), 1, 1);
     if (TP == 128)
-      conv_small_kernel<128, true><<<grid, 256, small_lds(128), as_stream(stream)>>>(a);
+      launch_small_kernel<128, true, false>(a, grid, as_stream(stream));
     else
-      conv_small_kernel<64, true><<<grid, 256, small_lds(64), as_stream(stream)>>>(a);
+      launch_small_kernel<64, true, false>(a, grid, as_stream(stream));
     rc = check_launch("conv3x3 BFP16 emulation");
   } else if (rc == 0) {
     rc = -1;
