@@ -114,6 +114,11 @@ __device__ inline uint16_t f32_to_bf16(float f) {
   return f != f ? uint16_t(0x7FC0) : h;
 }
 
+// A buffer resource's record count from a byte extent, clamped to 2^31 - 1 with integer
+// compares (HIP's min over int64_t resolves to the double overload, whose VALU result makes
+// a resource built from it per-lane: every access through it then runs a waterfall loop).
+__device__ inline int clamp_records(int64_t bytes) { return bytes < 0x7FFFFFFF ? int(bytes) : 0x7FFFFFFF; }
+
 // Split-K partial sums: init + src[z * stride] + src[(z + step) * stride] + ... over
 // indices below n, added left to right in that order (the fixed association every
 // deterministic reduce here keeps), with eight loads issued before their sums: a loop of

@@ -1305,7 +1305,7 @@ void conv_small_kernel(RowsArgs a) {
     const int64_t pbase = (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
     const int64_t ptotal = (a.m_total + kGroupOutRows - 1) / kGroupOutRows * a.chunks * kGroupRows * kKStep;
     prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xp + pbase), 0,
-                                            int(min<int64_t>((ptotal - pbase) * 2, 0x7FFFFFFF)), 0x00020000);
+                                            clamp_records((ptotal - pbase) * 2), 0x00020000);
   }
   const int pvo = (tid >> 3) * 128 + (tid & 7) * 16;
   auto load_chunk = [&](int ch) {
@@ -1891,7 +1891,7 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
 #pragma unroll
       for (int t = 0; t < 9; ++t) ob[e * 9 + t] = f32_to_bf16(s[t]);
     __syncthreads();
-    const int n_out = int(min(int64_t(EPB), npair - base)) * 9;
+    const int n_out = int(npair - base < EPB ? npair - base : int64_t(EPB)) * 9;
     for (int j = threadIdx.x; j < n_out; j += 256) gw[base * 9 + j] = ob[j];
     __syncthreads();  // red and ob are rewritten by the next pass
   }
@@ -2761,17 +2761,27 @@ void wgrad_rows_kernel(WgRowsArgs a) {
   else
     ktiles(std::false_type{});
 
-  // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci
+  // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci.  Buffer stores
+  // from the workgroup's corner (co0, tap 0, ci0): a 32-bit offset per lane and row, the tap
+  // as a uniform offset (every store is inside the partials: co < co_pad, ci < ci_pad)
   const int lr = lane & 31;
-  float* pbase = a.part + int64_t(split) * a.co_pad * 9 * a.ci_pad;
-  const int ci = ci0 + wn * 32 + lr;
+  {
+    // (wave-uniform: read from lane 0, so that the resource is a scalar one)
+    const int64_t c64 = (int64_t(split) * a.co_pad * 9 + int64_t(co0) * 9) * a.ci_pad + ci0;
+    const int64_t corner = int64_t(uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(c64)))) |
+                                   (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(c64 >> 32)))) << 32));
+    const int64_t left = (int64_t(a.splits) * a.co_pad * 9 * a.ci_pad - corner) * 4;
+    const auto prs = __builtin_amdgcn_make_buffer_rsrc(a.part + corner, 0, clamp_records(left), 0x00020000);
+    const int tstride = a.ci_pad * 4;
+    int roff[16];
 #pragma unroll
-  for (int t = 0; t < 9; ++t)
+    for (int i = 0; i < 16; ++i) roff[i] = ((wm * 32 + mfma_row(i, lane)) * 9 * a.ci_pad + wn * 32 + lr) * 4;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int co = co0 + wm * 32 + mfma_row(i, lane);
-      pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][i];
-    }
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[t][i]), prs, roff[i], t * tstride, 0);
+  }
   if (do_bias) {
     // lanes l and l+32 hold the two 8-row halves of channel row l % 32
     const float other = __shfl_down(bsum, 32, 64);
@@ -3051,17 +3061,27 @@ void wgrad_rows5_kernel(WgRowsArgs a) {
       run(std::false_type{});
   }
 
-  // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci
+  // partials: part[split][co][tap][ci]; lanes 0..31 write 32 consecutive ci.  Buffer stores
+  // from the workgroup's corner (co0, tap 0, ci0): a 32-bit offset per lane and row, the tap
+  // as a uniform offset (every store is inside the partials: co < co_pad, ci < ci_pad)
   const int lr = lane & 31;
-  float* pbase = a.part + int64_t(split) * a.co_pad * 9 * a.ci_pad;
-  const int ci = ci0 + wn * 32 + lr;
+  {
+    // (wave-uniform: read from lane 0, so that the resource is a scalar one)
+    const int64_t c64 = (int64_t(split) * a.co_pad * 9 + int64_t(co0) * 9) * a.ci_pad + ci0;
+    const int64_t corner = int64_t(uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(c64)))) |
+                                   (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(c64 >> 32)))) << 32));
+    const int64_t left = (int64_t(a.splits) * a.co_pad * 9 * a.ci_pad - corner) * 4;
+    const auto prs = __builtin_amdgcn_make_buffer_rsrc(a.part + corner, 0, clamp_records(left), 0x00020000);
+    const int tstride = a.ci_pad * 4;
+    int roff[16];
 #pragma unroll
-  for (int t = 0; t < 9; ++t)
+    for (int i = 0; i < 16; ++i) roff[i] = ((wm * 32 + mfma_row(i, lane)) * 9 * a.ci_pad + wn * 32 + lr) * 4;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int co = co0 + wm * 32 + mfma_row(i, lane);
-      pbase[(int64_t(co) * 9 + t) * a.ci_pad + ci] = acc[t][i];
-    }
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[t][i]), prs, roff[i], t * tstride, 0);
+  }
   if (do_bias) {
     // lanes l and l+32 hold the two 8-row halves of channel row l % 32
     const float other = __shfl_down(bsum, 32, 64);
