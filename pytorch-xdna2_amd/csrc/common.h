@@ -119,6 +119,17 @@ __device__ inline uint16_t f32_to_bf16(float f) {
 // a resource built from it per-lane: every access through it then runs a waterfall loop).
 __device__ inline int clamp_records(int64_t bytes) { return bytes < 0x7FFFFFFF ? int(bytes) : 0x7FFFFFFF; }
 
+// A buffer resource over bytes from p, built from lane 0's values: a scalar resource even
+// where the compiler cannot prove its inputs wave-uniform (a per-lane resource turns every
+// access through it into a waterfall loop).  Callers pass wave-uniform values.
+__device__ inline __amdgpu_buffer_rsrc_t uniform_buffer_rsrc(const void* p, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint64_t u = uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))))) |
+                     (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))))) << 32);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0, __builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+
 // Split-K partial sums: init + src[z * stride] + src[(z + step) * stride] + ... over
 // indices below n, added left to right in that order (the fixed association every
 // deterministic reduce here keeps), with eight loads issued before their sums: a loop of

@@ -85,7 +85,7 @@ __device__ inline void store_block(const GemmArgs& g, int batch, int split, cons
   const int lr = lane & 31;
   if (g.part) {
     float* P = g.part + (int64_t(split) * g.batch + batch) * g.M * g.N;
-    const auto prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, g.part_bytes, 0x00020000);
+    const auto prs = uniform_buffer_rsrc(P, g.part_bytes);
     int noff[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -106,10 +106,9 @@ __device__ inline void store_block(const GemmArgs& g, int batch, int split, cons
       }
     return;
   }
-  const auto crs = __builtin_amdgcn_make_buffer_rsrc(g.c + int64_t(batch) * g.c_batch, 0, g.c_bytes, 0x00020000);
+  const auto crs = uniform_buffer_rsrc(g.c + int64_t(batch) * g.c_batch, g.c_bytes);
   const bool bias = g.bias_mode != 0 && g.beta != 0.0f;
-  const auto brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(g.bias), 0, bias ? g.bias_bytes : 0,
-                                                     0x00020000);
+  const auto brs = uniform_buffer_rsrc(g.bias, bias ? g.bias_bytes : 0);
   int noff[NJ], nbo[NJ];
   float bn[NJ];
 #pragma unroll
