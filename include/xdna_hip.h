@@ -129,6 +129,11 @@ int xdna_hip_event_synchronize(void* event);
 int xdna_hip_event_query(void* event);
 int xdna_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int xdna_hip_stream_wait_event(void* stream, void* event);
+/* No counterpart in the reference: a stream of the current device at the default
+ * priority, ordered against other streams only by events (the backend's side stream for
+ * weight gradients that run beside input gradients inside a captured graph).  NULL on
+ * error.  Not destroyed: it lives until the process ends. */
+void* xdna_hip_stream_create(void);
 
 /* ------------------------------------------------------------------------ */
 /* conv3x3w layouts: NCHW <-> tiled padded-grid rows (bit-exact with the     */

@@ -579,6 +579,17 @@ int xdna_hip_stream_wait_event(void* stream, void* event) {
   return 0;
 }
 
+void* xdna_hip_stream_create(void) {
+  hipStream_t s = nullptr;
+  // default priority; non-blocking: ordered against other streams by events only
+  const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    launch_failed("hipStreamCreateWithFlags", e);
+    return nullptr;
+  }
+  return s;
+}
+
 }  // extern "C"
 
 extern "C" int xdna_round_bf16(const float* in, uint16_t* out, int64_t n, void* stream) {

@@ -60,6 +60,10 @@ std::atomic<int> g_wgrad_form{[] {
   const int v = e ? std::atoi(e) : 0;
   return v < 0 || v > 2 ? 0 : v;
 }()};
+std::atomic<int> g_wgrad_overlap{[] {
+  const char* e = std::getenv("XDNA_WGRAD_OVERLAP");
+  return e && std::atoi(e) == 1 ? 1 : 0;
+}()};
 
 namespace {
 
@@ -706,6 +710,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, mod) {
     g_wgrad_form.store(m);
   });
   mod.def("wgrad_form", [] { return g_wgrad_form.load(); });
+  mod.def("set_wgrad_overlap", [](int m) {
+    TORCH_CHECK(m == 0 || m == 1, "xdna: weight-gradient overlap must be 0 or 1");
+    g_wgrad_overlap.store(m);
+  });
+  mod.def("wgrad_overlap", [] { return g_wgrad_overlap.load(); });
   mod.def("set_conv_layout", [](int m) {
     TORCH_CHECK(m >= 0 && m <= 1, "xdna: conv layout must be 0 or 1");
     g_conv_layout.store(m);

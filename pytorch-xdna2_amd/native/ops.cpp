@@ -1037,29 +1037,86 @@ void hip_wgrad(const at::Tensor& input, const at::Tensor& dy, at::Tensor& gw, at
 
 // Weight gradient (+ bias gradient) on the packed row layout: x packed here, dY in the
 // packed form its input gradient already read (`dpacked`), so neither is copied
-// channel-major.  The packs are snapshots, as in the channel-major form.
-void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int layout, int64_t Cout, at::Tensor& gw,
-                    at::Tensor* gb) {
-  const int64_t B = input.size(0), Cin = input.size(1), H = input.size(2), W = input.size(3);
-  at::Tensor xpacked = take_packed_input(input, layout);
-  if (xpacked.defined()) {
+// channel-major.  The packs are snapshots, as in the channel-major form.  Split in two:
+// wgrad_rows_prepare makes every buffer the launch uses (x's pack, the workspace, gw, gb),
+// wgrad_rows_launch enqueues the kernels on a given stream.
+struct WgradRowsJob {
+  at::Tensor xpacked, ws;
+  size_t wsb = 0;
+  int64_t B = 0, Cin = 0, Cout = 0, H = 0, W = 0;
+  int layout = 0;
+};
+
+WgradRowsJob wgrad_rows_prepare(const at::Tensor& input, int layout, int64_t Cout, at::Tensor& gw, at::Tensor* gb) {
+  WgradRowsJob j;
+  j.B = input.size(0), j.Cin = input.size(1), j.H = input.size(2), j.W = input.size(3), j.Cout = Cout;
+  j.layout = layout;
+  j.xpacked = take_packed_input(input, layout);
+  if (j.xpacked.defined()) {
     ScopedCount sk("hip_conv3x3.dw_rows.kept_pack");
   } else {
-    xpacked = pack_rows(input, layout);
+    j.xpacked = pack_rows(input, layout);
   }
-  void* st = current_stream();
-  const size_t wsb =
-      xdna_conv3x3_wgrad_rows_workspace_bytes(int(B), int(Cin), int(Cout), int(H), int(W), layout);
-  at::Tensor ws = alloc_bytes(wsb);
-  gw = empty_xdna({Cout, Cin, 3, 3}, at::kBFloat16);
+  j.wsb = xdna_conv3x3_wgrad_rows_workspace_bytes(int(j.B), int(j.Cin), int(Cout), int(j.H), int(j.W), layout);
+  j.ws = alloc_bytes(j.wsb);
+  gw = empty_xdna({Cout, j.Cin, 3, 3}, at::kBFloat16);
   if (gb) *gb = empty_xdna({Cout}, at::kBFloat16);
-  KernelTimer kt("conv3x3_wgrad", 2.0 * double(B) * double(H) * double(W) * double(Cin) * double(Cout) * 9.0);
-  check_abi(xdna_conv3x3_wgrad_rows_bf16(static_cast<const uint16_t*>(xpacked.const_data_ptr()),
+  return j;
+}
+
+void wgrad_rows_launch(const WgradRowsJob& j, const at::Tensor& dpacked, at::Tensor& gw, at::Tensor* gb, void* st) {
+  check_abi(xdna_conv3x3_wgrad_rows_bf16(static_cast<const uint16_t*>(j.xpacked.const_data_ptr()),
                                          static_cast<const uint16_t*>(dpacked.const_data_ptr()),
                                          static_cast<uint16_t*>(gw.data_ptr()),
-                                         gb ? static_cast<uint16_t*>(gb->data_ptr()) : nullptr, int(B), int(Cin),
-                                         int(Cout), int(H), int(W), layout, ws.data_ptr(), wsb, st),
+                                         gb ? static_cast<uint16_t*>(gb->data_ptr()) : nullptr, int(j.B),
+                                         int(j.Cin), int(j.Cout), int(j.H), int(j.W), j.layout, j.ws.data_ptr(),
+                                         j.wsb, st),
             "conv wgrad rows");
+}
+
+void hip_wgrad_rows(const at::Tensor& input, const at::Tensor& dpacked, int layout, int64_t Cout, at::Tensor& gw,
+                    at::Tensor* gb) {
+  const WgradRowsJob j = wgrad_rows_prepare(input, layout, Cout, gw, gb);
+  KernelTimer kt("conv3x3_wgrad", 2.0 * double(j.B) * double(j.H) * double(j.W) * double(j.Cin) * double(Cout) * 9.0);
+  wgrad_rows_launch(j, dpacked, gw, gb, current_stream());
+}
+
+// The weight gradient beside the input gradient in captured graphs.  A captured backward of
+// a 3x3 layer that needs both forks the weight gradient onto a side stream once dY is
+// packed and joins it back after both are enqueued, so in the graph they are parallel
+// branches (on small grids each fills a fraction of the CUs).  Every buffer the weight
+// gradient uses is made before the fork and released after the join: the caching allocator
+// hands a freed block to the next allocation in capture order, which parallel branches do
+// not follow, so no block one branch frees may reach the other.  Eager work keeps one
+// stream.  Opt-in (XDNA_WGRAD_OVERLAP=1 or set_wgrad_overlap(1); g_wgrad_overlap): on the
+// style network's step the graph replays slower with it (436 -> 396 it/s), each fork and
+// join costing about 17 us of synchronization between the branches' hardware queues, more
+// than the two small kernels gain by sharing the CUs.
+
+struct SideStream {
+  void* stream = nullptr;
+  void* fork = nullptr;
+  void* join = nullptr;
+};
+std::mutex g_side_mu;
+SideStream g_side;
+
+// The side stream and its two events, made outside capture (creating a stream is not a
+// call a capture may record): the eager steps that precede a capture make them.
+bool side_stream_ready(bool may_create) {
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  if (g_side.stream) return true;
+  if (!may_create) return false;
+  void* f = xdna_hip_event_create(0);
+  void* j = f ? xdna_hip_event_create(0) : nullptr;
+  void* s = j ? xdna_hip_stream_create() : nullptr;
+  if (!s) {
+    if (f) xdna_hip_event_destroy(f);
+    if (j) xdna_hip_event_destroy(j);
+    return false;
+  }
+  g_side = SideStream{s, f, j};
+  return true;
 }
 
 // Which weight-gradient form a 3x3 layer takes: the rows form (its x operand is the
@@ -1110,6 +1167,16 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   const bool dx_nchw = hip && mask[0] && !dw_rows && !strided && nchw_route(go, weight.size(1), true);
   if (hip && ((mask[0] && !dx_nchw) || dw_rows))
     gop = strided ? pack_rows_spread(grad_output, go_sizes[2], go_sizes[3], layout) : pack_rows(go, layout);
+  // the rows weight gradient beside the input gradient (captured graphs only)
+  const bool both = dw_rows && mask[0];
+  const int64_t ctag = both && g_wgrad_overlap.load() ? capture_tag() : 0;
+  if (both && ctag == 0 && g_wgrad_overlap.load()) side_stream_ready(true);
+  const bool beside = ctag != 0 && side_stream_ready(false);
+  WgradRowsJob wjob;
+  if (beside) {
+    wjob = wgrad_rows_prepare(input, layout, weight.size(0), gw, mask[2] ? &gb : nullptr);
+    check_abi(xdna_hip_event_record(g_side.fork, current_stream()), "conv backward fork");
+  }
   if (hip && mask[0]) {
     ScopedCount sc("hip_conv3x3.dx.run");
     gi = dx_nchw ? hip_conv_nchw(go, weight, nullptr, true)
@@ -1129,7 +1196,15 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     ScopedCount sc("hip_conv3x3.dw.run");
     if (dw_rows) {
       ScopedCount sr("hip_conv3x3.dw_rows.run");
-      hip_wgrad_rows(input, gop, layout, weight.size(0), gw, mask[2] ? &gb : nullptr);
+      if (beside) {
+        ScopedCount sb("hip_conv3x3.dw_rows.beside_dx");
+        check_abi(xdna_hip_stream_wait_event(g_side.stream, g_side.fork), "conv backward fork");
+        wgrad_rows_launch(wjob, gop, gw, mask[2] ? &gb : nullptr, g_side.stream);
+        check_abi(xdna_hip_event_record(g_side.join, g_side.stream), "conv backward join");
+        check_abi(xdna_hip_stream_wait_event(current_stream(), g_side.join), "conv backward join");
+      } else {
+        hip_wgrad_rows(input, gop, layout, weight.size(0), gw, mask[2] ? &gb : nullptr);
+      }
     } else {
       hip_wgrad(input, go, gw, mask[2] ? &gb : nullptr);
     }

@@ -49,6 +49,8 @@ extern std::atomic<int> g_mode;
 extern std::atomic<int> g_gconv_mode;
 // 3x3 weight gradient: 0 (default) and 2 the rows form, 1 the channel-major form.
 extern std::atomic<int> g_wgrad_form;
+// 1: captured 3x3 backwards run the rows weight gradient beside the input gradient (opt-in)
+extern std::atomic<int> g_wgrad_overlap;
 // Row layout of the 3x3 conv operands: 1 (default) tight strips, 0 the reference's layout.
 extern std::atomic<int> g_conv_layout;
 // 1: the 3x3 / stride-1 forward and input-gradient convs emulate the reference NPU's BFP16

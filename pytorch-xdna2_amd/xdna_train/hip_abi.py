@@ -59,6 +59,7 @@ SIGNATURES = {
     "xdna_hip_event_query": (I, [P]),
     "xdna_hip_event_elapsed_ms": (I, [P, P, ctypes.POINTER(F)]),
     "xdna_hip_stream_wait_event": (I, [P, P]),
+    "xdna_hip_stream_create": (P, []),
     "xdna_hip_cache_pool_current": (L, []),
     "xdna_hip_stream_capturing": (I, [P]),
     "xdna_hip_set_wait_timeout_ms": (I, [L]),

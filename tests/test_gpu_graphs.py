@@ -155,3 +155,45 @@ def test_replays_see_eager_writes_of_adopted_trainable_weights(between):
     assert lg == le
     for a, b in zip(pe, pg):
         assert torch.equal(a, b)
+
+
+def _replayed_params(overlap):
+    """Two eager steps, a captured third, three replays; the weight gradients of the
+    3x3 layers whose input gradient is also needed run beside it when `overlap`."""
+    nat = xdna_train.device.native()
+    before = nat.wgrad_overlap()
+    nat.set_wgrad_overlap(overlap)
+    try:
+        g = torch.Generator().manual_seed(5)
+        x, t = torch.randn(8, 64, 12, 12, generator=g).bfloat16().to(X), torch.randn(8, 64, generator=g).to(X)
+        m = _model(3).to(X)
+        opt = torch.optim.Adam(m.parameters(), lr=1e-3, fused=True, capturable=True)
+        step = _step_fn(m, opt, x, t)
+        for _ in range(2):
+            step()
+        xdna_train.reset_mapped_cpu_stats()
+        graph = torch.xdna.Graph()
+        with torch.xdna.graph(graph):
+            loss = step()
+        beside = _stat_calls("hip_conv3x3.dw_rows.beside_dx")
+        losses = []
+        for _ in range(3):
+            graph.replay()
+            torch.xdna.synchronize()
+            losses.append(float(loss))
+        return beside, losses, [p.detach().cpu() for p in m.parameters()]
+    finally:
+        nat.set_wgrad_overlap(before)
+
+
+def test_captured_weight_gradient_beside_input_gradient():
+    """With the opt-in overlap, the second conv's weight gradient in a captured step forks
+    onto the side stream (its input gradient is needed too) and joins before the
+    optimizer: the replays give the bits of the same step captured on one stream."""
+    print("graph: weight gradient beside the input gradient", flush=True)
+    beside, losses, params = _replayed_params(1)
+    beside0, losses0, params0 = _replayed_params(0)
+    assert beside == 1 and beside0 == 0
+    assert losses == losses0
+    for a, b in zip(params, params0):
+        assert torch.equal(a, b)
