@@ -1194,7 +1194,15 @@ void conv_rows6_kernel(RowsArgs a) {
 // loads of a wave reads one contiguous run of a channel plane; border, padding and
 // past-the-end rows read zeros (an offset past the buffer's range).
 constexpr int kSCo = 64;                  // output channels per workgroup
-constexpr int kSWPitch = 9 * kKStep + 8;  // LDS pitch of a staged weight row (584)
+// LDS pitch of a staged weight row (672 elements, 16 banks mod 64): with the slab's pieces
+// swizzled per row (sw_piece) both its writes (four lanes per row: the rows of a lane group
+// on disjoint 16-bank windows) and the fragment reads (sixteen rows per lane group on
+// distinct bank quads) are free of bank conflicts; the 584-element pitch put the rows of a
+// write's lane group on overlapping banks
+constexpr int kSWPitch = 9 * kKStep + 96;
+// 16-byte piece p of staged weight row r sits at sw_piece(r, p): bits 0-1 of p XOR bits 2-3
+// of r (a permutation inside each aligned block of 4 pieces)
+__device__ inline int sw_piece(int r, int p) { return p ^ ((r >> 2) & 3); }
 
 __device__ inline float round_bf16(float v) { return __uint_as_float(uint32_t(f32_to_bf16(v)) << 16); }
 
@@ -1299,7 +1307,7 @@ void conv_small_kernel(RowsArgs a) {
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.wt + int64_t(co0) * K), 0, kSCo * K * 2, 0x00020000);
   const int wvo = wrow * K * 2 + wq * 16;
-  uint16_t* const wlds = ws + wrow * kSWPitch + wq * 8;
+  uint16_t* const wlds = ws + wrow * kSWPitch + sw_piece(wrow, wq) * 8;  // pieces wq + 4 j (j * 32 below)
   __amdgpu_buffer_rsrc_t prs;
   if constexpr (!NCHW) {
     const int64_t pbase = (int64_t(g) * a.chunks * kGroupRows + r0) * kKStep;
@@ -1350,7 +1358,12 @@ void conv_small_kernel(RowsArgs a) {
   };
 
   load_chunk(ch0);
-  const uint16_t* wa_base = ws + (wm * 32 + lr) * kSWPitch + lk;
+  // fragment k-step (tap, ks) of this lane: piece 8 tap + 2 ks + lk / 8 of weight row
+  // wm * 32 + lr, at its swizzled place (the tap in the immediate offset)
+  const uint16_t* wa_k[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    wa_k[ks] = ws + (wm * 32 + lr) * kSWPitch + sw_piece(wm * 32 + lr, 2 * ks + (lk >> 3)) * 8;
   const uint16_t* xb = xs + (wn * (TP / 2) + lr) * kPitch + lk;
   for (int ch = ch0; ch < ch1; ++ch) {
     __syncthreads();  // the previous chunk's reads of xs / ws are done
@@ -1364,7 +1377,7 @@ void conv_small_kernel(RowsArgs a) {
     const uint16_t* xrow[3] = {xb, xb + a.wp * kPitch, xb + 2 * a.wp * kPitch};
     auto fetch = [&](int step) {
       const int tap = step >> 2, ks = step & 3, slot = step % (kPre + 1);
-      aq[slot] = *reinterpret_cast<const u32x4_t*>(wa_base + tap * kKStep + ks * 16);
+      aq[slot] = *reinterpret_cast<const u32x4_t*>(wa_k[ks] + tap * kKStep);
       const uint16_t* xq = xrow[tap / 3] + (tap % 3) * kPitch + ks * 16;
 #pragma unroll
       for (int n = 0; n < NT; ++n) bq[slot][n] = *reinterpret_cast<const u32x4_t*>(xq + n * 32 * kPitch);
