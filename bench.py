@@ -332,8 +332,8 @@ def sweep_flops(shapes):
 # ---------------------------------------------------------------------------------------
 # CPU baseline: the reference's CPU BF16 path (stock PyTorch CPU kernels) timed on this
 # box's host cores, in worker processes alternating with the GPU timing of the same
-# workload (ABBA over rounds), median of the per-round medians (BASELINE.md's method,
-# after benchmarks/end_to_end_speed.py:53-64, 98-107 and model_zoo.py:281-286).
+# workload (ABBA over rounds), median of the per-round medians (the reference's method,
+# benchmarks/end_to_end_speed.py:53-64, 98-107 and model_zoo.py:281-286).
 # ---------------------------------------------------------------------------------------
 # every C and H of the sweep at N16: the sample the CPU conv rate is measured on
 CPU_SWEEP_SAMPLE = [(16, c, h) for c in (64, 128, 256, 512) for h in (18, 36, 72)]
@@ -491,7 +491,7 @@ def kernel_summary(report):
 
 
 def shape_table(torch, C, X, reps=5, cpu=True, log=None):
-    """Per-shape figures of the sweep (BASELINE.md's C2 report, after
+    """Per-shape figures of the sweep (the reference's per-shape report of config 2,
     benchmarks/conv_shape_sweep.py:60-126): each shape's fwd + dgrad + wgrad step with its
     weight written first (wall time over `reps` steps), the kernel time of every direction
     (HIP events on the launch stream) as TFLOP/s and a fraction of the dense bf16 peak, the
